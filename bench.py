@@ -1,0 +1,258 @@
+"""Benchmark of the GRM hot path on one MI355X.
+
+Headline (value): BASELINE config 2 - fused chunk-update + query application,
+bf16 q/k/v, fp32 state, B*H = 64 sequences, T = 2048, d_k = d_v = 128,
+chunk = 64, with the T/64 per-chunk state snapshots.  One step = one launch of
+grm_hip_chunk_update_fwd over the whole batch, inputs resident in HBM,
+outputs preallocated.  value = tokens/s = 64 * 2048 / (seconds per step).
+
+Also reported: BASELINE config 3 routing (score + top-k + softmax) and the
+materialised top-k gather of 128x128 fp32 states (GB/s against HBM peak), and
+the torch-CPU port of the reference's CPU path on the host (cpu_baseline).
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-gather] [--no-cpu]
+"""
+
+from __future__ import annotations
+
+import argparse
+import ctypes
+import json
+import os
+import statistics
+import sys
+import time
+from pathlib import Path
+
+REPO = Path(__file__).resolve().parent
+sys.path.insert(0, str(REPO))
+
+HBM_PEAK_GBS = 8000.0       # MI355X HBM3E, GB/s
+BF16_PEAK_TFLOPS = 2500.0   # MI355X dense bf16 MFMA
+METRIC = "chunk-update+query tokens/s & %MFMA peak; top-k gather GB/s & %HBM, 1 GPU"
+
+
+def log(msg: str) -> None:
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def c2_counts(BH=64, T=2048, dk=128, dv=128, C=64, in_b=2, out_b=2):
+    """Algorithmic FLOPs and compulsory HBM bytes of one config-2 step."""
+    tokens = BH * T
+    flops = tokens * (2 * C * (dk + dv) + 4 * dk * dv)
+    bytes_ = tokens * (2 * dk + dv) * in_b + tokens * dv * out_b + BH * dv * dk * 4 + BH * (T // C) * dv * dk * 4
+    return flops, bytes_
+
+
+def make_c2(dev, torch, BH=64, T=2048, D=128, seed=0):
+    g = torch.Generator().manual_seed(seed)
+    q = torch.nn.functional.normalize(torch.randn(BH, T, D, generator=g), dim=-1).to(torch.bfloat16)
+    k = torch.nn.functional.normalize(torch.randn(BH, T, D, generator=g), dim=-1).to(torch.bfloat16)
+    v = torch.randn(BH, T, D, generator=g).to(torch.bfloat16)
+    m = torch.randn(BH, D, D, generator=g) * 0.02
+    return k, v, q, m
+
+
+def timed_launches(torch, fn, steps: int, warmup: int, stream):
+    """Run fn warmup times, then time `steps` launches with events on `stream`."""
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    starts = [torch.cuda.Event(enable_timing=True) for _ in range(steps)]
+    ends = [torch.cuda.Event(enable_timing=True) for _ in range(steps)]
+    t0 = time.perf_counter()
+    for i in range(steps):
+        starts[i].record(stream)
+        fn()
+        ends[i].record(stream)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    per = [s.elapsed_time(e) * 1e-3 for s, e in zip(starts, ends)]
+    return wall, per
+
+
+def bench_c2(torch, dev, steps, warmup):
+    from rnn_with_grm_amd import capi
+
+    lib = capi.load()
+    k, v, q, m = [t.to(dev) for t in make_c2(dev, torch)]
+    BH, T, D = k.shape
+    hidden = torch.empty((BH, T, D), dtype=torch.bfloat16, device=dev)
+    mem_out = torch.empty((BH, D, D), dtype=torch.float32, device=dev)
+    snaps = torch.empty((BH, T // 64, D, D), dtype=torch.float32, device=dev)
+    stream = torch.cuda.current_stream(dev)
+    sp = ctypes.c_void_p(stream.cuda_stream)
+    P = lambda t: ctypes.c_void_p(t.data_ptr())  # noqa: E731
+    args = (P(k), P(v), P(q), P(m), P(hidden), P(mem_out), P(snaps), BH, T, D, D, capi.BF16, capi.F32, 0.97, 64, sp)
+
+    def step():
+        rc = lib.grm_hip_chunk_update_fwd(*args)
+        if rc != 0:
+            raise RuntimeError(capi.last_error())
+
+    wall, per = timed_launches(torch, step, steps, warmup, stream)
+    return wall, per, (k, v, q, m, hidden, snaps)
+
+
+def bench_c3(torch, dev, steps, warmup):
+    """Routing over the archive summaries, then the materialised gather."""
+    from rnn_with_grm_amd import capi
+
+    lib = capi.load()
+    BH, Q, S, D, K = 64, 2048, 256, 128, 8
+    g = torch.Generator().manual_seed(1)
+    q = torch.nn.functional.normalize(torch.randn(BH, Q, D, generator=g), dim=-1).to(torch.bfloat16).to(dev)
+    keys = torch.nn.functional.normalize(torch.randn(BH, S, D, generator=g), dim=-1).to(torch.bfloat16).to(dev)
+    states = (torch.randn(BH, S, D, D, device=dev) * 0.02)
+    stream = torch.cuda.current_stream(dev)
+    sp = ctypes.c_void_p(stream.cuda_stream)
+    P = lambda t: ctypes.c_void_p(t.data_ptr())  # noqa: E731
+    idx = torch.empty((BH, Q, K), dtype=torch.int64, device=dev)
+    sc = torch.empty((BH, Q, K), dtype=torch.float32, device=dev)
+    gt = torch.empty((BH, Q, K), dtype=torch.float32, device=dev)
+    scale = 1.0 / D ** 0.5
+
+    def route():
+        rc = lib.grm_hip_topk_route(P(q), P(keys), P(idx), P(sc), P(gt), BH, Q, S, D, capi.BF16, K, scale, 1.0, sp)
+        if rc != 0:
+            raise RuntimeError(capi.last_error())
+
+    r_wall, r_per = timed_launches(torch, route, max(3, steps), warmup, stream)
+    out = torch.empty((BH, Q, K, D, D), dtype=torch.float32, device=dev)
+
+    def gather():
+        rc = lib.grm_hip_batched_gather(P(states), P(idx), P(out), BH, S, Q * K, D * D, 4, None, sp)
+        if rc != 0:
+            raise RuntimeError(capi.last_error())
+
+    g_steps = max(3, min(steps, 10))
+    g_wall, g_per = timed_launches(torch, gather, g_steps, min(warmup, 2), stream)
+    # spot check: one (b, q, r) row against the archive
+    b, qi, r = 5, 777, 3
+    s = int(idx[b, qi, r])
+    assert torch.equal(out[b, qi, r], states[b, s]), "gather spot check failed"
+    del out
+    route_bytes = q.numel() * 2 + keys.numel() * 2 + idx.numel() * 8 + 2 * sc.numel() * 4
+    gather_bytes = BH * Q * K * D * D * 4 + BH * S * D * D * 4 + idx.numel() * 8
+    return {
+        "route": {"ms": statistics.mean(r_per) * 1e3, "bytes": route_bytes,
+                  "flops": 2 * BH * Q * S * D},
+        "gather": {"ms": statistics.mean(g_per) * 1e3, "bytes": gather_bytes},
+    }
+
+
+def cpu_baseline(torch, budget_s: float = 20.0):
+    """The torch-CPU port of the reference's CPU path on config 2 (full shape)."""
+    from oracle import torch_port
+
+    threads = min(16, os.cpu_count() or 1)
+    torch.set_num_threads(threads)
+    k, v, q, m = make_c2(None, torch)
+    times = []
+    t_start = time.perf_counter()
+    while len(times) < 5 or (time.perf_counter() - t_start < budget_s and len(times) < 20):
+        t0 = time.perf_counter()
+        torch_port.segment_scan(k, v, q, m, 0.97, 64)
+        times.append(time.perf_counter() - t0)
+        if time.perf_counter() - t_start > 3 * budget_s:
+            break
+    med = statistics.median(times)
+    return {"value": k.shape[0] * k.shape[1] / med, "unit": "tokens/s", "cores": threads, "kind": "port",
+            "sample": f"full config 2 (64 x 2048 tokens, d=128, fp32 math on bf16-rounded inputs), "
+                      f"one _vectorized_chunk_update per 64-token segment, median of {len(times)} runs, "
+                      f"{threads} threads",
+            "seconds_per_step": med}
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--no-gather", action="store_true")
+    ap.add_argument("--no-cpu", action="store_true")
+    a = ap.parse_args()
+    if a.gpus != 1:
+        print(f"bench.py measures one GPU only; --gpus {a.gpus} is not supported in this build "
+              "(the hot path shards with zero communication over (b,h) sequences; see the design notes)",
+              file=sys.stderr)
+        return 2
+    import torch
+
+    from rnn_with_grm_amd import cuda_ops
+
+    if not torch.cuda.is_available():
+        print("no GPU visible", file=sys.stderr)
+        return 1
+    if not cuda_ops.load_grm_cuda_extension():
+        raise RuntimeError(f"GRM HIP extension not loaded: {cuda_ops._EXTENSION_LOAD_ERROR}")
+    dev = torch.device("cuda:0")
+
+    log(f"config 2 fused chunk-update+query: warmup {a.warmup}, steps {a.steps}")
+    wall, per, _ = bench_c2(torch, dev, a.steps, a.warmup)
+    flops, bytes_ = c2_counts()
+    t_step = wall / a.steps
+    t_kernel = statistics.mean(per)
+    tokens = 64 * 2048
+    achieved_gbs = bytes_ / t_kernel / 1e9
+    tflops = flops / t_kernel / 1e12
+    log(f"c2: {t_kernel * 1e6:.1f} us/launch (events), {t_step * 1e6:.1f} us/step (wall)")
+
+    traffic = None
+    tfile = REPO / "profiles" / "chunk_fwd_c2_traffic.json"
+    if tfile.exists():
+        try:
+            traffic = json.loads(tfile.read_text()).get("hbm_bytes_per_launch")
+        except Exception:
+            traffic = None
+
+    secondary = {}
+    if not a.no_gather:
+        log("config 3 routing + materialised gather (64 GiB output)")
+        c3 = bench_c3(torch, dev, a.steps, a.warmup)
+        r, gth = c3["route"], c3["gather"]
+        secondary["c3_topk_route"] = {"ms": round(r["ms"], 4), "GB/s": round(r["bytes"] / r["ms"] / 1e6, 1),
+                                      "TFLOP/s": round(r["flops"] / r["ms"] / 1e9, 2)}
+        gbs = gth["bytes"] / gth["ms"] / 1e6
+        secondary["c3_gather"] = {"ms": round(gth["ms"], 3), "GB/s": round(gbs, 1),
+                                  "hbm_frac": round(gbs / HBM_PEAK_GBS, 4),
+                                  "bytes": gth["bytes"], "bytes_convention": "compulsory: out write + archive read + idx"}
+        log(f"c3 gather: {gth['ms']:.2f} ms, {gbs:.0f} GB/s")
+
+    cpu = None
+    if not a.no_cpu:
+        log("cpu baseline (torch-CPU port, config 2)")
+        cpu = cpu_baseline(torch)
+        log(f"cpu: {cpu['value']:.3e} tokens/s on {cpu['cores']} threads")
+
+    line = {
+        "metric": METRIC,
+        "value": tokens / t_step,
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": a.steps,
+        "warmup": a.warmup,
+        "ms_per_step": t_step * 1e3,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (seeded N(0,1) q,k,v with q,k L2-normalised, state N(0,0.02))",
+        "config": {"workload": "BASELINE config 2: fused chunk-update + query, bf16 q/k/v, fp32 state, "
+                               "64 sequences (B*H) x 2048 tokens, d_k=d_v=128, chunk 64, 32 snapshots per sequence",
+                   "global_batch": 64, "seq_len": 2048, "parallelism": "single GPU"},
+        "roofline": {"bound": "hbm", "achieved": round(achieved_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(achieved_gbs / HBM_PEAK_GBS, 4), "traffic": traffic,
+                     "kernel": "chunk_fwd_kernel<BF16,128,16>", "algorithmic_bytes_per_launch": bytes_,
+                     "kernel_us": round(t_kernel * 1e6, 2),
+                     "mfma": {"TFLOP/s": round(tflops, 2), "peak": BF16_PEAK_TFLOPS,
+                              "frac": round(tflops / BF16_PEAK_TFLOPS, 5), "flops_per_launch": flops}},
+        "cpu_baseline": None if cpu is None else {k: cpu[k] for k in ("value", "unit", "cores", "kind", "sample")},
+        "secondary": secondary,
+    }
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -1,0 +1,166 @@
+/*
+ * grm_hip.h - C ABI of the MI355X (gfx950) GRM hot-path library, libgrm_hip.so.
+ *
+ * Every entry point takes raw device pointers, int64 sizes, dtype codes and a
+ * hipStream_t (passed as void*; NULL is the null stream).  It enqueues its
+ * kernels on that stream and returns without synchronising.  Nothing here
+ * allocates device memory, and nothing reads or writes torch objects.
+ *
+ * Return value: GRM_HIP_OK (0) on success.  A negative GRM_HIP_E* code means
+ * the arguments were rejected before any launch.  A positive value is the
+ * hipError_t of a failed launch.  grm_hip_last_error() returns a
+ * thread-local message describing the last failure.
+ *
+ * Layouts follow the reference op schemas (grm/csrc/bindings.cpp:6-10):
+ *   keys, queries   [batch, seq_len, key_dim]       row-major, contiguous
+ *   values, hidden  [batch, seq_len, value_dim]
+ *   memory          [batch, value_dim, key_dim]     (row = value index)
+ * Mixed precision: keys/values/queries share one dtype; memory may be that
+ * dtype or float32.  All accumulation is float32.
+ */
+#ifndef GRM_HIP_H
+#define GRM_HIP_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* dtype codes */
+#define GRM_HIP_F32 0
+#define GRM_HIP_F16 1
+#define GRM_HIP_BF16 2
+
+/* status codes */
+#define GRM_HIP_OK 0
+#define GRM_HIP_EINVAL (-1)      /* bad pointer, size or dtype */
+#define GRM_HIP_EUNSUPPORTED (-2) /* valid for the reference, not for this kernel (e.g. key_dim > 256) */
+
+/* Library ABI version (major * 100 + minor). */
+int grm_hip_abi_version(void);
+
+/* Thread-local text of the last error returned by any entry point. */
+const char* grm_hip_last_error(void);
+
+/* Number of kernels this library has launched in the process.  Lets a caller
+ * prove that a call ran on the native path. */
+uint64_t grm_hip_launch_count(void);
+
+/*
+ * Chunked linear-memory update fused with query application.
+ *   M_t = decay * M_{t-1} + (1 - decay) / sqrt(key_dim) * v_t k_t^T
+ *   h_t = M_t q_t
+ * Replaces grm_cuda::chunk_update_forward
+ *   (reference grm/csrc/bindings.cpp:6, chunk_update.cu:523-586, grm_cuda.cpp:46-90,
+ *    Python fallback grm/core/cuda_ops.py:218-254).
+ * hidden:     [batch, seq_len, value_dim] in the input dtype, or NULL to skip it.
+ * memory_out: [batch, value_dim, key_dim] in mem_dtype (may not alias memory), or
+ *             NULL to skip it when snapshots are requested.
+ * snapshots:  NULL, or float32 [batch, ceil(seq_len / snapshot_len), value_dim, key_dim]
+ *             holding the state after every snapshot_len tokens (the last one
+ *             is the final state).  This is the whole-sequence form of the op:
+ *             one call covers every segment of a sequence.
+ * snapshot_len: tokens per snapshot (> 0) when snapshots != NULL, ignored otherwise.
+ * Limits: 1 <= key_dim <= 256, value_dim >= 1; seq_len >= 0; batch >= 0.
+ */
+int grm_hip_chunk_update_fwd(const void* keys, const void* values, const void* queries,
+                             const void* memory, void* hidden, void* memory_out, float* snapshots,
+                             int64_t batch, int64_t seq_len, int64_t key_dim, int64_t value_dim,
+                             int in_dtype, int mem_dtype, double memory_decay,
+                             int64_t snapshot_len, void* stream);
+
+/*
+ * Gradient of grm_hip_chunk_update_fwd.
+ * Replaces grm_cuda::chunk_update_backward
+ *   (reference grm/csrc/bindings.cpp:7, chunk_update.cu:588-716, grm_cuda.cpp:92-126).
+ * grad_hidden [batch, seq_len, value_dim] and grad_memory_out [batch, value_dim, key_dim]
+ * come in the input dtype and mem_dtype; the four gradients are written in the
+ * dtype of the tensor they belong to.
+ * chunk_states: float32 workspace [batch, ceil(seq_len / 64), value_dim, key_dim]
+ *   (caller-provided; overwritten with the state at the start of each 64-token chunk).
+ * dkq_partial: float32 workspace [2, batch, ceil(value_dim / 16), seq_len, key_dim]
+ *   (caller-provided; per value-tile partial sums of grad_keys and grad_queries).
+ */
+int grm_hip_chunk_update_bwd(const void* grad_hidden, const void* grad_memory_out, const void* keys,
+                             const void* values, const void* queries, const void* memory,
+                             void* grad_keys, void* grad_values, void* grad_queries,
+                             void* grad_memory, float* chunk_states, float* dkq_partial,
+                             int64_t batch, int64_t seq_len, int64_t key_dim, int64_t value_dim,
+                             int in_dtype, int mem_dtype, double memory_decay, void* stream);
+
+/*
+ * Query application against stacked memories, float32 accumulation.
+ *   hidden[b, q, r, h] = sum_k memories[b, q, r, h, k] * queries[b, q, k]
+ * Rank 4 of the reference (memories [B, R, H, K], queries [B, K]) is n_query = 1.
+ * Replaces grm_cuda::apply_query_forward
+ *   (reference grm/csrc/bindings.cpp:8, apply_query.cu:186-254, grm_cuda.cpp:128-134).
+ * memories, queries and hidden share dtype.
+ */
+int grm_hip_apply_query_fwd(const void* memories, const void* queries, void* hidden,
+                            int64_t batch, int64_t n_query, int64_t routes, int64_t hidden_size,
+                            int64_t key_dim, int dtype, void* stream);
+
+/*
+ * Gradient of grm_hip_apply_query_fwd:
+ *   grad_memories[b, q, r, h, k] = grad_hidden[b, q, r, h] * queries[b, q, k]
+ *   grad_queries[b, q, k]        = sum_{r, h} grad_hidden[b, q, r, h] * memories[b, q, r, h, k]
+ * Replaces grm_cuda::apply_query_backward
+ *   (reference grm/csrc/bindings.cpp:9, apply_query.cu:256-330, grm_cuda.cpp:136-154).
+ */
+int grm_hip_apply_query_bwd(const void* grad_hidden, const void* memories, const void* queries,
+                            void* grad_memories, void* grad_queries, int64_t batch,
+                            int64_t n_query, int64_t routes, int64_t hidden_size, int64_t key_dim,
+                            int dtype, void* stream);
+
+/*
+ * Batched gather of archived segment states:
+ *   out[b, i, :] = memories[b, indices[b, i], :]      i < n_index, row of row_elems elements
+ * The reference's [B, R] and [B, Q, R] index shapes are n_index = R and Q * R.
+ * Replaces grm_cuda::batched_memory_gather
+ *   (reference grm/csrc/bindings.cpp:10, batched_gather.cu:91-181, grm_cuda.cpp:156-179).
+ * An index outside [0, segments) yields a zero row and, when bad_index_count is
+ * not NULL, increments that device int32 counter (the reference's CUDA kernel
+ * does not check; its CPU path raises).
+ */
+int grm_hip_batched_gather(const void* memories, const int64_t* indices, void* out, int64_t batch,
+                           int64_t segments, int64_t n_index, int64_t row_elems, int elem_bytes,
+                           int32_t* bad_index_count, void* stream);
+
+/*
+ * Segment routing: dot-product score, top-k and softmax gates.
+ *   score[b, q, s] = scale * sum_d queries[b, q, d] * keys[b, s, d]
+ * Each score is one float32 fused multiply-add chain over d = 0 .. dim-1 in
+ * order, so it is reproducible bit for bit on any IEEE machine.
+ * With k = min(top_k, n_keys) < n_keys: the k best scores, descending, ties to
+ * the lower index.  With k == n_keys: every score in index order (indices
+ * 0 .. n_keys-1), the reference's arange branch.
+ * gates = softmax(selected scores / temperature).
+ * Outputs are [batch, n_query, k]: indices int64, scores and gates float32.
+ * Replaces the routing of SegmentRecurrentMemoryModel._route_chunk
+ *   (reference grm/core/paper_grm.py:566-589) and TopKMemoryRetriever.forward
+ *   (grm/core/gating_unit.py:54-91); the reference runs it as torch ops.
+ * Limits: 1 <= top_k <= 32 when top_k < n_keys.
+ */
+int grm_hip_topk_route(const void* queries, const void* keys, int64_t* topk_indices,
+                       float* topk_scores, float* gates, int64_t batch, int64_t n_query,
+                       int64_t n_keys, int64_t dim, int dtype, int64_t top_k, float scale,
+                       float temperature, void* stream);
+
+/*
+ * Residual fusion of the online state with gated retrieved states:
+ *   x = h_online[n] + sum_r gates[n, r] * retrieved[n, r]
+ *   out[n] = layer_norm(x) * weight + bias      (ln_weight == NULL: no LayerNorm)
+ * Replaces RetrievedStateFusion residual mode
+ *   (reference grm/core/aggregator.py:67-145); the reference runs it as torch ops.
+ * h_online, retrieved, out, ln_weight and ln_bias share dtype; gates are float32.
+ */
+int grm_hip_fuse_residual(const void* h_online, const void* retrieved, const float* gates,
+                          const void* ln_weight, const void* ln_bias, void* out, int64_t rows,
+                          int64_t routes, int64_t hidden_size, int dtype, float eps, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* GRM_HIP_H */

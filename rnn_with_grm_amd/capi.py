@@ -1,0 +1,179 @@
+"""ctypes binding of libgrm_hip.so (the C ABI declared in include/grm_hip.h).
+
+This is what a non-torch host (or the reference's own FFI) binds.  The helpers
+below take torch tensors only to read their device pointers and the current
+HIP stream; the library itself sees raw pointers and sizes.  torch is
+imported before the library is loaded so both share one HIP runtime.
+"""
+
+from __future__ import annotations
+
+import ctypes
+from pathlib import Path
+from typing import Optional
+
+import torch
+
+LIB_PATH = Path(__file__).resolve().parent / "libgrm_hip.so"
+
+F32, F16, BF16 = 0, 1, 2
+OK, EINVAL, EUNSUPPORTED = 0, -1, -2
+
+_P = ctypes.c_void_p
+_I = ctypes.c_int64
+_C = ctypes.c_int
+
+# name -> (restype, argtypes); must match include/grm_hip.h
+SIGNATURES = {
+    "grm_hip_abi_version": (ctypes.c_int, []),
+    "grm_hip_last_error": (ctypes.c_char_p, []),
+    "grm_hip_launch_count": (ctypes.c_uint64, []),
+    "grm_hip_chunk_update_fwd": (_C, [_P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _C, _C, ctypes.c_double, _I, _P]),
+    "grm_hip_chunk_update_bwd": (_C, [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _C, _C,
+                                      ctypes.c_double, _P]),
+    "grm_hip_apply_query_fwd": (_C, [_P, _P, _P, _I, _I, _I, _I, _I, _C, _P]),
+    "grm_hip_apply_query_bwd": (_C, [_P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _C, _P]),
+    "grm_hip_batched_gather": (_C, [_P, _P, _P, _I, _I, _I, _I, _C, _P, _P]),
+    "grm_hip_topk_route": (_C, [_P, _P, _P, _P, _P, _I, _I, _I, _I, _C, _I, ctypes.c_float, ctypes.c_float, _P]),
+    "grm_hip_fuse_residual": (_C, [_P, _P, _P, _P, _P, _P, _I, _I, _I, _C, ctypes.c_float, _P]),
+}
+
+_lib: Optional[ctypes.CDLL] = None
+
+
+def load(path: Optional[Path] = None) -> ctypes.CDLL:
+    """Load libgrm_hip.so and declare every exported signature.  Raises if the
+    library or a symbol is missing."""
+    global _lib
+    if _lib is not None and path is None:
+        return _lib
+    p = Path(path) if path else LIB_PATH
+    if not p.exists():
+        raise FileNotFoundError(f"{p} not built; run `python -m rnn_with_grm_amd.build`")
+    lib = ctypes.CDLL(str(p))
+    for name, (res, args) in SIGNATURES.items():
+        fn = getattr(lib, name)
+        fn.restype = res
+        fn.argtypes = args
+    if path is None:
+        _lib = lib
+    return lib
+
+
+def dtype_code(dtype: torch.dtype) -> int:
+    return {torch.float32: F32, torch.float16: F16, torch.bfloat16: BF16}[dtype]
+
+
+def last_error() -> str:
+    return (load().grm_hip_last_error() or b"").decode()
+
+
+def launch_count() -> int:
+    return int(load().grm_hip_launch_count())
+
+
+def _ptr(t: Optional[torch.Tensor]):
+    return None if t is None else ctypes.c_void_p(t.data_ptr())
+
+
+def _stream(t: torch.Tensor):
+    return ctypes.c_void_p(torch.cuda.current_stream(t.device).cuda_stream)
+
+
+def _check(rc: int, what: str) -> None:
+    if rc != OK:
+        raise RuntimeError(f"{what} failed ({rc}): {last_error()}")
+
+
+def chunk_update_fwd(keys, values, queries, memory, decay: float, snapshot_len: int = 0):
+    """Returns (hidden, memory_out, snapshots or None); inputs must be contiguous device tensors."""
+    B, T, K = keys.shape
+    H = values.shape[2]
+    hidden = torch.empty((B, T, H), dtype=values.dtype, device=values.device)
+    memory_out = torch.empty_like(memory)
+    snaps = None
+    if snapshot_len > 0:
+        snaps = torch.empty((B, (T + snapshot_len - 1) // snapshot_len, H, K), dtype=torch.float32,
+                            device=keys.device)
+    rc = load().grm_hip_chunk_update_fwd(_ptr(keys), _ptr(values), _ptr(queries), _ptr(memory), _ptr(hidden),
+                                         _ptr(memory_out), _ptr(snaps), B, T, K, H, dtype_code(keys.dtype),
+                                         dtype_code(memory.dtype), float(decay), int(snapshot_len),
+                                         _stream(keys))
+    _check(rc, "grm_hip_chunk_update_fwd")
+    return hidden, memory_out, snaps
+
+
+def chunk_update_bwd(grad_hidden, grad_memory_out, keys, values, queries, memory, decay: float):
+    B, T, K = keys.shape
+    H = values.shape[2]
+    gk, gv, gq, gm = (torch.empty_like(keys), torch.empty_like(values), torch.empty_like(queries),
+                      torch.empty_like(memory))
+    states = torch.empty((B, max(1, (T + 63) // 64), H, K), dtype=torch.float32, device=keys.device)
+    partial = torch.empty((2, B, (H + 15) // 16, max(T, 1), K), dtype=torch.float32, device=keys.device)
+    rc = load().grm_hip_chunk_update_bwd(_ptr(grad_hidden), _ptr(grad_memory_out), _ptr(keys), _ptr(values),
+                                         _ptr(queries), _ptr(memory), _ptr(gk), _ptr(gv), _ptr(gq), _ptr(gm),
+                                         _ptr(states), _ptr(partial), B, T, K, H, dtype_code(keys.dtype),
+                                         dtype_code(memory.dtype), float(decay), _stream(keys))
+    _check(rc, "grm_hip_chunk_update_bwd")
+    return gk, gv, gq, gm
+
+
+def apply_query_fwd(memories, queries):
+    r5 = memories.dim() == 5
+    B = memories.shape[0]
+    Q = memories.shape[1] if r5 else 1
+    R, H, K = memories.shape[-3:]
+    out = torch.empty(memories.shape[:-1], dtype=memories.dtype, device=memories.device)
+    rc = load().grm_hip_apply_query_fwd(_ptr(memories), _ptr(queries), _ptr(out), B, Q, R, H, K,
+                                        dtype_code(memories.dtype), _stream(memories))
+    _check(rc, "grm_hip_apply_query_fwd")
+    return out
+
+
+def apply_query_bwd(grad_hidden, memories, queries):
+    r5 = memories.dim() == 5
+    B = memories.shape[0]
+    Q = memories.shape[1] if r5 else 1
+    R, H, K = memories.shape[-3:]
+    gm, gq = torch.empty_like(memories), torch.empty_like(queries)
+    rc = load().grm_hip_apply_query_bwd(_ptr(grad_hidden), _ptr(memories), _ptr(queries), _ptr(gm), _ptr(gq),
+                                        B, Q, R, H, K, dtype_code(memories.dtype), _stream(memories))
+    _check(rc, "grm_hip_apply_query_bwd")
+    return gm, gq
+
+
+def batched_gather(memories, indices, bad_count=None, out=None):
+    B, S = memories.shape[:2]
+    n_index = indices[0].numel() if B > 0 else 0
+    if out is None:
+        out = torch.empty((B,) + tuple(indices.shape[1:]) + tuple(memories.shape[2:]), dtype=memories.dtype,
+                          device=memories.device)
+    row = memories[0, 0].numel() if B > 0 and S > 0 else int(torch.tensor(memories.shape[2:]).prod())
+    rc = load().grm_hip_batched_gather(_ptr(memories), _ptr(indices), _ptr(out), B, S, n_index, row,
+                                       memories.element_size(), _ptr(bad_count), _stream(memories))
+    _check(rc, "grm_hip_batched_gather")
+    return out
+
+
+def topk_route(queries, keys, top_k: int, scale: float, temperature: float = 1.0):
+    B, Q, D = queries.shape
+    S = keys.shape[1]
+    k = min(top_k, S)
+    idx = torch.empty((B, Q, k), dtype=torch.int64, device=queries.device)
+    sc = torch.empty((B, Q, k), dtype=torch.float32, device=queries.device)
+    gt = torch.empty((B, Q, k), dtype=torch.float32, device=queries.device)
+    rc = load().grm_hip_topk_route(_ptr(queries), _ptr(keys), _ptr(idx), _ptr(sc), _ptr(gt), B, Q, S, D,
+                                   dtype_code(queries.dtype), int(top_k), float(scale), float(temperature),
+                                   _stream(queries))
+    _check(rc, "grm_hip_topk_route")
+    return gt, idx, sc
+
+
+def fuse_residual(h, retrieved, gates, weight=None, bias=None, eps: float = 1e-5):
+    N, H = h.shape
+    R = retrieved.shape[1]
+    out = torch.empty_like(h)
+    rc = load().grm_hip_fuse_residual(_ptr(h), _ptr(retrieved), _ptr(gates), _ptr(weight), _ptr(bias), _ptr(out),
+                                      N, R, H, dtype_code(h.dtype), float(eps), _stream(h))
+    _check(rc, "grm_hip_fuse_residual")
+    return out

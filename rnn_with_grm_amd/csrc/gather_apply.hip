@@ -1,0 +1,465 @@
+// Batched gather of archived segment states and query application, gfx950.
+//
+// Both are HBM-bound streams with no reuse worth tiling for:
+//   gather:      out[b, i, :] = memories[b, idx[b, i], :]
+//                (reference grm/csrc/batched_gather.cu:14-77, grm_cuda.cpp:156-179)
+//   apply fwd:   hidden[row] = sum_k M[row, k] * q[row / (R*H), k]
+//                (reference grm/csrc/apply_query.cu:14-75, grm_cuda.cpp:128-134)
+//   apply bwd:   dM[row, k] = dh[row] * q[row / (R*H), k]
+//                dq[bq, k]  = sum_{rh} dh[bq*R*H + rh] * M[bq*R*H + rh, k]
+//                (reference grm/csrc/apply_query.cu:77-169, grm_cuda.cpp:136-154)
+// The gather moves whole rows with 16-byte accesses and non-temporal stores
+// (the materialised output is never re-read by this kernel, while the archive
+// rows are re-read by many queries and should stay in L2 / MALL).  Rows are
+// split into eight contiguous ranges, one per XCD, so one XCD's L2 sees the
+// archive of only a few sequences at a time.
+#include <stdint.h>
+#include <string.h>
+
+#include "grm_hip.h"
+#include "grm_hip_common.h"
+
+namespace grmhip {
+namespace {
+
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+constexpr int GT = 256;  // threads per workgroup
+
+struct GatherArgs {
+  const void* mem;
+  const int64_t* idx;
+  void* out;
+  int64_t batch;
+  int64_t segments;
+  int64_t n_index;     // indices per batch entry
+  int64_t total_rows;  // batch * n_index
+  int64_t row_units;   // units per row
+  int tpr;             // threads per row (power of two, <= GT)
+  int xcd_split;       // grid is a multiple of 8: XCD x copies rows [x R/8, (x+1) R/8)
+  int32_t* bad;
+};
+
+template <typename U, bool NT>
+__device__ __forceinline__ void put(U* p, U v) {
+  if constexpr (NT) {
+    __builtin_nontemporal_store(v, p);
+  } else {
+    *p = v;
+  }
+}
+
+template <typename U, bool NT>
+__global__ __launch_bounds__(GT) void gather_kernel(const GatherArgs a) {
+  const int tpr = a.tpr;
+  const int rows_per_wg = GT / tpr;
+  const int sub = threadIdx.x / tpr;
+  const int lane = threadIdx.x % tpr;
+  int64_t lo = 0, hi = a.total_rows;
+  int64_t wg = blockIdx.x, nwg = gridDim.x;
+  if (a.xcd_split) {
+    const int64_t x = blockIdx.x & 7;
+    wg = blockIdx.x >> 3;
+    nwg = gridDim.x >> 3;
+    lo = a.total_rows * x / 8;
+    hi = a.total_rows * (x + 1) / 8;
+  }
+  const U* mem = static_cast<const U*>(a.mem);
+  U* out = static_cast<U*>(a.out);
+  const int64_t ru = a.row_units;
+  for (int64_t row = lo + wg * rows_per_wg + sub; row < hi; row += nwg * rows_per_wg) {
+    const int64_t b = row / a.n_index;
+    const int64_t s = a.idx[row];
+    const bool ok = s >= 0 && s < a.segments;
+    if (!ok && lane == 0 && a.bad != nullptr) atomicAdd(a.bad, 1);
+    const U* src = mem + (b * a.segments + (ok ? s : 0)) * ru;
+    U* dst = out + row * ru;
+    int64_t u = lane;
+    if (ok) {
+      for (; u + 3 * tpr < ru; u += 4 * tpr) {
+        const U v0 = src[u], v1 = src[u + tpr], v2 = src[u + 2 * tpr], v3 = src[u + 3 * tpr];
+        put<U, NT>(dst + u, v0);
+        put<U, NT>(dst + u + tpr, v1);
+        put<U, NT>(dst + u + 2 * tpr, v2);
+        put<U, NT>(dst + u + 3 * tpr, v3);
+      }
+      for (; u < ru; u += tpr) put<U, NT>(dst + u, src[u]);
+    } else {
+      U z;
+      memset(&z, 0, sizeof(z));
+      for (; u < ru; u += tpr) put<U, NT>(dst + u, z);
+    }
+  }
+}
+
+template <typename U, bool NT>
+int launch_gather(GatherArgs a, hipStream_t s) {
+  int tpr = 1;
+  while (tpr < GT && tpr < a.row_units) tpr <<= 1;
+  a.tpr = tpr;
+  const int64_t rows_per_wg = GT / tpr;
+  int64_t want = (a.total_rows + rows_per_wg - 1) / rows_per_wg;
+  // Enough workgroups to fill 256 CUs many times over; the loop covers the rest.
+  const int64_t cap = 256 * 32;
+  int64_t grid = want < cap ? want : cap;
+  a.xcd_split = 0;
+  if (grid >= 64) {
+    grid -= grid % 8;
+    a.xcd_split = 1;
+  }
+  if (grid < 1) grid = 1;
+  hipLaunchKernelGGL((gather_kernel<U, NT>), dim3(static_cast<unsigned>(grid)), dim3(GT), 0, s, a);
+  return check_launch("batched_gather");
+}
+
+bool aligned(const void* p, size_t n) { return (reinterpret_cast<uintptr_t>(p) % n) == 0; }
+
+// ---------------------------------------------------------------------------
+// apply_query forward: a group of G lanes per row, VEC elements per lane per step.
+struct ApplyArgs {
+  const void* mem;
+  const void* q;
+  void* out;
+  const void* dh;    // backward only
+  void* dmem;        // backward only
+  void* dq;          // backward only
+  int64_t rows;      // batch * n_query * routes * hidden
+  int64_t rh;        // routes * hidden (rows per query vector)
+  int64_t nq;        // batch * n_query
+  int kdim;
+  int group;         // lanes per row (power of two <= 64)
+  int vec;           // 16-byte vector path legal
+};
+
+template <class E>
+__device__ __forceinline__ void load_vec(const typename ET<E>::raw* p, int k, int K, bool vec,
+                                         float (&x)[8], int& cnt) {
+  // Loads up to 16 bytes starting at element k.
+  constexpr int V = (sizeof(typename ET<E>::raw) == 2) ? 8 : 4;
+  cnt = V;
+  if (vec && k + V <= K) {
+    if constexpr (V == 8) {
+      const U8<E> u = *reinterpret_cast<const U8<E>*>(p + k);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) x[i] = ET<E>::to_f(u.e[i]);
+    } else {
+      const float4 f = *reinterpret_cast<const float4*>(p + k);
+      x[0] = f.x; x[1] = f.y; x[2] = f.z; x[3] = f.w;
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < V; ++i) x[i] = (k + i < K) ? ET<E>::to_f(p[k + i]) : 0.f;
+  }
+}
+
+template <class E>
+__global__ __launch_bounds__(GT) void apply_fwd_kernel(const ApplyArgs a) {
+  using raw = typename ET<E>::raw;
+  constexpr int V = (sizeof(raw) == 2) ? 8 : 4;
+  constexpr int RPI = 4;  // rows per group per iteration (independent loads in flight)
+  const int G = a.group;
+  const int lane = threadIdx.x % G;
+  const int grp = threadIdx.x / G;
+  const int groups_per_wg = GT / G;
+  const int K = a.kdim;
+  const raw* mem = static_cast<const raw*>(a.mem);
+  const raw* q = static_cast<const raw*>(a.q);
+  raw* out = static_cast<raw*>(a.out);
+  const int64_t step = static_cast<int64_t>(gridDim.x) * groups_per_wg * RPI;
+  for (int64_t base = (static_cast<int64_t>(blockIdx.x) * groups_per_wg + grp) * RPI; base < a.rows;
+       base += step) {
+    float acc[RPI];
+#pragma unroll
+    for (int r = 0; r < RPI; ++r) acc[r] = 0.f;
+    for (int k0 = 0; k0 < K; k0 += G * V) {
+      const int k = k0 + lane * V;
+#pragma unroll
+      for (int r = 0; r < RPI; ++r) {
+        const int64_t row = base + r;
+        if (row < a.rows && k < K) {
+          float m[8], x[8];
+          int cnt;
+          load_vec<E>(mem + row * K, k, K, a.vec, m, cnt);
+          load_vec<E>(q + (row / a.rh) * K, k, K, a.vec, x, cnt);
+#pragma unroll
+          for (int i = 0; i < V; ++i) acc[r] = fmaf(m[i], x[i], acc[r]);
+        }
+      }
+    }
+#pragma unroll
+    for (int r = 0; r < RPI; ++r) {
+      float v = acc[r];
+      for (int off = G >> 1; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
+      const int64_t row = base + r;
+      if (lane == 0 && row < a.rows) out[row] = ET<E>::from_f(v);
+    }
+  }
+}
+
+// dM[row, k] = dh[row] * q[row / rh, k]
+template <class E>
+__global__ __launch_bounds__(GT) void apply_bwd_dmem_kernel(const ApplyArgs a) {
+  using raw = typename ET<E>::raw;
+  constexpr int V = (sizeof(raw) == 2) ? 8 : 4;
+  const int G = a.group;
+  const int lane = threadIdx.x % G;
+  const int grp = threadIdx.x / G;
+  const int groups_per_wg = GT / G;
+  const int K = a.kdim;
+  const raw* q = static_cast<const raw*>(a.q);
+  const raw* dh = static_cast<const raw*>(a.dh);
+  raw* dmem = static_cast<raw*>(a.dmem);
+  const int64_t step = static_cast<int64_t>(gridDim.x) * groups_per_wg;
+  for (int64_t row = static_cast<int64_t>(blockIdx.x) * groups_per_wg + grp; row < a.rows;
+       row += step) {
+    const float d = ET<E>::to_f(dh[row]);
+    const raw* qr = q + (row / a.rh) * K;
+    raw* dst = dmem + row * K;
+    for (int k = lane * V; k < K; k += G * V) {
+      float x[8];
+      int cnt;
+      load_vec<E>(qr, k, K, a.vec, x, cnt);
+      if (a.vec && k + V <= K) {
+        U8<E> u;
+        if constexpr (V == 8) {
+#pragma unroll
+          for (int i = 0; i < 8; ++i) u.e[i] = ET<E>::from_f(d * x[i]);
+          *reinterpret_cast<U8<E>*>(dst + k) = u;
+        } else {
+          *reinterpret_cast<float4*>(dst + k) = make_float4(d * x[0], d * x[1], d * x[2], d * x[3]);
+        }
+      } else {
+#pragma unroll
+        for (int i = 0; i < V; ++i)
+          if (k + i < K) dst[k + i] = ET<E>::from_f(d * x[i]);
+      }
+    }
+  }
+}
+
+// dq[bq, k] = sum_rh dh[bq*rh + i] * M[bq*rh + i, k]; one workgroup per bq,
+// threads = KT k-lanes x P row-partitions, fixed-order partial sums.
+template <class E>
+__global__ __launch_bounds__(GT) void apply_bwd_dq_kernel(const ApplyArgs a) {
+  using raw = typename ET<E>::raw;
+  __shared__ float part[GT];
+  const int K = a.kdim;
+  int KT = 1;
+  while (KT < K && KT < GT) KT <<= 1;
+  const int P = GT / KT;
+  const int kl = threadIdx.x % KT;
+  const int pi = threadIdx.x / KT;
+  const raw* mem = static_cast<const raw*>(a.mem);
+  const raw* dh = static_cast<const raw*>(a.dh);
+  raw* dq = static_cast<raw*>(a.dq);
+  for (int64_t bq = blockIdx.x; bq < a.nq; bq += gridDim.x) {
+    for (int k0 = 0; k0 < K; k0 += KT) {
+      const int k = k0 + kl;
+      float acc = 0.f;
+      if (k < K) {
+        for (int64_t i = pi; i < a.rh; i += P) {
+          const int64_t row = bq * a.rh + i;
+          acc = fmaf(ET<E>::to_f(dh[row]), ET<E>::to_f(mem[row * K + k]), acc);
+        }
+      }
+      part[threadIdx.x] = acc;
+      __syncthreads();
+      if (pi == 0 && k < K) {
+        float s = 0.f;
+        for (int p = 0; p < P; ++p) s += part[p * KT + kl];
+        dq[bq * K + k] = ET<E>::from_f(s);
+      }
+      __syncthreads();
+    }
+  }
+}
+
+int lanes_per_row(int64_t K, int elem_bytes) {
+  const int V = elem_bytes == 2 ? 8 : 4;
+  const int64_t need = (K + V - 1) / V;
+  int g = 1;
+  while (g < 64 && g < need) g <<= 1;
+  return g;
+}
+
+template <class E>
+int launch_apply_fwd(ApplyArgs a, hipStream_t s) {
+  const int64_t groups_per_wg = GT / a.group;
+  const int64_t want = (a.rows + groups_per_wg * 4 - 1) / (groups_per_wg * 4);
+  const int64_t grid = want < 256 * 64 ? want : 256 * 64;
+  hipLaunchKernelGGL(apply_fwd_kernel<E>, dim3(static_cast<unsigned>(grid < 1 ? 1 : grid)), dim3(GT),
+                     0, s, a);
+  return check_launch("apply_query_fwd");
+}
+
+template <class E>
+int launch_apply_bwd(ApplyArgs a, hipStream_t s) {
+  const int64_t groups_per_wg = GT / a.group;
+  int64_t want = (a.rows + groups_per_wg - 1) / groups_per_wg;
+  int64_t grid = want < 256 * 64 ? want : 256 * 64;
+  hipLaunchKernelGGL(apply_bwd_dmem_kernel<E>, dim3(static_cast<unsigned>(grid < 1 ? 1 : grid)),
+                     dim3(GT), 0, s, a);
+  int rc = check_launch("apply_query_bwd(grad_memories)");
+  if (rc != GRM_HIP_OK) return rc;
+  grid = a.nq < 256 * 64 ? a.nq : 256 * 64;
+  hipLaunchKernelGGL(apply_bwd_dq_kernel<E>, dim3(static_cast<unsigned>(grid < 1 ? 1 : grid)),
+                     dim3(GT), 0, s, a);
+  return check_launch("apply_query_bwd(grad_queries)");
+}
+
+int check_apply_sizes(const char* what, int64_t batch, int64_t n_query, int64_t routes,
+                      int64_t hidden_size, int64_t key_dim, int dtype) {
+  if (batch < 0 || n_query < 0 || routes < 0 || hidden_size < 0 || key_dim < 0) {
+    set_error("%s: negative size", what);
+    return GRM_HIP_EINVAL;
+  }
+  if (key_dim > INT32_MAX) {
+    set_error("%s: key_dim too large", what);
+    return GRM_HIP_EINVAL;
+  }
+  if (dtype < GRM_HIP_F32 || dtype > GRM_HIP_BF16) {
+    set_error("%s: unsupported dtype %d", what, dtype);
+    return GRM_HIP_EUNSUPPORTED;
+  }
+  return GRM_HIP_OK;
+}
+
+}  // namespace
+}  // namespace grmhip
+
+using namespace grmhip;
+
+extern "C" int grm_hip_batched_gather(const void* memories, const int64_t* indices, void* out,
+                                      int64_t batch, int64_t segments, int64_t n_index,
+                                      int64_t row_elems, int elem_bytes, int32_t* bad_index_count,
+                                      void* stream) {
+  if (batch < 0 || segments < 0 || n_index < 0 || row_elems < 0) {
+    set_error("batched_gather: negative size");
+    return GRM_HIP_EINVAL;
+  }
+  if (elem_bytes != 1 && elem_bytes != 2 && elem_bytes != 4 && elem_bytes != 8) {
+    set_error("batched_gather: unsupported element size %d", elem_bytes);
+    return GRM_HIP_EUNSUPPORTED;
+  }
+  const int64_t total_rows = batch * n_index;
+  if (total_rows == 0 || row_elems == 0) return GRM_HIP_OK;
+  if (memories == nullptr && segments > 0) {
+    set_error("batched_gather: null memories");
+    return GRM_HIP_EINVAL;
+  }
+  if (indices == nullptr || out == nullptr) {
+    set_error("batched_gather: null pointer");
+    return GRM_HIP_EINVAL;
+  }
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  GatherArgs a;
+  memset(&a, 0, sizeof(a));
+  a.mem = memories;
+  a.idx = indices;
+  a.out = out;
+  a.batch = batch;
+  a.segments = segments;
+  a.n_index = n_index;
+  a.total_rows = total_rows;
+  a.bad = bad_index_count;
+  const int64_t row_bytes = row_elems * elem_bytes;
+  if (row_bytes % 16 == 0 && aligned(memories, 16) && aligned(out, 16)) {
+    a.row_units = row_bytes / 16;
+    // Non-temporal stores only pay for outputs far larger than L2.
+    if (total_rows * row_bytes >= (int64_t(64) << 20)) return launch_gather<u32x4, true>(a, s);
+    return launch_gather<u32x4, false>(a, s);
+  }
+  a.row_units = row_elems;
+  switch (elem_bytes) {
+    case 1: return launch_gather<uint8_t, false>(a, s);
+    case 2: return launch_gather<uint16_t, false>(a, s);
+    case 4: return launch_gather<uint32_t, false>(a, s);
+    default: return launch_gather<uint64_t, false>(a, s);
+  }
+}
+
+extern "C" int grm_hip_apply_query_fwd(const void* memories, const void* queries, void* hidden,
+                                       int64_t batch, int64_t n_query, int64_t routes,
+                                       int64_t hidden_size, int64_t key_dim, int dtype,
+                                       void* stream) {
+  int rc = check_apply_sizes("apply_query_fwd", batch, n_query, routes, hidden_size, key_dim, dtype);
+  if (rc != GRM_HIP_OK) return rc;
+  const int64_t rows = batch * n_query * routes * hidden_size;
+  if (rows == 0) return GRM_HIP_OK;
+  if (memories == nullptr || queries == nullptr || hidden == nullptr) {
+    set_error("apply_query_fwd: null pointer");
+    return GRM_HIP_EINVAL;
+  }
+  const int eb = dtype == GRM_HIP_F32 ? 4 : 2;
+  ApplyArgs a;
+  memset(&a, 0, sizeof(a));
+  a.mem = memories;
+  a.q = queries;
+  a.out = hidden;
+  a.rows = rows;
+  a.rh = routes * hidden_size;
+  a.nq = batch * n_query;
+  a.kdim = static_cast<int>(key_dim);
+  a.group = lanes_per_row(key_dim, eb);
+  a.vec = (key_dim * eb) % 16 == 0 && aligned(memories, 16) && aligned(queries, 16);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  if (key_dim == 0) {
+    hipError_t e = hipMemsetAsync(hidden, 0, rows * eb, s);
+    if (e != hipSuccess) {
+      set_error("apply_query_fwd: hipMemsetAsync failed: %s", hipGetErrorString(e));
+      return static_cast<int>(e);
+    }
+    return GRM_HIP_OK;
+  }
+  switch (dtype) {
+    case GRM_HIP_F32: return launch_apply_fwd<F32>(a, s);
+    case GRM_HIP_F16: return launch_apply_fwd<F16>(a, s);
+    default: return launch_apply_fwd<BF16>(a, s);
+  }
+}
+
+extern "C" int grm_hip_apply_query_bwd(const void* grad_hidden, const void* memories,
+                                       const void* queries, void* grad_memories,
+                                       void* grad_queries, int64_t batch, int64_t n_query,
+                                       int64_t routes, int64_t hidden_size, int64_t key_dim,
+                                       int dtype, void* stream) {
+  int rc = check_apply_sizes("apply_query_bwd", batch, n_query, routes, hidden_size, key_dim, dtype);
+  if (rc != GRM_HIP_OK) return rc;
+  const int64_t rows = batch * n_query * routes * hidden_size;
+  const int64_t nq = batch * n_query;
+  const int eb = dtype == GRM_HIP_F32 ? 4 : 2;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  if (nq == 0 || key_dim == 0) return GRM_HIP_OK;
+  if (queries == nullptr || grad_queries == nullptr || (rows > 0 && (grad_hidden == nullptr ||
+                                                                     memories == nullptr ||
+                                                                     grad_memories == nullptr))) {
+    set_error("apply_query_bwd: null pointer");
+    return GRM_HIP_EINVAL;
+  }
+  if (rows == 0) {
+    hipError_t e = hipMemsetAsync(grad_queries, 0, nq * key_dim * eb, s);
+    if (e != hipSuccess) {
+      set_error("apply_query_bwd: hipMemsetAsync failed: %s", hipGetErrorString(e));
+      return static_cast<int>(e);
+    }
+    return GRM_HIP_OK;
+  }
+  ApplyArgs a;
+  memset(&a, 0, sizeof(a));
+  a.mem = memories;
+  a.q = queries;
+  a.dh = grad_hidden;
+  a.dmem = grad_memories;
+  a.dq = grad_queries;
+  a.rows = rows;
+  a.rh = routes * hidden_size;
+  a.nq = nq;
+  a.kdim = static_cast<int>(key_dim);
+  a.group = lanes_per_row(key_dim, eb);
+  a.vec = (key_dim * eb) % 16 == 0 && aligned(grad_memories, 16) && aligned(queries, 16);
+  switch (dtype) {
+    case GRM_HIP_F32: return launch_apply_bwd<F32>(a, s);
+    case GRM_HIP_F16: return launch_apply_bwd<F16>(a, s);
+    default: return launch_apply_bwd<BF16>(a, s);
+  }
+}

@@ -1,0 +1,605 @@
+// torch.ops.grm_cuda registration for the MI355X library (module grm_cuda_ext).
+//
+// The five schemas are the reference's, character for character
+// (reference grm/csrc/bindings.cpp:5-11), so grm.core.cuda_ops and every model
+// above it bind to this library unchanged.  Three more ops live in the same
+// namespace: segment_scan_forward (whole-sequence update with per-segment
+// state snapshots), topk_route (score -> top-k -> softmax) and fuse_residual.
+//
+// CUDA-key kernels (HIP devices dispatch on the CUDA key in PyTorch-ROCm)
+// check the inputs, allocate outputs with ATen on the input's device and call
+// the C ABI of libgrm_hip.so on the current stream.  Like the reference
+// (chunk_update.cu:529-531, apply_query.cu:187-189, batched_gather.cu:92-94),
+// inputs the kernels do not cover (e.g. float64) run the generic ATen
+// implementation on the same device; grm_hip_launch_count() shows which path
+// ran.  CPU-key kernels are the generic ATen implementations.
+#include <torch/extension.h>
+
+#include <c10/core/DeviceGuard.h>
+#include <c10/hip/HIPStream.h>
+
+#include <atomic>
+#include <cmath>
+#include <cstdlib>
+#include <tuple>
+#include <vector>
+
+#include "grm_hip.h"
+
+namespace grm {
+namespace {
+
+using at::Tensor;
+
+std::atomic<int64_t> g_generic_calls{0};
+
+int dtype_code(at::ScalarType t) {
+  switch (t) {
+    case at::kFloat: return GRM_HIP_F32;
+    case at::kHalf: return GRM_HIP_F16;
+    case at::kBFloat16: return GRM_HIP_BF16;
+    default: return -1;
+  }
+}
+
+void check_rc(int rc, const char* op) {
+  TORCH_CHECK(rc == GRM_HIP_OK, op, " failed (", rc, "): ", grm_hip_last_error());
+}
+
+void* current_stream(const Tensor& t) {
+  return static_cast<void*>(c10::hip::getCurrentHIPStream(t.device().index()).stream());
+}
+
+// ---------------------------------------------------------------------------
+// Argument checks (same conditions and error class as the reference,
+// grm/csrc/grm_cuda.cpp:13-42,159-161).
+void check_chunk_inputs(const Tensor& keys, const Tensor& values, const Tensor& queries,
+                        const Tensor& memory) {
+  TORCH_CHECK(keys.dim() == 3, "keys must have shape [B, T, K]");
+  TORCH_CHECK(values.dim() == 3, "values must have shape [B, T, H]");
+  TORCH_CHECK(queries.dim() == 3, "queries must have shape [B, T, K]");
+  TORCH_CHECK(memory.dim() == 3, "memory must have shape [B, H, K]");
+  TORCH_CHECK(keys.size(0) == values.size(0) && keys.size(1) == values.size(1),
+              "keys and values batch/time dims must match");
+  TORCH_CHECK(keys.sizes() == queries.sizes(), "keys and queries must have the same shape");
+  TORCH_CHECK(values.size(0) == memory.size(0), "memory batch dim must match values batch dim");
+  TORCH_CHECK(values.size(2) == memory.size(1), "memory hidden dim must match values hidden dim");
+  TORCH_CHECK(keys.size(2) == memory.size(2), "memory key dim must match keys key dim");
+}
+
+void check_apply_inputs(const Tensor& memories, const Tensor& queries) {
+  TORCH_CHECK(memories.dim() == 4 || memories.dim() == 5,
+              "memories must have shape [B, R, H, K] or [B, Q, R, H, K]");
+  if (memories.dim() == 4) {
+    TORCH_CHECK(queries.dim() == 2, "queries must have shape [B, K] when memories rank is 4");
+    TORCH_CHECK(memories.size(0) == queries.size(0), "batch dim mismatch between memories and queries");
+    TORCH_CHECK(memories.size(3) == queries.size(1), "key dim mismatch between memories and queries");
+    return;
+  }
+  TORCH_CHECK(queries.dim() == 3, "queries must have shape [B, Q, K] when memories rank is 5");
+  TORCH_CHECK(memories.size(0) == queries.size(0), "batch dim mismatch between memories and queries");
+  TORCH_CHECK(memories.size(1) == queries.size(1), "query dim mismatch between memories and queries");
+  TORCH_CHECK(memories.size(4) == queries.size(2), "key dim mismatch between memories and queries");
+}
+
+void check_gather_inputs(const Tensor& memories, const Tensor& indices) {
+  TORCH_CHECK(memories.dim() == 4, "memories_per_batch must have shape [B, S, H, K]");
+  TORCH_CHECK(indices.dim() == 2 || indices.dim() == 3,
+              "topk_indices must have shape [B, R] or [B, Q, R]");
+  TORCH_CHECK(memories.size(0) == indices.size(0),
+              "batch dim mismatch between memories_per_batch and topk_indices");
+}
+
+// ---------------------------------------------------------------------------
+// Generic ATen implementations (CPU key, and CUDA inputs outside the kernels).
+
+// Chunked closed form, 64 tokens at a time, computed in float32 (float64 for
+// float64 inputs).
+std::tuple<Tensor, Tensor, std::vector<Tensor>> chunk_math(const Tensor& keys, const Tensor& values,
+                                                           const Tensor& queries,
+                                                           const Tensor& memory, double decay,
+                                                           int64_t snapshot_len) {
+  const auto cdt = keys.scalar_type() == at::kDouble ? at::kDouble : at::kFloat;
+  const auto opts = keys.options().dtype(cdt);
+  Tensor k = keys.to(cdt), v = values.to(cdt), q = queries.to(cdt);
+  Tensor m = memory.to(cdt);
+  const int64_t T = keys.size(1);
+  const double c = (1.0 - decay) / std::sqrt(static_cast<double>(keys.size(2)));
+  const Tensor base = at::scalar_tensor(decay, opts);
+  const int64_t step = snapshot_len > 0 ? std::min<int64_t>(snapshot_len, 64) : 64;
+  std::vector<Tensor> outs, snaps;
+  int64_t since_snap = 0;
+  int64_t t0 = 0;
+  while (t0 < T) {
+    int64_t L = std::min(step, T - t0);
+    if (snapshot_len > 0) L = std::min(L, snapshot_len - since_snap);
+    Tensor kc = k.narrow(1, t0, L), vc = v.narrow(1, t0, L), qc = q.narrow(1, t0, L);
+    Tensor pos = at::arange(L, opts);
+    Tensor rel = pos.unsqueeze(1) - pos.unsqueeze(0);
+    Tensor dmask = at::where(rel >= 0, at::pow(base, rel.clamp_min(0)), at::zeros_like(rel));
+    Tensor s = at::bmm(qc, kc.transpose(1, 2)) * (dmask * c).unsqueeze(0);
+    Tensor h = at::bmm(qc, m.transpose(1, 2)) * at::pow(base, pos + 1).view({1, L, 1}) +
+               at::bmm(s, vc);
+    outs.push_back(h);
+    Tensor w = at::pow(base, (L - 1) - pos) * c;
+    m = at::pow(base, static_cast<double>(L)) * m +
+        at::bmm((vc * w.view({1, L, 1})).transpose(1, 2), kc);
+    since_snap += L;
+    t0 += L;
+    if (snapshot_len > 0 && (since_snap == snapshot_len || t0 == T)) {
+      snaps.push_back(m);
+      since_snap = 0;
+    }
+  }
+  Tensor hidden = outs.empty() ? at::zeros({keys.size(0), 0, values.size(2)}, opts) : at::cat(outs, 1);
+  return {hidden, m, snaps};
+}
+
+std::tuple<Tensor, Tensor, Tensor> chunk_update_forward_generic(const Tensor& keys,
+                                                                const Tensor& values,
+                                                                const Tensor& queries,
+                                                                const Tensor& memory,
+                                                                double decay) {
+  check_chunk_inputs(keys, values, queries, memory);
+  if (keys.size(1) == 0) {
+    return {at::zeros({keys.size(0), 0, values.size(2)}, values.options()), memory.contiguous(),
+            at::empty({0}, memory.options())};
+  }
+  auto res = chunk_math(keys, values, queries, memory, decay, 0);
+  return {std::get<0>(res).to(values.scalar_type()).contiguous(),
+          std::get<1>(res).to(memory.scalar_type()).contiguous(), at::empty({0}, memory.options())};
+}
+
+std::tuple<Tensor, Tensor, Tensor, Tensor> chunk_update_backward_generic(
+    const Tensor& grad_hidden, const Tensor& grad_memory_out, const Tensor& keys,
+    const Tensor& values, const Tensor& queries, const Tensor& memory, double decay) {
+  at::AutoGradMode grad_on(true);
+  Tensor k = keys.detach().clone().requires_grad_(true);
+  Tensor v = values.detach().clone().requires_grad_(true);
+  Tensor q = queries.detach().clone().requires_grad_(true);
+  Tensor m = memory.detach().clone().requires_grad_(true);
+  auto out = chunk_update_forward_generic(k, v, q, m, decay);
+  auto grads = torch::autograd::grad({std::get<0>(out), std::get<1>(out)}, {k, v, q, m},
+                                     {grad_hidden.to(values.scalar_type()).contiguous(),
+                                      grad_memory_out.to(memory.scalar_type()).contiguous()},
+                                     false, false, /*allow_unused=*/true);
+  auto fix = [](const Tensor& g, const Tensor& like) {
+    return g.defined() ? g.contiguous() : at::zeros_like(like);
+  };
+  return {fix(grads[0], keys), fix(grads[1], values), fix(grads[2], queries), fix(grads[3], memory)};
+}
+
+Tensor apply_query_forward_generic(const Tensor& memories, const Tensor& queries) {
+  check_apply_inputs(memories, queries);
+  if (memories.dim() == 5) return at::einsum("bqrhk,bqk->bqrh", {memories, queries}).contiguous();
+  return at::einsum("brhk,bk->brh", {memories, queries}).contiguous();
+}
+
+std::tuple<Tensor, Tensor> apply_query_backward_generic(const Tensor& grad_hidden,
+                                                        const Tensor& memories,
+                                                        const Tensor& queries) {
+  check_apply_inputs(memories, queries);
+  Tensor dh = grad_hidden.to(memories.scalar_type());
+  if (memories.dim() == 5) {
+    Tensor gm = (dh.unsqueeze(-1) * queries.unsqueeze(2).unsqueeze(2)).contiguous();
+    Tensor gq = at::einsum("bqrh,bqrhk->bqk", {dh, memories}).contiguous();
+    return {gm, gq};
+  }
+  Tensor gm = (dh.unsqueeze(-1) * queries.unsqueeze(1).unsqueeze(1)).contiguous();
+  Tensor gq = at::einsum("brh,brhk->bk", {dh, memories}).contiguous();
+  return {gm, gq};
+}
+
+Tensor batched_memory_gather_generic(const Tensor& memories, const Tensor& indices) {
+  check_gather_inputs(memories, indices);
+  const int64_t B = memories.size(0);
+  Tensor idx = indices.to(at::kLong).reshape({B, -1});
+  std::vector<int64_t> shape{B};
+  for (int64_t d = 1; d < indices.dim(); ++d) shape.push_back(indices.size(d));
+  shape.push_back(memories.size(2));
+  shape.push_back(memories.size(3));
+  std::vector<Tensor> rows;
+  rows.reserve(B);
+  for (int64_t b = 0; b < B; ++b) rows.push_back(memories[b].index_select(0, idx[b]));
+  if (B == 0) return at::empty(shape, memories.options());
+  return at::stack(rows, 0).reshape(shape).contiguous();
+}
+
+// Canonical routing on the host: one float32 FMA chain per score, ties to the
+// lower index; softmax in float32.
+std::tuple<Tensor, Tensor, Tensor> topk_route_cpu(const Tensor& queries, const Tensor& keys,
+                                                  int64_t top_k, double scale, double temperature) {
+  TORCH_CHECK(queries.dim() == 3 && keys.dim() == 3, "topk_route: queries [B, Q, D], keys [B, S, D]");
+  TORCH_CHECK(queries.size(0) == keys.size(0) && queries.size(2) == keys.size(2),
+              "topk_route: batch/dim mismatch");
+  TORCH_CHECK(top_k >= 1, "topk_route: top_k must be >= 1");
+  TORCH_CHECK(temperature > 0, "topk_route: temperature must be > 0");
+  const int64_t B = queries.size(0), Q = queries.size(1), S = keys.size(1), D = queries.size(2);
+  const int64_t k = std::min(top_k, S);
+  Tensor qf = queries.to(at::kFloat).contiguous(), kf = keys.to(at::kFloat).contiguous();
+  auto fopt = queries.options().dtype(at::kFloat);
+  Tensor idx = at::empty({B, Q, k}, queries.options().dtype(at::kLong));
+  Tensor sc = at::empty({B, Q, k}, fopt), gt = at::empty({B, Q, k}, fopt);
+  const float* qp = qf.data_ptr<float>();
+  const float* kp = kf.data_ptr<float>();
+  int64_t* ip = idx.data_ptr<int64_t>();
+  float* sp = sc.data_ptr<float>();
+  float* gp = gt.data_ptr<float>();
+  const float fs = static_cast<float>(scale), inv_t = 1.0f / static_cast<float>(temperature);
+  at::parallel_for(0, B * Q, 1, [&](int64_t lo, int64_t hi) {
+    std::vector<float> all(S);
+    std::vector<int64_t> order(S);
+    for (int64_t r = lo; r < hi; ++r) {
+      const int64_t b = r / Q;
+      const float* qr = qp + r * D;
+      for (int64_t s = 0; s < S; ++s) {
+        const float* kr = kp + (b * S + s) * D;
+        float acc = 0.f;
+        for (int64_t d = 0; d < D; ++d) acc = std::fma(qr[d], kr[d], acc);
+        all[s] = acc * fs;
+        order[s] = s;
+      }
+      if (k < S) {
+        std::stable_sort(order.begin(), order.end(),
+                         [&](int64_t x, int64_t y) { return all[x] > all[y]; });
+      }
+      float mx = -INFINITY;
+      for (int64_t m = 0; m < k; ++m) mx = std::max(mx, all[order[m]] * inv_t);
+      float sum = 0.f;
+      for (int64_t m = 0; m < k; ++m) sum += std::exp(all[order[m]] * inv_t - mx);
+      for (int64_t m = 0; m < k; ++m) {
+        ip[r * k + m] = order[m];
+        sp[r * k + m] = all[order[m]];
+        gp[r * k + m] = std::exp(all[order[m]] * inv_t - mx) / sum;
+      }
+    }
+  });
+  return {gt, idx, sc};
+}
+
+Tensor fuse_residual_generic(const Tensor& h, const Tensor& retrieved, const Tensor& gates,
+                             const c10::optional<Tensor>& weight, const c10::optional<Tensor>& bias,
+                             double eps) {
+  Tensor x = h.to(at::kFloat);
+  if (retrieved.size(1) > 0) {
+    x = x + (retrieved.to(at::kFloat) * gates.to(at::kFloat).unsqueeze(-1)).sum(1);
+  }
+  if (weight.has_value() && weight->defined()) {
+    x = at::layer_norm(x, {h.size(-1)}, weight->to(at::kFloat),
+                       bias.has_value() && bias->defined() ? bias->to(at::kFloat) : Tensor(), eps);
+  }
+  return x.to(h.scalar_type()).contiguous();
+}
+
+// ---------------------------------------------------------------------------
+// HIP (CUDA-key) implementations.
+
+bool same_cuda_device(std::initializer_list<const Tensor*> ts) {
+  const Tensor* first = *ts.begin();
+  for (const Tensor* t : ts) {
+    if (!t->is_cuda() || t->device() != first->device()) return false;
+  }
+  return true;
+}
+
+bool chunk_supported(const Tensor& keys, const Tensor& values, const Tensor& queries,
+                     const Tensor& memory) {
+  if (!same_cuda_device({&keys, &values, &queries, &memory})) return false;
+  const int in = dtype_code(keys.scalar_type());
+  if (in < 0 || values.scalar_type() != keys.scalar_type() ||
+      queries.scalar_type() != keys.scalar_type())
+    return false;
+  if (memory.scalar_type() != keys.scalar_type() && memory.scalar_type() != at::kFloat) return false;
+  return keys.size(2) >= 1 && keys.size(2) <= 256 && values.size(2) >= 1;
+}
+
+std::tuple<Tensor, Tensor, Tensor> chunk_update_forward_hip(const Tensor& keys, const Tensor& values,
+                                                            const Tensor& queries,
+                                                            const Tensor& memory, double decay) {
+  check_chunk_inputs(keys, values, queries, memory);
+  if (!chunk_supported(keys, values, queries, memory)) {
+    g_generic_calls.fetch_add(1);
+    return chunk_update_forward_generic(keys, values, queries, memory, decay);
+  }
+  c10::OptionalDeviceGuard guard(keys.device());
+  if (keys.size(1) == 0) {
+    return {at::zeros({keys.size(0), 0, values.size(2)}, values.options()), memory.contiguous(),
+            at::empty({0}, memory.options())};
+  }
+  Tensor k = keys.contiguous(), v = values.contiguous(), q = queries.contiguous();
+  Tensor m = memory.contiguous();
+  Tensor hidden = at::empty({k.size(0), k.size(1), v.size(2)}, v.options());
+  Tensor memory_out = at::empty_like(m);
+  check_rc(grm_hip_chunk_update_fwd(k.data_ptr(), v.data_ptr(), q.data_ptr(), m.data_ptr(),
+                                    hidden.data_ptr(), memory_out.data_ptr(), nullptr, k.size(0),
+                                    k.size(1), k.size(2), v.size(2), dtype_code(k.scalar_type()),
+                                    dtype_code(m.scalar_type()), decay, 0, current_stream(k)),
+           "chunk_update_forward");
+  return {hidden, memory_out, at::empty({0}, m.options())};
+}
+
+std::tuple<Tensor, Tensor, Tensor, Tensor> chunk_update_backward_hip(
+    const Tensor& grad_hidden, const Tensor& grad_memory_out, const Tensor& keys,
+    const Tensor& values, const Tensor& queries, const Tensor& memory, const Tensor& aux,
+    double decay) {
+  (void)aux;
+  check_chunk_inputs(keys, values, queries, memory);
+  if (!chunk_supported(keys, values, queries, memory) ||
+      !same_cuda_device({&keys, &grad_hidden, &grad_memory_out})) {
+    g_generic_calls.fetch_add(1);
+    return chunk_update_backward_generic(grad_hidden, grad_memory_out, keys, values, queries,
+                                         memory, decay);
+  }
+  c10::OptionalDeviceGuard guard(keys.device());
+  Tensor k = keys.contiguous(), v = values.contiguous(), q = queries.contiguous();
+  Tensor m = memory.contiguous();
+  Tensor gh = grad_hidden.to(v.scalar_type()).contiguous();
+  Tensor gmo = grad_memory_out.to(m.scalar_type()).contiguous();
+  const int64_t B = k.size(0), T = k.size(1), K = k.size(2), H = v.size(2);
+  if (T == 0) return {at::zeros_like(k), at::zeros_like(v), at::zeros_like(q), gmo.clone()};
+  Tensor gk = at::empty_like(k), gv = at::empty_like(v), gq = at::empty_like(q);
+  Tensor gm = at::empty_like(m);
+  auto f32 = k.options().dtype(at::kFloat);
+  Tensor states = at::empty({B, (T + 63) / 64, H, K}, f32);
+  Tensor partial = at::empty({2, B, (H + 15) / 16, T, K}, f32);
+  check_rc(grm_hip_chunk_update_bwd(gh.data_ptr(), gmo.data_ptr(), k.data_ptr(), v.data_ptr(),
+                                    q.data_ptr(), m.data_ptr(), gk.data_ptr(), gv.data_ptr(),
+                                    gq.data_ptr(), gm.data_ptr(), states.data_ptr<float>(),
+                                    partial.data_ptr<float>(), B, T, K, H,
+                                    dtype_code(k.scalar_type()), dtype_code(m.scalar_type()), decay,
+                                    current_stream(k)),
+           "chunk_update_backward");
+  return {gk, gv, gq, gm};
+}
+
+Tensor apply_query_forward_hip(const Tensor& memories, const Tensor& queries) {
+  check_apply_inputs(memories, queries);
+  const int dt = dtype_code(memories.scalar_type());
+  if (!same_cuda_device({&memories, &queries}) || dt < 0 ||
+      queries.scalar_type() != memories.scalar_type()) {
+    g_generic_calls.fetch_add(1);
+    return apply_query_forward_generic(memories, queries);
+  }
+  c10::OptionalDeviceGuard guard(memories.device());
+  Tensor mm = memories.contiguous(), q = queries.contiguous();
+  const bool r5 = mm.dim() == 5;
+  const int64_t B = mm.size(0), Q = r5 ? mm.size(1) : 1;
+  const int64_t R = mm.size(r5 ? 2 : 1), H = mm.size(r5 ? 3 : 2), K = mm.size(r5 ? 4 : 3);
+  Tensor out = r5 ? at::empty({B, Q, R, H}, mm.options()) : at::empty({B, R, H}, mm.options());
+  check_rc(grm_hip_apply_query_fwd(mm.data_ptr(), q.data_ptr(), out.data_ptr(), B, Q, R, H, K, dt,
+                                   current_stream(mm)),
+           "apply_query_forward");
+  return out;
+}
+
+std::tuple<Tensor, Tensor> apply_query_backward_hip(const Tensor& grad_hidden,
+                                                    const Tensor& memories, const Tensor& queries) {
+  check_apply_inputs(memories, queries);
+  const int dt = dtype_code(memories.scalar_type());
+  if (!same_cuda_device({&memories, &queries, &grad_hidden}) || dt < 0 ||
+      queries.scalar_type() != memories.scalar_type()) {
+    g_generic_calls.fetch_add(1);
+    return apply_query_backward_generic(grad_hidden, memories, queries);
+  }
+  c10::OptionalDeviceGuard guard(memories.device());
+  Tensor mm = memories.contiguous(), q = queries.contiguous();
+  Tensor dh = grad_hidden.to(mm.scalar_type()).contiguous();
+  const bool r5 = mm.dim() == 5;
+  const int64_t B = mm.size(0), Q = r5 ? mm.size(1) : 1;
+  const int64_t R = mm.size(r5 ? 2 : 1), H = mm.size(r5 ? 3 : 2), K = mm.size(r5 ? 4 : 3);
+  Tensor gm = at::empty_like(mm), gq = at::empty_like(q);
+  check_rc(grm_hip_apply_query_bwd(dh.data_ptr(), mm.data_ptr(), q.data_ptr(), gm.data_ptr(),
+                                   gq.data_ptr(), B, Q, R, H, K, dt, current_stream(mm)),
+           "apply_query_backward");
+  return {gm, gq};
+}
+
+bool check_indices_requested() {
+  const char* e = std::getenv("GRM_HIP_CHECK_INDICES");
+  return e != nullptr && e[0] != '\0' && e[0] != '0';
+}
+
+Tensor batched_memory_gather_hip(const Tensor& memories, const Tensor& indices) {
+  check_gather_inputs(memories, indices);
+  if (!same_cuda_device({&memories, &indices})) {
+    g_generic_calls.fetch_add(1);
+    return batched_memory_gather_generic(memories, indices);
+  }
+  c10::OptionalDeviceGuard guard(memories.device());
+  Tensor mm = memories.contiguous();
+  Tensor idx = indices.to(at::kLong).contiguous();
+  const int64_t B = mm.size(0), S = mm.size(1);
+  std::vector<int64_t> shape{B};
+  for (int64_t d = 1; d < idx.dim(); ++d) shape.push_back(idx.size(d));
+  shape.push_back(mm.size(2));
+  shape.push_back(mm.size(3));
+  Tensor out = at::empty(shape, mm.options());
+  const int64_t n_index = B > 0 ? idx.numel() / B : 0;
+  Tensor bad;
+  const bool check = check_indices_requested();
+  if (check) bad = at::zeros({1}, mm.options().dtype(at::kInt));
+  check_rc(grm_hip_batched_gather(mm.data_ptr(), idx.data_ptr<int64_t>(), out.data_ptr(), B, S,
+                                  n_index, mm.size(2) * mm.size(3),
+                                  static_cast<int>(mm.element_size()),
+                                  check ? bad.data_ptr<int32_t>() : nullptr, current_stream(mm)),
+           "batched_memory_gather");
+  if (check) {
+    const int64_t nbad = bad.item<int32_t>();
+    TORCH_CHECK_INDEX(nbad == 0, "batched_memory_gather: ", nbad,
+                      " index values outside [0, ", S, ")");
+  }
+  return out;
+}
+
+// ---- new ops --------------------------------------------------------------
+
+std::tuple<Tensor, Tensor, Tensor> segment_scan_forward_generic(const Tensor& keys,
+                                                                const Tensor& values,
+                                                                const Tensor& queries,
+                                                                const Tensor& memory, double decay,
+                                                                int64_t segment_len) {
+  check_chunk_inputs(keys, values, queries, memory);
+  TORCH_CHECK(segment_len >= 1, "segment_len must be >= 1");
+  auto res = chunk_math(keys, values, queries, memory, decay, segment_len);
+  auto& snaps = std::get<2>(res);
+  Tensor snap = snaps.empty()
+                    ? at::empty({keys.size(0), 0, values.size(2), keys.size(2)},
+                                keys.options().dtype(at::kFloat))
+                    : at::stack(snaps, 1).to(at::kFloat).contiguous();
+  return {std::get<0>(res).to(values.scalar_type()).contiguous(),
+          std::get<1>(res).to(memory.scalar_type()).contiguous(), snap};
+}
+
+std::tuple<Tensor, Tensor, Tensor> segment_scan_forward_hip(const Tensor& keys, const Tensor& values,
+                                                            const Tensor& queries,
+                                                            const Tensor& memory, double decay,
+                                                            int64_t segment_len) {
+  check_chunk_inputs(keys, values, queries, memory);
+  TORCH_CHECK(segment_len >= 1, "segment_len must be >= 1");
+  if (!chunk_supported(keys, values, queries, memory)) {
+    g_generic_calls.fetch_add(1);
+    return segment_scan_forward_generic(keys, values, queries, memory, decay, segment_len);
+  }
+  c10::OptionalDeviceGuard guard(keys.device());
+  Tensor k = keys.contiguous(), v = values.contiguous(), q = queries.contiguous();
+  Tensor m = memory.contiguous();
+  const int64_t B = k.size(0), T = k.size(1), K = k.size(2), H = v.size(2);
+  const int64_t n_snap = (T + segment_len - 1) / segment_len;
+  Tensor hidden = at::empty({B, T, H}, v.options());
+  Tensor memory_out = at::empty_like(m);
+  Tensor snaps = at::empty({B, n_snap, H, K}, k.options().dtype(at::kFloat));
+  if (T == 0) {
+    memory_out.copy_(m);
+    return {hidden, memory_out, snaps};
+  }
+  check_rc(grm_hip_chunk_update_fwd(k.data_ptr(), v.data_ptr(), q.data_ptr(), m.data_ptr(),
+                                    hidden.data_ptr(), memory_out.data_ptr(),
+                                    snaps.data_ptr<float>(), B, T, K, H,
+                                    dtype_code(k.scalar_type()), dtype_code(m.scalar_type()), decay,
+                                    segment_len, current_stream(k)),
+           "segment_scan_forward");
+  return {hidden, memory_out, snaps};
+}
+
+std::tuple<Tensor, Tensor, Tensor> topk_route_hip(const Tensor& queries, const Tensor& keys,
+                                                  int64_t top_k, double scale, double temperature) {
+  const int dt = dtype_code(queries.scalar_type());
+  if (!same_cuda_device({&queries, &keys}) || dt < 0 || keys.scalar_type() != queries.scalar_type() ||
+      std::min(top_k, keys.dim() == 3 ? keys.size(1) : 0) > 32) {
+    if (queries.is_cuda()) g_generic_calls.fetch_add(1);
+    auto r = topk_route_cpu(queries.cpu(), keys.cpu(), top_k, scale, temperature);
+    return {std::get<0>(r).to(queries.device()), std::get<1>(r).to(queries.device()),
+            std::get<2>(r).to(queries.device())};
+  }
+  TORCH_CHECK(queries.dim() == 3 && keys.dim() == 3, "topk_route: queries [B, Q, D], keys [B, S, D]");
+  TORCH_CHECK(queries.size(0) == keys.size(0) && queries.size(2) == keys.size(2),
+              "topk_route: batch/dim mismatch");
+  TORCH_CHECK(top_k >= 1, "topk_route: top_k must be >= 1");
+  TORCH_CHECK(temperature > 0, "topk_route: temperature must be > 0");
+  c10::OptionalDeviceGuard guard(queries.device());
+  Tensor q = queries.contiguous(), kk = keys.contiguous();
+  const int64_t B = q.size(0), Q = q.size(1), S = kk.size(1), D = q.size(2);
+  const int64_t k = std::min(top_k, S);
+  Tensor idx = at::empty({B, Q, k}, q.options().dtype(at::kLong));
+  Tensor sc = at::empty({B, Q, k}, q.options().dtype(at::kFloat));
+  Tensor gt = at::empty({B, Q, k}, q.options().dtype(at::kFloat));
+  if (k > 0 && Q > 0 && B > 0) {
+    check_rc(grm_hip_topk_route(q.data_ptr(), kk.data_ptr(), idx.data_ptr<int64_t>(),
+                                sc.data_ptr<float>(), gt.data_ptr<float>(), B, Q, S, D, dt, top_k,
+                                static_cast<float>(scale), static_cast<float>(temperature),
+                                current_stream(q)),
+             "topk_route");
+  }
+  return {gt, idx, sc};
+}
+
+Tensor fuse_residual_hip(const Tensor& h, const Tensor& retrieved, const Tensor& gates,
+                         const c10::optional<Tensor>& weight, const c10::optional<Tensor>& bias,
+                         double eps) {
+  TORCH_CHECK(h.dim() == 2 && retrieved.dim() == 3 && gates.dim() == 2,
+              "fuse_residual: h [N, H], retrieved [N, R, H], gates [N, R]");
+  TORCH_CHECK(retrieved.size(0) == h.size(0) && retrieved.size(2) == h.size(1) &&
+                  gates.size(0) == h.size(0) && gates.size(1) == retrieved.size(1),
+              "fuse_residual: shape mismatch");
+  const bool has_w = weight.has_value() && weight->defined();
+  const bool has_b = bias.has_value() && bias->defined();
+  const int dt = dtype_code(h.scalar_type());
+  bool ok = same_cuda_device({&h, &retrieved, &gates}) && dt >= 0 &&
+            retrieved.scalar_type() == h.scalar_type() && h.size(1) <= 2048;
+  if (has_w) ok = ok && weight->is_cuda() && weight->scalar_type() == h.scalar_type();
+  if (has_b) ok = ok && has_w && bias->is_cuda() && bias->scalar_type() == h.scalar_type();
+  if (!ok) {
+    if (h.is_cuda()) g_generic_calls.fetch_add(1);
+    return fuse_residual_generic(h, retrieved, gates, weight, bias, eps);
+  }
+  c10::OptionalDeviceGuard guard(h.device());
+  Tensor hc = h.contiguous(), rc = retrieved.contiguous();
+  Tensor gc = gates.to(at::kFloat).contiguous();
+  Tensor wc = has_w ? weight->contiguous() : Tensor();
+  Tensor bc = has_b ? bias->contiguous() : Tensor();
+  Tensor out = at::empty_like(hc);
+  check_rc(grm_hip_fuse_residual(hc.data_ptr(), rc.data_ptr(), gc.data_ptr<float>(),
+                                 has_w ? wc.data_ptr() : nullptr, has_b ? bc.data_ptr() : nullptr,
+                                 out.data_ptr(), hc.size(0), rc.size(1), hc.size(1), dt,
+                                 static_cast<float>(eps), current_stream(hc)),
+           "fuse_residual");
+  return out;
+}
+
+// CPU-key wrappers for the generic forms.
+std::tuple<Tensor, Tensor, Tensor, Tensor> chunk_update_backward_cpu(
+    const Tensor& grad_hidden, const Tensor& grad_memory_out, const Tensor& keys,
+    const Tensor& values, const Tensor& queries, const Tensor& memory, const Tensor& aux,
+    double decay) {
+  (void)aux;
+  check_chunk_inputs(keys, values, queries, memory);
+  return chunk_update_backward_generic(grad_hidden, grad_memory_out, keys, values, queries, memory,
+                                       decay);
+}
+
+}  // namespace
+}  // namespace grm
+
+TORCH_LIBRARY(grm_cuda, m) {
+  m.def("chunk_update_forward(Tensor keys, Tensor values, Tensor queries, Tensor memory, float memory_decay) -> (Tensor hidden, Tensor memory_out, Tensor aux)");
+  m.def("chunk_update_backward(Tensor grad_hidden, Tensor grad_memory_out, Tensor keys, Tensor values, Tensor queries, Tensor memory, Tensor aux, float memory_decay) -> (Tensor grad_keys, Tensor grad_values, Tensor grad_queries, Tensor grad_memory)");
+  m.def("apply_query_forward(Tensor memories, Tensor queries) -> Tensor");
+  m.def("apply_query_backward(Tensor grad_hidden, Tensor memories, Tensor queries) -> (Tensor grad_memories, Tensor grad_queries)");
+  m.def("batched_memory_gather(Tensor memories_per_batch, Tensor topk_indices) -> Tensor");
+  m.def("segment_scan_forward(Tensor keys, Tensor values, Tensor queries, Tensor memory, float memory_decay, int segment_len) -> (Tensor hidden, Tensor memory_out, Tensor snapshots)");
+  m.def("topk_route(Tensor queries, Tensor keys, int top_k, float scale, float temperature) -> (Tensor gates, Tensor indices, Tensor scores)");
+  m.def("fuse_residual(Tensor h_online, Tensor retrieved, Tensor gates, Tensor? weight, Tensor? bias, float eps) -> Tensor");
+}
+
+TORCH_LIBRARY_IMPL(grm_cuda, CPU, m) {
+  m.impl("chunk_update_forward", grm::chunk_update_forward_generic);
+  m.impl("chunk_update_backward", grm::chunk_update_backward_cpu);
+  m.impl("apply_query_forward", grm::apply_query_forward_generic);
+  m.impl("apply_query_backward", grm::apply_query_backward_generic);
+  m.impl("batched_memory_gather", grm::batched_memory_gather_generic);
+  m.impl("segment_scan_forward", grm::segment_scan_forward_generic);
+  m.impl("topk_route", grm::topk_route_cpu);
+  m.impl("fuse_residual", grm::fuse_residual_generic);
+}
+
+TORCH_LIBRARY_IMPL(grm_cuda, CUDA, m) {
+  m.impl("chunk_update_forward", grm::chunk_update_forward_hip);
+  m.impl("chunk_update_backward", grm::chunk_update_backward_hip);
+  m.impl("apply_query_forward", grm::apply_query_forward_hip);
+  m.impl("apply_query_backward", grm::apply_query_backward_hip);
+  m.impl("batched_memory_gather", grm::batched_memory_gather_hip);
+  m.impl("segment_scan_forward", grm::segment_scan_forward_hip);
+  m.impl("topk_route", grm::topk_route_hip);
+  m.impl("fuse_residual", grm::fuse_residual_hip);
+}
+
+PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
+  m.doc() = "GRM hot-path ops for MI355X (gfx950): torch.ops.grm_cuda backed by libgrm_hip.so";
+  m.attr("__grm_cuda_with_kernels__") = pybind11::bool_(true);
+  m.attr("__grm_hip_arch__") = "gfx950";
+  m.def("hip_launch_count", []() { return static_cast<uint64_t>(grm_hip_launch_count()); },
+        "Kernels launched by libgrm_hip.so in this process");
+  m.def("generic_path_calls", []() { return static_cast<int64_t>(grm::g_generic_calls.load()); },
+        "CUDA-key calls that ran the generic ATen implementation");
+  m.def("abi_version", []() { return grm_hip_abi_version(); });
+}

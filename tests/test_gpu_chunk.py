@@ -1,0 +1,178 @@
+"""GPU parity of the fused chunk-update + query kernel and its gradient.
+
+Compares libgrm_hip.so (through the C ABI and through torch.ops.grm_cuda) with
+the double-precision oracle on the same seeded inputs.  Tolerances: rtol 2e-2 /
+atol 2e-3 for bf16/f16 inputs with fp32 accumulation, 1e-5 for fp32 (the
+bounds the task's north star states), plus a relative-L2 bound.
+"""
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import oracle as orc
+from rnn_with_grm_amd import capi, cuda_ops
+
+pytestmark = pytest.mark.gpu
+
+TOL = {torch.float32: (1e-5, 1e-5), torch.bfloat16: (2e-2, 2e-3), torch.float16: (2e-2, 2e-3)}
+REL_L2 = {torch.float32: 1e-5, torch.bfloat16: 1e-2, torch.float16: 5e-3}
+
+
+def make_case(B, T, K, H, dtype, mem_dtype, seed=0, m_std=0.02):
+    g = torch.Generator().manual_seed(seed)
+    q = torch.nn.functional.normalize(torch.randn(B, T, K, generator=g), dim=-1).to(dtype)
+    k = torch.nn.functional.normalize(torch.randn(B, T, K, generator=g), dim=-1).to(dtype)
+    v = torch.randn(B, T, H, generator=g).to(dtype)
+    m = (torch.randn(B, H, K, generator=g) * m_std).to(mem_dtype)
+    return k, v, q, m
+
+
+def close(name, got, ref, dtype):
+    rtol, atol = TOL[dtype]
+    got = got.float().cpu().double().numpy()
+    np.testing.assert_allclose(got, ref, rtol=rtol, atol=atol, err_msg=name)
+    den = np.linalg.norm(ref)
+    if den > 0:
+        rel = np.linalg.norm(got - ref) / den
+        assert rel < REL_L2[dtype], f"{name}: relative L2 error {rel:.3e}"
+
+
+def oracle_fwd(k, v, q, m, decay, snap=0):
+    return orc.chunk_update_seq(k.double().numpy(), v.double().numpy(), q.double().numpy(), m.double().numpy(),
+                                decay, snap)
+
+
+@pytest.mark.parametrize("dtype,mem_dtype", [
+    (torch.bfloat16, torch.float32),
+    (torch.float16, torch.float32),
+    (torch.float32, torch.float32),
+    (torch.bfloat16, torch.bfloat16),
+    (torch.float16, torch.float16),
+])
+@pytest.mark.parametrize("B,T,K,H", [(2, 8, 8, 16), (3, 200, 64, 48), (2, 130, 128, 128), (1, 64, 256, 40),
+                                     (2, 77, 33, 20)])
+def test_chunk_forward_capi(dev, dtype, mem_dtype, B, T, K, H):
+    k, v, q, m = make_case(B, T, K, H, dtype, mem_dtype, seed=B * 1000 + T)
+    decay = 0.97
+    hid, mo, _ = capi.chunk_update_fwd(k.to(dev), v.to(dev), q.to(dev), m.to(dev), decay)
+    torch.cuda.synchronize()
+    rh, rm, _ = oracle_fwd(k, v, q, m, decay)
+    close("hidden", hid, rh, dtype)
+    close("memory_out", mo, rm, mem_dtype if mem_dtype != torch.float32 else dtype)
+
+
+def test_reference_case_fp32(dev):
+    """The reference's own parity shape (examples/test_grm.py:29-37,154-164:
+    B=2, d_v=16, d_k=8, chunk 64, unit-normal memory) at fp32."""
+    k, v, q, m = make_case(2, 64, 8, 16, torch.float32, torch.float32, seed=7, m_std=1.0)
+    hid, mo, aux = torch.ops.grm_cuda.chunk_update_forward(k.to(dev), v.to(dev), q.to(dev), m.to(dev), 0.97)
+    rh, rm, _ = oracle_fwd(k, v, q, m, 0.97)
+    close("hidden", hid, rh, torch.float32)
+    close("memory_out", mo, rm, torch.float32)
+    assert aux.numel() == 0
+
+
+@pytest.mark.parametrize("decay", [0.0, 0.5, 0.97, 1.0])
+def test_decay_edges(dev, decay):
+    k, v, q, m = make_case(2, 150, 64, 32, torch.float32, torch.float32, seed=3, m_std=0.5)
+    hid, mo, _ = capi.chunk_update_fwd(k.to(dev), v.to(dev), q.to(dev), m.to(dev), decay)
+    rh, rm, _ = oracle_fwd(k, v, q, m, decay)
+    close("hidden", hid, rh, torch.float32)
+    close("memory_out", mo, rm, torch.float32)
+
+
+@pytest.mark.parametrize("seg", [64, 128, 32, 100, 1])
+def test_segment_snapshots(dev, seg):
+    T = 300 if seg != 1 else 40
+    k, v, q, m = make_case(2, T, 128, 64, torch.bfloat16, torch.float32, seed=seg)
+    hid, mo, snaps = cuda_ops.cuda_segment_scan(k.to(dev), v.to(dev), q.to(dev), m.to(dev), 0.97, seg)
+    rh, rm, rs = oracle_fwd(k, v, q, m, 0.97, seg)
+    assert snaps.shape == (2, (T + seg - 1) // seg, 64, 128) and snaps.dtype == torch.float32
+    close("hidden", hid, rh, torch.bfloat16)
+    close("memory_out", mo, rm, torch.bfloat16)
+    close("snapshots", snaps, rs, torch.bfloat16)
+    # the last snapshot is the final state, bit for bit
+    assert torch.equal(snaps[:, -1], mo)
+
+
+def test_config2_shape(dev):
+    """BASELINE config 2 at full size (B*H=64, T=2048, d=128, C=64, bf16 in / fp32 state):
+    4 sequences against the oracle, plus size-independent properties on all 64."""
+    B, T, D = 64, 2048, 128
+    g = torch.Generator().manual_seed(0)
+    q = torch.nn.functional.normalize(torch.randn(B, T, D, generator=g), dim=-1).to(torch.bfloat16)
+    k = torch.nn.functional.normalize(torch.randn(B, T, D, generator=g), dim=-1).to(torch.bfloat16)
+    v = torch.randn(B, T, D, generator=g).to(torch.bfloat16)
+    m = torch.randn(B, D, D, generator=g) * 0.02
+    kd, vd, qd, md = k.to(dev), v.to(dev), q.to(dev), m.to(dev)
+    hid, mo, snaps = capi.chunk_update_fwd(kd, vd, qd, md, 0.97, 64)
+    hid2, mo2, _ = capi.chunk_update_fwd(kd, vd, qd, md, 0.97)
+    torch.cuda.synchronize()
+    assert torch.equal(hid, hid2) and torch.equal(mo, mo2), "snapshot output must not change the scan"
+    assert torch.equal(snaps[:, -1], mo)
+    assert torch.isfinite(hid.float()).all() and torch.isfinite(snaps).all()
+    for b in (0, 17, 40, 63):
+        rh, rm, rs = oracle_fwd(k[b:b + 1], v[b:b + 1], q[b:b + 1], m[b:b + 1], 0.97, 64)
+        close(f"hidden[{b}]", hid[b:b + 1], rh, torch.bfloat16)
+        close(f"snapshots[{b}]", snaps[b:b + 1], rs, torch.bfloat16)
+    # run-to-run determinism (no atomics)
+    hid3, _, snaps3 = capi.chunk_update_fwd(kd, vd, qd, md, 0.97, 64)
+    assert torch.equal(hid, hid3) and torch.equal(snaps, snaps3)
+
+
+def test_empty_and_zero_batch(dev):
+    k, v, q, m = make_case(2, 0, 16, 8, torch.float32, torch.float32)
+    hid, mo, aux = torch.ops.grm_cuda.chunk_update_forward(k.to(dev), v.to(dev), q.to(dev), m.to(dev), 0.9)
+    assert hid.shape == (2, 0, 8) and torch.equal(mo.cpu(), m)
+    k, v, q, m = make_case(0, 5, 16, 8, torch.float32, torch.float32)
+    hid, mo, _ = torch.ops.grm_cuda.chunk_update_forward(k.to(dev), v.to(dev), q.to(dev), m.to(dev), 0.9)
+    assert hid.shape == (0, 5, 8)
+
+
+def test_native_path_runs(dev):
+    ext = cuda_ops._EXTENSION_MODULE
+    before = ext.hip_launch_count()
+    k, v, q, m = make_case(2, 64, 32, 16, torch.bfloat16, torch.float32)
+    cuda_ops.cuda_chunk_update(k.to(dev), v.to(dev), q.to(dev), m.to(dev), 0.97)
+    assert ext.hip_launch_count() > before
+    status = cuda_ops.get_grm_cuda_runtime_status()
+    assert status["extension_loaded"] and status["compiled_with_cuda_kernels"] and status["cuda_backend_available"]
+
+
+@pytest.mark.parametrize("dtype,mem_dtype", [(torch.float32, torch.float32), (torch.bfloat16, torch.float32),
+                                             (torch.bfloat16, torch.bfloat16)])
+@pytest.mark.parametrize("B,T,K,H", [(2, 8, 8, 16), (2, 150, 64, 40), (1, 70, 128, 128)])
+def test_chunk_backward(dev, dtype, mem_dtype, B, T, K, H):
+    k, v, q, m = make_case(B, T, K, H, dtype, mem_dtype, seed=11)
+    g = torch.Generator().manual_seed(5)
+    dh = torch.randn(B, T, H, generator=g).to(dtype)
+    dm = torch.randn(B, H, K, generator=g).to(mem_dtype)
+    gk, gv, gq, gm = capi.chunk_update_bwd(dh.to(dev), dm.to(dev), k.to(dev), v.to(dev), q.to(dev), m.to(dev), 0.97)
+    torch.cuda.synchronize()
+    rk, rv, rq, rm = orc.chunk_update_bwd(dh.double().numpy(), dm.double().numpy(), k.double().numpy(),
+                                          v.double().numpy(), q.double().numpy(), m.double().numpy(), 0.97)
+    tol_dtype = torch.float32 if dtype == torch.float32 else torch.bfloat16
+    bw = {torch.float32: (5e-4, 5e-5)}  # the reference's CUDA gradient bound is 5e-4
+    for name, got, ref in (("grad_keys", gk, rk), ("grad_values", gv, rv), ("grad_queries", gq, rq),
+                           ("grad_memory", gm, rm)):
+        if tol_dtype == torch.float32:
+            np.testing.assert_allclose(got.double().cpu().numpy(), ref, rtol=bw[torch.float32][0],
+                                       atol=bw[torch.float32][1], err_msg=name)
+        else:
+            close(name, got, ref, torch.bfloat16)
+
+
+def test_autograd_through_cuda_ops(dev):
+    """cuda_chunk_update under autograd matches the fallback's autograd (the
+    reference's check, examples/test_grm.py:72-113)."""
+    k, v, q, m = make_case(2, 64, 8, 16, torch.float32, torch.float32, seed=2, m_std=1.0)
+
+    def run(debug):
+        ins = [t.to(dev).clone().requires_grad_(True) for t in (k, v, q, m)]
+        h, mo = cuda_ops.cuda_chunk_update(*ins, memory_decay=0.97, debug_fallback=debug)
+        (h.square().mean() + mo.square().mean()).backward()
+        return [t.grad for t in ins]
+
+    for a, b in zip(run(False), run(True)):
+        torch.testing.assert_close(a, b, atol=5e-4, rtol=5e-4)

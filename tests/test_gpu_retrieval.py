@@ -1,0 +1,186 @@
+"""GPU parity of the retrieval path: gather (bit-exact), apply-query, routing
+(bit-exact indices and scores) and residual fusion, against the CPU oracle."""
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import oracle as orc
+from rnn_with_grm_amd import capi, cuda_ops
+
+pytestmark = pytest.mark.gpu
+
+
+def norm(x):
+    return torch.nn.functional.normalize(x, dim=-1)
+
+
+# ---------------------------------------------------------------- gather
+def test_gather_reference_cases(dev):
+    """The fixed index tensors of the reference's gather test
+    (examples/test_grm.py:197-221), bit-exact."""
+    g = torch.Generator().manual_seed(0)
+    mem = torch.randn(2, 7, 4, 5, generator=g)
+    chunk_idx = torch.tensor([[[1, 3], [2, 5], [0, 6]], [[4, 2], [1, 0], [3, 5]]], dtype=torch.long)
+    flat_idx = torch.tensor([[0, 2, 4], [1, 3, 5]], dtype=torch.long)
+    for idx in (chunk_idx, flat_idx):
+        out = torch.ops.grm_cuda.batched_memory_gather(mem.to(dev), idx.to(dev))
+        ref, bad = orc.gather(mem.numpy(), idx.numpy())
+        assert bad == 0
+        assert np.array_equal(out.cpu().numpy(), ref)
+        out2 = capi.batched_gather(mem.to(dev), idx.to(dev))
+        assert torch.equal(out, out2)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16, torch.float64, torch.int32])
+@pytest.mark.parametrize("shape", [(3, 11, 5, 3), (2, 9, 128, 128), (4, 6, 1, 1)])
+def test_gather_dtypes(dev, dtype, shape):
+    g = torch.Generator().manual_seed(1)
+    mem = (torch.randn(*shape, generator=g) * 100).to(dtype)
+    B, S = shape[:2]
+    idx = torch.randint(0, S, (B, 13, 3), generator=g)
+    out = cuda_ops.cuda_batched_memory_gather(mem.to(dev), idx.to(dev))
+    ref, _ = orc.gather(mem.numpy() if dtype != torch.bfloat16 else mem.view(torch.int16).numpy(), idx.numpy())
+    got = out.cpu()
+    got = got.view(torch.int16).numpy() if dtype == torch.bfloat16 else got.numpy()
+    assert np.array_equal(got, ref)
+
+
+def test_gather_int32_indices_and_bad_index(dev):
+    mem = torch.arange(2 * 4 * 3 * 2, dtype=torch.float32).reshape(2, 4, 3, 2)
+    idx = torch.tensor([[0, 3, 9], [-1, 2, 1]], dtype=torch.int32)
+    bad = torch.zeros(1, dtype=torch.int32, device=dev)
+    out = capi.batched_gather(mem.to(dev), idx.to(torch.int64).to(dev), bad_count=bad)
+    ref, nbad = orc.gather(mem.numpy(), idx.numpy())
+    assert int(bad.item()) == nbad == 2
+    assert np.array_equal(out.cpu().numpy(), ref)
+    # int32 indices through the op are widened to int64 like the reference
+    good = torch.tensor([[0, 3, 1], [2, 2, 1]], dtype=torch.int32)
+    out = torch.ops.grm_cuda.batched_memory_gather(mem.to(dev), good.to(dev))
+    assert np.array_equal(out.cpu().numpy(), orc.gather(mem.numpy(), good.numpy())[0])
+
+
+def test_gather_config3_slice(dev):
+    """BASELINE config 3 geometry with Q reduced to 256: 128x128 fp32 states,
+    S=256, k=8; bit-exact against index_select plus a checksum of checksums."""
+    B, S, Q, R, D = 64, 256, 256, 8, 128
+    g = torch.Generator().manual_seed(4)
+    mem = (torch.randn(B, S, D, D, generator=g) * 0.02).to(dev)
+    idx = torch.randint(0, S, (B, Q, R), generator=g).to(dev)
+    out = capi.batched_gather(mem, idx)
+    ref = torch.stack([mem[b].index_select(0, idx[b].reshape(-1)) for b in range(B)]).reshape(out.shape)
+    assert torch.equal(out, ref)
+    per_row = out.double().sum(dim=(-1, -2))
+    expect = mem.double().sum(dim=(-1, -2))
+    expect = torch.gather(expect, 1, idx.reshape(B, -1)).reshape(B, Q, R)
+    assert torch.equal(per_row, expect)
+
+
+# ---------------------------------------------------------------- apply query
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("shape", [(2, 3, 4, 5, 6), (4, 7, 8, 128, 128), (3, 5, 2, 9, 33), (2, 4, 16, 64)])
+def test_apply_query(dev, dtype, shape):
+    g = torch.Generator().manual_seed(2)
+    mem = torch.randn(*shape, generator=g).to(dtype)
+    qshape = shape[:2] + shape[-1:] if len(shape) == 5 else (shape[0], shape[-1])
+    q = norm(torch.randn(*qshape, generator=g)).to(dtype)
+    out = capi.apply_query_fwd(mem.to(dev), q.to(dev))
+    out_op = torch.ops.grm_cuda.apply_query_forward(mem.to(dev), q.to(dev))
+    assert torch.equal(out, out_op)
+    ref = orc.apply_query(mem.double().numpy(), q.double().numpy())
+    rtol, atol = (1e-5, 1e-5) if dtype == torch.float32 else (2e-2, 2e-3)
+    np.testing.assert_allclose(out.double().cpu().numpy(), ref, rtol=rtol, atol=atol)
+
+
+@pytest.mark.parametrize("shape", [(2, 3, 4, 5, 6), (2, 3, 8, 64, 128), (3, 4, 16, 64)])
+def test_apply_query_backward(dev, shape):
+    g = torch.Generator().manual_seed(3)
+    mem = torch.randn(*shape, generator=g)
+    qshape = shape[:2] + shape[-1:] if len(shape) == 5 else (shape[0], shape[-1])
+    q = norm(torch.randn(*qshape, generator=g))
+    dh = torch.randn(*shape[:-1], generator=g)
+    gm, gq = capi.apply_query_bwd(dh.to(dev), mem.to(dev), q.to(dev))
+    rgm, rgq = orc.apply_query_bwd(dh.double().numpy(), mem.double().numpy(), q.double().numpy())
+    np.testing.assert_allclose(gm.double().cpu().numpy(), rgm, rtol=1e-5, atol=1e-6)
+    np.testing.assert_allclose(gq.double().cpu().numpy(), rgq, rtol=1e-5, atol=1e-5)
+
+
+def test_apply_query_autograd_reference_case(dev):
+    """examples/test_grm.py:167-194: native vs fallback forward and grads at 1e-5."""
+    g = torch.Generator().manual_seed(9)
+    mem = torch.randn(2, 3, 4, 5, 6, generator=g)
+    q = norm(torch.randn(2, 3, 6, generator=g))
+
+    def run(debug):
+        mm = mem.to(dev).clone().requires_grad_(True)
+        qq = q.to(dev).clone().requires_grad_(True)
+        h = cuda_ops.cuda_apply_query(mm, qq, debug_fallback=debug)
+        h.square().mean().backward()
+        return h.detach(), mm.grad, qq.grad
+
+    for a, b in zip(run(False), run(True)):
+        torch.testing.assert_close(a, b, atol=1e-5, rtol=1e-5)
+
+
+# ---------------------------------------------------------------- routing
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32, torch.float16])
+@pytest.mark.parametrize("B,Q,S,D,k", [(2, 37, 256, 128, 8), (3, 300, 64, 512, 8), (1, 50, 512, 128, 16),
+                                       (2, 20, 5, 16, 8), (2, 33, 40, 24, 32), (1, 10, 9, 130, 1)])
+def test_topk_route_bit_exact(dev, dtype, B, Q, S, D, k):
+    g = torch.Generator().manual_seed(B * 7 + S)
+    q = norm(torch.randn(B, Q, D, generator=g)).to(dtype)
+    keys = norm(torch.randn(B, S, D, generator=g)).to(dtype)
+    scale = 1.0 / D ** 0.5
+    gates, idx, sc = capi.topk_route(q.to(dev), keys.to(dev), k, scale)
+    og, oi, osc = orc.topk_route(q.float().numpy(), keys.float().numpy(), k, scale)
+    assert np.array_equal(idx.cpu().numpy(), oi)
+    assert np.array_equal(sc.cpu().numpy(), osc)
+    np.testing.assert_allclose(gates.cpu().numpy(), og, rtol=1e-5, atol=1e-6)
+    g2, i2, s2 = torch.ops.grm_cuda.topk_route(q.to(dev), keys.to(dev), k, scale, 1.0)
+    assert torch.equal(i2, idx) and torch.equal(s2, sc) and torch.equal(g2, gates)
+
+
+def test_topk_route_ties(dev):
+    """Duplicate keys give equal scores; the lower index must win every tie."""
+    g = torch.Generator().manual_seed(6)
+    base = norm(torch.randn(2, 8, 64, generator=g))
+    keys = torch.cat([base, base, base[:, :3]], dim=1)  # each score appears 2-3 times
+    q = norm(torch.randn(2, 25, 64, generator=g))
+    gates, idx, sc = capi.topk_route(q.to(dev), keys.to(dev), 5, 0.125)
+    og, oi, osc = orc.topk_route(q.numpy(), keys.numpy(), 5, 0.125)
+    assert np.array_equal(idx.cpu().numpy(), oi)
+    i = idx.cpu()
+    s = sc.cpu()
+    # within equal scores, indices ascend
+    eq = s[..., 1:] == s[..., :-1]
+    assert bool((i[..., 1:][eq] > i[..., :-1][eq]).all())
+
+
+def test_topk_route_config3_slice(dev):
+    """BASELINE config 3 routing geometry (S=256, d=128, k=8, bf16) on 8 of the 64 (b,h) pairs."""
+    B, Q, S, D = 8, 2048, 256, 128
+    g = torch.Generator().manual_seed(0)
+    q = norm(torch.randn(B, Q, D, generator=g)).to(torch.bfloat16)
+    keys = norm(torch.randn(B, S, D, generator=g)).to(torch.bfloat16)
+    gates, idx, sc = capi.topk_route(q.to(dev), keys.to(dev), 8, 1.0 / D ** 0.5)
+    og, oi, osc = orc.topk_route(q.float().numpy(), keys.float().numpy(), 8, 1.0 / D ** 0.5)
+    assert np.array_equal(idx.cpu().numpy(), oi)
+    assert np.array_equal(sc.cpu().numpy(), osc)
+
+
+# ---------------------------------------------------------------- fusion
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("N,R,H,ln", [(37, 8, 128, True), (5, 3, 512, True), (9, 0, 64, True), (12, 4, 100, False)])
+def test_fuse_residual(dev, dtype, N, R, H, ln):
+    g = torch.Generator().manual_seed(N)
+    h = torch.randn(N, H, generator=g).to(dtype)
+    r = torch.randn(N, R, H, generator=g).to(dtype)
+    gt = torch.softmax(torch.randn(N, R, generator=g), -1) if R > 0 else torch.zeros(N, 0)
+    w = (1 + 0.1 * torch.randn(H, generator=g)).to(dtype) if ln else None
+    b = (0.1 * torch.randn(H, generator=g)).to(dtype) if ln else None
+    out = capi.fuse_residual(h.to(dev), r.to(dev), gt.to(dev), None if w is None else w.to(dev),
+                             None if b is None else b.to(dev))
+    ref = orc.fuse_residual(h.double().numpy(), r.double().numpy(), gt.double().numpy(),
+                            None if w is None else w.double().numpy(), None if b is None else b.double().numpy())
+    rtol, atol = (1e-5, 1e-5) if dtype == torch.float32 else (2e-2, 2e-2)
+    np.testing.assert_allclose(out.double().cpu().numpy(), ref, rtol=rtol, atol=atol)
