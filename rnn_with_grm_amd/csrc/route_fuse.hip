@@ -65,8 +65,10 @@ __global__ __launch_bounds__(RT) void route_kernel(const RouteArgs a) {
   const raw* kb = static_cast<const raw*>(a.keys) + b * S * D;
   const int64_t obase = (b * a.n_query + qi) * a.k;
 
-  // Running top-k, descending.  Slots at or past k hold +inf so they never
-  // move; the k-th best score is kept in thr for the cheap reject test.
+  // Running top-k, descending.  Slots at or past k only receive entries
+  // shifted out of the top k; the k-th best score is kept in thr for the
+  // cheap reject test, so a candidate enters the network only if it belongs
+  // in the top k.
   float top_s[KMAX];
   int top_i[KMAX];
   const int k = a.k;
@@ -141,12 +143,16 @@ __global__ __launch_bounds__(RT) void route_kernel(const RouteArgs a) {
         for (int s = 0; s < ns; ++s) {
           const float v = sbuf[s * RT + threadIdx.x];
           if (v > thr) {
-            // Lands after every kept entry with an equal score (lower index).
+            // The new entry lands after every kept entry with an equal score
+            // (those have lower indices); from there on every entry shifts
+            // down one slot, keeping equal scores in index order.
             float cs = v;
             int ci = static_cast<int>(s0 + s);
+            bool shift = false;
 #pragma unroll
             for (int m = 0; m < KMAX; ++m) {
-              if (cs > top_s[m]) {
+              shift = shift || (cs > top_s[m]);
+              if (shift) {
                 const float ts = top_s[m];
                 const int ti = top_i[m];
                 top_s[m] = cs;

@@ -1,0 +1,183 @@
+"""The Python op surface on CPU: runtime status, kernel policies, the CPU-key
+implementations of torch.ops.grm_cuda and the PyTorch fallbacks, all checked
+against the oracle.  Mirrors the reference's own checks in
+examples/test_grm.py:29-221 where they apply to CPU tensors."""
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import oracle as orc
+from rnn_with_grm_amd import cuda_ops
+
+
+def make_chunk_case(T, B=2, H=16, K=8, dtype=torch.float32, seed=0):
+    g = torch.Generator().manual_seed(seed)
+    k = torch.nn.functional.normalize(torch.randn(B, T, K, generator=g), dim=-1).to(dtype)
+    v = torch.randn(B, T, H, generator=g).to(dtype)
+    q = torch.nn.functional.normalize(torch.randn(B, T, K, generator=g), dim=-1).to(dtype)
+    m = torch.randn(B, H, K, generator=g).to(dtype)
+    return k, v, q, m
+
+
+def np64(t):
+    return t.detach().double().numpy()
+
+
+def test_runtime_status_payload():
+    """Same keys, policy values and dispatch consistency as examples/test_grm.py:116-151."""
+    status = cuda_ops.get_grm_cuda_runtime_status()
+    for key in ("load_attempted", "extension_loaded", "compiled_with_cuda_sources", "compiled_with_cuda_kernels",
+                "torch_cuda_available", "cuda_backend_available", "load_error", "module_name", "registered_ops",
+                "dispatch_kernels", "kernel_policy"):
+        assert key in status
+    assert set(status["kernel_policy"]) == {"global", "chunk_update", "apply_query", "batched_memory_gather"}
+    assert all(p in {"auto", "native", "fallback"} for p in status["kernel_policy"].values())
+    assert status["extension_loaded"], status["load_error"]
+    assert status["compiled_with_cuda_sources"] and status["compiled_with_cuda_kernels"]
+    assert all(d["cuda"] for d in status["dispatch_kernels"].values())
+    assert all(status["registered_ops"].values())
+    assert status["hip"]["arch"] == "gfx950"
+    assert all(status["hip"]["extra_ops"].values())
+    assert status["cuda_backend_available"] == torch.cuda.is_available()
+
+
+def test_policy_precedence(monkeypatch):
+    monkeypatch.setenv("GRM_CUDA_KERNEL_POLICY", "fallback")
+    monkeypatch.setenv("GRM_CUDA_CHUNK_UPDATE_POLICY", "native")
+    monkeypatch.setenv("GRM_CUDA_APPLY_QUERY_POLICY", "bogus")
+    assert cuda_ops._get_kernel_policy("chunk_update") == "native"  # per-op beats global
+    assert cuda_ops._get_kernel_policy("apply_query") == "fallback"  # invalid per-op value is ignored
+    assert cuda_ops._get_kernel_policy("batched_memory_gather") == "fallback"
+    assert cuda_ops._get_kernel_policy("") == "fallback"
+    monkeypatch.delenv("GRM_CUDA_KERNEL_POLICY")
+    assert cuda_ops._get_kernel_policy("batched_memory_gather") == "auto"
+
+
+def test_gpu_tensor_without_extension_raises(monkeypatch):
+    monkeypatch.setattr(cuda_ops, "_EXTENSION_MODULE", None)
+    monkeypatch.setattr(cuda_ops, "_EXTENSION_LOAD_ATTEMPTED", True)
+    monkeypatch.setattr(cuda_ops, "_EXTENSION_LOAD_ERROR", "simulated import failure")
+    with pytest.raises(cuda_ops.GrmExtensionUnavailable, match="simulated import failure"):
+        cuda_ops._require_extension(torch.device("cuda"))
+    assert cuda_ops._require_extension(torch.device("cpu")) is False
+    status = cuda_ops.get_grm_cuda_runtime_status()
+    assert status["extension_loaded"] is False and status["load_error"] == "simulated import failure"
+
+
+@pytest.mark.parametrize("T", [0, 1, 8, 64, 100])
+@pytest.mark.parametrize("dtype,tol", [(torch.float64, 1e-12), (torch.float32, 1e-5)])
+def test_cpu_chunk_update_forward(T, dtype, tol):
+    k, v, q, m = make_chunk_case(T, dtype=dtype, seed=T)
+    h, mo, aux = torch.ops.grm_cuda.chunk_update_forward(k, v, q, m, 0.97)
+    assert aux.numel() == 0 and h.dtype == dtype and mo.dtype == dtype
+    rh, rm, _ = orc.chunk_update_seq(np64(k), np64(v), np64(q), np64(m), 0.97)
+    np.testing.assert_allclose(np64(h), rh, rtol=tol, atol=tol)
+    np.testing.assert_allclose(np64(mo), rm, rtol=tol, atol=tol)
+
+
+def test_cpu_chunk_update_backward():
+    k, v, q, m = make_chunk_case(70, H=12, K=6, dtype=torch.float64, seed=3)
+    g = torch.Generator().manual_seed(4)
+    dh = torch.randn(2, 70, 12, generator=g, dtype=torch.float64)
+    dm = torch.randn(2, 12, 6, generator=g, dtype=torch.float64)
+    grads = torch.ops.grm_cuda.chunk_update_backward(dh, dm, k, v, q, m, torch.empty(0), 0.9)
+    ref = orc.chunk_update_bwd(np64(dh), np64(dm), np64(k), np64(v), np64(q), np64(m), 0.9)
+    for got, want in zip(grads, ref):
+        np.testing.assert_allclose(np64(got), want, rtol=1e-10, atol=1e-12)
+
+
+def test_entrypoint_parity_reference_case():
+    """examples/test_grm.py:40-113 on CPU: chunk 8, native (CPU op) vs fallback, forward and grads at 1e-5."""
+    k, v, q, m = make_chunk_case(8, seed=11)
+
+    def run(debug, policy):
+        ins = [t.clone().requires_grad_(True) for t in (k, v, q, m)]
+        h, mo = cuda_ops.cuda_chunk_update(*ins, memory_decay=0.97, debug_fallback=debug)
+        (h.square().mean() + mo.square().mean()).backward()
+        return [h.detach(), mo.detach()] + [t.grad for t in ins]
+
+    ref = run(True, None)
+    import os
+    os.environ["GRM_CUDA_CHUNK_UPDATE_POLICY"] = "native"
+    try:
+        live = run(False, "native")
+    finally:
+        del os.environ["GRM_CUDA_CHUNK_UPDATE_POLICY"]
+    for a, b in zip(live, ref):
+        torch.testing.assert_close(a, b, atol=1e-5, rtol=1e-5)
+
+
+def test_fallback_chunk_update_matches_oracle():
+    k, v, q, m = make_chunk_case(64, dtype=torch.float64, seed=5)
+    h, mo = cuda_ops._vectorized_chunk_update(k, v, q, m, 0.97)
+    rh, rm, _ = orc.chunk_update_seq(np64(k), np64(v), np64(q), np64(m), 0.97)
+    np.testing.assert_allclose(np64(h), rh, rtol=1e-12, atol=1e-12)
+    np.testing.assert_allclose(np64(mo), rm, rtol=1e-12, atol=1e-12)
+
+
+@pytest.mark.parametrize("seg", [64, 30, 1])
+def test_cpu_segment_scan(seg):
+    k, v, q, m = make_chunk_case(130, H=8, K=16, dtype=torch.float64, seed=seg)
+    h, mo, snaps = torch.ops.grm_cuda.segment_scan_forward(k, v, q, m, 0.97, seg)
+    rh, rm, rs = orc.chunk_update_seq(np64(k), np64(v), np64(q), np64(m), 0.97, seg)
+    np.testing.assert_allclose(np64(h), rh, rtol=1e-12, atol=1e-12)
+    np.testing.assert_allclose(np64(snaps), rs, rtol=1e-6, atol=1e-7)  # snapshots are float32
+    h2, mo2, snaps2 = cuda_ops.cuda_segment_scan(k, v, q, m, 0.97, seg, debug_fallback=True)
+    np.testing.assert_allclose(np64(h2), rh, rtol=1e-12, atol=1e-12)
+    np.testing.assert_allclose(np64(snaps2), rs, rtol=1e-6, atol=1e-7)
+
+
+def test_cpu_gather_reference_cases():
+    g = torch.Generator().manual_seed(0)
+    mem = torch.randn(2, 7, 4, 5, generator=g)
+    for idx in (torch.tensor([[[1, 3], [2, 5], [0, 6]], [[4, 2], [1, 0], [3, 5]]]),
+                torch.tensor([[0, 2, 4], [1, 3, 5]])):
+        live = cuda_ops.cuda_batched_memory_gather(mem, idx)
+        ref = cuda_ops.cuda_batched_memory_gather(mem, idx, debug_fallback=True)
+        torch.testing.assert_close(live, ref, atol=0.0, rtol=0.0)
+        assert np.array_equal(live.numpy(), orc.gather(mem.numpy(), idx.numpy())[0])
+
+
+def test_cpu_apply_query_and_backward():
+    g = torch.Generator().manual_seed(1)
+    mem = torch.randn(2, 3, 4, 5, 6, generator=g, dtype=torch.float64)
+    q = torch.nn.functional.normalize(torch.randn(2, 3, 6, generator=g, dtype=torch.float64), dim=-1)
+    out = torch.ops.grm_cuda.apply_query_forward(mem, q)
+    np.testing.assert_allclose(np64(out), orc.apply_query(np64(mem), np64(q)), rtol=1e-13)
+    dh = torch.randn(2, 3, 4, 5, generator=g, dtype=torch.float64)
+    gm, gq = torch.ops.grm_cuda.apply_query_backward(dh, mem, q)
+    rgm, rgq = orc.apply_query_bwd(np64(dh), np64(mem), np64(q))
+    np.testing.assert_allclose(np64(gm), rgm, rtol=1e-13)
+    np.testing.assert_allclose(np64(gq), rgq, rtol=1e-12)
+
+
+@pytest.mark.parametrize("S,k", [(50, 8), (6, 8), (40, 32)])
+def test_cpu_topk_route_bit_exact(S, k):
+    g = torch.Generator().manual_seed(S)
+    q = torch.nn.functional.normalize(torch.randn(3, 21, 24, generator=g), dim=-1).to(torch.bfloat16)
+    keys = torch.nn.functional.normalize(torch.randn(3, S, 24, generator=g), dim=-1).to(torch.bfloat16)
+    gates, idx, sc = cuda_ops.cuda_topk_route(q, keys, k, 24 ** -0.5)
+    og, oi, osc = orc.topk_route(q.float().numpy(), keys.float().numpy(), k, 24 ** -0.5)
+    assert np.array_equal(idx.numpy(), oi) and np.array_equal(sc.numpy(), osc)
+    np.testing.assert_allclose(gates.numpy(), og, rtol=1e-6)
+
+
+def test_cpu_fuse_residual():
+    g = torch.Generator().manual_seed(2)
+    h, r = torch.randn(5, 32, generator=g), torch.randn(5, 3, 32, generator=g)
+    gt = torch.softmax(torch.randn(5, 3, generator=g), -1)
+    w, b = torch.randn(32, generator=g), torch.randn(32, generator=g)
+    out = cuda_ops.cuda_fuse_residual(h, r, gt, w, b)
+    ref = orc.fuse_residual(np64(h), np64(r), np64(gt), np64(w), np64(b))
+    np.testing.assert_allclose(out.numpy(), ref, rtol=1e-5, atol=1e-5)
+
+
+def test_shape_errors_raise_like_reference():
+    k, v, q, m = make_chunk_case(4)
+    with pytest.raises(RuntimeError, match="keys must have shape"):
+        torch.ops.grm_cuda.chunk_update_forward(k[0], v, q, m, 0.9)
+    with pytest.raises(RuntimeError, match="memory hidden dim"):
+        torch.ops.grm_cuda.chunk_update_forward(k, v, q, m[:, :3], 0.9)
+    with pytest.raises(RuntimeError, match="topk_indices must have shape"):
+        torch.ops.grm_cuda.batched_memory_gather(torch.randn(2, 3, 4, 5), torch.zeros(2, dtype=torch.long))
