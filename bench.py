@@ -80,10 +80,13 @@ def bench_c2(torch, dev, steps, warmup):
     hidden = torch.empty((BH, T, D), dtype=torch.bfloat16, device=dev)
     mem_out = torch.empty((BH, D, D), dtype=torch.float32, device=dev)
     snaps = torch.empty((BH, T // 64, D, D), dtype=torch.float32, device=dev)
+    wsb = capi.fwd_workspace_bytes(BH, T, D, D, 64)
+    ws = torch.empty(max(wsb // 4, 1), dtype=torch.float32, device=dev)
     stream = torch.cuda.current_stream(dev)
     sp = ctypes.c_void_p(stream.cuda_stream)
     P = lambda t: ctypes.c_void_p(t.data_ptr())  # noqa: E731
-    args = (P(k), P(v), P(q), P(m), P(hidden), P(mem_out), P(snaps), BH, T, D, D, capi.BF16, capi.F32, 0.97, 64, sp)
+    args = (P(k), P(v), P(q), P(m), P(hidden), P(mem_out), P(snaps), P(ws), wsb, BH, T, D, D, capi.BF16, capi.F32,
+            0.97, 64, sp)
 
     def step():
         rc = lib.grm_hip_chunk_update_fwd(*args)
@@ -171,7 +174,10 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-gather", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--c2-only", action="store_true", help="only the headline kernel (quick sweeps)")
     a = ap.parse_args()
+    if a.c2_only:
+        a.no_gather = a.no_cpu = True
     if a.gpus != 1:
         print(f"bench.py measures one GPU only; --gpus {a.gpus} is not supported in this build "
               "(the hot path shards with zero communication over (b,h) sequences; see the design notes)",

@@ -62,13 +62,24 @@ uint64_t grm_hip_launch_count(void);
  *             is the final state).  This is the whole-sequence form of the op:
  *             one call covers every segment of a sequence.
  * snapshot_len: tokens per snapshot (> 0) when snapshots != NULL, ignored otherwise.
- * Limits: 1 <= key_dim <= 256, value_dim >= 1; seq_len >= 0; batch >= 0.
+ * workspace:  optional device scratch of workspace_bytes (16-byte aligned).  With
+ *             at least grm_hip_chunk_update_fwd_workspace() bytes, long sequences
+ *             are split into time parts scanned in parallel (two launches);
+ *             with less (or NULL) each sequence is scanned by one workgroup chain.
+ *             Results are the same either way up to float rounding.
+ * Limits: 1 <= key_dim <= 256 (<= 128 for float32 inputs), value_dim >= 1;
+ * seq_len >= 0; batch >= 0.
  */
 int grm_hip_chunk_update_fwd(const void* keys, const void* values, const void* queries,
                              const void* memory, void* hidden, void* memory_out, float* snapshots,
-                             int64_t batch, int64_t seq_len, int64_t key_dim, int64_t value_dim,
-                             int in_dtype, int mem_dtype, double memory_decay,
-                             int64_t snapshot_len, void* stream);
+                             void* workspace, int64_t workspace_bytes, int64_t batch,
+                             int64_t seq_len, int64_t key_dim, int64_t value_dim, int in_dtype,
+                             int mem_dtype, double memory_decay, int64_t snapshot_len, void* stream);
+
+/* Workspace bytes grm_hip_chunk_update_fwd can use for these sizes (0: none).
+ * No counterpart in the reference (its kernel walks each sequence serially). */
+int64_t grm_hip_chunk_update_fwd_workspace(int64_t batch, int64_t seq_len, int64_t key_dim,
+                                           int64_t value_dim, int64_t snapshot_len);
 
 /*
  * Gradient of grm_hip_chunk_update_fwd.

@@ -28,7 +28,9 @@ SIGNATURES = {
     "grm_hip_abi_version": (ctypes.c_int, []),
     "grm_hip_last_error": (ctypes.c_char_p, []),
     "grm_hip_launch_count": (ctypes.c_uint64, []),
-    "grm_hip_chunk_update_fwd": (_C, [_P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _C, _C, ctypes.c_double, _I, _P]),
+    "grm_hip_chunk_update_fwd": (_C, [_P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _C, _C, ctypes.c_double,
+                                      _I, _P]),
+    "grm_hip_chunk_update_fwd_workspace": (_I, [_I, _I, _I, _I, _I]),
     "grm_hip_chunk_update_bwd": (_C, [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _C, _C,
                                       ctypes.c_double, _P]),
     "grm_hip_apply_query_fwd": (_C, [_P, _P, _P, _I, _I, _I, _I, _I, _C, _P]),
@@ -85,8 +87,13 @@ def _check(rc: int, what: str) -> None:
         raise RuntimeError(f"{what} failed ({rc}): {last_error()}")
 
 
-def chunk_update_fwd(keys, values, queries, memory, decay: float, snapshot_len: int = 0):
-    """Returns (hidden, memory_out, snapshots or None); inputs must be contiguous device tensors."""
+def fwd_workspace_bytes(B: int, T: int, K: int, H: int, snapshot_len: int = 0) -> int:
+    return int(load().grm_hip_chunk_update_fwd_workspace(B, T, K, H, snapshot_len))
+
+
+def chunk_update_fwd(keys, values, queries, memory, decay: float, snapshot_len: int = 0, split: bool = True):
+    """Returns (hidden, memory_out, snapshots or None); inputs must be contiguous device tensors.
+    split=False withholds the workspace, so each sequence is scanned by one workgroup chain."""
     B, T, K = keys.shape
     H = values.shape[2]
     hidden = torch.empty((B, T, H), dtype=values.dtype, device=values.device)
@@ -95,10 +102,12 @@ def chunk_update_fwd(keys, values, queries, memory, decay: float, snapshot_len: 
     if snapshot_len > 0:
         snaps = torch.empty((B, (T + snapshot_len - 1) // snapshot_len, H, K), dtype=torch.float32,
                             device=keys.device)
+    wsb = fwd_workspace_bytes(B, T, K, H, snapshot_len) if split else 0
+    ws = torch.empty((max(wsb, 4) + 3) // 4, dtype=torch.float32, device=keys.device) if wsb else None
     rc = load().grm_hip_chunk_update_fwd(_ptr(keys), _ptr(values), _ptr(queries), _ptr(memory), _ptr(hidden),
-                                         _ptr(memory_out), _ptr(snaps), B, T, K, H, dtype_code(keys.dtype),
-                                         dtype_code(memory.dtype), float(decay), int(snapshot_len),
-                                         _stream(keys))
+                                         _ptr(memory_out), _ptr(snaps), _ptr(ws), wsb, B, T, K, H,
+                                         dtype_code(keys.dtype), dtype_code(memory.dtype), float(decay),
+                                         int(snapshot_len), _stream(keys))
     _check(rc, "grm_hip_chunk_update_fwd")
     return hidden, memory_out, snaps
 

@@ -26,10 +26,6 @@
 #include "grm_hip.h"
 #include "grm_hip_common.h"
 
-extern "C" int grm_hip_chunk_update_fwd(const void*, const void*, const void*, const void*, void*,
-                                        void*, float*, int64_t, int64_t, int64_t, int64_t, int, int,
-                                        double, int64_t, void*);
-
 namespace grmhip {
 namespace {
 
@@ -288,8 +284,9 @@ extern "C" int grm_hip_chunk_update_bwd(const void* grad_hidden, const void* gra
     set_error("chunk_update_bwd: unsupported dtypes in=%d mem=%d", in_dtype, mem_dtype);
     return GRM_HIP_EUNSUPPORTED;
   }
-  if (key_dim > 256) {
-    set_error("chunk_update_bwd: key_dim %lld > 256", (long long)key_dim);
+  if (key_dim > 256 || (in_dtype == GRM_HIP_F32 && key_dim > 128)) {
+    set_error("chunk_update_bwd: key_dim %lld exceeds %d for this dtype", (long long)key_dim,
+              in_dtype == GRM_HIP_F32 ? 128 : 256);
     return GRM_HIP_EUNSUPPORTED;
   }
   if (!std::isfinite(memory_decay)) {
@@ -327,8 +324,8 @@ extern "C" int grm_hip_chunk_update_bwd(const void* grad_hidden, const void* gra
   // Re-run the forward to store the state after every 64-token chunk; its
   // hidden output and final state are not needed.
   int rc = grm_hip_chunk_update_fwd(keys, values, queries, memory, nullptr, nullptr, chunk_states,
-                                    batch, seq_len, key_dim, value_dim, in_dtype, mem_dtype,
-                                    memory_decay, BCT, stream);
+                                    nullptr, 0, batch, seq_len, key_dim, value_dim, in_dtype,
+                                    mem_dtype, memory_decay, BCT, stream);
   if (rc != GRM_HIP_OK) return rc;
 
   BwdArgs a;

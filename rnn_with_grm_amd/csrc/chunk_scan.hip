@@ -37,6 +37,7 @@ constexpr int CT = 64;         // token rows per chunk tile
 constexpr int NW = 4;          // waves per workgroup
 constexpr int NTHR = 64 * NW;  // threads per workgroup
 constexpr int PW_N = CT + 1;   // decay^0 .. decay^64
+constexpr size_t kMaxLds = 160 * 1024;  // LDS per CU on gfx950
 
 struct ChunkFwdArgs {
   const void* keys;
@@ -56,11 +57,12 @@ struct ChunkFwdArgs {
   int n_snap;
   int v_tiles;     // workgroups per sequence
   int mem_f32;     // memory / memory_out are float32 (else the input dtype)
-  int vec_k;       // keys/queries rows allow 8-element vector loads
-  int vec_v;       // values rows allow 8-element vector loads
-  int vec_o;       // hidden rows allow 4-element vector stores
   int vec_m;       // memory/memory_out/snapshot rows allow 4-element vector access
   int xcd_remap;   // grid is a multiple of 8: place a sequence's tiles on one XCD
+  int n_parts;     // time parts per sequence (1 = one workgroup walks the whole sequence)
+  int part_chunks; // chunks per part; every part but the last is full
+  float part_decay;   // decay^(part_chunks * chunk)
+  float* part_states; // [batch, n_parts - 1, dv, dk]: end-state contribution of each part
   float c;         // (1 - decay) / sqrt(d_k)
   float pw[PW_N];  // decay^n rounded from double
 };
@@ -135,35 +137,54 @@ __device__ __forceinline__ void store_state4(void* base, int64_t off, int col, i
 template <class E, int DKP, int DV>
 struct FwdShape {
   using raw = typename ET<E>::raw;
-  static constexpr int KS = DKP + 8;  // LDS row stride (elements) of K and of the state copy
-  static constexpr int VS = CT + 4;   // LDS row stride (elements) of V^T
+  static constexpr int KS = DKP + 8;  // LDS row stride (elements) of K, Q and the state copy
+  static constexpr int TS = CT + 4;   // LDS row stride (elements) of K^T, V^T and weighted V^T
   static constexpr int NKK = DKP / 32;
   static constexpr int VT = DV / 16;
   static constexpr int KT = DKP / 16;
   static constexpr int KTW = (KT + NW - 1) / NW;  // state key-tiles per wave
   static constexpr int NJP = CT / 32;             // 32-token slices of a chunk
+  static constexpr int NCU = DKP / 8;             // 8-element units per K/Q row
   static constexpr int K_UNITS = CT * DKP / 8 / NTHR;
   static constexpr int V_UNITS = CT * DV / 8;     // <= NTHR
-  static constexpr size_t lds_bytes =
-      (static_cast<size_t>(CT) * KS + static_cast<size_t>(DV) * KS + static_cast<size_t>(DV) * VS) *
-          sizeof(raw) +
-      PW_N * sizeof(float);
+  static constexpr size_t lds_elems = 2 * static_cast<size_t>(CT) * KS  // Ks, Qs
+                                      + static_cast<size_t>(DKP) * TS    // Kt
+                                      + static_cast<size_t>(DV) * KS     // Mb
+                                      + 2 * static_cast<size_t>(DV) * TS;  // Vt, Vw
+  static constexpr size_t lds_bytes = lds_elems * sizeof(raw) + PW_N * sizeof(float);
   static_assert(K_UNITS * NTHR * 8 == CT * DKP, "K tile must split evenly over the workgroup");
   static_assert(V_UNITS <= NTHR, "V tile must fit one unit per thread");
+  static_assert(NTHR % (16 * NCU) == 0 || (16 * NCU) % NTHR == 0, "row/unit map");
 };
 
-template <class E, int DKP, int DV>
+// Staging depth: the loads for chunk c+PF are issued while chunk c computes,
+// so each load has PF chunk-times to arrive (global latency is about 3 us,
+// a chunk computes in about 1 us).  32-wide tiles stage 2 deep so that two
+// waves fit per SIMD (VGPR + AGPR <= 256); 16-wide tiles fit with 3.
+template <int DV>
+constexpr int prefetch_depth() { return DV >= 32 ? 2 : 3; }
+
+// FULL = true: the fused scan (hidden, snapshots, final state) over one time
+// part, starting from the state the earlier parts leave behind.
+// FULL = false: the state-only pass that gives each part's end-state
+// contribution from a zero start (keys and values only; no S, no outputs).
+template <class E, int DKP, int DV, bool VEC, bool FULL>
 __global__ __launch_bounds__(NTHR) void chunk_fwd_kernel(const ChunkFwdArgs a) {
   using S = FwdShape<E, DKP, DV>;
   using raw = typename ET<E>::raw;
-  constexpr int KS = S::KS, VS = S::VS, NKK = S::NKK, VT = S::VT, KT = S::KT, KTW = S::KTW,
-                NJP = S::NJP, K_UNITS = S::K_UNITS, V_UNITS = S::V_UNITS;
+  constexpr int KS = S::KS, TS = S::TS, NKK = S::NKK, VT = S::VT, KT = S::KT, KTW = S::KTW,
+                NJP = S::NJP, NCU = S::NCU, K_UNITS = S::K_UNITS, V_UNITS = S::V_UNITS;
+  constexpr int ES = static_cast<int>(sizeof(raw));
+  constexpr int PF = prefetch_depth<DV>();
 
   extern __shared__ __align__(16) unsigned char smem[];
-  raw* Ks = reinterpret_cast<raw*>(smem);        // [CT][KS]   keys of the chunk
-  raw* Mb = Ks + CT * KS;                        // [DV][KS]   state copy, row = value index
-  raw* Vt = Mb + DV * KS;                        // [DV][VS]   values of the chunk, transposed
-  float* pw = reinterpret_cast<float*>(Vt + DV * VS);  // [PW_N]
+  raw* Ks = reinterpret_cast<raw*>(smem);  // [CT][KS]   keys, row = token
+  raw* Qs = Ks + CT * KS;                  // [CT][KS]   queries, row = token
+  raw* Kt = Qs + CT * KS;                  // [DKP][TS]  keys transposed, row = key index
+  raw* Mb = Kt + DKP * TS;                 // [DV][KS]   state copy, row = value index
+  raw* Vt = Mb + DV * KS;                  // [DV][TS]   values transposed, row = value index
+  raw* Vw = Vt + DV * TS;                  // [DV][TS]   c * decay^{L-1-j} * values, transposed
+  float* pw = reinterpret_cast<float*>(Vw + DV * TS);  // [PW_N]
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -176,14 +197,21 @@ __global__ __launch_bounds__(NTHR) void chunk_fwd_kernel(const ChunkFwdArgs a) {
     const int per = gridDim.x >> 3;
     wg = (wg & 7) * per + (wg >> 3);
   }
-  const int64_t b = wg / a.v_tiles;
+  // workgroup -> (sequence b, time part, value tile); tiles of one (b, part)
+  // are adjacent so they share an XCD and its L2.
+  const int parts_in_grid = FULL ? a.n_parts : a.n_parts - 1;
+  const int seq = wg / a.v_tiles;
+  const int64_t b = seq / parts_in_grid;
+  const int part = seq % parts_in_grid;
   const int v0 = (wg % a.v_tiles) * DV;
   const int dk = a.dk, dv = a.dv;
   const int64_t T = a.seq_len;
   const int chunk = a.chunk;
+  const int n_chunks = a.n_chunks;
+  const int c_begin = part * a.part_chunks;
+  const int c_end = min(c_begin + a.part_chunks, n_chunks);
   const bool f32m = a.mem_f32 != 0;
-  const bool vec_k = a.vec_k != 0, vec_v = a.vec_v != 0, vec_o = a.vec_o != 0,
-             vec_m = a.vec_m != 0;
+  const bool vec_m = a.vec_m != 0;
 
   const raw* keys = static_cast<const raw*>(a.keys) + b * T * dk;
   const raw* queries = static_cast<const raw*>(a.queries) + b * T * dk;
@@ -201,52 +229,96 @@ __global__ __launch_bounds__(NTHR) void chunk_fwd_kernel(const ChunkFwdArgs a) {
 #pragma unroll
     for (int vt = 0; vt < VT; ++vt) {
       const int v = v0 + 16 * vt + n;
-      st[q][vt] = (kt < KT) ? load_state4<E>(a.memory, (b * dv + v) * dk, 16 * kt + 4 * g, dk,
-                                             v < dv, f32m, vec_m)
-                            : f32x4{0.f, 0.f, 0.f, 0.f};
+      st[q][vt] = (FULL && kt < KT) ? load_state4<E>(a.memory, (b * dv + v) * dk, 16 * kt + 4 * g,
+                                                     dk, v < dv, f32m, vec_m)
+                                    : f32x4{0.f, 0.f, 0.f, 0.f};
+      // Start of part p: M_p = part_decay * M_{p-1} + D_{p-1}, from M_0 = memory.
+      if (FULL && kt < KT) {
+        for (int pp = 0; pp < part; ++pp) {
+          const f32x4 d = load_state4<F32>(a.part_states, ((b * (a.n_parts - 1) + pp) * dv + v) * dk,
+                                           16 * kt + 4 * g, dk, v < dv, true, vec_m);
+          st[q][vt] = st[q][vt] * a.part_decay + d;
+        }
+      }
     }
   }
 
-  // ---- chunk staging (global -> registers -> LDS)
-  U8<E> kst[K_UNITS];
-  U8<E> vst;
-  Frag8<E> qf[NKK], qn[NKK];
   const int i_loc = 16 * w + n;  // this lane's query row within a chunk
-
-  auto load_chunk = [&](int c, U8<E>* kd, U8<E>& vd, Frag8<E>* qd) {
+  // Tokens of chunk c; 0 outside this workgroup's part, so prefetches past
+  // the part read nothing.
+  auto chunk_len = [&](int c) -> int {
     const int64_t t0 = static_cast<int64_t>(c) * chunk;
-    const int L = static_cast<int>(min(static_cast<int64_t>(chunk), T - t0));
+    return (c < c_end) ? static_cast<int>(min(static_cast<int64_t>(chunk), T - t0)) : 0;
+  };
+  // Unit u of this thread covers K/Q row unit_row(u), elements unit_col(u) .. +8.
+  // A wave's 64 units span 16 rows x 4 column units, so the transposed LDS
+  // writes of K land on distinct banks.
+  auto unit_row = [&](int u) {
+    const int l = tid + NTHR * u;
+    return (l & 15) + 16 * (l / (16 * NCU));
+  };
+  auto unit_col = [&](int u) { return ((tid + NTHR * u) / 16 % NCU) * 8; };
+
+  // ---- staging (global -> registers -> LDS).  Each chunk gets buffer
+  // resources that end at its last valid row, so rows past the chunk (and
+  // every row past the last chunk) read as zero; columns past d_k / d_v are
+  // sent out of range with an offset select.
+  struct Stage {
+    U8<E> k[K_UNITS];
+    U8<E> q[K_UNITS];
+    U8<E> v;
+  };
+  auto load8 = [&](__amdgpu_buffer_rsrc_t r, int row_off, int col, int ncols) -> U8<E> {
+    if constexpr (VEC) {
+      return buf_load8<E>(r, col < ncols ? row_off + col * ES : kBufOOB);
+    } else {
+      U8<E> u;
 #pragma unroll
-    for (int u = 0; u < K_UNITS; ++u) {
-      const int idx = tid + NTHR * u;
-      const int row = idx / (DKP / 8);
-      const int col = (idx % (DKP / 8)) * 8;
-      kd[u] = load_u8<E>(keys + (t0 + row) * dk, col, dk, row < L, vec_k);
-    }
-    if (V_UNITS == NTHR || tid < V_UNITS) {
-      const int row = tid / (DV / 8);
-      const int col = v0 + (tid % (DV / 8)) * 8;
-      vd = load_u8<E>(values + (t0 + row) * dv, col, dv, row < L, vec_v);
-    }
-#pragma unroll
-    for (int kk = 0; kk < NKK; ++kk) {
-      U8<E> u = load_u8<E>(queries + (t0 + i_loc) * dk, 32 * kk + 8 * g, dk, i_loc < L, vec_k);
-      qd[kk] = __builtin_bit_cast(Frag8<E>, u);
+      for (int i = 0; i < 8; ++i) u.e[i] = buf_load1<E>(r, col + i < ncols ? row_off + (col + i) * ES : kBufOOB);
+      return u;
     }
   };
-  auto store_chunk = [&](const U8<E>* kd, const U8<E>& vd) {
+  auto load_chunk = [&](int c, Stage& sg) {
+    const int64_t t0 = static_cast<int64_t>(c) * chunk;
+    const int L = chunk_len(c);
+    const __amdgpu_buffer_rsrc_t rk = make_rsrc(keys + t0 * dk, static_cast<uint32_t>(L * dk * ES));
+    const __amdgpu_buffer_rsrc_t rq = make_rsrc(queries + t0 * dk, static_cast<uint32_t>(L * dk * ES));
+    const __amdgpu_buffer_rsrc_t rv = make_rsrc(values + t0 * dv, static_cast<uint32_t>(L * dv * ES));
 #pragma unroll
     for (int u = 0; u < K_UNITS; ++u) {
-      const int idx = tid + NTHR * u;
-      const int row = idx / (DKP / 8);
-      const int col = (idx % (DKP / 8)) * 8;
-      *reinterpret_cast<U8<E>*>(Ks + row * KS + col) = kd[u];
+      sg.k[u] = load8(rk, unit_row(u) * dk * ES, unit_col(u), dk);
+      if constexpr (FULL) sg.q[u] = load8(rq, unit_row(u) * dk * ES, unit_col(u), dk);
+    }
+    // Threads past the V tile load an out-of-range unit (zeros) so the load
+    // stays unconditional and never forces an early wait.
+    const int row = (tid % 16) + 16 * (tid / (16 * (DV / 8)));
+    const int col = v0 + ((tid / 16) % (DV / 8)) * 8;
+    sg.v = load8(rv, row * dv * ES, (V_UNITS == NTHR || tid < V_UNITS) ? col : dv, dv);
+  };
+  // K and Q go to LDS row-major (S / O operands), K also transposed
+  // (state-update operand); V goes transposed, plain (O operand) and scaled
+  // by c * decay^{L-1-j} (state-update operand), L being the staged chunk's length.
+  auto store_chunk = [&](int c, const Stage& sg) {
+#pragma unroll
+    for (int u = 0; u < K_UNITS; ++u) {
+      const int row = unit_row(u), col = unit_col(u);
+      if constexpr (FULL) {
+        *reinterpret_cast<U8<E>*>(Ks + row * KS + col) = sg.k[u];
+        *reinterpret_cast<U8<E>*>(Qs + row * KS + col) = sg.q[u];
+      }
+#pragma unroll
+      for (int e = 0; e < 8; ++e) Kt[(col + e) * TS + row] = sg.k[u].e[e];
     }
     if (V_UNITS == NTHR || tid < V_UNITS) {
-      const int row = tid / (DV / 8);
-      const int c8 = tid % (DV / 8);
+      const int L = chunk_len(c);
+      const int row = (tid % 16) + 16 * (tid / (16 * (DV / 8)));
+      const int c8 = (tid / 16) % (DV / 8);
+      const float wj = (row < L) ? a.c * pw[max(L - 1 - row, 0)] : 0.f;
 #pragma unroll
-      for (int e = 0; e < 8; ++e) Vt[(8 * c8 + e) * VS + row] = vd.e[e];
+      for (int e = 0; e < 8; ++e) {
+        if constexpr (FULL) Vt[(8 * c8 + e) * TS + row] = sg.v.e[e];
+        Vw[(8 * c8 + e) * TS + row] = ET<E>::from_f(ET<E>::to_f(sg.v.e[e]) * wj);
+      }
     }
   };
   auto store_state_copy = [&]() {
@@ -262,11 +334,13 @@ __global__ __launch_bounds__(NTHR) void chunk_fwd_kernel(const ChunkFwdArgs a) {
     }
   };
 
-  if (a.n_chunks > 0) {
-    load_chunk(0, kst, vst, qf);
-    store_chunk(kst, vst);
-  }
-  store_state_copy();
+  Stage sg0, sg1, sg2;
+  load_chunk(c_begin, sg0);
+  load_chunk(c_begin + 1, sg1);
+  if constexpr (PF == 3) load_chunk(c_begin + 2, sg2);
+  __syncthreads();  // pw visible before store_chunk reads it
+  store_chunk(c_begin, sg0);
+  if constexpr (FULL) store_state_copy();
   __syncthreads();
 
   // Causal decay coefficients of S, fixed for every chunk: lane row i = i_loc,
@@ -277,84 +351,102 @@ __global__ __launch_bounds__(NTHR) void chunk_fwd_kernel(const ChunkFwdArgs a) {
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
       const int j = 16 * jb + 4 * g + r;
-      coef[jb][r] = (jb <= w && j <= i_loc) ? a.c * pw[i_loc - j] : 0.f;
+      const float pv = pw[max(i_loc - j, 0)];
+      coef[jb][r] = (j <= i_loc) ? a.c * pv : 0.f;
     }
   }
 
-  for (int c = 0; c < a.n_chunks; ++c) {
+  // One chunk.  `ld` receives chunk c+PF (it held chunk c, already in LDS);
+  // `st_next` holds chunk c+1 and goes to LDS at the end.  Everything between
+  // the two barriers is branch-free so operand reads batch ahead of MFMAs.
+  auto step = [&](int c, Stage& ld, const Stage& st_next) {
     const int64_t t0 = static_cast<int64_t>(c) * chunk;
-    const int L = static_cast<int>(min(static_cast<int64_t>(chunk), T - t0));
-    if (c > 0) __syncthreads();  // LDS K, V^T and state copy of chunk c are in place
-    const bool has_next = c + 1 < a.n_chunks;
-    if (has_next) load_chunk(c + 1, kst, vst, qn);
+    const int L = chunk_len(c);
+    if (c > c_begin) __syncthreads();  // LDS operands and state copy of chunk c are in place
+    load_chunk(c + PF, ld);
 
-    // V^T fragments: rows v = 16 vt + n; slot s < 4 -> j = 32p + 4g + s,
-    // s >= 4 -> j = 32p + 16 + 4g + (s - 4).  Shared by O and the state update.
-    Frag8<E> vf[VT][NJP];
+    if constexpr (FULL) {
+    Frag8<E> qf[NKK];
 #pragma unroll
-    for (int vt = 0; vt < VT; ++vt) {
+    for (int kk = 0; kk < NKK; ++kk)
+      qf[kk] = *reinterpret_cast<const Frag8<E>*>(Qs + i_loc * KS + 32 * kk + 8 * g);
+
+    // S^T blocks: A = K rows j, B = Q rows i -> lane holds S[i = i_loc][j = 16jb + 4g + r].
+    // All four j-blocks are computed; the causal mask lives in coef.
+    f32x4 sacc[4];
 #pragma unroll
-      for (int p = 0; p < NJP; ++p) {
-        const raw* src = Vt + (16 * vt + n) * VS + 32 * p + 4 * g;
-        vf[vt][p] = lds_frag_4x2<E>(src, src + 16);
-      }
+    for (int jb = 0; jb < 4; ++jb) sacc[jb] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int kk = 0; kk < NKK; ++kk) {
+      Frag8<E> kf[4];
+#pragma unroll
+      for (int jb = 0; jb < 4; ++jb)
+        kf[jb] = *reinterpret_cast<const Frag8<E>*>(Ks + (16 * jb + n) * KS + 32 * kk + 8 * g);
+#pragma unroll
+      for (int jb = 0; jb < 4; ++jb) sacc[jb] = mfma8(kf[jb], qf[kk], sacc[jb]);
     }
-
-    if (16 * w < L) {
-      // S^T blocks: A = K rows j, B = Q rows i -> lane holds S[i = i_loc][j = 16jb + 4g + r].
-      f32x4 sacc[4];
-#pragma unroll
-      for (int jb = 0; jb < 4; ++jb) {
-        sacc[jb] = f32x4{0.f, 0.f, 0.f, 0.f};
-        if (jb <= w) {
-#pragma unroll
-          for (int kk = 0; kk < NKK; ++kk) {
-            const Frag8<E> kf =
-                *reinterpret_cast<const Frag8<E>*>(Ks + (16 * jb + n) * KS + 32 * kk + 8 * g);
-            sacc[jb] = mfma8(kf, qf[kk], sacc[jb]);
-          }
-        }
-      }
-      Frag8<E> pf[NJP];
-#pragma unroll
-      for (int p = 0; p < NJP; ++p) {
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          pf[p].e[r] = ET<E>::from_f(sacc[2 * p][r] * coef[2 * p][r]);
-          pf[p].e[4 + r] = ET<E>::from_f(sacc[2 * p + 1][r] * coef[2 * p + 1][r]);
-        }
-      }
-      const float s_start = (i_loc < L) ? pw[i_loc + 1] : 0.f;
-#pragma unroll
-      for (int vt = 0; vt < VT; ++vt) {
-        // O^T: A = state rows v, B = Q rows i -> lane holds O[i_loc][16vt + 4g + r].
-        f32x4 o = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-        for (int kk = 0; kk < NKK; ++kk) {
-          const Frag8<E> mf =
-              *reinterpret_cast<const Frag8<E>*>(Mb + (16 * vt + n) * KS + 32 * kk + 8 * g);
-          o = mfma8(mf, qf[kk], o);
-        }
-        o *= s_start;
-#pragma unroll
-        for (int p = 0; p < NJP; ++p) {
-          if (32 * p < 16 * (w + 1)) o = mfma8(vf[vt][p], pf[p], o);
-        }
-        if (i_loc < L && a.hidden != nullptr)
-          store4<E>(hidden + (t0 + i_loc) * dv, v0 + 16 * vt + 4 * g, o, dv, vec_o);
-      }
-    }
-
-    // State update.  Weights c * decay^{L-1-j} ride on the K^T operand.
-    float wt[NJP][8];
+    Frag8<E> pf[NJP];
 #pragma unroll
     for (int p = 0; p < NJP; ++p) {
 #pragma unroll
-      for (int s = 0; s < 8; ++s) {
-        const int j = 32 * p + (s < 4 ? 4 * g + s : 16 + 4 * g + (s - 4));
-        wt[p][s] = (j < L) ? a.c * pw[L - 1 - j] : 0.f;
+      for (int r = 0; r < 4; ++r) {
+        pf[p].e[r] = ET<E>::from_f(sacc[2 * p][r] * coef[2 * p][r]);
+        pf[p].e[4 + r] = ET<E>::from_f(sacc[2 * p + 1][r] * coef[2 * p + 1][r]);
       }
     }
+
+    // O^T: A = state rows v, B = Q rows i, then A = V^T rows v, B = P rows i
+    // -> lane holds O[i_loc][16vt + 4g + r].
+    f32x4 o[VT];
+#pragma unroll
+    for (int vt = 0; vt < VT; ++vt) o[vt] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int kk = 0; kk < NKK; ++kk) {
+      Frag8<E> mf[VT];
+#pragma unroll
+      for (int vt = 0; vt < VT; ++vt)
+        mf[vt] = *reinterpret_cast<const Frag8<E>*>(Mb + (16 * vt + n) * KS + 32 * kk + 8 * g);
+#pragma unroll
+      for (int vt = 0; vt < VT; ++vt) o[vt] = mfma8(mf[vt], qf[kk], o[vt]);
+    }
+    Frag8<E> vf[VT][NJP];
+#pragma unroll
+    for (int vt = 0; vt < VT; ++vt)
+#pragma unroll
+      for (int p = 0; p < NJP; ++p) {
+        const raw* src = Vt + (16 * vt + n) * TS + 32 * p + 4 * g;
+        vf[vt][p] = lds_frag_4x2<E>(src, src + 16);
+      }
+    const float s_start = (i_loc < L) ? pw[i_loc + 1] : 0.f;
+    const __amdgpu_buffer_rsrc_t rh =
+        make_rsrc(hidden + t0 * dv, static_cast<uint32_t>(a.hidden != nullptr ? L * dv * ES : 0));
+#pragma unroll
+    for (int vt = 0; vt < VT; ++vt) {
+      o[vt] *= s_start;
+#pragma unroll
+      for (int p = 0; p < NJP; ++p) o[vt] = mfma8(vf[vt][p], pf[p], o[vt]);
+      const int col = v0 + 16 * vt + 4 * g;
+      const int row_off = i_loc * dv * ES;
+      if constexpr (VEC) {
+        buf_store4<E>(rh, col < dv ? row_off + col * ES : kBufOOB, o[vt]);
+      } else {
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+          buf_store1<E>(rh, col + r < dv ? row_off + (col + r) * ES : kBufOOB, o[vt][r]);
+      }
+    }
+
+    }  // FULL
+
+    // State update: M^T = decay^L M^T + K^T (w V), A = K^T rows k, B = (wV)^T rows v.
+    Frag8<E> wf[VT][NJP];
+#pragma unroll
+    for (int vt = 0; vt < VT; ++vt)
+#pragma unroll
+      for (int p = 0; p < NJP; ++p) {
+        const raw* src = Vw + (16 * vt + n) * TS + 32 * p + 4 * g;
+        wf[vt][p] = lds_frag_4x2<E>(src, src + 16);
+      }
     const float decay_L = pw[L];
 #pragma unroll
     for (int q = 0; q < KTW; ++q) {
@@ -363,24 +455,23 @@ __global__ __launch_bounds__(NTHR) void chunk_fwd_kernel(const ChunkFwdArgs a) {
         Frag8<E> kf[NJP];
 #pragma unroll
         for (int p = 0; p < NJP; ++p) {
-#pragma unroll
-          for (int s = 0; s < 8; ++s) {
-            const int j = 32 * p + (s < 4 ? 4 * g + s : 16 + 4 * g + (s - 4));
-            kf[p].e[s] = ET<E>::from_f(ET<E>::to_f(Ks[j * KS + 16 * kt + n]) * wt[p][s]);
-          }
+          const raw* src = Kt + (16 * kt + n) * TS + 32 * p + 4 * g;
+          kf[p] = lds_frag_4x2<E>(src, src + 16);
         }
 #pragma unroll
         for (int vt = 0; vt < VT; ++vt) {
           f32x4 acc = st[q][vt] * decay_L;
 #pragma unroll
-          for (int p = 0; p < NJP; ++p) acc = mfma8(kf[p], vf[vt][p], acc);
+          for (int p = 0; p < NJP; ++p) acc = mfma8(kf[p], wf[vt][p], acc);
           st[q][vt] = acc;
         }
       }
     }
 
-    if (a.snap_every > 0 && ((c + 1) % a.snap_every == 0 || c + 1 == a.n_chunks)) {
+    if (FULL && a.snap_every > 0 && ((c + 1) % a.snap_every == 0 || c + 1 == n_chunks)) {
       const int si = c / a.snap_every;
+      const __amdgpu_buffer_rsrc_t rs =
+          make_rsrc(a.snapshots + (b * a.n_snap + si) * dv * dk, static_cast<uint32_t>(dv * dk * 4));
 #pragma unroll
       for (int q = 0; q < KTW; ++q) {
         const int kt = w + NW * q;
@@ -388,23 +479,51 @@ __global__ __launch_bounds__(NTHR) void chunk_fwd_kernel(const ChunkFwdArgs a) {
 #pragma unroll
           for (int vt = 0; vt < VT; ++vt) {
             const int v = v0 + 16 * vt + n;
-            store_state4<F32>(a.snapshots, ((b * a.n_snap + si) * dv + v) * dk, 16 * kt + 4 * g,
-                              dk, v < dv, true, vec_m, st[q][vt]);
+            const int k = 16 * kt + 4 * g;
+            if constexpr (VEC) {
+              buf_store4<F32>(rs, v < dv ? (v * dk + k) * 4 : kBufOOB, st[q][vt]);
+            } else {
+#pragma unroll
+              for (int r = 0; r < 4; ++r)
+                buf_store1<F32>(rs, (v < dv && k + r < dk) ? (v * dk + k + r) * 4 : kBufOOB, st[q][vt][r]);
+            }
           }
         }
       }
     }
 
     __syncthreads();  // every wave is done with chunk c's LDS
-    if (has_next) {
-      store_chunk(kst, vst);
-#pragma unroll
-      for (int kk = 0; kk < NKK; ++kk) qf[kk] = qn[kk];
-      store_state_copy();
+    store_chunk(c + 1, st_next);
+    if constexpr (FULL) store_state_copy();
+  };
+
+  for (int c = c_begin; c < c_end; c += PF) {
+    if constexpr (PF == 3) {
+      step(c, sg0, sg1);
+      if (c + 1 < c_end) step(c + 1, sg1, sg2);
+      if (c + 2 < c_end) step(c + 2, sg2, sg0);
+    } else {
+      step(c, sg0, sg1);
+      if (c + 1 < c_end) step(c + 1, sg1, sg0);
     }
   }
 
-  if (a.memory_out == nullptr) return;
+  if constexpr (!FULL) {
+#pragma unroll
+    for (int q = 0; q < KTW; ++q) {
+      const int kt = w + NW * q;
+      if (kt < KT) {
+#pragma unroll
+        for (int vt = 0; vt < VT; ++vt) {
+          const int v = v0 + 16 * vt + n;
+          store_state4<F32>(a.part_states, ((b * (a.n_parts - 1) + part) * dv + v) * dk, 16 * kt + 4 * g,
+                            dk, v < dv, true, vec_m, st[q][vt]);
+        }
+      }
+    }
+    return;
+  }
+  if (a.memory_out == nullptr || part != a.n_parts - 1) return;
 #pragma unroll
   for (int q = 0; q < KTW; ++q) {
     const int kt = w + NW * q;
@@ -419,37 +538,56 @@ __global__ __launch_bounds__(NTHR) void chunk_fwd_kernel(const ChunkFwdArgs a) {
   }
 }
 
-template <class E, int DKP, int DV>
-int launch_fwd(const ChunkFwdArgs& a, hipStream_t stream) {
+template <class E, int DKP, int DV, bool VEC, bool FULL>
+int launch_pass(ChunkFwdArgs a, hipStream_t stream) {
   using S = FwdShape<E, DKP, DV>;
+  static_assert(S::lds_bytes <= kMaxLds, "tile does not fit the LDS of one CU");
   static bool attr_set = false;
   if (!attr_set) {
-    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&chunk_fwd_kernel<E, DKP, DV>),
-                                       hipFuncAttributeMaxDynamicSharedMemorySize,
-                                       static_cast<int>(S::lds_bytes));
+    hipError_t e = hipFuncSetAttribute(
+        reinterpret_cast<const void*>(&chunk_fwd_kernel<E, DKP, DV, VEC, FULL>),
+        hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(S::lds_bytes));
     if (e != hipSuccess) {
       set_error("chunk_update_fwd: hipFuncSetAttribute failed: %s", hipGetErrorString(e));
       return static_cast<int>(e);
     }
     attr_set = true;
   }
-  const int64_t grid = a.batch * a.v_tiles;
-  hipLaunchKernelGGL((chunk_fwd_kernel<E, DKP, DV>), dim3(static_cast<unsigned>(grid)), dim3(NTHR),
-                     S::lds_bytes, stream, a);
-  return check_launch("chunk_update_fwd");
+  const int64_t grid = a.batch * (FULL ? a.n_parts : a.n_parts - 1) * a.v_tiles;
+  a.xcd_remap = (grid % 8 == 0) ? 1 : 0;
+  hipLaunchKernelGGL((chunk_fwd_kernel<E, DKP, DV, VEC, FULL>), dim3(static_cast<unsigned>(grid)),
+                     dim3(NTHR), S::lds_bytes, stream, a);
+  return check_launch(FULL ? "chunk_update_fwd" : "chunk_update_fwd(part states)");
 }
 
-template <class E, int DV>
+template <class E, int DKP, int DV, bool VEC>
+int launch_fwd(const ChunkFwdArgs& a, hipStream_t stream) {
+  if (a.n_parts > 1) {
+    const int rc = launch_pass<E, DKP, DV, VEC, false>(a, stream);
+    if (rc != GRM_HIP_OK) return rc;
+  }
+  return launch_pass<E, DKP, DV, VEC, true>(a, stream);
+}
+
+template <class E, int DV, bool VEC>
 int dispatch_dk(const ChunkFwdArgs& a, hipStream_t s) {
-  if (a.dk <= 32) return launch_fwd<E, 32, DV>(a, s);
-  if (a.dk <= 64) return launch_fwd<E, 64, DV>(a, s);
-  if (a.dk <= 128) return launch_fwd<E, 128, DV>(a, s);
-  return launch_fwd<E, 256, DV>(a, s);
+  if (a.dk <= 32) return launch_fwd<E, 32, DV, VEC>(a, s);
+  if (a.dk <= 64) return launch_fwd<E, 64, DV, VEC>(a, s);
+  if (a.dk <= 128) return launch_fwd<E, 128, DV, VEC>(a, s);
+  if constexpr (FwdShape<E, 256, DV>::lds_bytes <= kMaxLds) {
+    return launch_fwd<E, 256, DV, VEC>(a, s);
+  } else {
+    set_error("chunk_update_fwd: key_dim %d needs more LDS than a CU has for this dtype", a.dk);
+    return GRM_HIP_EUNSUPPORTED;
+  }
 }
 
+// 16-byte accesses need every row of keys/queries/values/hidden to start on
+// a 16-byte boundary; otherwise the element-wise variant (16-wide tiles) runs.
 template <class E>
-int dispatch_dv(const ChunkFwdArgs& a, int dv_tile, hipStream_t s) {
-  return dv_tile == 32 ? dispatch_dk<E, 32>(a, s) : dispatch_dk<E, 16>(a, s);
+int dispatch_dv(const ChunkFwdArgs& a, int dv_tile, bool vec, hipStream_t s) {
+  if (!vec) return dispatch_dk<E, 16, false>(a, s);
+  return dv_tile == 32 ? dispatch_dk<E, 32, true>(a, s) : dispatch_dk<E, 16, true>(a, s);
 }
 
 bool aligned(const void* p, size_t n) { return (reinterpret_cast<uintptr_t>(p) % n) == 0; }
@@ -464,6 +602,23 @@ int chunk_for_snapshot(int64_t snapshot_len) {
   return 1;
 }
 
+// Time parts per sequence.  Splitting costs an extra state pass over K and V,
+// so it is used only when (sequence, tile) workgroups would leave CUs idle:
+// the grid is grown to about one workgroup per CU (256), keeping at least 8
+// chunks per part.
+int parts_for(int64_t wgs, int64_t n_chunks) {
+  const char* env = getenv("GRM_HIP_CHUNK_PARTS");
+  if (env != nullptr) {
+    const int v = atoi(env);
+    if (v >= 1) return static_cast<int>(min(static_cast<int64_t>(v), n_chunks));
+  }
+  if (wgs >= 192) return 1;
+  int64_t p = (256 + wgs - 1) / wgs;
+  p = min(p, n_chunks / 8);
+  p = min(p, static_cast<int64_t>(64));
+  return static_cast<int>(max(p, static_cast<int64_t>(1)));
+}
+
 }  // namespace
 
 int tile_dv_for(int64_t batch, int64_t value_dim) {
@@ -472,20 +627,67 @@ int tile_dv_for(int64_t batch, int64_t value_dim) {
     const int v = atoi(env);
     if (v == 16 || v == 32) return v;
   }
-  // Prefer the wider tile only when it still gives every CU a workgroup.
-  return (batch * ((value_dim + 31) / 32) >= 512) ? 32 : 16;
+  // The wider tile halves the redundant Q K^T work per sequence; time parts
+  // (parts_for) supply the parallelism it gives up.
+  (void)batch;
+  return value_dim >= 32 ? 32 : 16;
 }
 
 }  // namespace grmhip
 
 using namespace grmhip;
 
+namespace {
+
+bool vec_ok(const void* keys, const void* values, const void* queries, const void* hidden,
+            const float* snapshots, int64_t key_dim, int64_t value_dim) {
+  return (key_dim % 8 == 0) && (value_dim % 8 == 0) && aligned(keys, 16) && aligned(queries, 16) &&
+         aligned(values, 16) && aligned(hidden, 16) && (snapshots == nullptr || aligned(snapshots, 16));
+}
+
+struct Plan {
+  int chunk;
+  int64_t n_chunks;
+  int dv_tile;
+  int v_tiles;
+  int n_parts;
+  int part_chunks;
+  int64_t workspace_bytes;
+};
+
+Plan make_plan(int64_t batch, int64_t seq_len, int64_t value_dim, int64_t key_dim,
+               int64_t snapshot_len, bool vec) {
+  Plan p;
+  p.chunk = snapshot_len > 0 ? chunk_for_snapshot(snapshot_len) : CT;
+  p.n_chunks = (seq_len + p.chunk - 1) / p.chunk;
+  p.dv_tile = vec ? tile_dv_for(batch, value_dim) : 16;
+  p.v_tiles = static_cast<int>((value_dim + p.dv_tile - 1) / p.dv_tile);
+  p.n_parts = parts_for(batch * p.v_tiles, p.n_chunks);
+  p.part_chunks = static_cast<int>((p.n_chunks + p.n_parts - 1) / p.n_parts);
+  p.n_parts = static_cast<int>((p.n_chunks + p.part_chunks - 1) / p.part_chunks);
+  if (p.n_parts < 1) p.n_parts = 1;
+  p.workspace_bytes = batch * (p.n_parts - 1) * value_dim * key_dim * 4;
+  return p;
+}
+
+}  // namespace
+
+extern "C" int64_t grm_hip_chunk_update_fwd_workspace(int64_t batch, int64_t seq_len,
+                                                      int64_t key_dim, int64_t value_dim,
+                                                      int64_t snapshot_len) {
+  if (batch <= 0 || seq_len <= 0 || key_dim < 1 || value_dim < 1) return 0;
+  // Sized for the 16-byte path; the element-wise path never needs more.
+  const Plan p = make_plan(batch, seq_len, value_dim, key_dim, snapshot_len,
+                           key_dim % 8 == 0 && value_dim % 8 == 0);
+  return p.workspace_bytes;
+}
+
 extern "C" int grm_hip_chunk_update_fwd(const void* keys, const void* values, const void* queries,
                                         const void* memory, void* hidden, void* memory_out,
-                                        float* snapshots, int64_t batch, int64_t seq_len,
-                                        int64_t key_dim, int64_t value_dim, int in_dtype,
-                                        int mem_dtype, double memory_decay, int64_t snapshot_len,
-                                        void* stream) {
+                                        float* snapshots, void* workspace, int64_t workspace_bytes,
+                                        int64_t batch, int64_t seq_len, int64_t key_dim,
+                                        int64_t value_dim, int in_dtype, int mem_dtype,
+                                        double memory_decay, int64_t snapshot_len, void* stream) {
   if (batch < 0 || seq_len < 0 || key_dim < 1 || value_dim < 1) {
     set_error("chunk_update_fwd: bad sizes batch=%lld seq_len=%lld key_dim=%lld value_dim=%lld",
               (long long)batch, (long long)seq_len, (long long)key_dim, (long long)value_dim);
@@ -496,8 +698,9 @@ extern "C" int grm_hip_chunk_update_fwd(const void* keys, const void* values, co
     set_error("chunk_update_fwd: unsupported dtypes in=%d mem=%d", in_dtype, mem_dtype);
     return GRM_HIP_EUNSUPPORTED;
   }
-  if (key_dim > 256) {
-    set_error("chunk_update_fwd: key_dim %lld > 256", (long long)key_dim);
+  if (key_dim > 256 || (in_dtype == GRM_HIP_F32 && key_dim > 128)) {
+    set_error("chunk_update_fwd: key_dim %lld exceeds %d for this dtype", (long long)key_dim,
+              in_dtype == GRM_HIP_F32 ? 128 : 256);
     return GRM_HIP_EUNSUPPORTED;
   }
   if (!std::isfinite(memory_decay)) {
@@ -539,31 +742,38 @@ extern "C" int grm_hip_chunk_update_fwd(const void* keys, const void* values, co
   a.seq_len = seq_len;
   a.dk = static_cast<int>(key_dim);
   a.dv = static_cast<int>(value_dim);
-  a.chunk = snapshots != nullptr ? chunk_for_snapshot(snapshot_len) : CT;
-  const int64_t n_chunks = (seq_len + a.chunk - 1) / a.chunk;
-  if (n_chunks > INT32_MAX) {
+  const bool vec = vec_ok(keys, values, queries, hidden, snapshots, key_dim, value_dim);
+  Plan plan = make_plan(batch, seq_len, value_dim, key_dim, snapshots != nullptr ? snapshot_len : 0, vec);
+  if (plan.n_chunks > INT32_MAX) {
     set_error("chunk_update_fwd: seq_len too large");
     return GRM_HIP_EINVAL;
   }
-  a.n_chunks = static_cast<int>(n_chunks);
+  // Without room for the per-part states, one workgroup walks each whole sequence.
+  if (plan.n_parts > 1 && (workspace == nullptr || workspace_bytes < plan.workspace_bytes ||
+                           !aligned(workspace, 16))) {
+    plan.n_parts = 1;
+    plan.part_chunks = static_cast<int>(plan.n_chunks);
+  }
+  const int dv_tile = plan.dv_tile;
+  a.chunk = plan.chunk;
+  a.n_chunks = static_cast<int>(plan.n_chunks);
   if (snapshots != nullptr) {
     a.snap_every = static_cast<int>(snapshot_len / a.chunk);
     a.n_snap = static_cast<int>((seq_len + snapshot_len - 1) / snapshot_len);
   }
-  const int dv_tile = tile_dv_for(batch, value_dim);
-  a.v_tiles = static_cast<int>((value_dim + dv_tile - 1) / dv_tile);
-  const int64_t grid = batch * a.v_tiles;
+  a.v_tiles = plan.v_tiles;
+  a.n_parts = plan.n_parts;
+  a.part_chunks = plan.part_chunks;
+  a.part_states = static_cast<float*>(workspace);
+  a.part_decay = static_cast<float>(std::pow(memory_decay, static_cast<double>(plan.part_chunks) * a.chunk));
+  const int64_t grid = batch * a.n_parts * a.v_tiles;
   if (grid > INT32_MAX) {
     set_error("chunk_update_fwd: batch too large for one launch");
     return GRM_HIP_EINVAL;
   }
   a.mem_f32 = mem_dtype == GRM_HIP_F32;
-  a.vec_k = (key_dim % 8 == 0) && aligned(keys, 16) && aligned(queries, 16);
-  a.vec_v = (value_dim % 8 == 0) && aligned(values, 16);
-  a.vec_o = (value_dim % 4 == 0) && aligned(hidden, 4 * in_b);
   a.vec_m = (key_dim % 4 == 0) && aligned(memory, 4 * mem_b) && aligned(memory_out, 4 * mem_b) &&
-            (snapshots == nullptr || aligned(snapshots, 16));
-  a.xcd_remap = (grid % 8 == 0) ? 1 : 0;
+            (snapshots == nullptr || aligned(snapshots, 16)) && aligned(workspace, 16);
   a.c = static_cast<float>((1.0 - memory_decay) / std::sqrt(static_cast<double>(key_dim)));
   for (int i = 0; i < PW_N; ++i) a.pw[i] = static_cast<float>(std::pow(memory_decay, i));
 
@@ -579,8 +789,8 @@ extern "C" int grm_hip_chunk_update_fwd(const void* keys, const void* values, co
     return GRM_HIP_OK;
   }
   switch (in_dtype) {
-    case GRM_HIP_F32: return dispatch_dv<F32>(a, dv_tile, s);
-    case GRM_HIP_F16: return dispatch_dv<F16>(a, dv_tile, s);
-    default: return dispatch_dv<BF16>(a, dv_tile, s);
+    case GRM_HIP_F32: return dispatch_dv<F32>(a, dv_tile, vec, s);
+    case GRM_HIP_F16: return dispatch_dv<F16>(a, dv_tile, vec, s);
+    default: return dispatch_dv<BF16>(a, dv_tile, vec, s);
   }
 }

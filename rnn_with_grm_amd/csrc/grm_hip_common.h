@@ -154,6 +154,74 @@ __device__ __forceinline__ void store4_raw(typename ET<E>::raw* p, f32x4 v) {
   }
 }
 
+// ---------------------------------------------------------------------------
+// Raw buffer access (gfx9 family).  A resource covers [base, base + bytes);
+// loads outside it return zero and stores outside it are dropped, so row and
+// column masks become offset selects instead of branches.
+constexpr int kBufOOB = 0x7ffffff0;  // an offset past every resource used here
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), static_cast<short>(0),
+                                           static_cast<int>(bytes), 0x00020000);
+}
+
+// Eight consecutive elements starting at byte offset `off` (OOB -> zeros).
+template <class E>
+__device__ __forceinline__ U8<E> buf_load8(__amdgpu_buffer_rsrc_t r, int off) {
+  typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+  if constexpr (sizeof(typename ET<E>::raw) == 2) {
+    const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0);
+    return __builtin_bit_cast(U8<E>, v);
+  } else {
+    const u32x4 a = __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0);
+    const u32x4 b = __builtin_amdgcn_raw_buffer_load_b128(r, off + 16, 0, 0);
+    U8<E> u;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      u.e[i] = __uint_as_float(a[i]);
+      u.e[4 + i] = __uint_as_float(b[i]);
+    }
+    return u;
+  }
+}
+
+// One element at byte offset `off` (OOB -> zero).
+template <class E>
+__device__ __forceinline__ typename ET<E>::raw buf_load1(__amdgpu_buffer_rsrc_t r, int off) {
+  if constexpr (sizeof(typename ET<E>::raw) == 2) {
+    return __builtin_amdgcn_raw_buffer_load_b16(r, off, 0, 0);
+  } else {
+    return __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(r, off, 0, 0));
+  }
+}
+
+// Four consecutive elements converted from fp32 (OOB -> dropped).
+template <class E>
+__device__ __forceinline__ void buf_store4(__amdgpu_buffer_rsrc_t r, int off, f32x4 v) {
+  if constexpr (sizeof(typename ET<E>::raw) == 2) {
+    typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+    u32x2 q;
+    q[0] = static_cast<uint32_t>(ET<E>::from_f(v[0])) | (static_cast<uint32_t>(ET<E>::from_f(v[1])) << 16);
+    q[1] = static_cast<uint32_t>(ET<E>::from_f(v[2])) | (static_cast<uint32_t>(ET<E>::from_f(v[3])) << 16);
+    __builtin_amdgcn_raw_buffer_store_b64(q, r, off, 0, 0);
+  } else {
+    typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+    u32x4 q;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) q[i] = __float_as_uint(v[i]);
+    __builtin_amdgcn_raw_buffer_store_b128(q, r, off, 0, 0);
+  }
+}
+
+template <class E>
+__device__ __forceinline__ void buf_store1(__amdgpu_buffer_rsrc_t r, int off, float v) {
+  if constexpr (sizeof(typename ET<E>::raw) == 2) {
+    __builtin_amdgcn_raw_buffer_store_b16(ET<E>::from_f(v), r, off, 0, 0);
+  } else {
+    __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(v), r, off, 0, 0);
+  }
+}
+
 __device__ __forceinline__ int lane_id() { return static_cast<int>(threadIdx.x) & 63; }
 
 }  // namespace grmhip

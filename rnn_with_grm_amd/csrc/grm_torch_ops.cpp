@@ -50,6 +50,13 @@ void* current_stream(const Tensor& t) {
   return static_cast<void*>(c10::hip::getCurrentHIPStream(t.device().index()).stream());
 }
 
+// Scratch for the time-split scan (per-part end states), allocated on the
+// tensor's device through the caching allocator.
+Tensor scan_workspace(const Tensor& like, int64_t B, int64_t T, int64_t K, int64_t H, int64_t snap) {
+  const int64_t bytes = grm_hip_chunk_update_fwd_workspace(B, T, K, H, snap);
+  return at::empty({(bytes + 3) / 4}, like.options().dtype(at::kFloat));
+}
+
 // ---------------------------------------------------------------------------
 // Argument checks (same conditions and error class as the reference,
 // grm/csrc/grm_cuda.cpp:13-42,159-161).
@@ -290,7 +297,8 @@ bool chunk_supported(const Tensor& keys, const Tensor& values, const Tensor& que
       queries.scalar_type() != keys.scalar_type())
     return false;
   if (memory.scalar_type() != keys.scalar_type() && memory.scalar_type() != at::kFloat) return false;
-  return keys.size(2) >= 1 && keys.size(2) <= 256 && values.size(2) >= 1;
+  const int64_t max_k = keys.scalar_type() == at::kFloat ? 128 : 256;
+  return keys.size(2) >= 1 && keys.size(2) <= max_k && values.size(2) >= 1;
 }
 
 std::tuple<Tensor, Tensor, Tensor> chunk_update_forward_hip(const Tensor& keys, const Tensor& values,
@@ -310,8 +318,10 @@ std::tuple<Tensor, Tensor, Tensor> chunk_update_forward_hip(const Tensor& keys, 
   Tensor m = memory.contiguous();
   Tensor hidden = at::empty({k.size(0), k.size(1), v.size(2)}, v.options());
   Tensor memory_out = at::empty_like(m);
+  Tensor ws = scan_workspace(k, k.size(0), k.size(1), k.size(2), v.size(2), 0);
   check_rc(grm_hip_chunk_update_fwd(k.data_ptr(), v.data_ptr(), q.data_ptr(), m.data_ptr(),
-                                    hidden.data_ptr(), memory_out.data_ptr(), nullptr, k.size(0),
+                                    hidden.data_ptr(), memory_out.data_ptr(), nullptr,
+                                    ws.numel() ? ws.data_ptr() : nullptr, ws.numel() * 4, k.size(0),
                                     k.size(1), k.size(2), v.size(2), dtype_code(k.scalar_type()),
                                     dtype_code(m.scalar_type()), decay, 0, current_stream(k)),
            "chunk_update_forward");
@@ -472,11 +482,13 @@ std::tuple<Tensor, Tensor, Tensor> segment_scan_forward_hip(const Tensor& keys, 
     memory_out.copy_(m);
     return {hidden, memory_out, snaps};
   }
+  Tensor ws = scan_workspace(k, B, T, K, H, segment_len);
   check_rc(grm_hip_chunk_update_fwd(k.data_ptr(), v.data_ptr(), q.data_ptr(), m.data_ptr(),
                                     hidden.data_ptr(), memory_out.data_ptr(),
-                                    snaps.data_ptr<float>(), B, T, K, H,
-                                    dtype_code(k.scalar_type()), dtype_code(m.scalar_type()), decay,
-                                    segment_len, current_stream(k)),
+                                    snaps.data_ptr<float>(), ws.numel() ? ws.data_ptr() : nullptr,
+                                    ws.numel() * 4, B, T, K, H, dtype_code(k.scalar_type()),
+                                    dtype_code(m.scalar_type()), decay, segment_len,
+                                    current_stream(k)),
            "segment_scan_forward");
   return {hidden, memory_out, snaps};
 }

@@ -14,7 +14,7 @@ HEADER = Path(__file__).resolve().parents[1] / "include" / "grm_hip.h"
 
 def declared_symbols():
     text = HEADER.read_text()
-    return sorted(set(re.findall(r"^\s*(?:int|const char\*|uint64_t)\s+(grm_hip_\w+)\s*\(", text, re.M)))
+    return sorted(set(re.findall(r"^\s*(?:int|int64_t|const char\*|uint64_t)\s+(grm_hip_\w+)\s*\(", text, re.M)))
 
 
 def test_header_declares_all_bound_symbols():
@@ -25,6 +25,14 @@ def test_library_exports_every_declared_symbol():
     lib = ctypes.CDLL(str(capi.LIB_PATH))
     for name in declared_symbols():
         assert hasattr(lib, name), name
+
+
+def test_workspace_query():
+    lib = capi.load()
+    assert lib.grm_hip_chunk_update_fwd_workspace(0, 10, 8, 8, 0) == 0
+    assert lib.grm_hip_chunk_update_fwd_workspace(4, 64, 64, 512, 0) == 0  # one chunk: no split
+    ws = lib.grm_hip_chunk_update_fwd_workspace(16, 65536, 128, 128, 128)  # long context splits
+    assert ws > 0 and ws % (16 * 128 * 128 * 4) == 0
 
 
 def test_abi_version_and_counters():
@@ -52,7 +60,7 @@ def test_chunk_fwd_rejects(kwargs, code):
     a.update(kwargs)
     fake = ctypes.c_void_p(16)  # never dereferenced: validation fails first
     rc = capi.load().grm_hip_chunk_update_fwd(fake, fake, fake, fake, fake, ctypes.c_void_p(32),
-                                              fake if a["snapshot"] else None, a["batch"], a["seq_len"],
+                                              fake if a["snapshot"] else None, None, 0, a["batch"], a["seq_len"],
                                               a["key_dim"], a["value_dim"], a["in_dtype"], a["mem_dtype"],
                                               a["decay"], a["snapshot_len"], None)
     assert rc == code
@@ -60,12 +68,12 @@ def test_chunk_fwd_rejects(kwargs, code):
 
 
 def test_chunk_fwd_zero_batch_is_noop():
-    assert capi.load().grm_hip_chunk_update_fwd(None, None, None, None, None, None, None, 0, 5, 8, 4,
+    assert capi.load().grm_hip_chunk_update_fwd(None, None, None, None, None, None, None, None, 0, 0, 5, 8, 4,
                                                 capi.BF16, capi.F32, 0.97, 0, None) == capi.OK
 
 
 def test_chunk_fwd_null_pointers_rejected():
-    rc = capi.load().grm_hip_chunk_update_fwd(None, None, None, None, None, None, None, 1, 5, 8, 4,
+    rc = capi.load().grm_hip_chunk_update_fwd(None, None, None, None, None, None, None, None, 0, 1, 5, 8, 4,
                                               capi.BF16, capi.F32, 0.97, 0, None)
     assert rc == capi.EINVAL
 

@@ -53,6 +53,8 @@ def oracle_fwd(k, v, q, m, decay, snap=0):
 @pytest.mark.parametrize("B,T,K,H", [(2, 8, 8, 16), (3, 200, 64, 48), (2, 130, 128, 128), (1, 64, 256, 40),
                                      (2, 77, 33, 20)])
 def test_chunk_forward_capi(dev, dtype, mem_dtype, B, T, K, H):
+    if dtype == torch.float32 and K > 128:
+        pytest.skip("float32 inputs take key_dim <= 128 (test_fp32_wide_keys covers the rejection)")
     k, v, q, m = make_case(B, T, K, H, dtype, mem_dtype, seed=B * 1000 + T)
     decay = 0.97
     hid, mo, _ = capi.chunk_update_fwd(k.to(dev), v.to(dev), q.to(dev), m.to(dev), decay)
@@ -60,6 +62,18 @@ def test_chunk_forward_capi(dev, dtype, mem_dtype, B, T, K, H):
     rh, rm, _ = oracle_fwd(k, v, q, m, decay)
     close("hidden", hid, rh, dtype)
     close("memory_out", mo, rm, mem_dtype if mem_dtype != torch.float32 else dtype)
+
+
+def test_fp32_wide_keys(dev):
+    """float32 with key_dim > 128 exceeds one CU's LDS: the C ABI refuses it and the
+    torch op runs the generic ATen path on the GPU, as the reference does for d_k > 128."""
+    k, v, q, m = make_case(1, 40, 192, 16, torch.float32, torch.float32, seed=1)
+    with pytest.raises(RuntimeError, match="exceeds 128"):
+        capi.chunk_update_fwd(k.to(dev), v.to(dev), q.to(dev), m.to(dev), 0.97)
+    hid, mo, _ = torch.ops.grm_cuda.chunk_update_forward(k.to(dev), v.to(dev), q.to(dev), m.to(dev), 0.97)
+    rh, rm, _ = oracle_fwd(k, v, q, m, 0.97)
+    close("hidden", hid, rh, torch.float32)
+    close("memory_out", mo, rm, torch.float32)
 
 
 def test_reference_case_fp32(dev):
@@ -119,6 +133,41 @@ def test_config2_shape(dev):
     # run-to-run determinism (no atomics)
     hid3, _, snaps3 = capi.chunk_update_fwd(kd, vd, qd, md, 0.97, 64)
     assert torch.equal(hid, hid3) and torch.equal(snaps, snaps3)
+
+
+@pytest.mark.parametrize("parts", [2, 3, 5])
+@pytest.mark.parametrize("seg", [0, 64, 100, 128])
+def test_time_split(dev, monkeypatch, parts, seg):
+    """Sequences split into time parts (state pass + scan pass) match the oracle
+    and the single-chain scan; ragged last part and odd snapshot lengths included."""
+    B, T, K, H = 3, 700, 128, 96
+    k, v, q, m = make_case(B, T, K, H, torch.bfloat16, torch.float32, seed=parts * 7 + seg)
+    kd, vd, qd, md = k.to(dev), v.to(dev), q.to(dev), m.to(dev)
+    monkeypatch.setenv("GRM_HIP_CHUNK_PARTS", str(parts))
+    assert capi.fwd_workspace_bytes(B, T, K, H, seg) > 0
+    hid, mo, snaps = capi.chunk_update_fwd(kd, vd, qd, md, 0.97, seg)
+    hid1, mo1, snaps1 = capi.chunk_update_fwd(kd, vd, qd, md, 0.97, seg, split=False)
+    torch.cuda.synchronize()
+    rh, rm, rs = oracle_fwd(k, v, q, m, 0.97, seg)
+    close("hidden", hid, rh, torch.bfloat16)
+    close("memory_out", mo, rm, torch.bfloat16)
+    if seg:
+        close("snapshots", snaps, rs, torch.bfloat16)
+        assert torch.equal(snaps[:, -1], mo)
+    # the split only reassociates fp32 sums of the state
+    torch.testing.assert_close(hid.float(), hid1.float(), rtol=2e-2, atol=2e-3)
+    torch.testing.assert_close(mo, mo1, rtol=1e-4, atol=1e-6)
+
+
+def test_long_context_split_fp32(dev, monkeypatch):
+    """fp32 long sequence, automatic part count, against the oracle at fp32 tolerance."""
+    B, T, K, H = 2, 4096, 64, 64
+    k, v, q, m = make_case(B, T, K, H, torch.float32, torch.float32, seed=5)
+    assert capi.fwd_workspace_bytes(B, T, K, H, 0) > 0
+    hid, mo, _ = capi.chunk_update_fwd(k.to(dev), v.to(dev), q.to(dev), m.to(dev), 0.97)
+    rh, rm, _ = oracle_fwd(k, v, q, m, 0.97)
+    close("hidden", hid, rh, torch.float32)
+    close("memory_out", mo, rm, torch.float32)
 
 
 def test_empty_and_zero_batch(dev):
