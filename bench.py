@@ -175,8 +175,10 @@ def main() -> int:
     ap.add_argument("--no-gather", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--c2-only", action="store_true", help="only the headline kernel (quick sweeps)")
+    ap.add_argument("--probe", action="store_true",
+                    help="counter runs: a 256 MiB device copy (calibration) then config-2 launches only")
     a = ap.parse_args()
-    if a.c2_only:
+    if a.c2_only or a.probe:
         a.no_gather = a.no_cpu = True
     if a.gpus != 1:
         print(f"bench.py measures one GPU only; --gpus {a.gpus} is not supported in this build "
@@ -194,6 +196,14 @@ def main() -> int:
         raise RuntimeError(f"GRM HIP extension not loaded: {cuda_ops._EXTENSION_LOAD_ERROR}")
     dev = torch.device("cuda:0")
 
+    if a.probe:
+        # Calibration for HBM byte counters: a plain copy of a known size.
+        src = torch.empty(256 << 20, dtype=torch.uint8, device=dev)
+        dst = torch.empty_like(src)
+        dst.copy_(src)
+        torch.cuda.synchronize()
+        log(f"probe copy: {src.numel()} bytes read and written")
+        del src, dst
     log(f"config 2 fused chunk-update+query: warmup {a.warmup}, steps {a.steps}")
     wall, per, _ = bench_c2(torch, dev, a.steps, a.warmup)
     flops, bytes_ = c2_counts()
