@@ -76,6 +76,30 @@ def test_gather_config3_slice(dev):
     assert torch.equal(per_row, expect)
 
 
+@pytest.mark.parametrize("B,S,N,D,dtype", [
+    (8, 16, 32, 128, torch.float32),     # 32-unit column tiles, 16 MiB out (regular stores)
+    (8, 64, 256, 128, torch.bfloat16),   # 16-unit column tiles, 64 MiB out (non-temporal stores)
+    (16, 600, 700, 64, torch.float32),   # 8-unit column tiles (600 states need the narrow slice)
+])
+def test_gather_column_tiles_with_bad_indices(dev, B, S, N, D, dtype):
+    """Shapes where every archived state is referenced about once or more, so the
+    column-tiled kernel runs; out-of-range indices give zero rows and are counted
+    once each."""
+    g = torch.Generator().manual_seed(5)
+    mem = (torch.randn(B, S, D, D, generator=g) * 0.02).to(dtype).to(dev)
+    idx = torch.randint(0, S, (B, N), generator=g)
+    idx[0, 3] = -1
+    idx[B - 1, N - 1] = S
+    idx[B // 2, 0] = 1 << 40
+    bad = torch.zeros(1, dtype=torch.int32, device=dev)
+    out = capi.batched_gather(mem, idx.to(dev), bad_count=bad)
+    ok = (idx >= 0) & (idx < S)
+    ref = torch.stack([mem[b].index_select(0, idx[b].clamp(0, S - 1).to(dev)) for b in range(B)])
+    ref[~ok.to(dev)] = 0
+    assert int(bad.item()) == 3
+    assert torch.equal(out, ref)
+
+
 # ---------------------------------------------------------------- apply query
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16])
 @pytest.mark.parametrize("shape", [(2, 3, 4, 5, 6), (4, 7, 8, 128, 128), (3, 5, 2, 9, 33), (2, 4, 16, 64)])
