@@ -1,0 +1,56 @@
+// Arguments shared by the two forward scan kernels (chunk_scan.hip: value
+// tiles of 16/32 columns, any dtype; chunk_scan_wide.hip: the whole 128-wide
+// value tile per workgroup for 16-bit inputs).
+#pragma once
+
+#include <stddef.h>
+#include <stdint.h>
+
+#include <hip/hip_runtime.h>
+
+namespace grmhip {
+
+constexpr int CT = 64;                  // token rows per chunk tile
+constexpr int PW_N = CT + 1;            // decay^0 .. decay^64
+constexpr size_t kMaxLds = 160 * 1024;  // LDS per CU on gfx950
+
+struct ChunkFwdArgs {
+  const void* keys;
+  const void* values;
+  const void* queries;
+  const void* memory;
+  void* hidden;
+  void* memory_out;
+  float* snapshots;
+  int64_t batch;
+  int64_t seq_len;
+  int dk;
+  int dv;
+  int chunk;       // tokens per chunk, 1..64
+  int n_chunks;
+  int snap_every;  // chunks per snapshot; 0 = no snapshots
+  int n_snap;
+  int v_tiles;     // workgroups per sequence
+  int mem_f32;     // memory / memory_out are float32 (else the input dtype)
+  int vec_m;       // memory/memory_out/snapshot rows allow 4-element vector access
+  int xcd_remap;   // grid is a multiple of 8: place a sequence's tiles on one XCD
+  int n_parts;     // time parts per sequence (1 = one workgroup walks the whole sequence)
+  int part_chunks; // chunks per part; every part but the last is full
+  float part_decay;   // decay^(part_chunks * chunk)
+  float* part_states; // [batch, n_parts - 1, dv, dk]: end-state contribution of each part
+  float c;         // (1 - decay) / sqrt(d_k)
+  float pw[PW_N];  // decay^n rounded from double
+};
+
+// Value columns per workgroup of the wide kernel.
+constexpr int kWideDv = 128;
+
+// The wide kernel covers 16-bit inputs with key_dim <= 128 and 16-byte
+// aligned rows (key_dim and value_dim multiples of 8).
+bool wide_supported(int in_dtype, int64_t key_dim, int64_t value_dim, bool vec);
+
+// Launches the state pass (when a.n_parts > 1) and the full pass of the wide
+// kernel; a.v_tiles counts 128-wide value tiles.
+int launch_scan_wide(const ChunkFwdArgs& a, int in_dtype, hipStream_t stream);
+
+}  // namespace grmhip

@@ -27,45 +27,15 @@
 
 #include <cmath>
 
+#include "chunk_scan.h"
 #include "grm_hip.h"
 #include "grm_hip_common.h"
 
 namespace grmhip {
 namespace {
 
-constexpr int CT = 64;         // token rows per chunk tile
 constexpr int NW = 4;          // waves per workgroup
 constexpr int NTHR = 64 * NW;  // threads per workgroup
-constexpr int PW_N = CT + 1;   // decay^0 .. decay^64
-constexpr size_t kMaxLds = 160 * 1024;  // LDS per CU on gfx950
-
-struct ChunkFwdArgs {
-  const void* keys;
-  const void* values;
-  const void* queries;
-  const void* memory;
-  void* hidden;
-  void* memory_out;
-  float* snapshots;
-  int64_t batch;
-  int64_t seq_len;
-  int dk;
-  int dv;
-  int chunk;       // tokens per chunk, 1..64
-  int n_chunks;
-  int snap_every;  // chunks per snapshot; 0 = no snapshots
-  int n_snap;
-  int v_tiles;     // workgroups per sequence
-  int mem_f32;     // memory / memory_out are float32 (else the input dtype)
-  int vec_m;       // memory/memory_out/snapshot rows allow 4-element vector access
-  int xcd_remap;   // grid is a multiple of 8: place a sequence's tiles on one XCD
-  int n_parts;     // time parts per sequence (1 = one workgroup walks the whole sequence)
-  int part_chunks; // chunks per part; every part but the last is full
-  float part_decay;   // decay^(part_chunks * chunk)
-  float* part_states; // [batch, n_parts - 1, dv, dk]: end-state contribution of each part
-  float c;         // (1 - decay) / sqrt(d_k)
-  float pw[PW_N];  // decay^n rounded from double
-};
 
 template <class E>
 __device__ __forceinline__ void store4(typename ET<E>::raw* row, int col, f32x4 v, int ncols,
@@ -646,6 +616,7 @@ bool vec_ok(const void* keys, const void* values, const void* queries, const voi
 }
 
 struct Plan {
+  bool wide;      // 128-wide value tiles (chunk_scan_wide.hip)
   int chunk;
   int64_t n_chunks;
   int dv_tile;
@@ -655,12 +626,20 @@ struct Plan {
   int64_t workspace_bytes;
 };
 
+// The wide kernel unless GRM_HIP_CHUNK_DV asks for the 16/32-column tiles.
+bool use_wide(int in_dtype, int64_t key_dim, int64_t value_dim, bool vec) {
+  const char* env = getenv("GRM_HIP_CHUNK_DV");
+  if (env != nullptr && (atoi(env) == 16 || atoi(env) == 32)) return false;
+  return wide_supported(in_dtype, key_dim, value_dim, vec);
+}
+
 Plan make_plan(int64_t batch, int64_t seq_len, int64_t value_dim, int64_t key_dim,
-               int64_t snapshot_len, bool vec) {
+               int64_t snapshot_len, bool vec, bool wide) {
   Plan p;
+  p.wide = wide;
   p.chunk = snapshot_len > 0 ? chunk_for_snapshot(snapshot_len) : CT;
   p.n_chunks = (seq_len + p.chunk - 1) / p.chunk;
-  p.dv_tile = vec ? tile_dv_for(batch, value_dim) : 16;
+  p.dv_tile = wide ? kWideDv : (vec ? tile_dv_for(batch, value_dim) : 16);
   p.v_tiles = static_cast<int>((value_dim + p.dv_tile - 1) / p.dv_tile);
   p.n_parts = parts_for(batch * p.v_tiles, p.n_chunks);
   p.part_chunks = static_cast<int>((p.n_chunks + p.n_parts - 1) / p.n_parts);
@@ -676,10 +655,13 @@ extern "C" int64_t grm_hip_chunk_update_fwd_workspace(int64_t batch, int64_t seq
                                                       int64_t key_dim, int64_t value_dim,
                                                       int64_t snapshot_len) {
   if (batch <= 0 || seq_len <= 0 || key_dim < 1 || value_dim < 1) return 0;
-  // Sized for the 16-byte path; the element-wise path never needs more.
-  const Plan p = make_plan(batch, seq_len, value_dim, key_dim, snapshot_len,
-                           key_dim % 8 == 0 && value_dim % 8 == 0);
-  return p.workspace_bytes;
+  // The dtype is not known here: size for whichever kernel needs more (the
+  // element-wise path never needs more than the 16-byte one).
+  const bool vec = key_dim % 8 == 0 && value_dim % 8 == 0;
+  const Plan narrow = make_plan(batch, seq_len, value_dim, key_dim, snapshot_len, vec, false);
+  const Plan wide = make_plan(batch, seq_len, value_dim, key_dim, snapshot_len, vec,
+                              use_wide(GRM_HIP_BF16, key_dim, value_dim, vec));
+  return narrow.workspace_bytes > wide.workspace_bytes ? narrow.workspace_bytes : wide.workspace_bytes;
 }
 
 extern "C" int grm_hip_chunk_update_fwd(const void* keys, const void* values, const void* queries,
@@ -743,7 +725,10 @@ extern "C" int grm_hip_chunk_update_fwd(const void* keys, const void* values, co
   a.dk = static_cast<int>(key_dim);
   a.dv = static_cast<int>(value_dim);
   const bool vec = vec_ok(keys, values, queries, hidden, snapshots, key_dim, value_dim);
-  Plan plan = make_plan(batch, seq_len, value_dim, key_dim, snapshots != nullptr ? snapshot_len : 0, vec);
+  const bool vec_m = (key_dim % 4 == 0) && aligned(memory, 4 * mem_b) && aligned(memory_out, 4 * mem_b) &&
+                     (snapshots == nullptr || aligned(snapshots, 16)) && aligned(workspace, 16);
+  const bool wide = vec_m && use_wide(in_dtype, key_dim, value_dim, vec);
+  Plan plan = make_plan(batch, seq_len, value_dim, key_dim, snapshots != nullptr ? snapshot_len : 0, vec, wide);
   if (plan.n_chunks > INT32_MAX) {
     set_error("chunk_update_fwd: seq_len too large");
     return GRM_HIP_EINVAL;
@@ -772,8 +757,7 @@ extern "C" int grm_hip_chunk_update_fwd(const void* keys, const void* values, co
     return GRM_HIP_EINVAL;
   }
   a.mem_f32 = mem_dtype == GRM_HIP_F32;
-  a.vec_m = (key_dim % 4 == 0) && aligned(memory, 4 * mem_b) && aligned(memory_out, 4 * mem_b) &&
-            (snapshots == nullptr || aligned(snapshots, 16)) && aligned(workspace, 16);
+  a.vec_m = vec_m;
   a.c = static_cast<float>((1.0 - memory_decay) / std::sqrt(static_cast<double>(key_dim)));
   for (int i = 0; i < PW_N; ++i) a.pw[i] = static_cast<float>(std::pow(memory_decay, i));
 
@@ -788,6 +772,7 @@ extern "C" int grm_hip_chunk_update_fwd(const void* keys, const void* values, co
     }
     return GRM_HIP_OK;
   }
+  if (plan.wide) return launch_scan_wide(a, in_dtype, s);
   switch (in_dtype) {
     case GRM_HIP_F32: return dispatch_dv<F32>(a, dv_tile, vec, s);
     case GRM_HIP_F16: return dispatch_dv<F16>(a, dv_tile, vec, s);

@@ -159,6 +159,26 @@ def test_time_split(dev, monkeypatch, parts, seg):
     torch.testing.assert_close(mo, mo1, rtol=1e-4, atol=1e-6)
 
 
+@pytest.mark.parametrize("B,T,K,H", [(2, 300, 128, 256), (3, 129, 64, 200), (1, 640, 96, 136), (4, 64, 16, 8)])
+def test_wide_and_narrow_tiles_agree(dev, monkeypatch, B, T, K, H):
+    """16-bit inputs run on 128-wide value tiles by default (several tiles and a
+    ragged last tile here); the 32-wide tiles (GRM_HIP_CHUNK_DV=32) compute the
+    same map.  Both against the oracle, and against each other."""
+    k, v, q, m = make_case(B, T, K, H, torch.bfloat16, torch.float32, seed=B * 31 + H)
+    kd, vd, qd, md = k.to(dev), v.to(dev), q.to(dev), m.to(dev)
+    hw, mw, sw = capi.chunk_update_fwd(kd, vd, qd, md, 0.97, 64)
+    monkeypatch.setenv("GRM_HIP_CHUNK_DV", "32")
+    hn, mn, sn = capi.chunk_update_fwd(kd, vd, qd, md, 0.97, 64)
+    torch.cuda.synchronize()
+    rh, rm, rs = oracle_fwd(k, v, q, m, 0.97, 64)
+    for tag, (h, mo, s) in (("wide", (hw, mw, sw)), ("narrow", (hn, mn, sn))):
+        close(f"{tag} hidden", h, rh, torch.bfloat16)
+        close(f"{tag} memory_out", mo, rm, torch.bfloat16)
+        close(f"{tag} snapshots", s, rs, torch.bfloat16)
+    torch.testing.assert_close(hw.float(), hn.float(), rtol=1e-2, atol=1e-3)
+    torch.testing.assert_close(mw, mn, rtol=1e-4, atol=1e-6)
+
+
 def test_long_context_split_fp32(dev, monkeypatch):
     """fp32 long sequence, automatic part count, against the oracle at fp32 tolerance."""
     B, T, K, H = 2, 4096, 64, 64
