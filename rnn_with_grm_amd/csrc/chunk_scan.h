@@ -38,6 +38,7 @@ struct ChunkFwdArgs {
   int part_chunks; // chunks per part; every part but the last is full
   float part_decay;   // decay^(part_chunks * chunk)
   float* part_states; // [batch, n_parts - 1, dv, dk]: end-state contribution of each part
+  int part_starts; // part_states[q] holds M_{q+1} (combined) rather than D_q (wide kernel)
   float c;         // (1 - decay) / sqrt(d_k)
   float pw[PW_N];  // decay^n rounded from double
 };
@@ -49,8 +50,8 @@ constexpr int kWideDv = 128;
 // aligned rows (key_dim and value_dim multiples of 8).
 bool wide_supported(int in_dtype, int64_t key_dim, int64_t value_dim, bool vec);
 
-// Launches the state pass (when a.n_parts > 1) and the full pass of the wide
-// kernel; a.v_tiles counts 128-wide value tiles.
-int launch_scan_wide(const ChunkFwdArgs& a, int in_dtype, hipStream_t stream);
+// Launches the wide kernel: with a.n_parts > 1 the state pass (and, for many
+// parts, the combine step), then the full pass.
+int launch_scan_wide(const ChunkFwdArgs& a, int in_dtype, int mem_dtype, hipStream_t stream);
 
 }  // namespace grmhip

@@ -451,7 +451,9 @@ __global__ __launch_bounds__(NTHR) void chunk_fwd_kernel(const ChunkFwdArgs a) {
             const int v = v0 + 16 * vt + n;
             const int k = 16 * kt + 4 * g;
             if constexpr (VEC) {
-              buf_store4<F32>(rs, v < dv ? (v * dk + k) * 4 : kBufOOB, st[q][vt]);
+              // Key tiles past d_k (padding of the 16-wide tiles) are not stored: their
+              // offsets would land in the next state row.
+              buf_store4<F32>(rs, (v < dv && k < dk) ? (v * dk + k) * 4 : kBufOOB, st[q][vt]);
             } else {
 #pragma unroll
               for (int r = 0; r < 4; ++r)
@@ -772,7 +774,7 @@ extern "C" int grm_hip_chunk_update_fwd(const void* keys, const void* values, co
     }
     return GRM_HIP_OK;
   }
-  if (plan.wide) return launch_scan_wide(a, in_dtype, s);
+  if (plan.wide) return launch_scan_wide(a, in_dtype, mem_dtype, s);
   switch (in_dtype) {
     case GRM_HIP_F32: return dispatch_dv<F32>(a, dv_tile, vec, s);
     case GRM_HIP_F16: return dispatch_dv<F16>(a, dv_tile, vec, s);

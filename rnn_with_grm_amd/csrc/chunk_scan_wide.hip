@@ -31,6 +31,7 @@
 #include <string.h>
 
 #include <cmath>
+#include <type_traits>
 
 #include "chunk_scan.h"
 #include "grm_hip.h"
@@ -39,20 +40,30 @@
 namespace grmhip {
 namespace {
 
-constexpr int WNW = 8;                    // waves per workgroup (two per SIMD)
-constexpr int WNT = 64 * WNW;             // threads per workgroup
-constexpr int DVT = kWideDv;              // value columns per workgroup
-constexpr int VB = DVT / (16 * WNW);      // 16-wide value blocks per wave
-static_assert(WNW == 8, "S blocks are split as 4 query blocks x 2 key halves");
+constexpr int VB = 1;  // 16-wide value blocks per wave
 
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef short s16x4 __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
 
-template <class E, int DKP>
+// Both passes run 8 waves (two per SIMD) on a 128-wide value tile; the state
+// pass keeps only K and V in LDS.
+constexpr int pass_threads(bool) { return 512; }
+
+// Up to this many parts the full pass combines M_0 and the earlier parts'
+// contributions itself; beyond it a combine step writes each part's starting
+// state and the full pass reads just that.
+constexpr int kCombineInPlaceParts = 4;
+
+template <class E, int DKP, bool FULL>
 struct WideShape {
   using raw = typename ET<E>::raw;
+  static constexpr int NW = 8;                  // waves per workgroup
+  static constexpr int NT = 64 * NW;            // threads per workgroup
+  static_assert(NT == pass_threads(FULL), "launch bound matches the tile");
+  static constexpr int DVT = 16 * VB * NW;      // value columns per workgroup
+  static_assert(!FULL || DVT == kWideDv, "full pass covers kWideDv value columns");
   // Row strides (elements) are 4 banks mod 64 (K, Q, V, output) or a distinct
   // multiple of 4 banks for each of 16 rows (P): 16-byte reads of 16 rows are
   // conflict-free and 8-byte reads of 16 consecutive rows (the transposed
@@ -64,12 +75,14 @@ struct WideShape {
   static constexpr int NKK = DKP / 32; // 32-deep key steps
   static constexpr int KU = DKP / 8;   // 16-byte units per K/Q row
   static constexpr int VU = DVT / 8;   // 16-byte units per V / output row
-  static constexpr int K_UNITS = CT * KU / WNT;
-  static constexpr int V_UNITS = CT * VU / WNT;
-  static constexpr int BUF = CT * (2 * KS + VS);  // one K/Q/V buffer, elements
+  static constexpr int K_UNITS = CT * KU / NT;
+  static constexpr int V_UNITS = CT * VU / NT;
+  static constexpr int KQ = FULL ? 2 : 1;            // K (and Q) tiles per buffer
+  static constexpr int BUF = CT * (KQ * KS + VS);    // one K/Q/V buffer, elements
+  static constexpr int EXTRA = FULL ? CT * (PS + VS) : 0;  // P and output tiles
   static constexpr size_t lds_bytes =
-      static_cast<size_t>(2 * BUF + CT * PS + CT * VS) * sizeof(raw) + PW_N * sizeof(float);
-  static_assert(K_UNITS * WNT == CT * KU && V_UNITS * WNT == CT * VU, "tiles split evenly");
+      static_cast<size_t>(2 * BUF + EXTRA) * sizeof(raw) + PW_N * sizeof(float);
+  static_assert(K_UNITS * NT == CT * KU && V_UNITS * NT == CT * VU, "tiles split evenly");
   static_assert(lds_bytes <= kMaxLds, "tile set must fit one CU's LDS");
 };
 
@@ -125,22 +138,30 @@ __device__ __forceinline__ void st_state4(__amdgpu_buffer_rsrc_t r, int off, boo
 }
 
 // FULL = true: hidden, snapshots and the final state over one time part,
-// starting from the state the earlier parts leave behind.
-// FULL = false: the state-only pass giving each earlier part's end-state
-// contribution from a zero start (keys and values only).
+// starting from M_p.  With a.part_starts the state pass's combine step has
+// already written M_p (p >= 1) to part_states[p - 1]; otherwise part_states
+// holds each earlier part's contribution D_q and the workgroup combines
+//   M_p = pd^p M_0 + sum_{q < p} pd^{p-1-q} D_q,  pd = decay^{part length}.
+// FULL = false: the state pass, D_q of each earlier part from a zero start
+// (keys and values only).
 template <class E, int DKP, bool FULL>
-__global__ __launch_bounds__(WNT, 1) void scan_wide_kernel(const ChunkFwdArgs a) {
-  using S = WideShape<E, DKP>;
+__global__ __launch_bounds__(pass_threads(FULL), 1) void scan_wide_kernel(const ChunkFwdArgs a) {
+  using S = WideShape<E, DKP, FULL>;
+  constexpr int WNT = S::NT, DVT = S::DVT;
   using raw = typename ET<E>::raw;
   constexpr int KS = S::KS, VS = S::VS, PS = S::PS, KT = S::KT, NKK = S::NKK, KU = S::KU, VU = S::VU,
                 K_UNITS = S::K_UNITS, V_UNITS = S::V_UNITS, BUF = S::BUF;
   constexpr int ES = static_cast<int>(sizeof(raw));
+  constexpr int PF = 2;  // chunks in flight between global memory and LDS
+  static_assert(PF % 2 == 0, "staging sets pair with the two LDS buffers");
+  using FullStep = std::integral_constant<bool, true>;
+  using StateStep = std::integral_constant<bool, false>;
 
   extern __shared__ __align__(16) unsigned char smem[];
-  raw* bufs = reinterpret_cast<raw*>(smem);            // 2 x { K [CT][KS], Q [CT][KS], V [CT][VS] }
-  raw* Ps = bufs + 2 * BUF;                             // [CT][PS]  P = S * coef, row = query
-  raw* Os = Ps + CT * PS;                               // [CT][VS]  output tile, row = query
-  float* pw = reinterpret_cast<float*>(Os + CT * VS);  // [PW_N]
+  raw* bufs = reinterpret_cast<raw*>(smem);  // 2 x { K [CT][KS], Q [CT][KS] (full pass), V [CT][VS] }
+  raw* Ps = bufs + 2 * BUF;                   // [CT][PS]  P = S * coef, row = query (full pass)
+  raw* Os = Ps + CT * PS;                     // [CT][VS]  output tile, row = query (full pass)
+  float* pw = reinterpret_cast<float*>(bufs + 2 * BUF + S::EXTRA);  // [PW_N]
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -153,11 +174,15 @@ __global__ __launch_bounds__(WNT, 1) void scan_wide_kernel(const ChunkFwdArgs a)
     const int per = gridDim.x >> 3;
     wg = (wg & 7) * per + (wg >> 3);
   }
+  // workgroup -> (sequence b, time part, value tile); the parts of a sequence
+  // are adjacent, so they share an XCD and earlier parts dispatch first.
   const int parts_in_grid = FULL ? a.n_parts : a.n_parts - 1;
-  const int seq = wg / a.v_tiles;
+  const int v_tiles = (a.dv + DVT - 1) / DVT;
+  const int vtile = wg % v_tiles;
+  const int seq = wg / v_tiles;
   const int64_t b = seq / parts_in_grid;
   const int part = seq % parts_in_grid;
-  const int v0 = (wg % a.v_tiles) * DVT;
+  const int v0 = vtile * DVT;
   const int dk = a.dk, dv = a.dv;
   const int64_t T = a.seq_len;
   const int chunk = a.chunk;
@@ -174,47 +199,75 @@ __global__ __launch_bounds__(WNT, 1) void scan_wide_kernel(const ChunkFwdArgs a)
   for (int i = tid; i < PW_N; i += WNT) pw[i] = a.pw[i];
 
   // ---- state: st[vb][kt], lane (g, n), register r = M[v][k] with
-  //      v = v0 + 32w + 16vb + n and k = 16kt + 4g + r.
+  //      v = v0 + 16 (VB w + vb) + n and k = 16kt + 4g + r.
   const int vl = 16 * VB * w + n;  // local value row of block 0 for this lane
   f32x4 st[VB][KT];
-  {
-    const int64_t mem_b = f32m ? 4 : ES;
-    const __amdgpu_buffer_rsrc_t rm =
-        make_rsrc(static_cast<const unsigned char*>(a.memory) + b * dv * dk * mem_b,
-                  static_cast<uint32_t>(dv * dk * mem_b));
+  auto state_off = [&](int vb, int kt) -> int {
+    const int v = v0 + vl + 16 * vb;
+    const int k = 16 * kt + 4 * g;
+    return (v < dv && k < dk) ? v * dk + k : kBufOOB;
+  };
+  auto zero_state = [&]() {
 #pragma unroll
-    for (int vb = 0; vb < VB; ++vb) {
+    for (int vb = 0; vb < VB; ++vb)
+#pragma unroll
+      for (int kt = 0; kt < KT; ++kt) st[vb][kt] = f32x4{0.f, 0.f, 0.f, 0.f};
+  };
+  const int64_t mem_b = f32m ? 4 : ES;
+  const __amdgpu_buffer_rsrc_t rmem =
+      make_rsrc(static_cast<const unsigned char*>(a.memory) + b * dv * dk * mem_b, static_cast<uint32_t>(dv * dk * mem_b));
+  auto part_rsrc = [&](int q) {
+    return make_rsrc(a.part_states + (b * (a.n_parts - 1) + q) * dv * dk, static_cast<uint32_t>(dv * dk * 4));
+  };
+  // st = pd^q_end M_0 + sum_{q < q_end} pd^{q_end-1-q} D_q, pd = decay^{part length}.
+  // Up to kCombineInPlaceParts - 1 contributions, all loads issued before any
+  // is used (one memory latency); D slots past q_end read as zero.
+  auto combine_start = [&](int q_end) {
+    constexpr int NQ = kCombineInPlaceParts - 1;
+    f32x4 d[NQ][VB][KT];
+#pragma unroll
+    for (int q = 0; q < NQ; ++q) {
+      const __amdgpu_buffer_rsrc_t rp = part_rsrc(q < q_end ? q : 0);
+#pragma unroll
+      for (int vb = 0; vb < VB; ++vb)
+#pragma unroll
+        for (int kt = 0; kt < KT; ++kt) {
+          const int off = state_off(vb, kt);
+          d[q][vb][kt] = ld_state4<F32>(rp, q < q_end ? off : kBufOOB, true);
+        }
+    }
+    float m = 1.f;  // pd^(q_end - 1 - q) for q = q_end - 1, q_end - 2, ...
+    zero_state();
+#pragma unroll
+    for (int q = NQ - 1; q >= 0; --q) {
+      if (q >= q_end) continue;
+#pragma unroll
+      for (int vb = 0; vb < VB; ++vb)
+#pragma unroll
+        for (int kt = 0; kt < KT; ++kt) st[vb][kt] += m * d[q][vb][kt];
+      m *= a.part_decay;
+    }
+#pragma unroll
+    for (int vb = 0; vb < VB; ++vb)
+#pragma unroll
+      for (int kt = 0; kt < KT; ++kt) st[vb][kt] += m * ld_state4<E>(rmem, state_off(vb, kt), f32m);
+  };
+  auto store_state = [&](__amdgpu_buffer_rsrc_t r) {
+#pragma unroll
+    for (int vb = 0; vb < VB; ++vb)
 #pragma unroll
       for (int kt = 0; kt < KT; ++kt) {
-        const int v = v0 + vl + 16 * vb;
-        const int k = 16 * kt + 4 * g;
-        const int off = (v < dv && k < dk) ? v * dk + k : kBufOOB;
-        st[vb][kt] = FULL ? ld_state4<E>(rm, off, f32m) : f32x4{0.f, 0.f, 0.f, 0.f};
+        const int off = state_off(vb, kt);
+        buf_store4<F32>(r, off == kBufOOB ? kBufOOB : off * 4, st[vb][kt]);
       }
-    }
-    if (FULL) {
-      for (int pp = 0; pp < part; ++pp) {
-        const __amdgpu_buffer_rsrc_t rp =
-            make_rsrc(a.part_states + (b * (a.n_parts - 1) + pp) * dv * dk, static_cast<uint32_t>(dv * dk * 4));
-#pragma unroll
-        for (int vb = 0; vb < VB; ++vb) {
-#pragma unroll
-          for (int kt = 0; kt < KT; ++kt) {
-            const int v = v0 + vl + 16 * vb;
-            const int k = 16 * kt + 4 * g;
-            const int off = (v < dv && k < dk) ? v * dk + k : kBufOOB;
-            st[vb][kt] = st[vb][kt] * a.part_decay + ld_state4<F32>(rp, off, true);
-          }
-        }
-      }
-    }
-  }
+  };
 
-  // Tokens of chunk c; 0 outside this workgroup's part, so loads past the
-  // part read nothing.
+  // Tokens of chunk c; 0 at or past the end of the chunk window being
+  // scanned, so loads past it read nothing.
+  int ce_cur = c_end;
   auto chunk_len = [&](int c) -> int {
     const int64_t t0 = static_cast<int64_t>(c) * chunk;
-    return (c < c_end) ? static_cast<int>(min(static_cast<int64_t>(chunk), T - t0)) : 0;
+    return (c < ce_cur) ? static_cast<int>(min(static_cast<int64_t>(chunk), T - t0)) : 0;
   };
 
   // ---- staging: unit u of this thread is row (tid + WNT u) / KU, 16-byte
@@ -224,7 +277,8 @@ __global__ __launch_bounds__(WNT, 1) void scan_wide_kernel(const ChunkFwdArgs a)
     U8<E> q[K_UNITS];
     U8<E> v[V_UNITS];
   };
-  auto load_chunk = [&](int c, Stage& sg) {
+  auto load_chunk = [&](int c, Stage& sg, auto full) {
+    constexpr bool F = decltype(full)::value;
     const int64_t t0 = static_cast<int64_t>(c) * chunk;
     const int L = chunk_len(c);
     const __amdgpu_buffer_rsrc_t rk = make_rsrc(keys + t0 * dk, static_cast<uint32_t>(L * dk * ES));
@@ -236,7 +290,7 @@ __global__ __launch_bounds__(WNT, 1) void scan_wide_kernel(const ChunkFwdArgs a)
       const int row = l / KU, col = 8 * (l % KU);
       const int off = col < dk ? (row * dk + col) * ES : kBufOOB;
       sg.k[u] = buf_load8<E>(rk, off);
-      if constexpr (FULL) sg.q[u] = buf_load8<E>(rq, off);
+      if constexpr (F) sg.q[u] = buf_load8<E>(rq, off);
     }
 #pragma unroll
     for (int u = 0; u < V_UNITS; ++u) {
@@ -245,16 +299,17 @@ __global__ __launch_bounds__(WNT, 1) void scan_wide_kernel(const ChunkFwdArgs a)
       sg.v[u] = buf_load8<E>(rv, col < dv ? (row * dv + col) * ES : kBufOOB);
     }
   };
-  auto store_chunk = [&](int buf, const Stage& sg) {
+  auto store_chunk = [&](int buf, const Stage& sg, auto full) {
+    constexpr bool F = decltype(full)::value;
     raw* Kb = bufs + buf * BUF;
     raw* Qb = Kb + CT * KS;
-    raw* Vb = Qb + CT * KS;
+    raw* Vb = Kb + S::KQ * CT * KS;
 #pragma unroll
     for (int u = 0; u < K_UNITS; ++u) {
       const int l = tid + WNT * u;
       const int row = l / KU, col = 8 * (l % KU);
       *reinterpret_cast<U8<E>*>(Kb + row * KS + col) = sg.k[u];
-      if constexpr (FULL) *reinterpret_cast<U8<E>*>(Qb + row * KS + col) = sg.q[u];
+      if constexpr (F) *reinterpret_cast<U8<E>*>(Qb + row * KS + col) = sg.q[u];
     }
 #pragma unroll
     for (int u = 0; u < V_UNITS; ++u) {
@@ -263,12 +318,12 @@ __global__ __launch_bounds__(WNT, 1) void scan_wide_kernel(const ChunkFwdArgs a)
       *reinterpret_cast<U8<E>*>(Vb + row * VS + col) = sg.v[u];
     }
   };
-  // Output tile of the previous chunk (Os) -> hidden rows, whole rows per wave.
+  // Output tile of a chunk (Os) -> hidden rows, whole rows per wave.
   auto flush_out = [&](int c) {
     const int64_t t0 = static_cast<int64_t>(c) * chunk;
     const int L = chunk_len(c);
-    const __amdgpu_buffer_rsrc_t rh =
-        make_rsrc(hidden + (hidden != nullptr ? t0 * dv : 0), static_cast<uint32_t>(hidden != nullptr ? L * dv * ES : 0));
+    const __amdgpu_buffer_rsrc_t rh = make_rsrc(hidden + (hidden != nullptr ? t0 * dv : 0),
+                                                static_cast<uint32_t>(hidden != nullptr ? L * dv * ES : 0));
 #pragma unroll
     for (int u = 0; u < V_UNITS; ++u) {
       const int l = tid + WNT * u;
@@ -278,30 +333,15 @@ __global__ __launch_bounds__(WNT, 1) void scan_wide_kernel(const ChunkFwdArgs a)
     }
   };
 
-  Stage sg0, sg1;
-  load_chunk(c_begin, sg0);
-  load_chunk(c_begin + 1, sg1);
-  __syncthreads();  // pw visible
-  store_chunk(0, sg0);
-
+  static_assert(!FULL || S::NW == 8, "S blocks are split as 4 query blocks x 2 key halves");
   // This wave's S block: query rows i = 16 i_blk + n, key columns
   // j = 32 j_half + 16 jj + 4g + r (jj = 0, 1), with causal coefficients.
   const int i_blk = w & 3;
   const int j_half = w >> 2;
   const int i_loc = 16 * i_blk + n;
   float coef[2][4];
-#pragma unroll
-  for (int jj = 0; jj < 2; ++jj) {
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const int j = 32 * j_half + 16 * jj + 4 * g + r;
-      coef[jj][r] = (j <= i_loc) ? a.c * pw[max(i_loc - j, 0)] : 0.f;
-    }
-  }
   // decay^{i+1} for the query rows i = 16 ib + n of this lane's output tiles.
   float s_start[4];
-#pragma unroll
-  for (int ib = 0; ib < 4; ++ib) s_start[ib] = pw[16 * ib + n + 1];
   // State-update weights c * decay^{L-1-j} for this lane's slots
   // j = 32p + 16 (s / 4) + 4g + s % 4 (the token order of every 64-deep operand).
   float wgt[2][8];
@@ -315,22 +355,21 @@ __global__ __launch_bounds__(WNT, 1) void scan_wide_kernel(const ChunkFwdArgs a)
       }
     }
   };
-  set_weights(CT);
-  int snap_phase = a.snap_every > 0 ? (c_begin + 1) % a.snap_every : 1;  // == 0: snapshot after this chunk
-  __syncthreads();
+  int snap_phase = 1;  // == 0: a snapshot follows the current chunk
 
-  auto step = [&](int c, int cur, Stage& ld, const Stage& nx) {
+  auto step = [&](int c, int cb, int cur, Stage& ld, const Stage& nx, auto full) {
+    constexpr bool F = decltype(full)::value;
     const int L = chunk_len(c);
     const raw* Kb = bufs + cur * BUF;
     const raw* Qb = Kb + CT * KS;
-    const raw* Vb = Qb + CT * KS;
-    if (c > c_begin) __syncthreads();  // chunk c in LDS; the previous output tile is complete
-    load_chunk(c + 2, ld);
-    if (FULL && c > c_begin) flush_out(c - 1);
+    const raw* Vb = Kb + S::KQ * CT * KS;
+    if (c > cb) __syncthreads();  // chunk c in LDS; the previous output tile is complete
+    load_chunk(c + PF, ld, full);
+    if (F && c > cb) flush_out(c - 1);
     if (L != CT) set_weights(L);
 
     f32x4 o[4][VB];
-    if constexpr (FULL) {
+    if constexpr (F) {
       // S^T blocks: A = K rows j, B = Q rows i -> lane holds S[i_loc][j] for
       // j = 32 j_half + 16 jj + 4g + r.  Blocks wholly above the diagonal are
       // neither computed nor read.
@@ -426,10 +465,10 @@ __global__ __launch_bounds__(WNT, 1) void scan_wide_kernel(const ChunkFwdArgs a)
       }
     }
 
-    store_chunk(cur ^ 1, nx);  // chunk c + 1 into the other buffer
-    __syncthreads();           // P complete; the previous output tile has left
+    store_chunk(cur ^ 1, nx, full);  // chunk c + 1 into the other buffer
+    __syncthreads();                 // P complete; the previous output tile has left
 
-    if constexpr (FULL) {
+    if constexpr (F) {
       // O^T += V^T P^T: A = V^T rows v, B = P rows i; P[i][j] = 0 for j > i.
 #pragma unroll
       for (int ib = 0; ib < 4; ++ib) {
@@ -447,61 +486,83 @@ __global__ __launch_bounds__(WNT, 1) void scan_wide_kernel(const ChunkFwdArgs a)
       }
       if (a.snap_every > 0 && (snap_phase == 0 || c + 1 == n_chunks)) {
         const int si = c / a.snap_every;
-        const __amdgpu_buffer_rsrc_t rs =
-            make_rsrc(a.snapshots + (b * a.n_snap + si) * dv * dk, static_cast<uint32_t>(dv * dk * 4));
-#pragma unroll
-        for (int vb = 0; vb < VB; ++vb) {
-#pragma unroll
-          for (int kt = 0; kt < KT; ++kt) {
-            const int v = v0 + vl + 16 * vb;
-            const int k = 16 * kt + 4 * g;
-            buf_store4<F32>(rs, (v < dv && k < dk) ? (v * dk + k) * 4 : kBufOOB, st[vb][kt]);
-          }
-        }
+        store_state(make_rsrc(a.snapshots + (b * a.n_snap + si) * dv * dk, static_cast<uint32_t>(dv * dk * 4)));
       }
       if (a.snap_every > 0) snap_phase = (snap_phase + 1 == a.snap_every) ? 0 : snap_phase + 1;
     }
   };
 
-  for (int c = c_begin; c < c_end; c += 2) {
-    step(c, 0, sg0, sg1);
-    if (c + 1 < c_end) step(c + 1, 1, sg1, sg0);
+  // Scans chunks [cb, ce) from the state in st.  init() may set it; its loads
+  // go out first, so the combine arithmetic runs while the chunk loads land.
+  auto scan = [&](auto full, int cb, int ce, auto init) {
+    constexpr bool F = decltype(full)::value;
+    ce_cur = ce;
+    Stage sg[PF];
+    init();
+#pragma unroll
+    for (int i = 0; i < PF; ++i) load_chunk(cb + i, sg[i], full);
+    __syncthreads();  // LDS buffers free, pw visible
+    store_chunk(0, sg[0], full);
+    if (F) snap_phase = a.snap_every > 0 ? (cb + 1) % a.snap_every : 1;
+    __syncthreads();
+    for (int c = cb; c < ce; c += PF) {
+#pragma unroll
+      for (int i = 0; i < PF; ++i) {
+        if (c + i < ce) step(c + i, cb, i & 1, sg[i], sg[(i + 1) % PF], full);
+      }
+    }
+    if constexpr (F) {
+      __syncthreads();
+      flush_out(ce - 1);
+    }
+  };
+  auto no_init = []() {};
+
+  __syncthreads();  // pw visible
+  set_weights(CT);
+  if constexpr (FULL) {
+#pragma unroll
+    for (int jj = 0; jj < 2; ++jj) {
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int j = 32 * j_half + 16 * jj + 4 * g + r;
+        coef[jj][r] = (j <= i_loc) ? a.c * pw[max(i_loc - j, 0)] : 0.f;
+      }
+    }
+#pragma unroll
+    for (int ib = 0; ib < 4; ++ib) s_start[ib] = pw[16 * ib + n + 1];
   }
 
-  if constexpr (FULL) {
-    __syncthreads();
-    flush_out(c_end - 1);
+  if constexpr (!FULL) {
+    zero_state();
+    scan(StateStep{}, c_begin, c_end, no_init);
+    store_state(part_rsrc(part));
+    return;
+  } else {
+    scan(FullStep{}, c_begin, c_end, [&]() {
+      if (a.part_starts && part > 0) {
+        const __amdgpu_buffer_rsrc_t rp = part_rsrc(part - 1);
+#pragma unroll
+        for (int vb = 0; vb < VB; ++vb)
+#pragma unroll
+          for (int kt = 0; kt < KT; ++kt) st[vb][kt] = ld_state4<F32>(rp, state_off(vb, kt), true);
+      } else {
+        combine_start(part);
+      }
+    });
     if (a.memory_out == nullptr || part != a.n_parts - 1) return;
-    const int64_t mem_b = f32m ? 4 : ES;
     const __amdgpu_buffer_rsrc_t ro = make_rsrc(static_cast<unsigned char*>(a.memory_out) + b * dv * dk * mem_b,
                                                 static_cast<uint32_t>(dv * dk * mem_b));
 #pragma unroll
-    for (int vb = 0; vb < VB; ++vb) {
+    for (int vb = 0; vb < VB; ++vb)
 #pragma unroll
-      for (int kt = 0; kt < KT; ++kt) {
-        const int v = v0 + vl + 16 * vb;
-        const int k = 16 * kt + 4 * g;
-        st_state4<E>(ro, (v < dv && k < dk) ? v * dk + k : kBufOOB, f32m, st[vb][kt]);
-      }
-    }
-  } else {
-    const __amdgpu_buffer_rsrc_t rp = make_rsrc(a.part_states + (b * (a.n_parts - 1) + part) * dv * dk,
-                                                static_cast<uint32_t>(dv * dk * 4));
-#pragma unroll
-    for (int vb = 0; vb < VB; ++vb) {
-#pragma unroll
-      for (int kt = 0; kt < KT; ++kt) {
-        const int v = v0 + vl + 16 * vb;
-        const int k = 16 * kt + 4 * g;
-        buf_store4<F32>(rp, (v < dv && k < dk) ? (v * dk + k) * 4 : kBufOOB, st[vb][kt]);
-      }
-    }
+      for (int kt = 0; kt < KT; ++kt) st_state4<E>(ro, state_off(vb, kt), f32m, st[vb][kt]);
   }
 }
 
 template <class E, int DKP, bool FULL>
 int launch_wide_pass(ChunkFwdArgs a, hipStream_t stream) {
-  using S = WideShape<E, DKP>;
+  using S = WideShape<E, DKP, FULL>;
   static bool attr_set = false;
   if (!attr_set) {
     hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&scan_wide_kernel<E, DKP, FULL>),
@@ -512,18 +573,59 @@ int launch_wide_pass(ChunkFwdArgs a, hipStream_t stream) {
     }
     attr_set = true;
   }
-  const int64_t grid = a.batch * (FULL ? a.n_parts : a.n_parts - 1) * a.v_tiles;
+  const int64_t v_tiles = (a.dv + S::DVT - 1) / S::DVT;
+  const int64_t grid = a.batch * (FULL ? a.n_parts : a.n_parts - 1) * v_tiles;
+  if (grid > INT32_MAX) {
+    set_error("chunk_update_fwd: batch too large for one launch");
+    return GRM_HIP_EINVAL;
+  }
   a.xcd_remap = (grid % 8 == 0) ? 1 : 0;
-  hipLaunchKernelGGL((scan_wide_kernel<E, DKP, FULL>), dim3(static_cast<unsigned>(grid)), dim3(WNT),
+  hipLaunchKernelGGL((scan_wide_kernel<E, DKP, FULL>), dim3(static_cast<unsigned>(grid)), dim3(S::NT),
                      S::lds_bytes, stream, a);
   return check_launch(FULL ? "chunk_update_fwd" : "chunk_update_fwd(part states)");
 }
 
+// Part starting states in place of the contributions: slot q of part_states
+// becomes M_{q+1} = pd M_q + D_q, one thread per four state elements.
+__global__ void combine_parts_kernel(const void* memory, float* part_states, int64_t batch, int64_t n_parts,
+                                     int64_t elems, int mem_f32, int mem_dtype, float part_decay) {
+  const int64_t units = elems / 4;
+  const int64_t total = batch * units;
+  for (int64_t i = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x; i < total;
+       i += static_cast<int64_t>(gridDim.x) * blockDim.x) {
+    const int64_t b = i / units, u = i - b * units;
+    f32x4 m;
+    if (mem_f32) {
+      m = reinterpret_cast<const f32x4*>(static_cast<const float*>(memory) + b * elems)[u];
+    } else {
+      const uint16_t* src = static_cast<const uint16_t*>(memory) + b * elems + 4 * u;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) m[r] = mem_dtype == GRM_HIP_F16 ? ET<F16>::to_f(src[r]) : ET<BF16>::to_f(src[r]);
+    }
+    f32x4* slots = reinterpret_cast<f32x4*>(part_states + b * (n_parts - 1) * elems) + u;
+    for (int64_t q = 0; q + 1 < n_parts; ++q) {
+      m = m * part_decay + slots[q * units];
+      slots[q * units] = m;
+    }
+  }
+}
+
 template <class E, int DKP>
-int launch_wide(const ChunkFwdArgs& a, hipStream_t stream) {
+int launch_wide(ChunkFwdArgs a, int mem_dtype, hipStream_t stream) {
+  a.part_starts = 0;
   if (a.n_parts > 1) {
     const int rc = launch_wide_pass<E, DKP, false>(a, stream);
     if (rc != GRM_HIP_OK) return rc;
+    if (a.n_parts > kCombineInPlaceParts) {
+      const int64_t units = a.batch * (static_cast<int64_t>(a.dv) * a.dk / 4);
+      const int64_t blocks = (units + 255) / 256 < 4096 ? (units + 255) / 256 : 4096;
+      hipLaunchKernelGGL(combine_parts_kernel, dim3(static_cast<unsigned>(blocks)), dim3(256), 0, stream, a.memory,
+                         a.part_states, a.batch, static_cast<int64_t>(a.n_parts),
+                         static_cast<int64_t>(a.dv) * a.dk, a.mem_f32, mem_dtype, a.part_decay);
+      const int rc2 = check_launch("chunk_update_fwd(part starts)");
+      if (rc2 != GRM_HIP_OK) return rc2;
+      a.part_starts = 1;
+    }
   }
   return launch_wide_pass<E, DKP, true>(a, stream);
 }
@@ -535,11 +637,11 @@ bool wide_supported(int in_dtype, int64_t key_dim, int64_t value_dim, bool vec) 
          value_dim % 8 == 0;
 }
 
-int launch_scan_wide(const ChunkFwdArgs& a, int in_dtype, hipStream_t stream) {
+int launch_scan_wide(const ChunkFwdArgs& a, int in_dtype, int mem_dtype, hipStream_t stream) {
   if (in_dtype == GRM_HIP_F16) {
-    return a.dk <= 64 ? launch_wide<F16, 64>(a, stream) : launch_wide<F16, 128>(a, stream);
+    return a.dk <= 64 ? launch_wide<F16, 64>(a, mem_dtype, stream) : launch_wide<F16, 128>(a, mem_dtype, stream);
   }
-  return a.dk <= 64 ? launch_wide<BF16, 64>(a, stream) : launch_wide<BF16, 128>(a, stream);
+  return a.dk <= 64 ? launch_wide<BF16, 64>(a, mem_dtype, stream) : launch_wide<BF16, 128>(a, mem_dtype, stream);
 }
 
 }  // namespace grmhip

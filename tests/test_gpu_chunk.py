@@ -135,11 +135,13 @@ def test_config2_shape(dev):
     assert torch.equal(hid, hid3) and torch.equal(snaps, snaps3)
 
 
-@pytest.mark.parametrize("parts", [2, 3, 5])
+@pytest.mark.parametrize("parts", [2, 3, 5, 9])
 @pytest.mark.parametrize("seg", [0, 64, 100, 128])
 def test_time_split(dev, monkeypatch, parts, seg):
-    """Sequences split into time parts (state pass + scan pass) match the oracle
-    and the single-chain scan; ragged last part and odd snapshot lengths included."""
+    """Sequences split into time parts match the oracle and the single-chain scan
+    (up to 4 parts each part combines the earlier contributions itself, beyond
+    that a combine step writes the starting states); ragged last part and odd
+    snapshot lengths included."""
     B, T, K, H = 3, 700, 128, 96
     k, v, q, m = make_case(B, T, K, H, torch.bfloat16, torch.float32, seed=parts * 7 + seg)
     kd, vd, qd, md = k.to(dev), v.to(dev), q.to(dev), m.to(dev)
