@@ -8,16 +8,16 @@
 //   apply bwd:   dM[row, k] = dh[row] * q[row / (R*H), k]
 //                dq[bq, k]  = sum_{rh} dh[bq*R*H + rh] * M[bq*R*H + rh, k]
 //                (reference grm/csrc/apply_query.cu:77-169, grm_cuda.cpp:136-154)
-// The gather has two kernels, both with 16-byte accesses and non-temporal
-// stores for large outputs (the materialised output is never re-read here):
+// The gather has two kernels, both with 16-byte accesses:
 //   - column-tiled, when every archived state is referenced about once or more
-//     (n_index >= segments): one workgroup per (sequence, column slice) keeps
-//     that slice of all the sequence's states in LDS and writes it into every
-//     output row, so the archive crosses HBM once and the kernel runs at the
-//     HBM write rate;
+//     (n_index >= segments): one workgroup per (sequence, row chunk, column
+//     slice) keeps that slice of all the sequence's states in LDS and writes it
+//     into its output rows, so the archive crosses HBM once and the kernel runs
+//     at the HBM write rate;
 //   - row-wise otherwise: one row per workgroup pass, rows split into eight
 //     contiguous ranges, one per XCD, so one XCD's L2 sees the archive of only
-//     a few sequences at a time.
+//     a few sequences at a time; non-temporal stores for large outputs (the
+//     materialised output is never re-read here).
 #include <stdint.h>
 #include <string.h>
 
@@ -98,19 +98,24 @@ __global__ __launch_bounds__(GT) void gather_kernel(const GatherArgs a) {
 }
 
 // Column-tiled gather for the many-queries case (n_index >= segments): workgroup
-// (b, t) stages units [t*W, (t+1)*W) of every archived state of sequence b in
-// LDS (S*W*16 bytes, read from HBM exactly once over the whole grid), then
-// writes that W-unit slice of every output row of b.  The archive is read once
-// instead of once per reference, so the kernel runs at the HBM write rate.
-constexpr int GC_THREADS = 512;
+// (b, row chunk, t) stages units [t*W, (t+1)*W) of every archived state of
+// sequence b in LDS (S*W*16 bytes; the archive crosses HBM once, the second row
+// chunk re-reads it from L2), then writes that W-unit slice of its output rows.
+// Workgroups of one (b, row chunk) are adjacent in launch order, so the rows
+// being written at any time form a narrow band of memory.  Plain stores: on
+// this path they sustain a higher HBM write rate than non-temporal ones.
+constexpr int GC_THREADS = 1024;
 constexpr int GC_UNROLL = 4;
+constexpr int GC_ROW_CHUNKS = 2;
 constexpr int64_t GC_MAX_LDS = 128 * 1024;
 
-template <int W, bool NT>
-__global__ __launch_bounds__(GC_THREADS) void gather_cols_kernel(const GatherArgs a, int64_t tiles) {
+template <int W>
+__global__ __launch_bounds__(GC_THREADS) void gather_cols_kernel(const GatherArgs a, int64_t tiles, int64_t chunks) {
   extern __shared__ u32x4 cols[];
-  const int64_t b = blockIdx.x / tiles;
-  const int64_t t = blockIdx.x - b * tiles;
+  const int64_t t = blockIdx.x % tiles;
+  const int64_t rest = blockIdx.x / tiles;
+  const int64_t ch = rest % chunks;
+  const int64_t b = rest / chunks;
   const int64_t S = a.segments, ru = a.row_units;
   const u32x4* src = static_cast<const u32x4*>(a.mem) + b * S * ru + t * W;
   for (int64_t e = threadIdx.x; e < S * W; e += GC_THREADS) {
@@ -120,12 +125,15 @@ __global__ __launch_bounds__(GC_THREADS) void gather_cols_kernel(const GatherArg
   __syncthreads();
   constexpr int RPP = GC_THREADS / W;  // output rows per pass
   const int w = threadIdx.x % W;
+  const int64_t rows = (a.n_index + chunks - 1) / chunks;
+  const int64_t r0 = ch * rows;
+  const int64_t r1 = min(a.n_index, r0 + rows);
   const int64_t* ib = a.idx + b * a.n_index;
   u32x4* ob = static_cast<u32x4*>(a.out) + b * a.n_index * ru + t * W + w;
   const bool count = a.bad != nullptr && t == 0 && w == 0;
   const u32x4 zero = {0u, 0u, 0u, 0u};
-  int64_t i = threadIdx.x / W;
-  for (; i + (GC_UNROLL - 1) * RPP < a.n_index; i += GC_UNROLL * RPP) {
+  int64_t i = r0 + threadIdx.x / W;
+  for (; i + (GC_UNROLL - 1) * RPP < r1; i += GC_UNROLL * RPP) {
     int64_t s[GC_UNROLL];
 #pragma unroll
     for (int r = 0; r < GC_UNROLL; ++r) s[r] = ib[i + r * RPP];
@@ -133,22 +141,22 @@ __global__ __launch_bounds__(GC_THREADS) void gather_cols_kernel(const GatherArg
     for (int r = 0; r < GC_UNROLL; ++r) {
       const bool ok = s[r] >= 0 && s[r] < S;
       if (!ok && count) atomicAdd(a.bad, 1);
-      put<u32x4, NT>(ob + (i + r * RPP) * ru, ok ? cols[s[r] * W + w] : zero);
+      ob[(i + r * RPP) * ru] = ok ? cols[s[r] * W + w] : zero;
     }
   }
-  for (; i < a.n_index; i += RPP) {
+  for (; i < r1; i += RPP) {
     const int64_t s = ib[i];
     const bool ok = s >= 0 && s < S;
     if (!ok && count) atomicAdd(a.bad, 1);
-    put<u32x4, NT>(ob + i * ru, ok ? cols[s * W + w] : zero);
+    ob[i * ru] = ok ? cols[s * W + w] : zero;
   }
 }
 
-template <int W, bool NT>
+template <int W>
 int launch_gather_cols(GatherArgs a, hipStream_t s) {
   static bool attr_set = false;
   if (!attr_set) {
-    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&gather_cols_kernel<W, NT>),
+    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&gather_cols_kernel<W>),
                                        hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(GC_MAX_LDS));
     if (e != hipSuccess) {
       set_error("batched_gather: hipFuncSetAttribute failed: %s", hipGetErrorString(e));
@@ -157,9 +165,10 @@ int launch_gather_cols(GatherArgs a, hipStream_t s) {
     attr_set = true;
   }
   const int64_t tiles = a.row_units / W;
+  const int64_t chunks = a.n_index >= GC_ROW_CHUNKS * GC_THREADS ? GC_ROW_CHUNKS : 1;
   const size_t lds = static_cast<size_t>(a.segments * W * 16);
-  hipLaunchKernelGGL((gather_cols_kernel<W, NT>), dim3(static_cast<unsigned>(a.batch * tiles)),
-                     dim3(GC_THREADS), lds, s, a, tiles);
+  hipLaunchKernelGGL((gather_cols_kernel<W>), dim3(static_cast<unsigned>(a.batch * chunks * tiles)),
+                     dim3(GC_THREADS), lds, s, a, tiles, chunks);
   return check_launch("batched_gather");
 }
 
@@ -171,17 +180,16 @@ int cols_width(const GatherArgs& a) {
   for (int w : {32, 16, 8}) {
     if (a.row_units % w != 0 || a.segments * w * 16 > GC_MAX_LDS) continue;
     const int64_t grid = a.batch * (a.row_units / w);
-    if (grid < 1024 || grid > INT32_MAX) continue;
+    if (grid < 1024 || grid * GC_ROW_CHUNKS > INT32_MAX) continue;
     return w;
   }
   return 0;
 }
 
-template <bool NT>
 int launch_cols_any(GatherArgs a, int w, hipStream_t s) {
-  if (w == 32) return launch_gather_cols<32, NT>(a, s);
-  if (w == 16) return launch_gather_cols<16, NT>(a, s);
-  return launch_gather_cols<8, NT>(a, s);
+  if (w == 32) return launch_gather_cols<32>(a, s);
+  if (w == 16) return launch_gather_cols<16>(a, s);
+  return launch_gather_cols<8>(a, s);
 }
 
 template <typename U, bool NT>
@@ -460,7 +468,7 @@ extern "C" int grm_hip_batched_gather(const void* memories, const int64_t* indic
     // Non-temporal stores only pay for outputs far larger than L2.
     const bool nt = total_rows * row_bytes >= (int64_t(64) << 20);
     const int w = cols_width(a);
-    if (w > 0) return nt ? launch_cols_any<true>(a, w, s) : launch_cols_any<false>(a, w, s);
+    if (w > 0) return launch_cols_any(a, w, s);
     if (nt) return launch_gather<u32x4, true>(a, s);
     return launch_gather<u32x4, false>(a, s);
   }
