@@ -11,6 +11,7 @@ from .cuda_ops import (  # noqa: F401
     cuda_batched_memory_gather,
     cuda_chunk_update,
     cuda_fuse_residual,
+    cuda_gather_apply,
     cuda_segment_scan,
     cuda_topk_route,
     get_grm_cuda_runtime_status,
@@ -25,6 +26,7 @@ __all__ = [
     "cuda_batched_memory_gather",
     "cuda_chunk_update",
     "cuda_fuse_residual",
+    "cuda_gather_apply",
     "cuda_segment_scan",
     "cuda_topk_route",
     "get_grm_cuda_runtime_status",

@@ -2,9 +2,10 @@
 //
 // The five schemas are the reference's, character for character
 // (reference grm/csrc/bindings.cpp:5-11), so grm.core.cuda_ops and every model
-// above it bind to this library unchanged.  Three more ops live in the same
+// above it bind to this library unchanged.  Four more ops live in the same
 // namespace: segment_scan_forward (whole-sequence update with per-segment
-// state snapshots), topk_route (score -> top-k -> softmax) and fuse_residual.
+// state snapshots), topk_route (score -> top-k -> softmax), fuse_residual and
+// gather_apply (gather + query application without materialising the states).
 //
 // CUDA-key kernels (HIP devices dispatch on the CUDA key in PyTorch-ROCm)
 // check the inputs, allocate outputs with ATen on the input's device and call
@@ -210,6 +211,23 @@ Tensor batched_memory_gather_generic(const Tensor& memories, const Tensor& indic
   for (int64_t b = 0; b < B; ++b) rows.push_back(memories[b].index_select(0, idx[b]));
   if (B == 0) return at::empty(shape, memories.options());
   return at::stack(rows, 0).reshape(shape).contiguous();
+}
+
+// gather_apply: the reference's composition apply_query_forward(
+// batched_memory_gather(memories, indices), queries.to(memories.dtype))
+// (grm/core/cuda_ops.py:370-402, paper_grm.py:229,301-313) in one op.
+void check_gather_apply_inputs(const Tensor& memories, const Tensor& indices, const Tensor& queries) {
+  check_gather_inputs(memories, indices);
+  TORCH_CHECK(queries.dim() == indices.dim(),
+              "gather_apply: queries must be [B, K] with indices [B, R], or [B, Q, K] with indices [B, Q, R]");
+  TORCH_CHECK(queries.size(0) == memories.size(0), "gather_apply: batch dim mismatch");
+  TORCH_CHECK(queries.size(-1) == memories.size(3), "gather_apply: key dim mismatch");
+  if (indices.dim() == 3) TORCH_CHECK(queries.size(1) == indices.size(1), "gather_apply: query dim mismatch");
+}
+
+Tensor gather_apply_generic(const Tensor& memories, const Tensor& indices, const Tensor& queries) {
+  check_gather_apply_inputs(memories, indices, queries);
+  return apply_query_forward_generic(batched_memory_gather_generic(memories, indices), queries.to(memories.scalar_type()));
 }
 
 // Canonical routing on the host: one float32 FMA chain per score, ties to the
@@ -441,6 +459,41 @@ Tensor batched_memory_gather_hip(const Tensor& memories, const Tensor& indices) 
   return out;
 }
 
+Tensor gather_apply_hip(const Tensor& memories, const Tensor& indices, const Tensor& queries) {
+  check_gather_apply_inputs(memories, indices, queries);
+  if (!same_cuda_device({&memories, &indices, &queries}) || dtype_code(memories.scalar_type()) < 0 ||
+      dtype_code(queries.scalar_type()) < 0 || memories.size(3) > 128 || memories.size(1) > 16384) {
+    g_generic_calls.fetch_add(1);
+    return gather_apply_generic(memories, indices, queries);
+  }
+  c10::OptionalDeviceGuard guard(memories.device());
+  Tensor mm = memories.contiguous();
+  Tensor idx = indices.to(at::kLong).contiguous();
+  Tensor q = queries.contiguous();
+  const int64_t B = mm.size(0), S = mm.size(1), H = mm.size(2), K = mm.size(3);
+  const int64_t Q = idx.dim() == 3 ? idx.size(1) : 1;
+  const int64_t R = idx.size(-1);
+  std::vector<int64_t> shape{B};
+  if (idx.dim() == 3) shape.push_back(Q);
+  shape.push_back(R);
+  shape.push_back(H);
+  Tensor out = at::empty(shape, mm.options());
+  const int64_t wsb = grm_hip_gather_apply_workspace(B, S, Q * R);
+  Tensor ws = at::empty({std::max<int64_t>(wsb, 16)}, mm.options().dtype(at::kByte));
+  Tensor bad;
+  const bool check = check_indices_requested();
+  if (check) bad = at::zeros({1}, mm.options().dtype(at::kInt));
+  check_rc(grm_hip_gather_apply(mm.data_ptr(), idx.data_ptr<int64_t>(), q.data_ptr(), out.data_ptr(), ws.data_ptr(),
+                                wsb, B, S, Q, R, H, K, dtype_code(mm.scalar_type()), dtype_code(q.scalar_type()),
+                                check ? bad.data_ptr<int32_t>() : nullptr, current_stream(mm)),
+           "gather_apply");
+  if (check) {
+    const int64_t nbad = bad.item<int32_t>();
+    TORCH_CHECK_INDEX(nbad == 0, "gather_apply: ", nbad, " index values outside [0, ", S, ")");
+  }
+  return out;
+}
+
 // ---- new ops --------------------------------------------------------------
 
 std::tuple<Tensor, Tensor, Tensor> segment_scan_forward_generic(const Tensor& keys,
@@ -581,6 +634,7 @@ TORCH_LIBRARY(grm_cuda, m) {
   m.def("segment_scan_forward(Tensor keys, Tensor values, Tensor queries, Tensor memory, float memory_decay, int segment_len) -> (Tensor hidden, Tensor memory_out, Tensor snapshots)");
   m.def("topk_route(Tensor queries, Tensor keys, int top_k, float scale, float temperature) -> (Tensor gates, Tensor indices, Tensor scores)");
   m.def("fuse_residual(Tensor h_online, Tensor retrieved, Tensor gates, Tensor? weight, Tensor? bias, float eps) -> Tensor");
+  m.def("gather_apply(Tensor memories, Tensor indices, Tensor queries) -> Tensor");
 }
 
 TORCH_LIBRARY_IMPL(grm_cuda, CPU, m) {
@@ -592,6 +646,7 @@ TORCH_LIBRARY_IMPL(grm_cuda, CPU, m) {
   m.impl("segment_scan_forward", grm::segment_scan_forward_generic);
   m.impl("topk_route", grm::topk_route_cpu);
   m.impl("fuse_residual", grm::fuse_residual_generic);
+  m.impl("gather_apply", grm::gather_apply_generic);
 }
 
 TORCH_LIBRARY_IMPL(grm_cuda, CUDA, m) {
@@ -603,6 +658,7 @@ TORCH_LIBRARY_IMPL(grm_cuda, CUDA, m) {
   m.impl("segment_scan_forward", grm::segment_scan_forward_hip);
   m.impl("topk_route", grm::topk_route_hip);
   m.impl("fuse_residual", grm::fuse_residual_hip);
+  m.impl("gather_apply", grm::gather_apply_hip);
 }
 
 PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {

@@ -1,0 +1,337 @@
+// Gather + query application over archived segment states, without
+// materialising the gathered states, gfx950.
+//
+//   out[b, q, r, h] = sum_k memories[b, idx[b, q, r], h, k] * q'[b, q, k]
+//
+// which is the reference's apply_query_forward(batched_memory_gather(M, idx), q)
+// (grm/core/cuda_ops.py:370-402; apply_query.cu:14-75 and batched_gather.cu:14-77
+// for the two kernels it chains, paper_grm.py:229,301-313 for the composition),
+// with q' = q cast to the memories' dtype as the caller does (paper_grm.py:301).
+//
+// The reference materialises [B, Q, R, d_v, d_k] (64 GiB at BASELINE config 3)
+// and reads it back.  Here the (q, r) pairs of each sequence are first sorted by
+// segment (one workgroup per sequence: LDS histogram, exclusive scan, scatter);
+// then one workgroup per (sequence, segment, 128-row value tile) reads that
+// archived state once into LDS and applies it to every query that selected it
+// with fp32 MFMA (16x16x4), 64 pairs at a time.  Each pair's output row is
+// written whole by exactly one workgroup, so the result does not depend on the
+// order in which the sort placed pairs.
+#include <stdint.h>
+#include <string.h>
+
+#include "grm_hip.h"
+#include "grm_hip_common.h"
+
+namespace grmhip {
+namespace {
+
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+constexpr int BK_THREADS = 1024;     // bucket kernel
+constexpr int64_t kMaxSegments = 16384;
+constexpr int AP_THREADS = 256;      // apply kernel: 4 waves
+constexpr int AP_V = 128;            // value rows per workgroup
+constexpr int AP_N = 64;             // (q, r) pairs per tile
+
+struct RetrieveArgs {
+  const void* mem;
+  const int64_t* idx;
+  const void* queries;
+  void* out;
+  int32_t* offsets;  // [batch, segments + 1]
+  int32_t* list;     // [batch, n_index]
+  int32_t* bad;
+  int64_t batch;
+  int64_t segments;
+  int64_t n_query;
+  int64_t routes;
+  int64_t n_index;  // n_query * routes
+  int dv;
+  int dk;
+  int v_tiles;
+};
+
+// ---------------------------------------------------------------------------
+// Pairs of one sequence sorted by segment.  Rows with an invalid index are
+// zeroed here and never enter a bucket.
+template <class EM>
+__global__ __launch_bounds__(BK_THREADS) void bucket_kernel(const RetrieveArgs a) {
+  using raw = typename ET<EM>::raw;
+  extern __shared__ int hist[];  // [segments]
+  __shared__ int wave_sum[BK_THREADS / 64];
+  __shared__ int total;
+  const int tid = threadIdx.x;
+  const int64_t b = blockIdx.x;
+  const int64_t S = a.segments, n = a.n_index;
+  const int64_t* ib = a.idx + b * n;
+  for (int64_t s = tid; s < S; s += BK_THREADS) hist[s] = 0;
+  __syncthreads();
+  for (int64_t i = tid; i < n; i += BK_THREADS) {
+    const int64_t s = ib[i];
+    if (s >= 0 && s < S) atomicAdd(&hist[s], 1);
+  }
+  __syncthreads();
+  // Exclusive scan of the histogram: thread t owns bins [t per, (t + 1) per).
+  const int per = static_cast<int>((S + BK_THREADS - 1) / BK_THREADS);
+  const int lo = min(static_cast<int64_t>(tid) * per, S);
+  const int hi = min(static_cast<int64_t>(lo) + per, S);
+  int local = 0;
+  for (int s = lo; s < hi; ++s) local += hist[s];
+  const int lane = tid & 63, wave = tid >> 6;
+  int incl = local;
+#pragma unroll
+  for (int d = 1; d < 64; d <<= 1) {
+    const int y = __shfl_up(incl, d, 64);
+    if (lane >= d) incl += y;
+  }
+  if (lane == 63) wave_sum[wave] = incl;
+  __syncthreads();
+  int base = 0;
+  for (int w = 0; w < wave; ++w) base += wave_sum[w];
+  if (tid == 0) {
+    int t = 0;
+    for (int w = 0; w < BK_THREADS / 64; ++w) t += wave_sum[w];
+    total = t;
+  }
+  int run = base + incl - local;
+  int32_t* off = a.offsets + b * (S + 1);
+  for (int s = lo; s < hi; ++s) {
+    const int c = hist[s];
+    off[s] = run;
+    hist[s] = run;
+    run += c;
+  }
+  __syncthreads();
+  if (tid == 0) off[S] = total;
+  int32_t* lb = a.list + b * n;
+  raw* ob = static_cast<raw*>(a.out) + b * n * a.dv;
+  for (int64_t i = tid; i < n; i += BK_THREADS) {
+    const int64_t s = ib[i];
+    if (s >= 0 && s < S) {
+      lb[atomicAdd(&hist[s], 1)] = static_cast<int32_t>(i);
+    } else {
+      for (int h = 0; h < a.dv; ++h) ob[i * a.dv + h] = ET<EM>::from_f(0.f);
+      if (a.bad != nullptr) atomicAdd(a.bad, 1);
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// One workgroup per (sequence, segment, 128-row value tile).  Wave w computes
+// value rows [32w, 32w + 32) for 64 pairs: D[v][p] = sum_k M[v][k] q'[p][k]
+// with A = state rows v, B = query rows p (lane (g, n) of a 16x16x4 operand
+// holds row n, key 4kk + g).
+template <class EM, class EQ, int DKP>
+__global__ __launch_bounds__(AP_THREADS) void apply_bucket_kernel(const RetrieveArgs a) {
+  using rawm = typename ET<EM>::raw;
+  using rawq = typename ET<EQ>::raw;
+  constexpr int MS = DKP + 4;                            // state tile row stride (floats)
+  constexpr int QS = (DKP > AP_V ? DKP : AP_V) + 4;      // query / output tile row stride
+  extern __shared__ __align__(16) float sm[];
+  float* Ms = sm;              // [AP_V][MS]
+  float* QO = Ms + AP_V * MS;  // [AP_N][QS]: queries, then the output tile
+  __shared__ int pair_id[AP_N];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63, g = lane >> 4, n = lane & 15;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int64_t vt = blockIdx.x % a.v_tiles;
+  const int64_t bs = blockIdx.x / a.v_tiles;
+  const int64_t b = bs / a.segments, s = bs % a.segments;
+  const int32_t* off = a.offsets + b * (a.segments + 1);
+  const int p_begin = off[s], p_end = off[s + 1];
+  if (p_begin == p_end) return;
+  const int dk = a.dk, dv = a.dv;
+  const int v0 = static_cast<int>(vt) * AP_V;
+
+  // State rows v0 .. v0 + 127 as fp32, zero past d_v and d_k.
+  const rawm* msrc = static_cast<const rawm*>(a.mem) + (b * a.segments + s) * dv * dk;
+  for (int e = tid; e < AP_V * DKP; e += AP_THREADS) {
+    const int v = e / DKP, k = e % DKP;
+    Ms[v * MS + k] = (v0 + v < dv && k < dk) ? ET<EM>::to_f(msrc[(v0 + v) * dk + k]) : 0.f;
+  }
+  const int32_t* lb = a.list + b * a.n_index;
+  const rawq* qsrc = static_cast<const rawq*>(a.queries) + b * a.n_query * dk;
+  rawm* obase = static_cast<rawm*>(a.out) + b * a.n_index * dv;
+
+  for (int p0 = p_begin; p0 < p_end; p0 += AP_N) {
+    const int np = min(AP_N, p_end - p0);
+    __syncthreads();  // state tile in place; previous output tile written out
+    if (tid < AP_N) pair_id[tid] = tid < np ? lb[p0 + tid] : -1;
+    __syncthreads();
+    for (int e = tid; e < AP_N * DKP; e += AP_THREADS) {
+      const int p = e / DKP, k = e % DKP;
+      const int pid = pair_id[p];
+      float x = 0.f;
+      if (pid >= 0 && k < dk) {
+        // the caller's cast of q to the memories' dtype
+        x = ET<EM>::to_f(ET<EM>::from_f(ET<EQ>::to_f(qsrc[(pid / a.routes) * dk + k])));
+      }
+      QO[p * QS + k] = x;
+    }
+    __syncthreads();
+    f32x4 acc[2][4];
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll 4
+    for (int kk = 0; kk < DKP / 4; ++kk) {
+      float av[2], bv[4];
+#pragma unroll
+      for (int i = 0; i < 2; ++i) av[i] = Ms[(32 * w + 16 * i + n) * MS + 4 * kk + g];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) bv[j] = QO[(16 * j + n) * QS + 4 * kk + g];
+#pragma unroll
+      for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(av[i], bv[j], acc[i][j], 0, 0, 0);
+    }
+    __syncthreads();  // query tile consumed
+    // lane (g, n) holds D[v = 32w + 16i + 4g + r][p = 16j + n]
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        *reinterpret_cast<f32x4*>(QO + (16 * j + n) * QS + 32 * w + 16 * i + 4 * g) = acc[i][j];
+    __syncthreads();
+    // whole output rows: pair p -> out[b, pair_id[p], v0 .. v0 + 127]
+    const int vcols = min(AP_V, dv - v0);
+    for (int e = tid; e < np * AP_V; e += AP_THREADS) {
+      const int p = e / AP_V, v = e % AP_V;
+      if (v < vcols) obase[static_cast<int64_t>(pair_id[p]) * dv + v0 + v] = ET<EM>::from_f(QO[p * QS + v]);
+    }
+  }
+}
+
+template <class EM, class EQ, int DKP>
+int launch_apply(const RetrieveArgs& a, hipStream_t s) {
+  constexpr int MS = DKP + 4;
+  constexpr int QS = (DKP > AP_V ? DKP : AP_V) + 4;
+  constexpr size_t lds = (static_cast<size_t>(AP_V) * MS + static_cast<size_t>(AP_N) * QS) * sizeof(float);
+  static_assert(lds <= 160 * 1024, "apply tiles fit one CU's LDS");
+  static bool attr_set = false;
+  if (!attr_set) {
+    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&apply_bucket_kernel<EM, EQ, DKP>),
+                                       hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds));
+    if (e != hipSuccess) {
+      set_error("gather_apply: hipFuncSetAttribute failed: %s", hipGetErrorString(e));
+      return static_cast<int>(e);
+    }
+    attr_set = true;
+  }
+  const int64_t grid = a.batch * a.segments * a.v_tiles;
+  hipLaunchKernelGGL((apply_bucket_kernel<EM, EQ, DKP>), dim3(static_cast<unsigned>(grid)), dim3(AP_THREADS), lds,
+                     s, a);
+  return check_launch("gather_apply");
+}
+
+template <class EM, class EQ>
+int dispatch_dk(const RetrieveArgs& a, hipStream_t s) {
+  if (a.dk <= 32) return launch_apply<EM, EQ, 32>(a, s);
+  if (a.dk <= 64) return launch_apply<EM, EQ, 64>(a, s);
+  return launch_apply<EM, EQ, 128>(a, s);
+}
+
+template <class EM>
+int dispatch_q(const RetrieveArgs& a, int q_dtype, hipStream_t s) {
+  switch (q_dtype) {
+    case GRM_HIP_F32: return dispatch_dk<EM, F32>(a, s);
+    case GRM_HIP_F16: return dispatch_dk<EM, F16>(a, s);
+    default: return dispatch_dk<EM, BF16>(a, s);
+  }
+}
+
+template <class EM>
+int launch_bucket(const RetrieveArgs& a, hipStream_t s) {
+  const size_t lds = static_cast<size_t>(a.segments) * sizeof(int);
+  static bool attr_set = false;
+  if (!attr_set) {
+    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&bucket_kernel<EM>),
+                                       hipFuncAttributeMaxDynamicSharedMemorySize,
+                                       static_cast<int>(kMaxSegments * sizeof(int)));
+    if (e != hipSuccess) {
+      set_error("gather_apply: hipFuncSetAttribute failed: %s", hipGetErrorString(e));
+      return static_cast<int>(e);
+    }
+    attr_set = true;
+  }
+  hipLaunchKernelGGL((bucket_kernel<EM>), dim3(static_cast<unsigned>(a.batch)), dim3(BK_THREADS), lds, s, a);
+  return check_launch("gather_apply(sort)");
+}
+
+int64_t offsets_bytes(int64_t batch, int64_t segments) { return (batch * (segments + 1) * 4 + 15) / 16 * 16; }
+
+}  // namespace
+}  // namespace grmhip
+
+using namespace grmhip;
+
+extern "C" int64_t grm_hip_gather_apply_workspace(int64_t batch, int64_t segments, int64_t n_index) {
+  if (batch <= 0 || segments < 0 || n_index <= 0) return 0;
+  return offsets_bytes(batch, segments) + batch * n_index * 4;
+}
+
+extern "C" int grm_hip_gather_apply(const void* memories, const int64_t* indices, const void* queries, void* out,
+                                    void* workspace, int64_t workspace_bytes, int64_t batch, int64_t segments,
+                                    int64_t n_query, int64_t routes, int64_t hidden_size, int64_t key_dim,
+                                    int mem_dtype, int q_dtype, int32_t* bad_index_count, void* stream) {
+  if (batch < 0 || segments < 0 || n_query < 0 || routes < 0 || hidden_size < 0 || key_dim < 1) {
+    set_error("gather_apply: negative size or key_dim < 1");
+    return GRM_HIP_EINVAL;
+  }
+  if (mem_dtype < GRM_HIP_F32 || mem_dtype > GRM_HIP_BF16 || q_dtype < GRM_HIP_F32 || q_dtype > GRM_HIP_BF16) {
+    set_error("gather_apply: unsupported dtypes mem=%d q=%d", mem_dtype, q_dtype);
+    return GRM_HIP_EUNSUPPORTED;
+  }
+  if (key_dim > 128 || segments > kMaxSegments) {
+    set_error("gather_apply: key_dim %lld > 128 or segments %lld > %lld", (long long)key_dim, (long long)segments,
+              (long long)kMaxSegments);
+    return GRM_HIP_EUNSUPPORTED;
+  }
+  const int64_t n_index = n_query * routes;
+  if (batch == 0 || n_index == 0 || hidden_size == 0) return GRM_HIP_OK;
+  if (n_index > INT32_MAX || hidden_size > INT32_MAX / 2 || batch * segments * ((hidden_size + AP_V - 1) / AP_V) > INT32_MAX) {
+    set_error("gather_apply: sizes exceed one launch");
+    return GRM_HIP_EINVAL;
+  }
+  if (indices == nullptr || queries == nullptr || out == nullptr || (segments > 0 && memories == nullptr)) {
+    set_error("gather_apply: null pointer");
+    return GRM_HIP_EINVAL;
+  }
+  const int64_t need = grm_hip_gather_apply_workspace(batch, segments, n_index);
+  if (workspace == nullptr || workspace_bytes < need || reinterpret_cast<uintptr_t>(workspace) % 16 != 0) {
+    set_error("gather_apply: workspace of %lld bytes (16-byte aligned) required", (long long)need);
+    return GRM_HIP_EINVAL;
+  }
+  RetrieveArgs a;
+  memset(&a, 0, sizeof(a));
+  a.mem = memories;
+  a.idx = indices;
+  a.queries = queries;
+  a.out = out;
+  a.offsets = static_cast<int32_t*>(workspace);
+  a.list = reinterpret_cast<int32_t*>(static_cast<unsigned char*>(workspace) + offsets_bytes(batch, segments));
+  a.bad = bad_index_count;
+  a.batch = batch;
+  a.segments = segments;
+  a.n_query = n_query;
+  a.routes = routes;
+  a.n_index = n_index;
+  a.dv = static_cast<int>(hidden_size);
+  a.dk = static_cast<int>(key_dim);
+  a.v_tiles = static_cast<int>((hidden_size + AP_V - 1) / AP_V);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  int rc;
+  switch (mem_dtype) {
+    case GRM_HIP_F32: rc = launch_bucket<F32>(a, s); break;
+    case GRM_HIP_F16: rc = launch_bucket<F16>(a, s); break;
+    default: rc = launch_bucket<BF16>(a, s); break;
+  }
+  if (rc != GRM_HIP_OK || segments == 0) return rc;
+  switch (mem_dtype) {
+    case GRM_HIP_F32: return dispatch_q<F32>(a, q_dtype, s);
+    case GRM_HIP_F16: return dispatch_q<F16>(a, q_dtype, s);
+    default: return dispatch_q<BF16>(a, q_dtype, s);
+  }
+}

@@ -34,7 +34,7 @@ _REGISTERED_OPS = (
     "apply_query_backward",
     "batched_memory_gather",
 )
-_EXTRA_OPS = ("segment_scan_forward", "topk_route", "fuse_residual")
+_EXTRA_OPS = ("segment_scan_forward", "topk_route", "fuse_residual", "gather_apply")
 
 _EXTENSION_MODULE: Optional[Any] = None
 _EXTENSION_LOAD_ATTEMPTED = False
@@ -385,12 +385,27 @@ def cuda_fuse_residual(h_online: Tensor, retrieved: Tensor, gates: Tensor, weigh
     return x
 
 
+def cuda_gather_apply(memories_per_batch: Tensor, topk_indices: Tensor, queries: Tensor, *, enabled: bool = True,
+                      debug_fallback: bool = False) -> Tensor:
+    """apply_query(batched_memory_gather(M, idx), q.to(M.dtype)) without materialising the
+    gathered states (cuda_ops.py:370-402, composed as in paper_grm.py:229,301-313).
+    The fused op has no backward: when autograd needs gradients the composition runs."""
+    needs_grad = torch.is_grad_enabled() and (memories_per_batch.requires_grad or queries.requires_grad)
+    if not needs_grad and _use_native("gather_apply", memories_per_batch.device, enabled=enabled,
+                                      debug_fallback=debug_fallback):
+        return torch.ops.grm_cuda.gather_apply(memories_per_batch, topk_indices, queries)
+    gathered = cuda_batched_memory_gather(memories_per_batch, topk_indices, enabled=enabled,
+                                          debug_fallback=debug_fallback)
+    return cuda_apply_query(gathered, queries.to(gathered.dtype), enabled=enabled, debug_fallback=debug_fallback)
+
+
 __all__ = [
     "GrmExtensionUnavailable",
     "cuda_apply_query",
     "cuda_batched_memory_gather",
     "cuda_chunk_update",
     "cuda_fuse_residual",
+    "cuda_gather_apply",
     "cuda_segment_scan",
     "cuda_topk_route",
     "get_grm_cuda_runtime_status",

@@ -173,6 +173,22 @@ def test_cpu_fuse_residual():
     np.testing.assert_allclose(out.numpy(), ref, rtol=1e-5, atol=1e-5)
 
 
+def test_cpu_gather_apply_is_the_composition():
+    """The generic gather_apply (CPU key) equals the oracle's gather then apply with the
+    queries cast to the memories' dtype; the CUDA-key kernel is checked against it on GPU."""
+    g = torch.Generator().manual_seed(3)
+    mem = torch.randn(2, 6, 10, 12, generator=g)
+    q = torch.randn(2, 4, 12, generator=g).to(torch.bfloat16)
+    idx = torch.randint(0, 6, (2, 4, 3), generator=g)
+    out = torch.ops.grm_cuda.gather_apply(mem, idx, q)
+    gathered, bad = orc.gather(mem.numpy(), idx.numpy())
+    ref = orc.apply_query(gathered, np64(q.float()))
+    assert bad == 0 and out.dtype == torch.float32 and out.shape == (2, 4, 3, 10)
+    np.testing.assert_allclose(out.numpy(), ref, rtol=1e-5, atol=1e-6)
+    with pytest.raises(RuntimeError, match="key dim mismatch"):
+        torch.ops.grm_cuda.gather_apply(mem, idx, q[..., :5])
+
+
 def test_shape_errors_raise_like_reference():
     k, v, q, m = make_chunk_case(4)
     with pytest.raises(RuntimeError, match="keys must have shape"):

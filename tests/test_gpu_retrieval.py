@@ -100,6 +100,93 @@ def test_gather_column_tiles_with_bad_indices(dev, B, S, N, D, dtype):
     assert torch.equal(out, ref)
 
 
+# ---------------------------------------------------------------- fused gather + apply
+def _cast_like(q, dtype):
+    return q.to(dtype).to(torch.float64)
+
+
+@pytest.mark.parametrize("mem_dtype,q_dtype", [(torch.float32, torch.bfloat16), (torch.float32, torch.float32),
+                                               (torch.bfloat16, torch.bfloat16), (torch.float16, torch.float32)])
+@pytest.mark.parametrize("B,S,Q,R,H,K", [(3, 7, 13, 3, 20, 8), (2, 40, 5, 50, 200, 64), (2, 256, 300, 8, 128, 128),
+                                         (1, 1, 4, 2, 8, 33)])
+def test_gather_apply_matches_composition(dev, mem_dtype, q_dtype, B, S, Q, R, H, K):
+    """gather_apply == apply_query(batched_gather(M, idx), q cast to M's dtype), the
+    reference's composition, against the oracle's gather and apply."""
+    g = torch.Generator().manual_seed(B * 100 + S)
+    mem = (torch.randn(B, S, H, K, generator=g) * 0.02).to(mem_dtype)
+    q = norm(torch.randn(B, Q, K, generator=g)).to(q_dtype)
+    idx = torch.randint(0, S, (B, Q, R), generator=g)
+    out = capi.gather_apply(mem.to(dev), idx.to(dev), q.to(dev))
+    gathered, bad = orc.gather(mem.float().numpy(), idx.numpy())
+    assert bad == 0
+    ref = orc.apply_query(gathered, _cast_like(q, mem_dtype).numpy())
+    assert out.dtype == mem_dtype and out.shape == (B, Q, R, H)
+    tol = (1e-5, 1e-6) if mem_dtype == torch.float32 else (2e-2, 2e-3)
+    np.testing.assert_allclose(out.float().cpu().double().numpy(), ref, rtol=tol[0], atol=tol[1])
+
+
+def test_gather_apply_bad_indices_and_rank2(dev):
+    """Out-of-range indices give zero rows and are counted; rank-2 indices ([B, R]
+    with queries [B, K]) go through the torch op like the reference's rank-4 apply."""
+    g = torch.Generator().manual_seed(11)
+    mem = torch.randn(2, 5, 16, 24, generator=g)
+    q = torch.randn(2, 6, 24, generator=g)
+    idx = torch.randint(0, 5, (2, 6, 3), generator=g)
+    idx[0, 1, 2] = 5
+    idx[1, 0, 0] = -3
+    bad = torch.zeros(1, dtype=torch.int32, device=dev)
+    out = capi.gather_apply(mem.to(dev), idx.to(dev), q.to(dev), bad_count=bad)
+    assert int(bad.item()) == 2
+    assert torch.count_nonzero(out[0, 1, 2]) == 0 and torch.count_nonzero(out[1, 0, 0]) == 0
+    ok = (idx >= 0) & (idx < 5)
+    ref = torch.einsum("bqrhk,bqk->bqrh", mem[torch.arange(2)[:, None, None], idx.clamp(0, 4)], q)
+    ref[~ok] = 0
+    torch.testing.assert_close(out.cpu(), ref, rtol=1e-5, atol=1e-6)
+    idx2 = torch.randint(0, 5, (2, 4), generator=g)
+    q2 = torch.randn(2, 24, generator=g)
+    out2 = torch.ops.grm_cuda.gather_apply(mem.to(dev), idx2.to(dev), q2.to(dev))
+    ref2 = torch.einsum("brhk,bk->brh", mem[torch.arange(2)[:, None], idx2], q2)
+    assert out2.shape == (2, 4, 16)
+    torch.testing.assert_close(out2.cpu(), ref2, rtol=1e-5, atol=1e-6)
+
+
+def test_gather_apply_config3_slice(dev):
+    """BASELINE config 3 geometry (128x128 fp32 states, S=256, k=8, bf16 queries) on 8 of
+    the 64 sequences with all 2048 queries, against the materialised composition on the GPU."""
+    B, S, Q, R, D = 8, 256, 2048, 8, 128
+    g = torch.Generator().manual_seed(12)
+    mem = (torch.randn(B, S, D, D, generator=g) * 0.02).to(dev)
+    q = norm(torch.randn(B, Q, D, generator=g)).to(torch.bfloat16).to(dev)
+    keys = norm(torch.randn(B, S, D, generator=g)).to(torch.bfloat16).to(dev)
+    gates, idx, _ = torch.ops.grm_cuda.topk_route(q, keys, R, 1.0 / D ** 0.5, 1.0)
+    fused = torch.ops.grm_cuda.gather_apply(mem, idx, q)
+    composed = torch.ops.grm_cuda.apply_query_forward(torch.ops.grm_cuda.batched_memory_gather(mem, idx),
+                                                      q.to(mem.dtype))
+    torch.testing.assert_close(fused, composed, rtol=1e-5, atol=1e-6)
+
+
+def test_gather_apply_autograd_falls_back(dev):
+    """With gradients required, cuda_gather_apply runs the differentiable composition:
+    the queries get their gradient through apply_query; like the reference's native
+    batched_memory_gather (cuda_ops.py:388-402, no autograd), the archive gets none."""
+    g = torch.Generator().manual_seed(13)
+    mem = torch.randn(2, 6, 8, 16, generator=g).to(dev).requires_grad_(True)
+    q = torch.randn(2, 5, 16, generator=g).to(dev).requires_grad_(True)
+    idx = torch.randint(0, 6, (2, 5, 3), generator=g).to(dev)
+    out = cuda_ops.cuda_gather_apply(mem, idx, q)
+    out.square().sum().backward()
+    assert mem.grad is None
+    q2 = q.detach().cpu().requires_grad_(True)
+    ref = torch.einsum("bqrhk,bqk->bqrh", mem.detach().cpu()[torch.arange(2)[:, None, None], idx.cpu()], q2)
+    ref.square().sum().backward()
+    torch.testing.assert_close(q.grad.cpu(), q2.grad, rtol=1e-4, atol=1e-5)
+    with torch.no_grad():
+        before = capi.launch_count()
+        fused = cuda_ops.cuda_gather_apply(mem, idx, q)
+        assert capi.launch_count() > before
+        torch.testing.assert_close(fused, out.detach(), rtol=1e-5, atol=1e-6)
+
+
 # ---------------------------------------------------------------- apply query
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16])
 @pytest.mark.parametrize("shape", [(2, 3, 4, 5, 6), (4, 7, 8, 128, 128), (3, 5, 2, 9, 33), (2, 4, 16, 64)])
