@@ -98,7 +98,8 @@ def bench_c2(torch, dev, steps, warmup):
 
 
 def bench_c3(torch, dev, steps, warmup):
-    """Routing over the archive summaries, then the materialised gather."""
+    """Routing over the archive summaries; the fused retrieval (gather_apply + fusion); the
+    materialised gather."""
     from rnn_with_grm_amd import capi
 
     lib = capi.load()
@@ -128,6 +129,43 @@ def bench_c3(torch, dev, steps, warmup):
         if rc != 0:
             raise RuntimeError(capi.last_error())
 
+    # The fused path: route -> gather_apply -> residual + LayerNorm, no materialised states.
+    retrieved = torch.empty((BH, Q, K, D), dtype=torch.float32, device=dev)
+    wsb = int(lib.grm_hip_gather_apply_workspace(BH, S, Q * K))
+    ws = torch.empty(wsb, dtype=torch.uint8, device=dev)
+    online = torch.randn(BH, D, D, device=dev) * 0.02
+    h_online = torch.bmm(q.float(), online.transpose(1, 2).contiguous()).reshape(BH * Q, D).contiguous()
+    ln_w = torch.ones(D, device=dev)
+    ln_b = torch.zeros(D, device=dev)
+    fused_out = torch.empty((BH * Q, D), dtype=torch.float32, device=dev)
+
+    def gather_apply():
+        rc = lib.grm_hip_gather_apply(P(states), P(idx), P(q), P(retrieved), P(ws), wsb, BH, S, Q, K, D, D, capi.F32,
+                                      capi.BF16, None, sp)
+        if rc != 0:
+            raise RuntimeError(capi.last_error())
+
+    def fuse():
+        rc = lib.grm_hip_fuse_residual(P(h_online), P(retrieved), P(gt), P(ln_w), P(ln_b), P(fused_out), BH * Q, K, D,
+                                       capi.F32, 1e-5, sp)
+        if rc != 0:
+            raise RuntimeError(capi.last_error())
+
+    def retrieval():
+        route()
+        gather_apply()
+        fuse()
+
+    ga_wall, ga_per = timed_launches(torch, gather_apply, max(3, steps), warmup, stream)
+    fu_wall, fu_per = timed_launches(torch, fuse, max(3, steps), warmup, stream)
+    rt_wall, rt_per = timed_launches(torch, retrieval, max(3, steps), warmup, stream)
+    # spot check of the fused path against the materialised composition for one query
+    b, qi = 7, 1500
+    sel = states[b, idx[b, qi]]                                    # [K, D, D]
+    r_ref = torch.einsum("rhk,k->rh", sel, q[b, qi].float())
+    assert torch.allclose(retrieved[b, qi], r_ref, rtol=1e-4, atol=1e-6), "gather_apply spot check failed"
+    del retrieved, ws, online, h_online, fused_out
+
     g_steps = max(3, min(steps, 10))
     g_wall, g_per = timed_launches(torch, gather, g_steps, min(warmup, 2), stream)
     # spot check: one (b, q, r) row against the archive
@@ -142,6 +180,11 @@ def bench_c3(torch, dev, steps, warmup):
     return {
         "route": {"ms": statistics.mean(r_per) * 1e3, "bytes": route_bytes,
                   "flops": 2 * BH * Q * S * D},
+        "gather_apply": {"ms": statistics.mean(ga_per) * 1e3,
+                         "bytes": BH * S * D * D * 4 + BH * Q * K * D * 4 + q.numel() * 2 + idx.numel() * 8,
+                         "flops": 2 * BH * Q * K * D * D},
+        "fuse": {"ms": statistics.mean(fu_per) * 1e3},
+        "retrieval": {"ms": statistics.mean(rt_per) * 1e3},
         "gather": {"ms": statistics.mean(g_per) * 1e3, "bytes": gather_bytes,
                    "fill_ms": statistics.mean(f_per) * 1e3, "fill_bytes": BH * Q * K * D * D * 4},
     }
@@ -241,6 +284,16 @@ def main() -> int:
                                                     "GB/s": round(gth["fill_bytes"] / gth["fill_ms"] / 1e6, 1),
                                                     "gather_time_vs_fill": round(gth["fill_ms"] / gth["ms"], 4)}}
         log(f"c3 gather: {gth['ms']:.2f} ms, {gbs:.0f} GB/s (fill of the output: {gth['fill_ms']:.2f} ms)")
+        ga, rt = c3["gather_apply"], c3["retrieval"]
+        secondary["c3_retrieval_fused"] = {
+            "what": "route -> gather_apply (no materialised states) -> residual + LayerNorm, per config-3 batch",
+            "ms": round(rt["ms"], 4), "route_ms": round(r["ms"], 4), "gather_apply_ms": round(ga["ms"], 4),
+            "fuse_ms": round(c3["fuse"]["ms"], 4),
+            "gather_apply_GB/s": round(ga["bytes"] / ga["ms"] / 1e6, 1),
+            "gather_apply_TFLOP/s_fp32": round(ga["flops"] / ga["ms"] / 1e9, 2),
+            "speedup_vs_materialised_gather_alone": round(gth["ms"] / rt["ms"], 2)}
+        log(f"c3 fused retrieval: {rt['ms']:.3f} ms (route {r['ms']:.3f}, gather_apply {ga['ms']:.3f}, "
+            f"fuse {c3['fuse']['ms']:.3f})")
 
     cpu = None
     if not a.no_cpu:

@@ -19,6 +19,8 @@
 #include <stdint.h>
 #include <string.h>
 
+#include <type_traits>
+
 #include "grm_hip.h"
 #include "grm_hip_common.h"
 
@@ -116,17 +118,41 @@ __global__ __launch_bounds__(BK_THREADS) void bucket_kernel(const RetrieveArgs a
   }
 }
 
+// Sixteen bytes of a row-major tile as fp32 values (8 elements for 16-bit types,
+// 4 for float32); an OOB offset reads zeros.
+template <class E>
+__device__ __forceinline__ void load16_f32(__amdgpu_buffer_rsrc_t r, int off, float* dst) {
+  const u32x4 u = __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0);
+  if constexpr (sizeof(typename ET<E>::raw) == 2) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      dst[2 * i] = ET<E>::to_f(static_cast<typename ET<E>::raw>(u[i] & 0xffffu));
+      dst[2 * i + 1] = ET<E>::to_f(static_cast<typename ET<E>::raw>(u[i] >> 16));
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) dst[i] = __uint_as_float(u[i]);
+  }
+}
+
 // ---------------------------------------------------------------------------
 // One workgroup per (sequence, segment, 128-row value tile).  Wave w computes
 // value rows [32w, 32w + 32) for 64 pairs: D[v][p] = sum_k M[v][k] q'[p][k]
 // with A = state rows v, B = query rows p (lane (g, n) of a 16x16x4 operand
 // holds row n, key 4kk + g).
-template <class EM, class EQ, int DKP>
+template <class EM, class EQ, int DKP, bool VEC>
 __global__ __launch_bounds__(AP_THREADS) void apply_bucket_kernel(const RetrieveArgs a) {
   using rawm = typename ET<EM>::raw;
   using rawq = typename ET<EQ>::raw;
   constexpr int MS = DKP + 4;                            // state tile row stride (floats)
   constexpr int QS = (DKP > AP_V ? DKP : AP_V) + 4;      // query / output tile row stride
+  constexpr int EPU_M = 16 / sizeof(rawm);               // elements per 16-byte unit
+  constexpr int EPU_Q = 16 / sizeof(rawq);
+  constexpr int UPR_M = DKP / EPU_M;                     // units per padded row
+  constexpr int UPR_Q = DKP / EPU_Q;
+  constexpr int M_UNITS = AP_V * UPR_M / AP_THREADS;     // per thread
+  constexpr int Q_UNITS = (AP_N * UPR_Q + AP_THREADS - 1) / AP_THREADS;
+  static_assert(M_UNITS * AP_THREADS == AP_V * UPR_M, "state tile splits evenly");
   extern __shared__ __align__(16) float sm[];
   float* Ms = sm;              // [AP_V][MS]
   float* QO = Ms + AP_V * MS;  // [AP_N][QS]: queries, then the output tile
@@ -146,12 +172,33 @@ __global__ __launch_bounds__(AP_THREADS) void apply_bucket_kernel(const Retrieve
 
   // State rows v0 .. v0 + 127 as fp32, zero past d_v and d_k.
   const rawm* msrc = static_cast<const rawm*>(a.mem) + (b * a.segments + s) * dv * dk;
-  for (int e = tid; e < AP_V * DKP; e += AP_THREADS) {
-    const int v = e / DKP, k = e % DKP;
-    Ms[v * MS + k] = (v0 + v < dv && k < dk) ? ET<EM>::to_f(msrc[(v0 + v) * dk + k]) : 0.f;
+  if constexpr (VEC) {
+    const __amdgpu_buffer_rsrc_t rm = make_rsrc(msrc, static_cast<uint32_t>(dv * dk * sizeof(rawm)));
+    float x[M_UNITS][EPU_M];
+#pragma unroll
+    for (int u = 0; u < M_UNITS; ++u) {
+      const int e = tid + AP_THREADS * u;
+      const int v = e / UPR_M, c = (e % UPR_M) * EPU_M;
+      load16_f32<EM>(rm, (v0 + v < dv && c < dk) ? ((v0 + v) * dk + c) * static_cast<int>(sizeof(rawm)) : kBufOOB,
+                     x[u]);
+    }
+#pragma unroll
+    for (int u = 0; u < M_UNITS; ++u) {
+      const int e = tid + AP_THREADS * u;
+      const int v = e / UPR_M, c = (e % UPR_M) * EPU_M;
+#pragma unroll
+      for (int i = 0; i < EPU_M; i += 4)
+        *reinterpret_cast<f32x4*>(Ms + v * MS + c + i) = f32x4{x[u][i], x[u][i + 1], x[u][i + 2], x[u][i + 3]};
+    }
+  } else {
+    for (int e = tid; e < AP_V * DKP; e += AP_THREADS) {
+      const int v = e / DKP, k = e % DKP;
+      Ms[v * MS + k] = (v0 + v < dv && k < dk) ? ET<EM>::to_f(msrc[(v0 + v) * dk + k]) : 0.f;
+    }
   }
   const int32_t* lb = a.list + b * a.n_index;
   const rawq* qsrc = static_cast<const rawq*>(a.queries) + b * a.n_query * dk;
+  const __amdgpu_buffer_rsrc_t rq = make_rsrc(qsrc, static_cast<uint32_t>(a.n_query * dk * sizeof(rawq)));
   rawm* obase = static_cast<rawm*>(a.out) + b * a.n_index * dv;
 
   for (int p0 = p_begin; p0 < p_end; p0 += AP_N) {
@@ -159,15 +206,41 @@ __global__ __launch_bounds__(AP_THREADS) void apply_bucket_kernel(const Retrieve
     __syncthreads();  // state tile in place; previous output tile written out
     if (tid < AP_N) pair_id[tid] = tid < np ? lb[p0 + tid] : -1;
     __syncthreads();
-    for (int e = tid; e < AP_N * DKP; e += AP_THREADS) {
-      const int p = e / DKP, k = e % DKP;
-      const int pid = pair_id[p];
-      float x = 0.f;
-      if (pid >= 0 && k < dk) {
-        // the caller's cast of q to the memories' dtype
-        x = ET<EM>::to_f(ET<EM>::from_f(ET<EQ>::to_f(qsrc[(pid / a.routes) * dk + k])));
+    // Query rows of the tile's pairs, cast to the memories' dtype (the caller's
+    // cast of q), as fp32.
+    if constexpr (VEC) {
+      float x[Q_UNITS][EPU_Q];
+#pragma unroll
+      for (int u = 0; u < Q_UNITS; ++u) {
+        const int e = tid + AP_THREADS * u;
+        const int p = min(e / UPR_Q, AP_N - 1), c = (e % UPR_Q) * EPU_Q;
+        const int pid = pair_id[p];
+        const int qoff = (e < AP_N * UPR_Q && pid >= 0 && c < dk)
+                             ? (static_cast<int>(pid / a.routes) * dk + c) * static_cast<int>(sizeof(rawq))
+                             : kBufOOB;
+        load16_f32<EQ>(rq, qoff, x[u]);
       }
-      QO[p * QS + k] = x;
+#pragma unroll
+      for (int u = 0; u < Q_UNITS; ++u) {
+        const int e = tid + AP_THREADS * u;
+        if (e >= AP_N * UPR_Q) continue;
+        const int p = e / UPR_Q, c = (e % UPR_Q) * EPU_Q;
+#pragma unroll
+        for (int i = 0; i < EPU_Q; i += 4) {
+          f32x4 y;
+#pragma unroll
+          for (int j = 0; j < 4; ++j) y[j] = ET<EM>::to_f(ET<EM>::from_f(x[u][i + j]));
+          *reinterpret_cast<f32x4*>(QO + p * QS + c + i) = y;
+        }
+      }
+    } else {
+      for (int e = tid; e < AP_N * DKP; e += AP_THREADS) {
+        const int p = e / DKP, k = e % DKP;
+        const int pid = pair_id[p];
+        float x = 0.f;
+        if (pid >= 0 && k < dk) x = ET<EM>::to_f(ET<EM>::from_f(ET<EQ>::to_f(qsrc[(pid / a.routes) * dk + k])));
+        QO[p * QS + k] = x;
+      }
     }
     __syncthreads();
     f32x4 acc[2][4];
@@ -204,7 +277,248 @@ __global__ __launch_bounds__(AP_THREADS) void apply_bucket_kernel(const Retrieve
   }
 }
 
+// Register-operand variant (16-byte aligned rows): no input tiles in LDS.  The
+// key order of every 4-deep fp32 MFMA step is permuted so that lane group g
+// owns keys [g*KG, (g+1)*KG), KG = DKP / 4: step t uses key g*KG + t in group g.
+// A lane then holds 32 (for d_k = 128) consecutive keys of its state row and of
+// its pair's query row, both loaded with 16-byte vector loads straight into the
+// operand registers.  Only the output tile goes through LDS (for whole-row
+// stores), so two or three workgroups share a CU and hide each other's latency.
 template <class EM, class EQ, int DKP>
+__global__ __launch_bounds__(AP_THREADS) void apply_reg_kernel(const RetrieveArgs a) {
+  using rawm = typename ET<EM>::raw;
+  using rawq = typename ET<EQ>::raw;
+  constexpr int KG = DKP / 4;                       // keys per lane group
+  constexpr int OS = AP_V + 4;                      // output tile row stride (floats)
+  constexpr int EPU_M = 16 / sizeof(rawm);
+  constexpr int EPU_Q = 16 / sizeof(rawq);
+  static_assert(KG % EPU_M == 0 && KG % EPU_Q == 0, "a lane's keys are whole 16-byte units");
+  __shared__ __align__(16) float Os[AP_N * OS];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63, g = lane >> 4, n = lane & 15;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int64_t vt = blockIdx.x % a.v_tiles;
+  const int64_t bs = blockIdx.x / a.v_tiles;
+  const int64_t b = bs / a.segments, s = bs % a.segments;
+  const int32_t* off = a.offsets + b * (a.segments + 1);
+  const int p_begin = off[s], p_end = off[s + 1];
+  if (p_begin == p_end) return;
+  const int dk = a.dk, dv = a.dv;
+  const int v0 = static_cast<int>(vt) * AP_V;
+  const int k0 = g * KG;
+
+  // A operands: state rows v = v0 + 32w + 16i + n, keys k0 .. k0 + KG - 1.
+  const rawm* msrc = static_cast<const rawm*>(a.mem) + (b * a.segments + s) * dv * dk;
+  const __amdgpu_buffer_rsrc_t rm = make_rsrc(msrc, static_cast<uint32_t>(dv * dk * sizeof(rawm)));
+  float am[2][KG];
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    const int v = v0 + 32 * w + 16 * i + n;
+#pragma unroll
+    for (int u = 0; u < KG / EPU_M; ++u) {
+      const int k = k0 + u * EPU_M;
+      load16_f32<EM>(rm, (v < dv && k < dk) ? (v * dk + k) * static_cast<int>(sizeof(rawm)) : kBufOOB,
+                     &am[i][u * EPU_M]);
+    }
+  }
+  const int32_t* lb = a.list + b * a.n_index;
+  const rawq* qsrc = static_cast<const rawq*>(a.queries) + b * a.n_query * dk;
+  const __amdgpu_buffer_rsrc_t rq = make_rsrc(qsrc, static_cast<uint32_t>(a.n_query * dk * sizeof(rawq)));
+  rawm* obase = static_cast<rawm*>(a.out) + b * a.n_index * dv;
+  const int vcols = min(AP_V, dv - v0);
+
+  for (int p0 = p_begin; p0 < p_end; p0 += AP_N) {
+    const int np = min(AP_N, p_end - p0);
+    f32x4 acc[2][4];
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      // B operand: the query of pair 16j + n, keys k0 .. k0 + KG - 1, cast to
+      // the memories' dtype (the caller's cast of q).
+      const int p = 16 * j + n;
+      const int pid = p < np ? lb[p0 + p] : -1;
+      float bq[KG];
+#pragma unroll
+      for (int u = 0; u < KG / EPU_Q; ++u) {
+        const int k = k0 + u * EPU_Q;
+        load16_f32<EQ>(rq, (pid >= 0 && k < dk) ? (static_cast<int>(pid / a.routes) * dk + k) *
+                                                      static_cast<int>(sizeof(rawq))
+                                                : kBufOOB,
+                       &bq[u * EPU_Q]);
+      }
+#pragma unroll
+      for (int t = 0; t < KG; ++t) bq[t] = ET<EM>::to_f(ET<EM>::from_f(bq[t]));
+#pragma unroll
+      for (int t = 0; t < KG; ++t) {
+#pragma unroll
+        for (int i = 0; i < 2; ++i) acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(am[i][t], bq[t], acc[i][j], 0, 0, 0);
+      }
+    }
+    __syncthreads();  // previous output tile written out
+    // lane (g, n) holds D[v = 32w + 16i + 4g + r][p = 16j + n]
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        *reinterpret_cast<f32x4*>(Os + (16 * j + n) * OS + 32 * w + 16 * i + 4 * g) = acc[i][j];
+    __syncthreads();
+    // whole output rows, four values per thread: pair p -> out[b, pair, v0 .. v0 + 127]
+    for (int e = tid; e < np * (AP_V / 4); e += AP_THREADS) {
+      const int p = e / (AP_V / 4), v = (e % (AP_V / 4)) * 4;
+      const int pid = lb[p0 + p];
+      const f32x4 val = *reinterpret_cast<const f32x4*>(Os + p * OS + v);
+      rawm* dst = obase + static_cast<int64_t>(pid) * dv + v0 + v;
+      if (v + 4 <= vcols) {
+        store4_raw<EM>(dst, val);
+      } else {
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+          if (v + r < vcols) dst[r] = ET<EM>::from_f(val[r]);
+      }
+    }
+  }
+}
+
+// 16-bit MFMA variant, exact: the memories are split into NPART parts of the
+// MFMA input type EF (one part when EM is EF; hi + mid + lo bf16 parts, which
+// together hold all 24 mantissa bits, when EM is float32), and the query cast
+// to EM is exact in EF, so every product is exact and only the float32
+// accumulation rounds, as in a float32 dot product.  Lane group g owns keys
+// [g*KG, (g+1)*KG); MFMA step c (16x16x32) takes keys g*KG + 8c .. + 7 from group g.
+template <class EM, class EQ, int DKP, class EF, int NPART>
+__global__ __launch_bounds__(AP_THREADS) void apply_mfma16_kernel(const RetrieveArgs a) {
+  using rawm = typename ET<EM>::raw;
+  using rawq = typename ET<EQ>::raw;
+  constexpr int KG = DKP / 4;
+  constexpr int NSTEP = KG / 8;
+  constexpr int OS = AP_V + 4;
+  constexpr int EPU_M = 16 / sizeof(rawm);
+  constexpr int EPU_Q = 16 / sizeof(rawq);
+  static_assert(KG % 8 == 0 && KG % EPU_M == 0 && KG % EPU_Q == 0, "a lane's keys are whole MFMA slots");
+  __shared__ __align__(16) float Os[AP_N * OS];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63, g = lane >> 4, n = lane & 15;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int64_t vt = blockIdx.x % a.v_tiles;
+  const int64_t bs = blockIdx.x / a.v_tiles;
+  const int64_t b = bs / a.segments, s = bs % a.segments;
+  const int32_t* off = a.offsets + b * (a.segments + 1);
+  const int p_begin = off[s], p_end = off[s + 1];
+  if (p_begin == p_end) return;
+  const int dk = a.dk, dv = a.dv;
+  const int v0 = static_cast<int>(vt) * AP_V;
+  const int k0 = g * KG;
+
+  // A operands: state rows v = v0 + 32w + 16i + n, keys k0 .. k0 + KG - 1, in parts.
+  const rawm* msrc = static_cast<const rawm*>(a.mem) + (b * a.segments + s) * dv * dk;
+  const __amdgpu_buffer_rsrc_t rm = make_rsrc(msrc, static_cast<uint32_t>(dv * dk * sizeof(rawm)));
+  Frag8<EF> am[2][NPART][NSTEP];
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    const int v = v0 + 32 * w + 16 * i + n;
+    float x[KG];
+#pragma unroll
+    for (int u = 0; u < KG / EPU_M; ++u) {
+      const int k = k0 + u * EPU_M;
+      load16_f32<EM>(rm, (v < dv && k < dk) ? (v * dk + k) * static_cast<int>(sizeof(rawm)) : kBufOOB,
+                     &x[u * EPU_M]);
+    }
+#pragma unroll
+    for (int c = 0; c < NSTEP; ++c) {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        float rest = x[8 * c + e];
+#pragma unroll
+        for (int part = 0; part < NPART; ++part) {
+          const typename ET<EF>::raw h = ET<EF>::from_f(rest);
+          am[i][part][c].e[e] = h;
+          rest -= ET<EF>::to_f(h);
+        }
+      }
+    }
+  }
+  const int32_t* lb = a.list + b * a.n_index;
+  const rawq* qsrc = static_cast<const rawq*>(a.queries) + b * a.n_query * dk;
+  const __amdgpu_buffer_rsrc_t rq = make_rsrc(qsrc, static_cast<uint32_t>(a.n_query * dk * sizeof(rawq)));
+  rawm* obase = static_cast<rawm*>(a.out) + b * a.n_index * dv;
+  const int vcols = min(AP_V, dv - v0);
+
+  for (int p0 = p_begin; p0 < p_end; p0 += AP_N) {
+    const int np = min(AP_N, p_end - p0);
+    f32x4 acc[2][4];
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int p = 16 * j + n;
+      const int pid = p < np ? lb[p0 + p] : -1;
+      float x[KG];
+#pragma unroll
+      for (int u = 0; u < KG / EPU_Q; ++u) {
+        const int k = k0 + u * EPU_Q;
+        load16_f32<EQ>(rq, (pid >= 0 && k < dk) ? (static_cast<int>(pid / a.routes) * dk + k) *
+                                                      static_cast<int>(sizeof(rawq))
+                                                : kBufOOB,
+                       &x[u * EPU_Q]);
+      }
+      Frag8<EF> bq[NSTEP];
+#pragma unroll
+      for (int c = 0; c < NSTEP; ++c)
+#pragma unroll
+        for (int e = 0; e < 8; ++e) bq[c].e[e] = ET<EF>::from_f(ET<EM>::to_f(ET<EM>::from_f(x[8 * c + e])));
+#pragma unroll
+      for (int c = 0; c < NSTEP; ++c)
+#pragma unroll
+        for (int part = 0; part < NPART; ++part)
+#pragma unroll
+          for (int i = 0; i < 2; ++i) acc[i][j] = mfma8(am[i][part][c], bq[c], acc[i][j]);
+    }
+    __syncthreads();  // previous output tile written out
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        *reinterpret_cast<f32x4*>(Os + (16 * j + n) * OS + 32 * w + 16 * i + 4 * g) = acc[i][j];
+    __syncthreads();
+    for (int e = tid; e < np * (AP_V / 4); e += AP_THREADS) {
+      const int p = e / (AP_V / 4), v = (e % (AP_V / 4)) * 4;
+      const int pid = lb[p0 + p];
+      const f32x4 val = *reinterpret_cast<const f32x4*>(Os + p * OS + v);
+      rawm* dst = obase + static_cast<int64_t>(pid) * dv + v0 + v;
+      if (v + 4 <= vcols) {
+        store4_raw<EM>(dst, val);
+      } else {
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+          if (v + r < vcols) dst[r] = ET<EM>::from_f(val[r]);
+      }
+    }
+  }
+}
+
+template <class EM, class EQ, int DKP, class EF, int NPART>
+int launch_apply_mfma16(const RetrieveArgs& a, hipStream_t s) {
+  const int64_t grid = a.batch * a.segments * a.v_tiles;
+  hipLaunchKernelGGL((apply_mfma16_kernel<EM, EQ, DKP, EF, NPART>), dim3(static_cast<unsigned>(grid)),
+                     dim3(AP_THREADS), 0, s, a);
+  return check_launch("gather_apply");
+}
+
+template <class EM, class EQ, int DKP>
+int launch_apply_reg(const RetrieveArgs& a, hipStream_t s) {
+  const int64_t grid = a.batch * a.segments * a.v_tiles;
+  hipLaunchKernelGGL((apply_reg_kernel<EM, EQ, DKP>), dim3(static_cast<unsigned>(grid)), dim3(AP_THREADS), 0, s, a);
+  return check_launch("gather_apply");
+}
+
+template <class EM, class EQ, int DKP, bool VEC>
 int launch_apply(const RetrieveArgs& a, hipStream_t s) {
   constexpr int MS = DKP + 4;
   constexpr int QS = (DKP > AP_V ? DKP : AP_V) + 4;
@@ -212,7 +526,7 @@ int launch_apply(const RetrieveArgs& a, hipStream_t s) {
   static_assert(lds <= 160 * 1024, "apply tiles fit one CU's LDS");
   static bool attr_set = false;
   if (!attr_set) {
-    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&apply_bucket_kernel<EM, EQ, DKP>),
+    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&apply_bucket_kernel<EM, EQ, DKP, VEC>),
                                        hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds));
     if (e != hipSuccess) {
       set_error("gather_apply: hipFuncSetAttribute failed: %s", hipGetErrorString(e));
@@ -221,16 +535,42 @@ int launch_apply(const RetrieveArgs& a, hipStream_t s) {
     attr_set = true;
   }
   const int64_t grid = a.batch * a.segments * a.v_tiles;
-  hipLaunchKernelGGL((apply_bucket_kernel<EM, EQ, DKP>), dim3(static_cast<unsigned>(grid)), dim3(AP_THREADS), lds,
-                     s, a);
+  hipLaunchKernelGGL((apply_bucket_kernel<EM, EQ, DKP, VEC>), dim3(static_cast<unsigned>(grid)), dim3(AP_THREADS),
+                     lds, s, a);
   return check_launch("gather_apply");
+}
+
+// 16-byte tile loads need whole units per row and 16-byte aligned bases.
+template <class EM, class EQ>
+bool vec_ok(const RetrieveArgs& a) {
+  const int em = 16 / static_cast<int>(sizeof(typename ET<EM>::raw));
+  const int eq = 16 / static_cast<int>(sizeof(typename ET<EQ>::raw));
+  return a.dk % em == 0 && a.dk % eq == 0 && reinterpret_cast<uintptr_t>(a.mem) % 16 == 0 &&
+         reinterpret_cast<uintptr_t>(a.queries) % 16 == 0 &&
+         a.dv * static_cast<int64_t>(a.dk) * static_cast<int64_t>(sizeof(typename ET<EM>::raw)) < INT32_MAX &&
+         a.n_query * static_cast<int64_t>(a.dk) * static_cast<int64_t>(sizeof(typename ET<EQ>::raw)) < INT32_MAX;
 }
 
 template <class EM, class EQ>
 int dispatch_dk(const RetrieveArgs& a, hipStream_t s) {
-  if (a.dk <= 32) return launch_apply<EM, EQ, 32>(a, s);
-  if (a.dk <= 64) return launch_apply<EM, EQ, 64>(a, s);
-  return launch_apply<EM, EQ, 128>(a, s);
+  if (vec_ok<EM, EQ>(a)) {
+    // Exact 16-bit MFMA when the query in the memories' dtype is exact in the
+    // MFMA input type: bf16 / f16 memories, or float32 memories with bf16 queries.
+    if constexpr (!std::is_same<EM, F32>::value || std::is_same<EQ, BF16>::value) {
+      using EF = typename std::conditional<std::is_same<EM, F16>::value, F16, BF16>::type;
+      constexpr int NPART = std::is_same<EM, F32>::value ? 3 : 1;
+      if (a.dk <= 32) return launch_apply_mfma16<EM, EQ, 32, EF, NPART>(a, s);
+      if (a.dk <= 64) return launch_apply_mfma16<EM, EQ, 64, EF, NPART>(a, s);
+      return launch_apply_mfma16<EM, EQ, 128, EF, NPART>(a, s);
+    } else {
+      if (a.dk <= 32) return launch_apply_reg<EM, EQ, 32>(a, s);
+      if (a.dk <= 64) return launch_apply_reg<EM, EQ, 64>(a, s);
+      return launch_apply_reg<EM, EQ, 128>(a, s);
+    }
+  }
+  if (a.dk <= 32) return launch_apply<EM, EQ, 32, false>(a, s);
+  if (a.dk <= 64) return launch_apply<EM, EQ, 64, false>(a, s);
+  return launch_apply<EM, EQ, 128, false>(a, s);
 }
 
 template <class EM>
