@@ -211,6 +211,314 @@ int launch_route(const RouteArgs& a, int64_t batch, hipStream_t s) {
 }
 
 // ---------------------------------------------------------------------------
+// MFMA routing for bf16 inputs with k < n_keys.  Same result as route_kernel,
+// bit for bit: the MFMA only narrows the search.
+//
+// 1. Each wave owns 64 query rows.  bf16 MFMAs give approximate scores A for
+//    32 keys at a time; every lane keeps the KN = KMAX + 4 best approximate
+//    scores of its row in a sorted register list of packed words
+//    (order-preserving float bits, low `ib` bits replaced by the key index).
+// 2. With S the exact score (the fp32 FMA chain of route_kernel), any key in
+//    the exact top k has A' >= tau - W, where tau is the k-th best packed
+//    score and W bounds |A' - S| twice over plus the ties the final
+//    multiplication by `scale` can create:
+//      |A - S| <= 4 * max(dim, 64) * 2^-23 * |q| * max_s |key_s|
+//    (both are fp32 sums of the same exact bf16 products; each rounding or
+//    truncation costs at most 2^-23 of the running sum of magnitudes, and a
+//    flushed denormal product at most 2^-126 * (|q| + |key|) per term).
+// 3. When the KN-th kept entry is below tau - W, the kept entries at or
+//    above tau - W are a superset of the exact top k: only they get the exact
+//    FMA chain, and the exact top k is chosen among them (ties to the lower
+//    index).  Otherwise (near-ties over more than four places, or inputs
+//    that are not finite) the lane scans every key exactly.
+constexpr int RM_THREADS = 256;  // four independent waves
+constexpr int RM_KT = 32;        // keys per tile
+constexpr int RM_ROW = RM_KT + 4;
+
+__device__ __forceinline__ uint32_t order_bits(float f) {
+  const uint32_t u = __float_as_uint(f);
+  return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+}
+
+__device__ __forceinline__ float unorder_bits(uint32_t u) {
+  return __uint_as_float((u & 0x80000000u) ? (u ^ 0x80000000u) : ~u);
+}
+
+// Exact score of one key: the fp32 FMA chain over d in increasing order, times scale.
+template <int DKP>
+__device__ __forceinline__ float exact_score(const uint4 (&qv)[DKP / 8], __amdgpu_buffer_rsrc_t rk,
+                                             int key, int dim, float scale) {
+  float acc = 0.f;
+#pragma unroll
+  for (int u = 0; u < DKP / 8; ++u) {
+    if (8 * u < dim) {
+      const U8<BF16> kv = buf_load8<BF16>(rk, (key * dim + 8 * u) * 2);
+      const U8<BF16> qq = __builtin_bit_cast(U8<BF16>, qv[u]);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) acc = fmaf(ET<BF16>::to_f(qq.e[e]), ET<BF16>::to_f(kv.e[e]), acc);
+    }
+  }
+  return acc * scale;
+}
+
+template <int KMAX>
+__device__ __forceinline__ void exact_insert(float (&ts)[KMAX], int (&ti)[KMAX], float cs, int ci) {
+#pragma unroll
+  for (int m = 0; m < KMAX; ++m) {
+    const bool better = cs > ts[m] || (cs == ts[m] && ci < ti[m]);
+    const float s0 = better ? cs : ts[m];
+    const int i0 = better ? ci : ti[m];
+    cs = better ? ts[m] : cs;
+    ci = better ? ti[m] : ci;
+    ts[m] = s0;
+    ti[m] = i0;
+  }
+}
+
+template <int DKP, int KMAX>
+__global__ __launch_bounds__(RM_THREADS) void route_mfma_kernel(const RouteArgs a, const int ib) {
+  constexpr int NC = DKP / 32;  // 32-element MFMA steps over d
+  constexpr int KN = KMAX + 4;
+  __shared__ __align__(16) uint32_t sc[4][64 * RM_ROW];
+  __shared__ float red[4];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63, g = lane >> 4, n = lane & 15;
+  const int w = tid >> 6;
+  const int64_t b = blockIdx.y;
+  const int D = a.dim;
+  const int S = static_cast<int>(a.n_keys);
+  const int k = a.k;
+  const uint16_t* kb = static_cast<const uint16_t*>(a.keys) + b * a.n_keys * D;
+  const __amdgpu_buffer_rsrc_t rk = make_rsrc(kb, static_cast<uint32_t>(a.n_keys * D * 2));
+
+  // Largest key norm of this batch entry (NaN if any key is not finite).
+  float kn2 = 0.f;
+  for (int s = tid; s < S; s += RM_THREADS) {
+    float t = 0.f;
+#pragma unroll
+    for (int u = 0; u < DKP / 8; ++u) {
+      if (8 * u < D) {
+        const U8<BF16> kv = buf_load8<BF16>(rk, (s * D + 8 * u) * 2);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const float x = ET<BF16>::to_f(kv.e[e]);
+          t = fmaf(x, x, t);
+        }
+      }
+    }
+    kn2 = (t <= INFINITY) ? fmaxf(kn2, t) : NAN;  // false for NaN
+  }
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) {
+    const float o = __shfl_xor(kn2, off, 64);
+    kn2 = (o <= INFINITY && kn2 <= INFINITY) ? fmaxf(kn2, o) : NAN;
+  }
+  if (lane == 0) red[w] = kn2;
+  __syncthreads();
+  float kmax2 = red[0];
+#pragma unroll
+  for (int i = 1; i < 4; ++i) kmax2 = (red[i] <= INFINITY && kmax2 <= INFINITY) ? fmaxf(kmax2, red[i]) : NAN;
+
+  const int64_t qw = static_cast<int64_t>(blockIdx.x) * RM_THREADS + 64 * w;  // first row of this wave
+  if (qw >= a.n_query) return;
+  const int64_t qi = qw + lane;
+  const bool active = qi < a.n_query;
+  const uint16_t* qb = static_cast<const uint16_t*>(a.q) + b * a.n_query * D;
+  const __amdgpu_buffer_rsrc_t rq = make_rsrc(qb, static_cast<uint32_t>(a.n_query * D * 2));
+
+  // B operands: rows qw + 16 qt + n, d = 32 c + 8 g .. + 7.
+  Frag8<BF16> bq[4][NC];
+  float qp[4];
+#pragma unroll
+  for (int qt = 0; qt < 4; ++qt) {
+    const int64_t row = qw + 16 * qt + n;
+    qp[qt] = 0.f;
+#pragma unroll
+    for (int c = 0; c < NC; ++c) {
+      const int d = 32 * c + 8 * g;
+      const U8<BF16> v = buf_load8<BF16>(rq, (row < a.n_query && d < D) ? static_cast<int>((row * D + d) * 2) : kBufOOB);
+      bq[qt][c] = __builtin_bit_cast(Frag8<BF16>, v);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const float x = ET<BF16>::to_f(v.e[e]);
+        qp[qt] = fmaf(x, x, qp[qt]);
+      }
+    }
+    qp[qt] += __shfl_xor(qp[qt], 16, 64);
+    qp[qt] += __shfl_xor(qp[qt], 32, 64);
+  }
+  // Lane 16 g + n owns row qw + 16 g + n, whose norm sits in qp[g].
+  const float qn2 = g == 0 ? qp[0] : g == 1 ? qp[1] : g == 2 ? qp[2] : qp[3];
+
+  const uint32_t imask = (1u << ib) - 1u;
+  uint32_t net[KN];
+#pragma unroll
+  for (int i = 0; i < KN; ++i) net[i] = 0u;
+  uint32_t* srow = &sc[w][0];
+
+  Frag8<BF16> ak[2][NC];
+  auto load_keys = [&](int s0) {
+#pragma unroll
+    for (int kt = 0; kt < 2; ++kt) {
+      const int row = s0 + 16 * kt + n;
+#pragma unroll
+      for (int c = 0; c < NC; ++c) {
+        const int d = 32 * c + 8 * g;
+        ak[kt][c] = __builtin_bit_cast(Frag8<BF16>, buf_load8<BF16>(rk, (row < S && d < D) ? (row * D + d) * 2 : kBufOOB));
+      }
+    }
+  };
+  load_keys(0);
+  for (int s0 = 0; s0 < S; s0 += RM_KT) {
+    f32x4 acc[4][2];
+#pragma unroll
+    for (int qt = 0; qt < 4; ++qt)
+#pragma unroll
+      for (int kt = 0; kt < 2; ++kt) {
+        acc[qt][kt] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int c = 0; c < NC; ++c) acc[qt][kt] = mfma8(ak[kt][c], bq[qt][c], acc[qt][kt]);
+      }
+    if (s0 + RM_KT < S) load_keys(s0 + RM_KT);
+    // acc[qt][kt][r] = A(key s0 + 16 kt + 4 g + r, row 16 qt + n)
+#pragma unroll
+    for (int qt = 0; qt < 4; ++qt)
+#pragma unroll
+      for (int kt = 0; kt < 2; ++kt) {
+        uint4 pk;
+        uint32_t* pe = reinterpret_cast<uint32_t*>(&pk);
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int key = s0 + 16 * kt + 4 * g + r;
+          pe[r] = key < S ? ((order_bits(acc[qt][kt][r]) & ~imask) | static_cast<uint32_t>(key)) : 0u;
+        }
+        *reinterpret_cast<uint4*>(srow + (16 * qt + n) * RM_ROW + 16 * kt + 4 * g) = pk;
+      }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    const uint32_t thr = net[KN - 1];
+    uint32_t m = 0u;
+#pragma unroll
+    for (int j4 = 0; j4 < RM_KT / 4; ++j4) {
+      const uint4 v = *reinterpret_cast<const uint4*>(srow + lane * RM_ROW + 4 * j4);
+      m |= (v.x > thr ? 1u : 0u) << (4 * j4);
+      m |= (v.y > thr ? 1u : 0u) << (4 * j4 + 1);
+      m |= (v.z > thr ? 1u : 0u) << (4 * j4 + 2);
+      m |= (v.w > thr ? 1u : 0u) << (4 * j4 + 3);
+    }
+    if (!active) m = 0u;
+    while (m != 0u) {
+      const int j = __builtin_ctz(m);
+      m &= m - 1u;
+      uint32_t p = srow[lane * RM_ROW + j];
+#pragma unroll
+      for (int i = 0; i < KN; ++i) {
+        const uint32_t hi = max(net[i], p);
+        p = min(net[i], p);
+        net[i] = hi;
+      }
+    }
+    // The next tile's writes must not pass this tile's reads.
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  }
+  if (!active) return;
+
+  // This row, packed, for the exact chains.
+  uint4 qv[DKP / 8];
+#pragma unroll
+  for (int u = 0; u < DKP / 8; ++u)
+    qv[u] = __builtin_bit_cast(uint4, buf_load8<BF16>(rq, 8 * u < D ? static_cast<int>((qi * D + 8 * u) * 2) : kBufOOB));
+
+  float top_s[KMAX];
+  int top_i[KMAX];
+#pragma unroll
+  for (int m = 0; m < KMAX; ++m) {
+    top_s[m] = -INFINITY;
+    top_i[m] = INT32_MAX;
+  }
+  uint32_t tau_u = net[0];
+#pragma unroll
+  for (int i = 1; i < KN; ++i) tau_u = (i == k - 1) ? net[i] : tau_u;
+  const float tau = unorder_bits(tau_u & ~imask);
+  const float a0 = unorder_bits(net[0] & ~imask);
+  const float qn = sqrtf(qn2) * 1.001f, km = sqrtf(kmax2) * 1.001f;
+  const float e_mfma = 4.f * static_cast<float>(max(D, 64)) * 0x1p-23f * qn * km;
+  const float eta = __uint_as_float(static_cast<uint32_t>(127 + ib - 22) << 23);  // 2^(ib-22): packing
+  const float r_abs = fmaxf(fabsf(tau), fabsf(a0)) + 4.f * e_mfma;
+  const float w0 = 2.f * e_mfma + 4.f * eta * (r_abs + 2.f * e_mfma);
+  const float wide = w0 + 0x1p-21f * (fabsf(tau) + 2.f * w0) + 0x1p-148f / a.scale +
+                     4.f * static_cast<float>(D) * 0x1p-126f * (qn + km);
+  const float theta = tau - wide;
+  const bool sound = qn * km < 1e30f && wide <= 1e30f;  // false for NaN and inf
+  const bool complete = S <= KN || unorder_bits(net[KN - 1] & ~imask) < theta;
+  if (sound && complete) {
+#pragma unroll
+    for (int i = 0; i < KN; ++i) {
+      if (i < S && unorder_bits(net[i] & ~imask) >= theta) {
+        const int key = static_cast<int>(net[i] & imask);
+        exact_insert<KMAX>(top_s, top_i, exact_score<DKP>(qv, rk, key, D, a.scale), key);
+      }
+    }
+  } else {
+    for (int key = 0; key < S; ++key)
+      exact_insert<KMAX>(top_s, top_i, exact_score<DKP>(qv, rk, key, D, a.scale), key);
+  }
+
+  const int64_t obase = (b * a.n_query + qi) * k;
+  const float mx = top_s[0] * a.inv_temp;
+  float e[KMAX];
+  float sum = 0.f;
+#pragma unroll
+  for (int m = 0; m < KMAX; ++m) {
+    e[m] = (m < k) ? expf(top_s[m] * a.inv_temp - mx) : 0.f;
+    sum += e[m];
+  }
+#pragma unroll
+  for (int m = 0; m < KMAX; ++m) {
+    if (m < k) {
+      a.idx[obase + m] = top_i[m];
+      a.scores[obase + m] = top_s[m];
+      a.gates[obase + m] = e[m] / sum;
+    }
+  }
+}
+
+// Whether route_mfma_kernel covers these arguments; ib = index bits.
+bool mfma_route_ok(const RouteArgs& a, int dtype, const void* queries, const void* keys, int* ib) {
+  if (dtype != GRM_HIP_BF16 || a.natural || !(a.scale > 0.f) || a.dim > 128 || a.dim % 8 != 0 ||
+      a.n_keys > 2048 || a.k > 32 || (reinterpret_cast<uintptr_t>(queries) | reinterpret_cast<uintptr_t>(keys)) % 16 != 0 ||
+      a.n_query * a.dim * 2 > INT32_MAX || a.n_keys * a.dim * 2 > INT32_MAX)
+    return false;
+  int bits = 1;
+  while ((int64_t{1} << bits) < a.n_keys) ++bits;
+  *ib = bits;
+  return true;
+}
+
+template <int DKP>
+int launch_route_mfma_dk(const RouteArgs& a, int64_t batch, int ib, hipStream_t s) {
+  const dim3 grid(static_cast<unsigned>((a.n_query + RM_THREADS - 1) / RM_THREADS), static_cast<unsigned>(batch));
+  if (a.k <= 8) {
+    hipLaunchKernelGGL((route_mfma_kernel<DKP, 8>), grid, dim3(RM_THREADS), 0, s, a, ib);
+  } else if (a.k <= 16) {
+    hipLaunchKernelGGL((route_mfma_kernel<DKP, 16>), grid, dim3(RM_THREADS), 0, s, a, ib);
+  } else {
+    hipLaunchKernelGGL((route_mfma_kernel<DKP, 32>), grid, dim3(RM_THREADS), 0, s, a, ib);
+  }
+  return check_launch("topk_route");
+}
+
+int launch_route_mfma(const RouteArgs& a, int64_t batch, int ib, hipStream_t s) {
+  if (a.dim <= 32) return launch_route_mfma_dk<32>(a, batch, ib, s);
+  if (a.dim <= 64) return launch_route_mfma_dk<64>(a, batch, ib, s);
+  return launch_route_mfma_dk<128>(a, batch, ib, s);
+}
+
+// ---------------------------------------------------------------------------
 struct FuseArgs {
   const void* h;
   const void* ret;
@@ -341,6 +649,8 @@ extern "C" int grm_hip_topk_route(const void* queries, const void* keys, int64_t
   a.scale = scale;
   a.inv_temp = 1.0f / temperature;
   hipStream_t s = static_cast<hipStream_t>(stream);
+  int ib = 0;
+  if (mfma_route_ok(a, dtype, queries, keys, &ib)) return launch_route_mfma(a, batch, ib, s);
   switch (dtype) {
     case GRM_HIP_F32: return launch_route<F32>(a, batch, s);
     case GRM_HIP_F16: return launch_route<F16>(a, batch, s);

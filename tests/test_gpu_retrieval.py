@@ -279,6 +279,50 @@ def test_topk_route_config3_slice(dev):
     assert np.array_equal(sc.cpu().numpy(), osc)
 
 
+def _near_tie_route_inputs(B, Q, S, D, hot, copies, seed):
+    """Keys that are element permutations of a few hot base keys, and queries whose
+    elements are all equal: such scores are equal in exact arithmetic and differ only
+    by the rounding of the FMA chain, so the top k is decided at the last bit."""
+    g = torch.Generator().manual_seed(seed)
+    keys = norm(torch.randn(B, S, D, generator=g))
+    pos = torch.randperm(S, generator=g)[: hot * copies].view(hot, copies)
+    for h in range(hot):
+        base = norm(torch.ones(D) + 0.5 * torch.randn(D, generator=g))
+        for c in range(copies):
+            keys[:, pos[h, c]] = base[torch.randperm(D, generator=g)]
+    q = norm(torch.randn(B, Q, D, generator=g))
+    q[:, ::2] = 1.0 / D ** 0.5  # every other row: equal elements
+    return q.to(torch.bfloat16), keys.to(torch.bfloat16)
+
+
+@pytest.mark.parametrize("S,D,k,hot,copies", [(256, 128, 8, 3, 5), (256, 128, 3, 1, 4), (512, 128, 16, 4, 6),
+                                              (100, 64, 8, 2, 3), (40, 24, 32, 3, 9), (300, 96, 1, 1, 30)])
+def test_topk_route_near_ties(dev, S, D, k, hot, copies):
+    """Rows whose best scores agree to the last few bits: the MFMA narrowing must keep
+    every key the exact FMA chain ranks in the top k (and scan all keys when more than
+    a few places are tied), so indices and scores still match the oracle bit for bit."""
+    B, Q = 2, 70
+    q, keys = _near_tie_route_inputs(B, Q, S, D, hot, copies, seed=S + k)
+    scale = 1.0 / D ** 0.5
+    gates, idx, sc = capi.topk_route(q.to(dev), keys.to(dev), k, scale)
+    og, oi, osc = orc.topk_route(q.float().numpy(), keys.float().numpy(), k, scale)
+    assert np.array_equal(idx.cpu().numpy(), oi)
+    assert np.array_equal(sc.cpu().numpy(), osc)
+    np.testing.assert_allclose(gates.cpu().numpy(), og, rtol=1e-5, atol=1e-6)
+
+
+def test_topk_route_unit_scale_and_large_norms(dev):
+    """Unnormalised bf16 inputs (norms up to ~1e3) and scale 1: the error bound of the
+    narrowing scales with the norms, the indices stay exact."""
+    g = torch.Generator().manual_seed(21)
+    q = (torch.randn(3, 90, 128, generator=g) * torch.rand(3, 90, 1, generator=g) * 100).to(torch.bfloat16)
+    keys = (torch.randn(3, 333, 128, generator=g) * 10).to(torch.bfloat16)
+    gates, idx, sc = capi.topk_route(q.to(dev), keys.to(dev), 12, 1.0)
+    og, oi, osc = orc.topk_route(q.float().numpy(), keys.float().numpy(), 12, 1.0)
+    assert np.array_equal(idx.cpu().numpy(), oi)
+    assert np.array_equal(sc.cpu().numpy(), osc)
+
+
 # ---------------------------------------------------------------- fusion
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
 @pytest.mark.parametrize("N,R,H,ln", [(37, 8, 128, True), (5, 3, 512, True), (9, 0, 64, True), (12, 4, 100, False)])
