@@ -22,6 +22,7 @@
 #include <string.h>
 
 #include <cmath>
+#include <type_traits>
 
 #include "grm_hip.h"
 #include "grm_hip_common.h"
@@ -593,6 +594,120 @@ __global__ __launch_bounds__(256) void fuse_kernel(const FuseArgs a) {
   }
 }
 
+// Vector form of fuse_kernel for 16-byte aligned rows (hidden a multiple of 8 /
+// 4 elements): `lpr` lanes (a power of two) share one row, each holding NV
+// 16-byte groups of it, so every access is a 16-byte load or store and all
+// routes' loads of a lane are in flight together.  Same arithmetic order per
+// element as fuse_kernel (the route sum, then the residual add).
+// One 16-byte group (8 16-bit or 4 fp32 elements) as floats; OOB -> zeros.
+template <class E>
+__device__ __forceinline__ void load_group(__amdgpu_buffer_rsrc_t r, int off, float (&f)[16 / sizeof(typename ET<E>::raw)]) {
+  typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+  const u32x4 q = __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0);
+  if constexpr (sizeof(typename ET<E>::raw) == 2) {
+    const U8<E> u = __builtin_bit_cast(U8<E>, q);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) f[e] = ET<E>::to_f(u.e[e]);
+  } else {
+#pragma unroll
+    for (int e = 0; e < 4; ++e) f[e] = __uint_as_float(q[e]);
+  }
+}
+
+template <class E, int NV>
+__global__ __launch_bounds__(256) void fuse_vec_kernel(const FuseArgs a, const int lpr) {
+  using raw = typename ET<E>::raw;
+  constexpr int VE = 16 / sizeof(raw);
+  typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+  const int tid = threadIdx.x;
+  const int sub = tid & (lpr - 1);
+  const int64_t row = static_cast<int64_t>(blockIdx.x) * (256 / lpr) + tid / lpr;
+  const bool live = row < a.rows;
+  const int H = a.hidden;
+  const int64_t rr = live ? row : 0;
+  const __amdgpu_buffer_rsrc_t rh = make_rsrc(static_cast<const raw*>(a.h) + rr * H, H * sizeof(raw));
+  const __amdgpu_buffer_rsrc_t rret =
+      make_rsrc(static_cast<const raw*>(a.ret) + rr * a.routes * H, static_cast<uint32_t>(a.routes * H * sizeof(raw)));
+  const float* g = a.gates + rr * a.routes;
+  float x[NV][VE];
+#pragma unroll
+  for (int v = 0; v < NV; ++v) {
+    const int c = (sub + lpr * v) * VE;
+    const int off = (live && c < H) ? c * static_cast<int>(sizeof(raw)) : kBufOOB;
+    float hv[VE];
+    load_group<E>(rh, off, hv);
+    float r[VE];
+#pragma unroll
+    for (int e = 0; e < VE; ++e) r[e] = 0.f;
+#pragma unroll 8
+    for (int j = 0; j < a.routes; ++j) {
+      const float gj = g[j];
+      const int o2 = (live && c < H) ? (j * H + c) * static_cast<int>(sizeof(raw)) : kBufOOB;
+      float rv[VE];
+      load_group<E>(rret, o2, rv);
+#pragma unroll
+      for (int e = 0; e < VE; ++e) r[e] = fmaf(gj, rv[e], r[e]);
+    }
+#pragma unroll
+    for (int e = 0; e < VE; ++e) x[v][e] = (c < H) ? hv[e] + r[e] : 0.f;
+  }
+  raw* out = static_cast<raw*>(a.out) + rr * H;
+  const __amdgpu_buffer_rsrc_t ro = make_rsrc(out, H * sizeof(raw));
+  auto store = [&](int v, const float (&y)[VE]) {
+    const int c = (sub + lpr * v) * VE;
+    const int off = (live && c < H) ? c * static_cast<int>(sizeof(raw)) : kBufOOB;
+    if constexpr (VE == 8) {
+      uint4 pk;
+      pk.x = ET<E>::from_f(y[0]) | (static_cast<uint32_t>(ET<E>::from_f(y[1])) << 16);
+      pk.y = ET<E>::from_f(y[2]) | (static_cast<uint32_t>(ET<E>::from_f(y[3])) << 16);
+      pk.z = ET<E>::from_f(y[4]) | (static_cast<uint32_t>(ET<E>::from_f(y[5])) << 16);
+      pk.w = ET<E>::from_f(y[6]) | (static_cast<uint32_t>(ET<E>::from_f(y[7])) << 16);
+      __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, pk), ro, off, 0, 0);
+    } else {
+      __builtin_amdgcn_raw_buffer_store_b128(
+          u32x4{__float_as_uint(y[0]), __float_as_uint(y[1]), __float_as_uint(y[2]), __float_as_uint(y[3])}, ro, off, 0, 0);
+    }
+  };
+  if (a.w == nullptr) {
+#pragma unroll
+    for (int v = 0; v < NV; ++v) store(v, x[v]);
+    return;
+  }
+  float sum = 0.f;
+#pragma unroll
+  for (int v = 0; v < NV; ++v)
+#pragma unroll
+    for (int e = 0; e < VE; ++e) sum += x[v][e];
+  for (int off = lpr >> 1; off > 0; off >>= 1) sum += __shfl_xor(sum, off, 64);
+  const float mean = sum / static_cast<float>(H);
+  float var = 0.f;
+#pragma unroll
+  for (int v = 0; v < NV; ++v) {
+    const int c = (sub + lpr * v) * VE;
+#pragma unroll
+    for (int e = 0; e < VE; ++e) {
+      const float d = x[v][e] - mean;
+      var = (c < H) ? fmaf(d, d, var) : var;
+    }
+  }
+  for (int off = lpr >> 1; off > 0; off >>= 1) var += __shfl_xor(var, off, 64);
+  const float rstd = 1.0f / sqrtf(var / static_cast<float>(H) + a.eps);
+  const __amdgpu_buffer_rsrc_t rw = make_rsrc(a.w, H * sizeof(raw));
+  const __amdgpu_buffer_rsrc_t rb = make_rsrc(a.bias, a.bias != nullptr ? H * sizeof(raw) : 0u);
+#pragma unroll
+  for (int v = 0; v < NV; ++v) {
+    const int c = (sub + lpr * v) * VE;
+    const int off = c < H ? c * static_cast<int>(sizeof(raw)) : kBufOOB;
+    float wv[VE], bv[VE];
+    load_group<E>(rw, off, wv);
+    load_group<E>(rb, off, bv);  // zeros without a bias
+    float y[VE];
+#pragma unroll
+    for (int e = 0; e < VE; ++e) y[e] = (x[v][e] - mean) * rstd * wv[e] + bv[e];
+    store(v, y);
+  }
+}
+
 bool aligned(const void* p, size_t n) { return (reinterpret_cast<uintptr_t>(p) % n) == 0; }
 
 }  // namespace
@@ -691,6 +806,35 @@ extern "C" int grm_hip_fuse_residual(const void* h_online, const void* retrieved
   a.hidden = static_cast<int>(hidden_size);
   a.eps = eps;
   hipStream_t s = static_cast<hipStream_t>(stream);
+  const int eb = dtype == GRM_HIP_F32 ? 4 : 2;
+  const int ve = 16 / eb;
+  const bool vec = hidden_size % ve == 0 && aligned(h_online, 16) && aligned(out, 16) &&
+                   (routes == 0 || aligned(retrieved, 16)) && (ln_weight == nullptr || aligned(ln_weight, 16)) &&
+                   (ln_bias == nullptr || aligned(ln_bias, 16)) && routes * hidden_size * eb <= INT32_MAX;
+  if (vec) {
+    // lanes per row: the power of two covering the row's 16-byte groups, at most 64
+    const int64_t groups = hidden_size / ve;
+    int lpr = 1;
+    while (lpr < 64 && lpr < groups) lpr <<= 1;
+    const int64_t nv = (groups + lpr - 1) / lpr;
+    const dim3 vgrid(static_cast<unsigned>((rows + 256 / lpr - 1) / (256 / lpr)));
+    auto go = [&](auto tag, auto nvc) {
+      using E = decltype(tag);
+      hipLaunchKernelGGL((fuse_vec_kernel<E, decltype(nvc)::value>), vgrid, dim3(256), 0, s, a, lpr);
+    };
+    auto by_nv = [&](auto tag) {
+      if (nv <= 1) go(tag, std::integral_constant<int, 1>{});
+      else if (nv <= 2) go(tag, std::integral_constant<int, 2>{});
+      else if (nv <= 4) go(tag, std::integral_constant<int, 4>{});
+      else go(tag, std::integral_constant<int, 8>{});
+    };
+    switch (dtype) {
+      case GRM_HIP_F32: by_nv(F32{}); break;
+      case GRM_HIP_F16: by_nv(F16{}); break;
+      default: by_nv(BF16{}); break;
+    }
+    return check_launch("fuse_residual");
+  }
   const dim3 grid(static_cast<unsigned>((rows + 3) / 4));
   switch (dtype) {
     case GRM_HIP_F32: hipLaunchKernelGGL(fuse_kernel<F32>, grid, dim3(256), 0, s, a); break;

@@ -324,8 +324,9 @@ def test_topk_route_unit_scale_and_large_norms(dev):
 
 
 # ---------------------------------------------------------------- fusion
-@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
-@pytest.mark.parametrize("N,R,H,ln", [(37, 8, 128, True), (5, 3, 512, True), (9, 0, 64, True), (12, 4, 100, False)])
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("N,R,H,ln", [(37, 8, 128, True), (5, 3, 512, True), (9, 0, 64, True), (12, 4, 100, False),
+                                      (70, 16, 2048, True), (33, 5, 24, True), (300, 8, 128, False), (3, 1, 1000, True)])
 def test_fuse_residual(dev, dtype, N, R, H, ln):
     g = torch.Generator().manual_seed(N)
     h = torch.randn(N, H, generator=g).to(dtype)
