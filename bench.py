@@ -190,6 +190,97 @@ def bench_c3(torch, dev, steps, warmup):
     }
 
 
+def bench_c5(torch, dev, steps, warmup):
+    """Config 5: one whole-sequence update call (16 heads x 65536 tokens, a snapshot every 128
+    tokens, 512 per head), then retrieval of k=16 archived states per token over those
+    snapshots: route -> gather_apply -> residual + LayerNorm.  Routing has no causal mask, as in
+    the reference's chunk path (every token sees all 512 states)."""
+    from rnn_with_grm_amd import capi
+
+    lib = capi.load()
+    BH, T, D, SEG, K = 16, 65536, 128, 128, 16
+    S = T // SEG
+    nrm = torch.nn.functional.normalize
+    g = torch.Generator().manual_seed(5)
+    q = nrm(torch.randn(BH, T, D, generator=g), dim=-1).to(torch.bfloat16).to(dev)
+    k = nrm(torch.randn(BH, T, D, generator=g), dim=-1).to(torch.bfloat16).to(dev)
+    v = torch.randn(BH, T, D, generator=g).to(torch.bfloat16).to(dev)
+    m0 = (torch.randn(BH, D, D, generator=g) * 0.02).to(dev)
+    summaries = nrm(torch.randn(BH, S, D, generator=g), dim=-1).to(torch.bfloat16).to(dev)
+    hidden = torch.empty(BH, T, D, dtype=torch.bfloat16, device=dev)
+    snaps = torch.empty(BH, S, D, D, device=dev)
+    stream = torch.cuda.current_stream(dev)
+    sp = ctypes.c_void_p(stream.cuda_stream)
+    P = lambda t: ctypes.c_void_p(t.data_ptr())  # noqa: E731
+    wsb = int(lib.grm_hip_chunk_update_fwd_workspace(BH, T, D, D, SEG))
+    ws = torch.empty(max(wsb, 16), dtype=torch.uint8, device=dev)
+
+    def update():
+        rc = lib.grm_hip_chunk_update_fwd(P(k), P(v), P(q), P(m0), P(hidden), None, P(snaps), P(ws), wsb, BH, T, D,
+                                          D, capi.BF16, capi.F32, 0.97, SEG, sp)
+        if rc != 0:
+            raise RuntimeError(capi.last_error())
+
+    u_wall, u_per = timed_launches(torch, update, max(3, steps), warmup, stream)
+    idx = torch.empty((BH, T, K), dtype=torch.int64, device=dev)
+    sc = torch.empty((BH, T, K), dtype=torch.float32, device=dev)
+    gt = torch.empty((BH, T, K), dtype=torch.float32, device=dev)
+    retrieved = torch.empty((BH, T, K, D), dtype=torch.float32, device=dev)
+    wsb2 = int(lib.grm_hip_gather_apply_workspace(BH, S, T * K))
+    ws2 = torch.empty(wsb2, dtype=torch.uint8, device=dev)
+    h_online = hidden.float().reshape(BH * T, D).contiguous()
+    ln_w = torch.ones(D, device=dev)
+    ln_b = torch.zeros(D, device=dev)
+    fused_out = torch.empty((BH * T, D), dtype=torch.float32, device=dev)
+
+    def route():
+        rc = lib.grm_hip_topk_route(P(q), P(summaries), P(idx), P(sc), P(gt), BH, T, S, D, capi.BF16, K,
+                                    1.0 / D ** 0.5, 1.0, sp)
+        if rc != 0:
+            raise RuntimeError(capi.last_error())
+
+    def gather_apply():
+        rc = lib.grm_hip_gather_apply(P(snaps), P(idx), P(q), P(retrieved), P(ws2), wsb2, BH, S, T, K, D, D,
+                                      capi.F32, capi.BF16, None, sp)
+        if rc != 0:
+            raise RuntimeError(capi.last_error())
+
+    def fuse():
+        rc = lib.grm_hip_fuse_residual(P(h_online), P(retrieved), P(gt), P(ln_w), P(ln_b), P(fused_out), BH * T, K,
+                                       D, capi.F32, 1e-5, sp)
+        if rc != 0:
+            raise RuntimeError(capi.last_error())
+
+    def retrieval():
+        route()
+        gather_apply()
+        fuse()
+
+    n = max(3, min(steps, 10))
+    r_wall, r_per = timed_launches(torch, route, n, min(warmup, 2), stream)
+    ga_wall, ga_per = timed_launches(torch, gather_apply, n, min(warmup, 2), stream)
+    fu_wall, fu_per = timed_launches(torch, fuse, n, min(warmup, 2), stream)
+    rt_wall, rt_per = timed_launches(torch, retrieval, n, min(warmup, 2), stream)
+    # spot checks: one token's retrieval against the composition, and its last snapshot
+    b, t = 3, 40000
+    r_ref = torch.einsum("rhk,k->rh", snaps[b, idx[b, t]], q[b, t].float())
+    assert torch.allclose(retrieved[b, t], r_ref, rtol=1e-4, atol=1e-6), "c5 gather_apply spot check failed"
+    assert bool(torch.isfinite(snaps[:, -1]).all()), "c5 snapshots not finite"
+    tokens = BH * T
+    upd_bytes = tokens * (2 * D + D) * 2 + tokens * D * 2 + BH * D * D * 4 + BH * S * D * D * 4
+    out = {
+        "update": {"us": statistics.mean(u_per) * 1e6, "bytes": upd_bytes, "tokens": tokens},
+        "route": {"ms": statistics.mean(r_per) * 1e3, "flops": 2 * tokens * S * D},
+        "gather_apply": {"ms": statistics.mean(ga_per) * 1e3,
+                         "bytes": BH * S * D * D * 4 + tokens * K * D * 4 + q.numel() * 2 + idx.numel() * 8,
+                         "flops": 2 * tokens * K * D * D},
+        "fuse": {"ms": statistics.mean(fu_per) * 1e3},
+        "retrieval": {"ms": statistics.mean(rt_per) * 1e3, "tokens": tokens},
+    }
+    del retrieved, h_online, fused_out, ws2, idx, sc, gt, snaps, hidden, q, k, v
+    return out
+
+
 def cpu_baseline(torch, budget_s: float = 20.0):
     """The torch-CPU port of the reference's CPU path on config 2 (full shape)."""
     from oracle import torch_port
@@ -294,6 +385,26 @@ def main() -> int:
             "speedup_vs_materialised_gather_alone": round(gth["ms"] / rt["ms"], 2)}
         log(f"c3 fused retrieval: {rt['ms']:.3f} ms (route {r['ms']:.3f}, gather_apply {ga['ms']:.3f}, "
             f"fuse {c3['fuse']['ms']:.3f})")
+
+    if not a.no_gather:
+        log("config 5: whole-sequence update (16 x 65536 tokens, 512 snapshots) + k=16 retrieval per token")
+        c5 = bench_c5(torch, dev, a.steps, a.warmup)
+        u, rt5, ga5 = c5["update"], c5["retrieval"], c5["gather_apply"]
+        ugbs = u["bytes"] / u["us"] / 1e3
+        secondary["c5_update"] = {"us": round(u["us"], 1), "tokens/s": round(u["tokens"] / u["us"] * 1e6),
+                                  "GB/s": round(ugbs, 1), "hbm_frac": round(ugbs / HBM_PEAK_GBS, 4),
+                                  "bytes": u["bytes"]}
+        secondary["c5_retrieval_fused"] = {
+            "what": "route (top-16 of 512 snapshots per token) -> gather_apply -> residual + LayerNorm, "
+                    "every token routed over all 512 states (no causal mask, as the reference's chunk path)",
+            "ms": round(rt5["ms"], 3), "tokens/s": round(rt5["tokens"] / rt5["ms"] * 1e3),
+            "route_ms": round(c5["route"]["ms"], 3), "gather_apply_ms": round(ga5["ms"], 3),
+            "fuse_ms": round(c5["fuse"]["ms"], 3),
+            "route_TFLOP/s": round(c5["route"]["flops"] / c5["route"]["ms"] / 1e9, 1),
+            "gather_apply_GB/s": round(ga5["bytes"] / ga5["ms"] / 1e6, 1),
+            "gather_apply_TFLOP/s_fp32": round(ga5["flops"] / ga5["ms"] / 1e9, 1)}
+        log(f"c5 update: {u['us']:.1f} us ({ugbs:.0f} GB/s); retrieval {rt5['ms']:.2f} ms (route "
+            f"{c5['route']['ms']:.2f}, gather_apply {ga5['ms']:.2f}, fuse {c5['fuse']['ms']:.2f})")
 
     cpu = None
     if not a.no_cpu:

@@ -29,7 +29,9 @@ namespace {
 
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
-constexpr int BK_THREADS = 1024;     // bucket kernel
+constexpr int BK_THREADS = 1024;     // bucket kernels
+constexpr int BK_ITEMS = 16384;      // pairs per workgroup when one sequence's pairs are split
+constexpr int64_t kMultiBucketPairs = 4 * BK_ITEMS;  // from this many pairs per sequence
 constexpr int64_t kMaxSegments = 16384;
 constexpr int AP_THREADS = 256;      // apply kernel: 4 waves
 constexpr int AP_V = 128;            // value rows per workgroup
@@ -51,29 +53,17 @@ struct RetrieveArgs {
   int dv;
   int dk;
   int v_tiles;
+  int32_t* partial;  // [batch, bk_chunks, segments]: per-chunk counts, then bases (multi-workgroup bucketing)
+  int bk_chunks;     // pair chunks of BK_ITEMS per sequence
 };
 
 // ---------------------------------------------------------------------------
-// Pairs of one sequence sorted by segment.  Rows with an invalid index are
-// zeroed here and never enter a bucket.
-template <class EM>
-__global__ __launch_bounds__(BK_THREADS) void bucket_kernel(const RetrieveArgs a) {
-  using raw = typename ET<EM>::raw;
-  extern __shared__ int hist[];  // [segments]
+// Exclusive scan of hist[0..S) in LDS, in place, by one workgroup of
+// BK_THREADS; offsets[s] gets the same values and offsets[S] the total.
+__device__ void bucket_offsets(int* hist, int64_t S, int32_t* offsets) {
   __shared__ int wave_sum[BK_THREADS / 64];
-  __shared__ int total;
   const int tid = threadIdx.x;
-  const int64_t b = blockIdx.x;
-  const int64_t S = a.segments, n = a.n_index;
-  const int64_t* ib = a.idx + b * n;
-  for (int64_t s = tid; s < S; s += BK_THREADS) hist[s] = 0;
-  __syncthreads();
-  for (int64_t i = tid; i < n; i += BK_THREADS) {
-    const int64_t s = ib[i];
-    if (s >= 0 && s < S) atomicAdd(&hist[s], 1);
-  }
-  __syncthreads();
-  // Exclusive scan of the histogram: thread t owns bins [t per, (t + 1) per).
+  // thread t owns bins [t per, (t + 1) per)
   const int per = static_cast<int>((S + BK_THREADS - 1) / BK_THREADS);
   const int lo = min(static_cast<int64_t>(tid) * per, S);
   const int hi = min(static_cast<int64_t>(lo) + per, S);
@@ -93,28 +83,117 @@ __global__ __launch_bounds__(BK_THREADS) void bucket_kernel(const RetrieveArgs a
   if (tid == 0) {
     int t = 0;
     for (int w = 0; w < BK_THREADS / 64; ++w) t += wave_sum[w];
-    total = t;
+    offsets[S] = t;
   }
   int run = base + incl - local;
-  int32_t* off = a.offsets + b * (S + 1);
   for (int s = lo; s < hi; ++s) {
     const int c = hist[s];
-    off[s] = run;
+    offsets[s] = run;
     hist[s] = run;
     run += c;
   }
   __syncthreads();
-  if (tid == 0) off[S] = total;
+}
+
+// A row whose index is outside [0, segments): zeros, and one count.
+template <class EM>
+__device__ __forceinline__ void zero_row(const RetrieveArgs& a, int64_t b, int64_t i) {
+  typename ET<EM>::raw* ob = static_cast<typename ET<EM>::raw*>(a.out) + (b * a.n_index + i) * a.dv;
+  for (int h = 0; h < a.dv; ++h) ob[h] = ET<EM>::from_f(0.f);
+  if (a.bad != nullptr) atomicAdd(a.bad, 1);
+}
+
+// Pairs of one sequence sorted by segment, one workgroup per sequence.  Rows
+// with an invalid index are zeroed here and never enter a bucket.
+template <class EM>
+__global__ __launch_bounds__(BK_THREADS) void bucket_kernel(const RetrieveArgs a) {
+  extern __shared__ int hist[];  // [segments]
+  const int tid = threadIdx.x;
+  const int64_t b = blockIdx.x;
+  const int64_t S = a.segments, n = a.n_index;
+  const int64_t* ib = a.idx + b * n;
+  for (int64_t s = tid; s < S; s += BK_THREADS) hist[s] = 0;
+  __syncthreads();
+  for (int64_t i = tid; i < n; i += BK_THREADS) {
+    const int64_t s = ib[i];
+    if (s >= 0 && s < S) atomicAdd(&hist[s], 1);
+  }
+  __syncthreads();
+  bucket_offsets(hist, S, a.offsets + b * (S + 1));
   int32_t* lb = a.list + b * n;
-  raw* ob = static_cast<raw*>(a.out) + b * n * a.dv;
   for (int64_t i = tid; i < n; i += BK_THREADS) {
     const int64_t s = ib[i];
     if (s >= 0 && s < S) {
       lb[atomicAdd(&hist[s], 1)] = static_cast<int32_t>(i);
     } else {
-      for (int h = 0; h < a.dv; ++h) ob[i * a.dv + h] = ET<EM>::from_f(0.f);
-      if (a.bad != nullptr) atomicAdd(a.bad, 1);
+      zero_row<EM>(a, b, i);
     }
+  }
+}
+
+// The same sort over many workgroups per sequence (three launches): counts per
+// chunk of BK_ITEMS pairs, per-(chunk, segment) bases, then the scatter.  The
+// order of pairs inside a segment does not change any result.
+template <class EM>
+__global__ __launch_bounds__(BK_THREADS) void bucket_count_kernel(const RetrieveArgs a) {
+  extern __shared__ int hist[];  // [segments]
+  const int tid = threadIdx.x;
+  const int64_t b = blockIdx.y, chunk = blockIdx.x;
+  const int64_t S = a.segments, n = a.n_index;
+  const int64_t i0 = chunk * BK_ITEMS, i1 = min(i0 + BK_ITEMS, n);
+  const int64_t* ib = a.idx + b * n;
+  for (int64_t s = tid; s < S; s += BK_THREADS) hist[s] = 0;
+  __syncthreads();
+  for (int64_t i = i0 + tid; i < i1; i += BK_THREADS) {
+    const int64_t s = ib[i];
+    if (s >= 0 && s < S) {
+      atomicAdd(&hist[s], 1);
+    } else {
+      zero_row<EM>(a, b, i);
+    }
+  }
+  __syncthreads();
+  int32_t* pc = a.partial + (b * a.bk_chunks + chunk) * S;
+  for (int64_t s = tid; s < S; s += BK_THREADS) pc[s] = hist[s];
+}
+
+__global__ __launch_bounds__(BK_THREADS) void bucket_bases_kernel(const RetrieveArgs a) {
+  extern __shared__ int hist[];  // [segments]: totals, then segment offsets
+  const int tid = threadIdx.x;
+  const int64_t b = blockIdx.x;
+  const int64_t S = a.segments;
+  int32_t* pb = a.partial + b * a.bk_chunks * S;
+  for (int64_t s = tid; s < S; s += BK_THREADS) {
+    int run = 0;
+    for (int c = 0; c < a.bk_chunks; ++c) {
+      const int v = pb[c * S + s];
+      pb[c * S + s] = run;
+      run += v;
+    }
+    hist[s] = run;
+  }
+  __syncthreads();
+  bucket_offsets(hist, S, a.offsets + b * (S + 1));
+  for (int64_t s = tid; s < S; s += BK_THREADS) {
+    const int off = hist[s];
+    for (int c = 0; c < a.bk_chunks; ++c) pb[c * S + s] += off;
+  }
+}
+
+__global__ __launch_bounds__(BK_THREADS) void bucket_scatter_kernel(const RetrieveArgs a) {
+  extern __shared__ int cur[];  // [segments]: next slot of each segment for this chunk
+  const int tid = threadIdx.x;
+  const int64_t b = blockIdx.y, chunk = blockIdx.x;
+  const int64_t S = a.segments, n = a.n_index;
+  const int64_t i0 = chunk * BK_ITEMS, i1 = min(i0 + BK_ITEMS, n);
+  const int64_t* ib = a.idx + b * n;
+  const int32_t* pc = a.partial + (b * a.bk_chunks + chunk) * S;
+  for (int64_t s = tid; s < S; s += BK_THREADS) cur[s] = pc[s];
+  __syncthreads();
+  int32_t* lb = a.list + b * n;
+  for (int64_t i = i0 + tid; i < i1; i += BK_THREADS) {
+    const int64_t s = ib[i];
+    if (s >= 0 && s < S) lb[atomicAdd(&cur[s], 1)] = static_cast<int32_t>(i);
   }
 }
 
@@ -399,6 +478,7 @@ __global__ __launch_bounds__(AP_THREADS) void apply_mfma16_kernel(const Retrieve
   constexpr int EPU_M = 16 / sizeof(rawm);
   constexpr int EPU_Q = 16 / sizeof(rawq);
   static_assert(KG % 8 == 0 && KG % EPU_M == 0 && KG % EPU_Q == 0, "a lane's keys are whole MFMA slots");
+  static_assert(AP_N == 64, "one pair per lane");
   __shared__ __align__(16) float Os[AP_N * OS];
 
   const int tid = threadIdx.x;
@@ -413,43 +493,63 @@ __global__ __launch_bounds__(AP_THREADS) void apply_mfma16_kernel(const Retrieve
   const int dk = a.dk, dv = a.dv;
   const int v0 = static_cast<int>(vt) * AP_V;
   const int k0 = g * KG;
+  const int32_t* lb = a.list + b * a.n_index;
+  // Pair ids of the first tile, one per lane (issued before the state loads so
+  // that waiting for them does not wait for the state).
+  int pid_l = lane < p_end - p_begin ? lb[p_begin + lane] : -1;
 
-  // A operands: state rows v = v0 + 32w + 16i + n, keys k0 .. k0 + KG - 1, in parts.
   const rawm* msrc = static_cast<const rawm*>(a.mem) + (b * a.segments + s) * dv * dk;
   const __amdgpu_buffer_rsrc_t rm = make_rsrc(msrc, static_cast<uint32_t>(dv * dk * sizeof(rawm)));
-  Frag8<EF> am[2][NPART][NSTEP];
+  float xm[2][KG];
 #pragma unroll
   for (int i = 0; i < 2; ++i) {
     const int v = v0 + 32 * w + 16 * i + n;
-    float x[KG];
 #pragma unroll
     for (int u = 0; u < KG / EPU_M; ++u) {
       const int k = k0 + u * EPU_M;
       load16_f32<EM>(rm, (v < dv && k < dk) ? (v * dk + k) * static_cast<int>(sizeof(rawm)) : kBufOOB,
-                     &x[u * EPU_M]);
-    }
-#pragma unroll
-    for (int c = 0; c < NSTEP; ++c) {
-#pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        float rest = x[8 * c + e];
-#pragma unroll
-        for (int part = 0; part < NPART; ++part) {
-          const typename ET<EF>::raw h = ET<EF>::from_f(rest);
-          am[i][part][c].e[e] = h;
-          rest -= ET<EF>::to_f(h);
-        }
-      }
+                     &xm[i][u * EPU_M]);
     }
   }
-  const int32_t* lb = a.list + b * a.n_index;
   const rawq* qsrc = static_cast<const rawq*>(a.queries) + b * a.n_query * dk;
   const __amdgpu_buffer_rsrc_t rq = make_rsrc(qsrc, static_cast<uint32_t>(a.n_query * dk * sizeof(rawq)));
   rawm* obase = static_cast<rawm*>(a.out) + b * a.n_index * dv;
   const int vcols = min(AP_V, dv - v0);
 
+  Frag8<EF> am[2][NPART][NSTEP];
+  bool split = false;
   for (int p0 = p_begin; p0 < p_end; p0 += AP_N) {
     const int np = min(AP_N, p_end - p0);
+    float xq[4][KG];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int pid = __shfl(pid_l, 16 * j + n, 64);
+#pragma unroll
+      for (int u = 0; u < KG / EPU_Q; ++u) {
+        const int k = k0 + u * EPU_Q;
+        load16_f32<EQ>(rq, (pid >= 0 && k < dk) ? (static_cast<int>(pid / a.routes) * dk + k) *
+                                                      static_cast<int>(sizeof(rawq))
+                                                : kBufOOB,
+                       &xq[j][u * EPU_Q]);
+      }
+    }
+    if (!split) {
+      split = true;
+#pragma unroll
+      for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int c = 0; c < NSTEP; ++c)
+#pragma unroll
+          for (int e = 0; e < 8; ++e) {
+            float rest = xm[i][8 * c + e];
+#pragma unroll
+            for (int part = 0; part < NPART; ++part) {
+              const typename ET<EF>::raw h = ET<EF>::from_f(rest);
+              am[i][part][c].e[e] = h;
+              rest -= ET<EF>::to_f(h);
+            }
+          }
+    }
     f32x4 acc[2][4];
 #pragma unroll
     for (int i = 0; i < 2; ++i)
@@ -457,22 +557,11 @@ __global__ __launch_bounds__(AP_THREADS) void apply_mfma16_kernel(const Retrieve
       for (int j = 0; j < 4; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-      const int p = 16 * j + n;
-      const int pid = p < np ? lb[p0 + p] : -1;
-      float x[KG];
-#pragma unroll
-      for (int u = 0; u < KG / EPU_Q; ++u) {
-        const int k = k0 + u * EPU_Q;
-        load16_f32<EQ>(rq, (pid >= 0 && k < dk) ? (static_cast<int>(pid / a.routes) * dk + k) *
-                                                      static_cast<int>(sizeof(rawq))
-                                                : kBufOOB,
-                       &x[u * EPU_Q]);
-      }
       Frag8<EF> bq[NSTEP];
 #pragma unroll
       for (int c = 0; c < NSTEP; ++c)
 #pragma unroll
-        for (int e = 0; e < 8; ++e) bq[c].e[e] = ET<EF>::from_f(ET<EM>::to_f(ET<EM>::from_f(x[8 * c + e])));
+        for (int e = 0; e < 8; ++e) bq[c].e[e] = ET<EF>::from_f(ET<EM>::to_f(ET<EM>::from_f(xq[j][8 * c + e])));
 #pragma unroll
       for (int c = 0; c < NSTEP; ++c)
 #pragma unroll
@@ -480,6 +569,8 @@ __global__ __launch_bounds__(AP_THREADS) void apply_mfma16_kernel(const Retrieve
 #pragma unroll
           for (int i = 0; i < 2; ++i) acc[i][j] = mfma8(am[i][part][c], bq[c], acc[i][j]);
     }
+    const int pid_cur = pid_l;
+    if (p0 + AP_N < p_end) pid_l = lane < p_end - p0 - AP_N ? lb[p0 + AP_N + lane] : -1;
     __syncthreads();  // previous output tile written out
 #pragma unroll
     for (int i = 0; i < 2; ++i)
@@ -487,17 +578,22 @@ __global__ __launch_bounds__(AP_THREADS) void apply_mfma16_kernel(const Retrieve
       for (int j = 0; j < 4; ++j)
         *reinterpret_cast<f32x4*>(Os + (16 * j + n) * OS + 32 * w + 16 * i + 4 * g) = acc[i][j];
     __syncthreads();
-    for (int e = tid; e < np * (AP_V / 4); e += AP_THREADS) {
-      const int p = e / (AP_V / 4), v = (e % (AP_V / 4)) * 4;
-      const int pid = lb[p0 + p];
-      const f32x4 val = *reinterpret_cast<const f32x4*>(Os + p * OS + v);
-      rawm* dst = obase + static_cast<int64_t>(pid) * dv + v0 + v;
-      if (v + 4 <= vcols) {
-        store4_raw<EM>(dst, val);
-      } else {
+    constexpr int PER = AP_N * (AP_V / 4) / AP_THREADS;  // stores per thread per full tile
 #pragma unroll
-        for (int r = 0; r < 4; ++r)
-          if (v + r < vcols) dst[r] = ET<EM>::from_f(val[r]);
+    for (int it = 0; it < PER; ++it) {
+      const int e = tid + AP_THREADS * it;
+      const int p = e / (AP_V / 4), v = (e % (AP_V / 4)) * 4;
+      const int pid = __shfl(pid_cur, p, 64);
+      if (p < np) {
+        const f32x4 val = *reinterpret_cast<const f32x4*>(Os + p * OS + v);
+        rawm* dst = obase + static_cast<int64_t>(pid) * dv + v0 + v;
+        if (v + 4 <= vcols) {
+          store4_raw<EM>(dst, val);
+        } else {
+#pragma unroll
+          for (int r = 0; r < 4; ++r)
+            if (v + r < vcols) dst[r] = ET<EM>::from_f(val[r]);
+        }
       }
     }
   }
@@ -582,25 +678,55 @@ int dispatch_q(const RetrieveArgs& a, int q_dtype, hipStream_t s) {
   }
 }
 
+int allow_segment_lds(const void* fn) {
+  const hipError_t e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                           static_cast<int>(kMaxSegments * sizeof(int)));
+  if (e != hipSuccess) {
+    set_error("gather_apply: hipFuncSetAttribute failed: %s", hipGetErrorString(e));
+    return static_cast<int>(e);
+  }
+  return GRM_HIP_OK;
+}
+
 template <class EM>
 int launch_bucket(const RetrieveArgs& a, hipStream_t s) {
   const size_t lds = static_cast<size_t>(a.segments) * sizeof(int);
-  static bool attr_set = false;
-  if (!attr_set) {
-    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&bucket_kernel<EM>),
-                                       hipFuncAttributeMaxDynamicSharedMemorySize,
-                                       static_cast<int>(kMaxSegments * sizeof(int)));
-    if (e != hipSuccess) {
-      set_error("gather_apply: hipFuncSetAttribute failed: %s", hipGetErrorString(e));
-      return static_cast<int>(e);
-    }
-    attr_set = true;
+  static int attr_rc = -1;
+  if (attr_rc != GRM_HIP_OK) {
+    attr_rc = allow_segment_lds(reinterpret_cast<const void*>(&bucket_kernel<EM>));
+    if (attr_rc == GRM_HIP_OK) attr_rc = allow_segment_lds(reinterpret_cast<const void*>(&bucket_count_kernel<EM>));
+    if (attr_rc == GRM_HIP_OK) attr_rc = allow_segment_lds(reinterpret_cast<const void*>(&bucket_bases_kernel));
+    if (attr_rc == GRM_HIP_OK) attr_rc = allow_segment_lds(reinterpret_cast<const void*>(&bucket_scatter_kernel));
+    if (attr_rc != GRM_HIP_OK) return attr_rc;
   }
-  hipLaunchKernelGGL((bucket_kernel<EM>), dim3(static_cast<unsigned>(a.batch)), dim3(BK_THREADS), lds, s, a);
-  return check_launch("gather_apply(sort)");
+  if (a.bk_chunks <= 1) {
+    hipLaunchKernelGGL((bucket_kernel<EM>), dim3(static_cast<unsigned>(a.batch)), dim3(BK_THREADS), lds, s, a);
+    return check_launch("gather_apply(sort)");
+  }
+  const dim3 grid(static_cast<unsigned>(a.bk_chunks), static_cast<unsigned>(a.batch));
+  hipLaunchKernelGGL((bucket_count_kernel<EM>), grid, dim3(BK_THREADS), lds, s, a);
+  int rc = check_launch("gather_apply(sort counts)");
+  if (rc != GRM_HIP_OK) return rc;
+  hipLaunchKernelGGL(bucket_bases_kernel, dim3(static_cast<unsigned>(a.batch)), dim3(BK_THREADS), lds, s, a);
+  rc = check_launch("gather_apply(sort bases)");
+  if (rc != GRM_HIP_OK) return rc;
+  hipLaunchKernelGGL(bucket_scatter_kernel, grid, dim3(BK_THREADS), lds, s, a);
+  return check_launch("gather_apply(sort scatter)");
 }
 
 int64_t offsets_bytes(int64_t batch, int64_t segments) { return (batch * (segments + 1) * 4 + 15) / 16 * 16; }
+
+// Pair chunks per sequence for the multi-workgroup sort (1: one workgroup per sequence).
+int64_t bucket_chunks(int64_t batch, int64_t n_index) {
+  return n_index >= kMultiBucketPairs && batch <= 65535 ? (n_index + BK_ITEMS - 1) / BK_ITEMS : 1;
+}
+
+int64_t list_bytes(int64_t batch, int64_t n_index) { return (batch * n_index * 4 + 15) / 16 * 16; }
+
+int64_t partial_bytes(int64_t batch, int64_t segments, int64_t n_index) {
+  const int64_t c = bucket_chunks(batch, n_index);
+  return c > 1 ? batch * c * segments * 4 : 0;
+}
 
 }  // namespace
 }  // namespace grmhip
@@ -609,7 +735,7 @@ using namespace grmhip;
 
 extern "C" int64_t grm_hip_gather_apply_workspace(int64_t batch, int64_t segments, int64_t n_index) {
   if (batch <= 0 || segments < 0 || n_index <= 0) return 0;
-  return offsets_bytes(batch, segments) + batch * n_index * 4;
+  return offsets_bytes(batch, segments) + list_bytes(batch, n_index) + partial_bytes(batch, segments, n_index);
 }
 
 extern "C" int grm_hip_gather_apply(const void* memories, const int64_t* indices, const void* queries, void* out,
@@ -652,6 +778,9 @@ extern "C" int grm_hip_gather_apply(const void* memories, const int64_t* indices
   a.out = out;
   a.offsets = static_cast<int32_t*>(workspace);
   a.list = reinterpret_cast<int32_t*>(static_cast<unsigned char*>(workspace) + offsets_bytes(batch, segments));
+  a.partial = reinterpret_cast<int32_t*>(static_cast<unsigned char*>(workspace) + offsets_bytes(batch, segments) +
+                                         list_bytes(batch, n_index));
+  a.bk_chunks = static_cast<int>(bucket_chunks(batch, n_index));
   a.bad = bad_index_count;
   a.batch = batch;
   a.segments = segments;

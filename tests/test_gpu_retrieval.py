@@ -165,6 +165,26 @@ def test_gather_apply_config3_slice(dev):
     torch.testing.assert_close(fused, composed, rtol=1e-5, atol=1e-6)
 
 
+def test_gather_apply_many_pairs_per_sequence(dev):
+    """72000 pairs per sequence take the multi-workgroup sort (chunks of 16384 pairs); with
+    invalid indices among them, against the composition on the CPU."""
+    B, S, Q, R, H, K = 2, 37, 9000, 8, 8, 16
+    g = torch.Generator().manual_seed(14)
+    mem = torch.randn(B, S, H, K, generator=g)
+    q = torch.randn(B, Q, K, generator=g)
+    idx = torch.randint(0, S, (B, Q, R), generator=g)
+    idx[0, 17, 3] = S
+    idx[1, 8999, 7] = -1
+    idx[1, 4000, :] = 36
+    bad = torch.zeros(1, dtype=torch.int32, device=dev)
+    out = capi.gather_apply(mem.to(dev), idx.to(dev), q.to(dev), bad_count=bad)
+    assert int(bad.item()) == 2
+    ok = (idx >= 0) & (idx < S)
+    ref = torch.einsum("bqrhk,bqk->bqrh", mem[torch.arange(B)[:, None, None], idx.clamp(0, S - 1)], q)
+    ref[~ok] = 0
+    torch.testing.assert_close(out.cpu(), ref, rtol=1e-5, atol=1e-5)
+
+
 def test_gather_apply_autograd_falls_back(dev):
     """With gradients required, cuda_gather_apply runs the differentiable composition:
     the queries get their gradient through apply_query; like the reference's native
