@@ -12,8 +12,9 @@ Differences, all deliberate:
     loaded the call raises instead of silently running PyTorch code.
   * ``auto`` runs the native apply-query kernel for rank-5 inputs too (the
     reference's auto policy sends rank 5 to einsum, cuda_ops.py:154-155).
-  * New whole-sequence / routing / fusion entry points: ``cuda_segment_scan``,
-    ``cuda_topk_route`` and ``cuda_fuse_residual``.
+  * New whole-sequence / routing / retrieval / fusion entry points:
+    ``cuda_segment_scan``, ``cuda_topk_route``, ``cuda_gather_apply`` and
+    ``cuda_fuse_residual``.
 """
 
 from __future__ import annotations
