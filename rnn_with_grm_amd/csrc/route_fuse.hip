@@ -235,6 +235,7 @@ int launch_route(const RouteArgs& a, int64_t batch, hipStream_t s) {
 constexpr int RM_THREADS = 256;  // four independent waves
 constexpr int RM_KT = 32;        // keys per tile
 constexpr int RM_ROW = RM_KT + 4;
+constexpr int RM_KC = 256;       // keys per LDS chunk of the exact pass
 
 __device__ __forceinline__ uint32_t order_bits(float f) {
   const uint32_t u = __float_as_uint(f);
@@ -245,21 +246,32 @@ __device__ __forceinline__ float unorder_bits(uint32_t u) {
   return __uint_as_float((u & 0x80000000u) ? (u ^ 0x80000000u) : ~u);
 }
 
-// Exact score of one key: the fp32 FMA chain over d in increasing order, times scale.
-template <int DKP>
-__device__ __forceinline__ float exact_score(const uint4 (&qv)[DKP / 8], __amdgpu_buffer_rsrc_t rk,
-                                             int key, int dim, float scale) {
-  float acc = 0.f;
+// Exact scores: each the fp32 FMA chain over d in increasing order, times
+// scale.  NCH chains at once (independent accumulators, the query converted
+// once per element); chain t reads the LDS key row rows[t].
+template <int DKP, int NCH>
+__device__ __forceinline__ void exact_scores_lds(const uint4 (&qv)[DKP / 8], const uint16_t* const (&rows)[NCH],
+                                                 int dim, float scale, float (&out)[NCH]) {
+  float acc[NCH];
+#pragma unroll
+  for (int t = 0; t < NCH; ++t) acc[t] = 0.f;
 #pragma unroll
   for (int u = 0; u < DKP / 8; ++u) {
     if (8 * u < dim) {
-      const U8<BF16> kv = buf_load8<BF16>(rk, (key * dim + 8 * u) * 2);
+      U8<BF16> kv[NCH];
+#pragma unroll
+      for (int t = 0; t < NCH; ++t) kv[t] = __builtin_bit_cast(U8<BF16>, *reinterpret_cast<const uint4*>(rows[t] + 8 * u));
       const U8<BF16> qq = __builtin_bit_cast(U8<BF16>, qv[u]);
 #pragma unroll
-      for (int e = 0; e < 8; ++e) acc = fmaf(ET<BF16>::to_f(qq.e[e]), ET<BF16>::to_f(kv.e[e]), acc);
+      for (int e = 0; e < 8; ++e) {
+        const float x = ET<BF16>::to_f(qq.e[e]);
+#pragma unroll
+        for (int t = 0; t < NCH; ++t) acc[t] = fmaf(x, ET<BF16>::to_f(kv[t].e[e]), acc[t]);
+      }
     }
   }
-  return acc * scale;
+#pragma unroll
+  for (int t = 0; t < NCH; ++t) out[t] = acc[t] * scale;
 }
 
 template <int KMAX>
@@ -277,10 +289,14 @@ __device__ __forceinline__ void exact_insert(float (&ts)[KMAX], int (&ti)[KMAX],
 }
 
 template <int DKP, int KMAX>
-__global__ __launch_bounds__(RM_THREADS) void route_mfma_kernel(const RouteArgs a, const int ib) {
+__global__ __launch_bounds__(RM_THREADS, 2) void route_mfma_kernel(const RouteArgs a, const int ib) {
   constexpr int NC = DKP / 32;  // 32-element MFMA steps over d
   constexpr int KN = KMAX + 4;
-  __shared__ __align__(16) uint32_t sc[4][64 * RM_ROW];
+  constexpr int KLS = DKP + 8;  // LDS key row stride (elements)
+  constexpr int TILE_BYTES = 4 * 64 * RM_ROW * 4;
+  constexpr int KEY_BYTES = RM_KC * KLS * 2;
+  // Score tiles during the MFMA pass; afterwards 256-key chunks for the exact chains.
+  __shared__ __align__(16) unsigned char smem[TILE_BYTES > KEY_BYTES ? TILE_BYTES : KEY_BYTES];
   __shared__ float red[4];
 
   const int tid = threadIdx.x;
@@ -322,7 +338,8 @@ __global__ __launch_bounds__(RM_THREADS) void route_mfma_kernel(const RouteArgs 
   for (int i = 1; i < 4; ++i) kmax2 = (red[i] <= INFINITY && kmax2 <= INFINITY) ? fmaxf(kmax2, red[i]) : NAN;
 
   const int64_t qw = static_cast<int64_t>(blockIdx.x) * RM_THREADS + 64 * w;  // first row of this wave
-  if (qw >= a.n_query) return;
+  // Every wave stays to the end: the exact chains stage keys with the whole workgroup.
+  const bool wave_live = qw < a.n_query;
   const int64_t qi = qw + lane;
   const bool active = qi < a.n_query;
   const uint16_t* qb = static_cast<const uint16_t*>(a.q) + b * a.n_query * D;
@@ -356,7 +373,7 @@ __global__ __launch_bounds__(RM_THREADS) void route_mfma_kernel(const RouteArgs 
   uint32_t net[KN];
 #pragma unroll
   for (int i = 0; i < KN; ++i) net[i] = 0u;
-  uint32_t* srow = &sc[w][0];
+  uint32_t* srow = reinterpret_cast<uint32_t*>(smem) + w * 64 * RM_ROW;
 
   Frag8<BF16> ak[2][NC];
   auto load_keys = [&](int s0) {
@@ -371,7 +388,8 @@ __global__ __launch_bounds__(RM_THREADS) void route_mfma_kernel(const RouteArgs 
     }
   };
   load_keys(0);
-  for (int s0 = 0; s0 < S; s0 += RM_KT) {
+  const int s_scan = wave_live ? S : 0;
+  for (int s0 = 0; s0 < s_scan; s0 += RM_KT) {
     f32x4 acc[4][2];
 #pragma unroll
     for (int qt = 0; qt < 4; ++qt)
@@ -426,13 +444,12 @@ __global__ __launch_bounds__(RM_THREADS) void route_mfma_kernel(const RouteArgs 
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
   }
-  if (!active) return;
-
   // This row, packed, for the exact chains.
   uint4 qv[DKP / 8];
 #pragma unroll
   for (int u = 0; u < DKP / 8; ++u)
-    qv[u] = __builtin_bit_cast(uint4, buf_load8<BF16>(rq, 8 * u < D ? static_cast<int>((qi * D + 8 * u) * 2) : kBufOOB));
+    qv[u] = __builtin_bit_cast(uint4, buf_load8<BF16>(rq, (active && 8 * u < D) ? static_cast<int>((qi * D + 8 * u) * 2)
+                                                                               : kBufOOB));
 
   float top_s[KMAX];
   int top_i[KMAX];
@@ -456,18 +473,71 @@ __global__ __launch_bounds__(RM_THREADS) void route_mfma_kernel(const RouteArgs 
   const float theta = tau - wide;
   const bool sound = qn * km < 1e30f && wide <= 1e30f;  // false for NaN and inf
   const bool complete = S <= KN || unorder_bits(net[KN - 1] & ~imask) < theta;
-  if (sound && complete) {
+  const bool scan_all = active && !(sound && complete);
+
+  // Candidate keys in ascending order (0xffffffff past the last), so that the
+  // candidates inside one key chunk are a contiguous run.
+  uint32_t ck[KN];
+#pragma unroll
+  for (int i = 0; i < KN; ++i) ck[i] = 0xffffffffu;
+#pragma unroll
+  for (int i = 0; i < KN; ++i) {
+    const bool take = active && !scan_all && i < S && unorder_bits(net[i] & ~imask) >= theta;
+    uint32_t x = take ? (net[i] & imask) : 0xffffffffu;
+#pragma unroll
+    for (int m = 0; m < KN; ++m) {
+      const uint32_t lo = min(ck[m], x);
+      x = max(ck[m], x);
+      ck[m] = lo;
+    }
+  }
+
+  // Key chunks through LDS; each lane walks its candidates in the chunk (or,
+  // for a row that needs it, every key of the chunk) with one copy of the chain.
+  const uint16_t* kl = reinterpret_cast<const uint16_t*>(smem);
+  for (int c0 = 0; c0 < S; c0 += RM_KC) {
+    const int c1 = min(S, c0 + RM_KC);
+    __syncthreads();  // score tiles / the previous chunk are no longer read
+    constexpr int UPR = DKP / 8;  // 16-byte units per padded row
+    for (int e = tid; e < RM_KC * UPR; e += RM_THREADS) {
+      const int r = e / UPR, u = e % UPR;
+      const int key = c0 + r;
+      const uint4 v = __builtin_bit_cast(
+          uint4, buf_load8<BF16>(rk, (key < c1 && 8 * u < D) ? (key * D + 8 * u) * 2 : kBufOOB));
+      *reinterpret_cast<uint4*>(reinterpret_cast<uint16_t*>(smem) + r * KLS + 8 * u) = v;
+    }
+    __syncthreads();
+    int lo = 0, hi = 0;
 #pragma unroll
     for (int i = 0; i < KN; ++i) {
-      if (i < S && unorder_bits(net[i] & ~imask) >= theta) {
-        const int key = static_cast<int>(net[i] & imask);
-        exact_insert<KMAX>(top_s, top_i, exact_score<DKP>(qv, rk, key, D, a.scale), key);
-      }
+      lo += ck[i] < static_cast<uint32_t>(c0) ? 1 : 0;
+      hi += ck[i] < static_cast<uint32_t>(c1) ? 1 : 0;
     }
-  } else {
-    for (int key = 0; key < S; ++key)
-      exact_insert<KMAX>(top_s, top_i, exact_score<DKP>(qv, rk, key, D, a.scale), key);
+    const int count = scan_all ? c1 - c0 : hi - lo;
+    constexpr int NCH = 2;  // chains per step
+#pragma unroll 1
+    for (int j = 0; j < count; j += NCH) {
+      int key[NCH];
+      const uint16_t* rows[NCH];
+#pragma unroll
+      for (int t = 0; t < NCH; ++t) {
+        key[t] = c0 + j + t;
+        if (!scan_all) {
+          uint32_t word = 0u;
+#pragma unroll
+          for (int i = 0; i < KN; ++i) word = (i == lo + j + t) ? ck[i] : word;
+          key[t] = static_cast<int>(word);
+        }
+        rows[t] = kl + (j + t < count ? key[t] - c0 : 0) * KLS;
+      }
+      float sc4[NCH];
+      exact_scores_lds<DKP, NCH>(qv, rows, D, a.scale, sc4);
+#pragma unroll
+      for (int t = 0; t < NCH; ++t)
+        if (j + t < count) exact_insert<KMAX>(top_s, top_i, sc4[t], key[t]);
+    }
   }
+  if (!active) return;
 
   const int64_t obase = (b * a.n_query + qi) * k;
   const float mx = top_s[0] * a.inv_temp;
