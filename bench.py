@@ -141,7 +141,7 @@ def bench_c3(torch, dev, steps, warmup):
 
     def gather_apply():
         rc = lib.grm_hip_gather_apply(P(states), P(idx), P(q), P(retrieved), P(ws), wsb, BH, S, Q, K, D, D, capi.F32,
-                                      capi.BF16, None, sp)
+                                      capi.BF16, capi.F32, None, sp)
         if rc != 0:
             raise RuntimeError(capi.last_error())
 
@@ -241,7 +241,7 @@ def bench_c5(torch, dev, steps, warmup):
 
     def gather_apply():
         rc = lib.grm_hip_gather_apply(P(snaps), P(idx), P(q), P(retrieved), P(ws2), wsb2, BH, S, T, K, D, D,
-                                      capi.F32, capi.BF16, None, sp)
+                                      capi.F32, capi.BF16, capi.F32, None, sp)
         if rc != 0:
             raise RuntimeError(capi.last_error())
 

@@ -140,15 +140,18 @@ int grm_hip_batched_gather(const void* memories, const int64_t* indices, void* o
 
 /*
  * Gather + query application without materialising the gathered states:
- *   out[b, q, r, h] = sum_k memories[b, indices[b, q, r], h, k] * queries'[b, q, k]
+ *   out[b, q, r, h] = sum_k memories'[b, indices[b, q, r], h, k] * queries'[b, q, k]
  * equal to grm_hip_apply_query_fwd over grm_hip_batched_gather(memories, indices), i.e.
  * the reference's apply_query_forward(batched_memory_gather(memories, indices), queries)
  *   (grm/core/cuda_ops.py:370-402, composed by the retriever in grm/core/paper_grm.py:229,301-313).
- * queries' is queries cast to mem_dtype first, as the reference's caller does
- * (paper_grm.py:301).  memories [batch, segments, hidden_size, key_dim] and out
- * [batch, n_query, routes, hidden_size] are mem_dtype; queries [batch, n_query,
- * key_dim] are q_dtype.  Every archived state is read from HBM once and applied
- * to all the queries that selected it; accumulation is float32.
+ * The arithmetic type is out_dtype: either mem_dtype, or float32 for 16-bit
+ * memories, which is the retriever's widening of the fp16 archive with
+ * .to(torch.float32) (paper_grm.py:227) done on load.  memories' and queries' are
+ * memories and queries cast to that type, as the reference's caller does
+ * (paper_grm.py:301).  memories [batch, segments, hidden_size, key_dim] are
+ * mem_dtype; out [batch, n_query, routes, hidden_size] is out_dtype; queries
+ * [batch, n_query, key_dim] are q_dtype.  Every archived state is read from HBM
+ * once and applied to all the queries that selected it; accumulation is float32.
  * An index outside [0, segments) yields a zero row and, when bad_index_count is
  * not NULL, increments that device int32 counter.
  * workspace: at least grm_hip_gather_apply_workspace(batch, segments, n_query * routes)
@@ -159,7 +162,7 @@ int64_t grm_hip_gather_apply_workspace(int64_t batch, int64_t segments, int64_t 
 int grm_hip_gather_apply(const void* memories, const int64_t* indices, const void* queries, void* out,
                          void* workspace, int64_t workspace_bytes, int64_t batch, int64_t segments,
                          int64_t n_query, int64_t routes, int64_t hidden_size, int64_t key_dim,
-                         int mem_dtype, int q_dtype, int32_t* bad_index_count, void* stream);
+                         int mem_dtype, int q_dtype, int out_dtype, int32_t* bad_index_count, void* stream);
 
 /*
  * Segment routing: dot-product score, top-k and softmax gates.

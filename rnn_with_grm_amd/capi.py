@@ -37,7 +37,7 @@ SIGNATURES = {
     "grm_hip_apply_query_bwd": (_C, [_P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _C, _P]),
     "grm_hip_batched_gather": (_C, [_P, _P, _P, _I, _I, _I, _I, _C, _P, _P]),
     "grm_hip_gather_apply_workspace": (_I, [_I, _I, _I]),
-    "grm_hip_gather_apply": (_C, [_P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _C, _C, _P, _P]),
+    "grm_hip_gather_apply": (_C, [_P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _C, _C, _C, _P, _P]),
     "grm_hip_topk_route": (_C, [_P, _P, _P, _P, _P, _I, _I, _I, _I, _C, _I, ctypes.c_float, ctypes.c_float, _P]),
     "grm_hip_fuse_residual": (_C, [_P, _P, _P, _P, _P, _P, _I, _I, _I, _C, ctypes.c_float, _P]),
 }
@@ -166,18 +166,20 @@ def batched_gather(memories, indices, bad_count=None, out=None):
     return out
 
 
-def gather_apply(memories, indices, queries, bad_count=None, out=None):
-    """out[b, q, r, :] = memories[b, indices[b, q, r]] @ queries[b, q] (queries cast to the
-    memories' dtype), without materialising the gathered states."""
+def gather_apply(memories, indices, queries, bad_count=None, out=None, dtype=None):
+    """out[b, q, r, :] = memories[b, indices[b, q, r]] @ queries[b, q] in `dtype` (the memories'
+    dtype by default, or float32: widened 16-bit memories), without materialising the gathered
+    states."""
     B, S, H, K = memories.shape
     Q, R = indices.shape[1], indices.shape[2]
+    dtype = dtype or memories.dtype
     if out is None:
-        out = torch.empty((B, Q, R, H), dtype=memories.dtype, device=memories.device)
+        out = torch.empty((B, Q, R, H), dtype=dtype, device=memories.device)
     wsb = int(load().grm_hip_gather_apply_workspace(B, S, Q * R))
     ws = torch.empty(max(wsb, 16), dtype=torch.uint8, device=memories.device)
     rc = load().grm_hip_gather_apply(_ptr(memories), _ptr(indices), _ptr(queries), _ptr(out), _ptr(ws), wsb, B, S,
                                      Q, R, H, K, dtype_code(memories.dtype), dtype_code(queries.dtype),
-                                     _ptr(bad_count), _stream(memories))
+                                     dtype_code(dtype), _ptr(bad_count), _stream(memories))
     _check(rc, "grm_hip_gather_apply")
     return out
 

@@ -215,7 +215,9 @@ Tensor batched_memory_gather_generic(const Tensor& memories, const Tensor& indic
 
 // gather_apply: the reference's composition apply_query_forward(
 // batched_memory_gather(memories, indices), queries.to(memories.dtype))
-// (grm/core/cuda_ops.py:370-402, paper_grm.py:229,301-313) in one op.
+// (grm/core/cuda_ops.py:370-402, paper_grm.py:229,301-313) in one op.  With
+// dtype=float32 the gathered 16-bit states are widened first, as the
+// retriever's .to(torch.float32) of the fp16 archive (paper_grm.py:227).
 void check_gather_apply_inputs(const Tensor& memories, const Tensor& indices, const Tensor& queries) {
   check_gather_inputs(memories, indices);
   TORCH_CHECK(queries.dim() == indices.dim(),
@@ -225,9 +227,18 @@ void check_gather_apply_inputs(const Tensor& memories, const Tensor& indices, co
   if (indices.dim() == 3) TORCH_CHECK(queries.size(1) == indices.size(1), "gather_apply: query dim mismatch");
 }
 
-Tensor gather_apply_generic(const Tensor& memories, const Tensor& indices, const Tensor& queries) {
+at::ScalarType gather_apply_dtype(const Tensor& memories, std::optional<at::ScalarType> dtype) {
+  const at::ScalarType t = dtype.value_or(memories.scalar_type());
+  TORCH_CHECK(t == memories.scalar_type() || t == at::kFloat,
+              "gather_apply: dtype must be the memories' dtype or float32");
+  return t;
+}
+
+Tensor gather_apply_generic(const Tensor& memories, const Tensor& indices, const Tensor& queries,
+                            std::optional<at::ScalarType> dtype) {
   check_gather_apply_inputs(memories, indices, queries);
-  return apply_query_forward_generic(batched_memory_gather_generic(memories, indices), queries.to(memories.scalar_type()));
+  const at::ScalarType t = gather_apply_dtype(memories, dtype);
+  return apply_query_forward_generic(batched_memory_gather_generic(memories, indices).to(t), queries.to(t));
 }
 
 // Canonical routing on the host: one float32 FMA chain per score, ties to the
@@ -459,12 +470,14 @@ Tensor batched_memory_gather_hip(const Tensor& memories, const Tensor& indices) 
   return out;
 }
 
-Tensor gather_apply_hip(const Tensor& memories, const Tensor& indices, const Tensor& queries) {
+Tensor gather_apply_hip(const Tensor& memories, const Tensor& indices, const Tensor& queries,
+                        std::optional<at::ScalarType> dtype) {
   check_gather_apply_inputs(memories, indices, queries);
+  const at::ScalarType t = gather_apply_dtype(memories, dtype);
   if (!same_cuda_device({&memories, &indices, &queries}) || dtype_code(memories.scalar_type()) < 0 ||
       dtype_code(queries.scalar_type()) < 0 || memories.size(3) > 128 || memories.size(1) > 16384) {
     g_generic_calls.fetch_add(1);
-    return gather_apply_generic(memories, indices, queries);
+    return gather_apply_generic(memories, indices, queries, dtype);
   }
   c10::OptionalDeviceGuard guard(memories.device());
   Tensor mm = memories.contiguous();
@@ -477,7 +490,7 @@ Tensor gather_apply_hip(const Tensor& memories, const Tensor& indices, const Ten
   if (idx.dim() == 3) shape.push_back(Q);
   shape.push_back(R);
   shape.push_back(H);
-  Tensor out = at::empty(shape, mm.options());
+  Tensor out = at::empty(shape, mm.options().dtype(t));
   const int64_t wsb = grm_hip_gather_apply_workspace(B, S, Q * R);
   Tensor ws = at::empty({std::max<int64_t>(wsb, 16)}, mm.options().dtype(at::kByte));
   Tensor bad;
@@ -485,7 +498,7 @@ Tensor gather_apply_hip(const Tensor& memories, const Tensor& indices, const Ten
   if (check) bad = at::zeros({1}, mm.options().dtype(at::kInt));
   check_rc(grm_hip_gather_apply(mm.data_ptr(), idx.data_ptr<int64_t>(), q.data_ptr(), out.data_ptr(), ws.data_ptr(),
                                 wsb, B, S, Q, R, H, K, dtype_code(mm.scalar_type()), dtype_code(q.scalar_type()),
-                                check ? bad.data_ptr<int32_t>() : nullptr, current_stream(mm)),
+                                dtype_code(t), check ? bad.data_ptr<int32_t>() : nullptr, current_stream(mm)),
            "gather_apply");
   if (check) {
     const int64_t nbad = bad.item<int32_t>();
@@ -634,7 +647,7 @@ TORCH_LIBRARY(grm_cuda, m) {
   m.def("segment_scan_forward(Tensor keys, Tensor values, Tensor queries, Tensor memory, float memory_decay, int segment_len) -> (Tensor hidden, Tensor memory_out, Tensor snapshots)");
   m.def("topk_route(Tensor queries, Tensor keys, int top_k, float scale, float temperature) -> (Tensor gates, Tensor indices, Tensor scores)");
   m.def("fuse_residual(Tensor h_online, Tensor retrieved, Tensor gates, Tensor? weight, Tensor? bias, float eps) -> Tensor");
-  m.def("gather_apply(Tensor memories, Tensor indices, Tensor queries) -> Tensor");
+  m.def("gather_apply(Tensor memories, Tensor indices, Tensor queries, ScalarType? dtype=None) -> Tensor");
 }
 
 TORCH_LIBRARY_IMPL(grm_cuda, CPU, m) {

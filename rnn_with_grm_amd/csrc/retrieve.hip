@@ -219,13 +219,14 @@ __device__ __forceinline__ void load16_f32(__amdgpu_buffer_rsrc_t r, int off, fl
 // value rows [32w, 32w + 32) for 64 pairs: D[v][p] = sum_k M[v][k] q'[p][k]
 // with A = state rows v, B = query rows p (lane (g, n) of a 16x16x4 operand
 // holds row n, key 4kk + g).
-template <class EM, class EQ, int DKP, bool VEC>
+template <class EL, class EM, class EQ, int DKP, bool VEC>
 __global__ __launch_bounds__(AP_THREADS) void apply_bucket_kernel(const RetrieveArgs a) {
-  using rawm = typename ET<EM>::raw;
+  using rawl = typename ET<EL>::raw;  // stored memories
+  using rawm = typename ET<EM>::raw;  // arithmetic / output type
   using rawq = typename ET<EQ>::raw;
   constexpr int MS = DKP + 4;                            // state tile row stride (floats)
   constexpr int QS = (DKP > AP_V ? DKP : AP_V) + 4;      // query / output tile row stride
-  constexpr int EPU_M = 16 / sizeof(rawm);               // elements per 16-byte unit
+  constexpr int EPU_M = 16 / sizeof(rawl);               // elements per 16-byte unit
   constexpr int EPU_Q = 16 / sizeof(rawq);
   constexpr int UPR_M = DKP / EPU_M;                     // units per padded row
   constexpr int UPR_Q = DKP / EPU_Q;
@@ -250,15 +251,15 @@ __global__ __launch_bounds__(AP_THREADS) void apply_bucket_kernel(const Retrieve
   const int v0 = static_cast<int>(vt) * AP_V;
 
   // State rows v0 .. v0 + 127 as fp32, zero past d_v and d_k.
-  const rawm* msrc = static_cast<const rawm*>(a.mem) + (b * a.segments + s) * dv * dk;
+  const rawl* msrc = static_cast<const rawl*>(a.mem) + (b * a.segments + s) * dv * dk;
   if constexpr (VEC) {
-    const __amdgpu_buffer_rsrc_t rm = make_rsrc(msrc, static_cast<uint32_t>(dv * dk * sizeof(rawm)));
+    const __amdgpu_buffer_rsrc_t rm = make_rsrc(msrc, static_cast<uint32_t>(dv * dk * sizeof(rawl)));
     float x[M_UNITS][EPU_M];
 #pragma unroll
     for (int u = 0; u < M_UNITS; ++u) {
       const int e = tid + AP_THREADS * u;
       const int v = e / UPR_M, c = (e % UPR_M) * EPU_M;
-      load16_f32<EM>(rm, (v0 + v < dv && c < dk) ? ((v0 + v) * dk + c) * static_cast<int>(sizeof(rawm)) : kBufOOB,
+      load16_f32<EL>(rm, (v0 + v < dv && c < dk) ? ((v0 + v) * dk + c) * static_cast<int>(sizeof(rawl)) : kBufOOB,
                      x[u]);
     }
 #pragma unroll
@@ -272,7 +273,7 @@ __global__ __launch_bounds__(AP_THREADS) void apply_bucket_kernel(const Retrieve
   } else {
     for (int e = tid; e < AP_V * DKP; e += AP_THREADS) {
       const int v = e / DKP, k = e % DKP;
-      Ms[v * MS + k] = (v0 + v < dv && k < dk) ? ET<EM>::to_f(msrc[(v0 + v) * dk + k]) : 0.f;
+      Ms[v * MS + k] = (v0 + v < dv && k < dk) ? ET<EL>::to_f(msrc[(v0 + v) * dk + k]) : 0.f;
     }
   }
   const int32_t* lb = a.list + b * a.n_index;
@@ -363,13 +364,14 @@ __global__ __launch_bounds__(AP_THREADS) void apply_bucket_kernel(const Retrieve
 // its pair's query row, both loaded with 16-byte vector loads straight into the
 // operand registers.  Only the output tile goes through LDS (for whole-row
 // stores), so two or three workgroups share a CU and hide each other's latency.
-template <class EM, class EQ, int DKP>
+template <class EL, class EM, class EQ, int DKP>
 __global__ __launch_bounds__(AP_THREADS) void apply_reg_kernel(const RetrieveArgs a) {
-  using rawm = typename ET<EM>::raw;
+  using rawl = typename ET<EL>::raw;  // stored memories
+  using rawm = typename ET<EM>::raw;  // arithmetic / output type
   using rawq = typename ET<EQ>::raw;
   constexpr int KG = DKP / 4;                       // keys per lane group
   constexpr int OS = AP_V + 4;                      // output tile row stride (floats)
-  constexpr int EPU_M = 16 / sizeof(rawm);
+  constexpr int EPU_M = 16 / sizeof(rawl);
   constexpr int EPU_Q = 16 / sizeof(rawq);
   static_assert(KG % EPU_M == 0 && KG % EPU_Q == 0, "a lane's keys are whole 16-byte units");
   __shared__ __align__(16) float Os[AP_N * OS];
@@ -388,8 +390,8 @@ __global__ __launch_bounds__(AP_THREADS) void apply_reg_kernel(const RetrieveArg
   const int k0 = g * KG;
 
   // A operands: state rows v = v0 + 32w + 16i + n, keys k0 .. k0 + KG - 1.
-  const rawm* msrc = static_cast<const rawm*>(a.mem) + (b * a.segments + s) * dv * dk;
-  const __amdgpu_buffer_rsrc_t rm = make_rsrc(msrc, static_cast<uint32_t>(dv * dk * sizeof(rawm)));
+  const rawl* msrc = static_cast<const rawl*>(a.mem) + (b * a.segments + s) * dv * dk;
+  const __amdgpu_buffer_rsrc_t rm = make_rsrc(msrc, static_cast<uint32_t>(dv * dk * sizeof(rawl)));
   float am[2][KG];
 #pragma unroll
   for (int i = 0; i < 2; ++i) {
@@ -397,7 +399,7 @@ __global__ __launch_bounds__(AP_THREADS) void apply_reg_kernel(const RetrieveArg
 #pragma unroll
     for (int u = 0; u < KG / EPU_M; ++u) {
       const int k = k0 + u * EPU_M;
-      load16_f32<EM>(rm, (v < dv && k < dk) ? (v * dk + k) * static_cast<int>(sizeof(rawm)) : kBufOOB,
+      load16_f32<EL>(rm, (v < dv && k < dk) ? (v * dk + k) * static_cast<int>(sizeof(rawl)) : kBufOOB,
                      &am[i][u * EPU_M]);
     }
   }
@@ -468,14 +470,15 @@ __global__ __launch_bounds__(AP_THREADS) void apply_reg_kernel(const RetrieveArg
 // to EM is exact in EF, so every product is exact and only the float32
 // accumulation rounds, as in a float32 dot product.  Lane group g owns keys
 // [g*KG, (g+1)*KG); MFMA step c (16x16x32) takes keys g*KG + 8c .. + 7 from group g.
-template <class EM, class EQ, int DKP, class EF, int NPART>
+template <class EL, class EM, class EQ, int DKP, class EF, int NPART>
 __global__ __launch_bounds__(AP_THREADS) void apply_mfma16_kernel(const RetrieveArgs a) {
-  using rawm = typename ET<EM>::raw;
+  using rawl = typename ET<EL>::raw;  // stored memories
+  using rawm = typename ET<EM>::raw;  // arithmetic / output type
   using rawq = typename ET<EQ>::raw;
   constexpr int KG = DKP / 4;
   constexpr int NSTEP = KG / 8;
   constexpr int OS = AP_V + 4;
-  constexpr int EPU_M = 16 / sizeof(rawm);
+  constexpr int EPU_M = 16 / sizeof(rawl);
   constexpr int EPU_Q = 16 / sizeof(rawq);
   static_assert(KG % 8 == 0 && KG % EPU_M == 0 && KG % EPU_Q == 0, "a lane's keys are whole MFMA slots");
   static_assert(AP_N == 64, "one pair per lane");
@@ -498,8 +501,8 @@ __global__ __launch_bounds__(AP_THREADS) void apply_mfma16_kernel(const Retrieve
   // that waiting for them does not wait for the state).
   int pid_l = lane < p_end - p_begin ? lb[p_begin + lane] : -1;
 
-  const rawm* msrc = static_cast<const rawm*>(a.mem) + (b * a.segments + s) * dv * dk;
-  const __amdgpu_buffer_rsrc_t rm = make_rsrc(msrc, static_cast<uint32_t>(dv * dk * sizeof(rawm)));
+  const rawl* msrc = static_cast<const rawl*>(a.mem) + (b * a.segments + s) * dv * dk;
+  const __amdgpu_buffer_rsrc_t rm = make_rsrc(msrc, static_cast<uint32_t>(dv * dk * sizeof(rawl)));
   float xm[2][KG];
 #pragma unroll
   for (int i = 0; i < 2; ++i) {
@@ -507,7 +510,7 @@ __global__ __launch_bounds__(AP_THREADS) void apply_mfma16_kernel(const Retrieve
 #pragma unroll
     for (int u = 0; u < KG / EPU_M; ++u) {
       const int k = k0 + u * EPU_M;
-      load16_f32<EM>(rm, (v < dv && k < dk) ? (v * dk + k) * static_cast<int>(sizeof(rawm)) : kBufOOB,
+      load16_f32<EL>(rm, (v < dv && k < dk) ? (v * dk + k) * static_cast<int>(sizeof(rawl)) : kBufOOB,
                      &xm[i][u * EPU_M]);
     }
   }
@@ -599,22 +602,23 @@ __global__ __launch_bounds__(AP_THREADS) void apply_mfma16_kernel(const Retrieve
   }
 }
 
-template <class EM, class EQ, int DKP, class EF, int NPART>
+template <class EL, class EM, class EQ, int DKP, class EF, int NPART>
 int launch_apply_mfma16(const RetrieveArgs& a, hipStream_t s) {
   const int64_t grid = a.batch * a.segments * a.v_tiles;
-  hipLaunchKernelGGL((apply_mfma16_kernel<EM, EQ, DKP, EF, NPART>), dim3(static_cast<unsigned>(grid)),
+  hipLaunchKernelGGL((apply_mfma16_kernel<EL, EM, EQ, DKP, EF, NPART>), dim3(static_cast<unsigned>(grid)),
                      dim3(AP_THREADS), 0, s, a);
   return check_launch("gather_apply");
 }
 
-template <class EM, class EQ, int DKP>
+template <class EL, class EM, class EQ, int DKP>
 int launch_apply_reg(const RetrieveArgs& a, hipStream_t s) {
   const int64_t grid = a.batch * a.segments * a.v_tiles;
-  hipLaunchKernelGGL((apply_reg_kernel<EM, EQ, DKP>), dim3(static_cast<unsigned>(grid)), dim3(AP_THREADS), 0, s, a);
+  hipLaunchKernelGGL((apply_reg_kernel<EL, EM, EQ, DKP>), dim3(static_cast<unsigned>(grid)), dim3(AP_THREADS), 0, s,
+                     a);
   return check_launch("gather_apply");
 }
 
-template <class EM, class EQ, int DKP, bool VEC>
+template <class EL, class EM, class EQ, int DKP, bool VEC>
 int launch_apply(const RetrieveArgs& a, hipStream_t s) {
   constexpr int MS = DKP + 4;
   constexpr int QS = (DKP > AP_V ? DKP : AP_V) + 4;
@@ -622,7 +626,7 @@ int launch_apply(const RetrieveArgs& a, hipStream_t s) {
   static_assert(lds <= 160 * 1024, "apply tiles fit one CU's LDS");
   static bool attr_set = false;
   if (!attr_set) {
-    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&apply_bucket_kernel<EM, EQ, DKP, VEC>),
+    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&apply_bucket_kernel<EL, EM, EQ, DKP, VEC>),
                                        hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds));
     if (e != hipSuccess) {
       set_error("gather_apply: hipFuncSetAttribute failed: %s", hipGetErrorString(e));
@@ -631,50 +635,70 @@ int launch_apply(const RetrieveArgs& a, hipStream_t s) {
     attr_set = true;
   }
   const int64_t grid = a.batch * a.segments * a.v_tiles;
-  hipLaunchKernelGGL((apply_bucket_kernel<EM, EQ, DKP, VEC>), dim3(static_cast<unsigned>(grid)), dim3(AP_THREADS),
-                     lds, s, a);
+  hipLaunchKernelGGL((apply_bucket_kernel<EL, EM, EQ, DKP, VEC>), dim3(static_cast<unsigned>(grid)),
+                     dim3(AP_THREADS), lds, s, a);
   return check_launch("gather_apply");
 }
 
 // 16-byte tile loads need whole units per row and 16-byte aligned bases.
-template <class EM, class EQ>
+template <class EL, class EQ>
 bool vec_ok(const RetrieveArgs& a) {
-  const int em = 16 / static_cast<int>(sizeof(typename ET<EM>::raw));
+  const int el = 16 / static_cast<int>(sizeof(typename ET<EL>::raw));
   const int eq = 16 / static_cast<int>(sizeof(typename ET<EQ>::raw));
-  return a.dk % em == 0 && a.dk % eq == 0 && reinterpret_cast<uintptr_t>(a.mem) % 16 == 0 &&
+  return a.dk % el == 0 && a.dk % eq == 0 && reinterpret_cast<uintptr_t>(a.mem) % 16 == 0 &&
          reinterpret_cast<uintptr_t>(a.queries) % 16 == 0 &&
-         a.dv * static_cast<int64_t>(a.dk) * static_cast<int64_t>(sizeof(typename ET<EM>::raw)) < INT32_MAX &&
+         a.dv * static_cast<int64_t>(a.dk) * static_cast<int64_t>(sizeof(typename ET<EL>::raw)) < INT32_MAX &&
          a.n_query * static_cast<int64_t>(a.dk) * static_cast<int64_t>(sizeof(typename ET<EQ>::raw)) < INT32_MAX;
 }
 
-template <class EM, class EQ>
+// Exact 16-bit MFMA when both operands are exact in one 16-bit MFMA input type
+// EF: the query in the arithmetic type EM must be exact in EF, and the stored
+// memories split into NPART parts of EF without loss.  Otherwise fp32 MFMA.
+template <class EL, class EM, class EQ>
+struct MfmaPlan {
+  static constexpr bool kSame = std::is_same<EL, EM>::value;
+  static constexpr bool kF32 = std::is_same<EM, F32>::value;
+  // EM 16-bit (then EL == EM): the query is cast to EM, EF = EM, one part.
+  // EM float32: queries bf16 with fp32 / bf16 / f16 memories (3 / 1 / 2 bf16
+  // parts), or f16 queries with f16 memories (one f16 part).
+  static constexpr bool kBf16Q = std::is_same<EQ, BF16>::value;
+  static constexpr bool kF16Both = std::is_same<EQ, F16>::value && std::is_same<EL, F16>::value;
+  static constexpr bool ok = !kF32 ? kSame : (kBf16Q || kF16Both);
+  using EF = typename std::conditional<!kF32, EM, typename std::conditional<kF16Both, F16, BF16>::type>::type;
+  static constexpr int parts = !kF32 ? 1
+                               : kF16Both ? 1
+                               : std::is_same<EL, F32>::value ? 3
+                               : std::is_same<EL, F16>::value ? 2
+                                                              : 1;
+};
+
+template <class EL, class EM, class EQ>
 int dispatch_dk(const RetrieveArgs& a, hipStream_t s) {
-  if (vec_ok<EM, EQ>(a)) {
-    // Exact 16-bit MFMA when the query in the memories' dtype is exact in the
-    // MFMA input type: bf16 / f16 memories, or float32 memories with bf16 queries.
-    if constexpr (!std::is_same<EM, F32>::value || std::is_same<EQ, BF16>::value) {
-      using EF = typename std::conditional<std::is_same<EM, F16>::value, F16, BF16>::type;
-      constexpr int NPART = std::is_same<EM, F32>::value ? 3 : 1;
-      if (a.dk <= 32) return launch_apply_mfma16<EM, EQ, 32, EF, NPART>(a, s);
-      if (a.dk <= 64) return launch_apply_mfma16<EM, EQ, 64, EF, NPART>(a, s);
-      return launch_apply_mfma16<EM, EQ, 128, EF, NPART>(a, s);
+  if (vec_ok<EL, EQ>(a)) {
+    using Plan = MfmaPlan<EL, EM, EQ>;
+    if constexpr (Plan::ok) {
+      using EF = typename Plan::EF;
+      constexpr int NPART = Plan::parts;
+      if (a.dk <= 32) return launch_apply_mfma16<EL, EM, EQ, 32, EF, NPART>(a, s);
+      if (a.dk <= 64) return launch_apply_mfma16<EL, EM, EQ, 64, EF, NPART>(a, s);
+      return launch_apply_mfma16<EL, EM, EQ, 128, EF, NPART>(a, s);
     } else {
-      if (a.dk <= 32) return launch_apply_reg<EM, EQ, 32>(a, s);
-      if (a.dk <= 64) return launch_apply_reg<EM, EQ, 64>(a, s);
-      return launch_apply_reg<EM, EQ, 128>(a, s);
+      if (a.dk <= 32) return launch_apply_reg<EL, EM, EQ, 32>(a, s);
+      if (a.dk <= 64) return launch_apply_reg<EL, EM, EQ, 64>(a, s);
+      return launch_apply_reg<EL, EM, EQ, 128>(a, s);
     }
   }
-  if (a.dk <= 32) return launch_apply<EM, EQ, 32, false>(a, s);
-  if (a.dk <= 64) return launch_apply<EM, EQ, 64, false>(a, s);
-  return launch_apply<EM, EQ, 128, false>(a, s);
+  if (a.dk <= 32) return launch_apply<EL, EM, EQ, 32, false>(a, s);
+  if (a.dk <= 64) return launch_apply<EL, EM, EQ, 64, false>(a, s);
+  return launch_apply<EL, EM, EQ, 128, false>(a, s);
 }
 
-template <class EM>
+template <class EL, class EM>
 int dispatch_q(const RetrieveArgs& a, int q_dtype, hipStream_t s) {
   switch (q_dtype) {
-    case GRM_HIP_F32: return dispatch_dk<EM, F32>(a, s);
-    case GRM_HIP_F16: return dispatch_dk<EM, F16>(a, s);
-    default: return dispatch_dk<EM, BF16>(a, s);
+    case GRM_HIP_F32: return dispatch_dk<EL, EM, F32>(a, s);
+    case GRM_HIP_F16: return dispatch_dk<EL, EM, F16>(a, s);
+    default: return dispatch_dk<EL, EM, BF16>(a, s);
   }
 }
 
@@ -741,7 +765,8 @@ extern "C" int64_t grm_hip_gather_apply_workspace(int64_t batch, int64_t segment
 extern "C" int grm_hip_gather_apply(const void* memories, const int64_t* indices, const void* queries, void* out,
                                     void* workspace, int64_t workspace_bytes, int64_t batch, int64_t segments,
                                     int64_t n_query, int64_t routes, int64_t hidden_size, int64_t key_dim,
-                                    int mem_dtype, int q_dtype, int32_t* bad_index_count, void* stream) {
+                                    int mem_dtype, int q_dtype, int out_dtype, int32_t* bad_index_count,
+                                    void* stream) {
   if (batch < 0 || segments < 0 || n_query < 0 || routes < 0 || hidden_size < 0 || key_dim < 1) {
     set_error("gather_apply: negative size or key_dim < 1");
     return GRM_HIP_EINVAL;
@@ -749,6 +774,10 @@ extern "C" int grm_hip_gather_apply(const void* memories, const int64_t* indices
   if (mem_dtype < GRM_HIP_F32 || mem_dtype > GRM_HIP_BF16 || q_dtype < GRM_HIP_F32 || q_dtype > GRM_HIP_BF16) {
     set_error("gather_apply: unsupported dtypes mem=%d q=%d", mem_dtype, q_dtype);
     return GRM_HIP_EUNSUPPORTED;
+  }
+  if (out_dtype != mem_dtype && out_dtype != GRM_HIP_F32) {
+    set_error("gather_apply: out_dtype %d must be the memories' dtype %d or float32", out_dtype, mem_dtype);
+    return GRM_HIP_EINVAL;
   }
   if (key_dim > 128 || segments > kMaxSegments) {
     set_error("gather_apply: key_dim %lld > 128 or segments %lld > %lld", (long long)key_dim, (long long)segments,
@@ -792,15 +821,22 @@ extern "C" int grm_hip_gather_apply(const void* memories, const int64_t* indices
   a.v_tiles = static_cast<int>((hidden_size + AP_V - 1) / AP_V);
   hipStream_t s = static_cast<hipStream_t>(stream);
   int rc;
-  switch (mem_dtype) {
+  switch (out_dtype) {
     case GRM_HIP_F32: rc = launch_bucket<F32>(a, s); break;
     case GRM_HIP_F16: rc = launch_bucket<F16>(a, s); break;
     default: rc = launch_bucket<BF16>(a, s); break;
   }
   if (rc != GRM_HIP_OK || segments == 0) return rc;
+  if (out_dtype == GRM_HIP_F32) {
+    // float32 arithmetic and output; 16-bit memories are widened exactly on load
+    switch (mem_dtype) {
+      case GRM_HIP_F32: return dispatch_q<F32, F32>(a, q_dtype, s);
+      case GRM_HIP_F16: return dispatch_q<F16, F32>(a, q_dtype, s);
+      default: return dispatch_q<BF16, F32>(a, q_dtype, s);
+    }
+  }
   switch (mem_dtype) {
-    case GRM_HIP_F32: return dispatch_q<F32>(a, q_dtype, s);
-    case GRM_HIP_F16: return dispatch_q<F16>(a, q_dtype, s);
-    default: return dispatch_q<BF16>(a, q_dtype, s);
+    case GRM_HIP_F16: return dispatch_q<F16, F16>(a, q_dtype, s);
+    default: return dispatch_q<BF16, BF16>(a, q_dtype, s);
   }
 }

@@ -386,17 +386,21 @@ def cuda_fuse_residual(h_online: Tensor, retrieved: Tensor, gates: Tensor, weigh
     return x
 
 
-def cuda_gather_apply(memories_per_batch: Tensor, topk_indices: Tensor, queries: Tensor, *, enabled: bool = True,
+def cuda_gather_apply(memories_per_batch: Tensor, topk_indices: Tensor, queries: Tensor,
+                      dtype: Optional[torch.dtype] = None, *, enabled: bool = True,
                       debug_fallback: bool = False) -> Tensor:
-    """apply_query(batched_memory_gather(M, idx), q.to(M.dtype)) without materialising the
-    gathered states (cuda_ops.py:370-402, composed as in paper_grm.py:229,301-313).
+    """apply_query(batched_memory_gather(M, idx).to(dtype), q.to(dtype)) without materialising
+    the gathered states (cuda_ops.py:370-402, composed as in paper_grm.py:227-229,301-313).
+    ``dtype`` is M's dtype by default; float32 widens 16-bit archives as the retriever does.
     The fused op has no backward: when autograd needs gradients the composition runs."""
     needs_grad = torch.is_grad_enabled() and (memories_per_batch.requires_grad or queries.requires_grad)
     if not needs_grad and _use_native("gather_apply", memories_per_batch.device, enabled=enabled,
                                       debug_fallback=debug_fallback):
-        return torch.ops.grm_cuda.gather_apply(memories_per_batch, topk_indices, queries)
+        return torch.ops.grm_cuda.gather_apply(memories_per_batch, topk_indices, queries, dtype)
     gathered = cuda_batched_memory_gather(memories_per_batch, topk_indices, enabled=enabled,
                                           debug_fallback=debug_fallback)
+    if dtype is not None:
+        gathered = gathered.to(dtype)
     return cuda_apply_query(gathered, queries.to(gathered.dtype), enabled=enabled, debug_fallback=debug_fallback)
 
 

@@ -187,6 +187,14 @@ def test_cpu_gather_apply_is_the_composition():
     np.testing.assert_allclose(out.numpy(), ref, rtol=1e-5, atol=1e-6)
     with pytest.raises(RuntimeError, match="key dim mismatch"):
         torch.ops.grm_cuda.gather_apply(mem, idx, q[..., :5])
+    # dtype=float32 on a float16 archive: widened states, float32 queries and output
+    m16 = mem.to(torch.float16)
+    wide = torch.ops.grm_cuda.gather_apply(m16, idx, q, torch.float32)
+    g16, _ = orc.gather(m16.double().numpy(), idx.numpy())
+    assert wide.dtype == torch.float32
+    np.testing.assert_allclose(wide.numpy(), orc.apply_query(g16, np64(q.float())), rtol=1e-5, atol=1e-6)
+    with pytest.raises(RuntimeError, match="memories' dtype or float32"):
+        torch.ops.grm_cuda.gather_apply(m16, idx, q, torch.bfloat16)
 
 
 def test_shape_errors_raise_like_reference():

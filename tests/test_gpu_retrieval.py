@@ -125,6 +125,26 @@ def test_gather_apply_matches_composition(dev, mem_dtype, q_dtype, B, S, Q, R, H
     np.testing.assert_allclose(out.float().cpu().double().numpy(), ref, rtol=tol[0], atol=tol[1])
 
 
+@pytest.mark.parametrize("mem_dtype,q_dtype", [(torch.float16, torch.bfloat16), (torch.float16, torch.float32),
+                                               (torch.float16, torch.float16), (torch.bfloat16, torch.bfloat16),
+                                               (torch.bfloat16, torch.float16), (torch.float32, torch.float32)])
+@pytest.mark.parametrize("B,S,Q,R,H,K", [(3, 7, 13, 3, 20, 8), (2, 64, 90, 8, 128, 64), (1, 5, 4, 2, 8, 33)])
+def test_gather_apply_widened(dev, mem_dtype, q_dtype, B, S, Q, R, H, K):
+    """dtype=float32: 16-bit archives widened on load, queries cast to float32, float32 out,
+    i.e. the retriever's stack(...).to(float32) then apply (paper_grm.py:227-229,301)."""
+    g = torch.Generator().manual_seed(B * 31 + K)
+    mem = (torch.randn(B, S, H, K, generator=g) * 0.05).to(mem_dtype)
+    q = norm(torch.randn(B, Q, K, generator=g)).to(q_dtype)
+    idx = torch.randint(0, S, (B, Q, R), generator=g)
+    out = capi.gather_apply(mem.to(dev), idx.to(dev), q.to(dev), dtype=torch.float32)
+    gathered, bad = orc.gather(mem.double().numpy(), idx.numpy())
+    ref = orc.apply_query(gathered, q.double().numpy())
+    assert out.dtype == torch.float32 and out.shape == (B, Q, R, H)
+    np.testing.assert_allclose(out.cpu().double().numpy(), ref, rtol=1e-5, atol=1e-6)
+    op = torch.ops.grm_cuda.gather_apply(mem.to(dev), idx.to(dev), q.to(dev), torch.float32)
+    assert torch.equal(op, out)
+
+
 def test_gather_apply_bad_indices_and_rank2(dev):
     """Out-of-range indices give zero rows and are counted; rank-2 indices ([B, R]
     with queries [B, K]) go through the torch op like the reference's rank-4 apply."""
