@@ -281,6 +281,46 @@ def bench_c5(torch, dev, steps, warmup):
     return out
 
 
+def bench_c4_archive(torch, dev, steps, warmup):
+    """Config 4's per-segment retrieval (B=4, hidden 512, d_k 64, 64-token segments, k=8, a full
+    64-segment float16 archive), two ways:
+      reference style - the retriever's own composition (paper_grm.py:227-229,301-313): stack the
+                        64 archived states, widen to float32, gather [B,64,8,512,64], apply;
+      device archive  - DeviceSegmentArchive.retrieve_from_indices: the float16 ring read in place
+                        by one fused gather + apply with float32 widening on load."""
+    from types import SimpleNamespace
+
+    from rnn_with_grm_amd import cuda_ops
+    from rnn_with_grm_amd.archive import DeviceSegmentArchive
+
+    B, H, K, SEG, R, CAP, DIN = 4, 512, 64, 64, 8, 64, 512
+    g = torch.Generator().manual_seed(4)
+    mems = [(torch.randn(B, H, K, generator=g) * 0.02).to(torch.float16).to(dev) for _ in range(CAP)]
+    summ = torch.randn(B, CAP, DIN, generator=g).to(dev)
+    arch = DeviceSegmentArchive(H, K, DIN, CAP, torch.float16).to(dev)
+    arch.push_segments(torch.stack(mems, 1), summ)
+    cell = SimpleNamespace(query_proj=torch.nn.Linear(DIN, K).to(dev))
+    x = torch.randn(B, SEG, DIN, generator=g).to(dev)
+    idx = torch.randint(0, CAP, (B, SEG, R), generator=g).to(dev)
+    stream = torch.cuda.current_stream(dev)
+
+    def reference_style():
+        allm = torch.stack(mems, dim=0).to(torch.float32).permute(1, 0, 2, 3).contiguous()
+        sel = cuda_ops.cuda_batched_memory_gather(allm, idx)
+        q = torch.nn.functional.normalize(cell.query_proj(x), p=2, dim=-1, eps=1e-6).to(sel.dtype)
+        return cuda_ops.cuda_apply_query(sel, q)
+
+    def device_archive():
+        return arch.retrieve_from_indices(x, idx, None, cell, dev, 0.97)
+
+    with torch.no_grad():
+        a, b = reference_style(), device_archive()
+        assert torch.allclose(a, b, rtol=1e-4, atol=1e-5), "c4 archive retrieval mismatch"
+        r_wall, r_per = timed_launches(torch, reference_style, max(3, steps), warmup, stream)
+        d_wall, d_per = timed_launches(torch, device_archive, max(3, steps), warmup, stream)
+    return {"reference_style_ms": statistics.mean(r_per) * 1e3, "device_archive_ms": statistics.mean(d_per) * 1e3}
+
+
 def cpu_baseline(torch, budget_s: float = 20.0):
     """The torch-CPU port of the reference's CPU path on config 2 (full shape)."""
     from oracle import torch_port
@@ -405,6 +445,17 @@ def main() -> int:
             "gather_apply_TFLOP/s_fp32": round(ga5["flops"] / ga5["ms"] / 1e9, 1)}
         log(f"c5 update: {u['us']:.1f} us ({ugbs:.0f} GB/s); retrieval {rt5['ms']:.2f} ms (route "
             f"{c5['route']['ms']:.2f}, gather_apply {ga5['ms']:.2f}, fuse {c5['fuse']['ms']:.2f})")
+
+    if not a.no_gather:
+        c4 = bench_c4_archive(torch, dev, a.steps, a.warmup)
+        secondary["c4_segment_retrieval"] = {
+            "what": "one 64-token segment's retrieval at config 4 (B=4, d_v=512, d_k=64, k=8, 64 float16 "
+                    "archived states): the retriever's stack + widen + gather + apply vs DeviceSegmentArchive",
+            "reference_style_ms": round(c4["reference_style_ms"], 4),
+            "device_archive_ms": round(c4["device_archive_ms"], 4),
+            "speedup": round(c4["reference_style_ms"] / c4["device_archive_ms"], 2)}
+        log(f"c4 segment retrieval: reference style {c4['reference_style_ms']:.3f} ms, device archive "
+            f"{c4['device_archive_ms']:.3f} ms")
 
     cpu = None
     if not a.no_cpu:

@@ -2,8 +2,12 @@
 application, top-k routing, archived-state gather and residual fusion.
 
 ``rnn_with_grm_amd.cuda_ops`` mirrors the reference's ``grm.core.cuda_ops``
-surface; ``rnn_with_grm_amd.capi`` binds the C ABI of libgrm_hip.so directly.
+surface; ``rnn_with_grm_amd.archive.DeviceSegmentArchive`` is a device ring
+drop-in for the reference's ``SegmentMemoryArchive``;
+``rnn_with_grm_amd.capi`` binds the C ABI of libgrm_hip.so directly.
 """
+
+from .archive import DeviceSegmentArchive, SegmentCheckpoint  # noqa: F401
 
 from .cuda_ops import (  # noqa: F401
     GrmExtensionUnavailable,
@@ -21,7 +25,9 @@ from .cuda_ops import (  # noqa: F401
 )
 
 __all__ = [
+    "DeviceSegmentArchive",
     "GrmExtensionUnavailable",
+    "SegmentCheckpoint",
     "cuda_apply_query",
     "cuda_batched_memory_gather",
     "cuda_chunk_update",
