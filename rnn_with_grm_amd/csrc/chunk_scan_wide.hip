@@ -152,7 +152,10 @@ __global__ __launch_bounds__(pass_threads(FULL), 1) void scan_wide_kernel(const 
   constexpr int KS = S::KS, VS = S::VS, PS = S::PS, KT = S::KT, NKK = S::NKK, KU = S::KU, VU = S::VU,
                 K_UNITS = S::K_UNITS, V_UNITS = S::V_UNITS, BUF = S::BUF;
   constexpr int ES = static_cast<int>(sizeof(raw));
-  constexpr int PF = 2;  // chunks in flight between global memory and LDS
+  // Chunks in flight between global memory and LDS: the full pass has no
+  // registers for more than two staging sets; the state pass stages K and V
+  // only and keeps four in flight.
+  constexpr int PF = FULL ? 2 : 4;
   static_assert(PF % 2 == 0, "staging sets pair with the two LDS buffers");
   using FullStep = std::integral_constant<bool, true>;
   using StateStep = std::integral_constant<bool, false>;
@@ -196,7 +199,10 @@ __global__ __launch_bounds__(pass_threads(FULL), 1) void scan_wide_kernel(const 
   const raw* values = static_cast<const raw*>(a.values) + b * T * dv;
   raw* hidden = a.hidden != nullptr ? static_cast<raw*>(a.hidden) + b * T * dv : nullptr;
 
-  for (int i = tid; i < PW_N; i += WNT) pw[i] = a.pw[i];
+  // The power table is the first load issued, so waiting for it later does
+  // not wait for the state and chunk loads issued after it.
+  static_assert(PW_N <= WNT, "one power per thread");
+  const float pw_first = tid < PW_N ? a.pw[tid] : 0.f;
 
   // ---- state: st[vb][kt], lane (g, n), register r = M[v][k] with
   //      v = v0 + 16 (VB w + vb) + n and k = 16kt + 4g + r.
@@ -220,11 +226,42 @@ __global__ __launch_bounds__(pass_threads(FULL), 1) void scan_wide_kernel(const 
     return make_rsrc(a.part_states + (b * (a.n_parts - 1) + q) * dv * dk, static_cast<uint32_t>(dv * dk * 4));
   };
   // st = pd^q_end M_0 + sum_{q < q_end} pd^{q_end-1-q} D_q, pd = decay^{part length}.
-  // Up to kCombineInPlaceParts - 1 contributions, all loads issued before any
-  // is used (one memory latency); D slots past q_end read as zero.
-  auto combine_start = [&](int q_end) {
-    constexpr int NQ = kCombineInPlaceParts - 1;
-    f32x4 d[NQ][VB][KT];
+  // issue_start() only issues the loads (M_0 into st, up to
+  // kCombineInPlaceParts - 1 contributions into d; D slots past q_end read as
+  // zero); finish_start() combines them once the chunk loads are out too.
+  // M_0 arrives as raw words (four fp32, or four 16-bit values in .xy) and is
+  // converted in finish_start(): one branch around all loads, so they issue
+  // back to back instead of each waiting for its conversion.
+  constexpr int NQ = FULL ? kCombineInPlaceParts - 1 : 1;
+  f32x4 d[NQ][VB][KT];
+  u32x4 m0raw[VB][KT];
+  auto issue_start = [&](int q_end, bool from_slot) {
+    if (from_slot) {  // the combine step wrote M_p into slot p - 1
+      const __amdgpu_buffer_rsrc_t rp = part_rsrc(q_end - 1);
+#pragma unroll
+      for (int vb = 0; vb < VB; ++vb)
+#pragma unroll
+        for (int kt = 0; kt < KT; ++kt) st[vb][kt] = ld_state4<F32>(rp, state_off(vb, kt), true);
+      return;
+    }
+    if (f32m) {
+#pragma unroll
+      for (int vb = 0; vb < VB; ++vb)
+#pragma unroll
+        for (int kt = 0; kt < KT; ++kt) {
+          const int off = state_off(vb, kt);
+          m0raw[vb][kt] = __builtin_amdgcn_raw_buffer_load_b128(rmem, off == kBufOOB ? kBufOOB : off * 4, 0, 0);
+        }
+    } else {
+#pragma unroll
+      for (int vb = 0; vb < VB; ++vb)
+#pragma unroll
+        for (int kt = 0; kt < KT; ++kt) {
+          const int off = state_off(vb, kt);
+          const u32x2 u = __builtin_amdgcn_raw_buffer_load_b64(rmem, off == kBufOOB ? kBufOOB : off * ES, 0, 0);
+          m0raw[vb][kt] = u32x4{u[0], u[1], 0u, 0u};
+        }
+    }
 #pragma unroll
     for (int q = 0; q < NQ; ++q) {
       const __amdgpu_buffer_rsrc_t rp = part_rsrc(q < q_end ? q : 0);
@@ -236,21 +273,52 @@ __global__ __launch_bounds__(pass_threads(FULL), 1) void scan_wide_kernel(const 
           d[q][vb][kt] = ld_state4<F32>(rp, q < q_end ? off : kBufOOB, true);
         }
     }
+  };
+  auto finish_start = [&](int q_end, bool from_slot) {
+    if (from_slot) return;
+    // Opaque register moves pin the first use of the loaded words here, after
+    // the barrier: otherwise the compiler hoists the sums above the chunk
+    // loads and every load waits for the state's latency first.
+#pragma unroll
+    for (int vb = 0; vb < VB; ++vb)
+#pragma unroll
+      for (int kt = 0; kt < KT; ++kt) {
+        asm volatile("" : "+v"(m0raw[vb][kt]));
+#pragma unroll
+        for (int q = 0; q < NQ; ++q) asm volatile("" : "+v"(d[q][vb][kt]));
+      }
     float m = 1.f;  // pd^(q_end - 1 - q) for q = q_end - 1, q_end - 2, ...
-    zero_state();
+    f32x4 acc[VB][KT];
+#pragma unroll
+    for (int vb = 0; vb < VB; ++vb)
+#pragma unroll
+      for (int kt = 0; kt < KT; ++kt) acc[vb][kt] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int q = NQ - 1; q >= 0; --q) {
       if (q >= q_end) continue;
 #pragma unroll
       for (int vb = 0; vb < VB; ++vb)
 #pragma unroll
-        for (int kt = 0; kt < KT; ++kt) st[vb][kt] += m * d[q][vb][kt];
+        for (int kt = 0; kt < KT; ++kt) acc[vb][kt] += m * d[q][vb][kt];
       m *= a.part_decay;
     }
 #pragma unroll
     for (int vb = 0; vb < VB; ++vb)
 #pragma unroll
-      for (int kt = 0; kt < KT; ++kt) st[vb][kt] += m * ld_state4<E>(rmem, state_off(vb, kt), f32m);
+      for (int kt = 0; kt < KT; ++kt) {
+        const u32x4 u = m0raw[vb][kt];
+        f32x4 m0;
+        if (f32m) {
+#pragma unroll
+          for (int i = 0; i < 4; ++i) m0[i] = __uint_as_float(u[i]);
+        } else {
+          m0[0] = ET<E>::to_f(static_cast<raw>(u[0] & 0xffffu));
+          m0[1] = ET<E>::to_f(static_cast<raw>(u[0] >> 16));
+          m0[2] = ET<E>::to_f(static_cast<raw>(u[1] & 0xffffu));
+          m0[3] = ET<E>::to_f(static_cast<raw>(u[1] >> 16));
+        }
+        st[vb][kt] = acc[vb][kt] + m * m0;
+      }
   };
   auto store_state = [&](__amdgpu_buffer_rsrc_t r) {
 #pragma unroll
@@ -492,16 +560,39 @@ __global__ __launch_bounds__(pass_threads(FULL), 1) void scan_wide_kernel(const 
     }
   };
 
-  // Scans chunks [cb, ce) from the state in st.  init() may set it; its loads
-  // go out first, so the combine arithmetic runs while the chunk loads land.
-  auto scan = [&](auto full, int cb, int ce, auto init) {
+  // Per-token weights of a full chunk, causal coefficients and query decays,
+  // from the power table in LDS.
+  auto prepare_weights = [&]() {
+    set_weights(CT);
+    if constexpr (FULL) {
+#pragma unroll
+      for (int jj = 0; jj < 2; ++jj) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int j = 32 * j_half + 16 * jj + 4 * g + r;
+          coef[jj][r] = (j <= i_loc) ? a.c * pw[max(i_loc - j, 0)] : 0.f;
+        }
+      }
+#pragma unroll
+      for (int ib = 0; ib < 4; ++ib) s_start[ib] = pw[16 * ib + n + 1];
+    }
+  };
+
+  // Scans chunks [cb, ce) from the state in st.  issue() sends the starting
+  // state's loads, then the first chunks' loads go out; only then does the
+  // workgroup wait (for the power table, the oldest load) and finish() combine
+  // the state while the chunks land.
+  auto scan = [&](auto full, int cb, int ce, auto issue, auto finish) {
     constexpr bool F = decltype(full)::value;
     ce_cur = ce;
     Stage sg[PF];
-    init();
+    issue();
 #pragma unroll
     for (int i = 0; i < PF; ++i) load_chunk(cb + i, sg[i], full);
-    __syncthreads();  // LDS buffers free, pw visible
+    if (tid < PW_N) pw[tid] = pw_first;
+    __syncthreads();  // pw visible
+    prepare_weights();
+    finish();
     store_chunk(0, sg[0], full);
     if (F) snap_phase = a.snap_every > 0 ? (cb + 1) % a.snap_every : 1;
     __syncthreads();
@@ -516,40 +607,16 @@ __global__ __launch_bounds__(pass_threads(FULL), 1) void scan_wide_kernel(const 
       flush_out(ce - 1);
     }
   };
-  auto no_init = []() {};
-
-  __syncthreads();  // pw visible
-  set_weights(CT);
-  if constexpr (FULL) {
-#pragma unroll
-    for (int jj = 0; jj < 2; ++jj) {
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int j = 32 * j_half + 16 * jj + 4 * g + r;
-        coef[jj][r] = (j <= i_loc) ? a.c * pw[max(i_loc - j, 0)] : 0.f;
-      }
-    }
-#pragma unroll
-    for (int ib = 0; ib < 4; ++ib) s_start[ib] = pw[16 * ib + n + 1];
-  }
 
   if constexpr (!FULL) {
     zero_state();
-    scan(StateStep{}, c_begin, c_end, no_init);
+    scan(StateStep{}, c_begin, c_end, []() {}, []() {});
     store_state(part_rsrc(part));
     return;
   } else {
-    scan(FullStep{}, c_begin, c_end, [&]() {
-      if (a.part_starts && part > 0) {
-        const __amdgpu_buffer_rsrc_t rp = part_rsrc(part - 1);
-#pragma unroll
-        for (int vb = 0; vb < VB; ++vb)
-#pragma unroll
-          for (int kt = 0; kt < KT; ++kt) st[vb][kt] = ld_state4<F32>(rp, state_off(vb, kt), true);
-      } else {
-        combine_start(part);
-      }
-    });
+    const bool from_slot = a.part_starts && part > 0;
+    scan(FullStep{}, c_begin, c_end, [&]() { issue_start(part, from_slot); },
+         [&]() { finish_start(part, from_slot); });
     if (a.memory_out == nullptr || part != a.n_parts - 1) return;
     const __amdgpu_buffer_rsrc_t ro = make_rsrc(static_cast<unsigned char*>(a.memory_out) + b * dv * dk * mem_b,
                                                 static_cast<uint32_t>(dv * dk * mem_b));
