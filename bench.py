@@ -321,6 +321,45 @@ def bench_c4_archive(torch, dev, steps, warmup):
     return {"reference_style_ms": statistics.mean(r_per) * 1e3, "device_archive_ms": statistics.mean(d_per) * 1e3}
 
 
+class SegmentMemoryLM:
+    """Config 4's language model: Embedding(32000, 512) -> HierarchicalSegmentMemoryModel
+    (4 layers, hidden 512, d_k 64, 64-token segments, capacity 64, top-8, float16 archive)
+    -> Linear(512, 32000), the composition of the reference's SegmentMemoryLanguageModel
+    (grm/utils/train.py:192-229).  Random init, bfloat16 weights."""
+
+    def __init__(self, torch, dev, vocab=32000, dim=512, layers=4, dk=64, seg=64, top_k=8):
+        from rnn_with_grm_amd.segment_model import HierarchicalSegmentMemoryModel
+
+        torch.manual_seed(0)
+        self.embedding = torch.nn.Embedding(vocab, dim)
+        self.grm = HierarchicalSegmentMemoryModel(dim, dim, dim, num_layers=layers, segment_length=seg,
+                                                  memory_capacity_segments=64, retrieval_top_k=top_k,
+                                                  memory_key_dim=dk, dropout=0.0, recomputation_ratio=0.0)
+        self.head = torch.nn.Linear(dim, vocab)
+        for m in (self.embedding, self.grm, self.head):
+            m.to(device=dev, dtype=torch.bfloat16).eval()
+
+    def __call__(self, ids):
+        out, _, _, _ = self.grm(self.embedding(ids), reset_memory=True)
+        return self.head(out)
+
+
+def bench_c4_model(torch, dev, steps, warmup):
+    """Config 4 end to end: one forward over 4 x 8192 token ids, every layer as whole-sequence
+    launches (scan, segment routing, gather_apply, fusion), the archive reset each step."""
+    B, T = 4, 8192
+    lm = SegmentMemoryLM(torch, dev)
+    g = torch.Generator().manual_seed(7)
+    ids = torch.randint(0, 32000, (B, T), generator=g).to(dev)
+    stream = torch.cuda.current_stream(dev)
+    with torch.no_grad():
+        logits = lm(ids)
+        assert logits.shape == (B, T, 32000) and torch.isfinite(logits.float()).all(), "c4 forward not finite"
+        wall, per = timed_launches(torch, lambda: lm(ids), max(3, min(steps, 10)), max(1, min(warmup, 3)), stream)
+    ms = statistics.mean(per) * 1e3
+    return {"ms": ms, "tokens": B * T}
+
+
 def cpu_baseline(torch, budget_s: float = 20.0):
     """The torch-CPU port of the reference's CPU path on config 2 (full shape)."""
     from oracle import torch_port
@@ -352,10 +391,11 @@ def main() -> int:
     ap.add_argument("--no-gather", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--c2-only", action="store_true", help="only the headline kernel (quick sweeps)")
+    ap.add_argument("--c4-only", action="store_true", help="the headline kernel and the config-4 model forward")
     ap.add_argument("--probe", action="store_true",
                     help="counter runs: a 256 MiB device copy (calibration) then config-2 launches only")
     a = ap.parse_args()
-    if a.c2_only or a.probe:
+    if a.c2_only or a.probe or a.c4_only:
         a.no_gather = a.no_cpu = True
     if a.gpus != 1:
         print(f"bench.py measures one GPU only; --gpus {a.gpus} is not supported in this build "
@@ -456,6 +496,16 @@ def main() -> int:
             "speedup": round(c4["reference_style_ms"] / c4["device_archive_ms"], 2)}
         log(f"c4 segment retrieval: reference style {c4['reference_style_ms']:.3f} ms, device archive "
             f"{c4['device_archive_ms']:.3f} ms")
+
+    if not a.no_gather or a.c4_only:
+        log("config 4 end-to-end forward (4 layers, 4 x 8192 tokens)")
+        m4 = bench_c4_model(torch, dev, a.steps, a.warmup)
+        secondary["c4_model_forward"] = {
+            "what": "config 4 LM forward, bf16 weights, random init: Embedding -> 4 x SegmentRecurrentMemoryLayer "
+                    "(hidden 512, d_k 64, segment 64, capacity 64, top-8, float16 archive) -> Linear(512, 32000); "
+                    "whole-sequence launches per layer, archive reset each forward",
+            "ms": round(m4["ms"], 3), "tokens/s": round(m4["tokens"] / m4["ms"] * 1e3)}
+        log(f"c4 forward: {m4['ms']:.2f} ms, {m4['tokens'] / m4['ms'] * 1e3:.3e} tokens/s")
 
     cpu = None
     if not a.no_cpu:

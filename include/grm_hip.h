@@ -185,6 +185,27 @@ int grm_hip_topk_route(const void* queries, const void* keys, int64_t* topk_indi
                        float temperature, void* stream);
 
 /*
+ * Segment routing over a growing archive, every segment of a sequence in one
+ * call (the whole-sequence form of the per-segment routing above).
+ * Query row t belongs to segment s = t / segment_len and is routed over the
+ * keys [lo, hi) with hi = base + s and lo = max(0, hi - capacity): the
+ * archive of at most `capacity` summaries as it stood when segment s ran,
+ * `base` entries having been archived before this sequence.  Within a window
+ * of n keys the rule is grm_hip_topk_route's: n > top_k selects the top_k best
+ * (descending, ties to the lower index); n <= top_k takes all n in index
+ * order and leaves slots n .. top_k-1 empty (index -1, score -inf, gate 0).
+ * Indices are absolute key positions (key j of the window is index lo + j).
+ * Outputs are [batch, n_query, top_k].
+ * Replaces the per-segment routing calls of the reference's segment loop
+ *   (grm/core/paper_grm.py:702-728 -> _route_chunk, :566-589) with one launch.
+ * Limits: 1 <= top_k <= 32; base + (n_query - 1) / segment_len <= n_keys.
+ */
+int grm_hip_segment_route(const void* queries, const void* keys, int64_t* topk_indices,
+                          float* topk_scores, float* gates, int64_t batch, int64_t n_query,
+                          int64_t n_keys, int64_t dim, int dtype, int64_t top_k, int64_t segment_len,
+                          int64_t base, int64_t capacity, float scale, float temperature, void* stream);
+
+/*
  * Residual fusion of the online state with gated retrieved states:
  *   x = h_online[n] + sum_r gates[n, r] * retrieved[n, r]
  *   out[n] = layer_norm(x) * weight + bias      (ln_weight == NULL: no LayerNorm)

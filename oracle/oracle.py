@@ -153,6 +153,32 @@ def topk_route(queries, keys, top_k: int, scale: float, temperature: float = 1.0
     return gt, idx, sc
 
 
+def segment_route(queries, keys, top_k: int, segment_len: int, base: int, capacity: int, scale: float,
+                  temperature: float = 1.0):
+    """Routing of each segment over the archive of its moment, as the
+    reference's segment loop does it (grm/core/paper_grm.py:702-728 calling
+    _route_chunk, :566-589, with get_segment_summaries, :148-160): the rows of
+    segment s see keys [lo, hi), hi = base + s, lo = max(0, hi - capacity), and
+    are routed by topk_route over exactly those keys.  Indices are returned as
+    absolute key positions; slots past a short window hold -1 / -inf / 0."""
+    q = np.asarray(queries, dtype=np.float32)
+    kk = np.asarray(keys, dtype=np.float32)
+    B, Q, _ = q.shape
+    idx = np.full((B, Q, top_k), -1, dtype=np.int64)
+    sc = np.full((B, Q, top_k), -np.inf, dtype=np.float32)
+    gt = np.zeros((B, Q, top_k), dtype=np.float64)
+    for t0 in range(0, Q, segment_len):
+        hi = min(kk.shape[1], base + t0 // segment_len)
+        lo = max(0, hi - capacity)
+        if hi <= lo:
+            continue
+        sl = slice(t0, min(Q, t0 + segment_len))
+        g, i, s_ = topk_route(q[:, sl], kk[:, lo:hi], top_k, scale, temperature)
+        n = g.shape[-1]
+        gt[:, sl, :n], idx[:, sl, :n], sc[:, sl, :n] = g, i + lo, s_
+    return gt, idx, sc
+
+
 def fuse_residual(h, retrieved, gates, weight=None, bias=None, eps: float = 1e-5) -> np.ndarray:
     hh, rr, gg = _d(h), _d(retrieved), _d(gates)
     N, H = hh.shape

@@ -187,9 +187,12 @@ class DeviceSegmentArchive(nn.Module):
                                                   checkpoint.memory_start.detach().to(self.memory_storage_dtype).clone()))
         self.total_pushed.add_(1)
 
-    def push_segments(self, memories: Tensor, summaries: Tensor, checkpoints=None) -> None:
+    def push_segments(self, memories: Tensor, summaries: Tensor, checkpoints=None, owned: bool = False) -> None:
         """n segments at once (the whole-sequence path): memories [B, n, d_v, d_k],
-        summaries [B, n, D], oldest first; equal to n calls of push."""
+        summaries [B, n, D], oldest first; equal to n calls of push.  With
+        owned=True the checkpoints' tensors are fresh copies the archive may keep
+        as they are (memory_start already in the storage dtype), so no per-segment
+        copies are made."""
         n = memories.size(1)
         if n == 0:
             return
@@ -197,8 +200,11 @@ class DeviceSegmentArchive(nn.Module):
         ring.allocate(memories[:, 0], summaries[:, 0], self.memory_storage_dtype)
         ring.write(memories.detach(), summaries.detach())
         for c in checkpoints or []:
-            ring.checkpoints.append(SegmentCheckpoint(c.inputs.detach().clone(),
-                                                      c.memory_start.detach().to(self.memory_storage_dtype).clone()))
+            if owned:
+                ring.checkpoints.append(SegmentCheckpoint(c.inputs, c.memory_start))
+            else:
+                ring.checkpoints.append(SegmentCheckpoint(
+                    c.inputs.detach().clone(), c.memory_start.detach().to(self.memory_storage_dtype).clone()))
         self.total_pushed.add_(n)
 
     # ------------------------------------------------------------- reads

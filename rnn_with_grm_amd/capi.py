@@ -39,6 +39,8 @@ SIGNATURES = {
     "grm_hip_gather_apply_workspace": (_I, [_I, _I, _I]),
     "grm_hip_gather_apply": (_C, [_P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _C, _C, _C, _P, _P]),
     "grm_hip_topk_route": (_C, [_P, _P, _P, _P, _P, _I, _I, _I, _I, _C, _I, ctypes.c_float, ctypes.c_float, _P]),
+    "grm_hip_segment_route": (_C, [_P, _P, _P, _P, _P, _I, _I, _I, _I, _C, _I, _I, _I, _I, ctypes.c_float,
+                                   ctypes.c_float, _P]),
     "grm_hip_fuse_residual": (_C, [_P, _P, _P, _P, _P, _P, _I, _I, _I, _C, ctypes.c_float, _P]),
 }
 
@@ -195,6 +197,20 @@ def topk_route(queries, keys, top_k: int, scale: float, temperature: float = 1.0
                                    dtype_code(queries.dtype), int(top_k), float(scale), float(temperature),
                                    _stream(queries))
     _check(rc, "grm_hip_topk_route")
+    return gt, idx, sc
+
+
+def segment_route(queries, keys, top_k: int, segment_len: int, base: int, capacity: int, scale: float,
+                  temperature: float = 1.0):
+    B, Q, D = queries.shape
+    S = keys.shape[1]
+    idx = torch.empty((B, Q, top_k), dtype=torch.int64, device=queries.device)
+    sc = torch.empty((B, Q, top_k), dtype=torch.float32, device=queries.device)
+    gt = torch.empty((B, Q, top_k), dtype=torch.float32, device=queries.device)
+    rc = load().grm_hip_segment_route(_ptr(queries), _ptr(keys), _ptr(idx), _ptr(sc), _ptr(gt), B, Q, S, D,
+                                      dtype_code(queries.dtype), int(top_k), int(segment_len), int(base),
+                                      int(capacity), float(scale), float(temperature), _stream(queries))
+    _check(rc, "grm_hip_segment_route")
     return gt, idx, sc
 
 

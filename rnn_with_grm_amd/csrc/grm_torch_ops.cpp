@@ -2,10 +2,12 @@
 //
 // The five schemas are the reference's, character for character
 // (reference grm/csrc/bindings.cpp:5-11), so grm.core.cuda_ops and every model
-// above it bind to this library unchanged.  Four more ops live in the same
+// above it bind to this library unchanged.  Five more ops live in the same
 // namespace: segment_scan_forward (whole-sequence update with per-segment
-// state snapshots), topk_route (score -> top-k -> softmax), fuse_residual and
-// gather_apply (gather + query application without materialising the states).
+// state snapshots), topk_route (score -> top-k -> softmax), segment_route (the
+// same routing for every segment of a sequence against the archive as it
+// grows), fuse_residual and gather_apply (gather + query application without
+// materialising the states).
 //
 // CUDA-key kernels (HIP devices dispatch on the CUDA key in PyTorch-ROCm)
 // check the inputs, allocate outputs with ATen on the input's device and call
@@ -287,6 +289,75 @@ std::tuple<Tensor, Tensor, Tensor> topk_route_cpu(const Tensor& queries, const T
         ip[r * k + m] = order[m];
         sp[r * k + m] = all[order[m]];
         gp[r * k + m] = std::exp(all[order[m]] * inv_t - mx) / sum;
+      }
+    }
+  });
+  return {gt, idx, sc};
+}
+
+// Segment routing over the archive as it grows (grm_hip_segment_route): row t
+// of segment s = t / segment_len is routed over keys [lo, hi), hi = base + s,
+// lo = max(0, hi - capacity), with topk_route's rule inside the window.
+void check_segment_route(const Tensor& queries, const Tensor& keys, int64_t top_k, int64_t segment_len,
+                         int64_t base, int64_t capacity, double temperature) {
+  TORCH_CHECK(queries.dim() == 3 && keys.dim() == 3, "segment_route: queries [B, Q, D], keys [B, S, D]");
+  TORCH_CHECK(queries.size(0) == keys.size(0) && queries.size(2) == keys.size(2),
+              "segment_route: batch/dim mismatch");
+  TORCH_CHECK(top_k >= 1 && top_k <= 32, "segment_route: top_k must be in [1, 32]");
+  TORCH_CHECK(segment_len >= 1 && base >= 0 && capacity >= 1,
+              "segment_route: segment_len >= 1, base >= 0 and capacity >= 1 required");
+  TORCH_CHECK(temperature > 0, "segment_route: temperature must be > 0");
+  TORCH_CHECK(queries.size(1) == 0 || base + (queries.size(1) - 1) / segment_len <= keys.size(1),
+              "segment_route: the last segment's window ends past the keys");
+}
+
+std::tuple<Tensor, Tensor, Tensor> segment_route_cpu(const Tensor& queries, const Tensor& keys, int64_t top_k,
+                                                     int64_t segment_len, int64_t base, int64_t capacity,
+                                                     double scale, double temperature) {
+  check_segment_route(queries, keys, top_k, segment_len, base, capacity, temperature);
+  const int64_t B = queries.size(0), Q = queries.size(1), S = keys.size(1), D = queries.size(2);
+  const int64_t k = top_k;
+  Tensor qf = queries.to(at::kFloat).contiguous(), kf = keys.to(at::kFloat).contiguous();
+  auto fopt = queries.options().dtype(at::kFloat);
+  Tensor idx = at::empty({B, Q, k}, queries.options().dtype(at::kLong));
+  Tensor sc = at::empty({B, Q, k}, fopt), gt = at::empty({B, Q, k}, fopt);
+  const float* qp = qf.data_ptr<float>();
+  const float* kp = kf.data_ptr<float>();
+  int64_t* ip = idx.data_ptr<int64_t>();
+  float* sp = sc.data_ptr<float>();
+  float* gp = gt.data_ptr<float>();
+  const float fs = static_cast<float>(scale), inv_t = 1.0f / static_cast<float>(temperature);
+  at::parallel_for(0, B * Q, 1, [&](int64_t r0, int64_t r1) {
+    std::vector<float> all;
+    std::vector<int64_t> order;
+    for (int64_t r = r0; r < r1; ++r) {
+      const int64_t b = r / Q, t = r % Q;
+      const int64_t hi = std::min(S, base + t / segment_len);
+      const int64_t lo = std::max<int64_t>(0, hi - capacity);
+      const int64_t n = hi - lo;
+      all.assign(n, 0.f);
+      order.resize(n);
+      const float* qr = qp + r * D;
+      for (int64_t j = 0; j < n; ++j) {
+        const float* kr = kp + (b * S + lo + j) * D;
+        float acc = 0.f;
+        for (int64_t d = 0; d < D; ++d) acc = std::fma(qr[d], kr[d], acc);
+        all[j] = acc * fs;
+        order[j] = j;
+      }
+      const int64_t kk = std::min(k, n);
+      if (kk < n) {
+        std::stable_sort(order.begin(), order.end(), [&](int64_t x, int64_t y) { return all[x] > all[y]; });
+      }
+      float mx = -INFINITY;
+      for (int64_t m = 0; m < kk; ++m) mx = std::max(mx, all[order[m]] * inv_t);
+      float sum = 0.f;
+      for (int64_t m = 0; m < kk; ++m) sum += std::exp(all[order[m]] * inv_t - mx);
+      for (int64_t m = 0; m < k; ++m) {
+        const bool filled = m < kk;
+        ip[r * k + m] = filled ? lo + order[m] : -1;
+        sp[r * k + m] = filled ? all[order[m]] : -INFINITY;
+        gp[r * k + m] = filled ? std::exp(all[order[m]] * inv_t - mx) / sum : 0.f;
       }
     }
   });
@@ -591,6 +662,33 @@ std::tuple<Tensor, Tensor, Tensor> topk_route_hip(const Tensor& queries, const T
   return {gt, idx, sc};
 }
 
+std::tuple<Tensor, Tensor, Tensor> segment_route_hip(const Tensor& queries, const Tensor& keys, int64_t top_k,
+                                                     int64_t segment_len, int64_t base, int64_t capacity,
+                                                     double scale, double temperature) {
+  check_segment_route(queries, keys, top_k, segment_len, base, capacity, temperature);
+  const int dt = dtype_code(queries.scalar_type());
+  if (!same_cuda_device({&queries, &keys}) || dt < 0 || keys.scalar_type() != queries.scalar_type()) {
+    if (queries.is_cuda()) g_generic_calls.fetch_add(1);
+    auto r = segment_route_cpu(queries.cpu(), keys.cpu(), top_k, segment_len, base, capacity, scale, temperature);
+    return {std::get<0>(r).to(queries.device()), std::get<1>(r).to(queries.device()),
+            std::get<2>(r).to(queries.device())};
+  }
+  c10::OptionalDeviceGuard guard(queries.device());
+  Tensor q = queries.contiguous(), kk = keys.contiguous();
+  const int64_t B = q.size(0), Q = q.size(1), S = kk.size(1), D = q.size(2);
+  Tensor idx = at::empty({B, Q, top_k}, q.options().dtype(at::kLong));
+  Tensor sc = at::empty({B, Q, top_k}, q.options().dtype(at::kFloat));
+  Tensor gt = at::empty({B, Q, top_k}, q.options().dtype(at::kFloat));
+  if (Q > 0 && B > 0) {
+    check_rc(grm_hip_segment_route(q.data_ptr(), S > 0 ? kk.data_ptr() : nullptr, idx.data_ptr<int64_t>(),
+                                   sc.data_ptr<float>(), gt.data_ptr<float>(), B, Q, S, D, dt, top_k,
+                                   segment_len, base, capacity, static_cast<float>(scale),
+                                   static_cast<float>(temperature), current_stream(q)),
+             "segment_route");
+  }
+  return {gt, idx, sc};
+}
+
 Tensor fuse_residual_hip(const Tensor& h, const Tensor& retrieved, const Tensor& gates,
                          const c10::optional<Tensor>& weight, const c10::optional<Tensor>& bias,
                          double eps) {
@@ -648,6 +746,7 @@ TORCH_LIBRARY(grm_cuda, m) {
   m.def("topk_route(Tensor queries, Tensor keys, int top_k, float scale, float temperature) -> (Tensor gates, Tensor indices, Tensor scores)");
   m.def("fuse_residual(Tensor h_online, Tensor retrieved, Tensor gates, Tensor? weight, Tensor? bias, float eps) -> Tensor");
   m.def("gather_apply(Tensor memories, Tensor indices, Tensor queries, ScalarType? dtype=None) -> Tensor");
+  m.def("segment_route(Tensor queries, Tensor keys, int top_k, int segment_len, int base, int capacity, float scale, float temperature) -> (Tensor gates, Tensor indices, Tensor scores)");
 }
 
 TORCH_LIBRARY_IMPL(grm_cuda, CPU, m) {
@@ -660,6 +759,7 @@ TORCH_LIBRARY_IMPL(grm_cuda, CPU, m) {
   m.impl("topk_route", grm::topk_route_cpu);
   m.impl("fuse_residual", grm::fuse_residual_generic);
   m.impl("gather_apply", grm::gather_apply_generic);
+  m.impl("segment_route", grm::segment_route_cpu);
 }
 
 TORCH_LIBRARY_IMPL(grm_cuda, CUDA, m) {
@@ -672,6 +772,7 @@ TORCH_LIBRARY_IMPL(grm_cuda, CUDA, m) {
   m.impl("topk_route", grm::topk_route_hip);
   m.impl("fuse_residual", grm::fuse_residual_hip);
   m.impl("gather_apply", grm::gather_apply_hip);
+  m.impl("segment_route", grm::segment_route_hip);
 }
 
 PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {

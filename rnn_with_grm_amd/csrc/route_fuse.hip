@@ -43,11 +43,17 @@ struct RouteArgs {
   int64_t n_query;
   int64_t n_keys;
   int dim;
-  int k;        // selected per query (k <= n_keys)
+  int k;        // selected per query (k <= n_keys; the output width when seg_len > 0)
   int natural;  // k == n_keys: index order, no selection
   int vec;      // 16-byte loads of query rows legal
   float scale;
   float inv_temp;
+  // Segment windows (seg_len > 0): query row t belongs to segment
+  // s = t / seg_len and sees the keys [lo, hi), hi = base + s,
+  // lo = max(0, hi - cap): the archive as it stood when segment s ran.
+  int seg_len;
+  int64_t base;
+  int64_t cap;
 };
 
 template <class E, int KMAX>
@@ -66,6 +72,23 @@ __global__ __launch_bounds__(RT) void route_kernel(const RouteArgs a) {
   const raw* kb = static_cast<const raw*>(a.keys) + b * S * D;
   const int64_t obase = (b * a.n_query + qi) * a.k;
 
+  // Keys this row may select, [lo, hi), and the keys the workgroup streams,
+  // [blk_lo, blk_hi) (windows only move forward with the row index).  A row
+  // whose window holds at most k keys takes all of them in index order.
+  int64_t lo = 0, hi = S, blk_lo = 0, blk_hi = S;
+  bool row_nat = false;
+  if (a.seg_len > 0) {
+    const int64_t r0 = static_cast<int64_t>(blockIdx.x) * RT;
+    const int64_t r1 = min(a.n_query, r0 + RT) - 1;
+    auto win_hi = [&](int64_t r) { return min(S, a.base + r / a.seg_len); };
+    auto win_lo = [&](int64_t h) { return h > a.cap ? h - a.cap : int64_t{0}; };
+    blk_hi = win_hi(r1);
+    blk_lo = win_lo(win_hi(r0));
+    hi = win_hi(active ? qi : r0);
+    lo = win_lo(hi);
+    row_nat = hi - lo <= a.k;
+  }
+
   // Running top-k, descending.  Slots at or past k only receive entries
   // shifted out of the top k; the k-th best score is kept in thr for the
   // cheap reject test, so a candidate enters the network only if it belongs
@@ -80,7 +103,7 @@ __global__ __launch_bounds__(RT) void route_kernel(const RouteArgs a) {
   }
   float thr = -INFINITY;
 
-  for (int64_t s0 = 0; s0 < S; s0 += SC) {
+  for (int64_t s0 = blk_lo; s0 < blk_hi; s0 += SC) {
     float acc[SC];
 #pragma unroll
     for (int s = 0; s < SC; ++s) acc[s] = 0.f;
@@ -89,7 +112,7 @@ __global__ __launch_bounds__(RT) void route_kernel(const RouteArgs a) {
       __syncthreads();
       for (int e = threadIdx.x; e < SC * DT; e += RT) {
         const int s = e / DT, d = e % DT;
-        ktile[e] = (s0 + s < S && d < dl) ? kb[(s0 + s) * D + d0 + d] : static_cast<raw>(0);
+        ktile[e] = (s0 + s < blk_hi && d < dl) ? kb[(s0 + s) * D + d0 + d] : static_cast<raw>(0);
       }
       __syncthreads();
       if (active) {
@@ -126,7 +149,7 @@ __global__ __launch_bounds__(RT) void route_kernel(const RouteArgs a) {
       }
     }
     if (active) {
-      const int ns = static_cast<int>(min(static_cast<int64_t>(SC), S - s0));
+      const int ns = static_cast<int>(min(static_cast<int64_t>(SC), blk_hi - s0));
       if (a.natural) {
 #pragma unroll
         for (int s = 0; s < SC; ++s) {
@@ -143,6 +166,21 @@ __global__ __launch_bounds__(RT) void route_kernel(const RouteArgs a) {
 #pragma unroll 1
         for (int s = 0; s < ns; ++s) {
           const float v = sbuf[s * RT + threadIdx.x];
+          const int64_t key = s0 + s;
+          if (a.seg_len > 0) {
+            if (key < lo || key >= hi) continue;
+            if (row_nat) {  // index order: slot key - lo
+              const int slot = static_cast<int>(key - lo);
+#pragma unroll
+              for (int m = 0; m < KMAX; ++m) {
+                if (m == slot) {
+                  top_s[m] = v;
+                  top_i[m] = static_cast<int>(key);
+                }
+              }
+              continue;
+            }
+          }
           if (v > thr) {
             // The new entry lands after every kept entry with an equal score
             // (those have lower indices); from there on every entry shifts
@@ -179,6 +217,30 @@ __global__ __launch_bounds__(RT) void route_kernel(const RouteArgs a) {
       a.gates[obase + s] = expf(a.scores[obase + s] * a.inv_temp - mx) / sum;
     return;
   }
+  if (row_nat) {
+    // Window of n <= k keys in index order; slots n .. k-1 stay empty
+    // (index -1, score -inf, gate 0).
+    const int n = static_cast<int>(hi - lo);
+    float mx = -INFINITY;
+#pragma unroll
+    for (int m = 0; m < KMAX; ++m) mx = (m < n) ? fmaxf(mx, top_s[m] * a.inv_temp) : mx;
+    float e[KMAX];
+    float sum = 0.f;
+#pragma unroll
+    for (int m = 0; m < KMAX; ++m) {
+      e[m] = (m < n) ? expf(top_s[m] * a.inv_temp - mx) : 0.f;
+      sum += e[m];
+    }
+#pragma unroll
+    for (int m = 0; m < KMAX; ++m) {
+      if (m < k) {
+        a.idx[obase + m] = (m < n) ? top_i[m] : -1;
+        a.scores[obase + m] = (m < n) ? top_s[m] : -INFINITY;
+        a.gates[obase + m] = (m < n) ? e[m] / sum : 0.f;
+      }
+    }
+    return;
+  }
   const float mx = top_s[0] * a.inv_temp;
   float e[KMAX];
   float sum = 0.f;
@@ -212,6 +274,164 @@ int launch_route(const RouteArgs& a, int64_t batch, hipStream_t s) {
 }
 
 // ---------------------------------------------------------------------------
+// Segment routing with short windows (grm_hip_segment_route when every
+// workgroup's key range fits WR_MAXK keys).  Same result as route_kernel's
+// window mode, bit for bit: every score is the same fp32 FMA chain.
+//
+// A workgroup owns WR_ROWS query rows with WR_LANES lanes per row; lane l of a
+// row computes the chains of keys l, l + WR_LANES, ... of the workgroup's key
+// range, so a row's keys are scored in parallel instead of by one thread.  Key
+// and query slices are staged in LDS.  The top k then follow from ranks: a
+// key's rank is the number of window keys that beat it (greater score, or an
+// equal score and a lower index), so slot = rank for every key with rank < k,
+// the order "score descending, ties to the lower index" with no serial
+// insertion.  Keys whose score is NaN or -inf are never selected, as in
+// route_kernel.
+constexpr int WR_ROWS = 32;
+constexpr int WR_LANES = 8;
+constexpr int WR_THREADS = WR_ROWS * WR_LANES;
+constexpr int WR_KPT = 16;                    // keys per lane per key chunk
+constexpr int WR_KC = WR_LANES * WR_KPT;      // keys per chunk
+constexpr int WR_MAXK = WR_KC;                // keys per workgroup (score buffer)
+constexpr int WR_DT = 64;                     // dims per staged slice
+
+template <class E>
+__global__ __launch_bounds__(WR_THREADS) void route_window_kernel(const RouteArgs a) {
+  using raw = typename ET<E>::raw;
+  constexpr int V = 16 / sizeof(raw);         // elements per 16-byte read
+  // Row stride WR_DT + 16 bytes: the 8 key rows a wave reads at one offset
+  // start in 8 distinct 4-bank groups.
+  constexpr int RS = WR_DT + V;
+  __shared__ __align__(16) raw ktile[WR_KC * RS];
+  __shared__ __align__(16) raw qtile[WR_ROWS * RS];
+  __shared__ float sc[WR_ROWS][WR_MAXK + 1];
+  __shared__ float out_s[WR_ROWS][32];
+  __shared__ int out_i[WR_ROWS][32];
+
+  const int tid = threadIdx.x;
+  const int lane = tid % WR_LANES;
+  const int rl = tid / WR_LANES;
+  const int64_t b = blockIdx.y;
+  const int64_t S = a.n_keys;
+  const int D = a.dim;
+  const int k = a.k;
+  const int64_t r0 = static_cast<int64_t>(blockIdx.x) * WR_ROWS;
+  const int64_t rlast = min(a.n_query, r0 + WR_ROWS) - 1;
+  const int64_t row = r0 + rl;
+  const bool active = row < a.n_query;
+  auto win_hi = [&](int64_t r) { return min(S, a.base + r / a.seg_len); };
+  auto win_lo = [&](int64_t h) { return h > a.cap ? h - a.cap : int64_t{0}; };
+  const int64_t blk_hi = win_hi(rlast);
+  const int64_t blk_lo = win_lo(win_hi(r0));
+  const int nk = static_cast<int>(blk_hi - blk_lo);  // <= WR_MAXK, checked on the host
+  const int64_t hi = win_hi(active ? row : r0);
+  const int64_t lo = win_lo(hi);
+  const bool row_nat = hi - lo <= k;
+
+  const raw* qb = static_cast<const raw*>(a.q) + (b * a.n_query + r0) * D;
+  const raw* kb = static_cast<const raw*>(a.keys) + (b * S + blk_lo) * D;
+
+  for (int m = tid; m < WR_ROWS * 32; m += WR_THREADS) {
+    out_s[m / 32][m % 32] = -INFINITY;
+    out_i[m / 32][m % 32] = -1;
+  }
+  for (int kc0 = 0; kc0 < nk; kc0 += WR_KC) {
+    float acc[WR_KPT];
+#pragma unroll
+    for (int j = 0; j < WR_KPT; ++j) acc[j] = 0.f;
+    for (int d0 = 0; d0 < D; d0 += WR_DT) {
+      __syncthreads();  // previous slice consumed
+      // stage WR_KC key rows and WR_ROWS query rows of dims [d0, d0 + WR_DT)
+      for (int u = tid; u < (WR_KC + WR_ROWS) * (WR_DT / V); u += WR_THREADS) {
+        const int r = u / (WR_DT / V);
+        const int c = (u % (WR_DT / V)) * V;
+        uint4 v = make_uint4(0, 0, 0, 0);
+        if (r < WR_KC) {
+          if (kc0 + r < nk && d0 + c < D) v = *reinterpret_cast<const uint4*>(kb + (kc0 + r) * static_cast<int64_t>(D) + d0 + c);
+          *reinterpret_cast<uint4*>(ktile + r * RS + c) = v;
+        } else {
+          const int qr = r - WR_KC;
+          if (r0 + qr < a.n_query && d0 + c < D) v = *reinterpret_cast<const uint4*>(qb + qr * static_cast<int64_t>(D) + d0 + c);
+          *reinterpret_cast<uint4*>(qtile + qr * RS + c) = v;
+        }
+      }
+      __syncthreads();
+      const int dl = min(WR_DT, D - d0);
+      for (int dd = 0; dd < dl; dd += V) {
+        struct RV { raw e[V]; };
+        const RV qv = __builtin_bit_cast(RV, *reinterpret_cast<const uint4*>(qtile + rl * RS + dd));
+        float x[V];
+#pragma unroll
+        for (int e = 0; e < V; ++e) x[e] = ET<E>::to_f(qv.e[e]);
+#pragma unroll
+        for (int j = 0; j < WR_KPT; ++j) {
+          const RV kv = __builtin_bit_cast(RV, *reinterpret_cast<const uint4*>(ktile + (lane + WR_LANES * j) * RS + dd));
+#pragma unroll
+          for (int e = 0; e < V; ++e) acc[j] = fmaf(x[e], ET<E>::to_f(kv.e[e]), acc[j]);
+        }
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < WR_KPT; ++j) {
+      const int kl = kc0 + lane + WR_LANES * j;
+      if (kl < nk) sc[rl][kl] = acc[j] * a.scale;
+    }
+  }
+  __syncthreads();  // every score of the row in sc
+
+  // Place this lane's keys: index order in a short window, rank otherwise.
+  if (active) {
+    for (int kl = lane; kl < nk; kl += WR_LANES) {
+      const int64_t key = blk_lo + kl;
+      if (key < lo || key >= hi) continue;
+      const float v = sc[rl][kl];
+      int slot;
+      if (row_nat) {
+        slot = static_cast<int>(key - lo);
+      } else {
+        if (!(v > -INFINITY)) continue;  // NaN or -inf: never selected
+        int rank = 0;
+        const int wl = static_cast<int>(lo - blk_lo), wh = static_cast<int>(hi - blk_lo);
+        for (int i = wl; i < wh && rank < k; ++i) {
+          const float u = sc[rl][i];
+          rank += (u > v || (u == v && i < kl)) ? 1 : 0;
+        }
+        if (rank >= k) continue;
+        slot = rank;
+      }
+      out_s[rl][slot] = v;
+      out_i[rl][slot] = static_cast<int>(key);
+    }
+  }
+  __syncthreads();
+  if (!active || lane != 0) return;
+  // Gates over the filled slots (a prefix), in slot order as route_kernel sums them.
+  const int64_t obase = (b * a.n_query + row) * k;
+  int n = 0;
+  for (int m = 0; m < k; ++m) n += out_i[rl][m] >= 0 ? 1 : 0;
+  float mx = -INFINITY;
+  if (row_nat) {
+    for (int m = 0; m < n; ++m) mx = fmaxf(mx, out_s[rl][m] * a.inv_temp);
+  } else if (n > 0) {
+    mx = out_s[rl][0] * a.inv_temp;
+  }
+  float sum = 0.f;
+  for (int m = 0; m < n; ++m) sum += expf(out_s[rl][m] * a.inv_temp - mx);
+  for (int m = 0; m < k; ++m) {
+    const bool f = m < n;
+    a.idx[obase + m] = f ? out_i[rl][m] : -1;
+    a.scores[obase + m] = f ? out_s[rl][m] : -INFINITY;
+    a.gates[obase + m] = f ? expf(out_s[rl][m] * a.inv_temp - mx) / sum : 0.f;
+  }
+}
+
+template <class E>
+int launch_route_window(const RouteArgs& a, int64_t batch, hipStream_t s) {
+  const dim3 grid(static_cast<unsigned>((a.n_query + WR_ROWS - 1) / WR_ROWS), static_cast<unsigned>(batch));
+  hipLaunchKernelGGL((route_window_kernel<E>), grid, dim3(WR_THREADS), 0, s, a);
+  return check_launch("segment_route");
+}
+
 // MFMA routing for bf16 inputs with k < n_keys.  Same result as route_kernel,
 // bit for bit: the MFMA only narrows the search.
 //
@@ -560,7 +780,7 @@ __global__ __launch_bounds__(RM_THREADS, 2) void route_mfma_kernel(const RouteAr
 
 // Whether route_mfma_kernel covers these arguments; ib = index bits.
 bool mfma_route_ok(const RouteArgs& a, int dtype, const void* queries, const void* keys, int* ib) {
-  if (dtype != GRM_HIP_BF16 || a.natural || !(a.scale > 0.f) || a.dim > 128 || a.dim % 8 != 0 ||
+  if (dtype != GRM_HIP_BF16 || a.natural || a.seg_len > 0 || !(a.scale > 0.f) || a.dim > 128 || a.dim % 8 != 0 ||
       a.n_keys > 2048 || a.k > 32 || (reinterpret_cast<uintptr_t>(queries) | reinterpret_cast<uintptr_t>(keys)) % 16 != 0 ||
       a.n_query * a.dim * 2 > INT32_MAX || a.n_keys * a.dim * 2 > INT32_MAX)
     return false;
@@ -836,6 +1056,76 @@ extern "C" int grm_hip_topk_route(const void* queries, const void* keys, int64_t
   hipStream_t s = static_cast<hipStream_t>(stream);
   int ib = 0;
   if (mfma_route_ok(a, dtype, queries, keys, &ib)) return launch_route_mfma(a, batch, ib, s);
+  switch (dtype) {
+    case GRM_HIP_F32: return launch_route<F32>(a, batch, s);
+    case GRM_HIP_F16: return launch_route<F16>(a, batch, s);
+    default: return launch_route<BF16>(a, batch, s);
+  }
+}
+
+extern "C" int grm_hip_segment_route(const void* queries, const void* keys, int64_t* topk_indices,
+                                     float* topk_scores, float* gates, int64_t batch, int64_t n_query,
+                                     int64_t n_keys, int64_t dim, int dtype, int64_t top_k,
+                                     int64_t segment_len, int64_t base, int64_t capacity, float scale,
+                                     float temperature, void* stream) {
+  if (batch < 0 || n_query < 0 || n_keys < 0 || dim < 0 || top_k < 1 || top_k > 32 || segment_len < 1 ||
+      base < 0 || capacity < 1) {
+    set_error("segment_route: bad sizes (1 <= top_k <= 32, segment_len >= 1, base >= 0, capacity >= 1)");
+    return GRM_HIP_EINVAL;
+  }
+  if (dtype < GRM_HIP_F32 || dtype > GRM_HIP_BF16) {
+    set_error("segment_route: unsupported dtype %d", dtype);
+    return GRM_HIP_EUNSUPPORTED;
+  }
+  if (!(temperature > 0.f) || !std::isfinite(scale)) {
+    set_error("segment_route: temperature must be > 0 and scale finite");
+    return GRM_HIP_EINVAL;
+  }
+  if (batch == 0 || n_query == 0) return GRM_HIP_OK;
+  if (base + (n_query - 1) / segment_len > n_keys) {
+    set_error("segment_route: the last segment's window ends past n_keys");
+    return GRM_HIP_EINVAL;
+  }
+  if (batch > 65535 || dim > INT32_MAX || n_keys > INT32_MAX || segment_len > INT32_MAX) {
+    set_error("segment_route: batch > 65535 or dims too large");
+    return GRM_HIP_EUNSUPPORTED;
+  }
+  if (queries == nullptr || (keys == nullptr && n_keys > 0) || topk_indices == nullptr ||
+      topk_scores == nullptr || gates == nullptr) {
+    set_error("segment_route: null pointer");
+    return GRM_HIP_EINVAL;
+  }
+  RouteArgs a;
+  memset(&a, 0, sizeof(a));
+  a.q = queries;
+  a.keys = keys;
+  a.idx = topk_indices;
+  a.scores = topk_scores;
+  a.gates = gates;
+  a.n_query = n_query;
+  a.n_keys = n_keys;
+  a.dim = static_cast<int>(dim);
+  a.k = static_cast<int>(top_k);
+  a.natural = 0;
+  const int eb = dtype == GRM_HIP_F32 ? 4 : 2;
+  a.vec = (dim * eb) % 16 == 0 && aligned(queries, 16);
+  a.scale = scale;
+  a.inv_temp = 1.0f / temperature;
+  a.seg_len = static_cast<int>(segment_len);
+  a.base = base;
+  a.cap = capacity;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  // A workgroup of WR_ROWS rows spans at most ceil((WR_ROWS - 1) / segment_len) + 1
+  // segments, so its keys number at most capacity + that - 1.
+  const int64_t span = capacity + (WR_ROWS - 1 + segment_len - 1) / segment_len;
+  const bool window_ok = span <= WR_MAXK && a.vec && aligned(keys, 16) && top_k <= 32;
+  if (window_ok) {
+    switch (dtype) {
+      case GRM_HIP_F32: return launch_route_window<F32>(a, batch, s);
+      case GRM_HIP_F16: return launch_route_window<F16>(a, batch, s);
+      default: return launch_route_window<BF16>(a, batch, s);
+    }
+  }
   switch (dtype) {
     case GRM_HIP_F32: return launch_route<F32>(a, batch, s);
     case GRM_HIP_F16: return launch_route<F16>(a, batch, s);

@@ -35,7 +35,7 @@ _REGISTERED_OPS = (
     "apply_query_backward",
     "batched_memory_gather",
 )
-_EXTRA_OPS = ("segment_scan_forward", "topk_route", "fuse_residual", "gather_apply")
+_EXTRA_OPS = ("segment_scan_forward", "topk_route", "fuse_residual", "gather_apply", "segment_route")
 
 _EXTENSION_MODULE: Optional[Any] = None
 _EXTENSION_LOAD_ATTEMPTED = False
@@ -372,6 +372,38 @@ def cuda_topk_route(queries: Tensor, keys: Tensor, top_k: int, scale: float, tem
     return torch.softmax(top / temperature, dim=-1), idx, top
 
 
+def cuda_segment_route(queries: Tensor, keys: Tensor, top_k: int, segment_len: int, base: int, capacity: int,
+                       scale: float, temperature: float = 1.0, *, enabled: bool = True,
+                       debug_fallback: bool = False) -> Tuple[Tensor, Tensor, Tensor]:
+    """Routing of every segment of a sequence in one call, as the reference's
+    segment loop routes each segment over the archive of the moment
+    (paper_grm.py:702-728 -> _route_chunk, :566-589).  Query row t of segment
+    s = t // segment_len sees keys [lo, hi), hi = base + s, lo = max(0, hi - capacity).
+    Returns (gates, indices, scores), each [B, Q, top_k]; indices are absolute key
+    positions, and a window of n <= top_k keys fills slots n.. with index -1,
+    score -inf and gate 0."""
+    if _use_native("topk_route", queries.device, enabled=enabled, debug_fallback=debug_fallback,
+                   auto_on_cpu=True):
+        return torch.ops.grm_cuda.segment_route(queries, keys, int(top_k), int(segment_len), int(base),
+                                                int(capacity), float(scale), float(temperature))
+    B, Q, _ = queries.shape
+    gates = queries.new_zeros((B, Q, top_k), dtype=torch.float32)
+    idx = torch.full((B, Q, top_k), -1, dtype=torch.long, device=queries.device)
+    scores = torch.full((B, Q, top_k), float("-inf"), dtype=torch.float32, device=queries.device)
+    for t0 in range(0, Q, segment_len):
+        hi = min(keys.size(1), base + t0 // segment_len)
+        lo = max(0, hi - capacity)
+        if hi <= lo:
+            continue
+        sl = slice(t0, t0 + segment_len)
+        g, i, sc = cuda_topk_route(queries[:, sl], keys[:, lo:hi], top_k, scale, temperature, enabled=False)
+        n = g.size(-1)
+        gates[:, sl, :n] = g.float()
+        idx[:, sl, :n] = i + lo
+        scores[:, sl, :n] = sc.float()
+    return gates, idx, scores
+
+
 def cuda_fuse_residual(h_online: Tensor, retrieved: Tensor, gates: Tensor, weight: Optional[Tensor] = None,
                        bias: Optional[Tensor] = None, eps: float = 1e-5, *, enabled: bool = True,
                        debug_fallback: bool = False) -> Tensor:
@@ -411,6 +443,7 @@ __all__ = [
     "cuda_chunk_update",
     "cuda_fuse_residual",
     "cuda_gather_apply",
+    "cuda_segment_route",
     "cuda_segment_scan",
     "cuda_topk_route",
     "get_grm_cuda_runtime_status",

@@ -163,6 +163,39 @@ def test_cpu_topk_route_bit_exact(S, k):
     np.testing.assert_allclose(gates.numpy(), og, rtol=1e-6)
 
 
+@pytest.mark.parametrize("T,seg,base,cap,k,S", [(200, 16, 0, 64, 8, 13), (96, 8, 5, 6, 4, 16), (64, 64, 0, 64, 8, 1),
+                                                 (70, 10, 3, 4, 32, 10)])
+def test_cpu_segment_route_matches_oracle(T, seg, base, cap, k, S):
+    """One call routes every segment over the archive of its moment: the oracle's
+    per-window topk_route, absolute indices, empty slots -1 / -inf / 0."""
+    g = torch.Generator().manual_seed(T + k)
+    q = torch.nn.functional.normalize(torch.randn(2, T, 24, generator=g), dim=-1).to(torch.bfloat16)
+    keys = torch.nn.functional.normalize(torch.randn(2, S, 24, generator=g), dim=-1).to(torch.bfloat16)
+    gates, idx, sc = cuda_ops.cuda_segment_route(q, keys, k, seg, base, cap, 24 ** -0.5)
+    og, oi, osc = orc.segment_route(q.float().numpy(), keys.float().numpy(), k, seg, base, cap, 24 ** -0.5)
+    assert np.array_equal(idx.numpy(), oi) and np.array_equal(sc.numpy(), osc)
+    np.testing.assert_allclose(gates.numpy(), og, rtol=1e-6, atol=1e-7)
+    # segment s sees min(base + s, cap) keys: every filled index lies in its window
+    for t in range(T):
+        hi = min(S, base + t // seg)
+        lo = max(0, hi - cap)
+        row = idx[:, t].numpy()
+        assert ((row == -1) | ((row >= lo) & (row < hi))).all()
+        assert (row >= 0).sum(-1).tolist() == [min(k, hi - lo)] * 2
+    # the PyTorch fallback (torch.topk per window) agrees away from near-ties
+    fg, fi, _ = cuda_ops.cuda_segment_route(q.float(), keys.float(), k, seg, base, cap, 24 ** -0.5, enabled=False)
+    assert np.array_equal(fi.numpy(), oi)
+    np.testing.assert_allclose(fg.numpy(), og, rtol=1e-5, atol=1e-7)
+
+
+def test_cpu_segment_route_rejects():
+    q = torch.zeros(1, 10, 4)
+    with pytest.raises(RuntimeError, match="window ends past"):
+        torch.ops.grm_cuda.segment_route(q, torch.zeros(1, 2, 4), 2, 3, 0, 8, 1.0, 1.0)
+    with pytest.raises(RuntimeError, match="top_k must be in"):
+        torch.ops.grm_cuda.segment_route(q, torch.zeros(1, 4, 4), 33, 3, 0, 8, 1.0, 1.0)
+
+
 def test_cpu_fuse_residual():
     g = torch.Generator().manual_seed(2)
     h, r = torch.randn(5, 32, generator=g), torch.randn(5, 3, 32, generator=g)

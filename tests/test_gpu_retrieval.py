@@ -291,6 +291,33 @@ def test_topk_route_bit_exact(dev, dtype, B, Q, S, D, k):
     assert torch.equal(i2, idx) and torch.equal(s2, sc) and torch.equal(g2, gates)
 
 
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32, torch.float16])
+@pytest.mark.parametrize("B,T,seg,base,cap,S,D,k", [
+    (2, 1000, 64, 0, 64, 16, 512, 8),     # config 4's shape class: windows grow from 0 to 15 keys
+    (1, 8192, 64, 0, 64, 128, 64, 8),     # a full config-4 layer sequence, capacity 64 caps the window
+    (3, 300, 7, 12, 20, 55, 96, 16),      # earlier archive entries (base), short partial last segment
+    (2, 130, 13, 2, 5, 12, 40, 32),       # windows never longer than k: index order throughout
+    (1, 64, 64, 0, 64, 1, 32, 8),         # one segment, empty archive: every slot empty
+    (1, 600, 64, 0, 200, 10, 64, 8),      # capacity beyond one workgroup's key buffer: per-row kernel
+    (2, 90, 9, 0, 16, 11, 30, 4),         # rows not 16-byte multiples: per-row kernel
+])
+def test_segment_route_bit_exact(dev, dtype, B, T, seg, base, cap, S, D, k):
+    """Every segment routed over the archive of its moment in one launch,
+    bit-exact against the oracle's per-window routing."""
+    g = torch.Generator().manual_seed(T + S)
+    q = norm(torch.randn(B, T, D, generator=g)).to(dtype)
+    keys = norm(torch.randn(B, S, D, generator=g)).to(dtype)
+    scale = 1.0 / D ** 0.5
+    print(f"segment_route {dtype} B={B} T={T} seg={seg} base={base} cap={cap} S={S} D={D} k={k}", flush=True)
+    gates, idx, sc = capi.segment_route(q.to(dev), keys.to(dev), k, seg, base, cap, scale)
+    og, oi, osc = orc.segment_route(q.float().numpy(), keys.float().numpy(), k, seg, base, cap, scale)
+    assert np.array_equal(idx.cpu().numpy(), oi)
+    assert np.array_equal(sc.cpu().numpy(), osc)
+    np.testing.assert_allclose(gates.cpu().numpy(), og, rtol=1e-5, atol=1e-6)
+    g2, i2, s2 = torch.ops.grm_cuda.segment_route(q.to(dev), keys.to(dev), k, seg, base, cap, scale, 1.0)
+    assert torch.equal(i2, idx) and torch.equal(s2, sc) and torch.equal(g2, gates)
+
+
 def test_topk_route_ties(dev):
     """Duplicate keys give equal scores; the lower index must win every tie."""
     g = torch.Generator().manual_seed(6)
