@@ -290,14 +290,16 @@ int launch_route(const RouteArgs& a, int64_t batch, hipStream_t s) {
 constexpr int WR_ROWS = 32;
 constexpr int WR_LANES = 8;
 constexpr int WR_THREADS = WR_ROWS * WR_LANES;
-constexpr int WR_KPT = 16;                    // keys per lane per key chunk
-constexpr int WR_KC = WR_LANES * WR_KPT;      // keys per chunk
-constexpr int WR_MAXK = WR_KC;                // keys per workgroup (score buffer)
+constexpr int WR_MAXK = 128;                  // keys per workgroup (score buffer)
 constexpr int WR_DT = 64;                     // dims per staged slice
 
-template <class E>
+// KPT keys per lane per key chunk: 8 when every workgroup's range is at most
+// 64 keys, else 16.
+template <class E, int KPT>
 __global__ __launch_bounds__(WR_THREADS) void route_window_kernel(const RouteArgs a) {
   using raw = typename ET<E>::raw;
+  constexpr int WR_KPT = KPT;
+  constexpr int WR_KC = WR_LANES * KPT;  // keys per chunk
   constexpr int V = 16 / sizeof(raw);         // elements per 16-byte read
   // Row stride WR_DT + 16 bytes: the 8 key rows a wave reads at one offset
   // start in 8 distinct 4-bank groups.
@@ -426,9 +428,13 @@ __global__ __launch_bounds__(WR_THREADS) void route_window_kernel(const RouteArg
 }
 
 template <class E>
-int launch_route_window(const RouteArgs& a, int64_t batch, hipStream_t s) {
+int launch_route_window(const RouteArgs& a, int64_t batch, int64_t span, hipStream_t s) {
   const dim3 grid(static_cast<unsigned>((a.n_query + WR_ROWS - 1) / WR_ROWS), static_cast<unsigned>(batch));
-  hipLaunchKernelGGL((route_window_kernel<E>), grid, dim3(WR_THREADS), 0, s, a);
+  if (span <= WR_LANES * 8) {
+    hipLaunchKernelGGL((route_window_kernel<E, 8>), grid, dim3(WR_THREADS), 0, s, a);
+  } else {
+    hipLaunchKernelGGL((route_window_kernel<E, 16>), grid, dim3(WR_THREADS), 0, s, a);
+  }
   return check_launch("segment_route");
 }
 
@@ -1115,15 +1121,19 @@ extern "C" int grm_hip_segment_route(const void* queries, const void* keys, int6
   a.base = base;
   a.cap = capacity;
   hipStream_t s = static_cast<hipStream_t>(stream);
-  // A workgroup of WR_ROWS rows spans at most ceil((WR_ROWS - 1) / segment_len) + 1
-  // segments, so its keys number at most capacity + that - 1.
-  const int64_t span = capacity + (WR_ROWS - 1 + segment_len - 1) / segment_len;
+  // Keys of one workgroup of WR_ROWS rows (r0 a multiple of WR_ROWS): hi runs
+  // from h0 = base + r0 / segment_len to h1 = base + r1 / segment_len, so the
+  // range is h1 - max(0, h0 - capacity) <= (h1 - h0) + min(n_keys, capacity).
+  // Without a segment boundary inside a workgroup (segment_len a multiple of
+  // WR_ROWS) h1 == h0; otherwise h1 - h0 <= (WR_ROWS - 1) / segment_len + 1.
+  const int64_t crossings = segment_len % WR_ROWS == 0 ? 0 : (WR_ROWS - 1) / segment_len + 1;
+  const int64_t span = std::min(n_keys, capacity) + crossings;
   const bool window_ok = span <= WR_MAXK && a.vec && aligned(keys, 16) && top_k <= 32;
   if (window_ok) {
     switch (dtype) {
-      case GRM_HIP_F32: return launch_route_window<F32>(a, batch, s);
-      case GRM_HIP_F16: return launch_route_window<F16>(a, batch, s);
-      default: return launch_route_window<BF16>(a, batch, s);
+      case GRM_HIP_F32: return launch_route_window<F32>(a, batch, span, s);
+      case GRM_HIP_F16: return launch_route_window<F16>(a, batch, span, s);
+      default: return launch_route_window<BF16>(a, batch, span, s);
     }
   }
   switch (dtype) {

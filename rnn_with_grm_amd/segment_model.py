@@ -99,12 +99,20 @@ class LinearMemoryCell(nn.Module):
             return torch.randn(shape, device=device, dtype=dtype) * 0.02
         raise ValueError(f"Unknown memory_init: {self.memory_init}")
 
-    def project(self, x: Tensor) -> Tuple[Tensor, Tensor, Tensor]:
-        """Normalised keys, values and normalised queries of every token."""
-        k = F.normalize(self.key_proj(x), p=2, dim=-1, eps=_NORM_EPS)
-        v = self.value_proj(x)
-        q = F.normalize(self.query_proj(x), p=2, dim=-1, eps=_NORM_EPS)
-        return k, v, q
+    def project(self, x: Tensor, extra: Optional[nn.Linear] = None) -> Tuple[Tensor, ...]:
+        """Normalised keys, values and normalised queries of every token, as one
+        GEMM over the concatenated weights; `extra` (a Linear on the same input)
+        joins the same GEMM and its output is returned last."""
+        mods = [self.key_proj, self.value_proj, self.query_proj] + ([extra] if extra is not None else [])
+        weight = torch.cat([m.weight for m in mods], 0)
+        if all(m.bias is None for m in mods):
+            bias = None
+        else:
+            bias = torch.cat([m.bias if m.bias is not None else m.weight.new_zeros(m.out_features) for m in mods])
+        outs = F.linear(x, weight, bias).split([m.out_features for m in mods], dim=-1)
+        k = F.normalize(outs[0], p=2, dim=-1, eps=_NORM_EPS)
+        q = F.normalize(outs[2], p=2, dim=-1, eps=_NORM_EPS)
+        return (k, outs[1], q) + tuple(outs[3:])
 
 
 class TopKMemoryRetriever(nn.Module):
@@ -332,7 +340,7 @@ class SegmentRecurrentMemoryModel(nn.Module):
             snaps.append(s2)
         return torch.cat(outs, 1), self._init_memory(B, memory.device, memory.dtype), torch.cat(snaps, 1)
 
-    def _retrieve(self, x: Tensor, q: Tensor, h_online: Tensor, states: Tensor, summaries: Tensor,
+    def _retrieve(self, x: Tensor, q: Tensor, q_r: Tensor, h_online: Tensor, states: Tensor, summaries: Tensor,
                   base: int) -> Tensor:
         """Routing, retrieval and fusion for every token at once
         (paper_grm.py:613-643 per segment).  states/summaries hold the archive
@@ -341,7 +349,6 @@ class SegmentRecurrentMemoryModel(nn.Module):
         seg, cap = self.segment_length, self.memory_capacity_segments
         gu = self.gating_unit
         grad = torch.is_grad_enabled() and any(p.requires_grad for p in self.parameters())
-        q_r = gu.query_proj(x)
         k_r = gu.key_proj(summaries.to(x.dtype))
         top_k = min(self.retrieval_top_k, cap)
         gates, idx, _ = cuda_ops.cuda_segment_route(q_r, k_r, top_k, seg, base, cap, gu.scale, gu.temperature,
@@ -417,7 +424,7 @@ class SegmentRecurrentMemoryModel(nn.Module):
             return out, last_hidden, memory, aux_dict(x.new_zeros(B, 0, self.hidden_size))
 
         seg = self.segment_length
-        k, v, q = self.memory_cell.project(x)
+        k, v, q, q_r = self.memory_cell.project(x, self.gating_unit.query_proj)
         h_online, memory_end, snaps = self._scan(k, v, q, memory)
         h_online = self.dropout(h_online)
 
@@ -438,7 +445,7 @@ class SegmentRecurrentMemoryModel(nn.Module):
             states, summaries = new_states, new_summaries
         n_seg = new_states.size(1)
         if base + n_seg > 1:
-            h_enhanced = self._retrieve(x, q, h_online, states, summaries, base)
+            h_enhanced = self._retrieve(x, q, q_r, h_online, states, summaries, base)
         else:
             h_enhanced = h_online
         y = self.output_proj(h_enhanced)
