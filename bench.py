@@ -193,8 +193,9 @@ def bench_c3(torch, dev, steps, warmup):
 def bench_c5(torch, dev, steps, warmup):
     """Config 5: one whole-sequence update call (16 heads x 65536 tokens, a snapshot every 128
     tokens, 512 per head), then retrieval of k=16 archived states per token over those
-    snapshots: route -> gather_apply -> residual + LayerNorm.  Routing has no causal mask, as in
-    the reference's chunk path (every token sees all 512 states)."""
+    snapshots: route -> gather_apply -> residual + LayerNorm, twice: every token over all 512
+    states (the reference's chunk routing has no causal mask), and with causal windows (the
+    tokens of segment s over snapshots 0..s-1, the archive of the model's segment loop)."""
     from rnn_with_grm_amd import capi
 
     lib = capi.load()
@@ -256,6 +257,18 @@ def bench_c5(torch, dev, steps, warmup):
         gather_apply()
         fuse()
 
+    def route_causal():
+        # segment s (128 tokens) sees the snapshots of segments < s, as in the model's segment loop
+        rc = lib.grm_hip_segment_route(P(q), P(summaries), P(idx), P(sc), P(gt), BH, T, S, D, capi.BF16, K, SEG, 0,
+                                       S, 1.0 / D ** 0.5, 1.0, sp)
+        if rc != 0:
+            raise RuntimeError(capi.last_error())
+
+    def retrieval_causal():
+        route_causal()
+        gather_apply()  # empty slots (index -1) give zero rows, and their gates are 0
+        fuse()
+
     n = max(3, min(steps, 10))
     r_wall, r_per = timed_launches(torch, route, n, min(warmup, 2), stream)
     ga_wall, ga_per = timed_launches(torch, gather_apply, n, min(warmup, 2), stream)
@@ -266,6 +279,9 @@ def bench_c5(torch, dev, steps, warmup):
     r_ref = torch.einsum("rhk,k->rh", snaps[b, idx[b, t]], q[b, t].float())
     assert torch.allclose(retrieved[b, t], r_ref, rtol=1e-4, atol=1e-6), "c5 gather_apply spot check failed"
     assert bool(torch.isfinite(snaps[:, -1]).all()), "c5 snapshots not finite"
+    rc_wall, rc_per = timed_launches(torch, route_causal, n, min(warmup, 2), stream)
+    rtc_wall, rtc_per = timed_launches(torch, retrieval_causal, n, min(warmup, 2), stream)
+    assert int(idx[b, t].max()) < t // SEG and int(idx[b, t].min()) >= 0, "c5 causal window violated"
     tokens = BH * T
     upd_bytes = tokens * (2 * D + D) * 2 + tokens * D * 2 + BH * D * D * 4 + BH * S * D * D * 4
     out = {
@@ -276,6 +292,8 @@ def bench_c5(torch, dev, steps, warmup):
                          "flops": 2 * tokens * K * D * D},
         "fuse": {"ms": statistics.mean(fu_per) * 1e3},
         "retrieval": {"ms": statistics.mean(rt_per) * 1e3, "tokens": tokens},
+        "route_causal": {"ms": statistics.mean(rc_per) * 1e3},
+        "retrieval_causal": {"ms": statistics.mean(rtc_per) * 1e3},
     }
     del retrieved, h_online, fused_out, ws2, idx, sc, gt, snaps, hidden, q, k, v
     return out
@@ -483,6 +501,12 @@ def main() -> int:
             "route_TFLOP/s": round(c5["route"]["flops"] / c5["route"]["ms"] / 1e9, 1),
             "gather_apply_GB/s": round(ga5["bytes"] / ga5["ms"] / 1e6, 1),
             "gather_apply_TFLOP/s_fp32": round(ga5["flops"] / ga5["ms"] / 1e9, 1)}
+        secondary["c5_retrieval_causal"] = {
+            "what": "the same retrieval with causal windows (segment routing: the tokens of segment s route over "
+                    "snapshots 0..s-1, as in the model's segment loop), route -> gather_apply -> residual + LayerNorm",
+            "ms": round(c5["retrieval_causal"]["ms"], 3),
+            "tokens/s": round(rt5["tokens"] / c5["retrieval_causal"]["ms"] * 1e3),
+            "route_ms": round(c5["route_causal"]["ms"], 3)}
         log(f"c5 update: {u['us']:.1f} us ({ugbs:.0f} GB/s); retrieval {rt5['ms']:.2f} ms (route "
             f"{c5['route']['ms']:.2f}, gather_apply {ga5['ms']:.2f}, fuse {c5['fuse']['ms']:.2f})")
 

@@ -568,6 +568,24 @@ __global__ __launch_bounds__(RM_THREADS, 2) void route_mfma_kernel(const RouteAr
   const bool wave_live = qw < a.n_query;
   const int64_t qi = qw + lane;
   const bool active = qi < a.n_query;
+
+  // Key windows (segment routing, seg_len > 0): row r sees [lo(r), hi(r)),
+  // hi = base + r / seg_len, lo = max(0, hi - cap); both move forward with r.
+  // Without windows every row sees [0, S).  A row whose window holds at most
+  // k keys takes all of them in index order.
+  auto win_hi = [&](int64_t r) -> int {
+    return a.seg_len > 0 ? static_cast<int>(min(a.n_keys, a.base + min(r, a.n_query - 1) / a.seg_len)) : S;
+  };
+  auto win_lo = [&](int h) -> int {
+    return a.seg_len > 0 ? static_cast<int>(h > a.cap ? h - a.cap : int64_t{0}) : 0;
+  };
+  const int row_hi = win_hi(qi), row_lo = win_lo(row_hi);
+  const int row_n = row_hi - row_lo;
+  const bool row_nat = a.seg_len > 0 && row_n <= k;
+  // Keys the wave scores (rows qw .. qw + 63) and keys the workgroup stages.
+  const int wave_lo = win_lo(win_hi(qw)) & ~(RM_KT - 1), wave_hi = win_hi(qw + 63);
+  const int64_t qb0 = static_cast<int64_t>(blockIdx.x) * RM_THREADS;
+  const int blk_lo = win_lo(win_hi(qb0)), blk_hi = win_hi(qb0 + RM_THREADS - 1);
   const uint16_t* qb = static_cast<const uint16_t*>(a.q) + b * a.n_query * D;
   const __amdgpu_buffer_rsrc_t rq = make_rsrc(qb, static_cast<uint32_t>(a.n_query * D * 2));
 
@@ -594,6 +612,13 @@ __global__ __launch_bounds__(RM_THREADS, 2) void route_mfma_kernel(const RouteAr
   }
   // Lane 16 g + n owns row qw + 16 g + n, whose norm sits in qp[g].
   const float qn2 = g == 0 ? qp[0] : g == 1 ? qp[1] : g == 2 ? qp[2] : qp[3];
+  // Windows of the rows this lane packs scores for: qw + 16 qt + n.
+  int pk_lo[4], pk_hi[4];
+#pragma unroll
+  for (int qt = 0; qt < 4; ++qt) {
+    pk_hi[qt] = win_hi(qw + 16 * qt + n);
+    pk_lo[qt] = win_lo(pk_hi[qt]);
+  }
 
   const uint32_t imask = (1u << ib) - 1u;
   uint32_t net[KN];
@@ -613,9 +638,9 @@ __global__ __launch_bounds__(RM_THREADS, 2) void route_mfma_kernel(const RouteAr
       }
     }
   };
-  load_keys(0);
-  const int s_scan = wave_live ? S : 0;
-  for (int s0 = 0; s0 < s_scan; s0 += RM_KT) {
+  load_keys(wave_lo);
+  const int s_scan = wave_live ? wave_hi : 0;
+  for (int s0 = wave_lo; s0 < s_scan; s0 += RM_KT) {
     f32x4 acc[4][2];
 #pragma unroll
     for (int qt = 0; qt < 4; ++qt)
@@ -625,7 +650,7 @@ __global__ __launch_bounds__(RM_THREADS, 2) void route_mfma_kernel(const RouteAr
 #pragma unroll
         for (int c = 0; c < NC; ++c) acc[qt][kt] = mfma8(ak[kt][c], bq[qt][c], acc[qt][kt]);
       }
-    if (s0 + RM_KT < S) load_keys(s0 + RM_KT);
+    if (s0 + RM_KT < s_scan) load_keys(s0 + RM_KT);
     // acc[qt][kt][r] = A(key s0 + 16 kt + 4 g + r, row 16 qt + n)
 #pragma unroll
     for (int qt = 0; qt < 4; ++qt)
@@ -636,7 +661,8 @@ __global__ __launch_bounds__(RM_THREADS, 2) void route_mfma_kernel(const RouteAr
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
           const int key = s0 + 16 * kt + 4 * g + r;
-          pe[r] = key < S ? ((order_bits(acc[qt][kt][r]) & ~imask) | static_cast<uint32_t>(key)) : 0u;
+          pe[r] = (key >= pk_lo[qt] && key < pk_hi[qt])
+                      ? ((order_bits(acc[qt][kt][r]) & ~imask) | static_cast<uint32_t>(key)) : 0u;
         }
         *reinterpret_cast<uint4*>(srow + (16 * qt + n) * RM_ROW + 16 * kt + 4 * g) = pk;
       }
@@ -698,8 +724,9 @@ __global__ __launch_bounds__(RM_THREADS, 2) void route_mfma_kernel(const RouteAr
                      4.f * static_cast<float>(D) * 0x1p-126f * (qn + km);
   const float theta = tau - wide;
   const bool sound = qn * km < 1e30f && wide <= 1e30f;  // false for NaN and inf
-  const bool complete = S <= KN || unorder_bits(net[KN - 1] & ~imask) < theta;
-  const bool scan_all = active && !(sound && complete);
+  const bool complete = row_n <= KN || unorder_bits(net[KN - 1] & ~imask) < theta;
+  // A short window (row_nat) is scored key by key in index order, like scan_all.
+  const bool scan_all = active && (row_nat || !(sound && complete));
 
   // Candidate keys in ascending order (0xffffffff past the last), so that the
   // candidates inside one key chunk are a contiguous run.
@@ -708,7 +735,7 @@ __global__ __launch_bounds__(RM_THREADS, 2) void route_mfma_kernel(const RouteAr
   for (int i = 0; i < KN; ++i) ck[i] = 0xffffffffu;
 #pragma unroll
   for (int i = 0; i < KN; ++i) {
-    const bool take = active && !scan_all && i < S && unorder_bits(net[i] & ~imask) >= theta;
+    const bool take = active && !scan_all && i < row_n && unorder_bits(net[i] & ~imask) >= theta;
     uint32_t x = take ? (net[i] & imask) : 0xffffffffu;
 #pragma unroll
     for (int m = 0; m < KN; ++m) {
@@ -721,8 +748,8 @@ __global__ __launch_bounds__(RM_THREADS, 2) void route_mfma_kernel(const RouteAr
   // Key chunks through LDS; each lane walks its candidates in the chunk (or,
   // for a row that needs it, every key of the chunk) with one copy of the chain.
   const uint16_t* kl = reinterpret_cast<const uint16_t*>(smem);
-  for (int c0 = 0; c0 < S; c0 += RM_KC) {
-    const int c1 = min(S, c0 + RM_KC);
+  for (int c0 = blk_lo; c0 < blk_hi; c0 += RM_KC) {
+    const int c1 = min(blk_hi, c0 + RM_KC);
     __syncthreads();  // score tiles / the previous chunk are no longer read
     constexpr int UPR = DKP / 8;  // 16-byte units per padded row
     for (int e = tid; e < RM_KC * UPR; e += RM_THREADS) {
@@ -739,7 +766,9 @@ __global__ __launch_bounds__(RM_THREADS, 2) void route_mfma_kernel(const RouteAr
       lo += ck[i] < static_cast<uint32_t>(c0) ? 1 : 0;
       hi += ck[i] < static_cast<uint32_t>(c1) ? 1 : 0;
     }
-    const int count = scan_all ? c1 - c0 : hi - lo;
+    // scan_all rows walk their window's keys of this chunk, [w0, w1)
+    const int w0 = max(c0, row_lo), w1 = min(c1, row_hi);
+    const int count = scan_all ? max(w1 - w0, 0) : hi - lo;
     constexpr int NCH = 2;  // chains per step
 #pragma unroll 1
     for (int j = 0; j < count; j += NCH) {
@@ -747,7 +776,7 @@ __global__ __launch_bounds__(RM_THREADS, 2) void route_mfma_kernel(const RouteAr
       const uint16_t* rows[NCH];
 #pragma unroll
       for (int t = 0; t < NCH; ++t) {
-        key[t] = c0 + j + t;
+        key[t] = w0 + j + t;
         if (!scan_all) {
           uint32_t word = 0u;
 #pragma unroll
@@ -759,13 +788,47 @@ __global__ __launch_bounds__(RM_THREADS, 2) void route_mfma_kernel(const RouteAr
       float sc4[NCH];
       exact_scores_lds<DKP, NCH>(qv, rows, D, a.scale, sc4);
 #pragma unroll
-      for (int t = 0; t < NCH; ++t)
-        if (j + t < count) exact_insert<KMAX>(top_s, top_i, sc4[t], key[t]);
+      for (int t = 0; t < NCH; ++t) {
+        if (j + t >= count) continue;
+        if (row_nat) {  // index order: slot key - row_lo
+#pragma unroll
+          for (int m = 0; m < KMAX; ++m) {
+            if (m == key[t] - row_lo) {
+              top_s[m] = sc4[t];
+              top_i[m] = key[t];
+            }
+          }
+        } else {
+          exact_insert<KMAX>(top_s, top_i, sc4[t], key[t]);
+        }
+      }
     }
   }
   if (!active) return;
 
   const int64_t obase = (b * a.n_query + qi) * k;
+  if (row_nat) {
+    // n <= k window keys in index order; slots n .. k-1 empty (-1, -inf, 0).
+    float mxn = -INFINITY;
+#pragma unroll
+    for (int m = 0; m < KMAX; ++m) mxn = (m < row_n) ? fmaxf(mxn, top_s[m] * a.inv_temp) : mxn;
+    float en[KMAX];
+    float sumn = 0.f;
+#pragma unroll
+    for (int m = 0; m < KMAX; ++m) {
+      en[m] = (m < row_n) ? expf(top_s[m] * a.inv_temp - mxn) : 0.f;
+      sumn += en[m];
+    }
+#pragma unroll
+    for (int m = 0; m < KMAX; ++m) {
+      if (m < k) {
+        a.idx[obase + m] = (m < row_n) ? top_i[m] : -1;
+        a.scores[obase + m] = (m < row_n) ? top_s[m] : -INFINITY;
+        a.gates[obase + m] = (m < row_n) ? en[m] / sumn : 0.f;
+      }
+    }
+    return;
+  }
   const float mx = top_s[0] * a.inv_temp;
   float e[KMAX];
   float sum = 0.f;
@@ -786,7 +849,7 @@ __global__ __launch_bounds__(RM_THREADS, 2) void route_mfma_kernel(const RouteAr
 
 // Whether route_mfma_kernel covers these arguments; ib = index bits.
 bool mfma_route_ok(const RouteArgs& a, int dtype, const void* queries, const void* keys, int* ib) {
-  if (dtype != GRM_HIP_BF16 || a.natural || a.seg_len > 0 || !(a.scale > 0.f) || a.dim > 128 || a.dim % 8 != 0 ||
+  if (dtype != GRM_HIP_BF16 || a.natural || !(a.scale > 0.f) || a.dim > 128 || a.dim % 8 != 0 ||
       a.n_keys > 2048 || a.k > 32 || (reinterpret_cast<uintptr_t>(queries) | reinterpret_cast<uintptr_t>(keys)) % 16 != 0 ||
       a.n_query * a.dim * 2 > INT32_MAX || a.n_keys * a.dim * 2 > INT32_MAX)
     return false;
@@ -1128,6 +1191,8 @@ extern "C" int grm_hip_segment_route(const void* queries, const void* keys, int6
   // WR_ROWS) h1 == h0; otherwise h1 - h0 <= (WR_ROWS - 1) / segment_len + 1.
   const int64_t crossings = segment_len % WR_ROWS == 0 ? 0 : (WR_ROWS - 1) / segment_len + 1;
   const int64_t span = std::min(n_keys, capacity) + crossings;
+  int ib = 0;
+  if (mfma_route_ok(a, dtype, queries, keys, &ib)) return launch_route_mfma(a, batch, ib, s);
   const bool window_ok = span <= WR_MAXK && a.vec && aligned(keys, 16) && top_k <= 32;
   if (window_ok) {
     switch (dtype) {

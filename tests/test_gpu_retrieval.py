@@ -300,6 +300,8 @@ def test_topk_route_bit_exact(dev, dtype, B, Q, S, D, k):
     (1, 64, 64, 0, 64, 1, 32, 8),         # one segment, empty archive: every slot empty
     (1, 600, 64, 0, 200, 10, 64, 8),      # capacity beyond one workgroup's key buffer: per-row kernel
     (2, 90, 9, 0, 16, 11, 30, 4),         # rows not 16-byte multiples: per-row kernel
+    (1, 2048, 4, 0, 512, 512, 128, 16),   # config 5's causal windows in miniature: up to 511 keys, 2 key chunks
+    (2, 700, 2, 100, 300, 450, 64, 8),    # base and capacity both bind; windows slide
 ])
 def test_segment_route_bit_exact(dev, dtype, B, T, seg, base, cap, S, D, k):
     """Every segment routed over the archive of its moment in one launch,
