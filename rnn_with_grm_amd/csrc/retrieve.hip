@@ -55,6 +55,15 @@ struct RetrieveArgs {
   int v_tiles;
   int32_t* partial;  // [batch, bk_chunks, segments]: per-chunk counts, then bases (multi-workgroup bucketing)
   int bk_chunks;     // pair chunks of BK_ITEMS per sequence
+  // Work tiles of the apply kernels: at most tile_pairs consecutive pairs of
+  // one segment each, so a segment that many queries selected is spread over
+  // several workgroups.  tiles [batch, tb_max] of (segment, first pair, end, 0);
+  // n_tiles [batch]; tile_base [batch, segments + 1] is the scan's scratch.
+  int4* tiles;
+  int32_t* n_tiles;
+  int32_t* tile_base;
+  int tb_max;
+  int tile_pairs;
 };
 
 // ---------------------------------------------------------------------------
@@ -96,11 +105,21 @@ __device__ void bucket_offsets(int* hist, int64_t S, int32_t* offsets) {
 }
 
 // A row whose index is outside [0, segments): zeros, and one count.
+// Called by every lane of a wave together (bad: this lane's pair i is
+// invalid): the wave writes each invalid pair's row with consecutive lanes on
+// consecutive elements, one row after another.
 template <class EM>
-__device__ __forceinline__ void zero_row(const RetrieveArgs& a, int64_t b, int64_t i) {
-  typename ET<EM>::raw* ob = static_cast<typename ET<EM>::raw*>(a.out) + (b * a.n_index + i) * a.dv;
-  for (int h = 0; h < a.dv; ++h) ob[h] = ET<EM>::from_f(0.f);
-  if (a.bad != nullptr) atomicAdd(a.bad, 1);
+__device__ __forceinline__ void zero_rows_wave(const RetrieveArgs& a, int64_t b, int64_t i, bool bad) {
+  uint64_t mask = __ballot(bad);
+  const int lane = threadIdx.x & 63;
+  if (mask != 0u && lane == 0 && a.bad != nullptr) atomicAdd(a.bad, static_cast<int>(__popcll(mask)));
+  while (mask != 0u) {
+    const int l = __ffsll(static_cast<unsigned long long>(mask)) - 1;
+    mask &= mask - 1u;
+    const int64_t row = __shfl(i, l, 64);
+    typename ET<EM>::raw* ob = static_cast<typename ET<EM>::raw*>(a.out) + (b * a.n_index + row) * a.dv;
+    for (int h = lane; h < a.dv; h += 64) ob[h] = ET<EM>::from_f(0.f);
+  }
 }
 
 // Pairs of one sequence sorted by segment, one workgroup per sequence.  Rows
@@ -121,13 +140,12 @@ __global__ __launch_bounds__(BK_THREADS) void bucket_kernel(const RetrieveArgs a
   __syncthreads();
   bucket_offsets(hist, S, a.offsets + b * (S + 1));
   int32_t* lb = a.list + b * n;
-  for (int64_t i = tid; i < n; i += BK_THREADS) {
-    const int64_t s = ib[i];
-    if (s >= 0 && s < S) {
-      lb[atomicAdd(&hist[s], 1)] = static_cast<int32_t>(i);
-    } else {
-      zero_row<EM>(a, b, i);
-    }
+  for (int64_t i0 = 0; i0 < n; i0 += BK_THREADS) {  // uniform trip count: whole waves zero rows
+    const int64_t i = i0 + tid;
+    const int64_t s = i < n ? ib[i] : 0;
+    const bool valid = s >= 0 && s < S;
+    if (i < n && valid) lb[atomicAdd(&hist[s], 1)] = static_cast<int32_t>(i);
+    zero_rows_wave<EM>(a, b, i, i < n && !valid);
   }
 }
 
@@ -144,13 +162,12 @@ __global__ __launch_bounds__(BK_THREADS) void bucket_count_kernel(const Retrieve
   const int64_t* ib = a.idx + b * n;
   for (int64_t s = tid; s < S; s += BK_THREADS) hist[s] = 0;
   __syncthreads();
-  for (int64_t i = i0 + tid; i < i1; i += BK_THREADS) {
-    const int64_t s = ib[i];
-    if (s >= 0 && s < S) {
-      atomicAdd(&hist[s], 1);
-    } else {
-      zero_row<EM>(a, b, i);
-    }
+  for (int64_t j0 = i0; j0 < i1; j0 += BK_THREADS) {  // uniform trip count: whole waves zero rows
+    const int64_t i = j0 + tid;
+    const int64_t s = i < i1 ? ib[i] : 0;
+    const bool valid = s >= 0 && s < S;
+    if (i < i1 && valid) atomicAdd(&hist[s], 1);
+    zero_rows_wave<EM>(a, b, i, i < i1 && !valid);
   }
   __syncthreads();
   int32_t* pc = a.partial + (b * a.bk_chunks + chunk) * S;
@@ -195,6 +212,28 @@ __global__ __launch_bounds__(BK_THREADS) void bucket_scatter_kernel(const Retrie
     const int64_t s = ib[i];
     if (s >= 0 && s < S) lb[atomicAdd(&cur[s], 1)] = static_cast<int32_t>(i);
   }
+}
+
+// The apply kernels' work list of one sequence: segment s with c pairs gives
+// ceil(c / tile_pairs) tiles, in segment order (one workgroup per sequence).
+__global__ __launch_bounds__(BK_THREADS) void tile_list_kernel(const RetrieveArgs a) {
+  extern __shared__ int hist[];  // [segments]: tiles per segment, then their first slot
+  const int tid = threadIdx.x;
+  const int64_t b = blockIdx.x;
+  const int64_t S = a.segments;
+  const int32_t* off = a.offsets + b * (S + 1);
+  const int tp = a.tile_pairs;
+  for (int64_t s = tid; s < S; s += BK_THREADS) hist[s] = (off[s + 1] - off[s] + tp - 1) / tp;
+  __syncthreads();
+  int32_t* base = a.tile_base + b * (S + 1);
+  bucket_offsets(hist, S, base);
+  int4* tl = a.tiles + b * a.tb_max;
+  for (int64_t s = tid; s < S; s += BK_THREADS) {
+    const int p0 = off[s], p1 = off[s + 1];
+    int slot = hist[s];
+    for (int p = p0; p < p1; p += tp) tl[slot++] = make_int4(static_cast<int>(s), p, min(p1, p + tp), 0);
+  }
+  if (tid == 0) a.n_tiles[b] = base[S];
 }
 
 // Sixteen bytes of a row-major tile as fp32 values (8 elements for 16-bit types,
@@ -242,11 +281,12 @@ __global__ __launch_bounds__(AP_THREADS) void apply_bucket_kernel(const Retrieve
   const int lane = tid & 63, g = lane >> 4, n = lane & 15;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int64_t vt = blockIdx.x % a.v_tiles;
-  const int64_t bs = blockIdx.x / a.v_tiles;
-  const int64_t b = bs / a.segments, s = bs % a.segments;
-  const int32_t* off = a.offsets + b * (a.segments + 1);
-  const int p_begin = off[s], p_end = off[s + 1];
-  if (p_begin == p_end) return;
+  const int64_t tile = blockIdx.x / a.v_tiles;
+  const int64_t b = blockIdx.y;
+  if (tile >= a.n_tiles[b]) return;
+  const int4 te = a.tiles[b * a.tb_max + tile];
+  const int64_t s = te.x;
+  const int p_begin = te.y, p_end = te.z;
   const int dk = a.dk, dv = a.dv;
   const int v0 = static_cast<int>(vt) * AP_V;
 
@@ -380,11 +420,12 @@ __global__ __launch_bounds__(AP_THREADS) void apply_reg_kernel(const RetrieveArg
   const int lane = tid & 63, g = lane >> 4, n = lane & 15;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int64_t vt = blockIdx.x % a.v_tiles;
-  const int64_t bs = blockIdx.x / a.v_tiles;
-  const int64_t b = bs / a.segments, s = bs % a.segments;
-  const int32_t* off = a.offsets + b * (a.segments + 1);
-  const int p_begin = off[s], p_end = off[s + 1];
-  if (p_begin == p_end) return;
+  const int64_t tile = blockIdx.x / a.v_tiles;
+  const int64_t b = blockIdx.y;
+  if (tile >= a.n_tiles[b]) return;
+  const int4 te = a.tiles[b * a.tb_max + tile];
+  const int64_t s = te.x;
+  const int p_begin = te.y, p_end = te.z;
   const int dk = a.dk, dv = a.dv;
   const int v0 = static_cast<int>(vt) * AP_V;
   const int k0 = g * KG;
@@ -488,11 +529,12 @@ __global__ __launch_bounds__(AP_THREADS) void apply_mfma16_kernel(const Retrieve
   const int lane = tid & 63, g = lane >> 4, n = lane & 15;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int64_t vt = blockIdx.x % a.v_tiles;
-  const int64_t bs = blockIdx.x / a.v_tiles;
-  const int64_t b = bs / a.segments, s = bs % a.segments;
-  const int32_t* off = a.offsets + b * (a.segments + 1);
-  const int p_begin = off[s], p_end = off[s + 1];
-  if (p_begin == p_end) return;
+  const int64_t tile = blockIdx.x / a.v_tiles;
+  const int64_t b = blockIdx.y;
+  if (tile >= a.n_tiles[b]) return;
+  const int4 te = a.tiles[b * a.tb_max + tile];
+  const int64_t s = te.x;
+  const int p_begin = te.y, p_end = te.z;
   const int dk = a.dk, dv = a.dv;
   const int v0 = static_cast<int>(vt) * AP_V;
   const int k0 = g * KG;
@@ -604,16 +646,16 @@ __global__ __launch_bounds__(AP_THREADS) void apply_mfma16_kernel(const Retrieve
 
 template <class EL, class EM, class EQ, int DKP, class EF, int NPART>
 int launch_apply_mfma16(const RetrieveArgs& a, hipStream_t s) {
-  const int64_t grid = a.batch * a.segments * a.v_tiles;
-  hipLaunchKernelGGL((apply_mfma16_kernel<EL, EM, EQ, DKP, EF, NPART>), dim3(static_cast<unsigned>(grid)),
+  const dim3 grid(static_cast<unsigned>(static_cast<int64_t>(a.tb_max) * a.v_tiles), static_cast<unsigned>(a.batch));
+  hipLaunchKernelGGL((apply_mfma16_kernel<EL, EM, EQ, DKP, EF, NPART>), grid,
                      dim3(AP_THREADS), 0, s, a);
   return check_launch("gather_apply");
 }
 
 template <class EL, class EM, class EQ, int DKP>
 int launch_apply_reg(const RetrieveArgs& a, hipStream_t s) {
-  const int64_t grid = a.batch * a.segments * a.v_tiles;
-  hipLaunchKernelGGL((apply_reg_kernel<EL, EM, EQ, DKP>), dim3(static_cast<unsigned>(grid)), dim3(AP_THREADS), 0, s,
+  const dim3 grid(static_cast<unsigned>(static_cast<int64_t>(a.tb_max) * a.v_tiles), static_cast<unsigned>(a.batch));
+  hipLaunchKernelGGL((apply_reg_kernel<EL, EM, EQ, DKP>), grid, dim3(AP_THREADS), 0, s,
                      a);
   return check_launch("gather_apply");
 }
@@ -634,8 +676,8 @@ int launch_apply(const RetrieveArgs& a, hipStream_t s) {
     }
     attr_set = true;
   }
-  const int64_t grid = a.batch * a.segments * a.v_tiles;
-  hipLaunchKernelGGL((apply_bucket_kernel<EL, EM, EQ, DKP, VEC>), dim3(static_cast<unsigned>(grid)),
+  const dim3 grid(static_cast<unsigned>(static_cast<int64_t>(a.tb_max) * a.v_tiles), static_cast<unsigned>(a.batch));
+  hipLaunchKernelGGL((apply_bucket_kernel<EL, EM, EQ, DKP, VEC>), grid,
                      dim3(AP_THREADS), lds, s, a);
   return check_launch("gather_apply");
 }
@@ -721,21 +763,27 @@ int launch_bucket(const RetrieveArgs& a, hipStream_t s) {
     if (attr_rc == GRM_HIP_OK) attr_rc = allow_segment_lds(reinterpret_cast<const void*>(&bucket_count_kernel<EM>));
     if (attr_rc == GRM_HIP_OK) attr_rc = allow_segment_lds(reinterpret_cast<const void*>(&bucket_bases_kernel));
     if (attr_rc == GRM_HIP_OK) attr_rc = allow_segment_lds(reinterpret_cast<const void*>(&bucket_scatter_kernel));
+    if (attr_rc == GRM_HIP_OK) attr_rc = allow_segment_lds(reinterpret_cast<const void*>(&tile_list_kernel));
     if (attr_rc != GRM_HIP_OK) return attr_rc;
   }
+  int rc;
   if (a.bk_chunks <= 1) {
     hipLaunchKernelGGL((bucket_kernel<EM>), dim3(static_cast<unsigned>(a.batch)), dim3(BK_THREADS), lds, s, a);
-    return check_launch("gather_apply(sort)");
+    rc = check_launch("gather_apply(sort)");
+  } else {
+    const dim3 grid(static_cast<unsigned>(a.bk_chunks), static_cast<unsigned>(a.batch));
+    hipLaunchKernelGGL((bucket_count_kernel<EM>), grid, dim3(BK_THREADS), lds, s, a);
+    rc = check_launch("gather_apply(sort counts)");
+    if (rc != GRM_HIP_OK) return rc;
+    hipLaunchKernelGGL(bucket_bases_kernel, dim3(static_cast<unsigned>(a.batch)), dim3(BK_THREADS), lds, s, a);
+    rc = check_launch("gather_apply(sort bases)");
+    if (rc != GRM_HIP_OK) return rc;
+    hipLaunchKernelGGL(bucket_scatter_kernel, grid, dim3(BK_THREADS), lds, s, a);
+    rc = check_launch("gather_apply(sort scatter)");
   }
-  const dim3 grid(static_cast<unsigned>(a.bk_chunks), static_cast<unsigned>(a.batch));
-  hipLaunchKernelGGL((bucket_count_kernel<EM>), grid, dim3(BK_THREADS), lds, s, a);
-  int rc = check_launch("gather_apply(sort counts)");
-  if (rc != GRM_HIP_OK) return rc;
-  hipLaunchKernelGGL(bucket_bases_kernel, dim3(static_cast<unsigned>(a.batch)), dim3(BK_THREADS), lds, s, a);
-  rc = check_launch("gather_apply(sort bases)");
-  if (rc != GRM_HIP_OK) return rc;
-  hipLaunchKernelGGL(bucket_scatter_kernel, grid, dim3(BK_THREADS), lds, s, a);
-  return check_launch("gather_apply(sort scatter)");
+  if (rc != GRM_HIP_OK || a.segments == 0) return rc;
+  hipLaunchKernelGGL(tile_list_kernel, dim3(static_cast<unsigned>(a.batch)), dim3(BK_THREADS), lds, s, a);
+  return check_launch("gather_apply(tile list)");
 }
 
 int64_t offsets_bytes(int64_t batch, int64_t segments) { return (batch * (segments + 1) * 4 + 15) / 16 * 16; }
@@ -749,7 +797,26 @@ int64_t list_bytes(int64_t batch, int64_t n_index) { return (batch * n_index * 4
 
 int64_t partial_bytes(int64_t batch, int64_t segments, int64_t n_index) {
   const int64_t c = bucket_chunks(batch, n_index);
-  return c > 1 ? batch * c * segments * 4 : 0;
+  return c > 1 ? (batch * c * segments * 4 + 15) / 16 * 16 : 0;
+}
+
+// Pairs per apply work tile: the mean pairs per segment (at least 512, a
+// multiple of the 64-pair MFMA tile), so balanced selections keep about one
+// tile per segment and a heavily selected segment is split.
+int64_t tile_pairs_for(int64_t segments, int64_t n_index) {
+  const int64_t mean = segments > 0 ? (n_index + segments - 1) / segments : n_index;
+  const int64_t tp = (mean + AP_N - 1) / AP_N * AP_N;
+  return tp > 8 * AP_N ? tp : 8 * AP_N;
+}
+
+// Tiles per sequence at most: sum_s ceil(c_s / tp) <= n_index / tp + segments.
+int64_t tiles_max(int64_t segments, int64_t n_index) {
+  const int64_t tp = tile_pairs_for(segments, n_index);
+  return (n_index + tp - 1) / tp + segments;
+}
+
+int64_t tiles_bytes(int64_t batch, int64_t segments, int64_t n_index) {
+  return batch * tiles_max(segments, n_index) * 16 + (batch * 4 + 15) / 16 * 16 + offsets_bytes(batch, segments);
 }
 
 }  // namespace
@@ -759,7 +826,8 @@ using namespace grmhip;
 
 extern "C" int64_t grm_hip_gather_apply_workspace(int64_t batch, int64_t segments, int64_t n_index) {
   if (batch <= 0 || segments < 0 || n_index <= 0) return 0;
-  return offsets_bytes(batch, segments) + list_bytes(batch, n_index) + partial_bytes(batch, segments, n_index);
+  return offsets_bytes(batch, segments) + list_bytes(batch, n_index) + partial_bytes(batch, segments, n_index) +
+         tiles_bytes(batch, segments, n_index);
 }
 
 extern "C" int grm_hip_gather_apply(const void* memories, const int64_t* indices, const void* queries, void* out,
@@ -786,7 +854,8 @@ extern "C" int grm_hip_gather_apply(const void* memories, const int64_t* indices
   }
   const int64_t n_index = n_query * routes;
   if (batch == 0 || n_index == 0 || hidden_size == 0) return GRM_HIP_OK;
-  if (n_index > INT32_MAX || hidden_size > INT32_MAX / 2 || batch * segments * ((hidden_size + AP_V - 1) / AP_V) > INT32_MAX) {
+  if (n_index > INT32_MAX || hidden_size > INT32_MAX / 2 || batch > 65535 ||
+      tiles_max(segments, n_index) * ((hidden_size + AP_V - 1) / AP_V) * AP_THREADS > UINT32_MAX) {
     set_error("gather_apply: sizes exceed one launch");
     return GRM_HIP_EINVAL;
   }
@@ -810,6 +879,17 @@ extern "C" int grm_hip_gather_apply(const void* memories, const int64_t* indices
   a.partial = reinterpret_cast<int32_t*>(static_cast<unsigned char*>(workspace) + offsets_bytes(batch, segments) +
                                          list_bytes(batch, n_index));
   a.bk_chunks = static_cast<int>(bucket_chunks(batch, n_index));
+  {
+    unsigned char* t0 = static_cast<unsigned char*>(workspace) + offsets_bytes(batch, segments) +
+                        list_bytes(batch, n_index) + partial_bytes(batch, segments, n_index);
+    a.tile_pairs = static_cast<int>(tile_pairs_for(segments, n_index));
+    a.tb_max = static_cast<int>(tiles_max(segments, n_index));
+    a.tiles = reinterpret_cast<int4*>(t0);
+    t0 += batch * a.tb_max * 16;
+    a.n_tiles = reinterpret_cast<int32_t*>(t0);
+    t0 += (batch * 4 + 15) / 16 * 16;
+    a.tile_base = reinterpret_cast<int32_t*>(t0);
+  }
   a.bad = bad_index_count;
   a.batch = batch;
   a.segments = segments;

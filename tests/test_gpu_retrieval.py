@@ -145,6 +145,32 @@ def test_gather_apply_widened(dev, mem_dtype, q_dtype, B, S, Q, R, H, K):
     assert torch.equal(op, out)
 
 
+@pytest.mark.parametrize("mem_dtype,q_dtype,H,K", [(torch.float32, torch.bfloat16, 128, 128),
+                                                   (torch.float16, torch.bfloat16, 256, 64),
+                                                   (torch.float32, torch.float32, 96, 32),
+                                                   (torch.float32, torch.float32, 40, 30)])
+def test_gather_apply_skewed_selection(dev, mem_dtype, q_dtype, H, K):
+    """Causal routing selects early segments far more often than late ones: segments
+    selected by many pairs are split over several work tiles.  Here segment 0 takes
+    every pair of most queries, segment 1 a third, the rest a thin random tail, and
+    some pairs are empty (-1)."""
+    g = torch.Generator().manual_seed(H + K)
+    B, S, Q, R = 2, 40, 3000, 4
+    mem = (torch.randn(B, S, H, K, generator=g) * 0.05).to(mem_dtype)
+    q = norm(torch.randn(B, Q, K, generator=g)).to(q_dtype)
+    idx = torch.randint(0, S, (B, Q, R), generator=g)
+    u = torch.rand(B, Q, R, generator=g)
+    idx[u < 0.6] = 0
+    idx[(u >= 0.6) & (u < 0.8)] = 1
+    idx[:, :50, 2:] = -1
+    out = capi.gather_apply(mem.to(dev), idx.to(dev), q.to(dev), dtype=torch.float32)
+    ok = idx >= 0
+    gathered, bad = orc.gather(mem.double().numpy(), idx.clamp(min=0).numpy())
+    ref = orc.apply_query(gathered, q.double().numpy())
+    ref[~ok.numpy()] = 0.0
+    np.testing.assert_allclose(out.cpu().double().numpy(), ref, rtol=1e-5, atol=1e-6)
+
+
 def test_gather_apply_bad_indices_and_rank2(dev):
     """Out-of-range indices give zero rows and are counted; rank-2 indices ([B, R]
     with queries [B, K]) go through the torch op like the reference's rank-4 apply."""
