@@ -93,7 +93,17 @@ def bench_c2(torch, dev, steps, warmup):
         if rc != 0:
             raise RuntimeError(capi.last_error())
 
-    wall, per = timed_launches(torch, step, steps, warmup, stream)
+    # value: K back-to-back steps between two synchronisations (no per-step events in the
+    # way); roofline: K more steps, each bracketed by HIP events on the kernels' stream.
+    for _ in range(warmup):
+        step()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        step()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    _, per = timed_launches(torch, step, steps, 0, stream)
     return wall, per, (k, v, q, m, hidden, snaps)
 
 
