@@ -337,27 +337,44 @@ __global__ __launch_bounds__(WR_THREADS) void route_window_kernel(const RouteArg
     out_s[m / 32][m % 32] = -INFINITY;
     out_i[m / 32][m % 32] = -1;
   }
+  // 16-byte units of one staged slice (WR_KC key rows and WR_ROWS query rows of
+  // WR_DT dims), and how many each thread moves.
+  constexpr int UNITS = (WR_KC + WR_ROWS) * (WR_DT / V);
+  constexpr int UPT = (UNITS + WR_THREADS - 1) / WR_THREADS;
   for (int kc0 = 0; kc0 < nk; kc0 += WR_KC) {
     float acc[WR_KPT];
 #pragma unroll
     for (int j = 0; j < WR_KPT; ++j) acc[j] = 0.f;
-    for (int d0 = 0; d0 < D; d0 += WR_DT) {
-      __syncthreads();  // previous slice consumed
-      // stage WR_KC key rows and WR_ROWS query rows of dims [d0, d0 + WR_DT)
-      for (int u = tid; u < (WR_KC + WR_ROWS) * (WR_DT / V); u += WR_THREADS) {
+    // The next slice's loads are issued before the current slice is computed.
+    uint4 st[UPT];
+    auto load_slice = [&](int d0) {
+#pragma unroll
+      for (int i = 0; i < UPT; ++i) {
+        const int u = tid + WR_THREADS * i;
         const int r = u / (WR_DT / V);
         const int c = (u % (WR_DT / V)) * V;
-        uint4 v = make_uint4(0, 0, 0, 0);
-        if (r < WR_KC) {
-          if (kc0 + r < nk && d0 + c < D) v = *reinterpret_cast<const uint4*>(kb + (kc0 + r) * static_cast<int64_t>(D) + d0 + c);
-          *reinterpret_cast<uint4*>(ktile + r * RS + c) = v;
-        } else {
-          const int qr = r - WR_KC;
-          if (r0 + qr < a.n_query && d0 + c < D) v = *reinterpret_cast<const uint4*>(qb + qr * static_cast<int64_t>(D) + d0 + c);
-          *reinterpret_cast<uint4*>(qtile + qr * RS + c) = v;
+        st[i] = make_uint4(0, 0, 0, 0);
+        if (u < UNITS && d0 + c < D) {
+          if (r < WR_KC) {
+            if (kc0 + r < nk) st[i] = *reinterpret_cast<const uint4*>(kb + (kc0 + r) * static_cast<int64_t>(D) + d0 + c);
+          } else if (r0 + (r - WR_KC) < a.n_query) {
+            st[i] = *reinterpret_cast<const uint4*>(qb + (r - WR_KC) * static_cast<int64_t>(D) + d0 + c);
+          }
         }
       }
+    };
+    load_slice(0);
+    for (int d0 = 0; d0 < D; d0 += WR_DT) {
+      __syncthreads();  // previous slice consumed
+#pragma unroll
+      for (int i = 0; i < UPT; ++i) {
+        const int u = tid + WR_THREADS * i;
+        const int r = u / (WR_DT / V);
+        const int c = (u % (WR_DT / V)) * V;
+        if (u < UNITS) *reinterpret_cast<uint4*>((r < WR_KC ? ktile + r * RS : qtile + (r - WR_KC) * RS) + c) = st[i];
+      }
       __syncthreads();
+      if (d0 + WR_DT < D) load_slice(d0 + WR_DT);
       const int dl = min(WR_DT, D - d0);
       for (int dd = 0; dd < dl; dd += V) {
         struct RV { raw e[V]; };
