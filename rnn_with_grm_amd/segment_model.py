@@ -48,7 +48,7 @@ replaced by their differentiable compositions.
 from __future__ import annotations
 
 import math
-from collections import deque
+from dataclasses import dataclass
 from typing import Any, Dict, List, Literal, Optional, Tuple
 
 import torch
@@ -62,9 +62,18 @@ from .archive import DeviceSegmentArchive, SegmentCheckpoint
 _NORM_EPS = 1e-6
 
 
+@dataclass
+class LinearMemoryState:
+    """Memory state of the linear cell (linear_attention.py:13-18)."""
+
+    memory: Tensor
+    h: Optional[Tensor] = None
+
+
 class LinearMemoryCell(nn.Module):
-    """Projections of the linear memory (linear_attention.py:21-60); same
-    parameters and initialisation order as the reference."""
+    """The linear memory cell (linear_attention.py:21-167); same parameters and
+    initialisation order as the reference.  Its recurrence runs on the chunked
+    scan: a whole sequence is one launch instead of one step per token."""
 
     def __init__(self, input_size: int, hidden_size: int, memory_key_dim: Optional[int] = None,
                  use_bias: bool = True, memory_init: Literal["zeros", "eye", "random"] = "zeros",
@@ -88,16 +97,44 @@ class LinearMemoryCell(nn.Module):
         if self.output_proj.bias is not None:
             nn.init.zeros_(self.output_proj.bias)
 
-    def init_memory(self, batch_size: int, device: torch.device, dtype: torch.dtype = torch.float32) -> Tensor:
+    def init_memory(self, batch_size: int, device: torch.device,
+                    dtype: torch.dtype = torch.float32) -> LinearMemoryState:
         shape = (batch_size, self.hidden_size, self.memory_key_dim)
         if self.memory_init == "zeros":
-            return torch.zeros(shape, device=device, dtype=dtype)
-        if self.memory_init == "eye":
+            memory = torch.zeros(shape, device=device, dtype=dtype)
+        elif self.memory_init == "eye":
             eye = torch.eye(self.hidden_size, self.memory_key_dim, device=device, dtype=dtype)
-            return eye.unsqueeze(0).expand(batch_size, -1, -1).clone()
-        if self.memory_init == "random":
-            return torch.randn(shape, device=device, dtype=dtype) * 0.02
-        raise ValueError(f"Unknown memory_init: {self.memory_init}")
+            memory = eye.unsqueeze(0).expand(batch_size, -1, -1).clone()
+        elif self.memory_init == "random":
+            memory = torch.randn(shape, device=device, dtype=dtype) * 0.02
+        else:
+            raise ValueError(f"Unknown memory_init: {self.memory_init}")
+        return LinearMemoryState(memory=memory)
+
+    def forward(self, x_t: Tensor, state: Optional[LinearMemoryState] = None) -> Tuple[Tensor, LinearMemoryState]:
+        """One token: M <- decay M + (1 - decay) v k^T / sqrt(d_k), h = M q, output_proj(h)
+        (linear_attention.py:97-121)."""
+        out, new_state = self.forward_sequence(x_t.unsqueeze(1), state)
+        return out[:, 0], new_state
+
+    def forward_sequence(self, x_seq: Tensor, state: Optional[LinearMemoryState] = None,
+                         return_all_outputs: bool = True) -> Tuple[Tensor, LinearMemoryState]:
+        """The per-token recurrence over x_seq [B, T, input] (linear_attention.py:123-167),
+        as one chunked scan."""
+        batch_size, seq_len, _ = x_seq.shape
+        if state is None:
+            state = self.init_memory(batch_size, x_seq.device, x_seq.dtype)
+        memory = state.memory
+        if seq_len == 0:
+            hidden = torch.zeros(batch_size, self.hidden_size, device=x_seq.device, dtype=x_seq.dtype)
+            output = self.output_proj(hidden)
+            outputs = x_seq.new_zeros(batch_size, 0, self.input_size) if return_all_outputs else output
+            return outputs, LinearMemoryState(memory=memory, h=hidden)
+        k, v, q = self.project(x_seq)
+        hidden, memory = cuda_ops.cuda_chunk_update(k, v, q, memory, self.memory_decay)
+        outputs = self.output_proj(hidden)
+        return (outputs if return_all_outputs else outputs[:, -1]), LinearMemoryState(memory=memory,
+                                                                                     h=hidden[:, -1])
 
     def project(self, x: Tensor, extra: Optional[nn.Linear] = None) -> Tuple[Tensor, ...]:
         """Normalised keys, values and normalised queries of every token, as one
@@ -116,8 +153,10 @@ class LinearMemoryCell(nn.Module):
 
 
 class TopKMemoryRetriever(nn.Module):
-    """Routing projections (gating_unit.py:14-92): same parameters, aliases
-    and initialisation as the reference."""
+    """Top-k retriever over segment summary keys (gating_unit.py:14-116): same
+    parameters, aliases and initialisation as the reference.  The models route
+    whole sequences through `cuda_segment_route`; `forward` is the reference's
+    per-query form."""
 
     def __init__(self, query_dim: int, key_dim: Optional[int] = None, hidden_dim: Optional[int] = None,
                  retrieval_top_k: int = 16, temperature: float = 1.0, use_causal_mask: bool = True,
@@ -141,6 +180,44 @@ class TopKMemoryRetriever(nn.Module):
         nn.init.xavier_uniform_(self.key_projection.weight)
         if self.output_projection is not None:
             nn.init.xavier_uniform_(self.output_projection.weight)
+
+    def _scores(self, query: Tensor, keys: Tensor, segment_offset: int) -> Tensor:
+        """Scaled projected dot products [B, S]; keys at or after segment_offset
+        masked out when 0 < segment_offset < S (gating_unit.py:63-80)."""
+        if keys.ndim == 2:
+            keys = keys.unsqueeze(0).expand(query.size(0), -1, -1)
+        pq = self.query_projection(query).unsqueeze(1)
+        pk = self.key_projection(keys)
+        scores = torch.matmul(pq, pk.transpose(-2, -1)).squeeze(1) * self.scale
+        num_keys = keys.size(1)
+        if self.use_causal_mask and 0 < segment_offset < num_keys:
+            later = torch.arange(num_keys, device=query.device) >= segment_offset
+            scores = scores.masked_fill(later.unsqueeze(0), float("-inf"))
+        return scores
+
+    def forward(self, query: Tensor, keys: Tensor, segment_offset: int = 0,
+                attention_mask: Optional[Tensor] = None) -> Tuple[Tensor, Tensor, Tensor]:
+        """One query per batch row against S keys: (routing weights, indices, scores)
+        (gating_unit.py:54-91).  k < S: the top k, descending; k >= S: every key in index order."""
+        scores = self._scores(query, keys, 0)
+        if attention_mask is not None:
+            scores = scores.masked_fill(~attention_mask.bool(), float("-inf"))
+        num_keys = scores.size(1)
+        if self.use_causal_mask and 0 < segment_offset < num_keys:
+            later = torch.arange(num_keys, device=query.device) >= segment_offset
+            scores = scores.masked_fill(later.unsqueeze(0), float("-inf"))
+        routes = min(self.retrieval_top_k, num_keys)
+        if routes < num_keys:
+            top, idx = torch.topk(scores, k=routes, dim=-1)
+        else:
+            top = scores
+            idx = torch.arange(num_keys, device=query.device).unsqueeze(0).expand(query.size(0), -1)
+        weights = self.dropout(F.softmax(top / self.temperature, dim=-1))
+        return weights, idx, scores
+
+    def compute_dense_routing_weights(self, query: Tensor, keys: Tensor, segment_offset: int = 0) -> Tensor:
+        """Softmax over every (unmasked) key (gating_unit.py:93-116)."""
+        return F.softmax(self._scores(query, keys, segment_offset) / self.temperature, dim=-1)
 
 
 class RetrievedStateFusion(nn.Module):
@@ -187,6 +264,61 @@ class RetrievedStateFusion(nn.Module):
     def fused_kernel_applies(self) -> bool:
         return self.retrieval_fusion_mode == "residual" and self.output_projection is None
 
+    def combine(self, online: Tensor, retrieved: Tensor,
+                routing_weights: Optional[Tensor] = None) -> Tuple[Tensor, Optional[Tensor]]:
+        """Weighted sum of [B, R, H] retrieved states (aggregator.py:67-104): uniform weights when
+        none are given; weights of another width are zero-padded or cut, then renormalised."""
+        if retrieved.size(1) == 0:
+            return torch.zeros_like(online), None
+        batch, routes, _ = retrieved.shape
+        w = routing_weights
+        if w is None:
+            w = torch.full((batch, routes), 1.0 / routes, device=online.device, dtype=online.dtype)
+        if w.dim() == 1:
+            w = w.unsqueeze(0)
+        if w.size(0) == 1 and batch > 1:
+            w = w.expand(batch, -1)
+        if w.size(1) != routes:
+            if w.size(1) < routes:
+                w = torch.cat([w, w.new_zeros(batch, routes - w.size(1))], dim=-1)
+            else:
+                w = w[:, :routes]
+            w = w / w.sum(dim=-1, keepdim=True).clamp(min=1e-9)
+        return (retrieved * w.unsqueeze(-1)).sum(dim=1), w
+
+    @staticmethod
+    def _states(online_state, retrieved_states, routing_weights, legacy: dict):
+        online_state = legacy.pop("h_online", None) if online_state is None else online_state
+        retrieved_states = legacy.pop("cached_states", None) if retrieved_states is None else retrieved_states
+        routing_weights = legacy.pop("gates", None) if routing_weights is None else routing_weights
+        if legacy:
+            raise TypeError(f"Unexpected keyword arguments: {', '.join(sorted(legacy))}")
+        if online_state is None or retrieved_states is None:
+            raise TypeError("`online_state` and `retrieved_states` must be provided.")
+        return online_state, retrieved_states, routing_weights
+
+    def forward(self, online_state: Optional[Tensor] = None, retrieved_states: Optional[Tensor] = None,
+                routing_weights: Optional[Tensor] = None, **legacy_kwargs) -> Tensor:
+        """Fused state [B, H] (aggregator.py:147-176); accepts the legacy names h_online,
+        cached_states and gates."""
+        online, retrieved, weights = self._states(online_state, retrieved_states, routing_weights, legacy_kwargs)
+        contribution, weights = self.combine(online, retrieved, weights)
+        return self.apply_rule(online, contribution, retrieved, weights)
+
+    def forward_with_auxiliary_statistics(self, online_state: Optional[Tensor] = None,
+                                          retrieved_states: Optional[Tensor] = None,
+                                          routing_weights: Optional[Tensor] = None,
+                                          **legacy_kwargs) -> Tuple[Tensor, Dict[str, float]]:
+        """The fused state plus norms, route count and routing entropy (aggregator.py:178-218)."""
+        online, retrieved, weights = self._states(online_state, retrieved_states, routing_weights, legacy_kwargs)
+        contribution, weights = self.combine(online, retrieved, weights)
+        fused = self.apply_rule(online, contribution, retrieved, weights)
+        entropy = 0.0 if weights is None else float(
+            (-(weights * torch.log(weights.clamp(min=1e-10))).sum(dim=-1).mean()).item())
+        stats = {"online_norm": float(online.norm().item()), "retrieved_norm": float(contribution.norm().item()),
+                 "num_retrieved": int(retrieved.size(1)), "routing_entropy": entropy}
+        return fused, stats
+
     def apply_rule(self, online: Tensor, contribution: Tensor, retrieved: Tensor, gates: Tensor) -> Tensor:
         """_apply_fusion_rule (aggregator.py:106-145) on [..., hidden] rows; retrieved [..., R, hidden]."""
         mode = self.retrieval_fusion_mode
@@ -202,8 +334,43 @@ class RetrievedStateFusion(nn.Module):
         elif mode == "linear":
             fused = self.online_projection(online) + self.memory_projection(contribution)
         else:  # memory_soup
-            fused = self.soup_projection(online + (retrieved * gates.unsqueeze(-1)).sum(dim=-2))
+            if retrieved.size(-2) == 0:
+                soup_input = online
+            else:
+                w = gates
+                if w is None:
+                    w = torch.full(retrieved.shape[:-1], 1.0 / max(1, retrieved.size(-2)), device=online.device,
+                                   dtype=online.dtype)
+                soup_input = online + (retrieved * w.unsqueeze(-1)).sum(dim=-2)
+            fused = self.soup_projection(soup_input)
         return self.dropout(self.layer_norm(fused))
+
+
+class ParameterMixtureFusion(nn.Module):
+    """LayerNorm(h + mean over layers l of sum_r g_r (w_l * r_r)) (aggregator.py:221-264)."""
+
+    def __init__(self, hidden_size: int, num_memory_layers: int = 2, segment_pooling_mode: str = "mean",
+                 use_layer_norm: bool = True, dropout: float = 0.1) -> None:
+        super().__init__()
+        self.hidden_size = hidden_size
+        self.num_memory_layers = num_memory_layers
+        self.segment_pooling_mode = segment_pooling_mode
+        self.segment_weights = nn.ParameterList(
+            [nn.Parameter(torch.full((hidden_size,), 0.1)) for _ in range(num_memory_layers)])
+        self.layer_norm = nn.LayerNorm(hidden_size) if use_layer_norm else nn.Identity()
+        self.dropout = nn.Dropout(dropout) if dropout > 0 else nn.Identity()
+
+    def forward(self, online_state: Tensor, retrieved_states: Tensor,
+                routing_weights: Optional[Tensor] = None) -> Tensor:
+        if retrieved_states.size(1) == 0:
+            return self.dropout(self.layer_norm(online_state))
+        batch, routes, _ = retrieved_states.shape
+        w = routing_weights
+        if w is None:
+            w = torch.full((batch, routes), 1.0 / routes, device=online_state.device, dtype=online_state.dtype)
+        mixed = [((retrieved_states * sw.view(1, 1, -1)) * w.unsqueeze(-1)).sum(dim=1) for sw in self.segment_weights]
+        mixture = mixed[0] if len(mixed) == 1 else torch.stack(mixed, dim=0).mean(dim=0)
+        return self.dropout(self.layer_norm(online_state + mixture))
 
 
 def _segment_means(x: Tensor, seg: int) -> Tensor:
@@ -295,7 +462,7 @@ class SegmentRecurrentMemoryModel(nn.Module):
         }
 
     def _init_memory(self, batch_size: int, device: torch.device, dtype: torch.dtype) -> Tensor:
-        return self.memory_cell.init_memory(batch_size, device, dtype)
+        return self.memory_cell.init_memory(batch_size, device, dtype).memory
 
     def clear_memory(self) -> None:
         self.memory_bank.clear()
@@ -430,11 +597,13 @@ class SegmentRecurrentMemoryModel(nn.Module):
 
         # The archive every segment of this sequence reads from: what was kept
         # before (deque order) followed by this sequence's segments, each state
-        # through the model dtype into the storage dtype as push() stores it.
+        # through the model dtype into the storage dtype as push() stores it,
+        # detached as the archive holds it (paper_grm.py:139-140): retrieval
+        # passes no gradient back into the scan or the summaries' inputs.
         bank = self.memory_bank
         storage = bank.memory_storage_dtype
-        new_states = snaps.to(dtype).to(storage)
-        new_summaries = _segment_means(x, seg).to(storage)
+        new_states = snaps.detach().to(dtype).to(storage)
+        new_summaries = _segment_means(x.detach(), seg).to(storage)
         ring = bank._groups.get(B)
         base = 0 if ring is None else len(ring)
         if base:
@@ -619,6 +788,16 @@ class HierarchicalSegmentMemoryModel(nn.Module):
         return self.layers[0].memory_bank
 
 
+def build_topk_memory_retriever(query_dim: int, key_dim: Optional[int] = None, retrieval_top_k: int = 16,
+                                **kwargs) -> TopKMemoryRetriever:
+    return TopKMemoryRetriever(query_dim=query_dim, key_dim=key_dim, retrieval_top_k=retrieval_top_k, **kwargs)
+
+
+def build_retrieved_state_fusion(hidden_size: int, retrieval_fusion_mode: str = "residual",
+                                 **kwargs) -> RetrievedStateFusion:
+    return RetrievedStateFusion(hidden_size=hidden_size, retrieval_fusion_mode=retrieval_fusion_mode, **kwargs)
+
+
 def build_segment_memory_model(input_size: int, hidden_size: int, output_size: int,
                                **kwargs) -> SegmentRecurrentMemoryModel:
     return SegmentRecurrentMemoryModel(input_size=input_size, hidden_size=hidden_size, output_size=output_size,
@@ -634,10 +813,14 @@ def build_hierarchical_segment_memory_model(input_size: int, hidden_size: int, o
 __all__ = [
     "HierarchicalSegmentMemoryModel",
     "LinearMemoryCell",
+    "LinearMemoryState",
+    "ParameterMixtureFusion",
     "RetrievedStateFusion",
     "SegmentRecurrentMemoryLayer",
     "SegmentRecurrentMemoryModel",
     "TopKMemoryRetriever",
     "build_hierarchical_segment_memory_model",
+    "build_retrieved_state_fusion",
     "build_segment_memory_model",
+    "build_topk_memory_retriever",
 ]

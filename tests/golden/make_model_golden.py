@@ -117,9 +117,107 @@ def run_cases(multilayer_grm, paper_grm, storage: torch.dtype, tag: str, data: d
         data[p + name] = t.numpy()
 
 
+def gradient_case(multilayer_grm, data: dict) -> None:
+    """Case G: the hierarchical model of case A in training mode (dropout 0,
+    float32 archive), two calls, the second reading the first's archive; the
+    gradient of the summed squared outputs for every parameter."""
+    torch.manual_seed(7)
+    model = multilayer_grm.HierarchicalSegmentMemoryModel(
+        input_size=32, hidden_size=24, output_size=16, num_layers=2, segment_length=8, memory_capacity_segments=5,
+        retrieval_top_k=3, memory_key_dim=8, dropout=0.0, recomputation_ratio=0.0,
+        memory_storage_dtype=torch.float32).train()
+    flat_state("G_", model, data)
+    g = torch.Generator().manual_seed(8)
+    x1 = torch.randn(2, 43, 32, generator=g)
+    x2 = torch.randn(2, 21, 32, generator=g)
+    o1, _, _, _ = model(x1)
+    o2, _, _, _ = model(x2)
+    (o1.square().mean() + o2.square().mean()).backward()
+    data["G_x1"], data["G_x2"] = x1.numpy(), x2.numpy()
+    data["G_out1"], data["G_out2"] = o1.detach().numpy(), o2.detach().numpy()
+    for name, prm in model.named_parameters():
+        if prm.grad is not None:
+            data[f"G_grad:{name}"] = prm.grad.numpy()
+
+
+def submodule_cases(data: dict) -> None:
+    """The building blocks the models are made of, called directly: the linear
+    memory cell, the per-query retriever (with the causal segment mask), every
+    fusion rule with and without routing weights, and the parameter-mixture fusion."""
+    from grm.core.aggregator import ParameterMixtureFusion, RetrievedStateFusion
+    from grm.core.gating_unit import TopKMemoryRetriever
+    from grm.core.linear_attention import LinearMemoryCell
+
+    g = torch.Generator().manual_seed(9)
+    torch.manual_seed(11)
+    cell = LinearMemoryCell(16, 12, memory_key_dim=8, memory_decay=0.9)
+    flat_state("Dcell_", cell, data)
+    xs = torch.randn(2, 9, 16, generator=g)
+    with torch.no_grad():
+        outs, st = cell.forward_sequence(xs)
+        last, st1 = cell.forward(xs[:, 0], st)
+        last_only, _ = cell.forward_sequence(xs, return_all_outputs=False)
+    for name, t in (("xs", xs), ("outs", outs), ("mem", st.memory), ("h", st.h), ("step_out", last),
+                    ("step_mem", st1.memory), ("step_h", st1.h), ("last_only", last_only)):
+        data["Dcell_" + name] = t.numpy()
+
+    torch.manual_seed(12)
+    ret = TopKMemoryRetriever(12, retrieval_top_k=3, dropout=0.0)
+    flat_state("Dret_", ret, data)
+    q = torch.randn(3, 12, generator=g)
+    keys = torch.randn(3, 7, 12, generator=g)
+    keys2 = torch.randn(7, 12, generator=g)
+    mask = torch.rand(3, 7, generator=g) > 0.3
+    with torch.no_grad():
+        cases = {"off5": ret(q, keys, segment_offset=5), "off0": ret(q, keys), "k2d": ret(q, keys2, segment_offset=2),
+                 "mask": ret(q, keys, attention_mask=mask)}
+        dense = ret.compute_dense_routing_weights(q, keys, segment_offset=4)
+    ret8 = TopKMemoryRetriever(12, retrieval_top_k=8, dropout=0.0)
+    ret8.load_state_dict(ret.state_dict())
+    with torch.no_grad():
+        cases["all"] = ret8(q, keys, segment_offset=3)
+    data["Dret_q"], data["Dret_keys"], data["Dret_keys2"] = q.numpy(), keys.numpy(), keys2.numpy()
+    data["Dret_mask"] = mask.numpy()
+    for name, (w, i, sc) in cases.items():
+        data[f"Dret_{name}_w"], data[f"Dret_{name}_i"], data[f"Dret_{name}_s"] = w.numpy(), i.numpy(), sc.numpy()
+    data["Dret_dense"] = dense.numpy()
+
+    online = torch.randn(4, 10, generator=g)
+    retrieved = torch.randn(4, 3, 10, generator=g)
+    weights = torch.softmax(torch.randn(4, 3, generator=g), -1)
+    data["Dfus_online"], data["Dfus_retrieved"], data["Dfus_weights"] = (online.numpy(), retrieved.numpy(),
+                                                                          weights.numpy())
+    modes = [("residual", False), ("residual", True), ("concat", False), ("gate", False), ("linear", False),
+             ("memory_soup", False)]
+    for n, (mode, proj) in enumerate(modes):
+        torch.manual_seed(20 + n)
+        fus = RetrievedStateFusion(10, retrieval_fusion_mode=mode, use_output_projection=proj, dropout=0.0)
+        pre = f"Dfus{n}_"
+        flat_state(pre, fus, data)
+        with torch.no_grad():
+            out, stats = fus.forward_with_auxiliary_statistics(online, retrieved, weights)
+            short = fus(online_state=online, retrieved_states=retrieved, routing_weights=weights[:, :2])
+            none_w = fus(h_online=online, cached_states=retrieved)
+            empty = fus(online, retrieved[:, :0], None)
+        data[pre + "out"], data[pre + "short"], data[pre + "none"], data[pre + "empty"] = (
+            out.numpy(), short.numpy(), none_w.numpy(), empty.numpy())
+        data[pre + "stats"] = np.array([stats["online_norm"], stats["retrieved_norm"], stats["num_retrieved"],
+                                        stats["routing_entropy"]])
+    torch.manual_seed(30)
+    mix = ParameterMixtureFusion(10, num_memory_layers=2, dropout=0.0)
+    with torch.no_grad():
+        mix.segment_weights[1].add_(torch.randn(10, generator=g) * 0.1)
+        data["Dmix_out"] = mix(online, retrieved, weights).numpy()
+        data["Dmix_none"] = mix(online, retrieved).numpy()
+        data["Dmix_empty"] = mix(online, retrieved[:, :0]).numpy()
+    flat_state("Dmix_", mix, data)
+
+
 def main() -> int:
     multilayer_grm, paper_grm = import_reference_core()
     data = {}
+    submodule_cases(data)
+    gradient_case(multilayer_grm, data)
     # float16 archives (the reference's default) and float32 archives (its
     # trainer's stage 1): the float32 ones pin the composition without the
     # float16 round trip, whose rounding boundaries a different float32

@@ -190,3 +190,141 @@ def test_training_mode_gradients_flow():
     for p in (grm.memory_cell.key_proj.weight, grm.memory_cell.value_proj.weight, grm.memory_cell.query_proj.weight,
               grm.gating_unit.query_projection.weight, grm.gating_unit.key_projection.weight, grm.output_proj.weight):
         assert p.grad is not None and torch.isfinite(p.grad).all() and p.grad.abs().sum() > 0
+
+
+def _load(module: torch.nn.Module, prefix: str) -> torch.nn.Module:
+    sd = {k[len(prefix) + 2:]: torch.from_numpy(FIX[k]) for k in FIX.files if k.startswith(prefix + "w:")}
+    module.load_state_dict(sd, strict=True)
+    return module.eval()
+
+
+def _cpu(name):
+    return torch.from_numpy(FIX[name])
+
+
+def _eq(a, name, rtol=2e-5, atol=2e-6):
+    np.testing.assert_allclose(a.detach().float().numpy(), FIX[name], rtol=rtol, atol=atol, err_msg=name)
+
+
+def test_linear_memory_cell_matches_reference():
+    """The cell's per-token recurrence (linear_attention.py:97-167) as one chunked scan: a whole
+    sequence, one step continuing from its state, and the last output only."""
+    cell = _load(sm.LinearMemoryCell(16, 12, memory_key_dim=8, memory_decay=0.9), "Dcell_")
+    xs = _cpu("Dcell_xs")
+    with torch.no_grad():
+        outs, st = cell.forward_sequence(xs)
+        step, st1 = cell(xs[:, 0], st)
+        last, _ = cell.forward_sequence(xs, return_all_outputs=False)
+        empty, st0 = cell.forward_sequence(xs[:, :0], return_all_outputs=False)
+    assert isinstance(st, sm.LinearMemoryState)
+    for a, n in ((outs, "outs"), (st.memory, "mem"), (st.h, "h"), (step, "step_out"), (st1.memory, "step_mem"),
+                 (st1.h, "step_h"), (last, "last_only")):
+        _eq(a, "Dcell_" + n)
+    # an empty sequence returns the output of a zero hidden state and leaves the memory alone
+    np.testing.assert_array_equal(empty.numpy(), np.broadcast_to(FIX["Dcell_w:output_proj.bias"], (2, 16)))
+    assert st0.memory.abs().sum() == 0 and st0.h.shape == (2, 12)
+
+
+@pytest.mark.parametrize("name", ["off5", "off0", "k2d", "mask", "all"])
+def test_topk_retriever_matches_reference(name):
+    """Per-query routing (gating_unit.py:54-91): the causal segment mask, shared 2-D keys, an
+    attention mask, and k >= S taking every key in index order."""
+    ret = _load(sm.TopKMemoryRetriever(12, retrieval_top_k=8 if name == "all" else 3, dropout=0.0), "Dret_")
+    q, keys, keys2, mask = _cpu("Dret_q"), _cpu("Dret_keys"), _cpu("Dret_keys2"), _cpu("Dret_mask")
+    call = {"off5": lambda: ret(q, keys, segment_offset=5), "off0": lambda: ret(q, keys),
+            "k2d": lambda: ret(q, keys2, segment_offset=2), "mask": lambda: ret(q, keys, attention_mask=mask),
+            "all": lambda: ret(q, keys, segment_offset=3)}[name]
+    with torch.no_grad():
+        w, i, sc = call()
+    np.testing.assert_array_equal(i.numpy(), FIX[f"Dret_{name}_i"])
+    _eq(w, f"Dret_{name}_w")
+    _eq(sc, f"Dret_{name}_s")
+
+
+def test_topk_retriever_dense_weights_match_reference():
+    ret = _load(sm.TopKMemoryRetriever(12, retrieval_top_k=3, dropout=0.0), "Dret_")
+    with torch.no_grad():
+        _eq(ret.compute_dense_routing_weights(_cpu("Dret_q"), _cpu("Dret_keys"), segment_offset=4), "Dret_dense")
+
+
+FUSION_MODES = [("residual", False), ("residual", True), ("concat", False), ("gate", False), ("linear", False),
+                ("memory_soup", False)]
+
+
+@pytest.mark.parametrize("n", range(len(FUSION_MODES)))
+def test_fusion_rules_match_reference(n):
+    """Every fusion rule (aggregator.py:67-218): given weights, weights of the wrong width
+    (padded and renormalised), none (uniform, through the legacy keyword names), no retrieved
+    states at all, and the auxiliary statistics."""
+    mode, proj = FUSION_MODES[n]
+    fus = _load(sm.RetrievedStateFusion(10, retrieval_fusion_mode=mode, use_output_projection=proj, dropout=0.0),
+                f"Dfus{n}_")
+    online, retrieved, weights = _cpu("Dfus_online"), _cpu("Dfus_retrieved"), _cpu("Dfus_weights")
+    with torch.no_grad():
+        out, stats = fus.forward_with_auxiliary_statistics(online, retrieved, weights)
+        short = fus(online_state=online, retrieved_states=retrieved, routing_weights=weights[:, :2])
+        none_w = fus(h_online=online, cached_states=retrieved)
+        empty = fus(online, retrieved[:, :0], None)
+    p = f"Dfus{n}_"
+    for a, name in ((out, "out"), (short, "short"), (none_w, "none"), (empty, "empty")):
+        _eq(a, p + name)
+    got = [stats["online_norm"], stats["retrieved_norm"], stats["num_retrieved"], stats["routing_entropy"]]
+    np.testing.assert_allclose(got, FIX[p + "stats"], rtol=1e-5, atol=1e-6)
+    with pytest.raises(TypeError):
+        fus(online, retrieved, weights, cached=retrieved)
+    with pytest.raises(TypeError):
+        fus(online_state=online)
+
+
+def test_parameter_mixture_fusion_matches_reference():
+    mix = _load(sm.ParameterMixtureFusion(10, num_memory_layers=2, dropout=0.0), "Dmix_")
+    online, retrieved, weights = _cpu("Dfus_online"), _cpu("Dfus_retrieved"), _cpu("Dfus_weights")
+    with torch.no_grad():
+        _eq(mix(online, retrieved, weights), "Dmix_out")
+        _eq(mix(online, retrieved), "Dmix_none")
+        _eq(mix(online, retrieved[:, :0]), "Dmix_empty")
+
+
+def test_builders():
+    ret = sm.build_topk_memory_retriever(12, retrieval_top_k=5, dropout=0.0)
+    assert isinstance(ret, sm.TopKMemoryRetriever) and ret.retrieval_top_k == 5 and ret.key_dim == 12
+    fus = sm.build_retrieved_state_fusion(10, "gate")
+    assert isinstance(fus, sm.RetrievedStateFusion) and fus.gate_projection is not None
+
+
+def case_g(dev):
+    """Training mode: two calls with autograd on, the second reading the first's archive,
+    against the reference model's parameter gradients (the archive is detached there too,
+    so retrieval passes gradient to the routing and fusion weights and the current token's
+    query only)."""
+    model = sm.HierarchicalSegmentMemoryModel(
+        input_size=32, hidden_size=24, output_size=16, num_layers=2, segment_length=8, memory_capacity_segments=5,
+        retrieval_top_k=3, memory_key_dim=8, dropout=0.0, recomputation_ratio=0.0,
+        memory_storage_dtype=torch.float32)
+    load_weights(model, "G_")
+    model = model.to(dev).train()
+    o1, _, _, _ = model(t("G_x1", dev))
+    o2, _, _, _ = model(t("G_x2", dev))
+    (o1.square().mean() + o2.square().mean()).backward()
+    rtol, atol = TOL[(dev.type, "32")]
+    close(o1, "G_out1", "32")
+    close(o2, "G_out2", "32")
+    for name, prm in model.named_parameters():
+        key = f"G_grad:{name}"
+        if key not in FIX.files:
+            assert prm.grad is None or not prm.grad.any(), name
+            continue
+        ref = FIX[key]
+        scale = float(np.abs(ref).max())
+        np.testing.assert_allclose(prm.grad.float().cpu().numpy(), ref, rtol=rtol * 10, atol=atol * 10 * max(scale, 1.0),
+                                   err_msg=name)
+
+
+def test_training_gradients_match_reference_cpu():
+    case_g(torch.device("cpu"))
+
+
+@pytest.mark.gpu
+def test_training_gradients_match_reference_gpu(dev):
+    print(f"training gradients case G on {dev}", flush=True)
+    case_g(dev)
