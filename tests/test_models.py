@@ -206,23 +206,38 @@ def _eq(a, name, rtol=2e-5, atol=2e-6):
     np.testing.assert_allclose(a.detach().float().numpy(), FIX[name], rtol=rtol, atol=atol, err_msg=name)
 
 
-def test_linear_memory_cell_matches_reference():
+def cell_case(dev):
     """The cell's per-token recurrence (linear_attention.py:97-167) as one chunked scan: a whole
     sequence, one step continuing from its state, and the last output only."""
-    cell = _load(sm.LinearMemoryCell(16, 12, memory_key_dim=8, memory_decay=0.9), "Dcell_")
-    xs = _cpu("Dcell_xs")
+    cell = _load(sm.LinearMemoryCell(16, 12, memory_key_dim=8, memory_decay=0.9), "Dcell_").to(dev)
+    xs = _cpu("Dcell_xs").to(dev)
     with torch.no_grad():
         outs, st = cell.forward_sequence(xs)
         step, st1 = cell(xs[:, 0], st)
         last, _ = cell.forward_sequence(xs, return_all_outputs=False)
         empty, st0 = cell.forward_sequence(xs[:, :0], return_all_outputs=False)
     assert isinstance(st, sm.LinearMemoryState)
+    rtol, atol = TOL[(dev.type, "32")]
     for a, n in ((outs, "outs"), (st.memory, "mem"), (st.h, "h"), (step, "step_out"), (st1.memory, "step_mem"),
                  (st1.h, "step_h"), (last, "last_only")):
-        _eq(a, "Dcell_" + n)
+        _eq(a.cpu(), "Dcell_" + n, rtol, atol)
     # an empty sequence returns the output of a zero hidden state and leaves the memory alone
-    np.testing.assert_array_equal(empty.numpy(), np.broadcast_to(FIX["Dcell_w:output_proj.bias"], (2, 16)))
+    np.testing.assert_array_equal(empty.cpu().numpy(), np.broadcast_to(FIX["Dcell_w:output_proj.bias"], (2, 16)))
     assert st0.memory.abs().sum() == 0 and st0.h.shape == (2, 12)
+
+
+def test_linear_memory_cell_matches_reference():
+    cell_case(torch.device("cpu"))
+
+
+@pytest.mark.gpu
+def test_linear_memory_cell_matches_reference_gpu(dev):
+    from rnn_with_grm_amd import cuda_ops
+
+    before = cuda_ops._EXTENSION_MODULE.hip_launch_count()
+    print(f"linear memory cell on {dev}", flush=True)
+    cell_case(dev)
+    assert cuda_ops._EXTENSION_MODULE.hip_launch_count() > before
 
 
 @pytest.mark.parametrize("name", ["off5", "off0", "k2d", "mask", "all"])
