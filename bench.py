@@ -460,7 +460,7 @@ def main() -> int:
     log(f"c2: {t_kernel * 1e6:.1f} us/launch (events), {t_step * 1e6:.1f} us/step (wall)")
 
     traffic = None
-    tfile = REPO / "profiles" / "scan_wide_c2_traffic.json"
+    tfile = REPO / "profiles" / "scan_vsplit_c2_traffic.json"
     if tfile.exists():
         try:
             traffic = json.loads(tfile.read_text()).get("hbm_bytes_per_launch")
@@ -565,7 +565,7 @@ def main() -> int:
                    "global_batch": 64, "seq_len": 2048, "parallelism": "single GPU"},
         "roofline": {"bound": "hbm", "achieved": round(achieved_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved_gbs / HBM_PEAK_GBS, 4), "traffic": traffic,
-                     "kernel": "scan_wide_kernel<BF16,128>: state pass + full pass of one grm_hip_chunk_update_fwd call",
+                     "kernel": "scan_vsplit_kernel<BF16,128,4>: the one launch of a grm_hip_chunk_update_fwd call",
                      "algorithmic_bytes_per_launch": bytes_,
                      "kernel_us": round(t_kernel * 1e6, 2),
                      "mfma": {"TFLOP/s": round(tflops, 2), "peak": BF16_PEAK_TFLOPS,

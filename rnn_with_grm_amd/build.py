@@ -28,8 +28,8 @@ LIB_HIP = PKG_DIR / "libgrm_hip.so"
 LIB_EXT = PKG_DIR / "grm_cuda_ext.so"
 
 OFFLOAD_ARCH = "gfx950"
-HIP_SOURCES = ["grm_capi.hip", "chunk_scan.hip", "chunk_scan_wide.hip", "chunk_bwd.hip", "gather_apply.hip",
-               "retrieve.hip", "route_fuse.hip"]
+HIP_SOURCES = ["grm_capi.hip", "chunk_scan.hip", "chunk_scan_wide.hip", "chunk_scan_vsplit.hip", "chunk_bwd.hip",
+               "gather_apply.hip", "retrieve.hip", "route_fuse.hip"]
 EXT_SOURCE = "grm_torch_ops.cpp"
 
 # Packed fp32 instructions are kept out of every kernel (the flag is for the

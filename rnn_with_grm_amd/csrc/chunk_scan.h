@@ -54,4 +54,16 @@ bool wide_supported(int in_dtype, int64_t key_dim, int64_t value_dim, bool vec);
 // parts, the combine step), then the full pass.
 int launch_scan_wide(const ChunkFwdArgs& a, int in_dtype, int mem_dtype, hipStream_t stream);
 
+// Value columns per workgroup of the value-split kernel, and the chunks its
+// loads run ahead of the chunk being scanned.
+constexpr int kVsplitDv = 32;
+constexpr int kVsplitPrefetch = 4;
+
+// The value-split kernel covers what the wide kernel covers with value_dim a
+// multiple of kVsplitDv; one workgroup walks each (sequence, value tile).
+bool vsplit_supported(int in_dtype, int64_t key_dim, int64_t value_dim, bool vec);
+
+// Launches the value-split kernel (a.n_parts must be 1, a.v_tiles = value_dim / kVsplitDv).
+int launch_scan_vsplit(const ChunkFwdArgs& a, int in_dtype, hipStream_t stream);
+
 }  // namespace grmhip

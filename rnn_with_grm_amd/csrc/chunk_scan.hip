@@ -619,6 +619,7 @@ bool vec_ok(const void* keys, const void* values, const void* queries, const voi
 
 struct Plan {
   bool wide;      // 128-wide value tiles (chunk_scan_wide.hip)
+  bool vsplit;    // 32-wide value tiles, whole sequence per workgroup (chunk_scan_vsplit.hip)
   int chunk;
   int64_t n_chunks;
   int dv_tile;
@@ -635,15 +636,28 @@ bool use_wide(int in_dtype, int64_t key_dim, int64_t value_dim, bool vec) {
   return wide_supported(in_dtype, key_dim, value_dim, vec);
 }
 
+// The value-split kernel where the wide kernel would need time parts (fewer
+// than 192 sequence x 128-column workgroups) and 32-column tiles give at least
+// as many workgroups instead.  GRM_HIP_CHUNK_VSPLIT=0 turns it off, =1 uses it
+// wherever it is supported.
+bool use_vsplit(int in_dtype, int64_t batch, int64_t key_dim, int64_t value_dim, bool vec, bool wide) {
+  if (!wide || !vsplit_supported(in_dtype, key_dim, value_dim, vec)) return false;
+  const char* env = getenv("GRM_HIP_CHUNK_VSPLIT");
+  if (env != nullptr && (env[0] == '0' || env[0] == '1')) return env[0] == '1';
+  const int64_t wide_wgs = batch * ((value_dim + kWideDv - 1) / kWideDv);
+  return wide_wgs < 192 && batch * (value_dim / kVsplitDv) >= 192;
+}
+
 Plan make_plan(int64_t batch, int64_t seq_len, int64_t value_dim, int64_t key_dim,
-               int64_t snapshot_len, bool vec, bool wide) {
+               int64_t snapshot_len, bool vec, bool wide, bool vsplit = false) {
   Plan p;
-  p.wide = wide;
+  p.wide = wide && !vsplit;
+  p.vsplit = vsplit;
   p.chunk = snapshot_len > 0 ? chunk_for_snapshot(snapshot_len) : CT;
   p.n_chunks = (seq_len + p.chunk - 1) / p.chunk;
-  p.dv_tile = wide ? kWideDv : (vec ? tile_dv_for(batch, value_dim) : 16);
+  p.dv_tile = vsplit ? kVsplitDv : wide ? kWideDv : (vec ? tile_dv_for(batch, value_dim) : 16);
   p.v_tiles = static_cast<int>((value_dim + p.dv_tile - 1) / p.dv_tile);
-  p.n_parts = parts_for(batch * p.v_tiles, p.n_chunks);
+  p.n_parts = vsplit ? 1 : parts_for(batch * p.v_tiles, p.n_chunks);
   p.part_chunks = static_cast<int>((p.n_chunks + p.n_parts - 1) / p.n_parts);
   p.n_parts = static_cast<int>((p.n_chunks + p.part_chunks - 1) / p.part_chunks);
   if (p.n_parts < 1) p.n_parts = 1;
@@ -730,7 +744,9 @@ extern "C" int grm_hip_chunk_update_fwd(const void* keys, const void* values, co
   const bool vec_m = (key_dim % 4 == 0) && aligned(memory, 4 * mem_b) && aligned(memory_out, 4 * mem_b) &&
                      (snapshots == nullptr || aligned(snapshots, 16)) && aligned(workspace, 16);
   const bool wide = vec_m && use_wide(in_dtype, key_dim, value_dim, vec);
-  Plan plan = make_plan(batch, seq_len, value_dim, key_dim, snapshots != nullptr ? snapshot_len : 0, vec, wide);
+  const bool vsplit = use_vsplit(in_dtype, batch, key_dim, value_dim, vec, wide);
+  Plan plan = make_plan(batch, seq_len, value_dim, key_dim, snapshots != nullptr ? snapshot_len : 0, vec, wide,
+                        vsplit);
   if (plan.n_chunks > INT32_MAX) {
     set_error("chunk_update_fwd: seq_len too large");
     return GRM_HIP_EINVAL;
@@ -774,6 +790,7 @@ extern "C" int grm_hip_chunk_update_fwd(const void* keys, const void* values, co
     }
     return GRM_HIP_OK;
   }
+  if (plan.vsplit) return launch_scan_vsplit(a, in_dtype, s);
   if (plan.wide) return launch_scan_wide(a, in_dtype, mem_dtype, s);
   switch (in_dtype) {
     case GRM_HIP_F32: return dispatch_dv<F32>(a, dv_tile, vec, s);

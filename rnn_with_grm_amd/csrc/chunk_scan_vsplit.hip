@@ -1,0 +1,509 @@
+// Fused chunked linear-memory update + query application (forward), value-split
+// variant for bf16 / f16 inputs with key_dim <= 128, gfx950.
+//
+// Maths (reference grm/core/cuda_ops.py:218-254 chunked form; the per-token
+// recurrence of grm/csrc/chunk_update.cu:82-123 and grm_cuda.cpp:74-83 is the
+// same map): for a chunk of L tokens starting from state M (rows = value
+// index v, columns = key index k), with c = (1 - decay) / sqrt(d_k),
+//   h_i  = decay^{i+1} M q_i + c * sum_{j<=i} decay^{i-j} (q_i . k_j) v_j
+//   M'   = decay^L M + c * sum_j decay^{L-1-j} v_j k_j^T
+//
+// Work decomposition.  Value columns are independent given K and Q, so each
+// sequence is split into 32-column value tiles, one workgroup each, and every
+// workgroup walks the whole sequence: no time split, no state pass, no re-read
+// of K and V.  The tiles of one sequence run on one XCD and read the same K
+// and Q rows, which the XCD's L2 serves after the first.
+//
+// The eight waves form a two-stage pipeline with one barrier per chunk; each
+// half runs its own loop (same barrier count), so neither carries the other's
+// registers.  In the step that scans chunk c:
+//   P waves (0-3)  issue the loads of chunk c + PF (registers hold PF chunks),
+//                  stage chunk c + 2 into LDS, flush the output tile of chunk
+//                  c - 1, and compute S = Q K^T of chunk c + 1 (wave p: query block p against the
+//                  key blocks at or below the diagonal), publishing
+//                  P = S * c * decay^{i-j};
+//   M waves (4-7)  wave (vh, kh): state rows v in [16 vh, +16) and key
+//                  columns [kh d/2, +d/2) as fp32 MFMA accumulators; they form
+//                  O^T = decay^{i+1} M Q^T + V^T P^T for value rows [16 vh, +16)
+//                  and queries [32 kh, +32) (M read from a 16-bit copy in LDS
+//                  that they rewrite after each update), then
+//                  M^T = decay^L M^T + K^T (w V), and the snapshot.
+// Chunk data lives in three LDS stage buffers (written two steps ahead, read
+// by the P waves one step ahead and by the M waves in their step); P, the
+// output tile and the 16-bit state copy are double-buffered.  K^T and V^T
+// operands come from the row-major tiles through the LDS transpose read
+// (ds_read_b64_tr_b16).  K, Q, V and the output tile have unpadded rows whose
+// 16-byte granules are XOR-swizzled by row, so that both the 16-byte reads of
+// 16 rows and the transposed 8-byte reads of 8 rows x 32 bytes (one half-wave)
+// land on distinct banks.
+#include <stdint.h>
+#include <string.h>
+
+#include "chunk_scan.h"
+#include "grm_hip.h"
+#include "grm_hip_common.h"
+
+namespace grmhip {
+namespace {
+
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef short s16x4 __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
+
+constexpr int kVsThreads = 512;   // 8 waves, two per SIMD
+constexpr int kVsPThreads = 256;  // the P waves
+constexpr int kVsStages = 3;      // LDS stage buffers
+
+template <class E, int DKP>
+struct VsShape {
+  using raw = typename ET<E>::raw;
+  static constexpr int DVT = kVsplitDv;  // value columns per workgroup
+  // Row strides (elements): K, Q, V and the output tile unpadded and
+  // swizzled (kq_at, v_at, o_at); the 16-bit state 4 banks mod 64, so the
+  // 16-byte reads of 16 rows are conflict-free; P 34 banks, the 8-byte reads
+  // of 16 rows on 32 distinct banks.
+  static constexpr int KS = DKP;
+  static constexpr int MS = DKP + 8;
+  static constexpr int VS = DVT;
+  static constexpr int PS = CT + 4;
+  static constexpr int OS = DVT;
+  static constexpr int KH = DKP / 2;   // key columns of one M wave's state
+  static constexpr int KT = KH / 16;   // 16-wide state tiles per M wave
+  static constexpr int NKK = DKP / 32; // 32-deep key steps
+  static constexpr int KU = DKP / 8;   // 16-byte units per K/Q row
+  static constexpr int VU = DVT / 8;   // 16-byte units per V / output row
+  static constexpr int K_UNITS = CT * KU / kVsPThreads;
+  static constexpr int BUF = CT * (2 * KS + VS);  // K, Q, V of one chunk
+  static constexpr int MB = DVT * MS;             // one 16-bit state copy
+  static constexpr size_t lds_elems =
+      static_cast<size_t>(kVsStages * BUF + 2 * CT * PS + 2 * CT * OS + 2 * MB);
+  static constexpr size_t lds_bytes = lds_elems * sizeof(raw) + PW_N * sizeof(float);
+  static_assert(K_UNITS * kVsPThreads == CT * KU && CT * VU == kVsPThreads, "tiles split evenly");
+  static_assert(lds_bytes <= kMaxLds, "tile set must fit one CU's LDS");
+};
+
+// Element offsets in the swizzled tiles; col is a multiple of 4 (an 8- or
+// 16-byte piece inside one 16-byte granule).  K/Q rows of DKP elements:
+// granule (col / 8) ^ s(row), s(row) = 2 (row & 7) | bit 3 of row for 16
+// granules per row, 2 ((row >> 1) & 3) | bit 3 of row for 8; rows 16 apart
+// share s, so the two halves of a transposed fragment are 16 rows apart.
+// V rows (32 elements): granule ^ 2 * bit 2 of row.  Output rows (32
+// elements): granule ^ ((row >> 2) & 3).
+template <int DKP>
+__device__ __forceinline__ int kq_at(int row, int col) {
+  const int s = DKP == 128 ? (((row & 7) << 1) | ((row >> 3) & 1)) : ((((row >> 1) & 3) << 1) | ((row >> 3) & 1));
+  return row * DKP + ((((col >> 3) ^ s)) << 3) + (col & 7);
+}
+__device__ __forceinline__ int v_at(int row, int col) {
+  return row * kVsplitDv + (((col >> 3) ^ (((row >> 2) & 1) << 1)) << 3) + (col & 7);
+}
+__device__ __forceinline__ int o_at(int row, int col) {
+  return row * kVsplitDv + (((col >> 3) ^ ((row >> 2) & 3)) << 3) + (col & 7);
+}
+
+// Stores of results nothing in this kernel reads again (hidden rows,
+// snapshots, the final state) carry the non-temporal policy: without it the
+// 20 KB a workgroup writes per chunk displace, in the XCD's L2, the K and Q
+// lines its sibling value tiles are about to read, and the scan runs ~25%
+// slower.  (Loads keep the default policy: K, Q and the 64-byte V slices are
+// shared between the tiles of a sequence.)
+constexpr int kStreamStore = 2;  // cache-policy bit NT
+
+__device__ __forceinline__ void store_stream(__amdgpu_buffer_rsrc_t r, int off, u32x4 v) {
+  __builtin_amdgcn_raw_buffer_store_b128(v, r, off, 0, kStreamStore);
+}
+__device__ __forceinline__ void store_stream_f32x4(__amdgpu_buffer_rsrc_t r, int off, f32x4 v) {
+  u32x4 q;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) q[i] = __float_as_uint(v[i]);
+  store_stream(r, off, q);
+}
+
+template <class E>
+__device__ __forceinline__ Frag8<E> vs_frag_tr(const typename ET<E>::raw* p_lo, const typename ET<E>::raw* p_hi) {
+  // Four 16-bit elements of a row-major tile, transposed across each 16-lane
+  // block: lane i of the block receives X[r0 + e][c0 + i] (e = 0..3) when lane
+  // s of the block passes &X[r0 + (s >> 2)][c0 + 4 (s & 3)].
+  const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(p_lo));
+  const s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(p_hi));
+  Frag8<E> f;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    f.e[e] = static_cast<typename ET<E>::raw>(static_cast<uint16_t>(lo[e]));
+    f.e[4 + e] = static_cast<typename ET<E>::raw>(static_cast<uint16_t>(hi[e]));
+  }
+  return f;
+}
+
+template <class E, int DKP, int PF>
+__global__ __launch_bounds__(kVsThreads, 1) void scan_vsplit_kernel(const ChunkFwdArgs a) {
+  using S = VsShape<E, DKP>;
+  constexpr int DVT = S::DVT;
+  using raw = typename ET<E>::raw;
+  constexpr int KS = S::KS, MS = S::MS, PS = S::PS, OS = S::OS, KH = S::KH, KT = S::KT, NKK = S::NKK,
+                KU = S::KU, VU = S::VU, K_UNITS = S::K_UNITS, BUF = S::BUF, MB = S::MB;
+  constexpr int ES = static_cast<int>(sizeof(raw));
+  static_assert(PF >= 3, "chunk c + 2 is staged in step c from registers loaded earlier");
+
+  extern __shared__ __align__(16) unsigned char smem[];
+  raw* stages = reinterpret_cast<raw*>(smem);     // 3 x { K [CT][KS], Q [CT][KS], V [CT][VS] }
+  raw* Pbuf = stages + kVsStages * BUF;            // 2 x [CT][PS]  P = S * coef, row = query
+  raw* Obuf = Pbuf + 2 * CT * PS;                  // 2 x [CT][OS]  output tile, row = query
+  raw* Mbuf = Obuf + 2 * CT * OS;                  // 2 x [DVT][MS] state before a chunk, 16-bit
+  float* pw = reinterpret_cast<float*>(Mbuf + 2 * MB);  // [PW_N]
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int g = lane >> 4;
+  const int n = lane & 15;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const bool p_wave = w < 4;
+  const int mw = w & 3;
+  const int vh = mw & 1;   // M waves: state and output value rows [16 vh, +16)
+  const int kh = mw >> 1;  // M waves: state key columns [KH kh, +KH), output queries [32 kh, +32)
+
+  int wg = blockIdx.x;
+  if (a.xcd_remap) {
+    const int per = gridDim.x >> 3;
+    wg = (wg & 7) * per + (wg >> 3);
+  }
+  // workgroup -> (sequence b, value tile); the tiles of a sequence are
+  // adjacent, so after the remap they share an XCD (and its L2).
+  const int v_tiles = a.v_tiles;
+  const int vtile = wg % v_tiles;
+  const int64_t b = wg / v_tiles;
+  const int v0 = vtile * DVT;
+  const int dk = a.dk, dv = a.dv;
+  const int64_t T = a.seq_len;
+  const int chunk = a.chunk;
+  const int n_chunks = a.n_chunks;
+  const bool f32m = a.mem_f32 != 0;
+
+  const raw* keys = static_cast<const raw*>(a.keys) + b * T * dk;
+  const raw* queries = static_cast<const raw*>(a.queries) + b * T * dk;
+  const raw* values = static_cast<const raw*>(a.values) + b * T * dv;
+  raw* hidden = a.hidden != nullptr ? static_cast<raw*>(a.hidden) + b * T * dv : nullptr;
+
+  auto chunk_len = [&](int c) -> int {
+    const int64_t t0 = static_cast<int64_t>(c) * chunk;
+    return (c < n_chunks) ? static_cast<int>(min(static_cast<int64_t>(chunk), T - t0)) : 0;
+  };
+  auto stage_k = [&](int c) { return stages + (c % kVsStages) * BUF; };
+
+  // ======================= P waves: staging, S, output flush
+  // K/Q unit u of P thread t is row (t + 256 u) / KU, 16-byte column
+  // (t + 256 u) % KU (a wave reads whole rows); its V / output unit is row
+  // t / VU of this workgroup's 32 columns.
+  struct Stage {
+    U8<E> k[K_UNITS];
+    U8<E> q[K_UNITS];
+    U8<E> v;
+  };
+  auto load_chunk = [&](int c, Stage& sg) {
+    const int64_t t0 = static_cast<int64_t>(c) * chunk;
+    const int L = chunk_len(c);
+    const __amdgpu_buffer_rsrc_t rk = make_rsrc(keys + t0 * dk, static_cast<uint32_t>(L * dk * ES));
+    const __amdgpu_buffer_rsrc_t rq = make_rsrc(queries + t0 * dk, static_cast<uint32_t>(L * dk * ES));
+    const __amdgpu_buffer_rsrc_t rv = make_rsrc(values + t0 * dv, static_cast<uint32_t>(L * dv * ES));
+#pragma unroll
+    for (int u = 0; u < K_UNITS; ++u) {
+      const int l = tid + kVsPThreads * u;
+      const int row = l / KU, col = 8 * (l % KU);
+      const int off = col < dk ? (row * dk + col) * ES : kBufOOB;
+      sg.k[u] = buf_load8<E>(rk, off);
+      sg.q[u] = buf_load8<E>(rq, off);
+    }
+    sg.v = buf_load8<E>(rv, ((tid / VU) * dv + v0 + 8 * (tid % VU)) * ES);
+  };
+  auto store_chunk = [&](int c, const Stage& sg) {
+    raw* Kb = stage_k(c);
+    raw* Qb = Kb + CT * KS;
+    raw* Vb = Qb + CT * KS;
+#pragma unroll
+    for (int u = 0; u < K_UNITS; ++u) {
+      const int l = tid + kVsPThreads * u;
+      const int row = l / KU, col = 8 * (l % KU);
+      *reinterpret_cast<U8<E>*>(Kb + kq_at<DKP>(row, col)) = sg.k[u];
+      *reinterpret_cast<U8<E>*>(Qb + kq_at<DKP>(row, col)) = sg.q[u];
+    }
+    *reinterpret_cast<U8<E>*>(Vb + v_at(tid / VU, 8 * (tid % VU))) = sg.v;
+  };
+  // Chunk -1 stores nothing (an empty resource): every step then issues the
+  // same memory instructions, which keeps the compiler's load-wait counts exact.
+  auto flush_out = [&](int c) {
+    const int64_t t0 = static_cast<int64_t>(max(c, 0)) * chunk;
+    const int L = c >= 0 ? chunk_len(c) : 0;
+    const __amdgpu_buffer_rsrc_t rh = make_rsrc(hidden + (hidden != nullptr ? t0 * dv : 0),
+                                                static_cast<uint32_t>(hidden != nullptr ? L * dv * ES : 0));
+    const int row = tid / VU, col = 8 * (tid % VU);
+    const u32x4 val = *reinterpret_cast<const u32x4*>(Obuf + (c & 1) * CT * OS + o_at(row, col));
+    store_stream(rh, (row * dv + v0 + col) * ES, val);
+  };
+  // P wave p: S rows i = 16 p + n against key blocks jb <= p (lane holds
+  // S[i][16 jb + 4g + r]); the blocks right of the diagonal are written as
+  // zeros, so the M waves read whole P rows without branches.
+  const int i_loc = 16 * mw + n;
+  float coef[4][4];
+  auto s_chunk = [&](int c) {
+    const raw* Kb = stage_k(c);
+    const raw* Qb = Kb + CT * KS;
+    raw* Pb = Pbuf + (c & 1) * CT * PS;
+    Frag8<E> qf[NKK];
+#pragma unroll
+    for (int kk = 0; kk < NKK; ++kk) qf[kk] = *reinterpret_cast<const Frag8<E>*>(Qb + kq_at<DKP>(i_loc, 32 * kk + 8 * g));
+#pragma unroll
+    for (int jb = 0; jb < 4; ++jb) {
+      f32x4 sacc = f32x4{0.f, 0.f, 0.f, 0.f};
+      if (jb <= mw) {
+#pragma unroll
+        for (int kk = 0; kk < NKK; ++kk) {
+          const Frag8<E> kf = *reinterpret_cast<const Frag8<E>*>(Kb + kq_at<DKP>(16 * jb + n, 32 * kk + 8 * g));
+          sacc = mfma8(kf, qf[kk], sacc);
+        }
+      }
+      store4_raw<E>(Pb + i_loc * PS + 16 * jb + 4 * g,
+                    sacc * f32x4{coef[jb][0], coef[jb][1], coef[jb][2], coef[jb][3]});
+    }
+  };
+
+  // ======================= M waves: state, output, snapshots
+  // state: st[kt], lane (g, n), register r = M[v][k] with
+  //        v = v0 + 16 vh + n and k = KH kh + 16 kt + 4g + r.
+  const int v_loc = 16 * vh + n;
+  f32x4 st[KT];
+  auto state_off = [&](int kt) -> int {
+    const int k = KH * kh + 16 * kt + 4 * g;
+    return k < dk ? (v0 + v_loc) * dk + k : kBufOOB;
+  };
+  const int64_t mem_b = f32m ? 4 : ES;
+  auto publish_state = [&](int slot) {
+    raw* Mb = Mbuf + slot * MB;
+#pragma unroll
+    for (int kt = 0; kt < KT; ++kt) store4_raw<E>(Mb + v_loc * MS + KH * kh + 16 * kt + 4 * g, st[kt]);
+  };
+  // decay^{i+1} for the query rows i = 32 kh + 16 ib + n of this lane's output tiles.
+  float s_start[2];
+  // State-update weights c * decay^{L-1-j} for this lane's slots
+  // j = 32p + 16 (s / 4) + 4g + s % 4 (the token order of every 64-deep operand).
+  float wgt[2][8];
+  auto set_weights = [&](int L) {
+#pragma unroll
+    for (int p = 0; p < 2; ++p) {
+#pragma unroll
+      for (int s = 0; s < 8; ++s) {
+        const int j = 32 * p + 16 * (s >> 2) + 4 * g + (s & 3);
+        wgt[p][s] = (j < L) ? a.c * pw[max(L - 1 - j, 0)] : 0.f;
+      }
+    }
+  };
+  int snap_phase = a.snap_every > 0 ? 1 % a.snap_every : 1;  // == 0: a snapshot follows the current chunk
+  auto m_chunk = [&](int c) {
+    const int L = chunk_len(c);
+    const raw* Kb = stage_k(c);
+    const raw* Qb = Kb + CT * KS;
+    const raw* Vb = Qb + CT * KS;
+    const raw* Pb = Pbuf + (c & 1) * CT * PS;
+    const raw* Mb = Mbuf + (c & 1) * MB;
+    raw* Ob = Obuf + (c & 1) * CT * OS;
+    if (L != CT) set_weights(L);
+    // Every LDS operand of the step is read first, so the reads overlap one
+    // another instead of each waiting for the product before it.
+    Frag8<E> mf[NKK], qf[2][NKK], vf[2], pf[2][2], kf[KT][2];
+#pragma unroll
+    for (int kk = 0; kk < NKK; ++kk) {
+      mf[kk] = *reinterpret_cast<const Frag8<E>*>(Mb + v_loc * MS + 32 * kk + 8 * g);
+#pragma unroll
+      for (int ib = 0; ib < 2; ++ib)
+        qf[ib][kk] = *reinterpret_cast<const Frag8<E>*>(Qb + kq_at<DKP>(32 * kh + 16 * ib + n, 32 * kk + 8 * g));
+    }
+    // V^T fragments (rows v, slots j = 32p + 16 (s / 4) + 4g + s % 4) for both
+    // products; each transposed read covers 16 consecutive token rows.  P rows
+    // and K^T fragments use the same slot order.
+#pragma unroll
+    for (int p = 0; p < 2; ++p) {
+      const raw* base = Vb + v_at(32 * p + 4 * g + (n >> 2), 16 * vh + 4 * (n & 3));
+      vf[p] = vs_frag_tr<E>(base, base + 16 * S::VS);
+#pragma unroll
+      for (int ib = 0; ib < 2; ++ib) {
+        const raw* src = Pb + (16 * (2 * kh + ib) + n) * PS + 32 * p + 4 * g;
+        pf[ib][p] = lds_frag_4x2<E>(src, src + 16);
+      }
+#pragma unroll
+      for (int kt = 0; kt < KT; ++kt) {
+        const raw* kb = Kb + kq_at<DKP>(32 * p + 4 * g + (n >> 2), KH * kh + 16 * kt + 4 * (n & 3));
+        kf[kt][p] = vs_frag_tr<E>(kb, kb + 16 * KS);
+      }
+    }
+    // O^T = decay^{i+1} M Q^T + V^T P^T: A = state rows v (16-bit copy) then
+    // V^T rows v; B = Q rows i then P rows i (P[i][j] = 0 for j > i).
+#pragma unroll
+    for (int ib = 0; ib < 2; ++ib) {
+      f32x4 o = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int kk = 0; kk < NKK; ++kk) o = mfma8(mf[kk], qf[ib][kk], o);
+      o *= s_start[ib];
+#pragma unroll
+      for (int p = 0; p < 2; ++p) o = mfma8(vf[p], pf[ib][p], o);
+      store4_raw<E>(Ob + o_at(16 * (2 * kh + ib) + n, 16 * vh + 4 * g), o);
+    }
+    // State update: M^T = decay^L M^T + K^T (w V); A = K^T rows k, B = (w V)^T rows v.
+    Frag8<E> wf[2];
+#pragma unroll
+    for (int p = 0; p < 2; ++p)
+#pragma unroll
+      for (int s = 0; s < 8; ++s) wf[p].e[s] = ET<E>::from_f(ET<E>::to_f(vf[p].e[s]) * wgt[p][s]);
+    const float decay_L = pw[L];
+#pragma unroll
+    for (int kt = 0; kt < KT; ++kt) {
+      f32x4 acc = st[kt] * decay_L;
+#pragma unroll
+      for (int p = 0; p < 2; ++p) acc = mfma8(kf[kt][p], wf[p], acc);
+      st[kt] = acc;
+    }
+    publish_state((c + 1) & 1);
+    if (a.snap_every > 0 && (snap_phase == 0 || c + 1 == n_chunks)) {
+      const int si = c / a.snap_every;
+      const __amdgpu_buffer_rsrc_t rs =
+          make_rsrc(a.snapshots + (b * a.n_snap + si) * dv * dk, static_cast<uint32_t>(dv * dk * 4));
+#pragma unroll
+      for (int kt = 0; kt < KT; ++kt) {
+        const int off = state_off(kt);
+        store_stream_f32x4(rs, off == kBufOOB ? kBufOOB : off * 4, st[kt]);
+      }
+    }
+    if (a.snap_every > 0) snap_phase = (snap_phase + 1 == a.snap_every) ? 0 : snap_phase + 1;
+  };
+
+  // ======================= the two loops
+  // Barriers: one after the prologue, one at the top of each step, one before
+  // the last flush; both halves pass the same number.  In step c the barrier
+  // orders every LDS producer before its consumers, and each buffer's next
+  // writer runs at least one step after its last reader.
+  static_assert(PW_N <= kVsPThreads, "one power per P thread");
+  if (p_wave) {
+    const float pw_first = tid < PW_N ? a.pw[tid] : 0.f;
+    Stage sg[PF];
+#pragma unroll
+    for (int i = 0; i < PF; ++i) load_chunk(i, sg[i]);
+    if (tid < PW_N) pw[tid] = pw_first;
+    store_chunk(0, sg[0]);
+    store_chunk(1, sg[1]);
+    __syncthreads();  // pw, chunks 0 and 1, M_0
+#pragma unroll
+    for (int jb = 0; jb < 4; ++jb) {
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int j = 16 * jb + 4 * g + r;
+        coef[jb][r] = (j <= i_loc) ? a.c * pw[max(i_loc - j, 0)] : 0.f;
+      }
+    }
+    s_chunk(0);
+    // Step c: load chunk c + PF into the slot chunk c held, stage chunk c + 2,
+    // flush chunk c - 1's output, S of chunk c + 1.
+    for (int c = 0; c < n_chunks; c += PF) {
+#pragma unroll
+      for (int i = 0; i < PF; ++i) {
+        if (c + i >= n_chunks) break;
+        __syncthreads();
+        load_chunk(c + i + PF, sg[i]);
+        store_chunk(c + i + 2, sg[(i + 2) % PF]);
+        flush_out(c + i - 1);
+        if (c + i + 1 < n_chunks) s_chunk(c + i + 1);
+      }
+    }
+    __syncthreads();
+    flush_out(n_chunks - 1);
+    return;
+  }
+
+  {
+    const __amdgpu_buffer_rsrc_t rmem = make_rsrc(static_cast<const unsigned char*>(a.memory) + b * dv * dk * mem_b,
+                                                  static_cast<uint32_t>(dv * dk * mem_b));
+#pragma unroll
+    for (int kt = 0; kt < KT; ++kt) {
+      const int off = state_off(kt);
+      if (f32m) {
+        const u32x4 u = __builtin_amdgcn_raw_buffer_load_b128(rmem, off == kBufOOB ? kBufOOB : off * 4, 0, 0);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) st[kt][i] = __uint_as_float(u[i]);
+      } else {
+        const u32x2 u = __builtin_amdgcn_raw_buffer_load_b64(rmem, off == kBufOOB ? kBufOOB : off * ES, 0, 0);
+        st[kt][0] = ET<E>::to_f(static_cast<raw>(u[0] & 0xffffu));
+        st[kt][1] = ET<E>::to_f(static_cast<raw>(u[0] >> 16));
+        st[kt][2] = ET<E>::to_f(static_cast<raw>(u[1] & 0xffffu));
+        st[kt][3] = ET<E>::to_f(static_cast<raw>(u[1] >> 16));
+      }
+    }
+  }
+  publish_state(0);
+  // The M waves carry the step's dependency chain: when an M wave and a P
+  // wave of one SIMD are both ready, the M wave issues first.
+  __builtin_amdgcn_s_setprio(2);
+  __syncthreads();  // pw, chunks 0 and 1, M_0
+  set_weights(CT);
+#pragma unroll
+  for (int ib = 0; ib < 2; ++ib) s_start[ib] = pw[32 * kh + 16 * ib + n + 1];
+  // Step c: scan chunk c.
+  for (int c = 0; c < n_chunks; ++c) {
+    __syncthreads();
+    m_chunk(c);
+  }
+  __syncthreads();
+  if (a.memory_out == nullptr) return;
+  const __amdgpu_buffer_rsrc_t ro = make_rsrc(static_cast<unsigned char*>(a.memory_out) + b * dv * dk * mem_b,
+                                              static_cast<uint32_t>(dv * dk * mem_b));
+#pragma unroll
+  for (int kt = 0; kt < KT; ++kt) {
+    const int off = state_off(kt);
+    if (f32m) {
+      store_stream_f32x4(ro, off == kBufOOB ? kBufOOB : off * 4, st[kt]);
+    } else {
+      buf_store4<E>(ro, off == kBufOOB ? kBufOOB : off * ES, st[kt]);
+    }
+  }
+}
+
+template <class E, int DKP>
+int launch_vsplit(ChunkFwdArgs a, hipStream_t stream) {
+  using S = VsShape<E, DKP>;
+  constexpr int PF = kVsplitPrefetch;
+  static bool attr_set = false;
+  if (!attr_set) {
+    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&scan_vsplit_kernel<E, DKP, PF>),
+                                       hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(S::lds_bytes));
+    if (e != hipSuccess) {
+      set_error("chunk_update_fwd: hipFuncSetAttribute failed: %s", hipGetErrorString(e));
+      return static_cast<int>(e);
+    }
+    attr_set = true;
+  }
+  if (a.n_parts != 1 || a.v_tiles * S::DVT != a.dv) {
+    set_error("chunk_update_fwd: value-split scan needs one part and value_dim = %d x tiles", S::DVT);
+    return GRM_HIP_EINVAL;
+  }
+  const int64_t grid = a.batch * a.v_tiles;
+  if (grid > INT32_MAX) {
+    set_error("chunk_update_fwd: batch too large for one launch");
+    return GRM_HIP_EINVAL;
+  }
+  a.xcd_remap = (grid % 8 == 0) ? 1 : 0;
+  hipLaunchKernelGGL((scan_vsplit_kernel<E, DKP, PF>), dim3(static_cast<unsigned>(grid)), dim3(kVsThreads),
+                     S::lds_bytes, stream, a);
+  return check_launch("chunk_update_fwd");
+}
+
+}  // namespace
+
+bool vsplit_supported(int in_dtype, int64_t key_dim, int64_t value_dim, bool vec) {
+  return wide_supported(in_dtype, key_dim, value_dim, vec) && value_dim % kVsplitDv == 0;
+}
+
+int launch_scan_vsplit(const ChunkFwdArgs& a, int in_dtype, hipStream_t stream) {
+  if (in_dtype == GRM_HIP_F16) {
+    return a.dk <= 64 ? launch_vsplit<F16, 64>(a, stream) : launch_vsplit<F16, 128>(a, stream);
+  }
+  return a.dk <= 64 ? launch_vsplit<BF16, 64>(a, stream) : launch_vsplit<BF16, 128>(a, stream);
+}
+
+}  // namespace grmhip

@@ -181,6 +181,56 @@ def test_wide_and_narrow_tiles_agree(dev, monkeypatch, B, T, K, H):
     torch.testing.assert_close(mw, mn, rtol=1e-4, atol=1e-6)
 
 
+@pytest.mark.parametrize("dtype,mem_dtype", [(torch.bfloat16, torch.float32), (torch.float16, torch.float32),
+                                             (torch.bfloat16, torch.bfloat16), (torch.float16, torch.float16)])
+@pytest.mark.parametrize("B,T,K,H,seg", [(2, 300, 128, 128, 64), (3, 129, 64, 64, 0), (1, 640, 96, 256, 100),
+                                         (2, 64, 128, 32, 128), (5, 1000, 32, 96, 32), (1, 7, 128, 128, 1)])
+def test_value_split_scan(dev, monkeypatch, dtype, mem_dtype, B, T, K, H, seg):
+    """The value-split scan (32-column value tiles, one workgroup per sequence and
+    tile, GRM_HIP_CHUNK_VSPLIT=1) against the oracle and against the 128-column
+    kernel (=0): ragged last chunks, key widths below the padded 64/128, one to
+    eight value tiles, snapshot lengths that set shorter chunks, 16-bit states."""
+    k, v, q, m = make_case(B, T, K, H, dtype, mem_dtype, seed=B * 97 + T + K)
+    kd, vd, qd, md = k.to(dev), v.to(dev), q.to(dev), m.to(dev)
+    print(f"value split B={B} T={T} K={K} H={H} seg={seg} {dtype} state {mem_dtype}", flush=True)
+    monkeypatch.setenv("GRM_HIP_CHUNK_VSPLIT", "1")
+    hs, ms, ss = capi.chunk_update_fwd(kd, vd, qd, md, 0.97, seg)
+    monkeypatch.setenv("GRM_HIP_CHUNK_VSPLIT", "0")
+    hw, mw, sw = capi.chunk_update_fwd(kd, vd, qd, md, 0.97, seg)
+    torch.cuda.synchronize()
+    rh, rm, rs = oracle_fwd(k, v, q, m, 0.97, seg)
+    close("hidden", hs, rh, dtype)
+    close("memory_out", ms, rm, dtype)
+    if seg:
+        close("snapshots", ss, rs, dtype)
+        if mem_dtype == torch.float32:
+            assert torch.equal(ss[:, -1], ms)
+    torch.testing.assert_close(hs.float(), hw.float(), rtol=1e-2, atol=1e-3)
+    torch.testing.assert_close(ms.float(), mw.float(), rtol=1e-2 if mem_dtype != torch.float32 else 1e-4,
+                               atol=1e-3 if mem_dtype != torch.float32 else 1e-6)
+
+
+def test_value_split_is_default_at_config2_shape(dev, monkeypatch):
+    """Config 2's shape (64 sequences x 128 value columns) takes the value-split scan
+    by default; it and the time-split 128-column scan agree, and it is deterministic."""
+    B, T, D = 64, 512, 128
+    k, v, q, m = make_case(B, T, D, D, torch.bfloat16, torch.float32, seed=11)
+    kd, vd, qd, md = k.to(dev), v.to(dev), q.to(dev), m.to(dev)
+    h0, m0, s0 = capi.chunk_update_fwd(kd, vd, qd, md, 0.97, 64)
+    monkeypatch.setenv("GRM_HIP_CHUNK_VSPLIT", "1")
+    h1, m1, s1 = capi.chunk_update_fwd(kd, vd, qd, md, 0.97, 64)
+    monkeypatch.setenv("GRM_HIP_CHUNK_VSPLIT", "0")
+    h2, m2, s2 = capi.chunk_update_fwd(kd, vd, qd, md, 0.97, 64)
+    torch.cuda.synchronize()
+    assert torch.equal(h0, h1) and torch.equal(s0, s1), "default path must be the value split here"
+    torch.testing.assert_close(h1.float(), h2.float(), rtol=1e-2, atol=1e-3)
+    torch.testing.assert_close(s1, s2, rtol=1e-4, atol=1e-6)
+    for b in (0, 63):
+        rh, rm, rs = oracle_fwd(k[b:b + 1], v[b:b + 1], q[b:b + 1], m[b:b + 1], 0.97, 64)
+        close(f"hidden[{b}]", h1[b:b + 1], rh, torch.bfloat16)
+        close(f"snapshots[{b}]", s1[b:b + 1], rs, torch.bfloat16)
+
+
 def test_long_context_split_fp32(dev, monkeypatch):
     """fp32 long sequence, automatic part count, against the oracle at fp32 tolerance."""
     B, T, K, H = 2, 4096, 64, 64
