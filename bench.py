@@ -93,17 +93,24 @@ def bench_c2(torch, dev, steps, warmup):
         if rc != 0:
             raise RuntimeError(capi.last_error())
 
-    # value: K back-to-back steps between two synchronisations (no per-step events in the
-    # way); roofline: K more steps, each bracketed by HIP events on the kernels' stream.
+    # One timed loop of K back-to-back steps, read by two clocks: the host clock between
+    # two synchronisations (value) and two HIP events on the kernel's stream around the
+    # same launches (roofline: average launch duration, with no per-launch event overhead,
+    # which is what a kernel trace of these launches reports).  Both come from the same
+    # launches because the box's clocks drift under sustained load (a second loop of the
+    # same kernel right after the first has run up to 20% slower).
     for _ in range(warmup):
         step()
     torch.cuda.synchronize()
+    ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     t0 = time.perf_counter()
+    ev0.record(stream)
     for _ in range(steps):
         step()
+    ev1.record(stream)
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
-    _, per = timed_launches(torch, step, steps, 0, stream)
+    per = [ev0.elapsed_time(ev1) * 1e-3 / steps]
     return wall, per, (k, v, q, m, hidden, snaps)
 
 
@@ -414,7 +421,7 @@ def cpu_baseline(torch, budget_s: float = 20.0):
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-gather", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
@@ -457,7 +464,7 @@ def main() -> int:
     tokens = 64 * 2048
     achieved_gbs = bytes_ / t_kernel / 1e9
     tflops = flops / t_kernel / 1e12
-    log(f"c2: {t_kernel * 1e6:.1f} us/launch (events), {t_step * 1e6:.1f} us/step (wall)")
+    log(f"c2: {t_kernel * 1e6:.1f} us/launch (events around {a.steps} launches), {t_step * 1e6:.1f} us/step (wall)")
 
     traffic = None
     tfile = REPO / "profiles" / "scan_vsplit_c2_traffic.json"
