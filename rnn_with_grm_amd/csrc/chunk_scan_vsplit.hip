@@ -22,12 +22,12 @@
 //                  c - 1, and compute S = Q K^T of chunk c + 1 (wave p: query block p against the
 //                  key blocks at or below the diagonal), publishing
 //                  P = S * c * decay^{i-j};
-//   M waves (4-7)  wave (vh, kh): state rows v in [16 vh, +16) and key
-//                  columns [kh d/2, +d/2) as fp32 MFMA accumulators; they form
-//                  O^T = decay^{i+1} M Q^T + V^T P^T for value rows [16 vh, +16)
-//                  and queries [32 kh, +32) (M read from a 16-bit copy in LDS
-//                  that they rewrite after each update), then
-//                  M^T = decay^L M^T + K^T (w V), and the snapshot.
+//   M waves (4-7)  waves 4-5 form O^T = decay^{i+1} M Q^T + V^T P^T for all
+//                  32 value rows and 32 queries each, M read from a 16-bit copy
+//                  in LDS; waves 6-7 hold the state (32 value rows x d/2 key
+//                  columns each, fp32 MFMA accumulators), update it,
+//                  M^T = decay^L M^T + K^T (w V), write the 16-bit copy the next
+//                  step reads, and store the snapshot.
 // Chunk data lives in three LDS stage buffers (written two steps ahead, read
 // by the P waves one step ahead and by the M waves in their step); P, the
 // output tile and the 16-bit state copy are double-buffered.  K^T and V^T
@@ -42,6 +42,8 @@
 #include "chunk_scan.h"
 #include "grm_hip.h"
 #include "grm_hip_common.h"
+
+#include <type_traits>
 
 namespace grmhip {
 namespace {
@@ -68,8 +70,8 @@ struct VsShape {
   static constexpr int VS = DVT;
   static constexpr int PS = CT + 4;
   static constexpr int OS = DVT;
-  static constexpr int KH = DKP / 2;   // key columns of one M wave's state
-  static constexpr int KT = KH / 16;   // 16-wide state tiles per M wave
+  static constexpr int KH = DKP / 2;   // key columns of one state wave
+  static constexpr int KT = KH / 16;   // 16-wide key tiles per state wave
   static constexpr int NKK = DKP / 32; // 32-deep key steps
   static constexpr int KU = DKP / 8;   // 16-byte units per K/Q row
   static constexpr int VU = DVT / 8;   // 16-byte units per V / output row
@@ -160,8 +162,6 @@ __global__ __launch_bounds__(kVsThreads, 1) void scan_vsplit_kernel(const ChunkF
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
   const bool p_wave = w < 4;
   const int mw = w & 3;
-  const int vh = mw & 1;   // M waves: state and output value rows [16 vh, +16)
-  const int kh = mw >> 1;  // M waves: state key columns [KH kh, +KH), output queries [32 kh, +32)
 
   int wg = blockIdx.x;
   if (a.xcd_remap) {
@@ -267,24 +267,32 @@ __global__ __launch_bounds__(kVsThreads, 1) void scan_vsplit_kernel(const ChunkF
     }
   };
 
-  // ======================= M waves: state, output, snapshots
-  // state: st[kt], lane (g, n), register r = M[v][k] with
-  //        v = v0 + 16 vh + n and k = KH kh + 16 kt + 4g + r.
-  const int v_loc = 16 * vh + n;
-  f32x4 st[KT];
-  auto state_off = [&](int kt) -> int {
-    const int k = KH * kh + 16 * kt + 4 * g;
-    return k < dk ? (v0 + v_loc) * dk + k : kBufOOB;
+  // ======================= M waves: output (waves 4-5) and state (waves 6-7)
+  // O wave oq: O^T for all 32 value rows and the queries [32 oq, +32), from the
+  //   16-bit state copy (M before the chunk), Q, V^T and P.
+  // U wave uk: the state rows v in [0, 32) and key columns [KH uk, +KH) as fp32
+  //   MFMA accumulators st[vb][kt], lane (g, n), register r = M[v][k] with
+  //   v = v0 + 16 vb + n and k = KH uk + 16 kt + 4g + r; it updates them, writes
+  //   them to the other 16-bit copy and stores the snapshot.
+  // The two read different data, so each reads only what it multiplies.
+  const bool o_wave = mw < 2;
+  const int uk = mw & 1;
+  f32x4 st[2][KT];
+  auto state_off = [&](int vb, int kt) -> int {
+    const int k = KH * uk + 16 * kt + 4 * g;
+    return k < dk ? (v0 + 16 * vb + n) * dk + k : kBufOOB;
   };
   const int64_t mem_b = f32m ? 4 : ES;
   auto publish_state = [&](int slot) {
     raw* Mb = Mbuf + slot * MB;
 #pragma unroll
-    for (int kt = 0; kt < KT; ++kt) store4_raw<E>(Mb + v_loc * MS + KH * kh + 16 * kt + 4 * g, st[kt]);
+    for (int vb = 0; vb < 2; ++vb)
+#pragma unroll
+      for (int kt = 0; kt < KT; ++kt) store4_raw<E>(Mb + (16 * vb + n) * MS + KH * uk + 16 * kt + 4 * g, st[vb][kt]);
   };
-  // decay^{i+1} for the query rows i = 32 kh + 16 ib + n of this lane's output tiles.
+  // O waves: decay^{i+1} for the query rows i = 32 oq + 16 ib + n of this lane's output tiles.
   float s_start[2];
-  // State-update weights c * decay^{L-1-j} for this lane's slots
+  // U waves: state-update weights c * decay^{L-1-j} for this lane's slots
   // j = 32p + 16 (s / 4) + 4g + s % 4 (the token order of every 64-deep operand).
   float wgt[2][8];
   auto set_weights = [&](int L) {
@@ -297,80 +305,120 @@ __global__ __launch_bounds__(kVsThreads, 1) void scan_vsplit_kernel(const ChunkF
       }
     }
   };
-  int snap_phase = a.snap_every > 0 ? 1 % a.snap_every : 1;  // == 0: a snapshot follows the current chunk
-  auto m_chunk = [&](int c) {
-    const int L = chunk_len(c);
-    const raw* Kb = stage_k(c);
-    const raw* Qb = Kb + CT * KS;
+  // V^T fragments (rows v, slots j = 32p + 16 (s / 4) + 4g + s % 4) for both
+  // products; each transposed read covers 16 consecutive token rows.  P rows
+  // and K^T fragments use the same slot order.
+  auto v_frags = [&](const raw* Vb, Frag8<E>(&vf)[2][2]) {
+#pragma unroll
+    for (int vb = 0; vb < 2; ++vb)
+#pragma unroll
+      for (int p = 0; p < 2; ++p) {
+        const raw* base = Vb + v_at(32 * p + 4 * g + (n >> 2), 16 * vb + 4 * (n & 3));
+        vf[vb][p] = vs_frag_tr<E>(base, base + 16 * S::VS);
+      }
+  };
+  // Every LDS operand of a step is read first, so the reads overlap one another
+  // instead of each waiting for the product before it.
+  auto o_chunk = [&](int c, auto oq_c) {
+    constexpr int oq = decltype(oq_c)::value;
+    const raw* Qb = stage_k(c) + CT * KS;
     const raw* Vb = Qb + CT * KS;
     const raw* Pb = Pbuf + (c & 1) * CT * PS;
     const raw* Mb = Mbuf + (c & 1) * MB;
     raw* Ob = Obuf + (c & 1) * CT * OS;
-    if (L != CT) set_weights(L);
-    // Every LDS operand of the step is read first, so the reads overlap one
-    // another instead of each waiting for the product before it.
-    Frag8<E> mf[NKK], qf[2][NKK], vf[2], pf[2][2], kf[KT][2];
+    Frag8<E> mf[2][NKK], qf[2][NKK], vf[2][2], pf[2][2];
 #pragma unroll
     for (int kk = 0; kk < NKK; ++kk) {
-      mf[kk] = *reinterpret_cast<const Frag8<E>*>(Mb + v_loc * MS + 32 * kk + 8 * g);
+#pragma unroll
+      for (int vb = 0; vb < 2; ++vb)
+        mf[vb][kk] = *reinterpret_cast<const Frag8<E>*>(Mb + (16 * vb + n) * MS + 32 * kk + 8 * g);
 #pragma unroll
       for (int ib = 0; ib < 2; ++ib)
-        qf[ib][kk] = *reinterpret_cast<const Frag8<E>*>(Qb + kq_at<DKP>(32 * kh + 16 * ib + n, 32 * kk + 8 * g));
+        qf[ib][kk] = *reinterpret_cast<const Frag8<E>*>(Qb + kq_at<DKP>(32 * oq + 16 * ib + n, 32 * kk + 8 * g));
     }
-    // V^T fragments (rows v, slots j = 32p + 16 (s / 4) + 4g + s % 4) for both
-    // products; each transposed read covers 16 consecutive token rows.  P rows
-    // and K^T fragments use the same slot order.
+    v_frags(Vb, vf);
+    // P slots 0-3 of fragment p are key block 2p, slots 4-7 key block 2p + 1;
+    // blocks right of the diagonal (never written) are taken as zeros, and a
+    // fragment wholly right of it is skipped.
 #pragma unroll
-    for (int p = 0; p < 2; ++p) {
-      const raw* base = Vb + v_at(32 * p + 4 * g + (n >> 2), 16 * vh + 4 * (n & 3));
-      vf[p] = vs_frag_tr<E>(base, base + 16 * S::VS);
+    for (int ib = 0; ib < 2; ++ib) {
+      const int iblk = 2 * oq + ib;
 #pragma unroll
-      for (int ib = 0; ib < 2; ++ib) {
-        const raw* src = Pb + (16 * (2 * kh + ib) + n) * PS + 32 * p + 4 * g;
+      for (int p = 0; p < 2; ++p) {
+        if (2 * p > iblk) continue;
+        const raw* src = Pb + (16 * iblk + n) * PS + 32 * p + 4 * g;
         pf[ib][p] = lds_frag_4x2<E>(src, src + 16);
-      }
+        if (2 * p + 1 > iblk) {
 #pragma unroll
-      for (int kt = 0; kt < KT; ++kt) {
-        const raw* kb = Kb + kq_at<DKP>(32 * p + 4 * g + (n >> 2), KH * kh + 16 * kt + 4 * (n & 3));
-        kf[kt][p] = vs_frag_tr<E>(kb, kb + 16 * KS);
+          for (int e = 4; e < 8; ++e) pf[ib][p].e[e] = 0;
+        }
       }
     }
     // O^T = decay^{i+1} M Q^T + V^T P^T: A = state rows v (16-bit copy) then
-    // V^T rows v; B = Q rows i then P rows i (P[i][j] = 0 for j > i).
+    // V^T rows v; B = Q rows i then P rows i.
 #pragma unroll
     for (int ib = 0; ib < 2; ++ib) {
-      f32x4 o = f32x4{0.f, 0.f, 0.f, 0.f};
+      const int iblk = 2 * oq + ib;
 #pragma unroll
-      for (int kk = 0; kk < NKK; ++kk) o = mfma8(mf[kk], qf[ib][kk], o);
-      o *= s_start[ib];
+      for (int vb = 0; vb < 2; ++vb) {
+        f32x4 o = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int p = 0; p < 2; ++p) o = mfma8(vf[p], pf[ib][p], o);
-      store4_raw<E>(Ob + o_at(16 * (2 * kh + ib) + n, 16 * vh + 4 * g), o);
+        for (int kk = 0; kk < NKK; ++kk) o = mfma8(mf[vb][kk], qf[ib][kk], o);
+        o *= s_start[ib];
+#pragma unroll
+        for (int p = 0; p < 2; ++p) {
+          if (2 * p > iblk) continue;
+          o = mfma8(vf[vb][p], pf[ib][p], o);
+        }
+        store4_raw<E>(Ob + o_at(16 * iblk + n, 16 * vb + 4 * g), o);
+      }
     }
-    // State update: M^T = decay^L M^T + K^T (w V); A = K^T rows k, B = (w V)^T rows v.
-    Frag8<E> wf[2];
+  };
+  int snap_phase = a.snap_every > 0 ? 1 % a.snap_every : 1;  // == 0: a snapshot follows the current chunk
+  auto u_chunk = [&](int c) {
+    const int L = chunk_len(c);
+    const raw* Kb = stage_k(c);
+    const raw* Vb = Kb + 2 * CT * KS;
+    if (L != CT) set_weights(L);
+    Frag8<E> vf[2][2], kf[KT][2];
+    v_frags(Vb, vf);
 #pragma unroll
     for (int p = 0; p < 2; ++p)
 #pragma unroll
-      for (int s = 0; s < 8; ++s) wf[p].e[s] = ET<E>::from_f(ET<E>::to_f(vf[p].e[s]) * wgt[p][s]);
+      for (int kt = 0; kt < KT; ++kt) {
+        const raw* kb = Kb + kq_at<DKP>(32 * p + 4 * g + (n >> 2), KH * uk + 16 * kt + 4 * (n & 3));
+        kf[kt][p] = vs_frag_tr<E>(kb, kb + 16 * KS);
+      }
+    // State update: M^T = decay^L M^T + K^T (w V); A = K^T rows k, B = (w V)^T rows v.
+    Frag8<E> wf[2][2];
+#pragma unroll
+    for (int vb = 0; vb < 2; ++vb)
+#pragma unroll
+      for (int p = 0; p < 2; ++p)
+#pragma unroll
+        for (int s = 0; s < 8; ++s) wf[vb][p].e[s] = ET<E>::from_f(ET<E>::to_f(vf[vb][p].e[s]) * wgt[p][s]);
     const float decay_L = pw[L];
 #pragma unroll
-    for (int kt = 0; kt < KT; ++kt) {
-      f32x4 acc = st[kt] * decay_L;
+    for (int vb = 0; vb < 2; ++vb)
 #pragma unroll
-      for (int p = 0; p < 2; ++p) acc = mfma8(kf[kt][p], wf[p], acc);
-      st[kt] = acc;
-    }
+      for (int kt = 0; kt < KT; ++kt) {
+        f32x4 acc = st[vb][kt] * decay_L;
+#pragma unroll
+        for (int p = 0; p < 2; ++p) acc = mfma8(kf[kt][p], wf[vb][p], acc);
+        st[vb][kt] = acc;
+      }
     publish_state((c + 1) & 1);
     if (a.snap_every > 0 && (snap_phase == 0 || c + 1 == n_chunks)) {
       const int si = c / a.snap_every;
       const __amdgpu_buffer_rsrc_t rs =
           make_rsrc(a.snapshots + (b * a.n_snap + si) * dv * dk, static_cast<uint32_t>(dv * dk * 4));
 #pragma unroll
-      for (int kt = 0; kt < KT; ++kt) {
-        const int off = state_off(kt);
-        store_stream_f32x4(rs, off == kBufOOB ? kBufOOB : off * 4, st[kt]);
-      }
+      for (int vb = 0; vb < 2; ++vb)
+#pragma unroll
+        for (int kt = 0; kt < KT; ++kt) {
+          const int off = state_off(vb, kt);
+          store_stream_f32x4(rs, off == kBufOOB ? kBufOOB : off * 4, st[vb][kt]);
+        }
     }
     if (a.snap_every > 0) snap_phase = (snap_phase + 1 == a.snap_every) ? 0 : snap_phase + 1;
   };
@@ -417,51 +465,64 @@ __global__ __launch_bounds__(kVsThreads, 1) void scan_vsplit_kernel(const ChunkF
     return;
   }
 
-  {
+  if (!o_wave) {
     const __amdgpu_buffer_rsrc_t rmem = make_rsrc(static_cast<const unsigned char*>(a.memory) + b * dv * dk * mem_b,
                                                   static_cast<uint32_t>(dv * dk * mem_b));
 #pragma unroll
-    for (int kt = 0; kt < KT; ++kt) {
-      const int off = state_off(kt);
-      if (f32m) {
-        const u32x4 u = __builtin_amdgcn_raw_buffer_load_b128(rmem, off == kBufOOB ? kBufOOB : off * 4, 0, 0);
+    for (int vb = 0; vb < 2; ++vb)
 #pragma unroll
-        for (int i = 0; i < 4; ++i) st[kt][i] = __uint_as_float(u[i]);
-      } else {
-        const u32x2 u = __builtin_amdgcn_raw_buffer_load_b64(rmem, off == kBufOOB ? kBufOOB : off * ES, 0, 0);
-        st[kt][0] = ET<E>::to_f(static_cast<raw>(u[0] & 0xffffu));
-        st[kt][1] = ET<E>::to_f(static_cast<raw>(u[0] >> 16));
-        st[kt][2] = ET<E>::to_f(static_cast<raw>(u[1] & 0xffffu));
-        st[kt][3] = ET<E>::to_f(static_cast<raw>(u[1] >> 16));
+      for (int kt = 0; kt < KT; ++kt) {
+        const int off = state_off(vb, kt);
+        if (f32m) {
+          const u32x4 u = __builtin_amdgcn_raw_buffer_load_b128(rmem, off == kBufOOB ? kBufOOB : off * 4, 0, 0);
+#pragma unroll
+          for (int i = 0; i < 4; ++i) st[vb][kt][i] = __uint_as_float(u[i]);
+        } else {
+          const u32x2 u = __builtin_amdgcn_raw_buffer_load_b64(rmem, off == kBufOOB ? kBufOOB : off * ES, 0, 0);
+          st[vb][kt][0] = ET<E>::to_f(static_cast<raw>(u[0] & 0xffffu));
+          st[vb][kt][1] = ET<E>::to_f(static_cast<raw>(u[0] >> 16));
+          st[vb][kt][2] = ET<E>::to_f(static_cast<raw>(u[1] & 0xffffu));
+          st[vb][kt][3] = ET<E>::to_f(static_cast<raw>(u[1] >> 16));
+        }
       }
-    }
+    publish_state(0);
   }
-  publish_state(0);
   // The M waves carry the step's dependency chain: when an M wave and a P
   // wave of one SIMD are both ready, the M wave issues first.
   __builtin_amdgcn_s_setprio(2);
   __syncthreads();  // pw, chunks 0 and 1, M_0
-  set_weights(CT);
+  if (o_wave) {
 #pragma unroll
-  for (int ib = 0; ib < 2; ++ib) s_start[ib] = pw[32 * kh + 16 * ib + n + 1];
+    for (int ib = 0; ib < 2; ++ib) s_start[ib] = pw[32 * (mw & 1) + 16 * ib + n + 1];
+  } else {
+    set_weights(CT);
+  }
   // Step c: scan chunk c.
   for (int c = 0; c < n_chunks; ++c) {
     __syncthreads();
-    m_chunk(c);
+    if (mw == 0) {
+      o_chunk(c, std::integral_constant<int, 0>{});
+    } else if (mw == 1) {
+      o_chunk(c, std::integral_constant<int, 1>{});
+    } else {
+      u_chunk(c);
+    }
   }
   __syncthreads();
-  if (a.memory_out == nullptr) return;
+  if (o_wave || a.memory_out == nullptr) return;
   const __amdgpu_buffer_rsrc_t ro = make_rsrc(static_cast<unsigned char*>(a.memory_out) + b * dv * dk * mem_b,
                                               static_cast<uint32_t>(dv * dk * mem_b));
 #pragma unroll
-  for (int kt = 0; kt < KT; ++kt) {
-    const int off = state_off(kt);
-    if (f32m) {
-      store_stream_f32x4(ro, off == kBufOOB ? kBufOOB : off * 4, st[kt]);
-    } else {
-      buf_store4<E>(ro, off == kBufOOB ? kBufOOB : off * ES, st[kt]);
+  for (int vb = 0; vb < 2; ++vb)
+#pragma unroll
+    for (int kt = 0; kt < KT; ++kt) {
+      const int off = state_off(vb, kt);
+      if (f32m) {
+        store_stream_f32x4(ro, off == kBufOOB ? kBufOOB : off * 4, st[vb][kt]);
+      } else {
+        buf_store4<E>(ro, off == kBufOOB ? kBufOOB : off * ES, st[vb][kt]);
+      }
     }
-  }
 }
 
 template <class E, int DKP>
