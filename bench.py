@@ -207,6 +207,43 @@ def bench_c3(torch, dev, steps, warmup):
     }
 
 
+def bench_published(torch, dev):
+    """The reference's only published figure is its chunk-update microbenchmark
+    (examples/benchmark_cuda_chunk_update.py defaults: B=4, 256 tokens, d_v=256, d_k=64, fp32,
+    decay 0.97, q and k L2-normalised, memory N(0,1); 10 warm-up and 50 timed calls of the
+    cuda_ops entry point, host clock; GRM_Architecture_Blueprint_v2.1.md:266-272 gives 0.219 ms
+    native and 0.724 ms for the PyTorch fallback on an unspecified NVIDIA GPU).  The same
+    protocol through this repository's cuda_ops entry point, native and fallback."""
+    from rnn_with_grm_amd import cuda_ops
+
+    g = torch.Generator().manual_seed(0)
+    B, T, H, K = 4, 256, 256, 64
+    keys = torch.nn.functional.normalize(torch.randn(B, T, K, generator=g), p=2, dim=-1, eps=1e-6).to(dev)
+    queries = torch.nn.functional.normalize(torch.randn(B, T, K, generator=g), p=2, dim=-1, eps=1e-6).to(dev)
+    values = torch.randn(B, T, H, generator=g).to(dev)
+    memory = torch.randn(B, H, K, generator=g).to(dev)
+
+    def run(debug_fallback):
+        for _ in range(10):
+            cuda_ops.cuda_chunk_update(keys, values, queries, memory, memory_decay=0.97, enabled=True,
+                                       debug_fallback=debug_fallback)
+            torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(50):
+            cuda_ops.cuda_chunk_update(keys, values, queries, memory, memory_decay=0.97, enabled=True,
+                                       debug_fallback=debug_fallback)
+        torch.cuda.synchronize()
+        return (time.perf_counter() - t0) / 50 * 1e3
+
+    native, fallback = run(False), run(True)
+    return {"what": "the reference's published chunk-update microbenchmark (B=4, 256 tokens, d_v=256, d_k=64, fp32, "
+                    "cuda_ops entry point, 50 calls, host clock), same protocol here; published: 0.219 ms native, "
+                    "0.724 ms fallback, unspecified NVIDIA GPU",
+            "native_ms": round(native, 4), "fallback_ms": round(fallback, 4),
+            "native_tokens/s": round(B * T / native * 1e3), "published_native_ms": 0.219,
+            "published_fallback_ms": 0.724, "native_vs_published": round(0.219 / native, 2)}
+
+
 def bench_c5(torch, dev, steps, warmup):
     """Config 5: one whole-sequence update call (16 heads x 65536 tokens, a snapshot every 128
     tokens, 512 per head), then retrieval of k=16 archived states per token over those
@@ -547,6 +584,12 @@ def main() -> int:
                     "whole-sequence launches per layer, archive reset each forward",
             "ms": round(m4["ms"], 3), "tokens/s": round(m4["tokens"] / m4["ms"] * 1e3)}
         log(f"c4 forward: {m4['ms']:.2f} ms, {m4['tokens'] / m4['ms'] * 1e3:.3e} tokens/s")
+
+    if not a.no_gather:
+        pub = bench_published(torch, dev)
+        secondary["published_microbench"] = pub
+        log(f"published microbench shape: native {pub['native_ms']:.4f} ms (published 0.219), fallback "
+            f"{pub['fallback_ms']:.4f} ms (published 0.724)")
 
     cpu = None
     if not a.no_cpu:

@@ -95,13 +95,16 @@ def fwd_workspace_bytes(B: int, T: int, K: int, H: int, snapshot_len: int = 0) -
     return int(load().grm_hip_chunk_update_fwd_workspace(B, T, K, H, snapshot_len))
 
 
-def chunk_update_fwd(keys, values, queries, memory, decay: float, snapshot_len: int = 0, split: bool = True):
-    """Returns (hidden, memory_out, snapshots or None); inputs must be contiguous device tensors.
-    split=False withholds the workspace, so each sequence is scanned by one workgroup chain."""
+def chunk_update_fwd(keys, values, queries, memory, decay: float, snapshot_len: int = 0, split: bool = True,
+                     want_hidden: bool = True, want_memory_out: bool = True):
+    """Returns (hidden, memory_out, snapshots), each None when not requested; inputs must be
+    contiguous device tensors.  split=False withholds the workspace, so each sequence is
+    scanned by one workgroup chain.  want_hidden / want_memory_out=False pass NULL for that
+    output (memory_out may be NULL only when snapshots are requested)."""
     B, T, K = keys.shape
     H = values.shape[2]
-    hidden = torch.empty((B, T, H), dtype=values.dtype, device=values.device)
-    memory_out = torch.empty_like(memory)
+    hidden = torch.empty((B, T, H), dtype=values.dtype, device=values.device) if want_hidden else None
+    memory_out = torch.empty_like(memory) if want_memory_out else None
     snaps = None
     if snapshot_len > 0:
         snaps = torch.empty((B, (T + snapshot_len - 1) // snapshot_len, H, K), dtype=torch.float32,

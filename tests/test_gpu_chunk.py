@@ -210,6 +210,25 @@ def test_value_split_scan(dev, monkeypatch, dtype, mem_dtype, B, T, K, H, seg):
                                atol=1e-3 if mem_dtype != torch.float32 else 1e-6)
 
 
+@pytest.mark.parametrize("vsplit", ["1", "0"])
+def test_optional_outputs(dev, monkeypatch, vsplit):
+    """hidden may be NULL, and memory_out may be NULL when snapshots are requested; the outputs
+    that are written equal those of the full call, on both 16-bit scan kernels."""
+    B, T, K, H, seg = 2, 300, 128, 128, 64
+    k, v, q, m = make_case(B, T, K, H, torch.bfloat16, torch.float32, seed=29)
+    kd, vd, qd, md = k.to(dev), v.to(dev), q.to(dev), m.to(dev)
+    monkeypatch.setenv("GRM_HIP_CHUNK_VSPLIT", vsplit)
+    h, mo, s = capi.chunk_update_fwd(kd, vd, qd, md, 0.97, seg)
+    h1, mo1, s1 = capi.chunk_update_fwd(kd, vd, qd, md, 0.97, seg, want_hidden=False)
+    h2, mo2, s2 = capi.chunk_update_fwd(kd, vd, qd, md, 0.97, seg, want_memory_out=False)
+    torch.cuda.synchronize()
+    assert h1 is None and mo2 is None
+    assert torch.equal(mo1, mo) and torch.equal(s1, s)
+    assert torch.equal(h2, h) and torch.equal(s2, s)
+    with pytest.raises(RuntimeError):
+        capi.chunk_update_fwd(kd, vd, qd, md, 0.97, 0, want_memory_out=False)
+
+
 def test_value_split_is_default_at_config2_shape(dev, monkeypatch):
     """Config 2's shape (64 sequences x 128 value columns) takes the value-split scan
     by default; it and the time-split 128-column scan agree, and it is deterministic."""
