@@ -22,6 +22,7 @@
 #include <string.h>
 
 #include <cmath>
+#include <cstdlib>
 
 #include "grm_hip.h"
 #include "grm_hip_common.h"
@@ -263,10 +264,421 @@ int launch_bwd(const BwdArgs& a, void* grad_keys, void* grad_queries, hipStream_
   return check_launch("chunk_update_bwd(grad_queries)");
 }
 
+
+// ---------------------------------------------------------------------------
+// Chunk-parallel MFMA backward for 16-bit inputs (key_dim <= 128, value_dim a
+// multiple of 32, 16-byte rows).  The per-token recurrence above, summed over a
+// 64-token chunk: from the chunk's starting state M (the forward's chunk
+// states) and the adjoint G at its end (dL/dM after its last token), with
+// D[i][j] = decay^{i-j} (j <= i), P = c (Q K^T) o D and dS = c (dH V^T) o D,
+//   dQ = decay^{i+1} dH M + dS K
+//   dK = dS^T Q + c decay^{L-1-j} V G
+//   dV = P^T dH + c decay^{L-1-j} K G^T
+//   G  <- decay^L G + dH^T diag(decay^{i+1}) Q      (the adjoint at the chunk's start)
+// One workgroup of 4 waves per (sequence, 32-column value tile) walks the
+// chunks from the last.  The tile's G lives in fp32 MFMA accumulators, with a
+// 16-bit copy in LDS for the products that read it.  dQ and dK sum over every
+// value column, so each tile writes a partial and tile_sum_kernel adds the
+// tiles in order: deterministic, no atomics.  Wave w owns query/key block w
+// (tokens [16w, +16)) of every product and G rows [16 (w & 1), +16) x key
+// tiles [KT/2 (w >> 1), +KT/2).
+constexpr int MB_DV = 32;
+constexpr int MB_NT = 256;
+
+struct BwdMArgs {
+  const void* dh;
+  const void* dmo;
+  const void* keys;
+  const void* values;
+  const void* queries;
+  const void* memory;
+  const float* states;  // [B, n_chunks, dv, dk] state after each chunk
+  void* dv_out;
+  void* dm_out;
+  float* part_k;  // [B, tiles, T, dk]
+  float* part_q;  // [B, tiles, T, dk]
+  int64_t batch;
+  int64_t T;
+  int dk;
+  int dv;
+  int tiles;
+  int n_chunks;
+  int mem_f32;
+  int xcd_remap;
+  float c;
+  float pw[BCT + 1];  // decay^0 .. decay^64
+};
+
+template <int DKP>
+struct BmShape {
+  static constexpr int KS = DKP + 8;    // K, Q and 16-bit M, G rows (4 banks mod 64)
+  static constexpr int VS = MB_DV + 8;  // V, dH rows
+  static constexpr int PS = BCT + 8;    // P, dS rows
+  static constexpr int KT = DKP / 16;   // 16-wide key tiles
+  static constexpr int NKK = DKP / 32;  // 32-deep key steps
+  static constexpr int KU = DKP / 8;    // 16-byte units per K/Q row
+  static constexpr int K_UNITS = BCT * KU / MB_NT;
+  static constexpr int M_UNITS = MB_DV * KU / MB_NT;
+  static constexpr size_t lds_bytes =
+      static_cast<size_t>(2 * BCT * KS + 2 * BCT * VS + 3 * MB_DV * KS + 2 * BCT * PS) * 2 + (BCT + 1) * 4;
+  static_assert(K_UNITS * MB_NT == BCT * KU && M_UNITS * MB_NT == MB_DV * KU, "tiles split evenly");
+};
+
+template <class E>
+__device__ __forceinline__ Frag8<E> bw_frag_tr(const typename ET<E>::raw* p_lo, const typename ET<E>::raw* p_hi) {
+  // Four 16-bit elements of a row-major tile, transposed across each 16-lane
+  // block: lane i of the block receives X[r0 + e][c0 + i] (e = 0..3) when lane
+  // s of the block passes &X[r0 + (s >> 2)][c0 + 4 (s & 3)].
+  typedef short s16x4 __attribute__((ext_vector_type(4)));
+  typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
+  const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(p_lo));
+  const s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(p_hi));
+  Frag8<E> f;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    f.e[e] = static_cast<typename ET<E>::raw>(static_cast<uint16_t>(lo[e]));
+    f.e[4 + e] = static_cast<typename ET<E>::raw>(static_cast<uint16_t>(hi[e]));
+  }
+  return f;
+}
+
+template <class E, int DKP>
+__global__ __launch_bounds__(MB_NT, 1) void chunk_bwd_mfma_kernel(const BwdMArgs a) {
+  using S = BmShape<DKP>;
+  using raw = typename ET<E>::raw;
+  typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+  typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+  constexpr int KS = S::KS, VS = S::VS, PS = S::PS, KT = S::KT, NKK = S::NKK, KU = S::KU;
+  constexpr int GT = KT / 2;  // G key tiles per wave
+  constexpr int ES = 2;
+
+  extern __shared__ __align__(16) unsigned char smem[];
+  raw* Ks = reinterpret_cast<raw*>(smem);  // [BCT][KS]
+  raw* Qs = Ks + BCT * KS;                  // [BCT][KS]
+  raw* Vs = Qs + BCT * KS;                  // [BCT][VS] value tile columns
+  raw* Hs = Vs + BCT * VS;                  // [BCT][VS] grad_hidden tile columns
+  raw* Ms = Hs + BCT * VS;                  // [MB_DV][KS] the chunk's starting state, 16-bit
+  raw* Gs = Ms + MB_DV * KS;                // 2 x [MB_DV][KS] adjoint at the chunk's end, 16-bit
+  raw* Ps = Gs + 2 * MB_DV * KS;            // [BCT][PS] P
+  raw* Ds = Ps + BCT * PS;                  // [BCT][PS] dS
+  float* pw = reinterpret_cast<float*>(Ds + BCT * PS);
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int g = lane >> 4;
+  const int n = lane & 15;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+
+  int wg = blockIdx.x;
+  if (a.xcd_remap) {
+    const int per = gridDim.x >> 3;
+    wg = (wg & 7) * per + (wg >> 3);
+  }
+  const int tile = wg % a.tiles;
+  const int64_t b = wg / a.tiles;
+  const int v0 = tile * MB_DV;
+  const int dk = a.dk, dv = a.dv;
+  const int64_t T = a.T;
+  const float c = a.c;
+  const bool f32m = a.mem_f32 != 0;
+  const raw* keys = static_cast<const raw*>(a.keys) + b * T * dk;
+  const raw* queries = static_cast<const raw*>(a.queries) + b * T * dk;
+  const raw* values = static_cast<const raw*>(a.values) + b * T * dv;
+  const raw* dh = static_cast<const raw*>(a.dh) + b * T * dv;
+  if (tid <= BCT) pw[tid] = a.pw[tid];
+
+  // ---- the adjoint: gacc[t], lane (g, n), register r = G[v][k] with
+  //      v = v0 + 16 gvb + n and k = 16 (gk0 + t) + 4g + r.
+  const int gvb = w & 1, gk0 = GT * (w >> 1);
+  f32x4 gacc[GT];
+  auto g_off = [&](int t) -> int {
+    const int k = 16 * (gk0 + t) + 4 * g;
+    return k < dk ? (v0 + 16 * gvb + n) * dk + k : kBufOOB;
+  };
+  const int64_t mem_b = f32m ? 4 : ES;
+  {
+    const __amdgpu_buffer_rsrc_t rg = make_rsrc(static_cast<const unsigned char*>(a.dmo) + b * dv * dk * mem_b,
+                                                static_cast<uint32_t>(dv * dk * mem_b));
+#pragma unroll
+    for (int t = 0; t < GT; ++t) {
+      const int off = g_off(t);
+      if (f32m) {
+        const u32x4 u = __builtin_amdgcn_raw_buffer_load_b128(rg, off == kBufOOB ? kBufOOB : off * 4, 0, 0);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) gacc[t][i] = __uint_as_float(u[i]);
+      } else {
+        const u32x2 u = __builtin_amdgcn_raw_buffer_load_b64(rg, off == kBufOOB ? kBufOOB : off * ES, 0, 0);
+        gacc[t][0] = ET<E>::to_f(static_cast<raw>(u[0] & 0xffffu));
+        gacc[t][1] = ET<E>::to_f(static_cast<raw>(u[0] >> 16));
+        gacc[t][2] = ET<E>::to_f(static_cast<raw>(u[1] & 0xffffu));
+        gacc[t][3] = ET<E>::to_f(static_cast<raw>(u[1] >> 16));
+      }
+    }
+  }
+  auto publish_g = [&](int slot) {
+    raw* Gb = Gs + slot * MB_DV * KS;
+#pragma unroll
+    for (int t = 0; t < GT; ++t) store4_raw<E>(Gb + (16 * gvb + n) * KS + 16 * (gk0 + t) + 4 * g, gacc[t]);
+  };
+  publish_g(0);
+  int gslot = 0;
+  __syncthreads();  // pw
+
+  // Causal coefficients c decay^{i-j} of this wave's P / dS rows i = 16w + n
+  // against keys j = 16 jb + 4g + r; decay^{i+1} of its dQ rows; decay^{i+1} of
+  // the token slots i = 32p + 16 (s / 4) + 4g + s % 4 of the adjoint update.
+  float coef[4][4];
+#pragma unroll
+  for (int jb = 0; jb < 4; ++jb)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int i = 16 * w + n, j = 16 * jb + 4 * g + r;
+      coef[jb][r] = (j <= i) ? c * pw[max(i - j, 0)] : 0.f;
+    }
+  const float sq = pw[16 * w + n + 1];
+  float gw[2][8];
+#pragma unroll
+  for (int p = 0; p < 2; ++p)
+#pragma unroll
+    for (int s = 0; s < 8; ++s) gw[p][s] = pw[32 * p + 16 * (s >> 2) + 4 * g + (s & 3) + 1];
+
+  for (int ch = a.n_chunks - 1; ch >= 0; --ch) {
+    const int64_t t0 = static_cast<int64_t>(ch) * BCT;
+    const int L = static_cast<int>(min(static_cast<int64_t>(BCT), T - t0));
+    // ---- the chunk: K and Q rows, the tile's V and dH columns, the tile's starting state
+    {
+      const __amdgpu_buffer_rsrc_t rk = make_rsrc(keys + t0 * dk, static_cast<uint32_t>(L * dk * ES));
+      const __amdgpu_buffer_rsrc_t rq = make_rsrc(queries + t0 * dk, static_cast<uint32_t>(L * dk * ES));
+      const __amdgpu_buffer_rsrc_t rv = make_rsrc(values + t0 * dv, static_cast<uint32_t>(L * dv * ES));
+      const __amdgpu_buffer_rsrc_t rh = make_rsrc(dh + t0 * dv, static_cast<uint32_t>(L * dv * ES));
+#pragma unroll
+      for (int u = 0; u < S::K_UNITS; ++u) {
+        const int l = tid + MB_NT * u;
+        const int row = l / KU, col = 8 * (l % KU);
+        const int off = col < dk ? (row * dk + col) * ES : kBufOOB;
+        *reinterpret_cast<U8<E>*>(Ks + row * KS + col) = buf_load8<E>(rk, off);
+        *reinterpret_cast<U8<E>*>(Qs + row * KS + col) = buf_load8<E>(rq, off);
+      }
+      {
+        const int row = tid >> 2, col = 8 * (tid & 3);
+        const int off = (row * dv + v0 + col) * ES;
+        *reinterpret_cast<U8<E>*>(Vs + row * VS + col) = buf_load8<E>(rv, off);
+        *reinterpret_cast<U8<E>*>(Hs + row * VS + col) = buf_load8<E>(rh, off);
+      }
+      const bool from_m0 = ch == 0;
+      const unsigned char* msrc = from_m0 ? static_cast<const unsigned char*>(a.memory) + b * dv * dk * mem_b
+                                          : reinterpret_cast<const unsigned char*>(
+                                                a.states + (b * a.n_chunks + ch - 1) * dv * dk);
+      const bool src32 = !from_m0 || f32m;
+      const __amdgpu_buffer_rsrc_t rm = make_rsrc(msrc, static_cast<uint32_t>(dv * dk * (src32 ? 4 : ES)));
+#pragma unroll
+      for (int u = 0; u < S::M_UNITS; ++u) {
+        const int l = tid + MB_NT * u;
+        const int row = l / KU, col = 8 * (l % KU);
+        const int el = col < dk ? (v0 + row) * dk + col : -1;
+        U8<E> val;
+        if (src32) {
+          const u32x4 x0 = __builtin_amdgcn_raw_buffer_load_b128(rm, el < 0 ? kBufOOB : el * 4, 0, 0);
+          const u32x4 x1 = __builtin_amdgcn_raw_buffer_load_b128(rm, el < 0 ? kBufOOB : el * 4 + 16, 0, 0);
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            val.e[i] = ET<E>::from_f(__uint_as_float(x0[i]));
+            val.e[4 + i] = ET<E>::from_f(__uint_as_float(x1[i]));
+          }
+        } else {
+          val = buf_load8<E>(rm, el < 0 ? kBufOOB : el * ES);
+        }
+        *reinterpret_cast<U8<E>*>(Ms + row * KS + col) = val;
+      }
+    }
+    __syncthreads();  // chunk in LDS
+
+    // ---- P and dS rows of query block w (blocks right of the diagonal are zeros)
+    {
+      Frag8<E> qf[NKK];
+#pragma unroll
+      for (int kk = 0; kk < NKK; ++kk)
+        qf[kk] = *reinterpret_cast<const Frag8<E>*>(Qs + (16 * w + n) * KS + 32 * kk + 8 * g);
+      const Frag8<E> hf = *reinterpret_cast<const Frag8<E>*>(Hs + (16 * w + n) * VS + 8 * g);
+#pragma unroll
+      for (int jb = 0; jb < 4; ++jb) {
+        f32x4 sacc = f32x4{0.f, 0.f, 0.f, 0.f}, aacc = f32x4{0.f, 0.f, 0.f, 0.f};
+        if (jb <= w) {
+#pragma unroll
+          for (int kk = 0; kk < NKK; ++kk) {
+            const Frag8<E> kf = *reinterpret_cast<const Frag8<E>*>(Ks + (16 * jb + n) * KS + 32 * kk + 8 * g);
+            sacc = mfma8(kf, qf[kk], sacc);
+          }
+          const Frag8<E> vfj = *reinterpret_cast<const Frag8<E>*>(Vs + (16 * jb + n) * VS + 8 * g);
+          aacc = mfma8(vfj, hf, aacc);
+        }
+        const f32x4 cf = f32x4{coef[jb][0], coef[jb][1], coef[jb][2], coef[jb][3]};
+        store4_raw<E>(Ps + (16 * w + n) * PS + 16 * jb + 4 * g, sacc * cf);
+        store4_raw<E>(Ds + (16 * w + n) * PS + 16 * jb + 4 * g, aacc * cf);
+      }
+    }
+    __syncthreads();  // P and dS complete
+
+    const raw* Gb = Gs + gslot * MB_DV * KS;
+    const int jrow = 16 * w + n;  // this lane's key / query row
+    const float wl = (jrow < L) ? c * pw[max(L - 1 - jrow, 0)] : 0.f;
+    // ---- dQ rows of block w: D[kcol][i] = decay^{i+1} sum_v M[v][kcol] dH[i][v] + sum_j K[j][kcol] dS[i][j]
+    {
+      const __amdgpu_buffer_rsrc_t rpq = make_rsrc(a.part_q + ((b * a.tiles + tile) * T + t0) * dk,
+                                                   static_cast<uint32_t>(L * dk * 4));
+      const Frag8<E> hq = lds_frag_4x2<E>(Hs + jrow * VS + 4 * g, Hs + jrow * VS + 4 * g + 16);
+      Frag8<E> dsf[2];
+#pragma unroll
+      for (int p = 0; p < 2; ++p)
+        dsf[p] = lds_frag_4x2<E>(Ds + jrow * PS + 32 * p + 4 * g, Ds + jrow * PS + 32 * p + 4 * g + 16);
+#pragma unroll
+      for (int kt = 0; kt < KT; ++kt) {
+        const raw* mb = Ms + (4 * g + (n >> 2)) * KS + 16 * kt + 4 * (n & 3);
+        const Frag8<E> mT = bw_frag_tr<E>(mb, mb + 16 * KS);
+        f32x4 acc = mfma8(mT, hq, f32x4{0.f, 0.f, 0.f, 0.f}) * sq;
+#pragma unroll
+        for (int p = 0; p < 2; ++p) {
+          if (32 * p > 16 * w + 15) continue;
+          const raw* kb = Ks + (32 * p + 4 * g + (n >> 2)) * KS + 16 * kt + 4 * (n & 3);
+          acc = mfma8(bw_frag_tr<E>(kb, kb + 16 * KS), dsf[p], acc);
+        }
+        const int kc = 16 * kt + 4 * g;
+        const u32x4 q = u32x4{__float_as_uint(acc[0]), __float_as_uint(acc[1]), __float_as_uint(acc[2]),
+                              __float_as_uint(acc[3])};
+        __builtin_amdgcn_raw_buffer_store_b128(q, rpq, kc < dk ? (jrow * dk + kc) * 4 : kBufOOB, 0, 0);
+      }
+    }
+    // ---- dK rows of block w: D[kcol][j] = c decay^{L-1-j} sum_v G[v][kcol] V[j][v] + sum_i Q[i][kcol] dS[i][j]
+    //      dV rows of block w: D[v][j]    = c decay^{L-1-j} sum_k G[v][k] K[j][k] + sum_i dH[i][v] P[i][j]
+    {
+      // Columns j of dS and P: lane n holds rows i = 32p + 4g + e (+16), column 16w + n.
+      Frag8<E> dsT[2], pT[2];
+#pragma unroll
+      for (int p = 0; p < 2; ++p) {
+        const int off = (32 * p + 4 * g + (n >> 2)) * PS + 16 * w + 4 * (n & 3);
+        dsT[p] = bw_frag_tr<E>(Ds + off, Ds + off + 16 * PS);
+        pT[p] = bw_frag_tr<E>(Ps + off, Ps + off + 16 * PS);
+      }
+      const __amdgpu_buffer_rsrc_t rpk = make_rsrc(a.part_k + ((b * a.tiles + tile) * T + t0) * dk,
+                                                   static_cast<uint32_t>(L * dk * 4));
+      const Frag8<E> vj = lds_frag_4x2<E>(Vs + jrow * VS + 4 * g, Vs + jrow * VS + 4 * g + 16);
+#pragma unroll
+      for (int kt = 0; kt < KT; ++kt) {
+        const raw* gbt = Gb + (4 * g + (n >> 2)) * KS + 16 * kt + 4 * (n & 3);
+        f32x4 acc = mfma8(bw_frag_tr<E>(gbt, gbt + 16 * KS), vj, f32x4{0.f, 0.f, 0.f, 0.f}) * wl;
+#pragma unroll
+        for (int p = 0; p < 2; ++p) {
+          if (32 * p + 31 < 16 * w) continue;
+          const raw* qb = Qs + (32 * p + 4 * g + (n >> 2)) * KS + 16 * kt + 4 * (n & 3);
+          acc = mfma8(bw_frag_tr<E>(qb, qb + 16 * KS), dsT[p], acc);
+        }
+        const int kc = 16 * kt + 4 * g;
+        const u32x4 q = u32x4{__float_as_uint(acc[0]), __float_as_uint(acc[1]), __float_as_uint(acc[2]),
+                              __float_as_uint(acc[3])};
+        __builtin_amdgcn_raw_buffer_store_b128(q, rpk, kc < dk ? (jrow * dk + kc) * 4 : kBufOOB, 0, 0);
+      }
+      const __amdgpu_buffer_rsrc_t rdv = make_rsrc(static_cast<raw*>(a.dv_out) + (b * T + t0) * dv,
+                                                   static_cast<uint32_t>(L * dv * ES));
+      Frag8<E> kr[NKK];
+#pragma unroll
+      for (int kk = 0; kk < NKK; ++kk)
+        kr[kk] = *reinterpret_cast<const Frag8<E>*>(Ks + jrow * KS + 32 * kk + 8 * g);
+#pragma unroll
+      for (int vb = 0; vb < 2; ++vb) {
+        f32x4 acc = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int kk = 0; kk < NKK; ++kk)
+          acc = mfma8(*reinterpret_cast<const Frag8<E>*>(Gb + (16 * vb + n) * KS + 32 * kk + 8 * g), kr[kk], acc);
+        acc *= wl;
+#pragma unroll
+        for (int p = 0; p < 2; ++p) {
+          if (32 * p + 31 < 16 * w) continue;
+          const raw* hb = Hs + (32 * p + 4 * g + (n >> 2)) * VS + 16 * vb + 4 * (n & 3);
+          acc = mfma8(bw_frag_tr<E>(hb, hb + 16 * VS), pT[p], acc);
+        }
+        buf_store4<E>(rdv, (jrow * dv + v0 + 16 * vb + 4 * g) * ES, acc);
+      }
+    }
+    // ---- the adjoint at the chunk's start: G = decay^L G + sum_i decay^{i+1} dH[i][v] Q[i][k]
+    {
+      Frag8<E> hw[2];
+#pragma unroll
+      for (int p = 0; p < 2; ++p) {
+        const raw* hb = Hs + (32 * p + 4 * g + (n >> 2)) * VS + 16 * gvb + 4 * (n & 3);
+        const Frag8<E> h = bw_frag_tr<E>(hb, hb + 16 * VS);
+#pragma unroll
+        for (int s = 0; s < 8; ++s) hw[p].e[s] = ET<E>::from_f(ET<E>::to_f(h.e[s]) * gw[p][s]);
+      }
+      const float decay_L = pw[L];
+#pragma unroll
+      for (int t = 0; t < GT; ++t) {
+        f32x4 acc = gacc[t] * decay_L;
+#pragma unroll
+        for (int p = 0; p < 2; ++p) {
+          const raw* qb = Qs + (32 * p + 4 * g + (n >> 2)) * KS + 16 * (gk0 + t) + 4 * (n & 3);
+          acc = mfma8(bw_frag_tr<E>(qb, qb + 16 * KS), hw[p], acc);
+        }
+        gacc[t] = acc;
+      }
+      gslot ^= 1;
+      publish_g(gslot);
+    }
+    __syncthreads();  // every read of this chunk's tiles done; the new 16-bit G visible
+  }
+
+  // grad_memory: the adjoint at the sequence's start.
+  const __amdgpu_buffer_rsrc_t ro = make_rsrc(static_cast<unsigned char*>(a.dm_out) + b * dv * dk * mem_b,
+                                              static_cast<uint32_t>(dv * dk * mem_b));
+#pragma unroll
+  for (int t = 0; t < GT; ++t) {
+    const int off = g_off(t);
+    if (f32m) {
+      buf_store4<F32>(ro, off == kBufOOB ? kBufOOB : off * 4, gacc[t]);
+    } else {
+      buf_store4<E>(ro, off == kBufOOB ? kBufOOB : off * ES, gacc[t]);
+    }
+  }
+}
+
+template <class E, int DKP>
+int launch_bwd_mfma(BwdMArgs a, void* grad_keys, void* grad_queries, hipStream_t s) {
+  using S = BmShape<DKP>;
+  static bool attr_set = false;
+  if (!attr_set) {
+    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&chunk_bwd_mfma_kernel<E, DKP>),
+                                       hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(S::lds_bytes));
+    if (e != hipSuccess) {
+      set_error("chunk_update_bwd: hipFuncSetAttribute failed: %s", hipGetErrorString(e));
+      return static_cast<int>(e);
+    }
+    attr_set = true;
+  }
+  const int64_t grid = a.batch * a.tiles;
+  a.xcd_remap = (grid % 8 == 0) ? 1 : 0;
+  hipLaunchKernelGGL((chunk_bwd_mfma_kernel<E, DKP>), dim3(static_cast<unsigned>(grid)), dim3(MB_NT), S::lds_bytes,
+                     s, a);
+  int rc = check_launch("chunk_update_bwd");
+  if (rc != GRM_HIP_OK) return rc;
+  const int64_t n = a.batch * a.T * a.dk;
+  const int64_t want = (n + 255) / 256;
+  const unsigned g = static_cast<unsigned>(want < 256 * 64 ? want : 256 * 64);
+  hipLaunchKernelGGL(tile_sum_kernel<E>, dim3(g < 1 ? 1 : g), dim3(256), 0, s, a.part_k, grad_keys, a.batch,
+                     a.tiles, a.T, a.dk);
+  rc = check_launch("chunk_update_bwd(grad_keys)");
+  if (rc != GRM_HIP_OK) return rc;
+  hipLaunchKernelGGL(tile_sum_kernel<E>, dim3(g < 1 ? 1 : g), dim3(256), 0, s, a.part_q, grad_queries, a.batch,
+                     a.tiles, a.T, a.dk);
+  return check_launch("chunk_update_bwd(grad_queries)");
+}
+
 }  // namespace
 }  // namespace grmhip
 
 using namespace grmhip;
+
+namespace {
+bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+}  // namespace
 
 extern "C" int grm_hip_chunk_update_bwd(const void* grad_hidden, const void* grad_memory_out,
                                         const void* keys, const void* values, const void* queries,
@@ -327,6 +739,43 @@ extern "C" int grm_hip_chunk_update_bwd(const void* grad_hidden, const void* gra
                                     nullptr, 0, batch, seq_len, key_dim, value_dim, in_dtype,
                                     mem_dtype, memory_decay, BCT, stream);
   if (rc != GRM_HIP_OK) return rc;
+
+  const char* env = getenv("GRM_HIP_BWD_MFMA");
+  const bool mfma = (env == nullptr || env[0] != '0') && (in_dtype == GRM_HIP_BF16 || in_dtype == GRM_HIP_F16) &&
+                    key_dim <= 128 && key_dim % 8 == 0 && value_dim % MB_DV == 0 &&
+                    aligned16(grad_hidden) && aligned16(keys) && aligned16(values) && aligned16(queries) &&
+                    aligned16(grad_values) && aligned16(dkq_partial) && aligned16(memory) &&
+                    aligned16(grad_memory_out) && aligned16(grad_memory) && aligned16(chunk_states);
+  if (mfma) {
+    BwdMArgs m;
+    memset(&m, 0, sizeof(m));
+    m.dh = grad_hidden;
+    m.dmo = grad_memory_out;
+    m.keys = keys;
+    m.values = values;
+    m.queries = queries;
+    m.memory = memory;
+    m.states = chunk_states;
+    m.dv_out = grad_values;
+    m.dm_out = grad_memory;
+    m.tiles = static_cast<int>(value_dim / MB_DV);
+    m.part_k = dkq_partial;
+    m.part_q = dkq_partial + batch * m.tiles * seq_len * key_dim;
+    m.batch = batch;
+    m.T = seq_len;
+    m.dk = static_cast<int>(key_dim);
+    m.dv = static_cast<int>(value_dim);
+    m.n_chunks = static_cast<int>(n_chunks);
+    m.mem_f32 = mem_dtype == GRM_HIP_F32;
+    m.c = static_cast<float>((1.0 - memory_decay) / std::sqrt(static_cast<double>(key_dim)));
+    for (int i = 0; i <= BCT; ++i) m.pw[i] = static_cast<float>(std::pow(memory_decay, i));
+    if (in_dtype == GRM_HIP_F16) {
+      return key_dim <= 64 ? launch_bwd_mfma<F16, 64>(m, grad_keys, grad_queries, s)
+                           : launch_bwd_mfma<F16, 128>(m, grad_keys, grad_queries, s);
+    }
+    return key_dim <= 64 ? launch_bwd_mfma<BF16, 64>(m, grad_keys, grad_queries, s)
+                         : launch_bwd_mfma<BF16, 128>(m, grad_keys, grad_queries, s);
+  }
 
   BwdArgs a;
   memset(&a, 0, sizeof(a));

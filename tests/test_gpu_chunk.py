@@ -303,6 +303,46 @@ def test_chunk_backward(dev, dtype, mem_dtype, B, T, K, H):
             close(name, got, ref, torch.bfloat16)
 
 
+def close_scaled(name, got, ref, rel_l2, max_frac):
+    """|got - ref| against the scale of the whole tensor: relative L2 error and max error as a
+    fraction of max |ref|.  The MFMA backward rounds the chunk's starting state, the adjoint,
+    P and dS to the input's 16-bit type as MFMA operands, so its error scales with the tensor,
+    not with each element."""
+    got = got.float().cpu().double().numpy()
+    den = np.linalg.norm(ref)
+    rel = np.linalg.norm(got - ref) / den if den > 0 else np.linalg.norm(got)
+    assert rel < rel_l2, f"{name}: relative L2 error {rel:.3e}"
+    scale = np.abs(ref).max()
+    assert np.abs(got - ref).max() <= max_frac * max(scale, 1e-30), f"{name}: max error beyond {max_frac} x max|ref|"
+
+
+@pytest.mark.parametrize("dtype,mem_dtype", [(torch.bfloat16, torch.float32), (torch.float16, torch.float32),
+                                             (torch.bfloat16, torch.bfloat16), (torch.float16, torch.float16)])
+@pytest.mark.parametrize("B,T,K,H", [(2, 300, 128, 128), (3, 129, 64, 64), (1, 640, 96, 96), (2, 64, 128, 32),
+                                     (1, 7, 128, 32), (2, 200, 32, 64)])
+def test_mfma_backward(dev, monkeypatch, dtype, mem_dtype, B, T, K, H):
+    """The chunk-parallel MFMA backward (16-bit inputs, value_dim a multiple of 32) against the
+    double-precision oracle and against the scalar per-token kernel (GRM_HIP_BWD_MFMA=0):
+    ragged last chunks, key widths below the padded 64/128, one to four value tiles, one chunk."""
+    k, v, q, m = make_case(B, T, K, H, dtype, mem_dtype, seed=B * 13 + T)
+    g = torch.Generator().manual_seed(7)
+    dh = torch.randn(B, T, H, generator=g).to(dtype)
+    dm = torch.randn(B, H, K, generator=g).to(mem_dtype)
+    args = [t.to(dev) for t in (dh, dm, k, v, q, m)]
+    print(f"mfma backward B={B} T={T} K={K} H={H} {dtype} state {mem_dtype}", flush=True)
+    got = capi.chunk_update_bwd(*args, 0.97)
+    monkeypatch.setenv("GRM_HIP_BWD_MFMA", "0")
+    scalar = capi.chunk_update_bwd(*args, 0.97)
+    torch.cuda.synchronize()
+    ref = orc.chunk_update_bwd(dh.double().numpy(), dm.double().numpy(), k.double().numpy(), v.double().numpy(),
+                               q.double().numpy(), m.double().numpy(), 0.97)
+    rel_l2 = 1e-2 if dtype == torch.bfloat16 or mem_dtype == torch.bfloat16 else 5e-3
+    for name, x, y, r in zip(("grad_keys", "grad_values", "grad_queries", "grad_memory"), got, scalar, ref):
+        assert torch.isfinite(x.float()).all(), name
+        close_scaled(name, x, r, rel_l2, 2e-2)
+        close_scaled(name + " vs scalar kernel", x, y.float().cpu().double().numpy(), rel_l2, 2e-2)
+
+
 def test_autograd_through_cuda_ops(dev):
     """cuda_chunk_update under autograd matches the fallback's autograd (the
     reference's check, examples/test_grm.py:72-113)."""
