@@ -240,6 +240,28 @@ __global__ __launch_bounds__(256) void tile_sum_kernel(const float* part, void* 
   }
 }
 
+// The same sum for two partial arrays at once, 16 bytes of each tile per
+// thread: quad i of [batch, T * dk / 4] (plane = T * dk / 4 quads per
+// sequence); thread indices from `quads` on take the second array.
+template <class E>
+__global__ __launch_bounds__(256) void tile_sum4_kernel(const float* part0, const float* part1, void* out0,
+                                                        void* out1, int tiles, int64_t plane, int64_t quads) {
+  for (int64_t j = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x; j < 2 * quads;
+       j += static_cast<int64_t>(gridDim.x) * 256) {
+    const bool second = j >= quads;
+    const int64_t i = second ? j - quads : j;
+    const int64_t b = i / plane;
+    using f32x4 = float __attribute__((ext_vector_type(4)));
+    const f32x4* p = reinterpret_cast<const f32x4*>(second ? part1 : part0) + b * tiles * plane + (i - b * plane);
+    f32x4 acc = __builtin_nontemporal_load(p);
+    for (int t = 1; t < tiles; ++t) acc += __builtin_nontemporal_load(p + t * plane);
+    static_assert(sizeof(typename ET<E>::raw) == 2, "16-bit outputs");
+    const uint32_t lo = static_cast<uint32_t>(ET<E>::from_f(acc[0])) | static_cast<uint32_t>(ET<E>::from_f(acc[1])) << 16;
+    const uint32_t hi = static_cast<uint32_t>(ET<E>::from_f(acc[2])) | static_cast<uint32_t>(ET<E>::from_f(acc[3])) << 16;
+    reinterpret_cast<uint2*>(second ? out1 : out0)[i] = make_uint2(lo, hi);
+  }
+}
+
 template <class E>
 int launch_bwd(const BwdArgs& a, void* grad_keys, void* grad_queries, hipStream_t s) {
   const dim3 grid(static_cast<unsigned>(a.batch * a.tiles));
@@ -442,55 +464,89 @@ __global__ __launch_bounds__(MB_NT, 1) void chunk_bwd_mfma_kernel(const BwdMArgs
 #pragma unroll
     for (int s = 0; s < 8; ++s) gw[p][s] = pw[32 * p + 16 * (s >> 2) + 4 * g + (s & 3) + 1];
 
+  // ---- chunk staging: loads of chunk ch - 1 are in flight while chunk ch is
+  // processed.  K/Q unit u of thread t is row (t + 256 u) / KU, 16-byte column
+  // (t + 256 u) % KU; its V / dH unit is row t / 4, columns 8 (t % 4) of the
+  // tile; its state unit u is row (t + 256 u) / KU of the tile, 8 key columns.
+  struct Stage {
+    U8<E> k[S::K_UNITS];
+    U8<E> q[S::K_UNITS];
+    U8<E> v, h;
+    u32x4 m[S::M_UNITS][2];  // 8 fp32 values, or 8 16-bit values in m[u][0]
+  };
+  auto load_chunk = [&](int ch, Stage& sg) {
+    const int64_t t0 = static_cast<int64_t>(ch) * BCT;
+    const int L = static_cast<int>(min(static_cast<int64_t>(BCT), T - t0));
+    const __amdgpu_buffer_rsrc_t rk = make_rsrc(keys + t0 * dk, static_cast<uint32_t>(L * dk * ES));
+    const __amdgpu_buffer_rsrc_t rq = make_rsrc(queries + t0 * dk, static_cast<uint32_t>(L * dk * ES));
+    const __amdgpu_buffer_rsrc_t rv = make_rsrc(values + t0 * dv, static_cast<uint32_t>(L * dv * ES));
+    const __amdgpu_buffer_rsrc_t rh = make_rsrc(dh + t0 * dv, static_cast<uint32_t>(L * dv * ES));
+#pragma unroll
+    for (int u = 0; u < S::K_UNITS; ++u) {
+      const int l = tid + MB_NT * u;
+      const int row = l / KU, col = 8 * (l % KU);
+      const int off = col < dk ? (row * dk + col) * ES : kBufOOB;
+      sg.k[u] = buf_load8<E>(rk, off);
+      sg.q[u] = buf_load8<E>(rq, off);
+    }
+    const int off = ((tid >> 2) * dv + v0 + 8 * (tid & 3)) * ES;
+    sg.v = buf_load8<E>(rv, off);
+    sg.h = buf_load8<E>(rh, off);
+    const bool from_m0 = ch == 0;
+    const unsigned char* msrc = from_m0 ? static_cast<const unsigned char*>(a.memory) + b * dv * dk * mem_b
+                                        : reinterpret_cast<const unsigned char*>(
+                                              a.states + (b * a.n_chunks + ch - 1) * dv * dk);
+    const bool src32 = !from_m0 || f32m;
+    const __amdgpu_buffer_rsrc_t rm = make_rsrc(msrc, static_cast<uint32_t>(dv * dk * (src32 ? 4 : ES)));
+#pragma unroll
+    for (int u = 0; u < S::M_UNITS; ++u) {
+      const int l = tid + MB_NT * u;
+      const int row = l / KU, col = 8 * (l % KU);
+      const int el = col < dk ? (v0 + row) * dk + col : -1;
+      if (src32) {
+        sg.m[u][0] = __builtin_amdgcn_raw_buffer_load_b128(rm, el < 0 ? kBufOOB : el * 4, 0, 0);
+        sg.m[u][1] = __builtin_amdgcn_raw_buffer_load_b128(rm, el < 0 ? kBufOOB : el * 4 + 16, 0, 0);
+      } else {
+        sg.m[u][0] = __builtin_amdgcn_raw_buffer_load_b128(rm, el < 0 ? kBufOOB : el * ES, 0, 0);
+      }
+    }
+  };
+  auto store_chunk = [&](int ch, const Stage& sg) {
+    const bool src32 = ch != 0 || f32m;
+#pragma unroll
+    for (int u = 0; u < S::K_UNITS; ++u) {
+      const int l = tid + MB_NT * u;
+      const int row = l / KU, col = 8 * (l % KU);
+      *reinterpret_cast<U8<E>*>(Ks + row * KS + col) = sg.k[u];
+      *reinterpret_cast<U8<E>*>(Qs + row * KS + col) = sg.q[u];
+    }
+    *reinterpret_cast<U8<E>*>(Vs + (tid >> 2) * VS + 8 * (tid & 3)) = sg.v;
+    *reinterpret_cast<U8<E>*>(Hs + (tid >> 2) * VS + 8 * (tid & 3)) = sg.h;
+#pragma unroll
+    for (int u = 0; u < S::M_UNITS; ++u) {
+      const int l = tid + MB_NT * u;
+      const int row = l / KU, col = 8 * (l % KU);
+      U8<E> val;
+      if (src32) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          val.e[i] = ET<E>::from_f(__uint_as_float(sg.m[u][0][i]));
+          val.e[4 + i] = ET<E>::from_f(__uint_as_float(sg.m[u][1][i]));
+        }
+      } else {
+        val = __builtin_bit_cast(U8<E>, sg.m[u][0]);
+      }
+      *reinterpret_cast<U8<E>*>(Ms + row * KS + col) = val;
+    }
+  };
+
+  Stage stage;
+  load_chunk(a.n_chunks - 1, stage);
   for (int ch = a.n_chunks - 1; ch >= 0; --ch) {
     const int64_t t0 = static_cast<int64_t>(ch) * BCT;
     const int L = static_cast<int>(min(static_cast<int64_t>(BCT), T - t0));
-    // ---- the chunk: K and Q rows, the tile's V and dH columns, the tile's starting state
-    {
-      const __amdgpu_buffer_rsrc_t rk = make_rsrc(keys + t0 * dk, static_cast<uint32_t>(L * dk * ES));
-      const __amdgpu_buffer_rsrc_t rq = make_rsrc(queries + t0 * dk, static_cast<uint32_t>(L * dk * ES));
-      const __amdgpu_buffer_rsrc_t rv = make_rsrc(values + t0 * dv, static_cast<uint32_t>(L * dv * ES));
-      const __amdgpu_buffer_rsrc_t rh = make_rsrc(dh + t0 * dv, static_cast<uint32_t>(L * dv * ES));
-#pragma unroll
-      for (int u = 0; u < S::K_UNITS; ++u) {
-        const int l = tid + MB_NT * u;
-        const int row = l / KU, col = 8 * (l % KU);
-        const int off = col < dk ? (row * dk + col) * ES : kBufOOB;
-        *reinterpret_cast<U8<E>*>(Ks + row * KS + col) = buf_load8<E>(rk, off);
-        *reinterpret_cast<U8<E>*>(Qs + row * KS + col) = buf_load8<E>(rq, off);
-      }
-      {
-        const int row = tid >> 2, col = 8 * (tid & 3);
-        const int off = (row * dv + v0 + col) * ES;
-        *reinterpret_cast<U8<E>*>(Vs + row * VS + col) = buf_load8<E>(rv, off);
-        *reinterpret_cast<U8<E>*>(Hs + row * VS + col) = buf_load8<E>(rh, off);
-      }
-      const bool from_m0 = ch == 0;
-      const unsigned char* msrc = from_m0 ? static_cast<const unsigned char*>(a.memory) + b * dv * dk * mem_b
-                                          : reinterpret_cast<const unsigned char*>(
-                                                a.states + (b * a.n_chunks + ch - 1) * dv * dk);
-      const bool src32 = !from_m0 || f32m;
-      const __amdgpu_buffer_rsrc_t rm = make_rsrc(msrc, static_cast<uint32_t>(dv * dk * (src32 ? 4 : ES)));
-#pragma unroll
-      for (int u = 0; u < S::M_UNITS; ++u) {
-        const int l = tid + MB_NT * u;
-        const int row = l / KU, col = 8 * (l % KU);
-        const int el = col < dk ? (v0 + row) * dk + col : -1;
-        U8<E> val;
-        if (src32) {
-          const u32x4 x0 = __builtin_amdgcn_raw_buffer_load_b128(rm, el < 0 ? kBufOOB : el * 4, 0, 0);
-          const u32x4 x1 = __builtin_amdgcn_raw_buffer_load_b128(rm, el < 0 ? kBufOOB : el * 4 + 16, 0, 0);
-#pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            val.e[i] = ET<E>::from_f(__uint_as_float(x0[i]));
-            val.e[4 + i] = ET<E>::from_f(__uint_as_float(x1[i]));
-          }
-        } else {
-          val = buf_load8<E>(rm, el < 0 ? kBufOOB : el * ES);
-        }
-        *reinterpret_cast<U8<E>*>(Ms + row * KS + col) = val;
-      }
-    }
+    store_chunk(ch, stage);
+    if (ch > 0) load_chunk(ch - 1, stage);
     __syncthreads();  // chunk in LDS
 
     // ---- P and dS rows of query block w (blocks right of the diagonal are zeros)
@@ -659,16 +715,13 @@ int launch_bwd_mfma(BwdMArgs a, void* grad_keys, void* grad_queries, hipStream_t
                      s, a);
   int rc = check_launch("chunk_update_bwd");
   if (rc != GRM_HIP_OK) return rc;
-  const int64_t n = a.batch * a.T * a.dk;
-  const int64_t want = (n + 255) / 256;
-  const unsigned g = static_cast<unsigned>(want < 256 * 64 ? want : 256 * 64);
-  hipLaunchKernelGGL(tile_sum_kernel<E>, dim3(g < 1 ? 1 : g), dim3(256), 0, s, a.part_k, grad_keys, a.batch,
-                     a.tiles, a.T, a.dk);
-  rc = check_launch("chunk_update_bwd(grad_keys)");
-  if (rc != GRM_HIP_OK) return rc;
-  hipLaunchKernelGGL(tile_sum_kernel<E>, dim3(g < 1 ? 1 : g), dim3(256), 0, s, a.part_q, grad_queries, a.batch,
-                     a.tiles, a.T, a.dk);
-  return check_launch("chunk_update_bwd(grad_queries)");
+  // Both gradients in one launch: 4 columns per thread (key_dim % 8 == 0 here).
+  const int64_t quads = a.batch * a.T * a.dk / 4;
+  const int64_t want = (2 * quads + 255) / 256;
+  const unsigned g = static_cast<unsigned>(want < 256 * 128 ? want : 256 * 128);
+  hipLaunchKernelGGL(tile_sum4_kernel<E>, dim3(g < 1 ? 1 : g), dim3(256), 0, s, a.part_k, a.part_q, grad_keys,
+                     grad_queries, a.tiles, a.T * a.dk / 4, quads);
+  return check_launch("chunk_update_bwd(grad_keys, grad_queries)");
 }
 
 }  // namespace
