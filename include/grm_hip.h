@@ -89,9 +89,11 @@ int64_t grm_hip_chunk_update_fwd_workspace(int64_t batch, int64_t seq_len, int64
  * come in the input dtype and mem_dtype; the four gradients are written in the
  * dtype of the tensor they belong to.
  * chunk_states: float32 workspace [batch, ceil(seq_len / 64), value_dim, key_dim]
- *   (caller-provided; overwritten with the state at the start of each 64-token chunk).
+ *   (caller-provided; overwritten with the state after each 64-token chunk).
  * dkq_partial: float32 workspace [2, batch, ceil(value_dim / 16), seq_len, key_dim]
- *   (caller-provided; per value-tile partial sums of grad_keys and grad_queries).
+ *   (caller-provided; per value-tile partial sums of grad_keys and grad_queries: 16-column
+ *   tiles in the scalar kernel, 32-column tiles [2, batch, value_dim / 32, seq_len, key_dim]
+ *   at the front of the same buffer in the MFMA kernel for 16-bit inputs).
  */
 int grm_hip_chunk_update_bwd(const void* grad_hidden, const void* grad_memory_out, const void* keys,
                              const void* values, const void* queries, const void* memory,
