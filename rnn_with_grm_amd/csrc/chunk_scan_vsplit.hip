@@ -242,28 +242,36 @@ __global__ __launch_bounds__(kVsThreads, 1) void scan_vsplit_kernel(const ChunkF
   };
   // P wave p: S rows i = 16 p + n against key blocks jb <= p (lane holds
   // S[i][16 jb + 4g + r]); the blocks right of the diagonal are written as
-  // zeros, so the M waves read whole P rows without branches.
+  // zeros, so the M waves read whole P rows without branches.  The wave index
+  // is a compile-time constant here: every K fragment the wave multiplies is
+  // read first and its p + 1 block chains interleave.
   const int i_loc = 16 * mw + n;
   float coef[4][4];
-  auto s_chunk = [&](int c) {
+  auto s_chunk = [&](int c, auto mw_c) {
+    constexpr int MW = decltype(mw_c)::value;
     const raw* Kb = stage_k(c);
     const raw* Qb = Kb + CT * KS;
     raw* Pb = Pbuf + (c & 1) * CT * PS;
-    Frag8<E> qf[NKK];
+    Frag8<E> qf[NKK], kf[MW + 1][NKK];
 #pragma unroll
-    for (int kk = 0; kk < NKK; ++kk) qf[kk] = *reinterpret_cast<const Frag8<E>*>(Qb + kq_at<DKP>(i_loc, 32 * kk + 8 * g));
+    for (int kk = 0; kk < NKK; ++kk) qf[kk] = *reinterpret_cast<const Frag8<E>*>(Qb + kq_at<DKP>(16 * MW + n, 32 * kk + 8 * g));
+#pragma unroll
+    for (int jb = 0; jb <= MW; ++jb)
+#pragma unroll
+      for (int kk = 0; kk < NKK; ++kk)
+        kf[jb][kk] = *reinterpret_cast<const Frag8<E>*>(Kb + kq_at<DKP>(16 * jb + n, 32 * kk + 8 * g));
+    f32x4 sacc[MW + 1];
+#pragma unroll
+    for (int jb = 0; jb <= MW; ++jb) sacc[jb] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int kk = 0; kk < NKK; ++kk)
+#pragma unroll
+      for (int jb = 0; jb <= MW; ++jb) sacc[jb] = mfma8(kf[jb][kk], qf[kk], sacc[jb]);
 #pragma unroll
     for (int jb = 0; jb < 4; ++jb) {
-      f32x4 sacc = f32x4{0.f, 0.f, 0.f, 0.f};
-      if (jb <= mw) {
-#pragma unroll
-        for (int kk = 0; kk < NKK; ++kk) {
-          const Frag8<E> kf = *reinterpret_cast<const Frag8<E>*>(Kb + kq_at<DKP>(16 * jb + n, 32 * kk + 8 * g));
-          sacc = mfma8(kf, qf[kk], sacc);
-        }
-      }
-      store4_raw<E>(Pb + i_loc * PS + 16 * jb + 4 * g,
-                    sacc * f32x4{coef[jb][0], coef[jb][1], coef[jb][2], coef[jb][3]});
+      const f32x4 val = jb <= MW ? sacc[jb <= MW ? jb : 0] * f32x4{coef[jb][0], coef[jb][1], coef[jb][2], coef[jb][3]}
+                                 : f32x4{0.f, 0.f, 0.f, 0.f};
+      store4_raw<E>(Pb + (16 * MW + n) * PS + 16 * jb + 4 * g, val);
     }
   };
 
@@ -429,7 +437,7 @@ __global__ __launch_bounds__(kVsThreads, 1) void scan_vsplit_kernel(const ChunkF
   // orders every LDS producer before its consumers, and each buffer's next
   // writer runs at least one step after its last reader.
   static_assert(PW_N <= kVsPThreads, "one power per P thread");
-  if (p_wave) {
+  auto p_loop = [&](auto mw_c) {
     const float pw_first = tid < PW_N ? a.pw[tid] : 0.f;
     Stage sg[PF];
 #pragma unroll
@@ -446,7 +454,7 @@ __global__ __launch_bounds__(kVsThreads, 1) void scan_vsplit_kernel(const ChunkF
         coef[jb][r] = (j <= i_loc) ? a.c * pw[max(i_loc - j, 0)] : 0.f;
       }
     }
-    s_chunk(0);
+    s_chunk(0, mw_c);
     // Step c: load chunk c + PF into the slot chunk c held, stage chunk c + 2,
     // flush chunk c - 1's output, S of chunk c + 1.
     for (int c = 0; c < n_chunks; c += PF) {
@@ -457,11 +465,22 @@ __global__ __launch_bounds__(kVsThreads, 1) void scan_vsplit_kernel(const ChunkF
         load_chunk(c + i + PF, sg[i]);
         store_chunk(c + i + 2, sg[(i + 2) % PF]);
         flush_out(c + i - 1);
-        if (c + i + 1 < n_chunks) s_chunk(c + i + 1);
+        if (c + i + 1 < n_chunks) s_chunk(c + i + 1, mw_c);
       }
     }
     __syncthreads();
     flush_out(n_chunks - 1);
+  };
+  if (p_wave) {
+    if (mw == 0) {
+      p_loop(std::integral_constant<int, 0>{});
+    } else if (mw == 1) {
+      p_loop(std::integral_constant<int, 1>{});
+    } else if (mw == 2) {
+      p_loop(std::integral_constant<int, 2>{});
+    } else {
+      p_loop(std::integral_constant<int, 3>{});
+    }
     return;
   }
 

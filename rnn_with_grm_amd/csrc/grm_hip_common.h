@@ -18,6 +18,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <type_traits>
+
 namespace grmhip {
 
 typedef float f32x4 __attribute__((ext_vector_type(4)));
@@ -57,6 +59,22 @@ template <> struct ET<BF16> {
     return __builtin_bit_cast(uint16_t, static_cast<__bf16>(f));
   }
 };
+
+// Two values in a 16-bit input dtype packed into 32 bits (first in the low
+// half): one conversion instruction for the pair, rounding as from_f.
+template <class E>
+__device__ __forceinline__ uint32_t pack2(float a, float b) {
+  static_assert(sizeof(typename ET<E>::raw) == 2, "16-bit types");
+  typedef float f32x2_t __attribute__((ext_vector_type(2)));
+  const f32x2_t v = {a, b};
+  if constexpr (std::is_same_v<E, BF16>) {
+    typedef __bf16 h2_t __attribute__((ext_vector_type(2)));
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, h2_t));
+  } else {
+    typedef _Float16 h2_t __attribute__((ext_vector_type(2)));
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, h2_t));
+  }
+}
 
 // Eight consecutive elements of one row (16 B for 16-bit types, 32 B for f32).
 template <class E> struct U8 {
@@ -146,8 +164,8 @@ template <class E>
 __device__ __forceinline__ void store4_raw(typename ET<E>::raw* p, f32x4 v) {
   if constexpr (sizeof(typename ET<E>::raw) == 2) {
     uint2 q;
-    q.x = static_cast<uint32_t>(ET<E>::from_f(v[0])) | (static_cast<uint32_t>(ET<E>::from_f(v[1])) << 16);
-    q.y = static_cast<uint32_t>(ET<E>::from_f(v[2])) | (static_cast<uint32_t>(ET<E>::from_f(v[3])) << 16);
+    q.x = pack2<E>(v[0], v[1]);
+    q.y = pack2<E>(v[2], v[3]);
     *reinterpret_cast<uint2*>(p) = q;
   } else {
     *reinterpret_cast<float4*>(p) = make_float4(v[0], v[1], v[2], v[3]);
@@ -201,8 +219,8 @@ __device__ __forceinline__ void buf_store4(__amdgpu_buffer_rsrc_t r, int off, f3
   if constexpr (sizeof(typename ET<E>::raw) == 2) {
     typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
     u32x2 q;
-    q[0] = static_cast<uint32_t>(ET<E>::from_f(v[0])) | (static_cast<uint32_t>(ET<E>::from_f(v[1])) << 16);
-    q[1] = static_cast<uint32_t>(ET<E>::from_f(v[2])) | (static_cast<uint32_t>(ET<E>::from_f(v[3])) << 16);
+    q[0] = pack2<E>(v[0], v[1]);
+    q[1] = pack2<E>(v[2], v[3]);
     __builtin_amdgcn_raw_buffer_store_b64(q, r, off, 0, 0);
   } else {
     typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
