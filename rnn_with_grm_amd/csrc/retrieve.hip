@@ -509,8 +509,10 @@ __global__ __launch_bounds__(AP_THREADS) void apply_reg_kernel(const RetrieveArg
 // MFMA input type EF (one part when EM is EF; hi + mid + lo bf16 parts, which
 // together hold all 24 mantissa bits, when EM is float32), and the query cast
 // to EM is exact in EF, so every product is exact and only the float32
-// accumulation rounds, as in a float32 dot product.  Lane group g owns keys
-// [g*KG, (g+1)*KG); MFMA step c (16x16x32) takes keys g*KG + 8c .. + 7 from group g.
+// accumulation rounds, as in a float32 dot product.  MFMA step c (16x16x32)
+// takes keys 32c + 8g .. + 7 from lane group g, so the four groups of a row
+// read consecutive bytes: each state load instruction covers whole 128-byte
+// lines of 16 rows (fp32 states) instead of 16-byte pieces of 64 lines.
 template <class EL, class EM, class EQ, int DKP, class EF, int NPART>
 __global__ __launch_bounds__(AP_THREADS) void apply_mfma16_kernel(const RetrieveArgs a) {
   using rawl = typename ET<EL>::raw;  // stored memories
@@ -537,7 +539,9 @@ __global__ __launch_bounds__(AP_THREADS) void apply_mfma16_kernel(const Retrieve
   const int p_begin = te.y, p_end = te.z;
   const int dk = a.dk, dv = a.dv;
   const int v0 = static_cast<int>(vt) * AP_V;
-  const int k0 = g * KG;
+  // Register slot x (0 .. KG - 1) of a lane's state row / query holds key key_of(x).
+  auto key_of = [&](int x) { return 32 * (x >> 3) + 8 * g + (x & 7); };
+  static_assert(EPU_M <= 8 && EPU_Q <= 8, "a 16-byte load stays inside one MFMA slot group");
   const int32_t* lb = a.list + b * a.n_index;
   // Pair ids of the first tile, one per lane (issued before the state loads so
   // that waiting for them does not wait for the state).
@@ -551,7 +555,7 @@ __global__ __launch_bounds__(AP_THREADS) void apply_mfma16_kernel(const Retrieve
     const int v = v0 + 32 * w + 16 * i + n;
 #pragma unroll
     for (int u = 0; u < KG / EPU_M; ++u) {
-      const int k = k0 + u * EPU_M;
+      const int k = key_of(u * EPU_M);
       load16_f32<EL>(rm, (v < dv && k < dk) ? (v * dk + k) * static_cast<int>(sizeof(rawl)) : kBufOOB,
                      &xm[i][u * EPU_M]);
     }
@@ -571,7 +575,7 @@ __global__ __launch_bounds__(AP_THREADS) void apply_mfma16_kernel(const Retrieve
       const int pid = __shfl(pid_l, 16 * j + n, 64);
 #pragma unroll
       for (int u = 0; u < KG / EPU_Q; ++u) {
-        const int k = k0 + u * EPU_Q;
+        const int k = key_of(u * EPU_Q);
         load16_f32<EQ>(rq, (pid >= 0 && k < dk) ? (static_cast<int>(pid / a.routes) * dk + k) *
                                                       static_cast<int>(sizeof(rawq))
                                                 : kBufOOB,
