@@ -569,17 +569,33 @@ __global__ __launch_bounds__(AP_THREADS) void apply_mfma16_kernel(const Retrieve
   bool split = false;
   for (int p0 = p_begin; p0 < p_end; p0 += AP_N) {
     const int np = min(AP_N, p_end - p0);
-    float xq[4][KG];
+    // The query's MFMA operand: q cast to EM, then to EF.  When both casts are
+    // exact (a 16-bit query of type EF, EM float32 or EF) the operand is the
+    // query's own bits, loaded as they are (half the registers of float32).
+    constexpr bool kRawQ = std::is_same_v<EQ, EF> && (std::is_same_v<EM, F32> || std::is_same_v<EM, EQ>);
+    float xq[kRawQ ? 1 : 4][kRawQ ? 1 : KG];
+    Frag8<EF> rq8[4][kRawQ ? NSTEP : 1];
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       const int pid = __shfl(pid_l, 16 * j + n, 64);
+      if constexpr (kRawQ) {
 #pragma unroll
-      for (int u = 0; u < KG / EPU_Q; ++u) {
-        const int k = key_of(u * EPU_Q);
-        load16_f32<EQ>(rq, (pid >= 0 && k < dk) ? (static_cast<int>(pid / a.routes) * dk + k) *
-                                                      static_cast<int>(sizeof(rawq))
-                                                : kBufOOB,
-                       &xq[j][u * EPU_Q]);
+        for (int c = 0; c < NSTEP; ++c) {
+          const int k = key_of(8 * c);
+          const int off = (pid >= 0 && k < dk) ? (static_cast<int>(pid / a.routes) * dk + k) *
+                                                     static_cast<int>(sizeof(rawq))
+                                               : kBufOOB;
+          rq8[j][c] = __builtin_bit_cast(Frag8<EF>, __builtin_amdgcn_raw_buffer_load_b128(rq, off, 0, 0));
+        }
+      } else {
+#pragma unroll
+        for (int u = 0; u < KG / EPU_Q; ++u) {
+          const int k = key_of(u * EPU_Q);
+          load16_f32<EQ>(rq, (pid >= 0 && k < dk) ? (static_cast<int>(pid / a.routes) * dk + k) *
+                                                        static_cast<int>(sizeof(rawq))
+                                                  : kBufOOB,
+                         &xq[j][u * EPU_Q]);
+        }
       }
     }
     if (!split) {
@@ -608,9 +624,14 @@ __global__ __launch_bounds__(AP_THREADS) void apply_mfma16_kernel(const Retrieve
     for (int j = 0; j < 4; ++j) {
       Frag8<EF> bq[NSTEP];
 #pragma unroll
-      for (int c = 0; c < NSTEP; ++c)
+      for (int c = 0; c < NSTEP; ++c) {
+        if constexpr (kRawQ) {
+          bq[c] = rq8[j][c];
+        } else {
 #pragma unroll
-        for (int e = 0; e < 8; ++e) bq[c].e[e] = ET<EF>::from_f(ET<EM>::to_f(ET<EM>::from_f(xq[j][8 * c + e])));
+          for (int e = 0; e < 8; ++e) bq[c].e[e] = ET<EF>::from_f(ET<EM>::to_f(ET<EM>::from_f(xq[j][8 * c + e])));
+        }
+      }
 #pragma unroll
       for (int c = 0; c < NSTEP; ++c)
 #pragma unroll
