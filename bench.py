@@ -114,6 +114,36 @@ def bench_c2(torch, dev, steps, warmup):
     return wall, per, (k, v, q, m, hidden, snaps)
 
 
+def bench_c2_bwd(torch, dev, steps, warmup):
+    """chunk_update_backward at config 2 through the C ABI: the forward recompute of the
+    chunk states, the chunk-parallel MFMA backward and the tile sums, timed with events
+    around `steps` back-to-back calls."""
+    from rnn_with_grm_amd import capi
+
+    k, v, q, m = [t.to(dev) for t in make_c2(dev, torch)]
+    BH, T, D = k.shape
+    g = torch.Generator().manual_seed(5)
+    dh = (torch.randn(BH, T, D, generator=g) * 0.01).to(torch.bfloat16).to(dev)
+    dmo = (torch.randn(BH, D, D, generator=g) * 0.01).to(dev)
+    stream = torch.cuda.current_stream(dev)
+
+    def step():
+        return capi.chunk_update_bwd(dh, dmo, k, v, q, m, 0.97)
+
+    for _ in range(warmup):
+        out = step()
+    torch.cuda.synchronize()
+    ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    ev0.record(stream)
+    for _ in range(steps):
+        out = step()
+    ev1.record(stream)
+    torch.cuda.synchronize()
+    if not all(bool(torch.isfinite(t.float()).all()) for t in out):
+        raise RuntimeError("config-2 backward produced non-finite gradients")
+    return {"ms": ev0.elapsed_time(ev1) / steps, "tokens": BH * T}
+
+
 def bench_c3(torch, dev, steps, warmup):
     """Routing over the archive summaries; the fused retrieval (gather_apply + fusion); the
     materialised gather."""
@@ -464,10 +494,11 @@ def main() -> int:
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--c2-only", action="store_true", help="only the headline kernel (quick sweeps)")
     ap.add_argument("--c4-only", action="store_true", help="the headline kernel and the config-4 model forward")
+    ap.add_argument("--bwd-only", action="store_true", help="the headline kernel and the config-2 backward")
     ap.add_argument("--probe", action="store_true",
                     help="counter runs: a 256 MiB device copy (calibration) then config-2 launches only")
     a = ap.parse_args()
-    if a.c2_only or a.probe or a.c4_only:
+    if a.c2_only or a.probe or a.c4_only or a.bwd_only:
         a.no_gather = a.no_cpu = True
     if a.gpus != 1:
         print(f"bench.py measures one GPU only; --gpus {a.gpus} is not supported in this build "
@@ -512,6 +543,14 @@ def main() -> int:
             traffic = None
 
     secondary = {}
+    if not a.no_gather or a.bwd_only:
+        log("config 2 backward (chunk_update_backward: recompute + MFMA backward + tile sums)")
+        bw = bench_c2_bwd(torch, dev, max(3, a.steps // 2), 2)
+        secondary["c2_backward"] = {
+            "what": "chunk_update_backward at config 2 (bf16 q/k/v, fp32 state): forward recompute of the 32 "
+                    "chunk states, chunk-parallel MFMA backward, tile sums; events around back-to-back calls",
+            "ms": round(bw["ms"], 4), "tokens/s": round(bw["tokens"] / bw["ms"] * 1e3)}
+        log(f"c2 backward: {bw['ms']:.3f} ms per call")
     if not a.no_gather:
         log("config 3 routing + materialised gather (64 GiB output)")
         c3 = bench_c3(torch, dev, a.steps, a.warmup)
