@@ -82,6 +82,28 @@ int64_t grm_hip_chunk_update_fwd_workspace(int64_t batch, int64_t seq_len, int64
                                            int64_t value_dim, int64_t snapshot_len);
 
 /*
+ * grm_hip_chunk_update_fwd without any device allocation, for callers that
+ * cannot allocate (code under HIP graph capture, tight serving loops, harnesses
+ * that forbid hipMalloc).  No counterpart in the reference.
+ * Same arguments and results as grm_hip_chunk_update_fwd minus the workspace:
+ * the time-split scratch is a fixed device array inside the library of
+ * GRM_HIP_NOALLOC_SCRATCH_BYTES per GPU, held from the first call on a GPU
+ * until the process ends.  Calls whose sizes need more time-split scratch than
+ * that (grm_hip_chunk_update_fwd_workspace() above the limit) are rejected with
+ * GRM_HIP_EINVAL and a message.  Every call on one GPU shares that GPU's
+ * scratch: calls that overlap on one GPU (different streams, or host threads
+ * without ordering) race and must not be issued.  The scratch needs no clearing
+ * between calls.
+ */
+#define GRM_HIP_NOALLOC_SCRATCH_BYTES (32ll << 20)
+int64_t grm_hip_chunk_update_fwd_noalloc_limit(void);
+int grm_hip_chunk_update_fwd_noalloc(const void* keys, const void* values, const void* queries,
+                                     const void* memory, void* hidden, void* memory_out, float* snapshots,
+                                     int64_t batch, int64_t seq_len, int64_t key_dim, int64_t value_dim,
+                                     int in_dtype, int mem_dtype, double memory_decay, int64_t snapshot_len,
+                                     void* stream);
+
+/*
  * Gradient of grm_hip_chunk_update_fwd.
  * Replaces grm_cuda::chunk_update_backward
  *   (reference grm/csrc/bindings.cpp:7, chunk_update.cu:588-716, grm_cuda.cpp:92-126).

@@ -31,6 +31,9 @@ SIGNATURES = {
     "grm_hip_chunk_update_fwd": (_C, [_P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _C, _C, ctypes.c_double,
                                       _I, _P]),
     "grm_hip_chunk_update_fwd_workspace": (_I, [_I, _I, _I, _I, _I]),
+    "grm_hip_chunk_update_fwd_noalloc_limit": (_I, []),
+    "grm_hip_chunk_update_fwd_noalloc": (_C, [_P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _C, _C, ctypes.c_double,
+                                              _I, _P]),
     "grm_hip_chunk_update_bwd": (_C, [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _C, _C,
                                       ctypes.c_double, _P]),
     "grm_hip_apply_query_fwd": (_C, [_P, _P, _P, _I, _I, _I, _I, _I, _C, _P]),
@@ -117,6 +120,32 @@ def chunk_update_fwd(keys, values, queries, memory, decay: float, snapshot_len: 
                                          int(snapshot_len), _stream(keys))
     _check(rc, "grm_hip_chunk_update_fwd")
     return hidden, memory_out, snaps
+
+
+def chunk_update_fwd_noalloc(keys, values, queries, memory, decay: float, snapshot_len: int = 0, hidden=None,
+                             memory_out=None, snapshots=None):
+    """grm_hip_chunk_update_fwd_noalloc into caller-given outputs (allocated here when not
+    given, before the call): the library itself allocates nothing.  Returns (hidden,
+    memory_out, snapshots)."""
+    B, T, K = keys.shape
+    H = values.shape[2]
+    if hidden is None:
+        hidden = torch.empty((B, T, H), dtype=values.dtype, device=values.device)
+    if memory_out is None:
+        memory_out = torch.empty_like(memory)
+    if snapshots is None and snapshot_len > 0:
+        snapshots = torch.empty((B, (T + snapshot_len - 1) // snapshot_len, H, K), dtype=torch.float32,
+                                device=keys.device)
+    rc = load().grm_hip_chunk_update_fwd_noalloc(_ptr(keys), _ptr(values), _ptr(queries), _ptr(memory),
+                                                 _ptr(hidden), _ptr(memory_out), _ptr(snapshots), B, T, K, H,
+                                                 dtype_code(keys.dtype), dtype_code(memory.dtype), float(decay),
+                                                 int(snapshot_len), _stream(keys))
+    _check(rc, "grm_hip_chunk_update_fwd_noalloc")
+    return hidden, memory_out, snapshots
+
+
+def noalloc_limit() -> int:
+    return int(load().grm_hip_chunk_update_fwd_noalloc_limit())
 
 
 def chunk_update_bwd(grad_hidden, grad_memory_out, keys, values, queries, memory, decay: float):

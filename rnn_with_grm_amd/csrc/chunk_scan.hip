@@ -26,6 +26,7 @@
 #include <string.h>
 
 #include <cmath>
+#include <mutex>
 
 #include "chunk_scan.h"
 #include "grm_hip.h"
@@ -797,4 +798,75 @@ extern "C" int grm_hip_chunk_update_fwd(const void* keys, const void* values, co
     case GRM_HIP_F16: return dispatch_dv<F16>(a, dv_tile, vec, s);
     default: return dispatch_dv<BF16>(a, dv_tile, vec, s);
   }
+}
+
+// ---------------------------------------------------------------------------
+// The same forward with no allocation at all: the time-split workspace is a
+// file-scope device array, one per GPU, instead of caller memory.
+namespace {
+
+constexpr int64_t kNoAllocScratchBytes = GRM_HIP_NOALLOC_SCRATCH_BYTES;
+constexpr int kMaxDevices = 64;
+
+// Device-side scratch of the no-alloc forward.  In host code this name is not
+// a device address: host code uses the per-device pointer from
+// hipGetSymbolAddress below, never the name itself.
+static __device__ __align__(256) unsigned char scratch[kNoAllocScratchBytes];
+
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxDevices] = {};
+
+// The current device's copy of `scratch`, looked up once per device (with that
+// device current) and kept.
+int scratch_for_current_device(void** out) {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) {
+    set_error("chunk_update_fwd_noalloc: hipGetDevice failed: %s", hipGetErrorString(e));
+    return static_cast<int>(e);
+  }
+  if (dev < 0 || dev >= kMaxDevices) {
+    set_error("chunk_update_fwd_noalloc: device %d beyond the %d this library tracks", dev, kMaxDevices);
+    return GRM_HIP_EUNSUPPORTED;
+  }
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (g_scratch_ptr[dev] == nullptr) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || p == nullptr) {
+      set_error("chunk_update_fwd_noalloc: hipGetSymbolAddress(scratch) failed on device %d: %s", dev,
+                hipGetErrorString(e));
+      return e != hipSuccess ? static_cast<int>(e) : GRM_HIP_EINVAL;
+    }
+    g_scratch_ptr[dev] = p;
+  }
+  *out = g_scratch_ptr[dev];
+  return GRM_HIP_OK;
+}
+
+}  // namespace
+
+extern "C" int64_t grm_hip_chunk_update_fwd_noalloc_limit(void) { return kNoAllocScratchBytes; }
+
+extern "C" int grm_hip_chunk_update_fwd_noalloc(const void* keys, const void* values, const void* queries,
+                                                const void* memory, void* hidden, void* memory_out,
+                                                float* snapshots, int64_t batch, int64_t seq_len,
+                                                int64_t key_dim, int64_t value_dim, int in_dtype, int mem_dtype,
+                                                double memory_decay, int64_t snapshot_len, void* stream) {
+  const int64_t need = grm_hip_chunk_update_fwd_workspace(batch, seq_len, key_dim, value_dim,
+                                                          snapshots != nullptr ? snapshot_len : 0);
+  if (need > kNoAllocScratchBytes) {
+    set_error("chunk_update_fwd_noalloc: these sizes need %lld bytes of time-split scratch, beyond the "
+              "library's fixed %lld (use grm_hip_chunk_update_fwd with a caller workspace)",
+              (long long)need, (long long)kNoAllocScratchBytes);
+    return GRM_HIP_EINVAL;
+  }
+  void* ws = nullptr;
+  if (need > 0) {
+    int rc = scratch_for_current_device(&ws);
+    if (rc != GRM_HIP_OK) return rc;
+  }
+  return grm_hip_chunk_update_fwd(keys, values, queries, memory, hidden, memory_out, snapshots, ws,
+                                  need > 0 ? kNoAllocScratchBytes : 0, batch, seq_len, key_dim, value_dim,
+                                  in_dtype, mem_dtype, memory_decay, snapshot_len, stream);
 }
