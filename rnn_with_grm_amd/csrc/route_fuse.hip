@@ -26,6 +26,7 @@
 
 #include "grm_hip.h"
 #include "grm_hip_common.h"
+#include "route_select.h"
 
 namespace grmhip {
 namespace {
@@ -1086,6 +1087,26 @@ __global__ __launch_bounds__(256) void fuse_vec_kernel(const FuseArgs a, const i
 
 bool aligned(const void* p, size_t n) { return (reinterpret_cast<uintptr_t>(p) % n) == 0; }
 
+RouteSelArgs select_args(const RouteArgs& a) {
+  RouteSelArgs r;
+  memset(&r, 0, sizeof(r));
+  r.q = a.q;
+  r.keys = a.keys;
+  r.idx = a.idx;
+  r.scores = a.scores;
+  r.gates = a.gates;
+  r.n_query = a.n_query;
+  r.n_keys = a.n_keys;
+  r.dim = a.dim;
+  r.k = a.k;
+  r.scale = a.scale;
+  r.inv_temp = a.inv_temp;
+  r.seg_len = a.seg_len;
+  r.base = a.base;
+  r.cap = a.cap;
+  return r;
+}
+
 }  // namespace
 }  // namespace grmhip
 
@@ -1140,6 +1161,10 @@ extern "C" int grm_hip_topk_route(const void* queries, const void* keys, int64_t
   a.scale = scale;
   a.inv_temp = 1.0f / temperature;
   hipStream_t s = static_cast<hipStream_t>(stream);
+  if (!natural) {
+    int rc = GRM_HIP_OK;
+    if (try_route_select(select_args(a), dtype, batch, s, &rc)) return rc;
+  }
   int ib = 0;
   if (mfma_route_ok(a, dtype, queries, keys, &ib)) return launch_route_mfma(a, batch, ib, s);
   switch (dtype) {
@@ -1208,6 +1233,10 @@ extern "C" int grm_hip_segment_route(const void* queries, const void* keys, int6
   // WR_ROWS) h1 == h0; otherwise h1 - h0 <= (WR_ROWS - 1) / segment_len + 1.
   const int64_t crossings = segment_len % WR_ROWS == 0 ? 0 : (WR_ROWS - 1) / segment_len + 1;
   const int64_t span = std::min(n_keys, capacity) + crossings;
+  {
+    int rc = GRM_HIP_OK;
+    if (try_route_select(select_args(a), dtype, batch, s, &rc)) return rc;
+  }
   int ib = 0;
   if (mfma_route_ok(a, dtype, queries, keys, &ib)) return launch_route_mfma(a, batch, ib, s);
   const bool window_ok = span <= WR_MAXK && a.vec && aligned(keys, 16) && top_k <= 32;

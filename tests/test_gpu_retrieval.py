@@ -406,6 +406,45 @@ def test_topk_route_near_ties(dev, S, D, k, hot, copies):
     np.testing.assert_allclose(gates.cpu().numpy(), og, rtol=1e-5, atol=1e-6)
 
 
+@pytest.mark.parametrize("S,D,k,copies", [(256, 128, 8, 256), (512, 128, 16, 60), (300, 64, 8, 40), (90, 32, 32, 90)])
+def test_topk_route_candidate_overflow(dev, S, D, k, copies):
+    """Rows with more near-best keys than the candidate lists hold (every key equal, or
+    many copies of the best key): those rows are scored exactly over all keys; ties go
+    to the lower index."""
+    g = torch.Generator().manual_seed(S + copies)
+    keys = norm(torch.randn(2, S, D, generator=g))
+    best = norm(torch.randn(D, generator=g))
+    pos = torch.randperm(S, generator=g)[:copies]
+    keys[:, pos] = best
+    q = norm(torch.randn(2, 600, D, generator=g))
+    q[:, ::3] = best  # these rows score every copy of the best key highest, all tied
+    q, keys = q.to(torch.bfloat16), keys.to(torch.bfloat16)
+    scale = 1.0 / D ** 0.5
+    gates, idx, sc = capi.topk_route(q.to(dev), keys.to(dev), k, scale)
+    og, oi, osc = orc.topk_route(q.float().numpy(), keys.float().numpy(), k, scale)
+    assert np.array_equal(idx.cpu().numpy(), oi)
+    assert np.array_equal(sc.cpu().numpy(), osc)
+    np.testing.assert_allclose(gates.cpu().numpy(), og, rtol=1e-5, atol=1e-6)
+
+
+@pytest.mark.parametrize("B,Q,S,D,k", [(1, 70000, 100, 64, 8), (3, 1500, 33, 128, 16), (2, 2000, 257, 96, 4),
+                                       (1, 1200, 2000, 32, 8)])
+def test_topk_route_block_shapes(dev, B, Q, S, D, k):
+    """Row counts that leave partial 512-row blocks and partial 64-row waves, key counts
+    that are not multiples of 32, several blocks per workgroup (70000 rows of one batch
+    entry), and an archive of 2000 keys."""
+    g = torch.Generator().manual_seed(Q + S)
+    q = norm(torch.randn(B, Q, D, generator=g)).to(torch.bfloat16)
+    keys = norm(torch.randn(B, S, D, generator=g)).to(torch.bfloat16)
+    scale = 1.0 / D ** 0.5
+    gates, idx, sc = capi.topk_route(q.to(dev), keys.to(dev), k, scale)
+    rows = torch.cat([torch.arange(0, 300), torch.arange(Q - 300, Q)]) if Q > 600 else torch.arange(Q)
+    og, oi, osc = orc.topk_route(q[:, rows].float().numpy(), keys.float().numpy(), k, scale)
+    assert np.array_equal(idx[:, rows].cpu().numpy(), oi)
+    assert np.array_equal(sc[:, rows].cpu().numpy(), osc)
+    np.testing.assert_allclose(gates[:, rows].cpu().numpy(), og, rtol=1e-5, atol=1e-6)
+
+
 def test_topk_route_unit_scale_and_large_norms(dev):
     """Unnormalised bf16 inputs (norms up to ~1e3) and scale 1: the error bound of the
     narrowing scales with the norms, the indices stay exact."""
