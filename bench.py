@@ -513,7 +513,7 @@ def main() -> int:
         print("no GPU visible", file=sys.stderr)
         return 1
     if not cuda_ops.load_grm_cuda_extension():
-        raise RuntimeError(f"GRM HIP extension not loaded: {cuda_ops._EXTENSION_LOAD_ERROR}")
+        raise RuntimeError(f"GRM HIP extension not loaded: {cuda_ops.extension_load_error()}")
     dev = torch.device("cuda:0")
 
     if a.probe:

@@ -110,8 +110,11 @@ int grm_hip_chunk_update_fwd_noalloc(const void* keys, const void* values, const
  * grad_hidden [batch, seq_len, value_dim] and grad_memory_out [batch, value_dim, key_dim]
  * come in the input dtype and mem_dtype; the four gradients are written in the
  * dtype of the tensor they belong to.
- * chunk_states: float32 workspace [batch, ceil(seq_len / 64), value_dim, key_dim]
- *   (caller-provided; overwritten with the state after each 64-token chunk).
+ * chunk_states: float32 [batch, ceil(seq_len / 64), value_dim, key_dim], the state after
+ *   each 64-token chunk.  states_given != 0: the caller filled it (the forward's
+ *   64-token snapshots, grm_hip_chunk_update_fwd with snapshot_len 64, passed from the
+ *   forward as the op's aux); otherwise it is a workspace that the backward fills by
+ *   running the forward again.
  * dkq_partial: float32 workspace [2, batch, ceil(value_dim / 16), seq_len, key_dim]
  *   (caller-provided; per value-tile partial sums of grad_keys and grad_queries: 16-column
  *   tiles in the scalar kernel, 32-column tiles [2, batch, value_dim / 32, seq_len, key_dim]
@@ -120,7 +123,7 @@ int grm_hip_chunk_update_fwd_noalloc(const void* keys, const void* values, const
 int grm_hip_chunk_update_bwd(const void* grad_hidden, const void* grad_memory_out, const void* keys,
                              const void* values, const void* queries, const void* memory,
                              void* grad_keys, void* grad_values, void* grad_queries,
-                             void* grad_memory, float* chunk_states, float* dkq_partial,
+                             void* grad_memory, float* chunk_states, int states_given, float* dkq_partial,
                              int64_t batch, int64_t seq_len, int64_t key_dim, int64_t value_dim,
                              int in_dtype, int mem_dtype, double memory_decay, void* stream);
 
@@ -142,6 +145,8 @@ int grm_hip_apply_query_fwd(const void* memories, const void* queries, void* hid
  *   grad_queries[b, q, k]        = sum_{r, h} grad_hidden[b, q, r, h] * memories[b, q, r, h, k]
  * Replaces grm_cuda::apply_query_backward
  *   (reference grm/csrc/bindings.cpp:9, apply_query.cu:256-330, grm_cuda.cpp:136-154).
+ * grad_memories may be NULL: only grad_queries is computed (a retrieved archive
+ * needs no gradient; the reference always writes both).
  */
 int grm_hip_apply_query_bwd(const void* grad_hidden, const void* memories, const void* queries,
                             void* grad_memories, void* grad_queries, int64_t batch,

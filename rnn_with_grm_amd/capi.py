@@ -34,7 +34,7 @@ SIGNATURES = {
     "grm_hip_chunk_update_fwd_noalloc_limit": (_I, []),
     "grm_hip_chunk_update_fwd_noalloc": (_C, [_P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _C, _C, ctypes.c_double,
                                               _I, _P]),
-    "grm_hip_chunk_update_bwd": (_C, [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _C, _C,
+    "grm_hip_chunk_update_bwd": (_C, [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _C, _P, _I, _I, _I, _I, _C, _C,
                                       ctypes.c_double, _P]),
     "grm_hip_apply_query_fwd": (_C, [_P, _P, _P, _I, _I, _I, _I, _I, _C, _P]),
     "grm_hip_apply_query_bwd": (_C, [_P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _C, _P]),
@@ -148,16 +148,21 @@ def noalloc_limit() -> int:
     return int(load().grm_hip_chunk_update_fwd_noalloc_limit())
 
 
-def chunk_update_bwd(grad_hidden, grad_memory_out, keys, values, queries, memory, decay: float):
+def chunk_update_bwd(grad_hidden, grad_memory_out, keys, values, queries, memory, decay: float,
+                     chunk_states=None):
+    """chunk_states: the forward's float32 64-token snapshots [B, ceil(T/64), H, K], or None
+    (the backward scans again to produce them)."""
     B, T, K = keys.shape
     H = values.shape[2]
     gk, gv, gq, gm = (torch.empty_like(keys), torch.empty_like(values), torch.empty_like(queries),
                       torch.empty_like(memory))
-    states = torch.empty((B, max(1, (T + 63) // 64), H, K), dtype=torch.float32, device=keys.device)
+    given = chunk_states is not None
+    states = chunk_states if given else torch.empty((B, max(1, (T + 63) // 64), H, K), dtype=torch.float32,
+                                                     device=keys.device)
     partial = torch.empty((2, B, (H + 15) // 16, max(T, 1), K), dtype=torch.float32, device=keys.device)
     rc = load().grm_hip_chunk_update_bwd(_ptr(grad_hidden), _ptr(grad_memory_out), _ptr(keys), _ptr(values),
                                          _ptr(queries), _ptr(memory), _ptr(gk), _ptr(gv), _ptr(gq), _ptr(gm),
-                                         _ptr(states), _ptr(partial), B, T, K, H, dtype_code(keys.dtype),
+                                         _ptr(states), int(given), _ptr(partial), B, T, K, H, dtype_code(keys.dtype),
                                          dtype_code(memory.dtype), float(decay), _stream(keys))
     _check(rc, "grm_hip_chunk_update_bwd")
     return gk, gv, gq, gm

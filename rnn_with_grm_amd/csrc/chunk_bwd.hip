@@ -737,7 +737,7 @@ extern "C" int grm_hip_chunk_update_bwd(const void* grad_hidden, const void* gra
                                         const void* keys, const void* values, const void* queries,
                                         const void* memory, void* grad_keys, void* grad_values,
                                         void* grad_queries, void* grad_memory, float* chunk_states,
-                                        float* dkq_partial, int64_t batch, int64_t seq_len,
+                                        int states_given, float* dkq_partial, int64_t batch, int64_t seq_len,
                                         int64_t key_dim, int64_t value_dim, int in_dtype,
                                         int mem_dtype, double memory_decay, void* stream) {
   if (batch < 0 || seq_len < 0 || key_dim < 1 || value_dim < 1) {
@@ -786,12 +786,14 @@ extern "C" int grm_hip_chunk_update_bwd(const void* grad_hidden, const void* gra
     set_error("chunk_update_bwd: problem too large for one launch");
     return GRM_HIP_EINVAL;
   }
-  // Re-run the forward to store the state after every 64-token chunk; its
-  // hidden output and final state are not needed.
-  int rc = grm_hip_chunk_update_fwd(keys, values, queries, memory, nullptr, nullptr, chunk_states,
-                                    nullptr, 0, batch, seq_len, key_dim, value_dim, in_dtype,
-                                    mem_dtype, memory_decay, BCT, stream);
-  if (rc != GRM_HIP_OK) return rc;
+  // Without the forward's chunk states, run the forward again to store the
+  // state after every 64-token chunk; its hidden output and final state are not needed.
+  if (!states_given) {
+    const int rc = grm_hip_chunk_update_fwd(keys, values, queries, memory, nullptr, nullptr, chunk_states,
+                                            nullptr, 0, batch, seq_len, key_dim, value_dim, in_dtype,
+                                            mem_dtype, memory_decay, BCT, stream);
+    if (rc != GRM_HIP_OK) return rc;
+  }
 
   const char* env = getenv("GRM_HIP_BWD_MFMA");
   const bool mfma = (env == nullptr || env[0] != '0') && (in_dtype == GRM_HIP_BF16 || in_dtype == GRM_HIP_F16) &&

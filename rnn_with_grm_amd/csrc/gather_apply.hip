@@ -394,14 +394,15 @@ int launch_apply_fwd(ApplyArgs a, hipStream_t s) {
 
 template <class E>
 int launch_apply_bwd(ApplyArgs a, hipStream_t s) {
-  const int64_t groups_per_wg = GT / a.group;
-  int64_t want = (a.rows + groups_per_wg - 1) / groups_per_wg;
-  int64_t grid = want < 256 * 64 ? want : 256 * 64;
-  hipLaunchKernelGGL(apply_bwd_dmem_kernel<E>, dim3(static_cast<unsigned>(grid < 1 ? 1 : grid)),
-                     dim3(GT), 0, s, a);
-  int rc = check_launch("apply_query_bwd(grad_memories)");
-  if (rc != GRM_HIP_OK) return rc;
-  grid = a.nq < 256 * 64 ? a.nq : 256 * 64;
+  if (a.dmem != nullptr) {  // NULL: the caller needs grad_queries only
+    const int64_t groups_per_wg = GT / a.group;
+    const int64_t want = (a.rows + groups_per_wg - 1) / groups_per_wg;
+    const int64_t g = want < 256 * 64 ? want : 256 * 64;
+    hipLaunchKernelGGL(apply_bwd_dmem_kernel<E>, dim3(static_cast<unsigned>(g < 1 ? 1 : g)), dim3(GT), 0, s, a);
+    const int rc = check_launch("apply_query_bwd(grad_memories)");
+    if (rc != GRM_HIP_OK) return rc;
+  }
+  const int64_t grid = a.nq < 256 * 64 ? a.nq : 256 * 64;
   hipLaunchKernelGGL(apply_bwd_dq_kernel<E>, dim3(static_cast<unsigned>(grid < 1 ? 1 : grid)),
                      dim3(GT), 0, s, a);
   return check_launch("apply_query_bwd(grad_queries)");
@@ -534,8 +535,7 @@ extern "C" int grm_hip_apply_query_bwd(const void* grad_hidden, const void* memo
   hipStream_t s = static_cast<hipStream_t>(stream);
   if (nq == 0 || key_dim == 0) return GRM_HIP_OK;
   if (queries == nullptr || grad_queries == nullptr || (rows > 0 && (grad_hidden == nullptr ||
-                                                                     memories == nullptr ||
-                                                                     grad_memories == nullptr))) {
+                                                                     memories == nullptr))) {
     set_error("apply_query_bwd: null pointer");
     return GRM_HIP_EINVAL;
   }

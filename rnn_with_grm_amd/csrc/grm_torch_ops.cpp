@@ -432,7 +432,6 @@ std::tuple<Tensor, Tensor, Tensor, Tensor> chunk_update_backward_hip(
     const Tensor& grad_hidden, const Tensor& grad_memory_out, const Tensor& keys,
     const Tensor& values, const Tensor& queries, const Tensor& memory, const Tensor& aux,
     double decay) {
-  (void)aux;
   check_chunk_inputs(keys, values, queries, memory);
   if (!chunk_supported(keys, values, queries, memory) ||
       !same_cuda_device({&keys, &grad_hidden, &grad_memory_out})) {
@@ -450,11 +449,17 @@ std::tuple<Tensor, Tensor, Tensor, Tensor> chunk_update_backward_hip(
   Tensor gk = at::empty_like(k), gv = at::empty_like(v), gq = at::empty_like(q);
   Tensor gm = at::empty_like(m);
   auto f32 = k.options().dtype(at::kFloat);
-  Tensor states = at::empty({B, (T + 63) / 64, H, K}, f32);
+  // aux from this library's forward under autograd holds the state after every
+  // 64-token chunk (float32 [B, ceil(T/64), H, K]); anything else (the reference's
+  // empty aux) means the backward scans again to produce them.
+  const std::vector<int64_t> state_shape = {B, (T + 63) / 64, H, K};
+  const bool given = aux.defined() && aux.is_cuda() && aux.device() == k.device() &&
+                     aux.scalar_type() == at::kFloat && aux.sizes().vec() == state_shape && aux.is_contiguous();
+  Tensor states = given ? aux : at::empty(state_shape, f32);
   Tensor partial = at::empty({2, B, (H + 15) / 16, T, K}, f32);
   check_rc(grm_hip_chunk_update_bwd(gh.data_ptr(), gmo.data_ptr(), k.data_ptr(), v.data_ptr(),
                                     q.data_ptr(), m.data_ptr(), gk.data_ptr(), gv.data_ptr(),
-                                    gq.data_ptr(), gm.data_ptr(), states.data_ptr<float>(),
+                                    gq.data_ptr(), gm.data_ptr(), states.data_ptr<float>(), given ? 1 : 0,
                                     partial.data_ptr<float>(), B, T, K, H,
                                     dtype_code(k.scalar_type()), dtype_code(m.scalar_type()), decay,
                                     current_stream(k)),
@@ -480,6 +485,37 @@ Tensor apply_query_forward_hip(const Tensor& memories, const Tensor& queries) {
                                    current_stream(mm)),
            "apply_query_forward");
   return out;
+}
+
+// grad_queries of apply_query_forward alone (the memories need no gradient).
+Tensor apply_query_backward_queries_generic(const Tensor& grad_hidden, const Tensor& memories,
+                                            const Tensor& queries) {
+  check_apply_inputs(memories, queries);
+  Tensor dh = grad_hidden.to(memories.scalar_type());
+  if (memories.dim() == 5) return at::einsum("bqrh,bqrhk->bqk", {dh, memories}).contiguous();
+  return at::einsum("brh,brhk->bk", {dh, memories}).contiguous();
+}
+
+Tensor apply_query_backward_queries_hip(const Tensor& grad_hidden, const Tensor& memories,
+                                        const Tensor& queries) {
+  check_apply_inputs(memories, queries);
+  const int dt = dtype_code(memories.scalar_type());
+  if (!same_cuda_device({&memories, &queries, &grad_hidden}) || dt < 0 ||
+      queries.scalar_type() != memories.scalar_type()) {
+    g_generic_calls.fetch_add(1);
+    return apply_query_backward_queries_generic(grad_hidden, memories, queries);
+  }
+  c10::OptionalDeviceGuard guard(memories.device());
+  Tensor mm = memories.contiguous(), q = queries.contiguous();
+  Tensor dh = grad_hidden.to(mm.scalar_type()).contiguous();
+  const bool r5 = mm.dim() == 5;
+  const int64_t B = mm.size(0), Q = r5 ? mm.size(1) : 1;
+  const int64_t R = mm.size(r5 ? 2 : 1), H = mm.size(r5 ? 3 : 2), K = mm.size(r5 ? 4 : 3);
+  Tensor gq = at::empty_like(q);
+  check_rc(grm_hip_apply_query_bwd(dh.data_ptr(), mm.data_ptr(), q.data_ptr(), nullptr, gq.data_ptr(), B, Q,
+                                   R, H, K, dt, current_stream(mm)),
+           "apply_query_backward_queries");
+  return gq;
 }
 
 std::tuple<Tensor, Tensor> apply_query_backward_hip(const Tensor& grad_hidden,
@@ -741,6 +777,7 @@ TORCH_LIBRARY(grm_cuda, m) {
   m.def("chunk_update_backward(Tensor grad_hidden, Tensor grad_memory_out, Tensor keys, Tensor values, Tensor queries, Tensor memory, Tensor aux, float memory_decay) -> (Tensor grad_keys, Tensor grad_values, Tensor grad_queries, Tensor grad_memory)");
   m.def("apply_query_forward(Tensor memories, Tensor queries) -> Tensor");
   m.def("apply_query_backward(Tensor grad_hidden, Tensor memories, Tensor queries) -> (Tensor grad_memories, Tensor grad_queries)");
+  m.def("apply_query_backward_queries(Tensor grad_hidden, Tensor memories, Tensor queries) -> Tensor");
   m.def("batched_memory_gather(Tensor memories_per_batch, Tensor topk_indices) -> Tensor");
   m.def("segment_scan_forward(Tensor keys, Tensor values, Tensor queries, Tensor memory, float memory_decay, int segment_len) -> (Tensor hidden, Tensor memory_out, Tensor snapshots)");
   m.def("topk_route(Tensor queries, Tensor keys, int top_k, float scale, float temperature) -> (Tensor gates, Tensor indices, Tensor scores)");
@@ -754,6 +791,7 @@ TORCH_LIBRARY_IMPL(grm_cuda, CPU, m) {
   m.impl("chunk_update_backward", grm::chunk_update_backward_cpu);
   m.impl("apply_query_forward", grm::apply_query_forward_generic);
   m.impl("apply_query_backward", grm::apply_query_backward_generic);
+  m.impl("apply_query_backward_queries", grm::apply_query_backward_queries_generic);
   m.impl("batched_memory_gather", grm::batched_memory_gather_generic);
   m.impl("segment_scan_forward", grm::segment_scan_forward_generic);
   m.impl("topk_route", grm::topk_route_cpu);
@@ -767,6 +805,7 @@ TORCH_LIBRARY_IMPL(grm_cuda, CUDA, m) {
   m.impl("chunk_update_backward", grm::chunk_update_backward_hip);
   m.impl("apply_query_forward", grm::apply_query_forward_hip);
   m.impl("apply_query_backward", grm::apply_query_backward_hip);
+  m.impl("apply_query_backward_queries", grm::apply_query_backward_queries_hip);
   m.impl("batched_memory_gather", grm::batched_memory_gather_hip);
   m.impl("segment_scan_forward", grm::segment_scan_forward_hip);
   m.impl("topk_route", grm::topk_route_hip);

@@ -1,20 +1,22 @@
 """GRM hot-path op wrappers over the MI355X extension (torch.ops.grm_cuda).
 
-Same public surface as the reference's ``grm.core.cuda_ops``
-(reference grm/core/cuda_ops.py:405-413): lazy extension loading,
-per-op ``auto/native/fallback`` policies read from the same environment
-variables with the same precedence, the same runtime-status dictionary, the
-same autograd wrappers and the same pure-PyTorch fallbacks (selected by
-``debug_fallback=True`` or a ``fallback`` policy).
+Public surface of the reference's ``grm.core.cuda_ops`` (reference
+grm/core/cuda_ops.py:405-413): the lazily loaded op library, per-op
+``auto/native/fallback`` policies read from the same environment variables
+with the same precedence, the runtime-status dictionary with the same keys,
+autograd wrappers, and PyTorch fallbacks (``debug_fallback=True`` or a
+``fallback`` policy) with the same error messages.
 
-Differences, all deliberate:
+Deliberate differences:
   * On a GPU tensor the native path is mandatory: if the extension cannot be
-    loaded the call raises instead of silently running PyTorch code.
+    loaded the call raises instead of running PyTorch code.
   * ``auto`` runs the native apply-query kernel for rank-5 inputs too (the
     reference's auto policy sends rank 5 to einsum, cuda_ops.py:154-155).
-  * New whole-sequence / routing / retrieval / fusion entry points:
-    ``cuda_segment_scan``, ``cuda_topk_route``, ``cuda_gather_apply`` and
-    ``cuda_fuse_residual``.
+  * Under autograd, the forward scan also returns the state after every
+    64-token chunk as ``aux``; the backward reads it instead of re-running the
+    scan (the schema allows it, bindings.cpp:6-7; the reference's aux is empty).
+  * New entry points: ``cuda_segment_scan``, ``cuda_topk_route``,
+    ``cuda_segment_route``, ``cuda_gather_apply`` and ``cuda_fuse_residual``.
 """
 
 from __future__ import annotations
@@ -27,312 +29,334 @@ from typing import Any, Dict, Optional, Tuple
 import torch
 from torch import Tensor
 
-_IMPORT_CANDIDATES = ("rnn_with_grm_amd.grm_cuda_ext", "grm_cuda_ext", "grm.grm_cuda_ext")
-_REGISTERED_OPS = (
+# The reference's five op schemas (bindings.cpp:6-10) and this library's additions.
+SCHEMA_OPS = (
     "chunk_update_forward",
     "chunk_update_backward",
     "apply_query_forward",
     "apply_query_backward",
     "batched_memory_gather",
 )
-_EXTRA_OPS = ("segment_scan_forward", "topk_route", "fuse_residual", "gather_apply", "segment_route")
+EXTRA_OPS = ("segment_scan_forward", "topk_route", "fuse_residual", "gather_apply", "segment_route",
+             "apply_query_backward_queries")
 
-_EXTENSION_MODULE: Optional[Any] = None
-_EXTENSION_LOAD_ATTEMPTED = False
-_EXTENSION_LOAD_ERROR = ""
-_KERNEL_POLICY_ENV = "GRM_CUDA_KERNEL_POLICY"
-_KERNEL_POLICY_OP_ENVS = {
+# Environment variables of the reference (cuda_ops.py:26-32): one per op and a global one.
+GLOBAL_POLICY_ENV = "GRM_CUDA_KERNEL_POLICY"
+OP_POLICY_ENV = {
     "chunk_update": "GRM_CUDA_CHUNK_UPDATE_POLICY",
     "apply_query": "GRM_CUDA_APPLY_QUERY_POLICY",
     "batched_memory_gather": "GRM_CUDA_BATCHED_GATHER_POLICY",
 }
-_VALID_KERNEL_POLICIES = {"auto", "native", "fallback"}
+POLICIES = ("auto", "native", "fallback")
+
+# Chunk length of the backward's state checkpoints (BCT in csrc/chunk_bwd.hip).
+_STATE_CHUNK = 64
 
 
 class GrmExtensionUnavailable(RuntimeError):
     """The HIP extension is required for a GPU tensor but could not be loaded."""
 
 
-def _has_registered_ops() -> bool:
-    namespace = getattr(torch.ops, "grm_cuda", None)
-    if namespace is None:
+class _OpLibrary:
+    """The compiled op library, imported on first use.  A failed import is not
+    retried unless forced, and its reasons are kept for the status report."""
+
+    module_names = ("rnn_with_grm_amd.grm_cuda_ext", "grm_cuda_ext", "grm.grm_cuda_ext")
+
+    def __init__(self) -> None:
+        self.module: Optional[Any] = None
+        self.attempted = False
+        self.error = ""
+
+    @staticmethod
+    def namespace():
+        return getattr(torch.ops, "grm_cuda", None)
+
+    def schemas_present(self) -> bool:
+        ns = self.namespace()
+        return ns is not None and all(hasattr(ns, op) for op in SCHEMA_OPS)
+
+    def load(self, force: bool = False) -> bool:
+        if self.module is not None and not force:
+            return True
+        if self.attempted and not force:
+            return False
+        self.attempted, self.module, self.error = True, None, ""
+        reasons = []
+        for name in self.module_names:
+            try:
+                candidate = importlib.import_module(name)
+            except Exception as exc:  # recorded, reported by the status dictionary
+                reasons.append(f"{name}: {type(exc).__name__}: {exc}")
+                continue
+            if self.schemas_present():
+                self.module = candidate
+                return True
+            reasons.append(f"{name}: torch.ops.grm_cuda registration missing")
+        self.error = "; ".join(reasons)
         return False
-    return all(hasattr(namespace, name) for name in _REGISTERED_OPS)
+
+    @staticmethod
+    def has_kernel(op: str, key: str) -> bool:
+        probe = getattr(torch._C, "_dispatch_has_kernel_for_dispatch_key", None)
+        if probe is None:
+            return False
+        try:
+            return bool(probe(f"grm_cuda::{op}", key))
+        except Exception:
+            return False
+
+    def kernel_table(self) -> Dict[str, Dict[str, bool]]:
+        return {op: {"cuda": self.has_kernel(op, "CUDA"),
+                     "composite_explicit_autograd": self.has_kernel(op, "CompositeExplicitAutograd")}
+                for op in SCHEMA_OPS}
 
 
-def _has_dispatch_kernel(op_name: str, dispatch_key: str) -> bool:
-    checker = getattr(torch._C, "_dispatch_has_kernel_for_dispatch_key", None)
-    if checker is None:
-        return False
-    try:
-        return bool(checker(f"grm_cuda::{op_name}", dispatch_key))
-    except Exception:
-        return False
+_LIB = _OpLibrary()
 
 
-def _get_dispatch_kernel_status() -> Dict[str, Dict[str, bool]]:
-    return {
-        name: {
-            "cuda": _has_dispatch_kernel(name, "CUDA"),
-            "composite_explicit_autograd": _has_dispatch_kernel(name, "CompositeExplicitAutograd"),
-        }
-        for name in _REGISTERED_OPS
-    }
+def extension_module() -> Optional[Any]:
+    """The loaded op-library module (None before a successful load)."""
+    return _LIB.module
+
+
+def extension_load_error() -> str:
+    """Why the last load attempt failed ('' after a success)."""
+    return _LIB.error
 
 
 def load_grm_cuda_extension(force: bool = False) -> bool:
-    """Import the extension once; ``force`` retries.  Mirrors cuda_ops.py:62-89."""
-    global _EXTENSION_MODULE, _EXTENSION_LOAD_ATTEMPTED, _EXTENSION_LOAD_ERROR
-    if _EXTENSION_MODULE is not None and not force:
-        return True
-    if _EXTENSION_LOAD_ATTEMPTED and not force:
-        return False
-    _EXTENSION_LOAD_ATTEMPTED = True
-    _EXTENSION_MODULE = None
-    _EXTENSION_LOAD_ERROR = ""
-    errors = []
-    for module_name in _IMPORT_CANDIDATES:
-        try:
-            module = importlib.import_module(module_name)
-        except Exception as exc:  # import failure is recorded, as in the reference
-            errors.append(f"{module_name}: {type(exc).__name__}: {exc}")
-            continue
-        if not _has_registered_ops():
-            errors.append(f"{module_name}: torch.ops.grm_cuda registration missing")
-            continue
-        _EXTENSION_MODULE = module
-        _EXTENSION_LOAD_ERROR = ""
-        return True
-    _EXTENSION_LOAD_ERROR = "; ".join(errors)
-    return False
+    """Import the op library once (``force`` tries again); True when its ops are registered."""
+    return _LIB.load(force)
 
 
 def is_grm_cpp_extension_available() -> bool:
-    return load_grm_cuda_extension()
+    return _LIB.load()
 
 
 def is_grm_cuda_available() -> bool:
-    if not load_grm_cuda_extension():
+    if not _LIB.load():
         return False
-    status = _get_dispatch_kernel_status()
-    return all(s["cuda"] for s in status.values()) and torch.cuda.is_available()
+    return torch.cuda.is_available() and all(entry["cuda"] for entry in _LIB.kernel_table().values())
 
 
-def _get_kernel_policy(op_name: str) -> str:
-    for env_name in (_KERNEL_POLICY_OP_ENVS.get(op_name, ""), _KERNEL_POLICY_ENV):
-        if not env_name:
-            continue
-        value = os.environ.get(env_name, "").strip().lower()
-        if value and value in _VALID_KERNEL_POLICIES:
+def kernel_policy(op_name: str) -> str:
+    """The op's own variable wins over the global one; unset or unknown values are skipped."""
+    for env in (OP_POLICY_ENV.get(op_name), GLOBAL_POLICY_ENV):
+        value = os.environ.get(env, "").strip().lower() if env else ""
+        if value in POLICIES:
             return value
     return "auto"
 
 
 def get_grm_cuda_runtime_status() -> Dict[str, Any]:
-    """Same keys as the reference (cuda_ops.py:185-215), plus ``hip``."""
-    extension_loaded = load_grm_cuda_extension()
-    namespace = getattr(torch.ops, "grm_cuda", None)
-    registered_ops = {name: bool(namespace and hasattr(namespace, name)) for name in _REGISTERED_OPS}
-    compiled_with_cuda_sources = bool(
-        getattr(_EXTENSION_MODULE, "__grm_cuda_with_kernels__", False) if _EXTENSION_MODULE is not None else False
+    """The reference's status keys (cuda_ops.py:198-215), plus ``hip``."""
+    loaded = _LIB.load()
+    ns = _LIB.namespace()
+    table = _LIB.kernel_table() if loaded else {op: {"cuda": False, "composite_explicit_autograd": False}
+                                                for op in SCHEMA_OPS}
+    with_sources = loaded and bool(getattr(_LIB.module, "__grm_cuda_with_kernels__", False))
+    with_kernels = with_sources and all(entry["cuda"] for entry in table.values())
+    gpu = torch.cuda.is_available()
+    status: Dict[str, Any] = dict(
+        load_attempted=_LIB.attempted,
+        extension_loaded=loaded,
+        compiled_with_cuda_sources=with_sources,
+        compiled_with_cuda_kernels=with_kernels,
+        torch_cuda_available=gpu,
+        cuda_backend_available=with_kernels and gpu,
+        load_error=_LIB.error,
+        module_name=_LIB.module.__name__ if loaded else "",
+        registered_ops={op: ns is not None and hasattr(ns, op) for op in SCHEMA_OPS},
+        dispatch_kernels=table,
+        kernel_policy={"global": kernel_policy(""), **{op: kernel_policy(op) for op in OP_POLICY_ENV}},
     )
-    dispatch_kernels = _get_dispatch_kernel_status() if extension_loaded else {
-        name: {"cuda": False, "composite_explicit_autograd": False} for name in _REGISTERED_OPS
-    }
-    compiled_with_cuda_kernels = compiled_with_cuda_sources and all(s["cuda"] for s in dispatch_kernels.values())
-    status: Dict[str, Any] = {
-        "load_attempted": _EXTENSION_LOAD_ATTEMPTED,
-        "extension_loaded": extension_loaded,
-        "compiled_with_cuda_sources": compiled_with_cuda_sources,
-        "compiled_with_cuda_kernels": compiled_with_cuda_kernels,
-        "torch_cuda_available": torch.cuda.is_available(),
-        "cuda_backend_available": compiled_with_cuda_kernels and torch.cuda.is_available(),
-        "load_error": _EXTENSION_LOAD_ERROR,
-        "module_name": getattr(_EXTENSION_MODULE, "__name__", "") if _EXTENSION_MODULE is not None else "",
-        "registered_ops": registered_ops,
-        "dispatch_kernels": dispatch_kernels,
-        "kernel_policy": {
-            "global": _get_kernel_policy(""),
-            "chunk_update": _get_kernel_policy("chunk_update"),
-            "apply_query": _get_kernel_policy("apply_query"),
-            "batched_memory_gather": _get_kernel_policy("batched_memory_gather"),
-        },
-    }
-    if _EXTENSION_MODULE is not None:
+    if loaded:
         status["hip"] = {
-            "arch": getattr(_EXTENSION_MODULE, "__grm_hip_arch__", ""),
-            "launch_count": int(_EXTENSION_MODULE.hip_launch_count()),
-            "generic_path_calls": int(_EXTENSION_MODULE.generic_path_calls()),
-            "extra_ops": {name: bool(namespace and hasattr(namespace, name)) for name in _EXTRA_OPS},
+            "arch": getattr(_LIB.module, "__grm_hip_arch__", ""),
+            "launch_count": int(_LIB.module.hip_launch_count()),
+            "generic_path_calls": int(_LIB.module.generic_path_calls()),
+            "extra_ops": {op: ns is not None and hasattr(ns, op) for op in EXTRA_OPS},
         }
     return status
 
 
-def _require_extension(device: torch.device) -> bool:
-    """True when the native op should run.  On a GPU the extension is
-    mandatory; on CPU its absence falls back like the reference."""
-    if load_grm_cuda_extension():
+def _native_required(device: torch.device) -> bool:
+    """True when the op library is there.  A GPU tensor needs it; on the CPU its
+    absence means the PyTorch path, as in the reference."""
+    if _LIB.load():
         return True
     if device.type == "cuda":
         raise GrmExtensionUnavailable(
             "GRM HIP extension (grm_cuda_ext / libgrm_hip.so) is not loaded; build it with "
-            f"`python -m rnn_with_grm_amd.build`. Load error: {_EXTENSION_LOAD_ERROR}"
-        )
+            f"`python -m rnn_with_grm_amd.build`. Load error: {_LIB.error}")
     return False
 
 
-def _use_native(op_name: str, device: torch.device, *, enabled: bool, debug_fallback: bool,
+def _run_native(op_name: str, device: torch.device, *, enabled: bool, debug_fallback: bool,
                 auto_on_cpu: bool = False) -> bool:
-    if not enabled or debug_fallback:
+    """Which path a call takes: disabled or debug calls and a ``fallback`` policy take
+    PyTorch; ``native`` takes the library; ``auto`` takes it on the GPU (and on the CPU
+    where the reference's auto rule does)."""
+    if debug_fallback or not enabled:
         return False
-    policy = _get_kernel_policy(op_name)
-    if policy == "fallback":
+    policy = kernel_policy(op_name)
+    if policy == "fallback" or not _native_required(device):
         return False
-    if not _require_extension(device):
-        return False
-    if policy == "native":
-        return True
-    return device.type == "cuda" or auto_on_cpu
+    return policy == "native" or device.type == "cuda" or auto_on_cpu
 
 
 # ---------------------------------------------------------------------------
-# Pure-PyTorch fallbacks (same maths as cuda_ops.py:218-284).
+# PyTorch paths (the maths of the reference's fallbacks, cuda_ops.py:218-284).
 
-def _vectorized_chunk_update(keys: Tensor, values: Tensor, queries: Tensor, memory: Tensor,
-                             memory_decay: float) -> Tuple[Tensor, Tensor]:
-    batch, length, key_dim = keys.shape
-    if length == 0:
-        return values.new_zeros(batch, 0, values.size(-1)), memory
-    lam = torch.as_tensor(memory_decay, device=memory.device, dtype=memory.dtype)
-    pos = torch.arange(length, device=memory.device, dtype=memory.dtype)
-    inv_sqrt = 1.0 / math.sqrt(float(key_dim))
-    carried = torch.matmul(queries, memory.transpose(1, 2)) * torch.pow(lam, pos + 1.0).view(1, length, 1)
-    gap = pos.view(-1, 1) - pos.view(1, -1)
-    decay_tri = torch.pow(lam, gap.clamp_min(0)) * (gap >= 0).to(memory.dtype)
-    attn = torch.matmul(queries, keys.transpose(1, 2)) * inv_sqrt * decay_tri
-    hidden = carried + (1.0 - lam) * torch.matmul(attn, values)
-    tail = (1.0 - lam) * torch.pow(lam, (length - 1) - pos) * inv_sqrt
-    delta = torch.matmul((values * tail.view(1, length, 1)).transpose(1, 2), keys)
-    memory_out = torch.pow(lam, torch.tensor(float(length), device=memory.device, dtype=memory.dtype)) * memory + delta
-    return hidden, memory_out
+def _decay_powers(decay: float, n: int, like: Tensor) -> Tensor:
+    """decay ** [0, 1, ..., n] in like's dtype and device."""
+    base = torch.full((n + 1,), float(decay), dtype=like.dtype, device=like.device)
+    return base.pow(torch.arange(n + 1, dtype=like.dtype, device=like.device))
 
 
-def _fallback_apply_query(memories: Tensor, queries: Tensor) -> Tensor:
-    if memories.ndim == 5:
-        return torch.einsum("bqrhk,bqk->bqrh", memories, queries)
-    if memories.ndim == 4:
-        return torch.einsum("brhk,bk->brh", memories, queries)
+def _torch_chunk_update(keys: Tensor, values: Tensor, queries: Tensor, memory: Tensor,
+                        memory_decay: float) -> Tuple[Tensor, Tensor]:
+    """One chunk of L tokens from state M in closed form, c = (1 - decay) / sqrt(d_k):
+    h_i = decay^(i+1) M q_i + c sum_{j<=i} decay^(i-j) (q_i . k_j) v_j,
+    M'  = decay^L M + c sum_j decay^(L-1-j) v_j k_j^T."""
+    B, L, K = keys.shape
+    if L == 0:
+        return values.new_zeros(B, 0, values.size(-1)), memory
+    powers = _decay_powers(memory_decay, L, memory)
+    c = (1.0 - float(memory_decay)) / math.sqrt(float(K))
+    step = torch.arange(L, device=memory.device)
+    lag = step.view(L, 1) - step.view(1, L)
+    causal = torch.where(lag >= 0, powers[lag.clamp_min(0)], torch.zeros((), dtype=memory.dtype,
+                                                                           device=memory.device))
+    carried = torch.bmm(queries, memory.transpose(1, 2)) * powers[1:].view(1, L, 1)
+    within = torch.bmm(torch.bmm(queries, keys.transpose(1, 2)) * causal, values) * c
+    tail = powers[:L].flip(0) * c                                   # c decay^(L-1-j)
+    memory_out = powers[L] * memory + torch.bmm((values * tail.view(1, L, 1)).transpose(1, 2), keys)
+    return carried + within, memory_out
+
+
+def _torch_apply_query(memories: Tensor, queries: Tensor) -> Tensor:
+    if memories.ndim == 5:                      # [B, Q, R, H, K] x [B, Q, K]
+        return torch.matmul(memories, queries[:, :, None, :, None]).squeeze(-1)
+    if memories.ndim == 4:                      # [B, R, H, K] x [B, K]
+        return torch.matmul(memories, queries[:, None, :, None]).squeeze(-1)
     raise ValueError(f"Unsupported memory rank for apply-query: {memories.ndim}")
 
 
-def _fallback_batched_memory_gather(memories_per_batch: Tensor, topk_indices: Tensor) -> Tensor:
+def _torch_batched_gather(memories_per_batch: Tensor, topk_indices: Tensor) -> Tensor:
     if memories_per_batch.ndim != 4:
         raise ValueError(f"Expected memories_per_batch rank 4, got {memories_per_batch.ndim}")
     if topk_indices.ndim not in (2, 3):
         raise ValueError(f"Expected topk_indices rank 2 or 3, got {topk_indices.ndim}")
-    rows = [memories_per_batch[b].index_select(0, topk_indices[b].reshape(-1))
-            for b in range(memories_per_batch.size(0))]
-    shape = (memories_per_batch.size(0), *topk_indices.shape[1:], *memories_per_batch.shape[2:])
-    if not rows:
-        return memories_per_batch.new_empty(shape)
-    return torch.stack(rows, 0).reshape(shape).contiguous()
+    B = memories_per_batch.size(0)
+    flat = topk_indices.reshape(B, -1).long()
+    rows = torch.arange(B, device=memories_per_batch.device).view(B, 1).expand_as(flat)
+    picked = memories_per_batch[rows, flat]
+    return picked.reshape(B, *topk_indices.shape[1:], *memories_per_batch.shape[2:]).contiguous()
 
 
 # ---------------------------------------------------------------------------
 # Autograd wrappers.
 
-class ChunkUpdateCudaFn(torch.autograd.Function):
-    """Native forward/backward (cuda_ops.py:287-321); grads come back in the
-    dtype of the tensor they belong to."""
+def _scan_grads(ctx, grad_hidden: Optional[Tensor], grad_memory_out: Optional[Tensor], chunk_states: Tensor):
+    """chunk_update_backward with missing output gradients as zeros, each gradient cast
+    to the dtype of its input (cuda_ops.py:304-309)."""
+    keys, values, queries, memory = ctx.saved_tensors[:4]
+    if grad_hidden is None:
+        grad_hidden = values.new_zeros(keys.size(0), keys.size(1), values.size(2))
+    if grad_memory_out is None:
+        grad_memory_out = torch.zeros_like(memory)
+    return torch.ops.grm_cuda.chunk_update_backward(
+        grad_hidden.to(values.dtype).contiguous(), grad_memory_out.to(memory.dtype).contiguous(),
+        keys, values, queries, memory, chunk_states, ctx.decay)
+
+
+class _ChunkScanFn(torch.autograd.Function):
+    """The fused scan.  When gradients are wanted, the forward also keeps the state
+    after every 64-token chunk (the whole-sequence op with 64-token snapshots), and
+    the backward reads those instead of scanning again."""
 
     @staticmethod
     def forward(ctx, keys: Tensor, values: Tensor, queries: Tensor, memory: Tensor, memory_decay: float):
-        hidden, memory_out, aux = torch.ops.grm_cuda.chunk_update_forward(keys, values, queries, memory,
-                                                                            float(memory_decay))
-        ctx.memory_decay = float(memory_decay)
-        ctx.save_for_backward(keys, values, queries, memory, aux)
+        ctx.decay = float(memory_decay)
+        if any(ctx.needs_input_grad[:4]):
+            hidden, memory_out, states = torch.ops.grm_cuda.segment_scan_forward(
+                keys, values, queries, memory, ctx.decay, _STATE_CHUNK)
+            if memory_out.dtype != memory.dtype:
+                memory_out = memory_out.to(memory.dtype)
+        else:
+            hidden, memory_out, states = torch.ops.grm_cuda.chunk_update_forward(
+                keys, values, queries, memory, ctx.decay)
+        ctx.save_for_backward(keys, values, queries, memory, states)
         return hidden, memory_out
 
     @staticmethod
     def backward(ctx, grad_hidden: Tensor, grad_memory_out: Tensor):
-        keys, values, queries, memory, aux = ctx.saved_tensors
-        if grad_hidden is None:
-            grad_hidden = torch.zeros((keys.size(0), keys.size(1), values.size(2)), dtype=values.dtype,
-                                      device=values.device)
-        if grad_memory_out is None:
-            grad_memory_out = torch.zeros_like(memory)
-        gk, gv, gq, gm = torch.ops.grm_cuda.chunk_update_backward(
-            grad_hidden.to(values.dtype).contiguous(), grad_memory_out.to(memory.dtype).contiguous(),
-            keys, values, queries, memory, aux, float(ctx.memory_decay))
-        return gk, gv, gq, gm, None
+        return (*_scan_grads(ctx, grad_hidden, grad_memory_out, ctx.saved_tensors[4]), None)
 
 
-class SegmentScanCudaFn(torch.autograd.Function):
-    """Whole-sequence scan with per-segment snapshots; snapshots carry no gradient."""
+class _SegmentScanFn(torch.autograd.Function):
+    """Whole-sequence scan with per-segment snapshots; snapshots carry no gradient.
+    With 64-token segments the snapshots are the backward's chunk states."""
 
     @staticmethod
     def forward(ctx, keys, values, queries, memory, memory_decay: float, segment_len: int):
+        ctx.decay = float(memory_decay)
         hidden, memory_out, snapshots = torch.ops.grm_cuda.segment_scan_forward(
-            keys, values, queries, memory, float(memory_decay), int(segment_len))
-        ctx.memory_decay = float(memory_decay)
-        ctx.save_for_backward(keys, values, queries, memory)
+            keys, values, queries, memory, ctx.decay, int(segment_len))
+        states = snapshots if int(segment_len) == _STATE_CHUNK else memory.new_empty(0)
+        ctx.save_for_backward(keys, values, queries, memory, states)
         ctx.mark_non_differentiable(snapshots)
         return hidden, memory_out, snapshots
 
     @staticmethod
     def backward(ctx, grad_hidden, grad_memory_out, _grad_snapshots):
-        keys, values, queries, memory = ctx.saved_tensors
-        if grad_hidden is None:
-            grad_hidden = torch.zeros((keys.size(0), keys.size(1), values.size(2)), dtype=values.dtype,
-                                      device=values.device)
-        if grad_memory_out is None:
-            grad_memory_out = torch.zeros_like(memory)
-        aux = memory.new_empty(0)
-        gk, gv, gq, gm = torch.ops.grm_cuda.chunk_update_backward(
-            grad_hidden.to(values.dtype).contiguous(), grad_memory_out.to(memory.dtype).contiguous(),
-            keys, values, queries, memory, aux, float(ctx.memory_decay))
-        return gk, gv, gq, gm, None, None
+        return (*_scan_grads(ctx, grad_hidden, grad_memory_out, ctx.saved_tensors[4]), None, None)
 
 
-class ApplyQueryCudaFn(torch.autograd.Function):
+class _ApplyQueryFn(torch.autograd.Function):
+    """Native apply-query.  The backward forms grad_memories only when the memories
+    need it (a retrieved archive never does)."""
+
     @staticmethod
     def forward(ctx, memories: Tensor, queries: Tensor):
-        hidden = torch.ops.grm_cuda.apply_query_forward(memories, queries)
         ctx.save_for_backward(memories, queries)
-        return hidden
+        return torch.ops.grm_cuda.apply_query_forward(memories, queries)
 
     @staticmethod
     def backward(ctx, grad_hidden: Tensor):
         memories, queries = ctx.saved_tensors
-        grad_memories, grad_queries = torch.ops.grm_cuda.apply_query_backward(
-            grad_hidden.to(memories.dtype).contiguous(), memories, queries)
-        return grad_memories, grad_queries
+        grad_hidden = grad_hidden.to(memories.dtype).contiguous()
+        if not ctx.needs_input_grad[0]:
+            return None, torch.ops.grm_cuda.apply_query_backward_queries(grad_hidden, memories, queries)
+        return torch.ops.grm_cuda.apply_query_backward(grad_hidden, memories, queries)
 
 
 # ---------------------------------------------------------------------------
-# Entry points (cuda_ops.py:347-402 and the new ones).
+# Entry points (the reference's cuda_ops.py:347-402, then this library's own).
 
 def cuda_chunk_update(keys: Tensor, values: Tensor, queries: Tensor, memory: Tensor, memory_decay: float, *,
                       enabled: bool = True, debug_fallback: bool = False) -> Tuple[Tensor, Tensor]:
-    if _use_native("chunk_update", memory.device, enabled=enabled, debug_fallback=debug_fallback):
-        return ChunkUpdateCudaFn.apply(keys, values, queries, memory, float(memory_decay))
-    return _vectorized_chunk_update(keys, values, queries, memory, memory_decay)
+    if _run_native("chunk_update", memory.device, enabled=enabled, debug_fallback=debug_fallback):
+        return _ChunkScanFn.apply(keys, values, queries, memory, float(memory_decay))
+    return _torch_chunk_update(keys, values, queries, memory, memory_decay)
 
 
 def cuda_apply_query(memories: Tensor, queries: Tensor, *, enabled: bool = True,
                      debug_fallback: bool = False) -> Tensor:
-    if _use_native("apply_query", memories.device, enabled=enabled, debug_fallback=debug_fallback):
-        return ApplyQueryCudaFn.apply(memories, queries)
-    return _fallback_apply_query(memories, queries)
+    if _run_native("apply_query", memories.device, enabled=enabled, debug_fallback=debug_fallback):
+        return _ApplyQueryFn.apply(memories, queries)
+    return _torch_apply_query(memories, queries)
 
 
 def cuda_batched_memory_gather(memories_per_batch: Tensor, topk_indices: Tensor, *, enabled: bool = True,
                                debug_fallback: bool = False) -> Tensor:
-    # The reference's auto policy uses the extension on CPU too (cuda_ops.py:158-174).
-    if _use_native("batched_memory_gather", memories_per_batch.device, enabled=enabled,
+    # The reference's auto rule uses the library on the CPU too (cuda_ops.py:158-174).
+    if _run_native("batched_memory_gather", memories_per_batch.device, enabled=enabled,
                    debug_fallback=debug_fallback, auto_on_cpu=True):
         return torch.ops.grm_cuda.batched_memory_gather(memories_per_batch, topk_indices)
-    return _fallback_batched_memory_gather(memories_per_batch, topk_indices)
+    return _torch_batched_gather(memories_per_batch, topk_indices)
 
 
 def cuda_segment_scan(keys: Tensor, values: Tensor, queries: Tensor, memory: Tensor, memory_decay: float,
@@ -340,35 +364,35 @@ def cuda_segment_scan(keys: Tensor, values: Tensor, queries: Tensor, memory: Ten
                       debug_fallback: bool = False) -> Tuple[Tensor, Tensor, Tensor]:
     """Whole sequence in one call.  Returns (hidden [B,T,H], memory_out [B,H,K],
     snapshots float32 [B, ceil(T/segment_len), H, K] = state after each segment)."""
-    if _use_native("chunk_update", memory.device, enabled=enabled, debug_fallback=debug_fallback):
-        return SegmentScanCudaFn.apply(keys, values, queries, memory, float(memory_decay), int(segment_len))
-    outs, snaps = [], []
-    state = memory
-    for t0 in range(0, keys.size(1), segment_len):
-        sl = slice(t0, t0 + segment_len)
-        h, state = _vectorized_chunk_update(keys[:, sl], values[:, sl], queries[:, sl], state, memory_decay)
-        outs.append(h)
-        snaps.append(state.float())
-    hidden = torch.cat(outs, 1) if outs else values.new_zeros(values.size(0), 0, values.size(2))
-    snapshots = torch.stack(snaps, 1) if snaps else memory.new_zeros(memory.size(0), 0, *memory.shape[1:]).float()
-    return hidden, state, snapshots
+    if _run_native("chunk_update", memory.device, enabled=enabled, debug_fallback=debug_fallback):
+        return _SegmentScanFn.apply(keys, values, queries, memory, float(memory_decay), int(segment_len))
+    T = keys.size(1)
+    hiddens, snapshots, state = [], [], memory
+    for t0 in range(0, T, segment_len):
+        part = slice(t0, t0 + segment_len)
+        h, state = _torch_chunk_update(keys[:, part], values[:, part], queries[:, part], state, memory_decay)
+        hiddens.append(h)
+        snapshots.append(state.float())
+    if not hiddens:
+        return (values.new_zeros(values.size(0), 0, values.size(2)), memory,
+                memory.new_zeros(memory.size(0), 0, *memory.shape[1:]).float())
+    return torch.cat(hiddens, 1), state, torch.stack(snapshots, 1)
 
 
 def cuda_topk_route(queries: Tensor, keys: Tensor, top_k: int, scale: float, temperature: float = 1.0, *,
                     enabled: bool = True, debug_fallback: bool = False) -> Tuple[Tensor, Tensor, Tensor]:
     """Score -> top-k -> softmax (paper_grm.py:566-589).  Returns (gates, indices, scores).
     Native scores are one float32 FMA chain per score; ties go to the lower index."""
-    if _use_native("topk_route", queries.device, enabled=enabled, debug_fallback=debug_fallback,
+    if _run_native("topk_route", queries.device, enabled=enabled, debug_fallback=debug_fallback,
                    auto_on_cpu=True):
         return torch.ops.grm_cuda.topk_route(queries, keys, int(top_k), float(scale), float(temperature))
     scores = torch.matmul(queries, keys.transpose(1, 2)) * scale
-    k = min(top_k, keys.size(1))
-    if k < keys.size(1):
-        top, idx = torch.topk(scores, k=k, dim=-1)
-    else:
+    S = keys.size(1)
+    if min(top_k, S) < S:
+        top, idx = torch.topk(scores, k=min(top_k, S), dim=-1)
+    else:  # every key, in index order
         top = scores
-        idx = torch.arange(keys.size(1), device=queries.device).view(1, 1, -1).expand(
-            queries.size(0), queries.size(1), -1)
+        idx = torch.arange(S, device=queries.device).expand(queries.size(0), queries.size(1), S)
     return torch.softmax(top / temperature, dim=-1), idx, top
 
 
@@ -382,7 +406,7 @@ def cuda_segment_route(queries: Tensor, keys: Tensor, top_k: int, segment_len: i
     Returns (gates, indices, scores), each [B, Q, top_k]; indices are absolute key
     positions, and a window of n <= top_k keys fills slots n.. with index -1,
     score -inf and gate 0."""
-    if _use_native("topk_route", queries.device, enabled=enabled, debug_fallback=debug_fallback,
+    if _run_native("topk_route", queries.device, enabled=enabled, debug_fallback=debug_fallback,
                    auto_on_cpu=True):
         return torch.ops.grm_cuda.segment_route(queries, keys, int(top_k), int(segment_len), int(base),
                                                 int(capacity), float(scale), float(temperature))
@@ -390,17 +414,14 @@ def cuda_segment_route(queries: Tensor, keys: Tensor, top_k: int, segment_len: i
     gates = queries.new_zeros((B, Q, top_k), dtype=torch.float32)
     idx = torch.full((B, Q, top_k), -1, dtype=torch.long, device=queries.device)
     scores = torch.full((B, Q, top_k), float("-inf"), dtype=torch.float32, device=queries.device)
-    for t0 in range(0, Q, segment_len):
-        hi = min(keys.size(1), base + t0 // segment_len)
+    for seg, t0 in enumerate(range(0, Q, segment_len)):
+        hi = min(keys.size(1), base + seg)
         lo = max(0, hi - capacity)
-        if hi <= lo:
-            continue
-        sl = slice(t0, t0 + segment_len)
-        g, i, sc = cuda_topk_route(queries[:, sl], keys[:, lo:hi], top_k, scale, temperature, enabled=False)
-        n = g.size(-1)
-        gates[:, sl, :n] = g.float()
-        idx[:, sl, :n] = i + lo
-        scores[:, sl, :n] = sc.float()
+        if hi > lo:
+            rows = slice(t0, t0 + segment_len)
+            g, i, sc = cuda_topk_route(queries[:, rows], keys[:, lo:hi], top_k, scale, temperature, enabled=False)
+            n = g.size(-1)
+            gates[:, rows, :n], idx[:, rows, :n], scores[:, rows, :n] = g.float(), i + lo, sc.float()
     return gates, idx, scores
 
 
@@ -408,11 +429,11 @@ def cuda_fuse_residual(h_online: Tensor, retrieved: Tensor, gates: Tensor, weigh
                        bias: Optional[Tensor] = None, eps: float = 1e-5, *, enabled: bool = True,
                        debug_fallback: bool = False) -> Tensor:
     """LayerNorm(h + sum_r g_r r_r) (aggregator.py:67-145, residual mode); no LN when weight is None."""
-    if _use_native("fuse_residual", h_online.device, enabled=enabled, debug_fallback=debug_fallback):
+    if _run_native("fuse_residual", h_online.device, enabled=enabled, debug_fallback=debug_fallback):
         return torch.ops.grm_cuda.fuse_residual(h_online, retrieved, gates, weight, bias, float(eps))
     x = h_online
     if retrieved.size(1) > 0:
-        x = x + (retrieved * gates.to(retrieved.dtype).unsqueeze(-1)).sum(1)
+        x = x + torch.einsum("nr,nrh->nh", gates.to(retrieved.dtype), retrieved)
     if weight is not None:
         x = torch.nn.functional.layer_norm(x, (h_online.size(-1),), weight, bias, eps)
     return x
@@ -426,7 +447,7 @@ def cuda_gather_apply(memories_per_batch: Tensor, topk_indices: Tensor, queries:
     ``dtype`` is M's dtype by default; float32 widens 16-bit archives as the retriever does.
     The fused op has no backward: when autograd needs gradients the composition runs."""
     needs_grad = torch.is_grad_enabled() and (memories_per_batch.requires_grad or queries.requires_grad)
-    if not needs_grad and _use_native("gather_apply", memories_per_batch.device, enabled=enabled,
+    if not needs_grad and _run_native("gather_apply", memories_per_batch.device, enabled=enabled,
                                       debug_fallback=debug_fallback):
         return torch.ops.grm_cuda.gather_apply(memories_per_batch, topk_indices, queries, dtype)
     gathered = cuda_batched_memory_gather(memories_per_batch, topk_indices, enabled=enabled,
@@ -446,8 +467,11 @@ __all__ = [
     "cuda_segment_route",
     "cuda_segment_scan",
     "cuda_topk_route",
+    "extension_load_error",
+    "extension_module",
     "get_grm_cuda_runtime_status",
     "is_grm_cpp_extension_available",
     "is_grm_cuda_available",
+    "kernel_policy",
     "load_grm_cuda_extension",
 ]

@@ -22,5 +22,5 @@ def dev():
         pytest.skip("no GPU")
     from rnn_with_grm_amd import cuda_ops
 
-    assert cuda_ops.load_grm_cuda_extension(), cuda_ops._EXTENSION_LOAD_ERROR
+    assert cuda_ops.load_grm_cuda_extension(), cuda_ops.extension_load_error()
     return torch.device("cuda:0")

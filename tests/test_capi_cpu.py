@@ -37,7 +37,7 @@ def test_workspace_query():
 
 def test_abi_version_and_counters():
     lib = capi.load()
-    assert lib.grm_hip_abi_version() == 100
+    assert lib.grm_hip_abi_version() == 101
     assert capi.launch_count() >= 0
 
 
@@ -98,5 +98,5 @@ def test_other_entry_points_reject():
                                      None) == capi.EINVAL  # segment_len 0
     assert lib.grm_hip_fuse_residual(fake, fake, fake, None, None, fake, 1, 1, 4096, 0, 1e-5,
                                      None) == capi.EUNSUPPORTED
-    assert lib.grm_hip_chunk_update_bwd(fake, fake, fake, fake, fake, fake, fake, fake, fake, fake, fake, fake,
+    assert lib.grm_hip_chunk_update_bwd(fake, fake, fake, fake, fake, fake, fake, fake, fake, fake, fake, 0, fake,
                                         1, 4, 512, 4, 0, 0, 0.9, None) == capi.EUNSUPPORTED

@@ -46,21 +46,21 @@ def test_policy_precedence(monkeypatch):
     monkeypatch.setenv("GRM_CUDA_KERNEL_POLICY", "fallback")
     monkeypatch.setenv("GRM_CUDA_CHUNK_UPDATE_POLICY", "native")
     monkeypatch.setenv("GRM_CUDA_APPLY_QUERY_POLICY", "bogus")
-    assert cuda_ops._get_kernel_policy("chunk_update") == "native"  # per-op beats global
-    assert cuda_ops._get_kernel_policy("apply_query") == "fallback"  # invalid per-op value is ignored
-    assert cuda_ops._get_kernel_policy("batched_memory_gather") == "fallback"
-    assert cuda_ops._get_kernel_policy("") == "fallback"
+    assert cuda_ops.kernel_policy("chunk_update") == "native"  # per-op beats global
+    assert cuda_ops.kernel_policy("apply_query") == "fallback"  # invalid per-op value is ignored
+    assert cuda_ops.kernel_policy("batched_memory_gather") == "fallback"
+    assert cuda_ops.kernel_policy("") == "fallback"
     monkeypatch.delenv("GRM_CUDA_KERNEL_POLICY")
-    assert cuda_ops._get_kernel_policy("batched_memory_gather") == "auto"
+    assert cuda_ops.kernel_policy("batched_memory_gather") == "auto"
 
 
 def test_gpu_tensor_without_extension_raises(monkeypatch):
-    monkeypatch.setattr(cuda_ops, "_EXTENSION_MODULE", None)
-    monkeypatch.setattr(cuda_ops, "_EXTENSION_LOAD_ATTEMPTED", True)
-    monkeypatch.setattr(cuda_ops, "_EXTENSION_LOAD_ERROR", "simulated import failure")
+    monkeypatch.setattr(cuda_ops._LIB, "module", None)
+    monkeypatch.setattr(cuda_ops._LIB, "attempted", True)
+    monkeypatch.setattr(cuda_ops._LIB, "error", "simulated import failure")
     with pytest.raises(cuda_ops.GrmExtensionUnavailable, match="simulated import failure"):
-        cuda_ops._require_extension(torch.device("cuda"))
-    assert cuda_ops._require_extension(torch.device("cpu")) is False
+        cuda_ops._native_required(torch.device("cuda"))
+    assert cuda_ops._native_required(torch.device("cpu")) is False
     status = cuda_ops.get_grm_cuda_runtime_status()
     assert status["extension_loaded"] is False and status["load_error"] == "simulated import failure"
 
@@ -110,7 +110,7 @@ def test_entrypoint_parity_reference_case():
 
 def test_fallback_chunk_update_matches_oracle():
     k, v, q, m = make_chunk_case(64, dtype=torch.float64, seed=5)
-    h, mo = cuda_ops._vectorized_chunk_update(k, v, q, m, 0.97)
+    h, mo = cuda_ops._torch_chunk_update(k, v, q, m, 0.97)
     rh, rm, _ = orc.chunk_update_seq(np64(k), np64(v), np64(q), np64(m), 0.97)
     np.testing.assert_allclose(np64(h), rh, rtol=1e-12, atol=1e-12)
     np.testing.assert_allclose(np64(mo), rm, rtol=1e-12, atol=1e-12)

@@ -271,7 +271,7 @@ def test_empty_and_zero_batch(dev):
 
 
 def test_native_path_runs(dev):
-    ext = cuda_ops._EXTENSION_MODULE
+    ext = cuda_ops.extension_module()
     before = ext.hip_launch_count()
     k, v, q, m = make_case(2, 64, 32, 16, torch.bfloat16, torch.float32)
     cuda_ops.cuda_chunk_update(k.to(dev), v.to(dev), q.to(dev), m.to(dev), 0.97)
@@ -356,3 +356,31 @@ def test_autograd_through_cuda_ops(dev):
 
     for a, b in zip(run(False), run(True)):
         torch.testing.assert_close(a, b, atol=5e-4, rtol=5e-4)
+
+
+@pytest.mark.parametrize("dtype,mem_dtype,T", [(torch.bfloat16, torch.float32, 300), (torch.float32, torch.float32, 70),
+                                               (torch.bfloat16, torch.bfloat16, 64)])
+def test_autograd_passes_chunk_states(dev, dtype, mem_dtype, T):
+    """Under autograd the forward keeps the state after every 64-token chunk as aux and the
+    backward reads it instead of scanning again: the gradients are bit-identical to the
+    backward that scans again, and the backward launches fewer kernels."""
+    k, v, q, m = make_case(2, T, 64, 96, dtype, mem_dtype, seed=T)
+    ins = [t.to(dev).requires_grad_(True) for t in (k, v, q, m)]
+    h, mo = cuda_ops.cuda_chunk_update(*ins, memory_decay=0.97)
+    g = torch.Generator().manual_seed(1)
+    dh = torch.randn(h.shape, generator=g).to(dtype).to(dev)
+    dm = torch.randn(mo.shape, generator=g).to(mem_dtype).to(dev)
+    before = capi.launch_count()
+    gk, gv, gq, gm = torch.autograd.grad((h, mo), ins, (dh, dm))
+    torch.cuda.synchronize()
+    with_states = capi.launch_count() - before
+    before = capi.launch_count()
+    rk, rv, rq, rm = capi.chunk_update_bwd(dh, dm, *[t.detach() for t in ins], 0.97)
+    torch.cuda.synchronize()
+    rescan = capi.launch_count() - before
+    assert with_states < rescan
+    for a, b in zip((gk, gv, gq, gm), (rk, rv, rq, rm)):
+        assert torch.equal(a, b)
+    # and the forward under autograd is the plain forward's
+    h0, mo0, _ = capi.chunk_update_fwd(*[t.detach() for t in ins], 0.97)
+    assert torch.equal(h.detach(), h0) and torch.equal(mo.detach(), mo0)

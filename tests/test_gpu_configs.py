@@ -286,7 +286,7 @@ def test_c4_model_forward_tracks_float32(dev):
     g = torch.Generator().manual_seed(7)
     ids = torch.randint(0, V, (B, T), generator=g).to(dev)
     outs = {}
-    before = cuda_ops._EXTENSION_MODULE.hip_launch_count()
+    before = cuda_ops.extension_module().hip_launch_count()
     for dt in (torch.float32, torch.bfloat16):
         print(f"config 4 model forward {dt}", flush=True)
         e = emb.to(device=dev, dtype=dt).eval()
@@ -296,7 +296,7 @@ def test_c4_model_forward_tracks_float32(dev):
         torch.cuda.synchronize()
         outs[dt] = o.float()
         assert torch.isfinite(outs[dt]).all()
-    assert cuda_ops._EXTENSION_MODULE.hip_launch_count() > before
+    assert cuda_ops.extension_module().hip_launch_count() > before
     a, r = outs[torch.bfloat16], outs[torch.float32]
     rel = float((a - r).norm() / r.norm())
     per_tok = ((a - r).norm(dim=-1) / r.norm(dim=-1).clamp_min(1e-12))

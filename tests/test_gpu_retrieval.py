@@ -474,3 +474,21 @@ def test_fuse_residual(dev, dtype, N, R, H, ln):
                             None if w is None else w.double().numpy(), None if b is None else b.double().numpy())
     rtol, atol = (1e-5, 1e-5) if dtype == torch.float32 else (2e-2, 2e-2)
     np.testing.assert_allclose(out.double().cpu().numpy(), ref, rtol=rtol, atol=atol)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("shape", [(2, 3, 8, 64, 128), (3, 4, 16, 64)])
+def test_apply_query_backward_queries_only(dev, dtype, shape):
+    """Memories that need no gradient (a retrieved archive): the backward computes grad_queries
+    only, equal to apply_query_backward's, and never forms grad_memories."""
+    g = torch.Generator().manual_seed(17)
+    mem = torch.randn(*shape, generator=g).to(dtype).to(dev)
+    qshape = shape[:2] + shape[-1:] if len(shape) == 5 else (shape[0], shape[-1])
+    q = norm(torch.randn(*qshape, generator=g)).to(dtype).to(dev).requires_grad_(True)
+    dh = torch.randn(*shape[:-1], generator=g).to(dtype).to(dev)
+    _, gq_full = torch.ops.grm_cuda.apply_query_backward(dh, mem, q.detach())
+    gq_only = torch.ops.grm_cuda.apply_query_backward_queries(dh, mem, q.detach())
+    assert torch.equal(gq_only, gq_full)
+    out = cuda_ops.cuda_apply_query(mem, q)
+    (gq_auto,) = torch.autograd.grad(out, (q,), dh)
+    assert torch.equal(gq_auto, gq_full)

@@ -31,14 +31,14 @@ def t(name, dev):
     return torch.from_numpy(FIX[name]).to(dev)
 
 
-# CPU: float32 ops in the reference's order up to GEMM blocking.  GPU: the
-# MFMA scan and library GEMMs sum in other orders (float32 archives: 1e-4).
-# Through a float16 archive a state element on a float16 rounding boundary can
-# round the other way on the GPU (one float16 step, 2^-11 relative), and the
-# LayerNorm after retrieval scales that by 1/std of its input: the bar there is
-# 2e-3 / 5e-4, still far below what a wrong window, segment order or fusion
-# rule produces (differences of order 0.1).
-TOL = {("cpu", "16"): (2e-5, 2e-6), ("cpu", "32"): (2e-5, 2e-6),
+# CPU: float32 ops of this repository's chunked closed form, which sums in
+# another order than the reference's fallback.  GPU: the MFMA scan and library
+# GEMMs sum in other orders again (float32 archives: 1e-4).  Through a float16
+# archive a state element on a float16 rounding boundary can round the other way
+# (one float16 step, 2^-11 relative), and the LayerNorm after retrieval scales
+# that by 1/std of its input: the bar there is 2e-3 / 5e-4, still far below what
+# a wrong window, segment order or fusion rule produces (differences of order 0.1).
+TOL = {("cpu", "16"): (2e-3, 5e-4), ("cpu", "32"): (2e-5, 2e-6),
        ("cuda", "16"): (2e-3, 5e-4), ("cuda", "32"): (1e-4, 3e-5)}
 
 
@@ -77,7 +77,9 @@ def case_a(dev, tag):
     rtol, atol = TOL[(dev.type, tag)]
     np.testing.assert_allclose(ck_in, FIX[p + "L1_arch_ckpt_in"], rtol=rtol, atol=atol)  # layer 0's outputs
     if tag == "16":
-        steps = 1 if dev.type == "cpu" else 2
+        # archived float16 entries: one rounding step for the state's own sum order,
+        # one more for the layer input that the other sum order moved
+        steps = 2
         for ours, name in ((mem, "L1_arch_mem"), (summ, "L1_arch_sum"), (m0, "L1_arch_ckpt_m0")):
             within_f16_steps(ours, FIX[p + name], steps)
     else:
@@ -128,7 +130,7 @@ def test_models_match_reference_cpu(case, tag):
 def test_models_match_reference_gpu(case, tag, dev):
     from rnn_with_grm_amd import cuda_ops
 
-    ext = cuda_ops._EXTENSION_MODULE
+    ext = cuda_ops.extension_module()
     before = ext.hip_launch_count()
     print(f"model parity {case.__name__} float{tag} archive on {dev}", flush=True)
     case(dev, tag)
@@ -156,9 +158,9 @@ def test_models_16bit_track_float32(dtype, dev):
 
     from rnn_with_grm_amd import cuda_ops
 
-    before = cuda_ops._EXTENSION_MODULE.hip_launch_count()
+    before = cuda_ops.extension_module().hip_launch_count()
     low, ref = run(dtype), run(torch.float32)
-    assert cuda_ops._EXTENSION_MODULE.hip_launch_count() > before
+    assert cuda_ops.extension_module().hip_launch_count() > before
     for a, r in zip(low, ref):
         rel = float((a - r).norm() / r.norm())
         assert rel < 3e-2, rel
@@ -234,10 +236,10 @@ def test_linear_memory_cell_matches_reference():
 def test_linear_memory_cell_matches_reference_gpu(dev):
     from rnn_with_grm_amd import cuda_ops
 
-    before = cuda_ops._EXTENSION_MODULE.hip_launch_count()
+    before = cuda_ops.extension_module().hip_launch_count()
     print(f"linear memory cell on {dev}", flush=True)
     cell_case(dev)
-    assert cuda_ops._EXTENSION_MODULE.hip_launch_count() > before
+    assert cuda_ops.extension_module().hip_launch_count() > before
 
 
 @pytest.mark.parametrize("name", ["off5", "off0", "k2d", "mask", "all"])
