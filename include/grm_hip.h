@@ -206,7 +206,7 @@ int grm_hip_gather_apply(const void* memories, const int64_t* indices, const voi
  * Replaces the routing of SegmentRecurrentMemoryModel._route_chunk
  *   (reference grm/core/paper_grm.py:566-589) and TopKMemoryRetriever.forward
  *   (grm/core/gating_unit.py:54-91); the reference runs it as torch ops.
- * Limits: 1 <= top_k <= 32 when top_k < n_keys.
+ * Limits: 1 <= top_k <= 128 when top_k < n_keys (top_k > 32 runs a slower per-row list).
  */
 int grm_hip_topk_route(const void* queries, const void* keys, int64_t* topk_indices,
                        float* topk_scores, float* gates, int64_t batch, int64_t n_query,
@@ -227,7 +227,7 @@ int grm_hip_topk_route(const void* queries, const void* keys, int64_t* topk_indi
  * Outputs are [batch, n_query, top_k].
  * Replaces the per-segment routing calls of the reference's segment loop
  *   (grm/core/paper_grm.py:702-728 -> _route_chunk, :566-589) with one launch.
- * Limits: 1 <= top_k <= 32; base + (n_query - 1) / segment_len <= n_keys.
+ * Limits: 1 <= top_k <= 128; base + (n_query - 1) / segment_len <= n_keys.
  */
 int grm_hip_segment_route(const void* queries, const void* keys, int64_t* topk_indices,
                           float* topk_scores, float* gates, int64_t batch, int64_t n_query,

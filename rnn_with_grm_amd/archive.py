@@ -218,9 +218,14 @@ class DeviceSegmentArchive(nn.Module):
         return ring.summaries.index_select(1, ring.order(ring.summaries.device)).to(device=device, dtype=target)
 
     def slots(self, topk_indices: Tensor, batch_size: int) -> Tensor:
-        """Deque positions (0 = oldest kept) -> ring slots, for reading the ring in place."""
+        """Deque positions (0 = oldest kept) -> ring slots, for reading the ring in place.
+        A position outside [0, len) (such as the -1 of an empty routing slot) stays
+        invalid (-1): the gather kernels then write a zero row and count it, instead of
+        reading whatever state the ring holds in that slot."""
         ring = self._groups[batch_size]
-        return (topk_indices.to(torch.long) + ring.start()) % ring.capacity
+        pos = topk_indices.to(torch.long)
+        valid = (pos >= 0) & (pos < len(ring))
+        return torch.where(valid, (pos + ring.start()) % ring.capacity, torch.full_like(pos, -1))
 
     def _empty_retrieval(self, topk_indices: Tensor, device, last: tuple) -> Tensor:
         lead = (topk_indices.size(0),) + ((topk_indices.size(1),) if topk_indices.ndim == 3 else ())

@@ -303,7 +303,7 @@ void check_segment_route(const Tensor& queries, const Tensor& keys, int64_t top_
   TORCH_CHECK(queries.dim() == 3 && keys.dim() == 3, "segment_route: queries [B, Q, D], keys [B, S, D]");
   TORCH_CHECK(queries.size(0) == keys.size(0) && queries.size(2) == keys.size(2),
               "segment_route: batch/dim mismatch");
-  TORCH_CHECK(top_k >= 1 && top_k <= 32, "segment_route: top_k must be in [1, 32]");
+  TORCH_CHECK(top_k >= 1 && top_k <= 128, "segment_route: top_k must be in [1, 128]");
   TORCH_CHECK(segment_len >= 1 && base >= 0 && capacity >= 1,
               "segment_route: segment_len >= 1, base >= 0 and capacity >= 1 required");
   TORCH_CHECK(temperature > 0, "segment_route: temperature must be > 0");
@@ -666,33 +666,41 @@ std::tuple<Tensor, Tensor, Tensor> segment_scan_forward_hip(const Tensor& keys, 
   return {hidden, memory_out, snaps};
 }
 
+// Queries and keys in one arithmetic type on their device: a mixed or unsupported
+// pair is widened to float32 there (bf16 and f16 values are exact in float32, and
+// the score is a float32 FMA chain either way).  Routing never leaves the GPU.
+std::pair<Tensor, Tensor> route_operands(const char* what, const Tensor& queries, const Tensor& keys) {
+  TORCH_CHECK(queries.is_cuda() && keys.is_cuda() && queries.device() == keys.device(),
+              what, ": queries and keys must be on the same GPU");
+  Tensor q = queries, kk = keys;
+  if (q.scalar_type() != kk.scalar_type() || dtype_code(q.scalar_type()) < 0) {
+    q = q.to(at::kFloat);
+    kk = kk.to(at::kFloat);
+  }
+  return {q.contiguous(), kk.contiguous()};
+}
+
 std::tuple<Tensor, Tensor, Tensor> topk_route_hip(const Tensor& queries, const Tensor& keys,
                                                   int64_t top_k, double scale, double temperature) {
-  const int dt = dtype_code(queries.scalar_type());
-  if (!same_cuda_device({&queries, &keys}) || dt < 0 || keys.scalar_type() != queries.scalar_type() ||
-      std::min(top_k, keys.dim() == 3 ? keys.size(1) : 0) > 32) {
-    if (queries.is_cuda()) g_generic_calls.fetch_add(1);
-    auto r = topk_route_cpu(queries.cpu(), keys.cpu(), top_k, scale, temperature);
-    return {std::get<0>(r).to(queries.device()), std::get<1>(r).to(queries.device()),
-            std::get<2>(r).to(queries.device())};
-  }
   TORCH_CHECK(queries.dim() == 3 && keys.dim() == 3, "topk_route: queries [B, Q, D], keys [B, S, D]");
   TORCH_CHECK(queries.size(0) == keys.size(0) && queries.size(2) == keys.size(2),
               "topk_route: batch/dim mismatch");
   TORCH_CHECK(top_k >= 1, "topk_route: top_k must be >= 1");
   TORCH_CHECK(temperature > 0, "topk_route: temperature must be > 0");
+  const int64_t k = std::min(top_k, keys.size(1));
+  TORCH_CHECK(k == keys.size(1) || k <= 128, "topk_route: top_k beyond 128 (and below n_keys) is not routed "
+              "on the GPU");
   c10::OptionalDeviceGuard guard(queries.device());
-  Tensor q = queries.contiguous(), kk = keys.contiguous();
+  auto [q, kk] = route_operands("topk_route", queries, keys);
   const int64_t B = q.size(0), Q = q.size(1), S = kk.size(1), D = q.size(2);
-  const int64_t k = std::min(top_k, S);
   Tensor idx = at::empty({B, Q, k}, q.options().dtype(at::kLong));
   Tensor sc = at::empty({B, Q, k}, q.options().dtype(at::kFloat));
   Tensor gt = at::empty({B, Q, k}, q.options().dtype(at::kFloat));
   if (k > 0 && Q > 0 && B > 0) {
     check_rc(grm_hip_topk_route(q.data_ptr(), kk.data_ptr(), idx.data_ptr<int64_t>(),
-                                sc.data_ptr<float>(), gt.data_ptr<float>(), B, Q, S, D, dt, top_k,
-                                static_cast<float>(scale), static_cast<float>(temperature),
-                                current_stream(q)),
+                                sc.data_ptr<float>(), gt.data_ptr<float>(), B, Q, S, D,
+                                dtype_code(q.scalar_type()), top_k, static_cast<float>(scale),
+                                static_cast<float>(temperature), current_stream(q)),
              "topk_route");
   }
   return {gt, idx, sc};
@@ -702,24 +710,18 @@ std::tuple<Tensor, Tensor, Tensor> segment_route_hip(const Tensor& queries, cons
                                                      int64_t segment_len, int64_t base, int64_t capacity,
                                                      double scale, double temperature) {
   check_segment_route(queries, keys, top_k, segment_len, base, capacity, temperature);
-  const int dt = dtype_code(queries.scalar_type());
-  if (!same_cuda_device({&queries, &keys}) || dt < 0 || keys.scalar_type() != queries.scalar_type()) {
-    if (queries.is_cuda()) g_generic_calls.fetch_add(1);
-    auto r = segment_route_cpu(queries.cpu(), keys.cpu(), top_k, segment_len, base, capacity, scale, temperature);
-    return {std::get<0>(r).to(queries.device()), std::get<1>(r).to(queries.device()),
-            std::get<2>(r).to(queries.device())};
-  }
   c10::OptionalDeviceGuard guard(queries.device());
-  Tensor q = queries.contiguous(), kk = keys.contiguous();
+  auto [q, kk] = route_operands("segment_route", queries, keys);
   const int64_t B = q.size(0), Q = q.size(1), S = kk.size(1), D = q.size(2);
   Tensor idx = at::empty({B, Q, top_k}, q.options().dtype(at::kLong));
   Tensor sc = at::empty({B, Q, top_k}, q.options().dtype(at::kFloat));
   Tensor gt = at::empty({B, Q, top_k}, q.options().dtype(at::kFloat));
   if (Q > 0 && B > 0) {
     check_rc(grm_hip_segment_route(q.data_ptr(), S > 0 ? kk.data_ptr() : nullptr, idx.data_ptr<int64_t>(),
-                                   sc.data_ptr<float>(), gt.data_ptr<float>(), B, Q, S, D, dt, top_k,
-                                   segment_len, base, capacity, static_cast<float>(scale),
-                                   static_cast<float>(temperature), current_stream(q)),
+                                   sc.data_ptr<float>(), gt.data_ptr<float>(), B, Q, S, D,
+                                   dtype_code(q.scalar_type()), top_k, segment_len, base, capacity,
+                                   static_cast<float>(scale), static_cast<float>(temperature),
+                                   current_stream(q)),
              "segment_route");
   }
   return {gt, idx, sc};

@@ -32,6 +32,7 @@ namespace grmhip {
 namespace {
 
 constexpr int RT = 256;  // threads (= query rows) per routing workgroup
+constexpr int kRouteMaxK = 128;  // largest top_k routed on the GPU
 constexpr int SC = 32;   // keys per LDS tile
 constexpr int DT = 128;  // key dims per LDS tile
 
@@ -268,8 +269,12 @@ int launch_route(const RouteArgs& a, int64_t batch, hipStream_t s) {
     hipLaunchKernelGGL((route_kernel<E, 8>), grid, dim3(RT), 0, s, a);
   } else if (km <= 16) {
     hipLaunchKernelGGL((route_kernel<E, 16>), grid, dim3(RT), 0, s, a);
-  } else {
+  } else if (km <= 32) {
     hipLaunchKernelGGL((route_kernel<E, 32>), grid, dim3(RT), 0, s, a);
+  } else if (km <= 64) {  // lists past 32 entries: correct, not fast (registers spill)
+    hipLaunchKernelGGL((route_kernel<E, 64>), grid, dim3(RT), 0, s, a);
+  } else {
+    hipLaunchKernelGGL((route_kernel<E, kRouteMaxK>), grid, dim3(RT), 0, s, a);
   }
   return check_launch("topk_route");
 }
@@ -1130,8 +1135,8 @@ extern "C" int grm_hip_topk_route(const void* queries, const void* keys, int64_t
   }
   const int64_t k = top_k < n_keys ? top_k : n_keys;
   const bool natural = k == n_keys;
-  if (!natural && k > 32) {
-    set_error("topk_route: top_k %lld > 32", (long long)k);
+  if (!natural && k > kRouteMaxK) {
+    set_error("topk_route: top_k %lld > %d", (long long)k, kRouteMaxK);
     return GRM_HIP_EUNSUPPORTED;
   }
   if (batch == 0 || n_query == 0 || k == 0) return GRM_HIP_OK;
@@ -1179,9 +1184,10 @@ extern "C" int grm_hip_segment_route(const void* queries, const void* keys, int6
                                      int64_t n_keys, int64_t dim, int dtype, int64_t top_k,
                                      int64_t segment_len, int64_t base, int64_t capacity, float scale,
                                      float temperature, void* stream) {
-  if (batch < 0 || n_query < 0 || n_keys < 0 || dim < 0 || top_k < 1 || top_k > 32 || segment_len < 1 ||
+  if (batch < 0 || n_query < 0 || n_keys < 0 || dim < 0 || top_k < 1 || top_k > kRouteMaxK || segment_len < 1 ||
       base < 0 || capacity < 1) {
-    set_error("segment_route: bad sizes (1 <= top_k <= 32, segment_len >= 1, base >= 0, capacity >= 1)");
+    set_error("segment_route: bad sizes (1 <= top_k <= %d, segment_len >= 1, base >= 0, capacity >= 1)",
+              kRouteMaxK);
     return GRM_HIP_EINVAL;
   }
   if (dtype < GRM_HIP_F32 || dtype > GRM_HIP_BF16) {

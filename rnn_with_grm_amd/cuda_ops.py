@@ -249,8 +249,10 @@ def _torch_batched_gather(memories_per_batch: Tensor, topk_indices: Tensor) -> T
         raise ValueError(f"Expected memories_per_batch rank 4, got {memories_per_batch.ndim}")
     if topk_indices.ndim not in (2, 3):
         raise ValueError(f"Expected topk_indices rank 2 or 3, got {topk_indices.ndim}")
-    B = memories_per_batch.size(0)
+    B, S = memories_per_batch.shape[:2]
     flat = topk_indices.reshape(B, -1).long()
+    if flat.numel() and bool(((flat < 0) | (flat >= S)).any()):
+        raise IndexError("index out of range in self")  # what index_select raises there
     rows = torch.arange(B, device=memories_per_batch.device).view(B, 1).expand_as(flat)
     picked = memories_per_batch[rows, flat]
     return picked.reshape(B, *topk_indices.shape[1:], *memories_per_batch.shape[2:]).contiguous()

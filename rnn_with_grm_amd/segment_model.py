@@ -524,9 +524,10 @@ class SegmentRecurrentMemoryModel(nn.Module):
         idx0 = idx.clamp(min=0)
         if grad:
             # Differentiable gates: the selected scores again, as torch ops.
-            sel = torch.gather(k_r.unsqueeze(1).expand(B, T, -1, -1), 2,
-                               idx0.unsqueeze(-1).expand(-1, -1, -1, k_r.size(-1)))
-            scores = (q_r.unsqueeze(2) * sel).sum(-1) * gu.scale
+            # Indexing k_r directly keeps the backward at [B, S, D] (a gather from an
+            # expanded [B, T, S, D] view would scatter into a dense tensor of that size).
+            rows = torch.arange(B, device=idx0.device).view(B, 1, 1)
+            scores = (q_r.unsqueeze(2) * k_r[rows, idx0]).sum(-1) * gu.scale
             scores = scores.masked_fill(~filled, float("-inf"))
             gates = torch.softmax(scores.float() / gu.temperature, dim=-1).masked_fill(~filled, 0.0)
         gates = gu.dropout(gates)

@@ -169,3 +169,29 @@ def test_archive_on_device_matches_restatement():
     want = ref.applied(x, idx, cell)
     torch.testing.assert_close(got.cpu(), want, rtol=1e-4, atol=1e-5)
     assert torch.equal(arch.retrieve_memories(idx.to(dev), None, None, dev, 0.97).cpu(), ref.memories(idx))
+
+
+def test_invalid_positions_stay_invalid():
+    """A position outside the kept deque (the -1 of an empty routing slot, or one past the
+    end) is not remapped onto a ring slot: on the CPU the gather raises, as index_select
+    does in the reference's CPU path."""
+    arch = DeviceSegmentArchive(8, 4, 6, 3, torch.float32)
+    g = torch.Generator().manual_seed(9)
+    arch.push_segments(torch.randn(2, 5, 8, 4, generator=g), torch.randn(2, 5, 6, generator=g))
+    slots = arch.slots(torch.tensor([[0, 2, -1, 3]]), 2)
+    assert slots[0, 2] == -1 and slots[0, 3] == -1 and bool((slots[0, :2] >= 0).all())
+    with pytest.raises((IndexError, RuntimeError)):
+        arch.retrieve_memories(torch.tensor([[0, -1], [1, 2]]), None, None, torch.device("cpu"), 0.97)
+
+
+@pytest.mark.gpu
+def test_invalid_positions_read_zero_on_device():
+    """On the GPU the gather writes a zero row for an invalid position (and counts it)."""
+    dev = torch.device("cuda:0")
+    arch = DeviceSegmentArchive(8, 4, 6, 3, torch.float32).to(dev)
+    g = torch.Generator().manual_seed(9)
+    mems = torch.randn(2, 5, 8, 4, generator=g)
+    arch.push_segments(mems.to(dev), torch.randn(2, 5, 6, generator=g).to(dev))
+    got = arch.retrieve_memories(torch.tensor([[0, -1], [2, 3]], device=dev), None, None, dev, 0.97).cpu()
+    assert torch.count_nonzero(got[0, 1]) == 0 and torch.count_nonzero(got[1, 1]) == 0
+    assert torch.equal(got[0, 0], mems[0, 2]) and torch.equal(got[1, 0], mems[1, 4])

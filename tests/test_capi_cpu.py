@@ -88,12 +88,12 @@ def test_other_entry_points_reject():
     assert lib.grm_hip_apply_query_fwd(fake, fake, fake, -2, 1, 1, 1, 4, 0, None) == capi.EINVAL
     assert lib.grm_hip_topk_route(fake, fake, fake, fake, fake, 1, 1, 4, 4, 0, 0, 1.0, 1.0, None) == capi.EINVAL
     assert lib.grm_hip_topk_route(fake, fake, fake, fake, fake, 1, 1, 4, 4, 0, 2, 1.0, 0.0, None) == capi.EINVAL
-    assert lib.grm_hip_topk_route(fake, fake, fake, fake, fake, 1, 1, 100, 4, 0, 40, 1.0, 1.0,
+    assert lib.grm_hip_topk_route(fake, fake, fake, fake, fake, 1, 1, 1000, 4, 0, 200, 1.0, 1.0,
                                   None) == capi.EUNSUPPORTED
     assert lib.grm_hip_segment_route(fake, fake, fake, fake, fake, 1, 10, 2, 4, 0, 2, 3, 0, 8, 1.0, 1.0,
                                      None) == capi.EINVAL  # window past the keys
-    assert lib.grm_hip_segment_route(fake, fake, fake, fake, fake, 1, 10, 4, 4, 0, 40, 3, 0, 8, 1.0, 1.0,
-                                     None) == capi.EINVAL  # top_k > 32
+    assert lib.grm_hip_segment_route(fake, fake, fake, fake, fake, 1, 10, 4, 4, 0, 200, 3, 0, 8, 1.0, 1.0,
+                                     None) == capi.EINVAL  # top_k > 128
     assert lib.grm_hip_segment_route(fake, fake, fake, fake, fake, 1, 10, 4, 4, 0, 2, 0, 0, 8, 1.0, 1.0,
                                      None) == capi.EINVAL  # segment_len 0
     assert lib.grm_hip_fuse_residual(fake, fake, fake, None, None, fake, 1, 1, 4096, 0, 1e-5,

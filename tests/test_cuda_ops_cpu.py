@@ -193,7 +193,7 @@ def test_cpu_segment_route_rejects():
     with pytest.raises(RuntimeError, match="window ends past"):
         torch.ops.grm_cuda.segment_route(q, torch.zeros(1, 2, 4), 2, 3, 0, 8, 1.0, 1.0)
     with pytest.raises(RuntimeError, match="top_k must be in"):
-        torch.ops.grm_cuda.segment_route(q, torch.zeros(1, 4, 4), 33, 3, 0, 8, 1.0, 1.0)
+        torch.ops.grm_cuda.segment_route(q, torch.zeros(1, 4, 4), 129, 3, 0, 8, 1.0, 1.0)
 
 
 def test_cpu_fuse_residual():

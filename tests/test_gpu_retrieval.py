@@ -492,3 +492,38 @@ def test_apply_query_backward_queries_only(dev, dtype, shape):
     out = cuda_ops.cuda_apply_query(mem, q)
     (gq_auto,) = torch.autograd.grad(out, (q,), dh)
     assert torch.equal(gq_auto, gq_full)
+
+
+@pytest.mark.parametrize("k,S", [(40, 300), (100, 257), (128, 2000)])
+def test_topk_route_wide_k(dev, k, S):
+    """top_k beyond 32 (up to 128) is routed on the GPU, bit-exact; both entry points."""
+    g = torch.Generator().manual_seed(k + S)
+    q = norm(torch.randn(2, 90, 64, generator=g)).to(torch.bfloat16)
+    keys = norm(torch.randn(2, S, 64, generator=g)).to(torch.bfloat16)
+    scale = 0.125
+    gates, idx, sc = capi.topk_route(q.to(dev), keys.to(dev), k, scale)
+    og, oi, osc = orc.topk_route(q.float().numpy(), keys.float().numpy(), k, scale)
+    assert np.array_equal(idx.cpu().numpy(), oi) and np.array_equal(sc.cpu().numpy(), osc)
+    np.testing.assert_allclose(gates.cpu().numpy(), og, rtol=1e-5, atol=1e-6)
+    seg = 30
+    gates, idx, sc = capi.segment_route(q.to(dev), keys.to(dev), k, seg, S - 3, S, scale)
+    og, oi, osc = orc.segment_route(q.float().numpy(), keys.float().numpy(), k, seg, S - 3, S, scale)
+    assert np.array_equal(idx.cpu().numpy(), oi) and np.array_equal(sc.cpu().numpy(), osc)
+
+
+def test_routing_mixed_dtypes_stays_on_device(dev):
+    """float32 queries against bf16 keys: both widened to float32 on the GPU (the values are
+    exact), no host round trip; bit-exact against the oracle."""
+    g = torch.Generator().manual_seed(77)
+    q = norm(torch.randn(2, 50, 32, generator=g))
+    keys = norm(torch.randn(2, 70, 32, generator=g)).to(torch.bfloat16)
+    ext = cuda_ops.extension_module()
+    before = ext.generic_path_calls()
+    gates, idx, sc = torch.ops.grm_cuda.topk_route(q.to(dev), keys.to(dev), 8, 0.25, 1.0)
+    g2, i2, s2 = torch.ops.grm_cuda.segment_route(q.to(dev), keys.to(dev), 8, 5, 60, 40, 0.25, 1.0)
+    torch.cuda.synchronize()
+    assert ext.generic_path_calls() == before
+    og, oi, osc = orc.topk_route(q.numpy(), keys.float().numpy(), 8, 0.25)
+    assert np.array_equal(idx.cpu().numpy(), oi) and np.array_equal(sc.cpu().numpy(), osc)
+    og, oi, osc = orc.segment_route(q.numpy(), keys.float().numpy(), 8, 5, 60, 40, 0.25)
+    assert np.array_equal(i2.cpu().numpy(), oi) and np.array_equal(s2.cpu().numpy(), osc)

@@ -345,3 +345,40 @@ def test_training_gradients_match_reference_cpu():
 def test_training_gradients_match_reference_gpu(dev):
     print(f"training gradients case G on {dev}", flush=True)
     case_g(dev)
+
+
+def _wide_topk_model():
+    torch.manual_seed(3)
+    return sm.SegmentRecurrentMemoryModel(16, 24, 8, segment_length=4, memory_capacity_segments=64,
+                                          retrieval_top_k=40, memory_key_dim=8, dropout=0.0,
+                                          recomputation_ratio=0.0)
+
+
+def test_model_top_k_beyond_32_cpu():
+    """retrieval_top_k = 40 with more than 40 archived segments: the whole-sequence model
+    routes every segment (no error), and matches the same model on the PyTorch fallbacks."""
+    model = _wide_topk_model().eval()
+    x = torch.randn(2, 400, 16, generator=torch.Generator().manual_seed(4))
+    with torch.no_grad():
+        out, h, c, _ = model(x, reset_memory=True)
+        model.cuda_cpp_debug_fallback = True
+        ref, hr, cr, _ = model(x, reset_memory=True)
+    torch.testing.assert_close(out, ref, rtol=1e-4, atol=1e-5)
+    torch.testing.assert_close(c, cr, rtol=1e-4, atol=1e-5)
+
+
+@pytest.mark.gpu
+def test_model_top_k_beyond_32_gpu(dev):
+    """The same on the GPU: routing with 40 of up to 64 segments per row runs on the device."""
+    from rnn_with_grm_amd import cuda_ops
+
+    model = _wide_topk_model().eval()
+    x = torch.randn(2, 400, 16, generator=torch.Generator().manual_seed(4))
+    with torch.no_grad():
+        ref, _, cr, _ = model(x, reset_memory=True)
+        gpu = model.to(dev)
+        generic = cuda_ops.extension_module().generic_path_calls()
+        out, _, c, _ = gpu(x.to(dev), reset_memory=True)
+        assert cuda_ops.extension_module().generic_path_calls() == generic
+    torch.testing.assert_close(out.cpu(), ref, rtol=1e-4, atol=3e-5)
+    torch.testing.assert_close(c.cpu(), cr, rtol=1e-4, atol=3e-5)
