@@ -298,8 +298,13 @@ int launch_bwd(const BwdArgs& a, void* grad_keys, void* grad_queries, hipStream_
 //   dV = P^T dH + c decay^{L-1-j} K G^T
 //   G  <- decay^L G + dH^T diag(decay^{i+1}) Q      (the adjoint at the chunk's start)
 // One workgroup of 4 waves per (sequence, 32-column value tile) walks the
-// chunks from the last.  The tile's G lives in fp32 MFMA accumulators, with a
-// 16-bit copy in LDS for the products that read it.  dQ and dK sum over every
+// chunks from the last.  The tile's G lives in fp32 MFMA accumulators.  The
+// fp32 operands of the products (G, the chunk's starting state M and the
+// decay-weighted dH of the adjoint update) enter the MFMAs as hi + lo pairs of
+// 16-bit values (hi = x rounded, lo = x - hi rounded), two MFMAs per product,
+// so each carries ~16 (bf16) or ~22 (f16) significant bits instead of 8 / 11:
+// rounding them to one 16-bit value costs bf16 inputs ~1e-3 absolute error on
+// grad_memory over a few hundred tokens.  dQ and dK sum over every
 // value column, so each tile writes a partial and tile_sum_kernel adds the
 // tiles in order: deterministic, no atomics.  Wave w owns query/key block w
 // (tokens [16w, +16)) of every product and G rows [16 (w & 1), +16) x key
@@ -342,7 +347,7 @@ struct BmShape {
   static constexpr int K_UNITS = BCT * KU / MB_NT;
   static constexpr int M_UNITS = MB_DV * KU / MB_NT;
   static constexpr size_t lds_bytes =
-      static_cast<size_t>(2 * BCT * KS + 2 * BCT * VS + 3 * MB_DV * KS + 2 * BCT * PS) * 2 + (BCT + 1) * 4;
+      static_cast<size_t>(2 * BCT * KS + 2 * BCT * VS + 6 * MB_DV * KS + 2 * BCT * PS) * 2 + (BCT + 1) * 4;
   static_assert(K_UNITS * MB_NT == BCT * KU && M_UNITS * MB_NT == MB_DV * KU, "tiles split evenly");
 };
 
@@ -364,6 +369,17 @@ __device__ __forceinline__ Frag8<E> bw_frag_tr(const typename ET<E>::raw* p_lo, 
   return f;
 }
 
+// Four fp32 values as hi + lo 16-bit pairs: hi rounded as from_f, lo the
+// rounded remainder.
+template <class E>
+__device__ __forceinline__ void store4_split(typename ET<E>::raw* hi, typename ET<E>::raw* lo, f32x4 v) {
+  f32x4 r;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) r[i] = v[i] - ET<E>::to_f(ET<E>::from_f(v[i]));
+  store4_raw<E>(hi, v);
+  store4_raw<E>(lo, r);
+}
+
 template <class E, int DKP>
 __global__ __launch_bounds__(MB_NT, 1) void chunk_bwd_mfma_kernel(const BwdMArgs a) {
   using S = BmShape<DKP>;
@@ -379,9 +395,11 @@ __global__ __launch_bounds__(MB_NT, 1) void chunk_bwd_mfma_kernel(const BwdMArgs
   raw* Qs = Ks + BCT * KS;                  // [BCT][KS]
   raw* Vs = Qs + BCT * KS;                  // [BCT][VS] value tile columns
   raw* Hs = Vs + BCT * VS;                  // [BCT][VS] grad_hidden tile columns
-  raw* Ms = Hs + BCT * VS;                  // [MB_DV][KS] the chunk's starting state, 16-bit
-  raw* Gs = Ms + MB_DV * KS;                // 2 x [MB_DV][KS] adjoint at the chunk's end, 16-bit
-  raw* Ps = Gs + 2 * MB_DV * KS;            // [BCT][PS] P
+  raw* Ms = Hs + BCT * VS;                  // [MB_DV][KS] the chunk's starting state, hi
+  raw* Ml = Ms + MB_DV * KS;                // [MB_DV][KS] ... lo
+  raw* Gs = Ml + MB_DV * KS;                // 2 x [MB_DV][KS] adjoint at the chunk's end, hi
+  raw* Gl = Gs + 2 * MB_DV * KS;            // 2 x [MB_DV][KS] ... lo
+  raw* Ps = Gl + 2 * MB_DV * KS;            // [BCT][PS] P
   raw* Ds = Ps + BCT * PS;                  // [BCT][PS] dS
   float* pw = reinterpret_cast<float*>(Ds + BCT * PS);
 
@@ -438,9 +456,9 @@ __global__ __launch_bounds__(MB_NT, 1) void chunk_bwd_mfma_kernel(const BwdMArgs
     }
   }
   auto publish_g = [&](int slot) {
-    raw* Gb = Gs + slot * MB_DV * KS;
+    const int base = slot * MB_DV * KS + (16 * gvb + n) * KS + 4 * g;
 #pragma unroll
-    for (int t = 0; t < GT; ++t) store4_raw<E>(Gb + (16 * gvb + n) * KS + 16 * (gk0 + t) + 4 * g, gacc[t]);
+    for (int t = 0; t < GT; ++t) store4_split<E>(Gs + base + 16 * (gk0 + t), Gl + base + 16 * (gk0 + t), gacc[t]);
   };
   publish_g(0);
   int gslot = 0;
@@ -526,17 +544,19 @@ __global__ __launch_bounds__(MB_NT, 1) void chunk_bwd_mfma_kernel(const BwdMArgs
     for (int u = 0; u < S::M_UNITS; ++u) {
       const int l = tid + MB_NT * u;
       const int row = l / KU, col = 8 * (l % KU);
-      U8<E> val;
       if (src32) {
+        f32x4 x0, x1;
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-          val.e[i] = ET<E>::from_f(__uint_as_float(sg.m[u][0][i]));
-          val.e[4 + i] = ET<E>::from_f(__uint_as_float(sg.m[u][1][i]));
+          x0[i] = __uint_as_float(sg.m[u][0][i]);
+          x1[i] = __uint_as_float(sg.m[u][1][i]);
         }
+        store4_split<E>(Ms + row * KS + col, Ml + row * KS + col, x0);
+        store4_split<E>(Ms + row * KS + col + 4, Ml + row * KS + col + 4, x1);
       } else {
-        val = __builtin_bit_cast(U8<E>, sg.m[u][0]);
+        *reinterpret_cast<U8<E>*>(Ms + row * KS + col) = __builtin_bit_cast(U8<E>, sg.m[u][0]);
+        *reinterpret_cast<uint4*>(Ml + row * KS + col) = make_uint4(0u, 0u, 0u, 0u);
       }
-      *reinterpret_cast<U8<E>*>(Ms + row * KS + col) = val;
     }
   };
 
@@ -576,6 +596,7 @@ __global__ __launch_bounds__(MB_NT, 1) void chunk_bwd_mfma_kernel(const BwdMArgs
     __syncthreads();  // P and dS complete
 
     const raw* Gb = Gs + gslot * MB_DV * KS;
+    const raw* Glb = Gl + gslot * MB_DV * KS;
     const int jrow = 16 * w + n;  // this lane's key / query row
     const float wl = (jrow < L) ? c * pw[max(L - 1 - jrow, 0)] : 0.f;
     // ---- dQ rows of block w: D[kcol][i] = decay^{i+1} sum_v M[v][kcol] dH[i][v] + sum_j K[j][kcol] dS[i][j]
@@ -589,9 +610,9 @@ __global__ __launch_bounds__(MB_NT, 1) void chunk_bwd_mfma_kernel(const BwdMArgs
         dsf[p] = lds_frag_4x2<E>(Ds + jrow * PS + 32 * p + 4 * g, Ds + jrow * PS + 32 * p + 4 * g + 16);
 #pragma unroll
       for (int kt = 0; kt < KT; ++kt) {
-        const raw* mb = Ms + (4 * g + (n >> 2)) * KS + 16 * kt + 4 * (n & 3);
-        const Frag8<E> mT = bw_frag_tr<E>(mb, mb + 16 * KS);
-        f32x4 acc = mfma8(mT, hq, f32x4{0.f, 0.f, 0.f, 0.f}) * sq;
+        const int mo = (4 * g + (n >> 2)) * KS + 16 * kt + 4 * (n & 3);
+        f32x4 acc = mfma8(bw_frag_tr<E>(Ms + mo, Ms + mo + 16 * KS), hq, f32x4{0.f, 0.f, 0.f, 0.f});
+        acc = mfma8(bw_frag_tr<E>(Ml + mo, Ml + mo + 16 * KS), hq, acc) * sq;
 #pragma unroll
         for (int p = 0; p < 2; ++p) {
           if (32 * p > 16 * w + 15) continue;
@@ -620,8 +641,9 @@ __global__ __launch_bounds__(MB_NT, 1) void chunk_bwd_mfma_kernel(const BwdMArgs
       const Frag8<E> vj = lds_frag_4x2<E>(Vs + jrow * VS + 4 * g, Vs + jrow * VS + 4 * g + 16);
 #pragma unroll
       for (int kt = 0; kt < KT; ++kt) {
-        const raw* gbt = Gb + (4 * g + (n >> 2)) * KS + 16 * kt + 4 * (n & 3);
-        f32x4 acc = mfma8(bw_frag_tr<E>(gbt, gbt + 16 * KS), vj, f32x4{0.f, 0.f, 0.f, 0.f}) * wl;
+        const int go = (4 * g + (n >> 2)) * KS + 16 * kt + 4 * (n & 3);
+        f32x4 acc = mfma8(bw_frag_tr<E>(Gb + go, Gb + go + 16 * KS), vj, f32x4{0.f, 0.f, 0.f, 0.f});
+        acc = mfma8(bw_frag_tr<E>(Glb + go, Glb + go + 16 * KS), vj, acc) * wl;
 #pragma unroll
         for (int p = 0; p < 2; ++p) {
           if (32 * p + 31 < 16 * w) continue;
@@ -643,8 +665,11 @@ __global__ __launch_bounds__(MB_NT, 1) void chunk_bwd_mfma_kernel(const BwdMArgs
       for (int vb = 0; vb < 2; ++vb) {
         f32x4 acc = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-        for (int kk = 0; kk < NKK; ++kk)
-          acc = mfma8(*reinterpret_cast<const Frag8<E>*>(Gb + (16 * vb + n) * KS + 32 * kk + 8 * g), kr[kk], acc);
+        for (int kk = 0; kk < NKK; ++kk) {
+          const int go = (16 * vb + n) * KS + 32 * kk + 8 * g;
+          acc = mfma8(*reinterpret_cast<const Frag8<E>*>(Gb + go), kr[kk], acc);
+          acc = mfma8(*reinterpret_cast<const Frag8<E>*>(Glb + go), kr[kk], acc);
+        }
         acc *= wl;
 #pragma unroll
         for (int p = 0; p < 2; ++p) {
@@ -657,13 +682,17 @@ __global__ __launch_bounds__(MB_NT, 1) void chunk_bwd_mfma_kernel(const BwdMArgs
     }
     // ---- the adjoint at the chunk's start: G = decay^L G + sum_i decay^{i+1} dH[i][v] Q[i][k]
     {
-      Frag8<E> hw[2];
+      Frag8<E> hw[2], hwl[2];
 #pragma unroll
       for (int p = 0; p < 2; ++p) {
         const raw* hb = Hs + (32 * p + 4 * g + (n >> 2)) * VS + 16 * gvb + 4 * (n & 3);
         const Frag8<E> h = bw_frag_tr<E>(hb, hb + 16 * VS);
 #pragma unroll
-        for (int s = 0; s < 8; ++s) hw[p].e[s] = ET<E>::from_f(ET<E>::to_f(h.e[s]) * gw[p][s]);
+        for (int s = 0; s < 8; ++s) {
+          const float x = ET<E>::to_f(h.e[s]) * gw[p][s];
+          hw[p].e[s] = ET<E>::from_f(x);
+          hwl[p].e[s] = ET<E>::from_f(x - ET<E>::to_f(hw[p].e[s]));
+        }
       }
       const float decay_L = pw[L];
 #pragma unroll
@@ -672,14 +701,16 @@ __global__ __launch_bounds__(MB_NT, 1) void chunk_bwd_mfma_kernel(const BwdMArgs
 #pragma unroll
         for (int p = 0; p < 2; ++p) {
           const raw* qb = Qs + (32 * p + 4 * g + (n >> 2)) * KS + 16 * (gk0 + t) + 4 * (n & 3);
-          acc = mfma8(bw_frag_tr<E>(qb, qb + 16 * KS), hw[p], acc);
+          const Frag8<E> qT = bw_frag_tr<E>(qb, qb + 16 * KS);
+          acc = mfma8(qT, hw[p], acc);
+          acc = mfma8(qT, hwl[p], acc);
         }
         gacc[t] = acc;
       }
       gslot ^= 1;
       publish_g(gslot);
     }
-    __syncthreads();  // every read of this chunk's tiles done; the new 16-bit G visible
+    __syncthreads();  // every read of this chunk's tiles done; the new hi/lo G visible
   }
 
   // grad_memory: the adjoint at the sequence's start.

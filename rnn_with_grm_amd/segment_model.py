@@ -549,6 +549,10 @@ class SegmentRecurrentMemoryModel(nn.Module):
             fused = (self.dropout if soup else self.aggregator.dropout)(fused.view(B, T, H))
         else:
             contribution = (retrieved * gates.unsqueeze(-1)).sum(dim=2)
+            if h_online.dtype != contribution.dtype:
+                # A 16-bit model: its fusion layers hold 16-bit parameters, so the float32
+                # retrieval enters them in the model's dtype.
+                contribution, retrieved, gates = (t.to(h_online.dtype) for t in (contribution, retrieved, gates))
             if soup:
                 fused = self.dropout(self.memory_soup_norm(h_online + contribution))
             else:

@@ -303,17 +303,10 @@ def test_chunk_backward(dev, dtype, mem_dtype, B, T, K, H):
             close(name, got, ref, torch.bfloat16)
 
 
-def close_scaled(name, got, ref, rel_l2, max_frac):
-    """|got - ref| against the scale of the whole tensor: relative L2 error and max error as a
-    fraction of max |ref|.  The MFMA backward rounds the chunk's starting state, the adjoint,
-    P and dS to the input's 16-bit type as MFMA operands, so its error scales with the tensor,
-    not with each element."""
-    got = got.float().cpu().double().numpy()
-    den = np.linalg.norm(ref)
-    rel = np.linalg.norm(got - ref) / den if den > 0 else np.linalg.norm(got)
-    assert rel < rel_l2, f"{name}: relative L2 error {rel:.3e}"
-    scale = np.abs(ref).max()
-    assert np.abs(got - ref).max() <= max_frac * max(scale, 1e-30), f"{name}: max error beyond {max_frac} x max|ref|"
+def close_elementwise(name, got, ref, rtol=2e-2, atol=2e-3):
+    """|got - ref| <= atol + rtol |ref| for every element (the bar of the 16-bit paths)."""
+    got = got.float().cpu().double().numpy() if torch.is_tensor(got) else got
+    np.testing.assert_allclose(got, ref, rtol=rtol, atol=atol, err_msg=name)
 
 
 @pytest.mark.parametrize("dtype,mem_dtype", [(torch.bfloat16, torch.float32), (torch.float16, torch.float32),
@@ -322,8 +315,9 @@ def close_scaled(name, got, ref, rel_l2, max_frac):
                                      (1, 7, 128, 32), (2, 200, 32, 64)])
 def test_mfma_backward(dev, monkeypatch, dtype, mem_dtype, B, T, K, H):
     """The chunk-parallel MFMA backward (16-bit inputs, value_dim a multiple of 32) against the
-    double-precision oracle and against the scalar per-token kernel (GRM_HIP_BWD_MFMA=0):
-    ragged last chunks, key widths below the padded 64/128, one to four value tiles, one chunk."""
+    double-precision oracle and against the scalar per-token kernel (GRM_HIP_BWD_MFMA=0),
+    element by element at rtol 2e-2 / atol 2e-3: ragged last chunks, key widths below the
+    padded 64/128, one to four value tiles, one chunk."""
     k, v, q, m = make_case(B, T, K, H, dtype, mem_dtype, seed=B * 13 + T)
     g = torch.Generator().manual_seed(7)
     dh = torch.randn(B, T, H, generator=g).to(dtype)
@@ -336,11 +330,10 @@ def test_mfma_backward(dev, monkeypatch, dtype, mem_dtype, B, T, K, H):
     torch.cuda.synchronize()
     ref = orc.chunk_update_bwd(dh.double().numpy(), dm.double().numpy(), k.double().numpy(), v.double().numpy(),
                                q.double().numpy(), m.double().numpy(), 0.97)
-    rel_l2 = 1e-2 if dtype == torch.bfloat16 or mem_dtype == torch.bfloat16 else 5e-3
     for name, x, y, r in zip(("grad_keys", "grad_values", "grad_queries", "grad_memory"), got, scalar, ref):
         assert torch.isfinite(x.float()).all(), name
-        close_scaled(name, x, r, rel_l2, 2e-2)
-        close_scaled(name + " vs scalar kernel", x, y.float().cpu().double().numpy(), rel_l2, 2e-2)
+        close_elementwise(name, x, r)
+        close_elementwise(name + " vs scalar kernel", x, y.float().cpu().double().numpy())
 
 
 def test_autograd_through_cuda_ops(dev):

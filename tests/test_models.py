@@ -382,3 +382,52 @@ def test_model_top_k_beyond_32_gpu(dev):
         assert cuda_ops.extension_module().generic_path_calls() == generic
     torch.testing.assert_close(out.cpu(), ref, rtol=1e-4, atol=3e-5)
     torch.testing.assert_close(c.cpu(), cr, rtol=1e-4, atol=3e-5)
+
+
+def _bf16_training_grads(dev, dtype):
+    """Parameter gradients of one training call of a 2-layer model whose hidden size (64)
+    is a multiple of 32 and key size (32) a multiple of 8: in bf16 the scan's backward is
+    the chunk-parallel MFMA kernel."""
+    torch.manual_seed(11)
+    model = sm.HierarchicalSegmentMemoryModel(
+        input_size=48, hidden_size=64, output_size=16, num_layers=2, segment_length=32, memory_capacity_segments=8,
+        retrieval_top_k=3, memory_key_dim=32, dropout=0.0, recomputation_ratio=0.0)
+    model = model.to(device=dev, dtype=dtype).train()
+    x = torch.randn(2, 320, 48, generator=torch.Generator().manual_seed(12)).to(dev, dtype)
+    out, _, _, _ = model(x)
+    out.float().square().mean().backward()
+    return {n: p.grad.float() for n, p in model.named_parameters() if p.grad is not None}
+
+
+@pytest.mark.gpu
+def test_training_gradients_bf16_mfma_backward(dev, monkeypatch):
+    """bf16 training through the MFMA scan backward: every parameter gradient against the
+    same bf16 model with the per-token float32 backward kernel (GRM_HIP_BWD_MFMA=0; the two
+    runs differ only in the scan's backward) and against the float32 model (which also
+    differs by bf16 rounding of every activation), as relative L2 error per parameter.  The
+    float32 bar is looser for the routing projections, whose gradients pass through a
+    softmax over bf16 scores (measured ~7e-2 on the CPU path) than for the memory cell's
+    projections, which the scan's backward feeds directly (~2e-2)."""
+    print(f"bf16 training gradients, MFMA backward, on {dev}", flush=True)
+    mfma = _bf16_training_grads(dev, torch.bfloat16)
+    monkeypatch.setenv("GRM_HIP_BWD_MFMA", "0")
+    scalar = _bf16_training_grads(dev, torch.bfloat16)
+    monkeypatch.delenv("GRM_HIP_BWD_MFMA")
+    ref = _bf16_training_grads(dev, torch.float32)
+    assert mfma.keys() == scalar.keys() == ref.keys() and len(mfma) > 10
+    worst_kernel, worst_f32, worst_cell = 0.0, 0.0, 0.0
+    for name, r in ref.items():
+        den = float(r.norm())
+        if den == 0.0:
+            assert float(mfma[name].norm()) == 0.0, name
+            continue
+        rel_kernel = float((mfma[name] - scalar[name]).norm()) / max(float(scalar[name].norm()), 1e-30)
+        rel_f32 = float((mfma[name] - r).norm()) / den
+        print(f"  {name}: vs per-token kernel {rel_kernel:.2e}, vs float32 {rel_f32:.2e}", flush=True)
+        worst_kernel, worst_f32 = max(worst_kernel, rel_kernel), max(worst_f32, rel_f32)
+        if "memory_cell" in name:
+            worst_cell = max(worst_cell, rel_f32)
+        assert torch.isfinite(mfma[name]).all(), name
+    assert worst_kernel < 1e-2, worst_kernel
+    assert worst_cell < 4e-2, worst_cell
+    assert worst_f32 < 1.5e-1, worst_f32
