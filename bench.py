@@ -114,6 +114,47 @@ def bench_c2(torch, dev, steps, warmup):
     return wall, per, (k, v, q, m, hidden, snaps)
 
 
+def bench_n1(torch, dev, steps, warmup):
+    """The north-star shape: B*H = 64 sequences (B=8, H=8) x T = 8192 tokens, d_k = d_v = 128,
+    chunk 64, bf16 q/k/v, fp32 state, the 128 per-chunk snapshots of every sequence written;
+    one grm_hip_chunk_update_fwd launch per step, events around back-to-back launches."""
+    from rnn_with_grm_amd import capi
+
+    lib = capi.load()
+    BH, T, D = 64, 8192, 128
+    k, v, q, m = [t.to(dev) for t in make_c2(dev, torch, BH=BH, T=T, D=D, seed=3)]
+    hidden = torch.empty((BH, T, D), dtype=torch.bfloat16, device=dev)
+    mem_out = torch.empty((BH, D, D), dtype=torch.float32, device=dev)
+    snaps = torch.empty((BH, T // 64, D, D), dtype=torch.float32, device=dev)
+    wsb = capi.fwd_workspace_bytes(BH, T, D, D, 64)
+    ws = torch.empty(max(wsb // 4, 1), dtype=torch.float32, device=dev)
+    stream = torch.cuda.current_stream(dev)
+    sp = ctypes.c_void_p(stream.cuda_stream)
+    P = lambda t: ctypes.c_void_p(t.data_ptr())  # noqa: E731
+    args = (P(k), P(v), P(q), P(m), P(hidden), P(mem_out), P(snaps), P(ws), wsb, BH, T, D, D, capi.BF16, capi.F32,
+            0.97, 64, sp)
+
+    def step():
+        rc = lib.grm_hip_chunk_update_fwd(*args)
+        if rc != 0:
+            raise RuntimeError(capi.last_error())
+
+    for _ in range(warmup):
+        step()
+    torch.cuda.synchronize()
+    ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    ev0.record(stream)
+    for _ in range(steps):
+        step()
+    ev1.record(stream)
+    torch.cuda.synchronize()
+    if not (bool(torch.isfinite(snaps[:, -1]).all()) and torch.equal(snaps[:, -1], mem_out)):
+        raise RuntimeError("north-star shape: last snapshot differs from the final state")
+    flops, bytes_ = c2_counts(BH=BH, T=T, dk=D, dv=D)
+    del k, v, q, m, hidden, snaps, ws
+    return {"us": ev0.elapsed_time(ev1) * 1e3 / steps, "tokens": BH * T, "flops": flops, "bytes": bytes_}
+
+
 def bench_c2_bwd(torch, dev, steps, warmup):
     """chunk_update_backward at config 2 through the C ABI: the forward recompute of the
     chunk states, the chunk-parallel MFMA backward and the tile sums, timed with events
@@ -235,6 +276,48 @@ def bench_c3(torch, dev, steps, warmup):
         "gather": {"ms": statistics.mean(g_per) * 1e3, "bytes": gather_bytes,
                    "fill_ms": statistics.mean(f_per) * 1e3, "fill_bytes": BH * Q * K * D * D * 4},
     }
+
+
+def bench_routes(torch, dev, steps, warmup):
+    """Routing alone (score + top-k + softmax through the C ABI): config 3 (64 sequences x 2048
+    queries over 256 keys, top-8) and config 5 (16 heads x 65536 queries over 512 keys, top-16),
+    the latter also with causal segment windows (128-token segments)."""
+    from rnn_with_grm_amd import capi
+
+    lib = capi.load()
+    nrm = torch.nn.functional.normalize
+    stream = torch.cuda.current_stream(dev)
+    sp = ctypes.c_void_p(stream.cuda_stream)
+    P = lambda t: ctypes.c_void_p(t.data_ptr())  # noqa: E731
+    out = {}
+    for name, (BH, Q, S, D, K) in (("c3", (64, 2048, 256, 128, 8)), ("c5", (16, 65536, 512, 128, 16))):
+        g = torch.Generator().manual_seed(1)
+        q = nrm(torch.randn(BH, Q, D, generator=g), dim=-1).to(torch.bfloat16).to(dev)
+        keys = nrm(torch.randn(BH, S, D, generator=g), dim=-1).to(torch.bfloat16).to(dev)
+        idx = torch.empty((BH, Q, K), dtype=torch.int64, device=dev)
+        sc = torch.empty((BH, Q, K), dtype=torch.float32, device=dev)
+        gt = torch.empty((BH, Q, K), dtype=torch.float32, device=dev)
+
+        def topk():
+            rc = lib.grm_hip_topk_route(P(q), P(keys), P(idx), P(sc), P(gt), BH, Q, S, D, capi.BF16, K,
+                                        1.0 / D ** 0.5, 1.0, sp)
+            if rc != 0:
+                raise RuntimeError(capi.last_error())
+
+        def causal():
+            rc = lib.grm_hip_segment_route(P(q), P(keys), P(idx), P(sc), P(gt), BH, Q, S, D, capi.BF16, K, 128, 0, S,
+                                           1.0 / D ** 0.5, 1.0, sp)
+            if rc != 0:
+                raise RuntimeError(capi.last_error())
+
+        runs = [(name + "_topk_route", topk)] + ([(name + "_causal_route", causal)] if name == "c5" else [])
+        for label, fn in runs:
+            _, per = timed_launches(torch, fn, max(3, steps), warmup, stream)
+            out[label] = {"us": round(statistics.mean(per) * 1e6, 1), "rows": BH * Q, "keys": S, "top_k": K,
+                          "bytes": q.numel() * 2 + keys.numel() * 2 + idx.numel() * 8 + 2 * sc.numel() * 4,
+                          "flops": 2 * BH * Q * S * D}
+        del q, keys, idx, sc, gt
+    return out
 
 
 def bench_published(torch, dev):
@@ -462,27 +545,111 @@ def bench_c4_model(torch, dev, steps, warmup):
     return {"ms": ms, "tokens": B * T}
 
 
-def cpu_baseline(torch, budget_s: float = 20.0):
-    """The torch-CPU port of the reference's CPU path on config 2 (full shape)."""
-    from oracle import torch_port
+def host_cpu_info():
+    """The host's CPU model, logical CPU count, the CPUs this process may run on and its
+    cgroup CPU quota; `usable` is the smallest of these, the thread count the CPU legs use."""
+    model = None
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    count = os.cpu_count() or 1
+    affinity = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else count
+    quota = None
+    try:
+        with open("/sys/fs/cgroup/cpu.max") as f:
+            q, period = f.read().split()[:2]
+            if q != "max":
+                quota = float(q) / float(period)
+    except (OSError, ValueError):
+        pass
+    usable = min(count, affinity, int(quota) if quota and quota >= 1 else count)
+    return {"cpu_model": model, "os_cpu_count": count, "affinity_cpus": affinity, "cgroup_cpu_quota": quota,
+            "usable": max(1, usable)}
 
-    threads = min(16, os.cpu_count() or 1)
-    torch.set_num_threads(threads)
-    k, v, q, m = make_c2(None, torch)
+
+def _median_seconds(fn, min_runs=5, budget_s=4.0):
+    """One warm-up call, then at least min_runs timed calls (more while within budget_s)."""
+    fn()
     times = []
     t_start = time.perf_counter()
-    while len(times) < 5 or (time.perf_counter() - t_start < budget_s and len(times) < 20):
+    while len(times) < min_runs or (time.perf_counter() - t_start < budget_s and len(times) < 20):
         t0 = time.perf_counter()
-        torch_port.segment_scan(k, v, q, m, 0.97, 64)
+        fn()
         times.append(time.perf_counter() - t0)
-        if time.perf_counter() - t_start > 3 * budget_s:
-            break
-    med = statistics.median(times)
-    return {"value": k.shape[0] * k.shape[1] / med, "unit": "tokens/s", "cores": threads, "kind": "port",
-            "sample": f"full config 2 (64 x 2048 tokens, d=128, fp32 math on bf16-rounded inputs), "
-                      f"one _vectorized_chunk_update per 64-token segment, median of {len(times)} runs, "
-                      f"{threads} threads",
-            "seconds_per_step": med}
+    return statistics.median(times), len(times)
+
+
+def cpu_baseline(torch):
+    """The torch-CPU port of the reference's CPU path on the host, at the usable core count
+    and at one thread: config 1 and config 2 at full shape, configs 3 and 5 on slices whose
+    time is scaled linearly to the full configuration (stated per leg)."""
+    from oracle import torch_port
+
+    host = host_cpu_info()
+    nrm = torch.nn.functional.normalize
+    g = torch.Generator().manual_seed(0)
+    # config 1: fp32, B*H = 8, T = 512, d = 64, chunk 64, zero initial state
+    k1 = nrm(torch.randn(8, 512, 64, generator=g), dim=-1)
+    v1 = torch.randn(8, 512, 64, generator=g)
+    q1 = nrm(torch.randn(8, 512, 64, generator=g), dim=-1)
+    m1 = torch.zeros(8, 64, 64)
+    k2, v2, q2, m2 = make_c2(None, torch)
+    # config 3 slice: one of the 64 (b, h) sequences, 256 of its 2048 queries (x 512 to the full batch)
+    q3 = nrm(torch.randn(1, 256, 128, generator=g), dim=-1).to(torch.bfloat16)
+    keys3 = nrm(torch.randn(1, 256, 128, generator=g), dim=-1).to(torch.bfloat16)
+    st3 = torch.randn(1, 256, 128, 128, generator=g) * 0.02
+    h3 = torch.randn(256, 128, generator=g)
+    # config 5 slices: the update over one head's first 4096 tokens (x 256 to 16 heads x 65536), and
+    # the retrieval of 256 tokens of one head over its 512 snapshots (x 4096)
+    k5 = nrm(torch.randn(1, 4096, 128, generator=g), dim=-1).to(torch.bfloat16)
+    v5 = torch.randn(1, 4096, 128, generator=g).to(torch.bfloat16)
+    q5 = nrm(torch.randn(1, 4096, 128, generator=g), dim=-1).to(torch.bfloat16)
+    m5 = torch.randn(1, 128, 128, generator=g) * 0.02
+    keys5 = nrm(torch.randn(1, 512, 128, generator=g), dim=-1).to(torch.bfloat16)
+    st5 = torch.randn(1, 512, 128, 128, generator=g) * 0.02
+    ln_w, ln_b = torch.ones(128), torch.zeros(128)
+
+    def retrieval(q, keys, states, h, top_k):
+        gates, idx, _ = torch_port.route(q, keys, top_k, 1.0 / 128 ** 0.5)
+        sel = torch_port.gather(states, idx)
+        r = torch_port.apply_query(sel, q.float())
+        return torch_port.fuse_residual(h, r[0], gates[0], ln_w, ln_b)
+
+    legs = [
+        ("c1", "full config 1 (fp32, 8 x 512 tokens, d=64, chunk 64)", 8 * 512, 1,
+         lambda: torch_port.segment_scan(k1, v1, q1, m1, 0.97, 64)),
+        ("c2", "full config 2 (64 x 2048 tokens, d=128, bf16 inputs, fp32 math)", 64 * 2048, 1,
+         lambda: torch_port.segment_scan(k2, v2, q2, m2, 0.97, 64)),
+        ("c3_retrieval", "config 3 slice: 256 queries of 1 of 64 sequences, route top-8 of 256, gather, apply, "
+         "fuse; time x 512 for the full 64 x 2048 queries", 256, 512, lambda: retrieval(q3, keys3, st3, h3, 8)),
+        ("c5_update", "config 5 slice: 4096 tokens of 1 of 16 heads, chunk 128; time x 256 for 16 x 65536 tokens",
+         4096, 256, lambda: torch_port.segment_scan(k5, v5, q5, m5, 0.97, 128)),
+        ("c5_retrieval", "config 5 slice: 256 tokens of 1 of 16 heads, route top-16 of 512, gather, apply, fuse; "
+         "time x 4096 for 16 x 65536 tokens", 256, 4096,
+         lambda: retrieval(q5[:, :256], keys5, st5, h3, 16)),
+    ]
+    out = {}
+    for threads in (host["usable"], 1):
+        torch.set_num_threads(threads)
+        res = {}
+        for name, what, tokens, scale, fn in legs:
+            sec, runs = _median_seconds(fn, budget_s=2.0 if threads > 1 else 3.0)
+            res[name] = {"sample": what, "slice_seconds": round(sec, 6), "runs": runs,
+                         "full_config_seconds": round(sec * scale, 4),
+                         "tokens/s": round(tokens / sec)}
+        out[threads] = res
+    threads = host["usable"]
+    c2 = out[threads]["c2"]
+    return {"value": c2["tokens/s"], "unit": "tokens/s", "cores": threads, "kind": "port",
+            "sample": f"full config 2 (64 x 2048 tokens, d=128, fp32 math on bf16-rounded inputs), one "
+                      f"_vectorized_chunk_update per 64-token segment, median of {c2['runs']} runs on {threads} "
+                      f"threads (the host's usable CPUs: min of os.cpu_count(), affinity and cgroup quota)",
+            "host": host, "one_thread": out[1], "legs": out[threads]}
 
 
 def main() -> int:
@@ -495,10 +662,11 @@ def main() -> int:
     ap.add_argument("--c2-only", action="store_true", help="only the headline kernel (quick sweeps)")
     ap.add_argument("--c4-only", action="store_true", help="the headline kernel and the config-4 model forward")
     ap.add_argument("--bwd-only", action="store_true", help="the headline kernel and the config-2 backward")
+    ap.add_argument("--route-only", action="store_true", help="the headline kernel and config 3 / 5 routing")
     ap.add_argument("--probe", action="store_true",
                     help="counter runs: a 256 MiB device copy (calibration) then config-2 launches only")
     a = ap.parse_args()
-    if a.c2_only or a.probe or a.c4_only or a.bwd_only:
+    if a.c2_only or a.probe or a.c4_only or a.bwd_only or a.route_only:
         a.no_gather = a.no_cpu = True
     if a.gpus != 1:
         print(f"bench.py measures one GPU only; --gpus {a.gpus} is not supported in this build "
@@ -543,6 +711,26 @@ def main() -> int:
             traffic = None
 
     secondary = {}
+    if not a.no_gather:
+        log("north-star shape: B*H=64 x T=8192, d=128, chunk 64")
+        n1 = bench_n1(torch, dev, max(3, a.steps // 2), 2)
+        n1_gbs = n1["bytes"] / n1["us"] / 1e3
+        n1_tf = n1["flops"] / n1["us"] / 1e6
+        secondary["n1_update"] = {
+            "what": "north-star shape: fused chunk-update + query, B=8 x H=8 sequences x 8192 tokens, d_k=d_v=128, "
+                    "chunk 64, bf16 q/k/v, fp32 state, 128 snapshots per sequence; one launch per step",
+            "us": round(n1["us"], 1), "tokens/s": round(n1["tokens"] / n1["us"] * 1e6),
+            "roofline": {"bound": "hbm", "achieved": round(n1_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                         "frac": round(n1_gbs / HBM_PEAK_GBS, 4), "algorithmic_bytes_per_launch": n1["bytes"]},
+            "mfma": {"TFLOP/s": round(n1_tf, 2), "peak": BF16_PEAK_TFLOPS, "frac": round(n1_tf / BF16_PEAK_TFLOPS, 5),
+                     "flops_per_launch": n1["flops"]}}
+        log(f"n1: {n1['us']:.1f} us/launch, {n1_gbs:.0f} GB/s, {n1_tf:.1f} TFLOP/s")
+    if a.route_only:
+        log("routing only: config 3 and config 5")
+        for label, r in bench_routes(torch, dev, a.steps, a.warmup).items():
+            secondary[label] = dict(r, **{"GB/s": round(r["bytes"] / r["us"] / 1e3, 1),
+                                          "TFLOP/s": round(r["flops"] / r["us"] / 1e6, 2)})
+            log(f"{label}: {r['us']:.1f} us")
     if not a.no_gather or a.bwd_only:
         log("config 2 backward (chunk_update_backward: recompute + MFMA backward + tile sums)")
         bw = bench_c2_bwd(torch, dev, max(3, a.steps // 2), 2)
@@ -632,9 +820,10 @@ def main() -> int:
 
     cpu = None
     if not a.no_cpu:
-        log("cpu baseline (torch-CPU port, config 2)")
+        log("cpu baseline (torch-CPU port: configs 1 and 2 full, configs 3 and 5 slices)")
         cpu = cpu_baseline(torch)
-        log(f"cpu: {cpu['value']:.3e} tokens/s on {cpu['cores']} threads")
+        log(f"cpu: {cpu['value']:.3e} tokens/s on {cpu['cores']} threads ({cpu['host']}); one thread "
+            f"{cpu['one_thread']['c2']['tokens/s']:.3e}")
 
     line = {
         "metric": METRIC,
@@ -659,7 +848,7 @@ def main() -> int:
                      "kernel_us": round(t_kernel * 1e6, 2),
                      "mfma": {"TFLOP/s": round(tflops, 2), "peak": BF16_PEAK_TFLOPS,
                               "frac": round(tflops / BF16_PEAK_TFLOPS, 5), "flops_per_launch": flops}},
-        "cpu_baseline": None if cpu is None else {k: cpu[k] for k in ("value", "unit", "cores", "kind", "sample")},
+        "cpu_baseline": cpu,
         "secondary": secondary,
     }
     print(json.dumps(line), flush=True)

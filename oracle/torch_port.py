@@ -12,6 +12,7 @@ the product path.
   route             grm/core/paper_grm.py:566-589 (matmul * scale, topk, softmax)
   gather            grm/core/cuda_ops.py:265-284 (index_select per batch entry)
   apply_query       grm/core/cuda_ops.py:257-262 (einsum)
+  fuse_residual     grm/core/aggregator.py:67-145 (weighted sum + LayerNorm)
 """
 
 from __future__ import annotations
@@ -82,3 +83,11 @@ def apply_query(memories: Tensor, queries: Tensor) -> Tensor:
     if memories.ndim == 5:
         return torch.einsum("bqrhk,bqk->bqrh", memories, queries)
     return torch.einsum("brhk,bk->brh", memories, queries)
+
+
+def fuse_residual(h_online: Tensor, retrieved: Tensor, gates: Tensor, weight: Tensor, bias: Tensor,
+                  eps: float = 1e-5) -> Tensor:
+    """LayerNorm(h + sum_r gates_r retrieved_r): the residual fusion of
+    grm/core/aggregator.py:67-145 as the models call it (paper_grm.py:604-611)."""
+    contribution = (retrieved * gates.unsqueeze(-1)).sum(dim=-2)
+    return torch.nn.functional.layer_norm(h_online + contribution, (h_online.size(-1),), weight, bias, eps)
