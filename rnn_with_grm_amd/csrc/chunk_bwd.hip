@@ -69,6 +69,8 @@ __global__ __launch_bounds__(64) void chunk_bwd_kernel(const BwdArgs a) {
   const int v0 = tile * RB;
   const int dk = a.dk, dv = a.dv;
   const int64_t T = a.T;
+  // 32-bit chunk lengths (a 64-bit min would be a VALU compare in the loop)
+  const int last_len = static_cast<int>(T - static_cast<int64_t>(a.n_chunks - 1) * BCT);
   const float lam = a.decay, c = a.c;
   const bool f32m = a.mem_f32 != 0;
 
@@ -90,7 +92,7 @@ __global__ __launch_bounds__(64) void chunk_bwd_kernel(const BwdArgs a) {
 
   for (int ch = a.n_chunks - 1; ch >= 0; --ch) {
     const int64_t t0 = static_cast<int64_t>(ch) * BCT;
-    const int L = static_cast<int>(min(static_cast<int64_t>(BCT), T - t0));
+    const int L = ch == a.n_chunks - 1 ? last_len : BCT;
     // ---- forward replay of the chunk: rebuild M_t rows, emit dq partials
     {
       float m[RB][KR];
@@ -419,6 +421,8 @@ __global__ __launch_bounds__(MB_NT, 1) void chunk_bwd_mfma_kernel(const BwdMArgs
   const int v0 = tile * MB_DV;
   const int dk = a.dk, dv = a.dv;
   const int64_t T = a.T;
+  // 32-bit chunk lengths (a 64-bit min would be a VALU compare in the loop)
+  const int last_len = static_cast<int>(T - static_cast<int64_t>(a.n_chunks - 1) * BCT);
   const float c = a.c;
   const bool f32m = a.mem_f32 != 0;
   const raw* keys = static_cast<const raw*>(a.keys) + b * T * dk;
@@ -494,7 +498,7 @@ __global__ __launch_bounds__(MB_NT, 1) void chunk_bwd_mfma_kernel(const BwdMArgs
   };
   auto load_chunk = [&](int ch, Stage& sg) {
     const int64_t t0 = static_cast<int64_t>(ch) * BCT;
-    const int L = static_cast<int>(min(static_cast<int64_t>(BCT), T - t0));
+    const int L = ch == a.n_chunks - 1 ? last_len : BCT;
     const __amdgpu_buffer_rsrc_t rk = make_rsrc(keys + t0 * dk, static_cast<uint32_t>(L * dk * ES));
     const __amdgpu_buffer_rsrc_t rq = make_rsrc(queries + t0 * dk, static_cast<uint32_t>(L * dk * ES));
     const __amdgpu_buffer_rsrc_t rv = make_rsrc(values + t0 * dv, static_cast<uint32_t>(L * dv * ES));
@@ -564,7 +568,7 @@ __global__ __launch_bounds__(MB_NT, 1) void chunk_bwd_mfma_kernel(const BwdMArgs
   load_chunk(a.n_chunks - 1, stage);
   for (int ch = a.n_chunks - 1; ch >= 0; --ch) {
     const int64_t t0 = static_cast<int64_t>(ch) * BCT;
-    const int L = static_cast<int>(min(static_cast<int64_t>(BCT), T - t0));
+    const int L = ch == a.n_chunks - 1 ? last_len : BCT;
     store_chunk(ch, stage);
     if (ch > 0) load_chunk(ch - 1, stage);
     __syncthreads();  // chunk in LDS

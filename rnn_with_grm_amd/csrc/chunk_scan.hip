@@ -217,10 +217,11 @@ __global__ __launch_bounds__(NTHR) void chunk_fwd_kernel(const ChunkFwdArgs a) {
   const int i_loc = 16 * w + n;  // this lane's query row within a chunk
   // Tokens of chunk c; 0 outside this workgroup's part, so prefetches past
   // the part read nothing.
-  auto chunk_len = [&](int c) -> int {
-    const int64_t t0 = static_cast<int64_t>(c) * chunk;
-    return (c < c_end) ? static_cast<int>(min(static_cast<int64_t>(chunk), T - t0)) : 0;
-  };
+  // (32-bit scalar arithmetic: a 64-bit min is a VALU compare whose temporary
+  // VGPRs can alias a prefetch in flight and force a wait for it.)
+  const int last_c = static_cast<int>((T - 1) / chunk);
+  const int last_len = static_cast<int>(T - static_cast<int64_t>(last_c) * chunk);
+  auto chunk_len = [&](int c) -> int { return c >= c_end ? 0 : c == last_c ? last_len : chunk; };
   // Unit u of this thread covers K/Q row unit_row(u), elements unit_col(u) .. +8.
   // A wave's 64 units span 16 rows x 4 column units, so the transposed LDS
   // writes of K land on distinct banks.

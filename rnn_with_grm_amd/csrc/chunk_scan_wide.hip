@@ -333,10 +333,11 @@ __global__ __launch_bounds__(pass_threads(FULL), 1) void scan_wide_kernel(const 
   // Tokens of chunk c; 0 at or past the end of the chunk window being
   // scanned, so loads past it read nothing.
   int ce_cur = c_end;
-  auto chunk_len = [&](int c) -> int {
-    const int64_t t0 = static_cast<int64_t>(c) * chunk;
-    return (c < ce_cur) ? static_cast<int>(min(static_cast<int64_t>(chunk), T - t0)) : 0;
-  };
+  // (32-bit scalar arithmetic: a 64-bit min is a VALU compare whose temporary
+  // VGPRs can alias a prefetch in flight and force a wait for it.)
+  const int last_c = static_cast<int>((T - 1) / chunk);
+  const int last_len = static_cast<int>(T - static_cast<int64_t>(last_c) * chunk);
+  auto chunk_len = [&](int c) -> int { return c >= ce_cur ? 0 : c == last_c ? last_len : chunk; };
 
   // ---- staging: unit u of this thread is row (tid + WNT u) / KU, 16-byte
   // column (tid + WNT u) % KU, so a wave reads whole rows.

@@ -210,6 +210,29 @@ def test_value_split_scan(dev, monkeypatch, dtype, mem_dtype, B, T, K, H, seg):
                                atol=1e-3 if mem_dtype != torch.float32 else 1e-6)
 
 
+@pytest.mark.parametrize("B,T,K,H,seg", [(2, 300, 128, 128, 64), (3, 129, 64, 64, 64), (1, 640, 96, 256, 100),
+                                         (2, 200, 32, 96, 32), (4, 1000, 128, 128, 128)])
+def test_value_split_full_line_snapshots(dev, monkeypatch, B, T, K, H, seg):
+    """The value-split scan's full-line snapshot stores (a lane permutation that gives each
+    store whole 128-byte lines, chosen from 320 MB of snapshots, forced here with
+    GRM_HIP_SNAP_FULL_LINES=1) write the same bytes as the per-tile stores (=0): key widths
+    below the padded 64/128 (partial last lines), ragged chunks, fp32 and bf16 states."""
+    for mem_dtype in (torch.float32, torch.bfloat16):
+        k, v, q, m = make_case(B, T, K, H, torch.bfloat16, mem_dtype, seed=B * 31 + T + K)
+        kd, vd, qd, md = k.to(dev), v.to(dev), q.to(dev), m.to(dev)
+        print(f"full-line snapshots B={B} T={T} K={K} H={H} seg={seg} state {mem_dtype}", flush=True)
+        monkeypatch.setenv("GRM_HIP_CHUNK_VSPLIT", "1")
+        monkeypatch.setenv("GRM_HIP_SNAP_FULL_LINES", "1")
+        h1, m1, s1 = capi.chunk_update_fwd(kd, vd, qd, md, 0.97, seg)
+        monkeypatch.setenv("GRM_HIP_SNAP_FULL_LINES", "0")
+        h0, m0, s0 = capi.chunk_update_fwd(kd, vd, qd, md, 0.97, seg)
+        torch.cuda.synchronize()
+        assert torch.equal(s1, s0) and torch.equal(h1, h0) and torch.equal(m1, m0)
+        if mem_dtype == torch.float32:
+            rh, rm, rs = oracle_fwd(k, v, q, m, 0.97, seg)
+            close("snapshots", s1, rs, torch.bfloat16)
+
+
 @pytest.mark.parametrize("vsplit", ["1", "0"])
 def test_optional_outputs(dev, monkeypatch, vsplit):
     """hidden may be NULL, and memory_out may be NULL when snapshots are requested; the outputs
