@@ -39,9 +39,44 @@ struct ChunkFwdArgs {
   float part_decay;   // decay^(part_chunks * chunk)
   float* part_states; // [batch, n_parts - 1, dv, dk]: end-state contribution of each part
   int part_starts; // part_states[q] holds M_{q+1} (combined) rather than D_q (wide kernel)
+  int snap_full_lines; // value-split kernel: snapshot stores in whole 128-byte lines (full_line_pair)
   float c;         // (1 - decay) / sqrt(d_k)
   float pw[PW_N];  // decay^n rounded from double
 };
+
+// Snapshot bytes per call from which the value-split kernel stores snapshots
+// in whole 128-byte lines: below it the writes stay in the 256 MB memory-side
+// cache and the lane permutation only costs issue slots (config 2, value
+// split: 48.8 -> 62.9 us); above it half-line writes cost HBM efficiency
+// (64 x 8192 tokens: 290 -> 265 us).
+constexpr int64_t kFullLineSnapBytes = 320ll << 20;
+
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
+
+// Two 16x16 fp32 accumulator tiles of a state block, lane (g, n) holding row n,
+// columns 4g .. 4g + 3 of tile x and 16 + 4g .. of tile y (so x and y are the
+// two 64-byte halves of each row's 128-byte line), rearranged for two stores
+// that each cover 8 rows x 128 bytes: lane (g, n) gets 16-byte chunk
+// 2g + (n >> 3) of row n & 7 (oa) and of row 8 + (n & 7) (ob).  A DPP row
+// rotate by 8 moves rows n +- 8 within each 16-lane row; the 32- and 16-lane
+// swaps then gather the chunks across the four lane groups.
+__device__ __forceinline__ void full_line_pair(f32x4_t x, f32x4_t y, int n, f32x4_t& oa, f32x4_t& ob) {
+  constexpr int kRowRor8 = 0x128;
+  const bool half = (n >> 3) != 0;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const float xr = __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(x[i]), kRowRor8, 0xf, 0xf, false));
+    const float yr = __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(y[i]), kRowRor8, 0xf, 0xf, false));
+    const auto a32 = __builtin_amdgcn_permlane32_swap(__float_as_uint(half ? xr : x[i]),
+                                                      __float_as_uint(half ? yr : y[i]), false, false);
+    const auto a16 = __builtin_amdgcn_permlane16_swap(a32[0], a32[1], false, false);
+    oa[i] = __uint_as_float(half ? a16[1] : a16[0]);
+    const auto b32 = __builtin_amdgcn_permlane32_swap(__float_as_uint(half ? x[i] : xr),
+                                                      __float_as_uint(half ? y[i] : yr), false, false);
+    const auto b16 = __builtin_amdgcn_permlane16_swap(b32[0], b32[1], false, false);
+    ob[i] = __uint_as_float(half ? b16[1] : b16[0]);
+  }
+}
 
 // Value columns per workgroup of the wide kernel.
 constexpr int kWideDv = 128;

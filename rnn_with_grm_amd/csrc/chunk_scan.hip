@@ -778,6 +778,11 @@ extern "C" int grm_hip_chunk_update_fwd(const void* keys, const void* values, co
   }
   a.mem_f32 = mem_dtype == GRM_HIP_F32;
   a.vec_m = vec_m;
+  {
+    const int64_t snap_bytes = snapshots != nullptr ? batch * a.n_snap * value_dim * key_dim * 4 : 0;
+    a.snap_full_lines = snap_bytes >= kFullLineSnapBytes;
+    if (const char* env = getenv("GRM_HIP_SNAP_FULL_LINES")) a.snap_full_lines = env[0] == '1';
+  }
   a.c = static_cast<float>((1.0 - memory_decay) / std::sqrt(static_cast<double>(key_dim)));
   for (int i = 0; i < PW_N; ++i) a.pw[i] = static_cast<float>(std::pow(memory_decay, i));
 

@@ -39,8 +39,6 @@
 #include <stdint.h>
 #include <string.h>
 
-#include <cstdlib>
-
 #include "chunk_scan.h"
 #include "grm_hip.h"
 #include "grm_hip_common.h"
@@ -113,12 +111,7 @@ __device__ __forceinline__ int o_at(int row, int col) {
 // slower.  (Loads keep the default policy: K, Q and the 64-byte V slices are
 // shared between the tiles of a sequence.)
 constexpr int kStreamStore = 2;  // cache-policy bit NT
-constexpr int kDppRowRor8 = 0x128;  // DPP row_ror:8 (rotate each 16-lane row by 8)
-// Snapshot bytes per call from which the full-line snapshot stores pay: below
-// it the writes stay in the 256 MB memory-side cache and the lane permutation
-// only costs issue slots (config 2: 48.8 -> 62.9 us); above it the half-line
-// writes cost HBM efficiency (64 x 8192 tokens: 283 -> 255 us).
-constexpr int64_t kFullLineSnapBytes = 320ll << 20;
+
 
 __device__ __forceinline__ void store_stream(__amdgpu_buffer_rsrc_t r, int off, u32x4 v) {
   __builtin_amdgcn_raw_buffer_store_b128(v, r, off, 0, kStreamStore);
@@ -146,7 +139,7 @@ __device__ __forceinline__ Frag8<E> vs_frag_tr(const typename ET<E>::raw* p_lo, 
   return f;
 }
 
-template <class E, int DKP, int PF, bool FULL_LINES>
+template <class E, int DKP, int PF>
 __global__ __launch_bounds__(kVsThreads, 1) void scan_vsplit_kernel(const ChunkFwdArgs a) {
   using S = VsShape<E, DKP>;
   constexpr int DVT = S::DVT;
@@ -430,34 +423,16 @@ __global__ __launch_bounds__(kVsThreads, 1) void scan_vsplit_kernel(const ChunkF
       const int si = c / a.snap_every;
       const __amdgpu_buffer_rsrc_t rs =
           make_rsrc(a.snapshots + (b * a.n_snap + si) * dv * dk, static_cast<uint32_t>(dv * dk * 4));
-      if constexpr (FULL_LINES) {
-        // Each store instruction covers 8 state rows x 128 bytes instead of
-        // 16 rows x 64 bytes: key tiles 2p and 2p + 1 hold the two halves of
-        // every 128-byte line, and a row-rotate by 8 (DPP) plus the 32- and
-        // 16-lane swaps give lane (g, n) chunk 2 g + (n >> 3) of row n & 7 (first
-        // store) or 8 + (n & 7) (second).  Whole lines leave L2 as whole writes,
-        // which matters once the snapshots no longer fit the memory-side cache
-        // (the host enables this from 320 MB of snapshots).
+      if (a.snap_full_lines && KT % 2 == 0) {
+        // Whole 128-byte lines per store (full_line_pair): key tiles 2p and 2p + 1
+        // hold the two halves of every line of the wave's rows.
         const int half = n >> 3;
 #pragma unroll
         for (int vb = 0; vb < 2; ++vb)
 #pragma unroll
           for (int p = 0; p < KT / 2; ++p) {
             f32x4 oa, ob;
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-              const float x = st[vb][2 * p][i], y = st[vb][2 * p + 1][i];
-              const float xr = __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(x), kDppRowRor8, 0xf, 0xf, false));
-              const float yr = __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(y), kDppRowRor8, 0xf, 0xf, false));
-              const auto a32 = __builtin_amdgcn_permlane32_swap(__float_as_uint(half ? xr : x),
-                                                                __float_as_uint(half ? yr : y), false, false);
-              const auto a16 = __builtin_amdgcn_permlane16_swap(a32[0], a32[1], false, false);
-              oa[i] = __uint_as_float(half ? a16[1] : a16[0]);
-              const auto b32 = __builtin_amdgcn_permlane32_swap(__float_as_uint(half ? x : xr),
-                                                                __float_as_uint(half ? y : yr), false, false);
-              const auto b16 = __builtin_amdgcn_permlane16_swap(b32[0], b32[1], false, false);
-              ob[i] = __uint_as_float(half ? b16[1] : b16[0]);
-            }
+            full_line_pair(st[vb][2 * p], st[vb][2 * p + 1], n, oa, ob);
             const int k = KH * uk + 32 * p + 4 * (2 * g + half);
             const int offa = k < dk ? (v0 + 16 * vb + (n & 7)) * dk + k : kBufOOB;
             const int offb = k < dk ? (v0 + 16 * vb + 8 + (n & 7)) * dk + k : kBufOOB;
@@ -596,11 +571,8 @@ int launch_vsplit(ChunkFwdArgs a, hipStream_t stream) {
   constexpr int PF = kVsplitPrefetch;
   static bool attr_set = false;
   if (!attr_set) {
-    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&scan_vsplit_kernel<E, DKP, PF, false>),
+    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&scan_vsplit_kernel<E, DKP, PF>),
                                        hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(S::lds_bytes));
-    if (e == hipSuccess)
-      e = hipFuncSetAttribute(reinterpret_cast<const void*>(&scan_vsplit_kernel<E, DKP, PF, true>),
-                              hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(S::lds_bytes));
     if (e != hipSuccess) {
       set_error("chunk_update_fwd: hipFuncSetAttribute failed: %s", hipGetErrorString(e));
       return static_cast<int>(e);
@@ -617,16 +589,8 @@ int launch_vsplit(ChunkFwdArgs a, hipStream_t stream) {
     return GRM_HIP_EINVAL;
   }
   a.xcd_remap = (grid % 8 == 0) ? 1 : 0;
-  const int64_t snap_bytes = a.snap_every > 0 ? a.batch * a.n_snap * a.dv * static_cast<int64_t>(a.dk) * 4 : 0;
-  bool full_lines = snap_bytes >= kFullLineSnapBytes && S::KT % 2 == 0;
-  if (const char* env = getenv("GRM_HIP_SNAP_FULL_LINES")) full_lines = env[0] == '1' && S::KT % 2 == 0;
-  if (full_lines) {
-    hipLaunchKernelGGL((scan_vsplit_kernel<E, DKP, PF, true>), dim3(static_cast<unsigned>(grid)), dim3(kVsThreads),
-                       S::lds_bytes, stream, a);
-  } else {
-    hipLaunchKernelGGL((scan_vsplit_kernel<E, DKP, PF, false>), dim3(static_cast<unsigned>(grid)), dim3(kVsThreads),
-                       S::lds_bytes, stream, a);
-  }
+  hipLaunchKernelGGL((scan_vsplit_kernel<E, DKP, PF>), dim3(static_cast<unsigned>(grid)), dim3(kVsThreads),
+                     S::lds_bytes, stream, a);
   return check_launch("chunk_update_fwd");
 }
 

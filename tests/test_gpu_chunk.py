@@ -212,7 +212,7 @@ def test_value_split_scan(dev, monkeypatch, dtype, mem_dtype, B, T, K, H, seg):
 
 @pytest.mark.parametrize("B,T,K,H,seg", [(2, 300, 128, 128, 64), (3, 129, 64, 64, 64), (1, 640, 96, 256, 100),
                                          (2, 200, 32, 96, 32), (4, 1000, 128, 128, 128)])
-def test_value_split_full_line_snapshots(dev, monkeypatch, B, T, K, H, seg):
+def test_full_line_snapshots(dev, monkeypatch, B, T, K, H, seg):
     """The value-split scan's full-line snapshot stores (a lane permutation that gives each
     store whole 128-byte lines, chosen from 320 MB of snapshots, forced here with
     GRM_HIP_SNAP_FULL_LINES=1) write the same bytes as the per-tile stores (=0): key widths
