@@ -239,20 +239,38 @@ def bench_c3(torch, dev, steps, warmup):
         if rc != 0:
             raise RuntimeError(capi.last_error())
 
+    rfb = int(lib.grm_hip_retrieve_fuse_workspace(BH, S, Q * K, D))
+    rfws = torch.empty(rfb, dtype=torch.uint8, device=dev)
+    h3 = h_online.view(BH, Q, D)
+    fused3 = torch.empty_like(h3)
+
+    def retrieve_fuse():
+        rc = lib.grm_hip_retrieve_fuse(P(states), P(idx), P(q), P(gt), P(h3), P(ln_w), P(ln_b), P(fused3), P(rfws),
+                                       rfb, BH, S, Q, K, D, D, capi.F32, capi.BF16, capi.F32, 1e-5, None, sp)
+        if rc != 0:
+            raise RuntimeError(capi.last_error())
+
     def retrieval():
+        route()
+        retrieve_fuse()
+
+    def composition():
         route()
         gather_apply()
         fuse()
 
     ga_wall, ga_per = timed_launches(torch, gather_apply, max(3, steps), warmup, stream)
     fu_wall, fu_per = timed_launches(torch, fuse, max(3, steps), warmup, stream)
+    rf_wall, rf_per = timed_launches(torch, retrieve_fuse, max(3, steps), warmup, stream)
     rt_wall, rt_per = timed_launches(torch, retrieval, max(3, steps), warmup, stream)
+    cp_wall, cp_per = timed_launches(torch, composition, max(3, steps), warmup, stream)
+    assert torch.allclose(fused3.view(BH * Q, D), fused_out, rtol=2e-3, atol=2e-3), "retrieve_fuse spot check failed"
     # spot check of the fused path against the materialised composition for one query
     b, qi = 7, 1500
     sel = states[b, idx[b, qi]]                                    # [K, D, D]
     r_ref = torch.einsum("rhk,k->rh", sel, q[b, qi].float())
     assert torch.allclose(retrieved[b, qi], r_ref, rtol=1e-4, atol=1e-6), "gather_apply spot check failed"
-    del retrieved, ws, online, h_online, fused_out
+    del retrieved, ws, online, h_online, fused_out, rfws, fused3
 
     g_steps = max(3, min(steps, 10))
     g_wall, g_per = timed_launches(torch, gather, g_steps, min(warmup, 2), stream)
@@ -272,7 +290,9 @@ def bench_c3(torch, dev, steps, warmup):
                          "bytes": BH * S * D * D * 4 + BH * Q * K * D * 4 + q.numel() * 2 + idx.numel() * 8,
                          "flops": 2 * BH * Q * K * D * D},
         "fuse": {"ms": statistics.mean(fu_per) * 1e3},
+        "retrieve_fuse": {"ms": statistics.mean(rf_per) * 1e3},
         "retrieval": {"ms": statistics.mean(rt_per) * 1e3},
+        "composition": {"ms": statistics.mean(cp_per) * 1e3},
         "gather": {"ms": statistics.mean(g_per) * 1e3, "bytes": gather_bytes,
                    "fill_ms": statistics.mean(f_per) * 1e3, "fill_bytes": BH * Q * K * D * D * 4},
     }
@@ -419,7 +439,22 @@ def bench_c5(torch, dev, steps, warmup):
         if rc != 0:
             raise RuntimeError(capi.last_error())
 
+    rfb = int(lib.grm_hip_retrieve_fuse_workspace(BH, S, T * K, D))
+    rfws = torch.empty(rfb, dtype=torch.uint8, device=dev)
+    h5 = h_online.view(BH, T, D)
+    fused5 = torch.empty_like(h5)
+
+    def retrieve_fuse():
+        rc = lib.grm_hip_retrieve_fuse(P(snaps), P(idx), P(q), P(gt), P(h5), P(ln_w), P(ln_b), P(fused5), P(rfws),
+                                       rfb, BH, S, T, K, D, D, capi.F32, capi.BF16, capi.F32, 1e-5, None, sp)
+        if rc != 0:
+            raise RuntimeError(capi.last_error())
+
     def retrieval():
+        route()
+        retrieve_fuse()
+
+    def composition():
         route()
         gather_apply()
         fuse()
@@ -433,18 +468,21 @@ def bench_c5(torch, dev, steps, warmup):
 
     def retrieval_causal():
         route_causal()
-        gather_apply()  # empty slots (index -1) give zero rows, and their gates are 0
-        fuse()
+        retrieve_fuse()  # empty slots (index -1) contribute nothing
 
     n = max(3, min(steps, 10))
     r_wall, r_per = timed_launches(torch, route, n, min(warmup, 2), stream)
     ga_wall, ga_per = timed_launches(torch, gather_apply, n, min(warmup, 2), stream)
     fu_wall, fu_per = timed_launches(torch, fuse, n, min(warmup, 2), stream)
+    rf_wall, rf_per = timed_launches(torch, retrieve_fuse, n, min(warmup, 2), stream)
     rt_wall, rt_per = timed_launches(torch, retrieval, n, min(warmup, 2), stream)
+    cp_wall, cp_per = timed_launches(torch, composition, n, min(warmup, 2), stream)
     # spot checks: one token's retrieval against the composition, and its last snapshot
     b, t = 3, 40000
     r_ref = torch.einsum("rhk,k->rh", snaps[b, idx[b, t]], q[b, t].float())
     assert torch.allclose(retrieved[b, t], r_ref, rtol=1e-4, atol=1e-6), "c5 gather_apply spot check failed"
+    assert torch.allclose(fused5.view(BH * T, D)[b * T + t], fused_out[b * T + t], rtol=2e-3, atol=2e-3), \
+        "c5 retrieve_fuse spot check failed"
     assert bool(torch.isfinite(snaps[:, -1]).all()), "c5 snapshots not finite"
     rc_wall, rc_per = timed_launches(torch, route_causal, n, min(warmup, 2), stream)
     rtc_wall, rtc_per = timed_launches(torch, retrieval_causal, n, min(warmup, 2), stream)
@@ -458,11 +496,16 @@ def bench_c5(torch, dev, steps, warmup):
                          "bytes": BH * S * D * D * 4 + tokens * K * D * 4 + q.numel() * 2 + idx.numel() * 8,
                          "flops": 2 * tokens * K * D * D},
         "fuse": {"ms": statistics.mean(fu_per) * 1e3},
+        "retrieve_fuse": {"ms": statistics.mean(rf_per) * 1e3,
+                          "bytes": BH * S * D * D * 4 + q.numel() * 2 + idx.numel() * 8 + gt.numel() * 4 +
+                                   2 * tokens * D * 4,
+                          "intermediate_bytes": 2 * (tokens * K * D * 2 + tokens * K * 4)},
         "retrieval": {"ms": statistics.mean(rt_per) * 1e3, "tokens": tokens},
+        "composition": {"ms": statistics.mean(cp_per) * 1e3},
         "route_causal": {"ms": statistics.mean(rc_per) * 1e3},
         "retrieval_causal": {"ms": statistics.mean(rtc_per) * 1e3},
     }
-    del retrieved, h_online, fused_out, ws2, idx, sc, gt, snaps, hidden, q, k, v
+    del retrieved, h_online, fused_out, ws2, idx, sc, gt, snaps, hidden, q, k, v, rfws, fused5
     return out
 
 
@@ -756,14 +799,19 @@ def main() -> int:
         log(f"c3 gather: {gth['ms']:.2f} ms, {gbs:.0f} GB/s (fill of the output: {gth['fill_ms']:.2f} ms)")
         ga, rt = c3["gather_apply"], c3["retrieval"]
         secondary["c3_retrieval_fused"] = {
-            "what": "route -> gather_apply (no materialised states) -> residual + LayerNorm, per config-3 batch",
-            "ms": round(rt["ms"], 4), "route_ms": round(r["ms"], 4), "gather_apply_ms": round(ga["ms"], 4),
+            "what": "route -> retrieve_fuse (gather + apply + gate-weighted sum + residual + LayerNorm, no "
+                    "materialised states, row-scaled float16 per-route rows), per config-3 batch; the two-kernel "
+                    "composition (gather_apply in float32, then fuse_residual) beside it",
+            "ms": round(rt["ms"], 4), "route_ms": round(r["ms"], 4),
+            "retrieve_fuse_ms": round(c3["retrieve_fuse"]["ms"], 4),
+            "composition_ms": round(c3["composition"]["ms"], 4), "gather_apply_ms": round(ga["ms"], 4),
             "fuse_ms": round(c3["fuse"]["ms"], 4),
             "gather_apply_GB/s": round(ga["bytes"] / ga["ms"] / 1e6, 1),
             "gather_apply_TFLOP/s_fp32": round(ga["flops"] / ga["ms"] / 1e9, 2),
             "speedup_vs_materialised_gather_alone": round(gth["ms"] / rt["ms"], 2)}
-        log(f"c3 fused retrieval: {rt['ms']:.3f} ms (route {r['ms']:.3f}, gather_apply {ga['ms']:.3f}, "
-            f"fuse {c3['fuse']['ms']:.3f})")
+        log(f"c3 fused retrieval: {rt['ms']:.3f} ms (route {r['ms']:.3f}, retrieve_fuse "
+            f"{c3['retrieve_fuse']['ms']:.3f}); composition {c3['composition']['ms']:.3f} (gather_apply "
+            f"{ga['ms']:.3f}, fuse {c3['fuse']['ms']:.3f})")
 
     if not a.no_gather:
         log("config 5: whole-sequence update (16 x 65536 tokens, 512 snapshots) + k=16 retrieval per token")
@@ -773,23 +821,33 @@ def main() -> int:
         secondary["c5_update"] = {"us": round(u["us"], 1), "tokens/s": round(u["tokens"] / u["us"] * 1e6),
                                   "GB/s": round(ugbs, 1), "hbm_frac": round(ugbs / HBM_PEAK_GBS, 4),
                                   "bytes": u["bytes"]}
+        rf5 = c5["retrieve_fuse"]
+        rf_gbs = rf5["bytes"] / rf5["ms"] / 1e6
         secondary["c5_retrieval_fused"] = {
-            "what": "route (top-16 of 512 snapshots per token) -> gather_apply -> residual + LayerNorm, "
-                    "every token routed over all 512 states (no causal mask, as the reference's chunk path)",
+            "what": "route (top-16 of 512 snapshots per token) -> retrieve_fuse (gather + apply + gate-weighted sum "
+                    "+ residual + LayerNorm), every token routed over all 512 states (no causal mask, as the "
+                    "reference's chunk path); the two-kernel composition (gather_apply float32 rows, then "
+                    "fuse_residual) beside it",
             "ms": round(rt5["ms"], 3), "tokens/s": round(rt5["tokens"] / rt5["ms"] * 1e3),
-            "route_ms": round(c5["route"]["ms"], 3), "gather_apply_ms": round(ga5["ms"], 3),
+            "route_ms": round(c5["route"]["ms"], 3), "retrieve_fuse_ms": round(rf5["ms"], 3),
+            "retrieve_fuse_roofline": {"bound": "hbm", "achieved": round(rf_gbs, 1), "peak": HBM_PEAK_GBS,
+                                       "unit": "GB/s", "frac": round(rf_gbs / HBM_PEAK_GBS, 4),
+                                       "algorithmic_bytes": rf5["bytes"],
+                                       "float16_rows_written_and_read": rf5["intermediate_bytes"]},
+            "composition_ms": round(c5["composition"]["ms"], 3), "gather_apply_ms": round(ga5["ms"], 3),
             "fuse_ms": round(c5["fuse"]["ms"], 3),
             "route_TFLOP/s": round(c5["route"]["flops"] / c5["route"]["ms"] / 1e9, 1),
             "gather_apply_GB/s": round(ga5["bytes"] / ga5["ms"] / 1e6, 1),
             "gather_apply_TFLOP/s_fp32": round(ga5["flops"] / ga5["ms"] / 1e9, 1)}
         secondary["c5_retrieval_causal"] = {
             "what": "the same retrieval with causal windows (segment routing: the tokens of segment s route over "
-                    "snapshots 0..s-1, as in the model's segment loop), route -> gather_apply -> residual + LayerNorm",
+                    "snapshots 0..s-1, as in the model's segment loop), route -> retrieve_fuse",
             "ms": round(c5["retrieval_causal"]["ms"], 3),
             "tokens/s": round(rt5["tokens"] / c5["retrieval_causal"]["ms"] * 1e3),
             "route_ms": round(c5["route_causal"]["ms"], 3)}
         log(f"c5 update: {u['us']:.1f} us ({ugbs:.0f} GB/s); retrieval {rt5['ms']:.2f} ms (route "
-            f"{c5['route']['ms']:.2f}, gather_apply {ga5['ms']:.2f}, fuse {c5['fuse']['ms']:.2f})")
+            f"{c5['route']['ms']:.2f}, retrieve_fuse {rf5['ms']:.2f}); composition {c5['composition']['ms']:.2f} "
+            f"(gather_apply {ga5['ms']:.2f}, fuse {c5['fuse']['ms']:.2f})")
 
     if not a.no_gather:
         c4 = bench_c4_archive(torch, dev, a.steps, a.warmup)

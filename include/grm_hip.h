@@ -194,6 +194,37 @@ int grm_hip_gather_apply(const void* memories, const int64_t* indices, const voi
                          int mem_dtype, int q_dtype, int out_dtype, int32_t* bad_index_count, void* stream);
 
 /*
+ * Fused retrieval: gather + query application + gate-weighted sum + residual +
+ * LayerNorm, without the per-(query, route) rows of gather_apply in float32:
+ *   out[b, q, :] = LN(h_online[b, q, :] + sum_r gates[b, q, r] * M[b, idx[b, q, r]] q[b, q])
+ * the composition fuse_residual(h_online, gather_apply(memories, indices, queries,
+ * float32), gates, ln_weight, ln_bias), i.e. the reference's retriever followed by its
+ * aggregator (grm/core/paper_grm.py:229,301-313,604-611; grm/core/aggregator.py:67-145).
+ * The state products are the exact 16-bit MFMA products of gather_apply with float32
+ * accumulation; each gate-weighted row g * M q is kept in the workspace as float16
+ * scaled by a power of two per (pair, 128-value tile) so that its largest magnitude
+ * lies in [2^14, 2^15) (relative rounding 2^-11 of the tile's largest value, no
+ * overflow), and the sum over routes runs in float32 in route order 0 .. R-1: no
+ * atomics, deterministic.  Indices outside [0, segments) contribute nothing and,
+ * when bad_index_count is not NULL, increment that device int32 counter.
+ * memories [batch, segments, value_dim, key_dim] mem_dtype (float32 with bf16 queries,
+ * or 16-bit); queries [batch, n_query, key_dim] bf16 (f16 with f16 memories); gates
+ * [batch, n_query, routes] float32; h_online and out [batch, n_query, value_dim] and
+ * ln_weight / ln_bias [value_dim] are h_dtype, ln_weight NULL for no LayerNorm,
+ * ln_bias NULL for none; 16-byte aligned.
+ * workspace: grm_hip_retrieve_fuse_workspace(batch, segments, n_query * routes,
+ * value_dim) bytes, contents need not be initialised.
+ * Limits: key_dim <= 128 with 16-byte key rows, value_dim a multiple of 8 and <= 2048,
+ * segments <= 16384; otherwise GRM_HIP_EUNSUPPORTED (use gather_apply + fuse_residual).
+ */
+int64_t grm_hip_retrieve_fuse_workspace(int64_t batch, int64_t segments, int64_t n_index, int64_t value_dim);
+int grm_hip_retrieve_fuse(const void* memories, const int64_t* indices, const void* queries, const float* gates,
+                          const void* h_online, const void* ln_weight, const void* ln_bias, void* out,
+                          void* workspace, int64_t workspace_bytes, int64_t batch, int64_t segments,
+                          int64_t n_query, int64_t routes, int64_t value_dim, int64_t key_dim, int mem_dtype,
+                          int q_dtype, int h_dtype, float eps, int32_t* bad_index_count, void* stream);
+
+/*
  * Segment routing: dot-product score, top-k and softmax gates.
  *   score[b, q, s] = scale * sum_d queries[b, q, d] * keys[b, s, d]
  * Each score is one float32 fused multiply-add chain over d = 0 .. dim-1 in

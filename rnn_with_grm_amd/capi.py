@@ -41,6 +41,9 @@ SIGNATURES = {
     "grm_hip_batched_gather": (_C, [_P, _P, _P, _I, _I, _I, _I, _C, _P, _P]),
     "grm_hip_gather_apply_workspace": (_I, [_I, _I, _I]),
     "grm_hip_gather_apply": (_C, [_P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _C, _C, _C, _P, _P]),
+    "grm_hip_retrieve_fuse_workspace": (_I, [_I, _I, _I, _I]),
+    "grm_hip_retrieve_fuse": (_C, [_P, _P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _C, _C, _C,
+                                   ctypes.c_float, _P, _P]),
     "grm_hip_topk_route": (_C, [_P, _P, _P, _P, _P, _I, _I, _I, _I, _C, _I, ctypes.c_float, ctypes.c_float, _P]),
     "grm_hip_segment_route": (_C, [_P, _P, _P, _P, _P, _I, _I, _I, _I, _C, _I, _I, _I, _I, ctypes.c_float,
                                    ctypes.c_float, _P]),
@@ -220,6 +223,24 @@ def gather_apply(memories, indices, queries, bad_count=None, out=None, dtype=Non
                                      Q, R, H, K, dtype_code(memories.dtype), dtype_code(queries.dtype),
                                      dtype_code(dtype), _ptr(bad_count), _stream(memories))
     _check(rc, "grm_hip_gather_apply")
+    return out
+
+
+def retrieve_fuse(memories, indices, queries, gates, h_online, ln_weight=None, ln_bias=None, eps=1e-5,
+                  bad_count=None, out=None):
+    """out[b, q] = LN(h_online[b, q] + sum_r gates[b, q, r] * memories[b, indices[b, q, r]] @ queries[b, q]):
+    gather_apply (float32) + fuse_residual in one call, without the float32 [B, Q, R, H] rows."""
+    B, S, H, K = memories.shape
+    Q, R = indices.shape[1], indices.shape[2]
+    if out is None:
+        out = torch.empty_like(h_online)
+    wsb = int(load().grm_hip_retrieve_fuse_workspace(B, S, Q * R, H))
+    ws = torch.empty(max(wsb, 16), dtype=torch.uint8, device=memories.device)
+    rc = load().grm_hip_retrieve_fuse(_ptr(memories), _ptr(indices), _ptr(queries), _ptr(gates), _ptr(h_online),
+                                      _ptr(ln_weight), _ptr(ln_bias), _ptr(out), _ptr(ws), wsb, B, S, Q, R, H, K,
+                                      dtype_code(memories.dtype), dtype_code(queries.dtype),
+                                      dtype_code(h_online.dtype), float(eps), _ptr(bad_count), _stream(memories))
+    _check(rc, "grm_hip_retrieve_fuse")
     return out
 
 

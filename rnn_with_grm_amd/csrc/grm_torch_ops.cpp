@@ -2,12 +2,13 @@
 //
 // The five schemas are the reference's, character for character
 // (reference grm/csrc/bindings.cpp:5-11), so grm.core.cuda_ops and every model
-// above it bind to this library unchanged.  Five more ops live in the same
+// above it bind to this library unchanged.  Six more ops live in the same
 // namespace: segment_scan_forward (whole-sequence update with per-segment
 // state snapshots), topk_route (score -> top-k -> softmax), segment_route (the
 // same routing for every segment of a sequence against the archive as it
-// grows), fuse_residual and gather_apply (gather + query application without
-// materialising the states).
+// grows), fuse_residual, gather_apply (gather + query application without
+// materialising the states) and retrieve_fuse (gather_apply, the gate-weighted
+// sum and fuse_residual in one call).
 //
 // CUDA-key kernels (HIP devices dispatch on the CUDA key in PyTorch-ROCm)
 // check the inputs, allocate outputs with ATen on the input's device and call
@@ -376,6 +377,30 @@ Tensor fuse_residual_generic(const Tensor& h, const Tensor& retrieved, const Ten
                        bias.has_value() && bias->defined() ? bias->to(at::kFloat) : Tensor(), eps);
   }
   return x.to(h.scalar_type()).contiguous();
+}
+
+// retrieve_fuse: LN(h + sum_r gates_r (M[idx_r] q)) over [B, Q] rows, the
+// retriever's float32 gather + apply followed by the aggregator's residual +
+// LayerNorm (paper_grm.py:229,301-313,604-611; aggregator.py:67-145).
+void check_retrieve_fuse_inputs(const Tensor& memories, const Tensor& indices, const Tensor& queries,
+                                const Tensor& gates, const Tensor& h) {
+  TORCH_CHECK(indices.dim() == 3, "retrieve_fuse: indices must be [B, Q, R]");
+  check_gather_apply_inputs(memories, indices, queries);
+  TORCH_CHECK(gates.sizes() == indices.sizes(), "retrieve_fuse: gates must match indices [B, Q, R]");
+  TORCH_CHECK(h.dim() == 3 && h.size(0) == memories.size(0) && h.size(1) == indices.size(1) &&
+                  h.size(2) == memories.size(2),
+              "retrieve_fuse: h_online must be [B, Q, H]");
+}
+
+Tensor retrieve_fuse_generic(const Tensor& memories, const Tensor& indices, const Tensor& queries,
+                             const Tensor& gates, const Tensor& h, const c10::optional<Tensor>& weight,
+                             const c10::optional<Tensor>& bias, double eps) {
+  check_retrieve_fuse_inputs(memories, indices, queries, gates, h);
+  const int64_t B = h.size(0), Q = h.size(1), H = h.size(2), R = indices.size(2);
+  Tensor r = gather_apply_generic(memories, indices, queries, at::kFloat).reshape({B * Q, R, H});
+  return fuse_residual_generic(h.reshape({B * Q, H}), r.to(h.scalar_type()), gates.reshape({B * Q, R}), weight, bias,
+                               eps)
+      .reshape({B, Q, H});
 }
 
 // ---------------------------------------------------------------------------
@@ -760,6 +785,61 @@ Tensor fuse_residual_hip(const Tensor& h, const Tensor& retrieved, const Tensor&
   return out;
 }
 
+bool aligned16(const Tensor& t) { return reinterpret_cast<uintptr_t>(t.data_ptr()) % 16 == 0; }
+
+Tensor retrieve_fuse_hip(const Tensor& memories, const Tensor& indices, const Tensor& queries, const Tensor& gates,
+                         const Tensor& h, const c10::optional<Tensor>& weight, const c10::optional<Tensor>& bias,
+                         double eps) {
+  check_retrieve_fuse_inputs(memories, indices, queries, gates, h);
+  const bool has_w = weight.has_value() && weight->defined();
+  const bool has_b = bias.has_value() && bias->defined();
+  const int64_t B = memories.size(0), S = memories.size(1), H = memories.size(2), K = memories.size(3);
+  const int64_t Q = indices.size(1), R = indices.size(2);
+  const int md = dtype_code(memories.scalar_type()), qd = dtype_code(queries.scalar_type());
+  const int hd = dtype_code(h.scalar_type());
+  const bool q16 = queries.scalar_type() == at::kBFloat16 ||
+                   (queries.scalar_type() == at::kHalf && memories.scalar_type() == at::kHalf);
+  bool ok = same_cuda_device({&memories, &indices, &queries, &gates, &h}) && md >= 0 && qd >= 0 && hd >= 0 && q16 &&
+            K <= 128 && (K * 2) % 16 == 0 && H % 8 == 0 && H <= 2048 && S <= 16384 && B <= 65535;
+  if (has_w) ok = ok && weight->is_cuda() && weight->scalar_type() == h.scalar_type();
+  if (has_b) ok = ok && has_w && bias->is_cuda() && bias->scalar_type() == h.scalar_type();
+  if (!ok) {
+    // The two-kernel composition (gather_apply in float32, then fuse_residual).
+    const Tensor r = gather_apply_hip(memories, indices, queries, at::kFloat).reshape({B * Q, R, H});
+    return fuse_residual_hip(h.reshape({B * Q, H}), r.to(h.scalar_type()), gates.reshape({B * Q, R}), weight, bias,
+                             eps)
+        .reshape({B, Q, H});
+  }
+  c10::OptionalDeviceGuard guard(memories.device());
+  Tensor mm = memories.contiguous(), idx = indices.to(at::kLong).contiguous(), q = queries.contiguous();
+  Tensor gc = gates.to(at::kFloat).contiguous(), hc = h.contiguous();
+  Tensor wc = has_w ? weight->contiguous() : Tensor(), bc = has_b ? bias->contiguous() : Tensor();
+  if (!aligned16(mm) || !aligned16(q) || !aligned16(hc) || (has_w && !aligned16(wc)) || (has_b && !aligned16(bc))) {
+    mm = mm.clone();
+    q = q.clone();
+    hc = hc.clone();
+    if (has_w) wc = wc.clone();
+    if (has_b) bc = bc.clone();
+  }
+  Tensor out = at::empty_like(hc);
+  const int64_t wsb = grm_hip_retrieve_fuse_workspace(B, S, Q * R, H);
+  Tensor ws = at::empty({std::max<int64_t>(wsb, 16)}, mm.options().dtype(at::kByte));
+  Tensor bad;
+  const bool check = check_indices_requested();
+  if (check) bad = at::zeros({1}, mm.options().dtype(at::kInt));
+  check_rc(grm_hip_retrieve_fuse(mm.data_ptr(), idx.data_ptr<int64_t>(), q.data_ptr(), gc.data_ptr<float>(),
+                                 hc.data_ptr(), has_w ? wc.data_ptr() : nullptr, has_b ? bc.data_ptr() : nullptr,
+                                 out.data_ptr(), ws.data_ptr(), wsb, B, S, Q, R, H, K, md, qd, hd,
+                                 static_cast<float>(eps), check ? bad.data_ptr<int32_t>() : nullptr,
+                                 current_stream(mm)),
+           "retrieve_fuse");
+  if (check) {
+    const int64_t nbad = bad.item<int32_t>();
+    TORCH_CHECK_INDEX(nbad == 0, "retrieve_fuse: ", nbad, " index values outside [0, ", S, ")");
+  }
+  return out;
+}
+
 // CPU-key wrappers for the generic forms.
 std::tuple<Tensor, Tensor, Tensor, Tensor> chunk_update_backward_cpu(
     const Tensor& grad_hidden, const Tensor& grad_memory_out, const Tensor& keys,
@@ -786,6 +866,7 @@ TORCH_LIBRARY(grm_cuda, m) {
   m.def("fuse_residual(Tensor h_online, Tensor retrieved, Tensor gates, Tensor? weight, Tensor? bias, float eps) -> Tensor");
   m.def("gather_apply(Tensor memories, Tensor indices, Tensor queries, ScalarType? dtype=None) -> Tensor");
   m.def("segment_route(Tensor queries, Tensor keys, int top_k, int segment_len, int base, int capacity, float scale, float temperature) -> (Tensor gates, Tensor indices, Tensor scores)");
+  m.def("retrieve_fuse(Tensor memories, Tensor indices, Tensor queries, Tensor gates, Tensor h_online, Tensor? weight, Tensor? bias, float eps) -> Tensor");
 }
 
 TORCH_LIBRARY_IMPL(grm_cuda, CPU, m) {
@@ -800,6 +881,7 @@ TORCH_LIBRARY_IMPL(grm_cuda, CPU, m) {
   m.impl("fuse_residual", grm::fuse_residual_generic);
   m.impl("gather_apply", grm::gather_apply_generic);
   m.impl("segment_route", grm::segment_route_cpu);
+  m.impl("retrieve_fuse", grm::retrieve_fuse_generic);
 }
 
 TORCH_LIBRARY_IMPL(grm_cuda, CUDA, m) {
@@ -814,6 +896,7 @@ TORCH_LIBRARY_IMPL(grm_cuda, CUDA, m) {
   m.impl("fuse_residual", grm::fuse_residual_hip);
   m.impl("gather_apply", grm::gather_apply_hip);
   m.impl("segment_route", grm::segment_route_hip);
+  m.impl("retrieve_fuse", grm::retrieve_fuse_hip);
 }
 
 PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {

@@ -64,6 +64,11 @@ struct RetrieveArgs {
   int32_t* tile_base;
   int tb_max;
   int tile_pairs;
+  // Gate-weighted, row-scaled 16-bit output (retrieve_fuse): out holds float16
+  // rows of g * M q scaled by 2^sh per (pair, 128-value tile), scales[pair,
+  // tile] = 2^-sh.  nullptr: the plain [pairs, dv] output of gather_apply.
+  const float* gates;  // [batch, n_index]
+  float* scales;       // [batch, n_index, v_tiles]
 };
 
 // ---------------------------------------------------------------------------
@@ -119,6 +124,8 @@ __device__ __forceinline__ void zero_rows_wave(const RetrieveArgs& a, int64_t b,
     const int64_t row = __shfl(i, l, 64);
     typename ET<EM>::raw* ob = static_cast<typename ET<EM>::raw*>(a.out) + (b * a.n_index + row) * a.dv;
     for (int h = lane; h < a.dv; h += 64) ob[h] = ET<EM>::from_f(0.f);
+    if (a.scales != nullptr)
+      for (int t = lane; t < a.v_tiles; t += 64) a.scales[(b * a.n_index + row) * a.v_tiles + t] = 0.f;
   }
 }
 
@@ -513,7 +520,7 @@ __global__ __launch_bounds__(AP_THREADS) void apply_reg_kernel(const RetrieveArg
 // takes keys 32c + 8g .. + 7 from lane group g, so the four groups of a row
 // read consecutive bytes: each state load instruction covers whole 128-byte
 // lines of 16 rows (fp32 states) instead of 16-byte pieces of 64 lines.
-template <class EL, class EM, class EQ, int DKP, class EF, int NPART>
+template <class EL, class EM, class EQ, int DKP, class EF, int NPART, bool SCALED = false>
 __global__ __launch_bounds__(AP_THREADS) void apply_mfma16_kernel(const RetrieveArgs a) {
   using rawl = typename ET<EL>::raw;  // stored memories
   using rawm = typename ET<EM>::raw;  // arithmetic / output type
@@ -567,17 +574,19 @@ __global__ __launch_bounds__(AP_THREADS) void apply_mfma16_kernel(const Retrieve
 
   Frag8<EF> am[2][NPART][NSTEP];
   bool split = false;
-  for (int p0 = p_begin; p0 < p_end; p0 += AP_N) {
-    const int np = min(AP_N, p_end - p0);
-    // The query's MFMA operand: q cast to EM, then to EF.  When both casts are
-    // exact (a 16-bit query of type EF, EM float32 or EF) the operand is the
-    // query's own bits, loaded as they are (half the registers of float32).
-    constexpr bool kRawQ = std::is_same_v<EQ, EF> && (std::is_same_v<EM, F32> || std::is_same_v<EM, EQ>);
-    float xq[kRawQ ? 1 : 4][kRawQ ? 1 : KG];
-    Frag8<EF> rq8[4][kRawQ ? NSTEP : 1];
+  // The query's MFMA operand: q cast to EM, then to EF.  When both casts are
+  // exact (a 16-bit query of type EF, EM float32 or EF) the operand is the
+  // query's own bits, loaded as they are (half the registers of float32).
+  constexpr bool kRawQ = std::is_same_v<EQ, EF> && (std::is_same_v<EM, F32> || std::is_same_v<EM, EQ>);
+  float xq[kRawQ ? 1 : 4][kRawQ ? 1 : KG];
+  Frag8<EF> rq8[4][kRawQ ? NSTEP : 1];
+  // Query rows of a 64-pair step: lane 16 j + n holds pair j's row in slot j.
+  // The loads of step s + 1 are issued right after step s's products, so they
+  // overlap its output tile instead of opening the next step.
+  auto load_q = [&](int pid_src) {
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-      const int pid = __shfl(pid_l, 16 * j + n, 64);
+      const int pid = __shfl(pid_src, 16 * j + n, 64);
       if constexpr (kRawQ) {
 #pragma unroll
         for (int c = 0; c < NSTEP; ++c) {
@@ -598,6 +607,16 @@ __global__ __launch_bounds__(AP_THREADS) void apply_mfma16_kernel(const Retrieve
         }
       }
     }
+  };
+  load_q(pid_l);
+  for (int p0 = p_begin; p0 < p_end; p0 += AP_N) {
+    const int np = min(AP_N, p_end - p0);
+    const int pid_cur = pid_l;
+    const bool more = p0 + AP_N < p_end;
+    const int pid_next = (more && lane < p_end - p0 - AP_N) ? lb[p0 + AP_N + lane] : -1;
+    // The gate of this lane's pair, loaded while the tile's products run.
+    float gate_l = 0.f;
+    if constexpr (SCALED) gate_l = pid_cur >= 0 ? a.gates[b * a.n_index + pid_cur] : 0.f;
     if (!split) {
       split = true;
 #pragma unroll
@@ -639,8 +658,8 @@ __global__ __launch_bounds__(AP_THREADS) void apply_mfma16_kernel(const Retrieve
 #pragma unroll
           for (int i = 0; i < 2; ++i) acc[i][j] = mfma8(am[i][part][c], bq[c], acc[i][j]);
     }
-    const int pid_cur = pid_l;
-    if (p0 + AP_N < p_end) pid_l = lane < p_end - p0 - AP_N ? lb[p0 + AP_N + lane] : -1;
+    if (more) load_q(pid_next);
+    pid_l = pid_next;
     __syncthreads();  // previous output tile written out
 #pragma unroll
     for (int i = 0; i < 2; ++i)
@@ -654,6 +673,42 @@ __global__ __launch_bounds__(AP_THREADS) void apply_mfma16_kernel(const Retrieve
       const int e = tid + AP_THREADS * it;
       const int p = e / (AP_V / 4), v = (e % (AP_V / 4)) * 4;
       const int pid = __shfl(pid_cur, p, 64);
+      if constexpr (SCALED) {
+        // The 32 lanes of one half-wave hold pair p's 128 values of this tile:
+        // scale the gate-weighted row so its largest magnitude lies in
+        // [2^14, 2^15) and store it as float16 with the inverse power of two.
+        const float gp = __shfl(gate_l, p, 64);
+        const f32x4 val = *reinterpret_cast<const f32x4*>(Os + p * OS + v) * gp;
+        float m = fmaxf(fmaxf(fabsf(val[0]), fabsf(val[1])), fmaxf(fabsf(val[2]), fabsf(val[3])));
+        // maximum over the 32 lanes of the half-wave without LDS: quad swaps, the
+        // half-row and row mirrors (DPP), then the 16-lane row swap
+        m = fmaxf(m, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(m), 0xb1, 0xf, 0xf, false)));
+        m = fmaxf(m, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(m), 0x4e, 0xf, 0xf, false)));
+        m = fmaxf(m, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(m), 0x141, 0xf, 0xf, false)));
+        m = fmaxf(m, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(m), 0x140, 0xf, 0xf, false)));
+        {
+          const auto sw = __builtin_amdgcn_permlane16_swap(__float_as_uint(m), __float_as_uint(m), false, false);
+          m = fmaxf(__uint_as_float(sw[0]), __uint_as_float(sw[1]));
+        }
+        int ex = 0;
+        (void)frexpf(m, &ex);
+        const int sh = min(max(15 - ex, -100), 100);
+        if (p < np) {
+          uint16_t* dst = static_cast<uint16_t*>(a.out) + (b * a.n_index + pid) * static_cast<int64_t>(dv) + v0 + v;
+          if (v + 4 <= vcols) {
+            uint2 q;
+            q.x = pack2<F16>(ldexpf(val[0], sh), ldexpf(val[1], sh));
+            q.y = pack2<F16>(ldexpf(val[2], sh), ldexpf(val[3], sh));
+            *reinterpret_cast<uint2*>(dst) = q;
+          } else {
+#pragma unroll
+            for (int r = 0; r < 4; ++r)
+              if (v + r < vcols) dst[r] = ET<F16>::from_f(ldexpf(val[r], sh));
+          }
+          if ((tid & 31) == 0) a.scales[(b * a.n_index + pid) * a.v_tiles + vt] = ldexpf(1.f, -sh);
+        }
+        continue;
+      }
       if (p < np) {
         const f32x4 val = *reinterpret_cast<const f32x4*>(Os + p * OS + v);
         rawm* dst = obase + static_cast<int64_t>(pid) * dv + v0 + v;
@@ -669,10 +724,10 @@ __global__ __launch_bounds__(AP_THREADS) void apply_mfma16_kernel(const Retrieve
   }
 }
 
-template <class EL, class EM, class EQ, int DKP, class EF, int NPART>
+template <class EL, class EM, class EQ, int DKP, class EF, int NPART, bool SCALED = false>
 int launch_apply_mfma16(const RetrieveArgs& a, hipStream_t s) {
   const dim3 grid(static_cast<unsigned>(static_cast<int64_t>(a.tb_max) * a.v_tiles), static_cast<unsigned>(a.batch));
-  hipLaunchKernelGGL((apply_mfma16_kernel<EL, EM, EQ, DKP, EF, NPART>), grid,
+  hipLaunchKernelGGL((apply_mfma16_kernel<EL, EM, EQ, DKP, EF, NPART, SCALED>), grid,
                      dim3(AP_THREADS), 0, s, a);
   return check_launch("gather_apply");
 }
@@ -769,6 +824,193 @@ int dispatch_q(const RetrieveArgs& a, int q_dtype, hipStream_t s) {
   }
 }
 
+// ---------------------------------------------------------------------------
+// Residual + LayerNorm over the scaled rows of retrieve_fuse:
+//   out[t] = LN(h[t] + sum_r scales[t, r, c / 128] * rows[t, r, c])
+// with r in order 0 .. R-1 (the gates are already in the rows), a two-pass
+// mean / variance in fp32.  lpr lanes share a row, each covering NV groups of
+// 8 consecutive columns (16-byte float16 loads of the rows).
+struct FuseScaledArgs {
+  const void* h;
+  const uint16_t* rows;
+  const float* scales;
+  const void* w;
+  const void* bias;
+  void* out;
+  int64_t n_rows;
+  int routes;
+  int hidden;
+  int v_tiles;
+  float eps;
+};
+
+template <class E>
+__device__ __forceinline__ void load8(__amdgpu_buffer_rsrc_t r, int off, float (&f)[8]) {
+  if constexpr (sizeof(typename ET<E>::raw) == 2) {
+    const U8<E> u = __builtin_bit_cast(U8<E>, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0));
+#pragma unroll
+    for (int e = 0; e < 8; ++e) f[e] = ET<E>::to_f(u.e[e]);
+  } else {
+    const u32x4 lo = __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0);
+    const u32x4 hi = __builtin_amdgcn_raw_buffer_load_b128(r, off == kBufOOB ? kBufOOB : off + 16, 0, 0);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      f[e] = __uint_as_float(lo[e]);
+      f[4 + e] = __uint_as_float(hi[e]);
+    }
+  }
+}
+
+template <class E>
+__device__ __forceinline__ void store8(__amdgpu_buffer_rsrc_t r, int off, const float (&y)[8]) {
+  if constexpr (sizeof(typename ET<E>::raw) == 2) {
+    const u32x4 q = u32x4{pack2<E>(y[0], y[1]), pack2<E>(y[2], y[3]), pack2<E>(y[4], y[5]), pack2<E>(y[6], y[7])};
+    __builtin_amdgcn_raw_buffer_store_b128(q, r, off, 0, 0);
+  } else {
+    __builtin_amdgcn_raw_buffer_store_b128(
+        u32x4{__float_as_uint(y[0]), __float_as_uint(y[1]), __float_as_uint(y[2]), __float_as_uint(y[3])}, r, off, 0, 0);
+    __builtin_amdgcn_raw_buffer_store_b128(
+        u32x4{__float_as_uint(y[4]), __float_as_uint(y[5]), __float_as_uint(y[6]), __float_as_uint(y[7])}, r,
+        off == kBufOOB ? kBufOOB : off + 16, 0, 0);
+  }
+}
+
+template <class E, int NV>
+__global__ __launch_bounds__(256) void fuse_scaled_kernel(const FuseScaledArgs a, const int lpr) {
+  using raw = typename ET<E>::raw;
+  const int tid = threadIdx.x;
+  const int sub = tid & (lpr - 1);
+  const int64_t row = static_cast<int64_t>(blockIdx.x) * (256 / lpr) + tid / lpr;
+  const bool live = row < a.n_rows;
+  const int H = a.hidden;
+  const int64_t rr = live ? row : 0;
+  const __amdgpu_buffer_rsrc_t rh = make_rsrc(static_cast<const raw*>(a.h) + rr * H, H * sizeof(raw));
+  const __amdgpu_buffer_rsrc_t rrow =
+      make_rsrc(a.rows + rr * a.routes * H, static_cast<uint32_t>(a.routes * H * 2));
+  const float* sc = a.scales + rr * a.routes * a.v_tiles;
+  float x[NV][8];
+#pragma unroll
+  for (int v = 0; v < NV; ++v) {
+    const int c = (sub + lpr * v) * 8;
+    const bool in = live && c < H;
+    float hv[8];
+    load8<E>(rh, in ? c * static_cast<int>(sizeof(raw)) : kBufOOB, hv);
+    float r[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) r[e] = 0.f;
+    const int tile = c / AP_V;
+#pragma unroll 4
+    for (int j = 0; j < a.routes; ++j) {
+      const float sj = in ? sc[j * a.v_tiles + tile] : 0.f;
+      float rv[8];
+      load8<F16>(rrow, in ? (j * H + c) * 2 : kBufOOB, rv);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) r[e] = fmaf(sj, rv[e], r[e]);
+    }
+#pragma unroll
+    for (int e = 0; e < 8; ++e) x[v][e] = c < H ? hv[e] + r[e] : 0.f;
+  }
+  const __amdgpu_buffer_rsrc_t ro = make_rsrc(static_cast<raw*>(a.out) + rr * H, H * sizeof(raw));
+  auto out_off = [&](int v) {
+    const int c = (sub + lpr * v) * 8;
+    return (live && c < H) ? c * static_cast<int>(sizeof(raw)) : kBufOOB;
+  };
+  if (a.w == nullptr) {
+#pragma unroll
+    for (int v = 0; v < NV; ++v) store8<E>(ro, out_off(v), x[v]);
+    return;
+  }
+  float sum = 0.f;
+#pragma unroll
+  for (int v = 0; v < NV; ++v)
+#pragma unroll
+    for (int e = 0; e < 8; ++e) sum += x[v][e];
+  for (int off = lpr >> 1; off > 0; off >>= 1) sum += __shfl_xor(sum, off, 64);
+  const float mean = sum / static_cast<float>(H);
+  float var = 0.f;
+#pragma unroll
+  for (int v = 0; v < NV; ++v) {
+    const int c = (sub + lpr * v) * 8;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const float d = x[v][e] - mean;
+      var = c < H ? fmaf(d, d, var) : var;
+    }
+  }
+  for (int off = lpr >> 1; off > 0; off >>= 1) var += __shfl_xor(var, off, 64);
+  const float rstd = 1.0f / sqrtf(var / static_cast<float>(H) + a.eps);
+  const __amdgpu_buffer_rsrc_t rw = make_rsrc(a.w, H * sizeof(raw));
+  const __amdgpu_buffer_rsrc_t rb = make_rsrc(a.bias, a.bias != nullptr ? H * sizeof(raw) : 0u);
+#pragma unroll
+  for (int v = 0; v < NV; ++v) {
+    const int c = (sub + lpr * v) * 8;
+    const int off = c < H ? c * static_cast<int>(sizeof(raw)) : kBufOOB;
+    float wv[8], bv[8];
+    load8<E>(rw, off, wv);
+    load8<E>(rb, off, bv);  // zeros without a bias
+    float y[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) y[e] = (x[v][e] - mean) * rstd * wv[e] + bv[e];
+    store8<E>(ro, out_off(v), y);
+  }
+}
+
+template <class E>
+int launch_fuse_scaled(const FuseScaledArgs& a, hipStream_t s) {
+  const int groups = a.hidden / 8;
+  int lpr = 1;
+  while (lpr < 64 && lpr < groups) lpr <<= 1;
+  const int nv = (groups + lpr - 1) / lpr;
+  const dim3 grid(static_cast<unsigned>((a.n_rows + 256 / lpr - 1) / (256 / lpr)));
+  auto go = [&](auto nvc) {
+    hipLaunchKernelGGL((fuse_scaled_kernel<E, decltype(nvc)::value>), grid, dim3(256), 0, s, a, lpr);
+  };
+  if (nv <= 1) go(std::integral_constant<int, 1>{});
+  else if (nv <= 2) go(std::integral_constant<int, 2>{});
+  else if (nv <= 4) go(std::integral_constant<int, 4>{});
+  else go(std::integral_constant<int, 8>{});
+  return check_launch("retrieve_fuse(fuse)");
+}
+
+// The scaled apply runs the exact 16-bit MFMA kernel with float32 arithmetic;
+// other dtype pairs and unaligned shapes are not supported by retrieve_fuse.
+template <class EL, class EQ>
+int launch_apply_scaled(const RetrieveArgs& a, hipStream_t s) {
+  using Plan = MfmaPlan<EL, F32, EQ>;
+  if constexpr (Plan::ok) {
+    using EF = typename Plan::EF;
+    constexpr int NPART = Plan::parts;
+    if (a.dk <= 32) return launch_apply_mfma16<EL, F32, EQ, 32, EF, NPART, true>(a, s);
+    if (a.dk <= 64) return launch_apply_mfma16<EL, F32, EQ, 64, EF, NPART, true>(a, s);
+    return launch_apply_mfma16<EL, F32, EQ, 128, EF, NPART, true>(a, s);
+  } else {
+    set_error("retrieve_fuse: no exact 16-bit MFMA plan for these dtypes");
+    return GRM_HIP_EUNSUPPORTED;
+  }
+}
+
+template <class EL>
+bool scaled_ok_q(const RetrieveArgs& a, int q_dtype) {
+  switch (q_dtype) {
+    case GRM_HIP_F16: return MfmaPlan<EL, F32, F16>::ok && vec_ok<EL, F16>(a);
+    case GRM_HIP_BF16: return MfmaPlan<EL, F32, BF16>::ok && vec_ok<EL, BF16>(a);
+    default: return false;
+  }
+}
+
+bool scaled_supported(const RetrieveArgs& a, int mem_dtype, int q_dtype) {
+  switch (mem_dtype) {
+    case GRM_HIP_F32: return scaled_ok_q<F32>(a, q_dtype);
+    case GRM_HIP_F16: return scaled_ok_q<F16>(a, q_dtype);
+    default: return scaled_ok_q<BF16>(a, q_dtype);
+  }
+}
+
+template <class EL>
+int apply_scaled_q(const RetrieveArgs& a, int q_dtype, hipStream_t s) {
+  return q_dtype == GRM_HIP_F16 ? launch_apply_scaled<EL, F16>(a, s) : launch_apply_scaled<EL, BF16>(a, s);
+}
+
 int allow_segment_lds(const void* fn) {
   const hipError_t e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize,
                                            static_cast<int>(kMaxSegments * sizeof(int)));
@@ -849,6 +1091,49 @@ int64_t tiles_bytes(int64_t batch, int64_t segments, int64_t n_index) {
 
 using namespace grmhip;
 
+namespace grmhip {
+namespace {
+
+// The sort's workspace carve-up and the sizes, shared by gather_apply and
+// retrieve_fuse (the workspace of grm_hip_gather_apply_workspace comes first).
+void init_retrieve_args(RetrieveArgs& a, const void* memories, const int64_t* indices, const void* queries, void* out,
+                        void* workspace, int64_t batch, int64_t segments, int64_t n_query, int64_t routes,
+                        int64_t n_index, int64_t hidden_size, int64_t key_dim, int32_t* bad_index_count) {
+  memset(&a, 0, sizeof(a));
+  a.mem = memories;
+  a.idx = indices;
+  a.queries = queries;
+  a.out = out;
+  a.offsets = static_cast<int32_t*>(workspace);
+  a.list = reinterpret_cast<int32_t*>(static_cast<unsigned char*>(workspace) + offsets_bytes(batch, segments));
+  a.partial = reinterpret_cast<int32_t*>(static_cast<unsigned char*>(workspace) + offsets_bytes(batch, segments) +
+                                         list_bytes(batch, n_index));
+  a.bk_chunks = static_cast<int>(bucket_chunks(batch, n_index));
+  {
+    unsigned char* t0 = static_cast<unsigned char*>(workspace) + offsets_bytes(batch, segments) +
+                        list_bytes(batch, n_index) + partial_bytes(batch, segments, n_index);
+    a.tile_pairs = static_cast<int>(tile_pairs_for(segments, n_index));
+    a.tb_max = static_cast<int>(tiles_max(segments, n_index));
+    a.tiles = reinterpret_cast<int4*>(t0);
+    t0 += batch * a.tb_max * 16;
+    a.n_tiles = reinterpret_cast<int32_t*>(t0);
+    t0 += (batch * 4 + 15) / 16 * 16;
+    a.tile_base = reinterpret_cast<int32_t*>(t0);
+  }
+  a.bad = bad_index_count;
+  a.batch = batch;
+  a.segments = segments;
+  a.n_query = n_query;
+  a.routes = routes;
+  a.n_index = n_index;
+  a.dv = static_cast<int>(hidden_size);
+  a.dk = static_cast<int>(key_dim);
+  a.v_tiles = static_cast<int>((hidden_size + AP_V - 1) / AP_V);
+}
+
+}  // namespace
+}  // namespace grmhip
+
 extern "C" int64_t grm_hip_gather_apply_workspace(int64_t batch, int64_t segments, int64_t n_index) {
   if (batch <= 0 || segments < 0 || n_index <= 0) return 0;
   return offsets_bytes(batch, segments) + list_bytes(batch, n_index) + partial_bytes(batch, segments, n_index) +
@@ -894,36 +1179,8 @@ extern "C" int grm_hip_gather_apply(const void* memories, const int64_t* indices
     return GRM_HIP_EINVAL;
   }
   RetrieveArgs a;
-  memset(&a, 0, sizeof(a));
-  a.mem = memories;
-  a.idx = indices;
-  a.queries = queries;
-  a.out = out;
-  a.offsets = static_cast<int32_t*>(workspace);
-  a.list = reinterpret_cast<int32_t*>(static_cast<unsigned char*>(workspace) + offsets_bytes(batch, segments));
-  a.partial = reinterpret_cast<int32_t*>(static_cast<unsigned char*>(workspace) + offsets_bytes(batch, segments) +
-                                         list_bytes(batch, n_index));
-  a.bk_chunks = static_cast<int>(bucket_chunks(batch, n_index));
-  {
-    unsigned char* t0 = static_cast<unsigned char*>(workspace) + offsets_bytes(batch, segments) +
-                        list_bytes(batch, n_index) + partial_bytes(batch, segments, n_index);
-    a.tile_pairs = static_cast<int>(tile_pairs_for(segments, n_index));
-    a.tb_max = static_cast<int>(tiles_max(segments, n_index));
-    a.tiles = reinterpret_cast<int4*>(t0);
-    t0 += batch * a.tb_max * 16;
-    a.n_tiles = reinterpret_cast<int32_t*>(t0);
-    t0 += (batch * 4 + 15) / 16 * 16;
-    a.tile_base = reinterpret_cast<int32_t*>(t0);
-  }
-  a.bad = bad_index_count;
-  a.batch = batch;
-  a.segments = segments;
-  a.n_query = n_query;
-  a.routes = routes;
-  a.n_index = n_index;
-  a.dv = static_cast<int>(hidden_size);
-  a.dk = static_cast<int>(key_dim);
-  a.v_tiles = static_cast<int>((hidden_size + AP_V - 1) / AP_V);
+  init_retrieve_args(a, memories, indices, queries, out, workspace, batch, segments, n_query, routes, n_index,
+                     hidden_size, key_dim, bad_index_count);
   hipStream_t s = static_cast<hipStream_t>(stream);
   int rc;
   switch (out_dtype) {
@@ -943,5 +1200,113 @@ extern "C" int grm_hip_gather_apply(const void* memories, const int64_t* indices
   switch (mem_dtype) {
     case GRM_HIP_F16: return dispatch_q<F16, F16>(a, q_dtype, s);
     default: return dispatch_q<BF16, BF16>(a, q_dtype, s);
+  }
+}
+
+namespace {
+
+int64_t align16(int64_t n) { return (n + 15) / 16 * 16; }
+
+}  // namespace
+
+extern "C" int64_t grm_hip_retrieve_fuse_workspace(int64_t batch, int64_t segments, int64_t n_index,
+                                                   int64_t value_dim) {
+  if (batch <= 0 || segments < 0 || n_index <= 0 || value_dim <= 0) return 0;
+  const int64_t tiles = (value_dim + AP_V - 1) / AP_V;
+  return grm_hip_gather_apply_workspace(batch, segments, n_index) + align16(batch * n_index * value_dim * 2) +
+         align16(batch * n_index * tiles * 4);
+}
+
+extern "C" int grm_hip_retrieve_fuse(const void* memories, const int64_t* indices, const void* queries,
+                                     const float* gates, const void* h_online, const void* ln_weight,
+                                     const void* ln_bias, void* out, void* workspace, int64_t workspace_bytes,
+                                     int64_t batch, int64_t segments, int64_t n_query, int64_t routes,
+                                     int64_t value_dim, int64_t key_dim, int mem_dtype, int q_dtype, int h_dtype,
+                                     float eps, int32_t* bad_index_count, void* stream) {
+  if (batch < 0 || segments < 0 || n_query < 0 || routes < 0 || value_dim < 0 || key_dim < 1) {
+    set_error("retrieve_fuse: negative size or key_dim < 1");
+    return GRM_HIP_EINVAL;
+  }
+  if (mem_dtype < GRM_HIP_F32 || mem_dtype > GRM_HIP_BF16 || q_dtype < GRM_HIP_F32 || q_dtype > GRM_HIP_BF16 ||
+      h_dtype < GRM_HIP_F32 || h_dtype > GRM_HIP_BF16) {
+    set_error("retrieve_fuse: unsupported dtypes mem=%d q=%d h=%d", mem_dtype, q_dtype, h_dtype);
+    return GRM_HIP_EUNSUPPORTED;
+  }
+  if (key_dim > 128 || segments > kMaxSegments || value_dim % 8 != 0 || value_dim > 2048) {
+    set_error("retrieve_fuse: needs key_dim <= 128, segments <= %lld, value_dim a multiple of 8 and <= 2048",
+              (long long)kMaxSegments);
+    return GRM_HIP_EUNSUPPORTED;
+  }
+  const int64_t rows = batch * n_query;
+  const int64_t n_index = n_query * routes;
+  if (rows == 0 || value_dim == 0) return GRM_HIP_OK;
+  if (h_online == nullptr || out == nullptr || (n_index > 0 && (indices == nullptr || queries == nullptr ||
+                                                                gates == nullptr)) ||
+      (segments > 0 && memories == nullptr)) {
+    set_error("retrieve_fuse: null pointer");
+    return GRM_HIP_EINVAL;
+  }
+  if (n_index > INT32_MAX || batch > 65535 || routes * value_dim * 2 > INT32_MAX ||
+      tiles_max(segments, n_index) * ((value_dim + AP_V - 1) / AP_V) * AP_THREADS > UINT32_MAX) {
+    set_error("retrieve_fuse: sizes exceed one launch");
+    return GRM_HIP_EINVAL;
+  }
+  const int64_t need = grm_hip_retrieve_fuse_workspace(batch, segments, n_index, value_dim);
+  if (n_index > 0 &&
+      (workspace == nullptr || workspace_bytes < need || reinterpret_cast<uintptr_t>(workspace) % 16 != 0)) {
+    set_error("retrieve_fuse: workspace of %lld bytes (16-byte aligned) required", (long long)need);
+    return GRM_HIP_EINVAL;
+  }
+  const int hb = h_dtype == GRM_HIP_F32 ? 4 : 2;
+  if (reinterpret_cast<uintptr_t>(h_online) % 16 != 0 || reinterpret_cast<uintptr_t>(out) % 16 != 0 ||
+      (ln_weight != nullptr && reinterpret_cast<uintptr_t>(ln_weight) % 16 != 0) ||
+      (ln_bias != nullptr && reinterpret_cast<uintptr_t>(ln_bias) % 16 != 0) || (value_dim * hb) % 16 != 0) {
+    set_error("retrieve_fuse: h_online, out and the LayerNorm parameters must be 16-byte aligned");
+    return GRM_HIP_EUNSUPPORTED;
+  }
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const int v_tiles = static_cast<int>((value_dim + AP_V - 1) / AP_V);
+  unsigned char* rows16 = nullptr;
+  float* scales = nullptr;
+  if (n_index > 0) {
+    rows16 = static_cast<unsigned char*>(workspace) + grm_hip_gather_apply_workspace(batch, segments, n_index);
+    scales = reinterpret_cast<float*>(rows16 + align16(batch * n_index * value_dim * 2));
+    RetrieveArgs a;
+    init_retrieve_args(a, memories, indices, queries, rows16, workspace, batch, segments, n_query, routes, n_index,
+                       value_dim, key_dim, bad_index_count);
+    a.gates = gates;
+    a.scales = scales;
+    if (!scaled_supported(a, mem_dtype, q_dtype)) {
+      set_error("retrieve_fuse: needs bf16 queries (or f16 queries with f16 memories), 16-byte rows and "
+                "16-byte aligned memories and queries");
+      return GRM_HIP_EUNSUPPORTED;
+    }
+    int rc = launch_bucket<F16>(a, s);  // invalid pairs: zero rows and zero scales
+    if (rc != GRM_HIP_OK) return rc;
+    if (segments > 0) {
+      switch (mem_dtype) {
+        case GRM_HIP_F32: rc = apply_scaled_q<F32>(a, q_dtype, s); break;
+        case GRM_HIP_F16: rc = apply_scaled_q<F16>(a, q_dtype, s); break;
+        default: rc = apply_scaled_q<BF16>(a, q_dtype, s); break;
+      }
+      if (rc != GRM_HIP_OK) return rc;
+    }
+  }
+  FuseScaledArgs f;
+  f.h = h_online;
+  f.rows = reinterpret_cast<const uint16_t*>(rows16);
+  f.scales = scales;
+  f.w = ln_weight;
+  f.bias = ln_bias;
+  f.out = out;
+  f.n_rows = rows;
+  f.routes = static_cast<int>(routes);
+  f.hidden = static_cast<int>(value_dim);
+  f.v_tiles = v_tiles;
+  f.eps = eps;
+  switch (h_dtype) {
+    case GRM_HIP_F32: return launch_fuse_scaled<F32>(f, s);
+    case GRM_HIP_F16: return launch_fuse_scaled<F16>(f, s);
+    default: return launch_fuse_scaled<BF16>(f, s);
   }
 }

@@ -38,7 +38,7 @@ SCHEMA_OPS = (
     "batched_memory_gather",
 )
 EXTRA_OPS = ("segment_scan_forward", "topk_route", "fuse_residual", "gather_apply", "segment_route",
-             "apply_query_backward_queries")
+             "retrieve_fuse", "apply_query_backward_queries")
 
 # Environment variables of the reference (cuda_ops.py:26-32): one per op and a global one.
 GLOBAL_POLICY_ENV = "GRM_CUDA_KERNEL_POLICY"
@@ -357,7 +357,9 @@ def cuda_batched_memory_gather(memories_per_batch: Tensor, topk_indices: Tensor,
     # The reference's auto rule uses the library on the CPU too (cuda_ops.py:158-174).
     if _run_native("batched_memory_gather", memories_per_batch.device, enabled=enabled,
                    debug_fallback=debug_fallback, auto_on_cpu=True):
-        return torch.ops.grm_cuda.batched_memory_gather(memories_per_batch, topk_indices)
+        # The op has no backward (as the reference's native gather): the archive gets no
+        # gradient, stated here by detaching rather than left to autograd's fallback.
+        return torch.ops.grm_cuda.batched_memory_gather(memories_per_batch.detach(), topk_indices)
     return _torch_batched_gather(memories_per_batch, topk_indices)
 
 
@@ -459,6 +461,29 @@ def cuda_gather_apply(memories_per_batch: Tensor, topk_indices: Tensor, queries:
     return cuda_apply_query(gathered, queries.to(gathered.dtype), enabled=enabled, debug_fallback=debug_fallback)
 
 
+def cuda_retrieve_fuse(memories_per_batch: Tensor, topk_indices: Tensor, queries: Tensor, gates: Tensor,
+                       h_online: Tensor, weight: Optional[Tensor] = None, bias: Optional[Tensor] = None,
+                       eps: float = 1e-5, *, enabled: bool = True, debug_fallback: bool = False) -> Tensor:
+    """LayerNorm(h + sum_r gates_r (M[idx_r] q)) for [B, Q] rows: the retriever's float32 gather +
+    apply (paper_grm.py:227-229,301-313) followed by the aggregator's residual fusion
+    (aggregator.py:67-145, paper_grm.py:604-611), without the [B, Q, R, H] retrieved rows.
+    Inference only (no backward): under autograd the composition runs."""
+    needs_grad = torch.is_grad_enabled() and any(
+        t is not None and t.requires_grad for t in (memories_per_batch, queries, gates, h_online, weight, bias))
+    if not needs_grad and _run_native("retrieve_fuse", h_online.device, enabled=enabled,
+                                      debug_fallback=debug_fallback):
+        return torch.ops.grm_cuda.retrieve_fuse(memories_per_batch, topk_indices, queries, gates, h_online, weight,
+                                                bias, float(eps))
+    B, Q, H = h_online.shape
+    R = topk_indices.size(-1)
+    retrieved = cuda_gather_apply(memories_per_batch, topk_indices, queries, torch.float32, enabled=enabled,
+                                  debug_fallback=debug_fallback)
+    fused = cuda_fuse_residual(h_online.reshape(B * Q, H), retrieved.reshape(B * Q, R, H).to(h_online.dtype),
+                               gates.reshape(B * Q, R).to(h_online.dtype), weight, bias, eps, enabled=enabled,
+                               debug_fallback=debug_fallback)
+    return fused.reshape(B, Q, H)
+
+
 __all__ = [
     "GrmExtensionUnavailable",
     "cuda_apply_query",
@@ -466,6 +491,7 @@ __all__ = [
     "cuda_chunk_update",
     "cuda_fuse_residual",
     "cuda_gather_apply",
+    "cuda_retrieve_fuse",
     "cuda_segment_route",
     "cuda_segment_scan",
     "cuda_topk_route",

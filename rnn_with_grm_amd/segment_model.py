@@ -24,6 +24,7 @@ sequence instead of five per segment:
                         moment: base + s entries, the last `capacity` kept
   gather_apply          selected archived states applied to the query
   fuse_residual         LayerNorm(h_online + sum_r g_r r_r)
+                        (a 16-bit model runs the two as one retrieve_fuse)
   (projections and the output Linear stay library GEMMs)
 
 Archive contents and the state format are the reference's: states are stored
@@ -534,20 +535,30 @@ class SegmentRecurrentMemoryModel(nn.Module):
         # Retrieval in float32 (paper_grm.py:227,301): a 16-bit q is passed as is, its
         # values exact in float32, which lets the kernel use exact 16-bit MFMA.
         q_in = q if q.dtype in (torch.bfloat16, torch.float16) else q.to(torch.float32)
-        retrieved = cuda_ops.cuda_gather_apply(states, idx0, q_in, torch.float32,
-                                               debug_fallback=self.cuda_cpp_debug_fallback)
         soup = self.retrieval_fusion_mode == "memory_soup"
         if not grad and (soup or self.aggregator.fused_kernel_applies()):
             norm = self.memory_soup_norm if soup else self.aggregator.layer_norm
             weight = norm.weight.float() if isinstance(norm, nn.LayerNorm) else None
             bias = norm.bias.float() if isinstance(norm, nn.LayerNorm) else None
             eps = norm.eps if isinstance(norm, nn.LayerNorm) else 1e-5
-            H = h_online.size(-1)
-            fused = cuda_ops.cuda_fuse_residual(h_online.float().reshape(B * T, H),
-                                                retrieved.reshape(B * T, -1, H), gates.reshape(B * T, -1),
-                                                weight, bias, eps, debug_fallback=self.cuda_cpp_debug_fallback)
-            fused = (self.dropout if soup else self.aggregator.dropout)(fused.view(B, T, H))
+            if q.dtype in (torch.bfloat16, torch.float16):
+                # A 16-bit model: retrieval, gate-weighted sum, residual and LayerNorm in one
+                # op; the [B, T, k, H] retrieved rows are kept as row-scaled float16 (relative
+                # rounding 2^-11 of each row's largest value), never as float32.
+                fused = cuda_ops.cuda_retrieve_fuse(states, idx0, q_in, gates.float(), h_online.float(), weight, bias,
+                                                    eps, debug_fallback=self.cuda_cpp_debug_fallback)
+            else:
+                H = h_online.size(-1)
+                retrieved = cuda_ops.cuda_gather_apply(states, idx0, q_in, torch.float32,
+                                                       debug_fallback=self.cuda_cpp_debug_fallback)
+                fused = cuda_ops.cuda_fuse_residual(h_online.float().reshape(B * T, H),
+                                                    retrieved.reshape(B * T, -1, H), gates.reshape(B * T, -1),
+                                                    weight, bias, eps,
+                                                    debug_fallback=self.cuda_cpp_debug_fallback).view(B, T, H)
+            fused = (self.dropout if soup else self.aggregator.dropout)(fused)
         else:
+            retrieved = cuda_ops.cuda_gather_apply(states, idx0, q_in, torch.float32,
+                                                   debug_fallback=self.cuda_cpp_debug_fallback)
             contribution = (retrieved * gates.unsqueeze(-1)).sum(dim=2)
             if h_online.dtype != contribution.dtype:
                 # A 16-bit model: its fusion layers hold 16-bit parameters, so the float32

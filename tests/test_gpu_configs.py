@@ -199,6 +199,36 @@ def test_c5_retrieval(c5):
     np.testing.assert_allclose(fused[rows].cpu().double().numpy(), ref, rtol=1e-5, atol=1e-5)
 
 
+def test_c5_retrieve_fuse(c5):
+    """The fused retrieval at config 5 (16 heads x 65536 tokens, top-16 of 512 float32 snapshots,
+    bf16 queries): retrieve_fuse against the float32 two-kernel composition over every token,
+    and sampled tokens of two heads against the oracle's gather, apply and fusion, at the
+    north-star tolerance."""
+    BH, T, D = c5["BH"], c5["T"], c5["D"]
+    snaps, qd = c5["snaps"], c5["qd"]
+    gates, idx, _ = capi.topk_route(qd, c5["sd"], 16, 1.0 / D ** 0.5)
+    g = torch.Generator().manual_seed(8)
+    w = (1 + 0.1 * torch.randn(D, generator=g)).to(snaps.device)
+    bias = (0.1 * torch.randn(D, generator=g)).to(snaps.device)
+    h_online = c5["hid"].float()
+    fused = capi.retrieve_fuse(snaps, idx, qd, gates, h_online, w, bias)
+    rows = capi.gather_apply(snaps, idx, qd, dtype=torch.float32)
+    comp = capi.fuse_residual(h_online.view(BH * T, D), rows.view(BH * T, 16, D), gates.view(BH * T, 16), w, bias)
+    torch.cuda.synchronize()
+    del rows
+    diff = (fused.view(BH * T, D) - comp).abs().max().item()
+    assert diff < 2e-3, diff
+    for b in (2, 11):
+        toks = torch.randint(0, T, (32,), generator=g)
+        gathered, bad = orc.gather(snaps[b:b + 1].cpu().numpy(), idx[b:b + 1, toks].cpu().numpy())
+        assert bad == 0
+        r = orc.apply_query(gathered, c5["q"][b:b + 1, toks].double().numpy())
+        ref = orc.fuse_residual(h_online[b, toks].cpu().double().numpy(), r[0], gates[b, toks].cpu().double().numpy(),
+                                w.cpu().double().numpy(), bias.cpu().double().numpy())
+        np.testing.assert_allclose(fused[b, toks].cpu().double().numpy(), ref, rtol=2e-2, atol=2e-3,
+                                   err_msg=f"retrieve_fuse head {b}")
+
+
 def dev_of(t):
     return t.device
 

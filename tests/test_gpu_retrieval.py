@@ -536,3 +536,94 @@ def test_routing_mixed_dtypes_stays_on_device(dev):
     assert np.array_equal(idx.cpu().numpy(), oi) and np.array_equal(sc.cpu().numpy(), osc)
     og, oi, osc = orc.segment_route(q.numpy(), keys.float().numpy(), 8, 5, 60, 40, 0.25)
     assert np.array_equal(i2.cpu().numpy(), oi) and np.array_equal(s2.cpu().numpy(), osc)
+
+
+# ---------------------------------------------------------------- fused retrieval
+def _retrieve_fuse_ref(mem, idx, q, gates, h, w, b, eps=1e-5):
+    """The oracle's gather -> apply (float64) -> residual + LayerNorm, with zero rows for
+    indices outside [0, S)."""
+    B, Q, R = idx.shape
+    S, H = mem.shape[1], mem.shape[2]
+    mem64 = mem.double().numpy()
+    idx_np = idx.numpy()
+    valid = (idx_np >= 0) & (idx_np < S)
+    gathered, _ = orc.gather(mem64, np.where(valid, idx_np, 0))
+    r = orc.apply_query(gathered, q.double().numpy()) * valid[..., None]
+    return orc.fuse_residual(h.double().numpy().reshape(B * Q, H), r.reshape(B * Q, R, H),
+                             gates.double().numpy().reshape(B * Q, R),
+                             None if w is None else w.double().numpy(), None if b is None else b.double().numpy(),
+                             eps).reshape(B, Q, H)
+
+
+@pytest.mark.parametrize("mem_dtype", [torch.float32, torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("h_dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("B,Q,S,R,H,K,ln", [(2, 300, 37, 5, 128, 128, True), (3, 64, 8, 8, 512, 64, True),
+                                            (1, 129, 300, 16, 200, 32, False), (2, 50, 5, 3, 8, 64, True),
+                                            (1, 70, 3, 8, 264, 128, True)])
+def test_retrieve_fuse(dev, mem_dtype, h_dtype, B, Q, S, R, H, K, ln):
+    """retrieve_fuse (gather + apply + gate-weighted sum + residual + LayerNorm in one call)
+    against the oracle's composition element by element at rtol 2e-2 / atol 2e-3 (the
+    retrieved rows are kept as row-scaled float16: measured error ~1e-4), against the
+    float32 two-kernel composition (gather_apply + fuse_residual), and run to run bit for
+    bit: value widths of one to five 128-column tiles with a partial last tile, invalid
+    indices (-1, S) contributing nothing, no LayerNorm."""
+    g = torch.Generator().manual_seed(B * 7 + Q + H)
+    q_dtype = torch.float16 if mem_dtype == torch.float16 and Q % 2 == 0 else torch.bfloat16
+    mem = (torch.randn(B, S, H, K, generator=g) * 0.3).to(mem_dtype)
+    idx = torch.randint(0, S, (B, Q, R), generator=g)
+    idx[0, 1, 0] = -1
+    idx[-1, -1, -1] = S
+    q = norm(torch.randn(B, Q, K, generator=g)).to(q_dtype)
+    gates = torch.softmax(torch.randn(B, Q, R, generator=g), dim=-1)
+    h = torch.randn(B, Q, H, generator=g).to(h_dtype)
+    w = (1 + 0.1 * torch.randn(H, generator=g)).to(h_dtype) if ln else None
+    b = (0.1 * torch.randn(H, generator=g)).to(h_dtype) if ln else None
+    print(f"retrieve_fuse B={B} Q={Q} S={S} R={R} H={H} K={K} mem {mem_dtype} q {q_dtype} h {h_dtype} ln={ln}",
+          flush=True)
+    D = lambda t: None if t is None else t.to(dev)  # noqa: E731
+    bad = torch.zeros(1, dtype=torch.int32, device=dev)
+    args = (D(mem), D(idx), D(q), D(gates), D(h), D(w), D(b))
+    out = capi.retrieve_fuse(*args, bad_count=bad)
+    out2 = capi.retrieve_fuse(*args)
+    rows = capi.gather_apply(D(mem), D(idx), D(q), dtype=torch.float32)
+    comp = capi.fuse_residual(D(h).reshape(B * Q, H), rows.reshape(B * Q, R, H).to(h_dtype),
+                              D(gates).reshape(B * Q, R), D(w), D(b)).reshape(B, Q, H)
+    torch.cuda.synchronize()
+    assert out.dtype == h_dtype and out.shape == (B, Q, H)
+    assert int(bad.item()) == 2
+    assert torch.equal(out, out2), "retrieve_fuse is not deterministic"
+    ref = _retrieve_fuse_ref(mem, idx, q, gates, h, w, b)
+    got = out.float().cpu().double().numpy()
+    np.testing.assert_allclose(got, ref, rtol=2e-2, atol=2e-3)
+    if h_dtype == torch.float32:
+        err = np.abs(got - ref).max() / max(np.abs(ref).max(), 1e-30)
+        assert err < 2e-3, err
+        torch.testing.assert_close(out, comp, rtol=2e-3, atol=2e-3)
+
+
+def test_retrieve_fuse_op_and_model_path(dev):
+    """torch.ops.grm_cuda.retrieve_fuse on [B, Q, ...] tensors equals capi.retrieve_fuse, runs no
+    generic path, and its unsupported inputs (float32 queries) take the two-kernel HIP
+    composition with the same result as gather_apply + fuse_residual."""
+    from rnn_with_grm_amd import cuda_ops
+
+    g = torch.Generator().manual_seed(41)
+    B, Q, S, R, H, K = 2, 100, 20, 8, 256, 64
+    mem = (torch.randn(B, S, H, K, generator=g) * 0.1).to(dev)
+    idx = torch.randint(0, S, (B, Q, R), generator=g).to(dev)
+    q = norm(torch.randn(B, Q, K, generator=g)).to(torch.bfloat16).to(dev)
+    gates = torch.softmax(torch.randn(B, Q, R, generator=g), -1).to(dev)
+    h = torch.randn(B, Q, H, generator=g).to(dev)
+    w, b = torch.ones(H, device=dev), torch.zeros(H, device=dev)
+    ext = cuda_ops.extension_module()
+    generic = ext.generic_path_calls()
+    with torch.no_grad():
+        a = cuda_ops.cuda_retrieve_fuse(mem, idx, q, gates, h, w, b)
+    c = capi.retrieve_fuse(mem, idx, q, gates, h, w, b)
+    assert torch.equal(a, c) and ext.generic_path_calls() == generic
+    qf = q.float()
+    with torch.no_grad():
+        d = cuda_ops.cuda_retrieve_fuse(mem, idx, qf, gates, h, w, b)
+    rows = capi.gather_apply(mem, idx, qf, dtype=torch.float32)
+    e = capi.fuse_residual(h.reshape(B * Q, H), rows.reshape(B * Q, R, H), gates.reshape(B * Q, R), w, b)
+    assert torch.equal(d, e.reshape(B, Q, H))
