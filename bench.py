@@ -568,8 +568,15 @@ class SegmentMemoryLM:
             m.to(device=dev, dtype=torch.bfloat16).eval()
 
     def __call__(self, ids):
-        out, _, _, _ = self.grm(self.embedding(ids), reset_memory=True)
-        return self.head(out)
+        from rnn_with_grm_amd import segment_model
+
+        x = self.embedding(ids)
+        segment_model._mark("embedding", x)
+        out, _, _, _ = self.grm(x, reset_memory=True)
+        segment_model._mark("other (between phases)", out)
+        logits = self.head(out)
+        segment_model._mark("LM head GEMM (512 -> 32000)", logits)
+        return logits
 
 
 def bench_c4_model(torch, dev, steps, warmup):
@@ -584,8 +591,18 @@ def bench_c4_model(torch, dev, steps, warmup):
         logits = lm(ids)
         assert logits.shape == (B, T, 32000) and torch.isfinite(logits.float()).all(), "c4 forward not finite"
         wall, per = timed_launches(torch, lambda: lm(ids), max(3, min(steps, 10)), max(1, min(warmup, 3)), stream)
+        # Per-phase breakdown of one more forward, from events at the phase boundaries
+        # (summed over the 4 layers); the timed forwards above record none.
+        from rnn_with_grm_amd import segment_model
+
+        segment_model.PHASE_EVENTS = []
+        segment_model._mark("start", ids)
+        lm(ids)
+        torch.cuda.synchronize()
+        phases = segment_model.phase_times_ms()
+        segment_model.PHASE_EVENTS = None
     ms = statistics.mean(per) * 1e3
-    return {"ms": ms, "tokens": B * T}
+    return {"ms": ms, "tokens": B * T, "phases_ms": phases}
 
 
 def host_cpu_info():
@@ -867,8 +884,12 @@ def main() -> int:
             "what": "config 4 LM forward, bf16 weights, random init: Embedding -> 4 x SegmentRecurrentMemoryLayer "
                     "(hidden 512, d_k 64, segment 64, capacity 64, top-8, float16 archive) -> Linear(512, 32000); "
                     "whole-sequence launches per layer, archive reset each forward",
-            "ms": round(m4["ms"], 3), "tokens/s": round(m4["tokens"] / m4["ms"] * 1e3)}
+            "ms": round(m4["ms"], 3), "tokens/s": round(m4["tokens"] / m4["ms"] * 1e3),
+            "breakdown_ms": {k: round(v, 3) for k, v in sorted(m4["phases_ms"].items(), key=lambda kv: -kv[1])},
+            "breakdown_note": "one extra forward with events at the phase boundaries, summed over the 4 layers"}
         log(f"c4 forward: {m4['ms']:.2f} ms, {m4['tokens'] / m4['ms'] * 1e3:.3e} tokens/s")
+        for k, v in sorted(m4["phases_ms"].items(), key=lambda kv: -kv[1]):
+            log(f"  c4 phase {k}: {v:.3f} ms")
 
     if not a.no_gather:
         pub = bench_published(torch, dev)

@@ -209,8 +209,9 @@ int grm_hip_gather_apply(const void* memories, const int64_t* indices, const voi
  * when bad_index_count is not NULL, increment that device int32 counter.
  * memories [batch, segments, value_dim, key_dim] mem_dtype (float32 with bf16 queries,
  * or 16-bit); queries [batch, n_query, key_dim] bf16 (f16 with f16 memories); gates
- * [batch, n_query, routes] float32; h_online and out [batch, n_query, value_dim] and
- * ln_weight / ln_bias [value_dim] are h_dtype, ln_weight NULL for no LayerNorm,
+ * [batch, n_query, routes] float32; h_online and out [batch, n_query, value_dim] are
+ * h_dtype (the sum and the LayerNorm run in float32, out is rounded once);
+ * ln_weight / ln_bias [value_dim] are float32, ln_weight NULL for no LayerNorm,
  * ln_bias NULL for none; 16-byte aligned.
  * workspace: grm_hip_retrieve_fuse_workspace(batch, segments, n_query * routes,
  * value_dim) bytes, contents need not be initialised.
@@ -223,6 +224,36 @@ int grm_hip_retrieve_fuse(const void* memories, const int64_t* indices, const vo
                           void* workspace, int64_t workspace_bytes, int64_t batch, int64_t segments,
                           int64_t n_query, int64_t routes, int64_t value_dim, int64_t key_dim, int mem_dtype,
                           int q_dtype, int h_dtype, float eps, int32_t* bad_index_count, void* stream);
+
+/*
+ * Split of the concatenated projection rows of LinearMemoryCell.project,
+ * proj [rows, key_dim | value_dim | key_dim | extra_dim] (one GEMM over the
+ * key, value, query and an extra projection's weights), into contiguous
+ * keys / queries [rows, key_dim], L2-normalised as F.normalize(p=2, eps)
+ * (reference grm/core/paper_grm.py:491-493; the norm and its eps clamp are
+ * rounded to dtype before the division, as F.normalize does on a 16-bit row),
+ * values [rows, value_dim] and extra [rows, extra_dim] (the gating query
+ * projection of paper_grm.py:570-574; NULL when extra_dim is 0), copied.
+ * One pass over the rows in place of the split views' copies and two
+ * normalisations of several launches each.  dtype for every buffer.
+ * Limits: dims multiples of 8, 16-byte aligned buffers.
+ */
+int grm_hip_project_split(const void* proj, void* keys, void* values, void* queries, void* extra, int64_t rows,
+                          int64_t key_dim, int64_t value_dim, int64_t extra_dim, int dtype, float eps,
+                          void* stream);
+
+/*
+ * out = LayerNorm(x + residual) over rows of hidden_size: the block output of
+ * SegmentRecurrentMemoryLayer, layer_norm(outputs + x)
+ * (reference grm/core/multilayer_grm.py:92-97), in one pass.  x, residual and out
+ * are dtype; x + residual is rounded to dtype first (the torch add), then the
+ * statistics and the affine map run in float32.  weight / bias [hidden_size] are
+ * param_dtype; weight NULL for no affine map, bias NULL for none.
+ * Limits: hidden_size a multiple of 8 and <= 2048, 16-byte aligned buffers.
+ */
+int grm_hip_residual_layer_norm(const void* x, const void* residual, const void* weight, const void* bias,
+                                void* out, int64_t rows, int64_t hidden_size, int dtype, int param_dtype,
+                                float eps, void* stream);
 
 /*
  * Segment routing: dot-product score, top-k and softmax gates.

@@ -29,7 +29,7 @@ LIB_EXT = PKG_DIR / "grm_cuda_ext.so"
 
 OFFLOAD_ARCH = "gfx950"
 HIP_SOURCES = ["grm_capi.hip", "chunk_scan.hip", "chunk_scan_wide.hip", "chunk_scan_vsplit.hip", "chunk_bwd.hip",
-               "gather_apply.hip", "retrieve.hip", "route_fuse.hip", "route_select.hip"]
+               "gather_apply.hip", "retrieve.hip", "route_fuse.hip", "route_select.hip", "layer_glue.hip"]
 EXT_SOURCE = "grm_torch_ops.cpp"
 
 # Packed fp32 instructions are kept out of every kernel (the flag is for the

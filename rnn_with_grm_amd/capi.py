@@ -42,6 +42,8 @@ SIGNATURES = {
     "grm_hip_gather_apply_workspace": (_I, [_I, _I, _I]),
     "grm_hip_gather_apply": (_C, [_P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _C, _C, _C, _P, _P]),
     "grm_hip_retrieve_fuse_workspace": (_I, [_I, _I, _I, _I]),
+    "grm_hip_project_split": (_C, [_P, _P, _P, _P, _P, _I, _I, _I, _I, _C, ctypes.c_float, _P]),
+    "grm_hip_residual_layer_norm": (_C, [_P, _P, _P, _P, _P, _I, _I, _C, _C, ctypes.c_float, _P]),
     "grm_hip_retrieve_fuse": (_C, [_P, _P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _C, _C, _C,
                                    ctypes.c_float, _P, _P]),
     "grm_hip_topk_route": (_C, [_P, _P, _P, _P, _P, _I, _I, _I, _I, _C, _I, ctypes.c_float, ctypes.c_float, _P]),
@@ -241,6 +243,31 @@ def retrieve_fuse(memories, indices, queries, gates, h_online, ln_weight=None, l
                                       dtype_code(memories.dtype), dtype_code(queries.dtype),
                                       dtype_code(h_online.dtype), float(eps), _ptr(bad_count), _stream(memories))
     _check(rc, "grm_hip_retrieve_fuse")
+    return out
+
+
+def project_split(proj, key_dim: int, value_dim: int, extra_dim: int = 0, eps: float = 1e-6):
+    """(keys, values, queries, extra) from [..., key_dim + value_dim + key_dim + extra_dim] rows;
+    keys and queries L2-normalised."""
+    lead = proj.shape[:-1]
+    rows = int(proj.numel() // proj.shape[-1]) if proj.shape[-1] else 0
+    mk = lambda d: torch.empty(lead + (d,), dtype=proj.dtype, device=proj.device)  # noqa: E731
+    k, v, q = mk(key_dim), mk(value_dim), mk(key_dim)
+    e = mk(extra_dim) if extra_dim else None
+    rc = load().grm_hip_project_split(_ptr(proj), _ptr(k), _ptr(v), _ptr(q), _ptr(e), rows, key_dim, value_dim,
+                                      extra_dim, dtype_code(proj.dtype), float(eps), _stream(proj))
+    _check(rc, "grm_hip_project_split")
+    return k, v, q, e
+
+
+def residual_layer_norm(x, residual, weight=None, bias=None, eps: float = 1e-5, out=None):
+    H = x.shape[-1]
+    out = torch.empty_like(x) if out is None else out
+    pd = dtype_code(weight.dtype) if weight is not None else dtype_code(x.dtype)
+    rc = load().grm_hip_residual_layer_norm(_ptr(x), _ptr(residual), _ptr(weight), _ptr(bias), _ptr(out),
+                                            int(x.numel() // H) if H else 0, H, dtype_code(x.dtype), pd, float(eps),
+                                            _stream(x))
+    _check(rc, "grm_hip_residual_layer_norm")
     return out
 
 

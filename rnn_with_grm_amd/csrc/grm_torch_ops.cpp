@@ -2,13 +2,15 @@
 //
 // The five schemas are the reference's, character for character
 // (reference grm/csrc/bindings.cpp:5-11), so grm.core.cuda_ops and every model
-// above it bind to this library unchanged.  Six more ops live in the same
+// above it bind to this library unchanged.  Eight more ops live in the same
 // namespace: segment_scan_forward (whole-sequence update with per-segment
 // state snapshots), topk_route (score -> top-k -> softmax), segment_route (the
 // same routing for every segment of a sequence against the archive as it
 // grows), fuse_residual, gather_apply (gather + query application without
-// materialising the states) and retrieve_fuse (gather_apply, the gate-weighted
-// sum and fuse_residual in one call).
+// materialising the states), retrieve_fuse (gather_apply, the gate-weighted
+// sum and fuse_residual in one call), and the layer glue project_split (the
+// projection's split with L2-normalised keys and queries) and
+// residual_layer_norm (the block's LayerNorm(out + x)).
 //
 // CUDA-key kernels (HIP devices dispatch on the CUDA key in PyTorch-ROCm)
 // check the inputs, allocate outputs with ATen on the input's device and call
@@ -398,9 +400,33 @@ Tensor retrieve_fuse_generic(const Tensor& memories, const Tensor& indices, cons
   check_retrieve_fuse_inputs(memories, indices, queries, gates, h);
   const int64_t B = h.size(0), Q = h.size(1), H = h.size(2), R = indices.size(2);
   Tensor r = gather_apply_generic(memories, indices, queries, at::kFloat).reshape({B * Q, R, H});
-  return fuse_residual_generic(h.reshape({B * Q, H}), r.to(h.scalar_type()), gates.reshape({B * Q, R}), weight, bias,
-                               eps)
+  // float32 sum and LayerNorm, one rounding to h's dtype at the end
+  return fuse_residual_generic(h.reshape({B * Q, H}).to(at::kFloat), r, gates.reshape({B * Q, R}), weight, bias, eps)
+      .to(h.scalar_type())
       .reshape({B, Q, H});
+}
+
+// project_split: LinearMemoryCell.project's split of the concatenated
+// projection, F.normalize of keys and queries (paper_grm.py:491-493).
+void check_project_split(const Tensor& proj, int64_t dk, int64_t dv, int64_t de) {
+  TORCH_CHECK(proj.dim() >= 1 && dk >= 0 && dv >= 0 && de >= 0 && proj.size(-1) == 2 * dk + dv + de,
+              "project_split: last dim must be key_dim + value_dim + key_dim + extra_dim");
+}
+
+std::tuple<Tensor, Tensor, Tensor, Tensor> project_split_generic(const Tensor& proj, int64_t key_dim,
+                                                                 int64_t value_dim, int64_t extra_dim, double eps) {
+  check_project_split(proj, key_dim, value_dim, extra_dim);
+  auto parts = proj.split_with_sizes({key_dim, value_dim, key_dim, extra_dim}, -1);
+  auto normalise = [&](const Tensor& t) { return (t / t.norm(2, {-1}, true).clamp_min(eps)).contiguous(); };
+  return {normalise(parts[0]), parts[1].contiguous(), normalise(parts[2]), parts[3].contiguous()};
+}
+
+// residual_layer_norm: layer_norm(x + residual) (multilayer_grm.py:92-97).
+Tensor residual_layer_norm_generic(const Tensor& x, const Tensor& residual, const c10::optional<Tensor>& weight,
+                                   const c10::optional<Tensor>& bias, double eps) {
+  TORCH_CHECK(x.sizes() == residual.sizes() && x.dim() >= 1, "residual_layer_norm: x and residual must match");
+  return at::layer_norm(x + residual, {x.size(-1)}, weight.has_value() ? *weight : Tensor(),
+                        bias.has_value() ? *bias : Tensor(), eps);
 }
 
 // ---------------------------------------------------------------------------
@@ -801,19 +827,23 @@ Tensor retrieve_fuse_hip(const Tensor& memories, const Tensor& indices, const Te
                    (queries.scalar_type() == at::kHalf && memories.scalar_type() == at::kHalf);
   bool ok = same_cuda_device({&memories, &indices, &queries, &gates, &h}) && md >= 0 && qd >= 0 && hd >= 0 && q16 &&
             K <= 128 && (K * 2) % 16 == 0 && H % 8 == 0 && H <= 2048 && S <= 16384 && B <= 65535;
-  if (has_w) ok = ok && weight->is_cuda() && weight->scalar_type() == h.scalar_type();
-  if (has_b) ok = ok && has_w && bias->is_cuda() && bias->scalar_type() == h.scalar_type();
+  if (has_w) ok = ok && weight->is_cuda() && weight->numel() == H;
+  if (has_b) ok = ok && has_w && bias->is_cuda() && bias->numel() == H;
   if (!ok) {
     // The two-kernel composition (gather_apply in float32, then fuse_residual).
     const Tensor r = gather_apply_hip(memories, indices, queries, at::kFloat).reshape({B * Q, R, H});
-    return fuse_residual_hip(h.reshape({B * Q, H}), r.to(h.scalar_type()), gates.reshape({B * Q, R}), weight, bias,
-                             eps)
+    c10::optional<Tensor> wf, bf;
+    if (has_w) wf = weight->to(at::kFloat);
+    if (has_b) bf = bias->to(at::kFloat);
+    return fuse_residual_hip(h.reshape({B * Q, H}).to(at::kFloat), r, gates.reshape({B * Q, R}), wf, bf, eps)
+        .to(h.scalar_type())
         .reshape({B, Q, H});
   }
   c10::OptionalDeviceGuard guard(memories.device());
   Tensor mm = memories.contiguous(), idx = indices.to(at::kLong).contiguous(), q = queries.contiguous();
   Tensor gc = gates.to(at::kFloat).contiguous(), hc = h.contiguous();
-  Tensor wc = has_w ? weight->contiguous() : Tensor(), bc = has_b ? bias->contiguous() : Tensor();
+  Tensor wc = has_w ? weight->to(at::kFloat).contiguous() : Tensor();
+  Tensor bc = has_b ? bias->to(at::kFloat).contiguous() : Tensor();
   if (!aligned16(mm) || !aligned16(q) || !aligned16(hc) || (has_w && !aligned16(wc)) || (has_b && !aligned16(bc))) {
     mm = mm.clone();
     q = q.clone();
@@ -837,6 +867,64 @@ Tensor retrieve_fuse_hip(const Tensor& memories, const Tensor& indices, const Te
     const int64_t nbad = bad.item<int32_t>();
     TORCH_CHECK_INDEX(nbad == 0, "retrieve_fuse: ", nbad, " index values outside [0, ", S, ")");
   }
+  return out;
+}
+
+std::tuple<Tensor, Tensor, Tensor, Tensor> project_split_hip(const Tensor& proj, int64_t key_dim, int64_t value_dim,
+                                                             int64_t extra_dim, double eps) {
+  check_project_split(proj, key_dim, value_dim, extra_dim);
+  const int dt = dtype_code(proj.scalar_type());
+  if (!proj.is_cuda() || dt < 0 || key_dim % 8 || value_dim % 8 || extra_dim % 8) {
+    if (proj.is_cuda()) g_generic_calls.fetch_add(1);
+    return project_split_generic(proj, key_dim, value_dim, extra_dim, eps);
+  }
+  c10::OptionalDeviceGuard guard(proj.device());
+  Tensor p = proj.contiguous();
+  if (!aligned16(p)) p = p.clone();
+  auto lead = p.sizes().vec();
+  lead.pop_back();
+  auto mk = [&](int64_t d) {
+    auto shape = lead;
+    shape.push_back(d);
+    return at::empty(shape, p.options());
+  };
+  Tensor k = mk(key_dim), v = mk(value_dim), q = mk(key_dim), e = mk(extra_dim);
+  const int64_t rows = p.size(-1) > 0 ? p.numel() / p.size(-1) : 0;
+  check_rc(grm_hip_project_split(p.data_ptr(), k.data_ptr(), v.data_ptr(), q.data_ptr(),
+                                 extra_dim > 0 ? e.data_ptr() : nullptr, rows, key_dim, value_dim, extra_dim, dt,
+                                 static_cast<float>(eps), current_stream(p)),
+           "project_split");
+  return {k, v, q, e};
+}
+
+Tensor residual_layer_norm_hip(const Tensor& x, const Tensor& residual, const c10::optional<Tensor>& weight,
+                               const c10::optional<Tensor>& bias, double eps) {
+  TORCH_CHECK(x.sizes() == residual.sizes() && x.dim() >= 1, "residual_layer_norm: x and residual must match");
+  const bool has_w = weight.has_value() && weight->defined();
+  const bool has_b = bias.has_value() && bias->defined();
+  const int dt = dtype_code(x.scalar_type());
+  const int pd = has_w ? dtype_code(weight->scalar_type()) : dt;
+  const int64_t H = x.size(-1);
+  bool ok = same_cuda_device({&x, &residual}) && residual.scalar_type() == x.scalar_type() && dt >= 0 && pd >= 0 &&
+            H % 8 == 0 && H <= 2048;
+  if (has_w) ok = ok && weight->is_cuda() && weight->numel() == H;
+  if (has_b) ok = ok && has_w && bias->is_cuda() && bias->numel() == H && bias->scalar_type() == weight->scalar_type();
+  if (!ok) {
+    if (x.is_cuda()) g_generic_calls.fetch_add(1);
+    return residual_layer_norm_generic(x, residual, weight, bias, eps);
+  }
+  c10::OptionalDeviceGuard guard(x.device());
+  Tensor xc = x.contiguous(), rc = residual.contiguous();
+  Tensor wc = has_w ? weight->contiguous() : Tensor(), bc = has_b ? bias->contiguous() : Tensor();
+  if (!aligned16(xc)) xc = xc.clone();
+  if (!aligned16(rc)) rc = rc.clone();
+  if (has_w && !aligned16(wc)) wc = wc.clone();
+  if (has_b && !aligned16(bc)) bc = bc.clone();
+  Tensor out = at::empty_like(xc);
+  check_rc(grm_hip_residual_layer_norm(xc.data_ptr(), rc.data_ptr(), has_w ? wc.data_ptr() : nullptr,
+                                       has_b ? bc.data_ptr() : nullptr, out.data_ptr(), xc.numel() / H, H, dt, pd,
+                                       static_cast<float>(eps), current_stream(xc)),
+           "residual_layer_norm");
   return out;
 }
 
@@ -867,6 +955,8 @@ TORCH_LIBRARY(grm_cuda, m) {
   m.def("gather_apply(Tensor memories, Tensor indices, Tensor queries, ScalarType? dtype=None) -> Tensor");
   m.def("segment_route(Tensor queries, Tensor keys, int top_k, int segment_len, int base, int capacity, float scale, float temperature) -> (Tensor gates, Tensor indices, Tensor scores)");
   m.def("retrieve_fuse(Tensor memories, Tensor indices, Tensor queries, Tensor gates, Tensor h_online, Tensor? weight, Tensor? bias, float eps) -> Tensor");
+  m.def("project_split(Tensor proj, int key_dim, int value_dim, int extra_dim, float eps) -> (Tensor keys, Tensor values, Tensor queries, Tensor extra)");
+  m.def("residual_layer_norm(Tensor x, Tensor residual, Tensor? weight, Tensor? bias, float eps) -> Tensor");
 }
 
 TORCH_LIBRARY_IMPL(grm_cuda, CPU, m) {
@@ -882,6 +972,8 @@ TORCH_LIBRARY_IMPL(grm_cuda, CPU, m) {
   m.impl("gather_apply", grm::gather_apply_generic);
   m.impl("segment_route", grm::segment_route_cpu);
   m.impl("retrieve_fuse", grm::retrieve_fuse_generic);
+  m.impl("project_split", grm::project_split_generic);
+  m.impl("residual_layer_norm", grm::residual_layer_norm_generic);
 }
 
 TORCH_LIBRARY_IMPL(grm_cuda, CUDA, m) {
@@ -897,6 +989,8 @@ TORCH_LIBRARY_IMPL(grm_cuda, CUDA, m) {
   m.impl("gather_apply", grm::gather_apply_hip);
   m.impl("segment_route", grm::segment_route_hip);
   m.impl("retrieve_fuse", grm::retrieve_fuse_hip);
+  m.impl("project_split", grm::project_split_hip);
+  m.impl("residual_layer_norm", grm::residual_layer_norm_hip);
 }
 
 PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {

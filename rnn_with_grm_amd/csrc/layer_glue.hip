@@ -1,0 +1,315 @@
+// Per-layer glue of the whole-sequence models, gfx950: the passes around the
+// projection GEMM and after the layer's output, each one read and one write of
+// the rows instead of a chain of elementwise launches.
+//
+//   project_split        the concatenated k | v | q | extra projection output of
+//                        LinearMemoryCell.project (reference grm/core/paper_grm.py:
+//                        491-493: key_proj / value_proj / query_proj, F.normalize of
+//                        keys and queries; 570-574: the gating query projection) ->
+//                        contiguous keys and queries L2-normalised, values and extra.
+//   residual_layer_norm  LayerNorm(x + residual), SegmentRecurrentMemoryLayer's
+//                        block output (grm/core/multilayer_grm.py:92-97).
+//
+// Both follow the rounding of the torch ops they replace for 16-bit rows: the
+// norm and its eps clamp are rounded to the row dtype before the division
+// (F.normalize divides by a norm tensor of that dtype), and x + residual is
+// rounded to the row dtype before the LayerNorm, whose statistics are float32.
+// One wavefront per row, 16-byte accesses.
+#include <stdint.h>
+#include <string.h>
+
+#include "grm_hip.h"
+#include "grm_hip_common.h"
+
+namespace grmhip {
+namespace {
+
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+constexpr int GL_THREADS = 256;  // 4 rows per workgroup
+
+template <class E>
+__device__ __forceinline__ float round_to(float x) {
+  return ET<E>::to_f(ET<E>::from_f(x));
+}
+
+// Eight elements at byte offset off of a buffer as float (zeros past its end).
+template <class E>
+__device__ __forceinline__ void ld8(__amdgpu_buffer_rsrc_t r, int off, float (&f)[8]) {
+  if constexpr (sizeof(typename ET<E>::raw) == 2) {
+    const U8<E> u = __builtin_bit_cast(U8<E>, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0));
+#pragma unroll
+    for (int e = 0; e < 8; ++e) f[e] = ET<E>::to_f(u.e[e]);
+  } else {
+    const u32x4 lo = __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0);
+    const u32x4 hi = __builtin_amdgcn_raw_buffer_load_b128(r, off == kBufOOB ? kBufOOB : off + 16, 0, 0);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      f[e] = __uint_as_float(lo[e]);
+      f[4 + e] = __uint_as_float(hi[e]);
+    }
+  }
+}
+
+template <class E>
+__device__ __forceinline__ void st8(__amdgpu_buffer_rsrc_t r, int off, const float (&y)[8]) {
+  if constexpr (sizeof(typename ET<E>::raw) == 2) {
+    const u32x4 q = u32x4{pack2<E>(y[0], y[1]), pack2<E>(y[2], y[3]), pack2<E>(y[4], y[5]), pack2<E>(y[6], y[7])};
+    __builtin_amdgcn_raw_buffer_store_b128(q, r, off, 0, 0);
+  } else {
+    __builtin_amdgcn_raw_buffer_store_b128(
+        u32x4{__float_as_uint(y[0]), __float_as_uint(y[1]), __float_as_uint(y[2]), __float_as_uint(y[3])}, r, off, 0, 0);
+    __builtin_amdgcn_raw_buffer_store_b128(
+        u32x4{__float_as_uint(y[4]), __float_as_uint(y[5]), __float_as_uint(y[6]), __float_as_uint(y[7])}, r,
+        off == kBufOOB ? kBufOOB : off + 16, 0, 0);
+  }
+}
+
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
+  return v;
+}
+
+struct SplitArgs {
+  const void* proj;
+  void* keys;
+  void* values;
+  void* queries;
+  void* extra;
+  int64_t rows;
+  int dk, dv, de;  // multiples of 8
+  float eps;
+};
+
+// One row segment [c0, c0 + n) of the projection row into out (n a multiple of 8),
+// L2-normalised when NORM.
+template <class E, bool NORM>
+__device__ __forceinline__ void split_segment(const SplitArgs& a, int64_t row, int lane, int c0, int n, void* out) {
+  using raw = typename ET<E>::raw;
+  constexpr int ES = sizeof(raw);
+  const int W = 2 * a.dk + a.dv + a.de;
+  const __amdgpu_buffer_rsrc_t rs = make_rsrc(static_cast<const raw*>(a.proj) + row * W + c0, n * ES);
+  const __amdgpu_buffer_rsrc_t rd = make_rsrc(static_cast<raw*>(out) + row * n, n * ES);
+  const int units = n / 8;
+  if constexpr (!NORM) {
+    for (int u = lane; u < units; u += 64) {
+      float x[8];
+      ld8<E>(rs, u * 8 * ES, x);
+      st8<E>(rd, u * 8 * ES, x);
+    }
+  } else {
+    float ss = 0.f;
+    for (int u = lane; u < units; u += 64) {
+      float x[8];
+      ld8<E>(rs, u * 8 * ES, x);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) ss = fmaf(x[e], x[e], ss);
+    }
+    ss = wave_sum(ss);
+    // x / clamp_min(||x||, eps) with the norm and the clamp in the row dtype
+    const float den = round_to<E>(fmaxf(round_to<E>(sqrtf(ss)), a.eps));
+    for (int u = lane; u < units; u += 64) {
+      float x[8];
+      ld8<E>(rs, u * 8 * ES, x);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) x[e] = x[e] / den;
+      st8<E>(rd, u * 8 * ES, x);
+    }
+  }
+}
+
+template <class E>
+__global__ __launch_bounds__(GL_THREADS) void project_split_kernel(const SplitArgs a) {
+  const int lane = threadIdx.x & 63;
+  const int64_t row = static_cast<int64_t>(blockIdx.x) * (GL_THREADS / 64) + (threadIdx.x >> 6);
+  if (row >= a.rows) return;  // wave-uniform
+  split_segment<E, true>(a, row, lane, 0, a.dk, a.keys);
+  split_segment<E, false>(a, row, lane, a.dk, a.dv, a.values);
+  split_segment<E, true>(a, row, lane, a.dk + a.dv, a.dk, a.queries);
+  if (a.de > 0) split_segment<E, false>(a, row, lane, 2 * a.dk + a.dv, a.de, a.extra);
+}
+
+struct ResLnArgs {
+  const void* x;
+  const void* res;
+  const void* w;
+  const void* b;
+  void* out;
+  int64_t rows;
+  int hidden;  // multiple of 8, at most 64 * 8 * RLN_MAX
+  float eps;
+};
+
+constexpr int RLN_MAX = 4;  // 16-byte units per lane: hidden <= 2048
+
+template <class E, class P>
+__global__ __launch_bounds__(GL_THREADS) void residual_layer_norm_kernel(const ResLnArgs a) {
+  using raw = typename ET<E>::raw;
+  using rawp = typename ET<P>::raw;
+  constexpr int ES = sizeof(raw), PS = sizeof(rawp);
+  const int lane = threadIdx.x & 63;
+  const int64_t row = static_cast<int64_t>(blockIdx.x) * (GL_THREADS / 64) + (threadIdx.x >> 6);
+  if (row >= a.rows) return;  // wave-uniform
+  const int H = a.hidden, units = H / 8;
+  const __amdgpu_buffer_rsrc_t rx = make_rsrc(static_cast<const raw*>(a.x) + row * H, H * ES);
+  const __amdgpu_buffer_rsrc_t rr = make_rsrc(static_cast<const raw*>(a.res) + row * H, H * ES);
+  float s[RLN_MAX][8];
+  float sum = 0.f;
+#pragma unroll
+  for (int i = 0; i < RLN_MAX; ++i) {
+    const int u = lane + 64 * i;
+    const int off = u < units ? u * 8 * ES : kBufOOB;
+    float xv[8], rv[8];
+    ld8<E>(rx, off, xv);
+    ld8<E>(rr, off, rv);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      s[i][e] = round_to<E>(xv[e] + rv[e]);  // x + residual in the row dtype
+      sum += s[i][e];
+    }
+  }
+  const float mean = wave_sum(sum) / static_cast<float>(H);
+  float var = 0.f;
+#pragma unroll
+  for (int i = 0; i < RLN_MAX; ++i) {
+    const bool in = lane + 64 * i < units;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const float d = s[i][e] - mean;
+      var = in ? fmaf(d, d, var) : var;
+    }
+  }
+  const float rstd = 1.0f / sqrtf(wave_sum(var) / static_cast<float>(H) + a.eps);
+  const __amdgpu_buffer_rsrc_t rw = make_rsrc(a.w, a.w != nullptr ? H * PS : 0u);
+  const __amdgpu_buffer_rsrc_t rb = make_rsrc(a.b, a.b != nullptr ? H * PS : 0u);
+  const __amdgpu_buffer_rsrc_t ro = make_rsrc(static_cast<raw*>(a.out) + row * H, H * ES);
+#pragma unroll
+  for (int i = 0; i < RLN_MAX; ++i) {
+    const int u = lane + 64 * i;
+    if (u >= units) continue;
+    float wv[8], bv[8], y[8];
+    ld8<P>(rw, u * 8 * PS, wv);
+    ld8<P>(rb, u * 8 * PS, bv);  // zeros without a bias
+#pragma unroll
+    for (int e = 0; e < 8; ++e) y[e] = (s[i][e] - mean) * rstd * (a.w != nullptr ? wv[e] : 1.f) + bv[e];
+    st8<E>(ro, u * 8 * ES, y);
+  }
+}
+
+bool aligned16(const void* p) { return reinterpret_cast<uintptr_t>(p) % 16 == 0; }
+
+}  // namespace
+}  // namespace grmhip
+
+using namespace grmhip;
+
+extern "C" int grm_hip_project_split(const void* proj, void* keys, void* values, void* queries, void* extra,
+                                     int64_t rows, int64_t key_dim, int64_t value_dim, int64_t extra_dim,
+                                     int dtype, float eps, void* stream) {
+  if (rows < 0 || key_dim < 0 || value_dim < 0 || extra_dim < 0) {
+    set_error("project_split: negative size");
+    return GRM_HIP_EINVAL;
+  }
+  if (dtype < GRM_HIP_F32 || dtype > GRM_HIP_BF16) {
+    set_error("project_split: unsupported dtype %d", dtype);
+    return GRM_HIP_EUNSUPPORTED;
+  }
+  if (key_dim % 8 || value_dim % 8 || extra_dim % 8) {
+    set_error("project_split: key_dim, value_dim and extra_dim must be multiples of 8");
+    return GRM_HIP_EUNSUPPORTED;
+  }
+  const int eb = dtype == GRM_HIP_F32 ? 4 : 2;
+  if ((2 * key_dim + value_dim + extra_dim) * eb > INT32_MAX / 2) {
+    set_error("project_split: rows too wide");
+    return GRM_HIP_EINVAL;
+  }
+  if (rows == 0) return GRM_HIP_OK;
+  if (proj == nullptr || keys == nullptr || values == nullptr || queries == nullptr ||
+      (extra_dim > 0 && extra == nullptr)) {
+    set_error("project_split: null pointer");
+    return GRM_HIP_EINVAL;
+  }
+  if (!aligned16(proj) || !aligned16(keys) || !aligned16(values) || !aligned16(queries) ||
+      (extra_dim > 0 && !aligned16(extra))) {
+    set_error("project_split: buffers must be 16-byte aligned");
+    return GRM_HIP_EUNSUPPORTED;
+  }
+  SplitArgs a;
+  a.proj = proj;
+  a.keys = keys;
+  a.values = values;
+  a.queries = queries;
+  a.extra = extra;
+  a.rows = rows;
+  a.dk = static_cast<int>(key_dim);
+  a.dv = static_cast<int>(value_dim);
+  a.de = static_cast<int>(extra_dim);
+  a.eps = eps;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const dim3 grid(static_cast<unsigned>((rows + GL_THREADS / 64 - 1) / (GL_THREADS / 64)));
+  switch (dtype) {
+    case GRM_HIP_F32: hipLaunchKernelGGL(project_split_kernel<F32>, grid, dim3(GL_THREADS), 0, s, a); break;
+    case GRM_HIP_F16: hipLaunchKernelGGL(project_split_kernel<F16>, grid, dim3(GL_THREADS), 0, s, a); break;
+    default: hipLaunchKernelGGL(project_split_kernel<BF16>, grid, dim3(GL_THREADS), 0, s, a); break;
+  }
+  return check_launch("project_split");
+}
+
+extern "C" int grm_hip_residual_layer_norm(const void* x, const void* residual, const void* weight,
+                                           const void* bias, void* out, int64_t rows, int64_t hidden_size,
+                                           int dtype, int param_dtype, float eps, void* stream) {
+  if (rows < 0 || hidden_size < 0) {
+    set_error("residual_layer_norm: negative size");
+    return GRM_HIP_EINVAL;
+  }
+  if (dtype < GRM_HIP_F32 || dtype > GRM_HIP_BF16 || param_dtype < GRM_HIP_F32 || param_dtype > GRM_HIP_BF16) {
+    set_error("residual_layer_norm: unsupported dtypes %d / %d", dtype, param_dtype);
+    return GRM_HIP_EUNSUPPORTED;
+  }
+  if (hidden_size % 8 || hidden_size > 64 * 8 * RLN_MAX) {
+    set_error("residual_layer_norm: hidden_size must be a multiple of 8 and at most %d", 64 * 8 * RLN_MAX);
+    return GRM_HIP_EUNSUPPORTED;
+  }
+  if (rows == 0 || hidden_size == 0) return GRM_HIP_OK;
+  if (x == nullptr || residual == nullptr || out == nullptr || (bias != nullptr && weight == nullptr)) {
+    set_error("residual_layer_norm: null pointer (a bias needs a weight)");
+    return GRM_HIP_EINVAL;
+  }
+  if (!aligned16(x) || !aligned16(residual) || !aligned16(out) || (weight != nullptr && !aligned16(weight)) ||
+      (bias != nullptr && !aligned16(bias))) {
+    set_error("residual_layer_norm: buffers must be 16-byte aligned");
+    return GRM_HIP_EUNSUPPORTED;
+  }
+  ResLnArgs a;
+  a.x = x;
+  a.res = residual;
+  a.w = weight;
+  a.b = bias;
+  a.out = out;
+  a.rows = rows;
+  a.hidden = static_cast<int>(hidden_size);
+  a.eps = eps;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const dim3 grid(static_cast<unsigned>((rows + GL_THREADS / 64 - 1) / (GL_THREADS / 64)));
+  auto go = [&](auto et) {
+    using E = decltype(et);
+    switch (param_dtype) {
+      case GRM_HIP_F32:
+        hipLaunchKernelGGL((residual_layer_norm_kernel<E, F32>), grid, dim3(GL_THREADS), 0, s, a);
+        break;
+      case GRM_HIP_F16:
+        hipLaunchKernelGGL((residual_layer_norm_kernel<E, F16>), grid, dim3(GL_THREADS), 0, s, a);
+        break;
+      default:
+        hipLaunchKernelGGL((residual_layer_norm_kernel<E, BF16>), grid, dim3(GL_THREADS), 0, s, a);
+        break;
+    }
+  };
+  switch (dtype) {
+    case GRM_HIP_F32: go(F32{}); break;
+    case GRM_HIP_F16: go(F16{}); break;
+    default: go(BF16{}); break;
+  }
+  return check_launch("residual_layer_norm");
+}

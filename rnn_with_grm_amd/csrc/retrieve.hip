@@ -827,6 +827,7 @@ int dispatch_q(const RetrieveArgs& a, int q_dtype, hipStream_t s) {
 // ---------------------------------------------------------------------------
 // Residual + LayerNorm over the scaled rows of retrieve_fuse:
 //   out[t] = LN(h[t] + sum_r scales[t, r, c / 128] * rows[t, r, c])
+// h and out in E, the LayerNorm weight and bias in float32,
 // with r in order 0 .. R-1 (the gates are already in the rows), a two-pass
 // mean / variance in fp32.  lpr lanes share a row, each covering NV groups of
 // 8 consecutive columns (16-byte float16 loads of the rows).
@@ -939,15 +940,15 @@ __global__ __launch_bounds__(256) void fuse_scaled_kernel(const FuseScaledArgs a
   }
   for (int off = lpr >> 1; off > 0; off >>= 1) var += __shfl_xor(var, off, 64);
   const float rstd = 1.0f / sqrtf(var / static_cast<float>(H) + a.eps);
-  const __amdgpu_buffer_rsrc_t rw = make_rsrc(a.w, H * sizeof(raw));
-  const __amdgpu_buffer_rsrc_t rb = make_rsrc(a.bias, a.bias != nullptr ? H * sizeof(raw) : 0u);
+  const __amdgpu_buffer_rsrc_t rw = make_rsrc(a.w, H * 4);
+  const __amdgpu_buffer_rsrc_t rb = make_rsrc(a.bias, a.bias != nullptr ? H * 4 : 0u);
 #pragma unroll
   for (int v = 0; v < NV; ++v) {
     const int c = (sub + lpr * v) * 8;
-    const int off = c < H ? c * static_cast<int>(sizeof(raw)) : kBufOOB;
+    const int off = c < H ? c * 4 : kBufOOB;
     float wv[8], bv[8];
-    load8<E>(rw, off, wv);
-    load8<E>(rb, off, bv);  // zeros without a bias
+    load8<F32>(rw, off, wv);  // LayerNorm parameters are float32
+    load8<F32>(rb, off, bv);  // zeros without a bias
     float y[8];
 #pragma unroll
     for (int e = 0; e < 8; ++e) y[e] = (x[v][e] - mean) * rstd * wv[e] + bv[e];

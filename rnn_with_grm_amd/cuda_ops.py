@@ -38,7 +38,7 @@ SCHEMA_OPS = (
     "batched_memory_gather",
 )
 EXTRA_OPS = ("segment_scan_forward", "topk_route", "fuse_residual", "gather_apply", "segment_route",
-             "retrieve_fuse", "apply_query_backward_queries")
+             "retrieve_fuse", "project_split", "residual_layer_norm", "apply_query_backward_queries")
 
 # Environment variables of the reference (cuda_ops.py:26-32): one per op and a global one.
 GLOBAL_POLICY_ENV = "GRM_CUDA_KERNEL_POLICY"
@@ -478,10 +478,40 @@ def cuda_retrieve_fuse(memories_per_batch: Tensor, topk_indices: Tensor, queries
     R = topk_indices.size(-1)
     retrieved = cuda_gather_apply(memories_per_batch, topk_indices, queries, torch.float32, enabled=enabled,
                                   debug_fallback=debug_fallback)
-    fused = cuda_fuse_residual(h_online.reshape(B * Q, H), retrieved.reshape(B * Q, R, H).to(h_online.dtype),
-                               gates.reshape(B * Q, R).to(h_online.dtype), weight, bias, eps, enabled=enabled,
+    fused = cuda_fuse_residual(h_online.reshape(B * Q, H).float(), retrieved.reshape(B * Q, R, H),
+                               gates.reshape(B * Q, R).float(), None if weight is None else weight.float(),
+                               None if bias is None else bias.float(), eps, enabled=enabled,
                                debug_fallback=debug_fallback)
-    return fused.reshape(B, Q, H)
+    return fused.reshape(B, Q, H).to(h_online.dtype)
+
+
+def cuda_project_split(proj: Tensor, key_dim: int, value_dim: int, extra_dim: int = 0, eps: float = 1e-6, *,
+                       enabled: bool = True, debug_fallback: bool = False) -> Tuple[Tensor, ...]:
+    """(keys, values, queries[, extra]) of the concatenated projection rows, keys and queries
+    F.normalize'd (paper_grm.py:491-493; the extra part is the gating query projection,
+    paper_grm.py:570-574).  Inference only: under autograd the split views and
+    F.normalize run."""
+    if not (torch.is_grad_enabled() and proj.requires_grad) and _run_native(
+            "project_split", proj.device, enabled=enabled, debug_fallback=debug_fallback):
+        k, v, q, e = torch.ops.grm_cuda.project_split(proj, int(key_dim), int(value_dim), int(extra_dim), float(eps))
+        return (k, v, q) + ((e,) if extra_dim else ())
+    parts = proj.split([key_dim, value_dim, key_dim, extra_dim], dim=-1)
+    k = torch.nn.functional.normalize(parts[0], p=2, dim=-1, eps=eps)
+    q = torch.nn.functional.normalize(parts[2], p=2, dim=-1, eps=eps)
+    return (k, parts[1], q) + ((parts[3],) if extra_dim else ())
+
+
+def cuda_residual_layer_norm(x: Tensor, residual: Tensor, weight: Optional[Tensor] = None,
+                             bias: Optional[Tensor] = None, eps: float = 1e-5, *, enabled: bool = True,
+                             debug_fallback: bool = False) -> Tensor:
+    """layer_norm(x + residual) (multilayer_grm.py:92-97).  Inference only: under autograd
+    the add and torch's layer_norm run."""
+    needs_grad = torch.is_grad_enabled() and any(
+        t is not None and t.requires_grad for t in (x, residual, weight, bias))
+    if not needs_grad and _run_native("residual_layer_norm", x.device, enabled=enabled,
+                                      debug_fallback=debug_fallback):
+        return torch.ops.grm_cuda.residual_layer_norm(x, residual, weight, bias, float(eps))
+    return torch.nn.functional.layer_norm(x + residual, (x.size(-1),), weight, bias, eps)
 
 
 __all__ = [
@@ -491,6 +521,8 @@ __all__ = [
     "cuda_chunk_update",
     "cuda_fuse_residual",
     "cuda_gather_apply",
+    "cuda_project_split",
+    "cuda_residual_layer_norm",
     "cuda_retrieve_fuse",
     "cuda_segment_route",
     "cuda_segment_scan",

@@ -62,6 +62,28 @@ from .archive import DeviceSegmentArchive, SegmentCheckpoint
 
 _NORM_EPS = 1e-6
 
+# Phase timing for benchmarks: when a list, every phase boundary of the
+# whole-sequence forward appends (name, event) with an event recorded on the
+# current stream; None (the default) records nothing.
+PHASE_EVENTS: Optional[List[Tuple[str, Any]]] = None
+
+
+def _mark(name: str, like: Tensor) -> None:
+    if PHASE_EVENTS is not None and like.is_cuda:
+        ev = torch.cuda.Event(enable_timing=True)
+        ev.record()
+        PHASE_EVENTS.append((name, ev))
+
+
+def phase_times_ms() -> Dict[str, float]:
+    """Milliseconds per phase name between consecutive marks of PHASE_EVENTS (after a
+    synchronisation), summed over layers."""
+    out: Dict[str, float] = {}
+    evs = PHASE_EVENTS or []
+    for (_, e0), (name, e1) in zip(evs, evs[1:]):
+        out[name] = out.get(name, 0.0) + e0.elapsed_time(e1)
+    return out
+
 
 @dataclass
 class LinearMemoryState:
@@ -142,15 +164,30 @@ class LinearMemoryCell(nn.Module):
         GEMM over the concatenated weights; `extra` (a Linear on the same input)
         joins the same GEMM and its output is returned last."""
         mods = [self.key_proj, self.value_proj, self.query_proj] + ([extra] if extra is not None else [])
+        weight, bias = self._concat_params(mods)
+        proj = F.linear(x, weight, bias)
+        extra_dim = extra.out_features if extra is not None else 0
+        return cuda_ops.cuda_project_split(proj, self.memory_key_dim, self.hidden_size, extra_dim, _NORM_EPS)
+
+    def _concat_params(self, mods: List[nn.Linear]) -> Tuple[Tensor, Optional[Tensor]]:
+        """The projections' weights and biases concatenated for one GEMM; without autograd
+        the concatenation is kept until a parameter changes (in place or replaced)."""
+        params = [p for m in mods for p in (m.weight, m.bias) if p is not None]
+        cacheable = not (torch.is_grad_enabled() and any(p.requires_grad for p in params))
+        key = tuple((id(p), p.data_ptr(), p._version, p.dtype, p.device) for p in params)
+        cached = getattr(self, "_concat_cache", None)
+        if cacheable and cached is not None and cached[0] == key:
+            return cached[1], cached[2]
         weight = torch.cat([m.weight for m in mods], 0)
         if all(m.bias is None for m in mods):
             bias = None
         else:
             bias = torch.cat([m.bias if m.bias is not None else m.weight.new_zeros(m.out_features) for m in mods])
-        outs = F.linear(x, weight, bias).split([m.out_features for m in mods], dim=-1)
-        k = F.normalize(outs[0], p=2, dim=-1, eps=_NORM_EPS)
-        q = F.normalize(outs[2], p=2, dim=-1, eps=_NORM_EPS)
-        return (k, outs[1], q) + tuple(outs[3:])
+        if cacheable:
+            self._concat_cache = (key, weight, bias)
+        else:
+            self._concat_cache = None
+        return weight, bias
 
 
 class TopKMemoryRetriever(nn.Module):
@@ -519,8 +556,10 @@ class SegmentRecurrentMemoryModel(nn.Module):
         grad = torch.is_grad_enabled() and any(p.requires_grad for p in self.parameters())
         k_r = gu.key_proj(summaries.to(x.dtype))
         top_k = min(self.retrieval_top_k, cap)
+        _mark("routing key projection", x)
         gates, idx, _ = cuda_ops.cuda_segment_route(q_r, k_r, top_k, seg, base, cap, gu.scale, gu.temperature,
                                                     debug_fallback=self.cuda_cpp_debug_fallback)
+        _mark("segment routing (score, top-k, softmax)", x)
         filled = idx >= 0
         idx0 = idx.clamp(min=0)
         if grad:
@@ -545,8 +584,8 @@ class SegmentRecurrentMemoryModel(nn.Module):
                 # A 16-bit model: retrieval, gate-weighted sum, residual and LayerNorm in one
                 # op; the [B, T, k, H] retrieved rows are kept as row-scaled float16 (relative
                 # rounding 2^-11 of each row's largest value), never as float32.
-                fused = cuda_ops.cuda_retrieve_fuse(states, idx0, q_in, gates.float(), h_online.float(), weight, bias,
-                                                    eps, debug_fallback=self.cuda_cpp_debug_fallback)
+                fused = cuda_ops.cuda_retrieve_fuse(states, idx0, q_in, gates.float(), h_online, weight, bias, eps,
+                                                    debug_fallback=self.cuda_cpp_debug_fallback)
             else:
                 H = h_online.size(-1)
                 retrieved = cuda_ops.cuda_gather_apply(states, idx0, q_in, torch.float32,
@@ -568,6 +607,7 @@ class SegmentRecurrentMemoryModel(nn.Module):
                 fused = self.dropout(self.memory_soup_norm(h_online + contribution))
             else:
                 fused = self.aggregator.apply_rule(h_online, contribution, retrieved, gates)
+        _mark("retrieval (gather, apply, fuse, residual + LayerNorm)", x)
         fused = fused.to(h_online.dtype)
         if base == 0:  # the first segment found an empty archive: h_online unchanged
             if fused.requires_grad:
@@ -607,9 +647,12 @@ class SegmentRecurrentMemoryModel(nn.Module):
             return out, last_hidden, memory, aux_dict(x.new_zeros(B, 0, self.hidden_size))
 
         seg = self.segment_length
+        _mark("other (between phases)", x)
         k, v, q, q_r = self.memory_cell.project(x, self.gating_unit.query_proj)
+        _mark("projection GEMM + k/q normalise", x)
         h_online, memory_end, snaps = self._scan(k, v, q, memory)
         h_online = self.dropout(h_online)
+        _mark("scan (chunk update + query, snapshots)", x)
 
         # The archive every segment of this sequence reads from: what was kept
         # before (deque order) followed by this sequence's segments, each state
@@ -618,7 +661,7 @@ class SegmentRecurrentMemoryModel(nn.Module):
         # passes no gradient back into the scan or the summaries' inputs.
         bank = self.memory_bank
         storage = bank.memory_storage_dtype
-        new_states = snaps.detach().to(dtype).to(storage)
+        new_states = snaps.detach().to(dtype).to(storage)  # what push() stores, converted once
         new_summaries = _segment_means(x.detach(), seg).to(storage)
         ring = bank._groups.get(B)
         base = 0 if ring is None else len(ring)
@@ -629,11 +672,13 @@ class SegmentRecurrentMemoryModel(nn.Module):
         else:
             states, summaries = new_states, new_summaries
         n_seg = new_states.size(1)
+        _mark("archive states and summaries (conversions, segment means)", x)
         if base + n_seg > 1:
             h_enhanced = self._retrieve(x, q, q_r, h_online, states, summaries, base)
         else:
             h_enhanced = h_online
         y = self.output_proj(h_enhanced)
+        _mark("output projection GEMM", x)
 
         # Push every segment (paper_grm.py:718-724); only the last `capacity` survive.
         # Checkpoints of the kept segments: one time-major copy of their inputs
@@ -644,13 +689,15 @@ class SegmentRecurrentMemoryModel(nn.Module):
         if self.memory_initialization_mode == "independent":
             starts = torch.zeros((n_seg - first,) + tuple(memory.shape), dtype=storage, device=device)
         else:
-            prev = snaps[:, max(first - 1, 0):n_seg - 1].transpose(0, 1).to(dtype)
-            starts = (torch.cat([memory.detach().to(dtype).unsqueeze(0), prev], 0) if first == 0 else prev).to(storage)
+            # the end states of the previous segments, as stored (views of new_states)
+            prev = new_states[:, max(first - 1, 0):n_seg - 1].transpose(0, 1)
+            starts = torch.cat([memory.detach().to(dtype).to(storage).unsqueeze(0), prev], 0) if first == 0 else prev
         if first == 0:
             starts[0].copy_(memory.detach())
         checkpoints = [SegmentCheckpoint(inputs[(s - first) * seg:(s - first + 1) * seg], starts[s - first])
                        for s in range(first, n_seg)]
-        bank.push_segments(snaps.to(dtype), new_summaries, checkpoints, owned=True)
+        bank.push_segments(new_states, new_summaries, checkpoints, owned=True)
+        _mark("archive push (ring writes, checkpoints)", x)
         # Routes handed out, as the reference counts them per segment (paper_grm.py:230).
         routes = sum(B * (min(T, (s + 1) * seg) - s * seg) * min(self.retrieval_top_k, min(base + s, cap))
                      for s in range(n_seg))
@@ -715,11 +762,15 @@ class SegmentRecurrentMemoryLayer(nn.Module):
                                                        return_all_outputs=return_all_outputs,
                                                        return_hidden_states=return_hidden_states,
                                                        reset_memory=reset_memory)
-        if return_all_outputs:
-            outputs = self.layer_norm(outputs + x)
+        _mark("other (between phases)", x)
+        residual = x if return_all_outputs else (x[:, -1, :] if self.batch_first else x[-1, :, :])
+        if isinstance(self.layer_norm, nn.LayerNorm):
+            ln = self.layer_norm
+            outputs = cuda_ops.cuda_residual_layer_norm(outputs, residual, ln.weight, ln.bias, ln.eps,
+                                                        debug_fallback=self.grm.cuda_cpp_debug_fallback)
         else:
-            residual = x[:, -1, :] if self.batch_first else x[-1, :, :]
             outputs = self.layer_norm(outputs + residual)
+        _mark("layer residual + LayerNorm", x)
         return self.dropout(outputs), h_final, memory_final, aux
 
     @property

@@ -238,3 +238,25 @@ def test_shape_errors_raise_like_reference():
         torch.ops.grm_cuda.chunk_update_forward(k, v, q, m[:, :3], 0.9)
     with pytest.raises(RuntimeError, match="topk_indices must have shape"):
         torch.ops.grm_cuda.batched_memory_gather(torch.randn(2, 3, 4, 5), torch.zeros(2, dtype=torch.long))
+
+
+def test_glue_ops_cpu_match_torch():
+    """The CPU kernels of project_split and residual_layer_norm are the torch compositions."""
+    import torch.nn.functional as F
+
+    from rnn_with_grm_amd import cuda_ops as co
+
+    if not co.load_grm_cuda_extension():
+        pytest.skip("extension not built")
+    g = torch.Generator().manual_seed(5)
+    for dtype in (torch.float32, torch.bfloat16):
+        proj = torch.randn(2, 7, 8 + 16 + 8 + 8, generator=g).to(dtype)
+        k, v, q, e = torch.ops.grm_cuda.project_split(proj, 8, 16, 8, 1e-6)
+        parts = proj.split([8, 16, 8, 8], dim=-1)
+        assert torch.equal(k, F.normalize(parts[0], p=2, dim=-1, eps=1e-6))
+        assert torch.equal(q, F.normalize(parts[2], p=2, dim=-1, eps=1e-6))
+        assert torch.equal(v, parts[1]) and torch.equal(e, parts[3])
+        x, r = torch.randn(5, 16, generator=g).to(dtype), torch.randn(5, 16, generator=g).to(dtype)
+        w, b = torch.randn(16, generator=g).to(dtype), torch.randn(16, generator=g).to(dtype)
+        y = torch.ops.grm_cuda.residual_layer_norm(x, r, w, b, 1e-5)
+        assert torch.equal(y, F.layer_norm(x + r, (16,), w, b, 1e-5))

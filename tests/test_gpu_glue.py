@@ -1,0 +1,93 @@
+"""The per-layer glue kernels (layer_glue.hip) against the torch ops they replace:
+project_split (split of the concatenated projection, F.normalize of keys and queries;
+reference grm/core/paper_grm.py:491-493,570-574) and residual_layer_norm
+(layer_norm(x + residual), grm/core/multilayer_grm.py:92-97)."""
+
+import pytest
+import torch
+import torch.nn.functional as F
+
+from rnn_with_grm_amd import capi, cuda_ops
+
+pytestmark = pytest.mark.gpu
+
+
+def ulps_apart(a, b, dtype):
+    """Largest distance between a and b in units in the last place of dtype at |b|."""
+    a, b = a.double(), b.double()
+    eps = {torch.bfloat16: 2.0 ** -7, torch.float16: 2.0 ** -10, torch.float32: 2.0 ** -23}[dtype]
+    scale = torch.clamp(b.abs(), min=torch.finfo(dtype).tiny) * eps
+    return float(((a - b).abs() / scale).max())
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("lead,dk,dv,de", [((4, 300), 64, 512, 512), ((7,), 8, 24, 0), ((2, 33), 128, 128, 16),
+                                           ((1, 5), 32, 8, 8)])
+def test_project_split(dev, dtype, lead, dk, dv, de):
+    """Keys and queries within two units in the last place of F.normalize's (the kernel sums
+    the squares in another order, so the norm can differ by one unit before the same
+    roundings and the division), values and extra bit for bit; zero rows stay zero (the eps
+    clamp)."""
+    g = torch.Generator().manual_seed(dk + dv + de)
+    proj = torch.randn(*lead, 2 * dk + dv + de, generator=g).to(dtype)
+    proj.view(-1, proj.shape[-1])[0, :dk] = 0  # a zero key row
+    pd = proj.to(dev)
+    print(f"project_split lead={lead} dk={dk} dv={dv} de={de} {dtype}", flush=True)
+    k, v, q, e = capi.project_split(pd, dk, dv, de, 1e-6)
+    torch.cuda.synchronize()
+    parts = pd.split([dk, dv, dk, de], dim=-1)
+    rk = F.normalize(parts[0], p=2, dim=-1, eps=1e-6)
+    rq = F.normalize(parts[2], p=2, dim=-1, eps=1e-6)
+    assert k.is_contiguous() and v.is_contiguous() and q.is_contiguous()
+    assert torch.equal(v, parts[1]) and (de == 0 or torch.equal(e, parts[3]))
+    assert not k.view(-1, dk)[0].any()
+    for name, got, ref in (("keys", k, rk), ("queries", q, rq)):
+        assert ulps_apart(got, ref, dtype) <= 2.0, name
+        if dtype != torch.float32:  # the 16-bit rounding of the norm hides most sum-order differences
+            assert (got != ref).float().mean() < 0.02, name
+
+
+@pytest.mark.parametrize("dtype,pdtype", [(torch.float32, torch.float32), (torch.bfloat16, torch.bfloat16),
+                                          (torch.float16, torch.float16), (torch.bfloat16, torch.float32)])
+@pytest.mark.parametrize("rows,H,affine", [(1000, 512, True), (37, 8, True), (5, 2048, False), (64, 200, True)])
+def test_residual_layer_norm(dev, dtype, pdtype, rows, H, affine):
+    """Against F.layer_norm(x + residual): the sum rounded to the row dtype as torch's add
+    does, float32 statistics; 16-bit outputs within one unit in the last place (the
+    statistics are summed in another order), float32 within 1e-5."""
+    g = torch.Generator().manual_seed(rows + H)
+    x = (torch.randn(rows, H, generator=g) * 2 + 0.5).to(dtype).to(dev)
+    r = torch.randn(rows, H, generator=g).to(dtype).to(dev)
+    w = (1 + 0.1 * torch.randn(H, generator=g)).to(pdtype).to(dev) if affine else None
+    b = (0.1 * torch.randn(H, generator=g)).to(pdtype).to(dev) if affine else None
+    print(f"residual_layer_norm rows={rows} H={H} {dtype} params {pdtype} affine={affine}", flush=True)
+    out = capi.residual_layer_norm(x, r, w, b, 1e-5)
+    torch.cuda.synchronize()
+    s = (x + r)
+    ref = F.layer_norm(s.float(), (H,), None if w is None else w.float(), None if b is None else b.float(), 1e-5)
+    if dtype == torch.float32:
+        torch.testing.assert_close(out, ref, rtol=1e-5, atol=1e-5)
+    else:
+        assert (out.double() - ref.double()).abs().max() <= 2 ** -7 * ref.abs().max().item() + 1e-3
+
+
+def test_glue_ops_through_cuda_ops(dev):
+    """cuda_ops' wrappers take the native ops without autograd (no generic path) and the
+    torch compositions under autograd, with gradients."""
+    ext = cuda_ops.extension_module()
+    g = torch.Generator().manual_seed(2)
+    proj = torch.randn(3, 50, 64 + 128 + 64 + 32, generator=g).to(torch.bfloat16).to(dev)
+    x = torch.randn(3, 50, 256, generator=g).to(dev)
+    r = torch.randn(3, 50, 256, generator=g).to(dev)
+    ln = torch.nn.LayerNorm(256).to(dev)
+    generic = ext.generic_path_calls()
+    launches = capi.launch_count()
+    with torch.no_grad():
+        k, v, q, e = cuda_ops.cuda_project_split(proj, 64, 128, 32)
+        y = cuda_ops.cuda_residual_layer_norm(x, r, ln.weight, ln.bias, ln.eps)
+    assert ext.generic_path_calls() == generic and capi.launch_count() >= launches + 2
+    assert e.shape == (3, 50, 32) and k.shape == (3, 50, 64)
+    xr = x.clone().requires_grad_(True)
+    y2 = cuda_ops.cuda_residual_layer_norm(xr, r, ln.weight, ln.bias, ln.eps)
+    y2.sum().backward()
+    assert xr.grad is not None and ln.weight.grad is not None
+    torch.testing.assert_close(y, y2.detach(), rtol=1e-5, atol=1e-5)
