@@ -194,6 +194,26 @@ int grm_hip_gather_apply(const void* memories, const int64_t* indices, const voi
                          int mem_dtype, int q_dtype, int out_dtype, int32_t* bad_index_count, void* stream);
 
 /*
+ * The queries' gradient of gather_apply (float32 out), per pair:
+ *   grad_pairs[b, q, r, :] = memories[b, indices[b, q, r]]^T grad_out[b, q, r, :]
+ * grad_out [batch, n_query, routes, hidden_size] and grad_pairs [batch, n_query,
+ * routes, key_dim] are float32; the caller sums over routes (grad of q'[b, q] is
+ * sum_r grad_pairs[b, q, r]).  This is the backward of the reference's
+ * apply_query_forward(batched_memory_gather(M, idx), q) with respect to q
+ * (grm/core/cuda_ops.py:324-344,388-402; apply_query.cu:256-330) without the
+ * gathered states; the memories get no gradient (the archive is detached, as the
+ * reference's native gather has no backward).  Pairs with an index outside
+ * [0, segments) get zero rows and, when bad_index_count is not NULL, are counted.
+ * workspace: grm_hip_gather_apply_workspace(batch, segments, n_query * routes) bytes.
+ * Limits: key_dim <= 128, segments <= 16384, hidden_size x (key_dim rounded up to
+ * 16/32/64/128, + 16) x 4 bytes within 160 KB (the float32 state in LDS).
+ */
+int grm_hip_gather_apply_bwd_queries(const void* memories, const int64_t* indices, const float* grad_out,
+                                     float* grad_pairs, void* workspace, int64_t workspace_bytes, int64_t batch,
+                                     int64_t segments, int64_t n_query, int64_t routes, int64_t hidden_size,
+                                     int64_t key_dim, int mem_dtype, int32_t* bad_index_count, void* stream);
+
+/*
  * Fused retrieval: gather + query application + gate-weighted sum + residual +
  * LayerNorm, without the per-(query, route) rows of gather_apply in float32:
  *   out[b, q, :] = LN(h_online[b, q, :] + sum_r gates[b, q, r] * M[b, idx[b, q, r]] q[b, q])

@@ -42,6 +42,7 @@ SIGNATURES = {
     "grm_hip_gather_apply_workspace": (_I, [_I, _I, _I]),
     "grm_hip_gather_apply": (_C, [_P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _C, _C, _C, _P, _P]),
     "grm_hip_retrieve_fuse_workspace": (_I, [_I, _I, _I, _I]),
+    "grm_hip_gather_apply_bwd_queries": (_C, [_P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _C, _P, _P]),
     "grm_hip_project_split": (_C, [_P, _P, _P, _P, _P, _I, _I, _I, _I, _C, ctypes.c_float, _P]),
     "grm_hip_residual_layer_norm": (_C, [_P, _P, _P, _P, _P, _I, _I, _C, _C, ctypes.c_float, _P]),
     "grm_hip_retrieve_fuse": (_C, [_P, _P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _C, _C, _C,
@@ -226,6 +227,20 @@ def gather_apply(memories, indices, queries, bad_count=None, out=None, dtype=Non
                                      dtype_code(dtype), _ptr(bad_count), _stream(memories))
     _check(rc, "grm_hip_gather_apply")
     return out
+
+
+def gather_apply_bwd_queries(memories, indices, grad_out, bad_count=None):
+    """Per-pair queries' gradient of gather_apply: [B, Q, R, K] float32 = M[idx]^T grad_out."""
+    B, S, H, K = memories.shape
+    Q, R = indices.shape[1], indices.shape[2]
+    gp = torch.empty((B, Q, R, K), dtype=torch.float32, device=memories.device)
+    wsb = int(load().grm_hip_gather_apply_workspace(B, S, Q * R))
+    ws = torch.empty(max(wsb, 16), dtype=torch.uint8, device=memories.device)
+    rc = load().grm_hip_gather_apply_bwd_queries(_ptr(memories), _ptr(indices), _ptr(grad_out), _ptr(gp), _ptr(ws), wsb,
+                                                 B, S, Q, R, H, K, dtype_code(memories.dtype), _ptr(bad_count),
+                                                 _stream(memories))
+    _check(rc, "grm_hip_gather_apply_bwd_queries")
+    return gp
 
 
 def retrieve_fuse(memories, indices, queries, gates, h_online, ln_weight=None, ln_bias=None, eps=1e-5,

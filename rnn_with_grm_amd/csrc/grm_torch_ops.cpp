@@ -406,6 +406,18 @@ Tensor retrieve_fuse_generic(const Tensor& memories, const Tensor& indices, cons
       .reshape({B, Q, H});
 }
 
+// gather_apply_backward_queries: d(gather_apply(M, idx, q))/dq for a grad of the
+// output, sum_r M[idx_r]^T grad_r, in the queries' dtype (the cast of q to the
+// arithmetic type passes the gradient through unchanged, as autograd's .to()).
+Tensor gather_apply_backward_queries_generic(const Tensor& memories, const Tensor& indices, const Tensor& grad_out,
+                                             const Tensor& queries) {
+  check_gather_apply_inputs(memories, indices, queries);
+  Tensor sel = batched_memory_gather_generic(memories, indices).to(at::kFloat);  // [B, (Q,) R, H, K]
+  Tensor g = grad_out.to(at::kFloat);
+  Tensor dq = indices.dim() == 3 ? at::einsum("bqrhk,bqrh->bqk", {sel, g}) : at::einsum("brhk,brh->bk", {sel, g});
+  return dq.to(queries.scalar_type());
+}
+
 // project_split: LinearMemoryCell.project's split of the concatenated
 // projection, F.normalize of keys and queries (paper_grm.py:491-493).
 void check_project_split(const Tensor& proj, int64_t dk, int64_t dv, int64_t de) {
@@ -870,6 +882,42 @@ Tensor retrieve_fuse_hip(const Tensor& memories, const Tensor& indices, const Te
   return out;
 }
 
+Tensor gather_apply_backward_queries_hip(const Tensor& memories, const Tensor& indices, const Tensor& grad_out,
+                                         const Tensor& queries) {
+  check_gather_apply_inputs(memories, indices, queries);
+  const int64_t B = memories.size(0), S = memories.size(1), H = memories.size(2), K = memories.size(3);
+  const int64_t kp = K <= 16 ? 16 : K <= 32 ? 32 : K <= 64 ? 64 : 128;
+  if (!same_cuda_device({&memories, &indices, &grad_out, &queries}) || dtype_code(memories.scalar_type()) < 0 ||
+      K > 128 || S > 16384 || H * (kp + 16) * 4 > 160 * 1024) {
+    if (memories.is_cuda()) g_generic_calls.fetch_add(1);
+    return gather_apply_backward_queries_generic(memories, indices, grad_out, queries);
+  }
+  c10::OptionalDeviceGuard guard(memories.device());
+  Tensor mm = memories.contiguous();
+  Tensor idx = indices.to(at::kLong).contiguous();
+  Tensor g = grad_out.to(at::kFloat).contiguous();
+  const int64_t Q = idx.dim() == 3 ? idx.size(1) : 1;
+  const int64_t R = idx.size(-1);
+  Tensor gp = at::empty({B, Q, R, K}, mm.options().dtype(at::kFloat));
+  const int64_t wsb = grm_hip_gather_apply_workspace(B, S, Q * R);
+  Tensor ws = at::empty({std::max<int64_t>(wsb, 16)}, mm.options().dtype(at::kByte));
+  Tensor bad;
+  const bool check = check_indices_requested();
+  if (check) bad = at::zeros({1}, mm.options().dtype(at::kInt));
+  check_rc(grm_hip_gather_apply_bwd_queries(mm.data_ptr(), idx.data_ptr<int64_t>(), g.data_ptr<float>(),
+                                            gp.data_ptr<float>(), ws.data_ptr(), wsb, B, S, Q, R, H, K,
+                                            dtype_code(mm.scalar_type()), check ? bad.data_ptr<int32_t>() : nullptr,
+                                            current_stream(mm)),
+           "gather_apply_backward_queries");
+  if (check) {
+    const int64_t nbad = bad.item<int32_t>();
+    TORCH_CHECK_INDEX(nbad == 0, "gather_apply: ", nbad, " index values outside [0, ", S, ")");
+  }
+  Tensor dq = gp.sum(2);  // fixed-order reduction over the routes
+  if (idx.dim() == 2) dq = dq.squeeze(1);
+  return dq.to(queries.scalar_type());
+}
+
 std::tuple<Tensor, Tensor, Tensor, Tensor> project_split_hip(const Tensor& proj, int64_t key_dim, int64_t value_dim,
                                                              int64_t extra_dim, double eps) {
   check_project_split(proj, key_dim, value_dim, extra_dim);
@@ -956,6 +1004,7 @@ TORCH_LIBRARY(grm_cuda, m) {
   m.def("segment_route(Tensor queries, Tensor keys, int top_k, int segment_len, int base, int capacity, float scale, float temperature) -> (Tensor gates, Tensor indices, Tensor scores)");
   m.def("retrieve_fuse(Tensor memories, Tensor indices, Tensor queries, Tensor gates, Tensor h_online, Tensor? weight, Tensor? bias, float eps) -> Tensor");
   m.def("project_split(Tensor proj, int key_dim, int value_dim, int extra_dim, float eps) -> (Tensor keys, Tensor values, Tensor queries, Tensor extra)");
+  m.def("gather_apply_backward_queries(Tensor memories, Tensor indices, Tensor grad_out, Tensor queries) -> Tensor");
   m.def("residual_layer_norm(Tensor x, Tensor residual, Tensor? weight, Tensor? bias, float eps) -> Tensor");
 }
 
@@ -973,6 +1022,7 @@ TORCH_LIBRARY_IMPL(grm_cuda, CPU, m) {
   m.impl("segment_route", grm::segment_route_cpu);
   m.impl("retrieve_fuse", grm::retrieve_fuse_generic);
   m.impl("project_split", grm::project_split_generic);
+  m.impl("gather_apply_backward_queries", grm::gather_apply_backward_queries_generic);
   m.impl("residual_layer_norm", grm::residual_layer_norm_generic);
 }
 
@@ -990,6 +1040,7 @@ TORCH_LIBRARY_IMPL(grm_cuda, CUDA, m) {
   m.impl("segment_route", grm::segment_route_hip);
   m.impl("retrieve_fuse", grm::retrieve_fuse_hip);
   m.impl("project_split", grm::project_split_hip);
+  m.impl("gather_apply_backward_queries", grm::gather_apply_backward_queries_hip);
   m.impl("residual_layer_norm", grm::residual_layer_norm_hip);
 }
 

@@ -69,6 +69,7 @@ struct RetrieveArgs {
   // tile] = 2^-sh.  nullptr: the plain [pairs, dv] output of gather_apply.
   const float* gates;  // [batch, n_index]
   float* scales;       // [batch, n_index, v_tiles]
+  int out_row;         // elements per output row (dv; dk for the queries' gradient)
 };
 
 // ---------------------------------------------------------------------------
@@ -122,8 +123,8 @@ __device__ __forceinline__ void zero_rows_wave(const RetrieveArgs& a, int64_t b,
     const int l = __ffsll(static_cast<unsigned long long>(mask)) - 1;
     mask &= mask - 1u;
     const int64_t row = __shfl(i, l, 64);
-    typename ET<EM>::raw* ob = static_cast<typename ET<EM>::raw*>(a.out) + (b * a.n_index + row) * a.dv;
-    for (int h = lane; h < a.dv; h += 64) ob[h] = ET<EM>::from_f(0.f);
+    typename ET<EM>::raw* ob = static_cast<typename ET<EM>::raw*>(a.out) + (b * a.n_index + row) * a.out_row;
+    for (int h = lane; h < a.out_row; h += 64) ob[h] = ET<EM>::from_f(0.f);
     if (a.scales != nullptr)
       for (int t = lane; t < a.v_tiles; t += 64) a.scales[(b * a.n_index + row) * a.v_tiles + t] = 0.f;
   }
@@ -1012,6 +1013,107 @@ int apply_scaled_q(const RetrieveArgs& a, int q_dtype, hipStream_t s) {
   return q_dtype == GRM_HIP_F16 ? launch_apply_scaled<EL, F16>(a, s) : launch_apply_scaled<EL, BF16>(a, s);
 }
 
+// ---------------------------------------------------------------------------
+// The queries' gradient of gather_apply: for every pair (q, r) with a valid
+// index, dqp[b, q, r, :] = M[b, idx[b, q, r]]^T g[b, q, r, :] (float32 grad_out
+// rows of d_v, float32 result rows of d_k); the caller sums over r.  One
+// workgroup per (sequence, work tile) stages its segment's state in LDS as
+// float32 (row stride d_k + 16 floats, so the 64 lanes of one read - 16
+// consecutive keys of 4 consecutive rows - hit 64 distinct banks) and applies
+// its transpose with float32 MFMA (16x16x4): wave w takes 16 pairs at a time,
+// A = M^T (keys x 4 rows), B = the pairs' grad_out rows.  Each output row is
+// written by one wave: deterministic, no atomics.
+template <class EL, int DKP>
+__global__ __launch_bounds__(AP_THREADS) void apply_t_kernel(const RetrieveArgs a, const float* grad, float* dqp) {
+  using rawl = typename ET<EL>::raw;
+  extern __shared__ float Ms[];  // [dv][DKP + 16]
+  constexpr int MSK = DKP + 16;
+  constexpr int KB = DKP / 16;
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int64_t tile = blockIdx.x;
+  const int64_t b = blockIdx.y;
+  if (tile >= a.n_tiles[b]) return;
+  const int4 te = a.tiles[b * a.tb_max + tile];
+  const int64_t s = te.x;
+  const int p_begin = te.y, p_end = te.z;
+  const int dk = a.dk, dv = a.dv;
+  const rawl* msrc = static_cast<const rawl*>(a.mem) + (b * a.segments + s) * dv * dk;
+  for (int e = tid; e < dv * DKP; e += AP_THREADS) {
+    const int v = e / DKP, k = e % DKP;
+    Ms[v * MSK + k] = k < dk ? ET<EL>::to_f(msrc[v * dk + k]) : 0.f;
+  }
+  __syncthreads();
+  const int32_t* lb = a.list + b * a.n_index;
+  const int n = lane & 15, kq = lane >> 4;
+  for (int p0 = p_begin + 16 * w; p0 < p_end; p0 += 64) {
+    const int pid = p0 + n < p_end ? lb[p0 + n] : -1;
+    const float* grow = grad + (b * a.n_index + (pid >= 0 ? pid : 0)) * static_cast<int64_t>(dv);
+    f32x4 acc[KB];
+#pragma unroll
+    for (int kb = 0; kb < KB; ++kb) acc[kb] = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int v0 = 0; v0 < dv; v0 += 16) {
+      float bg[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int v = v0 + 4 * j + kq;
+        bg[j] = (pid >= 0 && v < dv) ? grow[v] : 0.f;
+      }
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int v = v0 + 4 * j + kq;
+#pragma unroll
+        for (int kb = 0; kb < KB; ++kb) {
+          const float am = v < dv ? Ms[v * MSK + 16 * kb + n] : 0.f;
+          acc[kb] = __builtin_amdgcn_mfma_f32_16x16x4f32(am, bg[j], acc[kb], 0, 0, 0);
+        }
+      }
+    }
+    // lane (kq, n) holds keys 16 kb + 4 kq + r of pair n (the pair its pid names)
+    if (pid >= 0) {
+      float* orow = dqp + (b * a.n_index + pid) * static_cast<int64_t>(dk);
+#pragma unroll
+      for (int kb = 0; kb < KB; ++kb) {
+        const int k = 16 * kb + 4 * kq;
+        if (k + 4 <= dk) {
+          *reinterpret_cast<f32x4*>(orow + k) = acc[kb];
+        } else {
+#pragma unroll
+          for (int r = 0; r < 4; ++r)
+            if (k + r < dk) orow[k + r] = acc[kb][r];
+        }
+      }
+    }
+  }
+}
+
+template <class EL, int DKP>
+int launch_apply_t(const RetrieveArgs& a, const float* grad, float* dqp, hipStream_t s) {
+  const size_t lds = static_cast<size_t>(a.dv) * (DKP + 16) * sizeof(float);
+  static bool attr_set = false;
+  if (!attr_set) {
+    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&apply_t_kernel<EL, DKP>),
+                                       hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
+    if (e != hipSuccess) {
+      set_error("gather_apply_bwd: hipFuncSetAttribute failed: %s", hipGetErrorString(e));
+      return static_cast<int>(e);
+    }
+    attr_set = true;
+  }
+  const dim3 grid(static_cast<unsigned>(a.tb_max), static_cast<unsigned>(a.batch));
+  hipLaunchKernelGGL((apply_t_kernel<EL, DKP>), grid, dim3(AP_THREADS), lds, s, a, grad, dqp);
+  return check_launch("gather_apply_bwd");
+}
+
+template <class EL>
+int dispatch_apply_t(const RetrieveArgs& a, const float* grad, float* dqp, hipStream_t s) {
+  if (a.dk <= 16) return launch_apply_t<EL, 16>(a, grad, dqp, s);
+  if (a.dk <= 32) return launch_apply_t<EL, 32>(a, grad, dqp, s);
+  if (a.dk <= 64) return launch_apply_t<EL, 64>(a, grad, dqp, s);
+  return launch_apply_t<EL, 128>(a, grad, dqp, s);
+}
+
 int allow_segment_lds(const void* fn) {
   const hipError_t e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize,
                                            static_cast<int>(kMaxSegments * sizeof(int)));
@@ -1129,6 +1231,7 @@ void init_retrieve_args(RetrieveArgs& a, const void* memories, const int64_t* in
   a.n_index = n_index;
   a.dv = static_cast<int>(hidden_size);
   a.dk = static_cast<int>(key_dim);
+  a.out_row = a.dv;
   a.v_tiles = static_cast<int>((hidden_size + AP_V - 1) / AP_V);
 }
 
@@ -1309,5 +1412,59 @@ extern "C" int grm_hip_retrieve_fuse(const void* memories, const int64_t* indice
     case GRM_HIP_F32: return launch_fuse_scaled<F32>(f, s);
     case GRM_HIP_F16: return launch_fuse_scaled<F16>(f, s);
     default: return launch_fuse_scaled<BF16>(f, s);
+  }
+}
+
+extern "C" int grm_hip_gather_apply_bwd_queries(const void* memories, const int64_t* indices, const float* grad_out,
+                                                float* grad_pairs, void* workspace, int64_t workspace_bytes,
+                                                int64_t batch, int64_t segments, int64_t n_query, int64_t routes,
+                                                int64_t hidden_size, int64_t key_dim, int mem_dtype,
+                                                int32_t* bad_index_count, void* stream) {
+  if (batch < 0 || segments < 0 || n_query < 0 || routes < 0 || hidden_size < 0 || key_dim < 1) {
+    set_error("gather_apply_bwd: negative size or key_dim < 1");
+    return GRM_HIP_EINVAL;
+  }
+  if (mem_dtype < GRM_HIP_F32 || mem_dtype > GRM_HIP_BF16) {
+    set_error("gather_apply_bwd: unsupported memories dtype %d", mem_dtype);
+    return GRM_HIP_EUNSUPPORTED;
+  }
+  const int64_t dkp = key_dim <= 16 ? 16 : key_dim <= 32 ? 32 : key_dim <= 64 ? 64 : 128;
+  if (key_dim > 128 || segments > kMaxSegments || hidden_size * (dkp + 16) * 4 > 160 * 1024) {
+    set_error("gather_apply_bwd: needs key_dim <= 128, segments <= %lld and the float32 state in LDS",
+              (long long)kMaxSegments);
+    return GRM_HIP_EUNSUPPORTED;
+  }
+  const int64_t n_index = n_query * routes;
+  if (batch == 0 || n_index == 0 || key_dim == 0) return GRM_HIP_OK;
+  if (n_index > INT32_MAX || batch > 65535 || tiles_max(segments, n_index) > UINT32_MAX) {
+    set_error("gather_apply_bwd: sizes exceed one launch");
+    return GRM_HIP_EINVAL;
+  }
+  if (indices == nullptr || grad_pairs == nullptr || (hidden_size > 0 && grad_out == nullptr) ||
+      (segments > 0 && memories == nullptr)) {
+    set_error("gather_apply_bwd: null pointer");
+    return GRM_HIP_EINVAL;
+  }
+  const int64_t need = grm_hip_gather_apply_workspace(batch, segments, n_index);
+  if (workspace == nullptr || workspace_bytes < need || reinterpret_cast<uintptr_t>(workspace) % 16 != 0 ||
+      reinterpret_cast<uintptr_t>(grad_pairs) % 16 != 0) {
+    set_error("gather_apply_bwd: workspace of %lld bytes and 16-byte aligned buffers required", (long long)need);
+    return GRM_HIP_EINVAL;
+  }
+  RetrieveArgs a;
+  init_retrieve_args(a, memories, indices, nullptr, grad_pairs, workspace, batch, segments, n_query, routes, n_index,
+                     hidden_size, key_dim, bad_index_count);
+  a.out_row = static_cast<int>(key_dim);  // invalid pairs: zero gradient rows
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  int rc = launch_bucket<F32>(a, s);
+  if (rc != GRM_HIP_OK || segments == 0) return rc;
+  if (hidden_size == 0) {
+    set_error("gather_apply_bwd: value_dim 0 with valid pairs");
+    return GRM_HIP_EUNSUPPORTED;
+  }
+  switch (mem_dtype) {
+    case GRM_HIP_F32: return dispatch_apply_t<F32>(a, grad_out, grad_pairs, s);
+    case GRM_HIP_F16: return dispatch_apply_t<F16>(a, grad_out, grad_pairs, s);
+    default: return dispatch_apply_t<BF16>(a, grad_out, grad_pairs, s);
   }
 }

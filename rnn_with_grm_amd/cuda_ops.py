@@ -38,7 +38,8 @@ SCHEMA_OPS = (
     "batched_memory_gather",
 )
 EXTRA_OPS = ("segment_scan_forward", "topk_route", "fuse_residual", "gather_apply", "segment_route",
-             "retrieve_fuse", "project_split", "residual_layer_norm", "apply_query_backward_queries")
+             "retrieve_fuse", "project_split", "residual_layer_norm", "gather_apply_backward_queries",
+             "apply_query_backward_queries")
 
 # Environment variables of the reference (cuda_ops.py:26-32): one per op and a global one.
 GLOBAL_POLICY_ENV = "GRM_CUDA_KERNEL_POLICY"
@@ -335,6 +336,26 @@ class _ApplyQueryFn(torch.autograd.Function):
         return torch.ops.grm_cuda.apply_query_backward(grad_hidden, memories, queries)
 
 
+class _GatherApplyFn(torch.autograd.Function):
+    """Native gather + apply with the queries' gradient from the transposed apply
+    (sum_r M[idx_r]^T g_r): neither direction forms the gathered [.., R, d_v, d_k] states.
+    The memories get no gradient (a detached archive)."""
+
+    @staticmethod
+    def forward(ctx, memories: Tensor, indices: Tensor, queries: Tensor, dtype):
+        ctx.save_for_backward(memories, indices, queries)
+        return torch.ops.grm_cuda.gather_apply(memories, indices, queries, dtype)
+
+    @staticmethod
+    def backward(ctx, grad_out: Tensor):
+        memories, indices, queries = ctx.saved_tensors
+        grad_q = None
+        if ctx.needs_input_grad[2]:
+            grad_q = torch.ops.grm_cuda.gather_apply_backward_queries(memories, indices, grad_out.contiguous(),
+                                                                      queries)
+        return None, None, grad_q, None
+
+
 # ---------------------------------------------------------------------------
 # Entry points (the reference's cuda_ops.py:347-402, then this library's own).
 
@@ -449,11 +470,16 @@ def cuda_gather_apply(memories_per_batch: Tensor, topk_indices: Tensor, queries:
     """apply_query(batched_memory_gather(M, idx).to(dtype), q.to(dtype)) without materialising
     the gathered states (cuda_ops.py:370-402, composed as in paper_grm.py:227-229,301-313).
     ``dtype`` is M's dtype by default; float32 widens 16-bit archives as the retriever does.
-    The fused op has no backward: when autograd needs gradients the composition runs."""
+    Under autograd, when only the queries need a gradient (a detached archive, as in the
+    models) the native op runs with the transposed apply as its backward; when the memories
+    need one too, the composition runs."""
     needs_grad = torch.is_grad_enabled() and (memories_per_batch.requires_grad or queries.requires_grad)
-    if not needs_grad and _run_native("gather_apply", memories_per_batch.device, enabled=enabled,
-                                      debug_fallback=debug_fallback):
+    native = _run_native("gather_apply", memories_per_batch.device, enabled=enabled, debug_fallback=debug_fallback)
+    if native and not needs_grad:
         return torch.ops.grm_cuda.gather_apply(memories_per_batch, topk_indices, queries, dtype)
+    if native and not memories_per_batch.requires_grad:
+        # only the queries need a gradient: the transposed apply gives it without the gathered states
+        return _GatherApplyFn.apply(memories_per_batch, topk_indices, queries, dtype)
     gathered = cuda_batched_memory_gather(memories_per_batch, topk_indices, enabled=enabled,
                                           debug_fallback=debug_fallback)
     if dtype is not None:

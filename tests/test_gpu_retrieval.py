@@ -630,3 +630,54 @@ def test_retrieve_fuse_op_and_model_path(dev):
     rows = capi.gather_apply(mem, idx, qf, dtype=torch.float32)
     e = capi.fuse_residual(h.reshape(B * Q, H), rows.reshape(B * Q, R, H), gates.reshape(B * Q, R), w, b)
     assert torch.equal(d, e.reshape(B, Q, H))
+
+
+# ---------------------------------------------------------------- gather_apply backward (queries)
+@pytest.mark.parametrize("mem_dtype", [torch.float32, torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("B,Q,S,R,H,K", [(2, 100, 37, 5, 128, 128), (3, 64, 8, 8, 512, 64), (1, 129, 300, 16, 200, 32),
+                                         (2, 50, 5, 3, 8, 64), (1, 70, 3, 8, 40, 20)])
+def test_gather_apply_bwd_queries(dev, mem_dtype, B, Q, S, R, H, K):
+    """The transposed apply (per pair M[idx]^T g, float32) summed over routes against the oracle's
+    apply-query backward on the gathered states, at 1e-5 of the gradient's scale; invalid
+    indices give zero rows and are counted."""
+    g = torch.Generator().manual_seed(B + Q + H + K)
+    mem = (torch.randn(B, S, H, K, generator=g) * 0.3).to(mem_dtype)
+    idx = torch.randint(0, S, (B, Q, R), generator=g)
+    idx[0, 2, 1] = -1
+    grad = torch.randn(B, Q, R, H, generator=g)
+    q = norm(torch.randn(B, Q, K, generator=g))
+    bad = torch.zeros(1, dtype=torch.int32, device=dev)
+    print(f"gather_apply_bwd_queries B={B} Q={Q} S={S} R={R} H={H} K={K} {mem_dtype}", flush=True)
+    gp = capi.gather_apply_bwd_queries(mem.to(dev), idx.to(dev), grad.to(dev), bad_count=bad)
+    torch.cuda.synchronize()
+    assert int(bad.item()) == 1
+    assert not gp[0, 2, 1].any()
+    valid = (idx >= 0).numpy()
+    gathered, _ = orc.gather(mem.double().numpy(), np.where(valid, idx.numpy(), 0))
+    gathered = gathered * valid[..., None, None]
+    _, ref = orc.apply_query_bwd(grad.double().numpy(), gathered, q.double().numpy())
+    # float32 sums of H products per pair and R pairs: 1e-5 of the gradient's scale
+    np.testing.assert_allclose(gp.sum(2).double().cpu().numpy(), ref, rtol=1e-5,
+                               atol=1e-5 * max(1.0, float(np.abs(ref).max())))
+
+
+def test_gather_apply_native_queries_gradient(dev):
+    """With a detached archive and queries that need a gradient, cuda_gather_apply runs the native
+    op with the transposed apply as its backward (no gathered states, no generic path); the
+    queries' gradient equals the composition's on the CPU."""
+    g = torch.Generator().manual_seed(23)
+    mem = (torch.randn(2, 9, 64, 32, generator=g) * 0.2).to(torch.float16).to(dev)
+    idx = torch.randint(0, 9, (2, 40, 4), generator=g).to(dev)
+    q = norm(torch.randn(2, 40, 32, generator=g)).to(torch.bfloat16).to(dev).requires_grad_(True)
+    ext = cuda_ops.extension_module()
+    generic = ext.generic_path_calls()
+    out = cuda_ops.cuda_gather_apply(mem, idx, q, torch.float32)
+    (out.square().sum()).backward()
+    torch.cuda.synchronize()
+    assert ext.generic_path_calls() == generic
+    q2 = q.detach().cpu().float().requires_grad_(True)
+    sel = mem.cpu().float()[torch.arange(2)[:, None, None], idx.cpu()]
+    ref = torch.einsum("bqrhk,bqk->bqrh", sel, q2)
+    ref.square().sum().backward()
+    torch.testing.assert_close(out.detach().cpu(), ref.detach(), rtol=1e-5, atol=1e-5)
+    torch.testing.assert_close(q.grad.float().cpu(), q2.grad, rtol=1e-2, atol=1e-2)  # q.grad is bf16
