@@ -712,6 +712,40 @@ def cpu_baseline(torch):
             "host": host, "one_thread": out[1], "legs": out[threads]}
 
 
+def bench_c4_train(torch, dev, steps, warmup):
+    """Config 4 training forward + backward (no optimizer step): the same LM and token ids,
+    cross-entropy over next-token targets, loss.backward() through the scan's MFMA backward,
+    the routing, the retrieval's queries gradient (transposed apply, no gathered states) and
+    the torch fusion.  Returns the mean step and the generic-path calls the steps made."""
+    from rnn_with_grm_amd import cuda_ops
+
+    B, T, V = 4, 8192, 32000
+    lm = SegmentMemoryLM(torch, dev)
+    params = [p for m in (lm.embedding, lm.grm, lm.head) for p in m.parameters()]
+    g = torch.Generator().manual_seed(7)
+    ids = torch.randint(0, V, (B, T), generator=g).to(dev)
+    targets = torch.roll(ids, -1, dims=1)
+    stream = torch.cuda.current_stream(dev)
+
+    def step():
+        for p in params:
+            p.grad = None
+        logits = lm(ids)
+        loss = torch.nn.functional.cross_entropy(logits.view(B * T, V).float(), targets.view(-1))
+        loss.backward()
+
+    step()
+    torch.cuda.synchronize()
+    grads = [p.grad for p in params if p.grad is not None]
+    assert len(grads) > len(params) // 2 and all(torch.isfinite(t.float()).all() for t in grads), \
+        "c4 training gradients missing or not finite"
+    generic0 = cuda_ops.get_grm_cuda_runtime_status()["hip"]["generic_path_calls"]
+    wall, per = timed_launches(torch, step, max(3, min(steps, 8)), max(1, min(warmup, 2)), stream)
+    generic = cuda_ops.get_grm_cuda_runtime_status()["hip"]["generic_path_calls"] - generic0
+    return {"ms": statistics.mean(per) * 1e3, "tokens": B * T, "generic_path_calls": generic,
+            "peak_gib": torch.cuda.max_memory_allocated(dev) / 2 ** 30}
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -721,12 +755,14 @@ def main() -> int:
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--c2-only", action="store_true", help="only the headline kernel (quick sweeps)")
     ap.add_argument("--c4-only", action="store_true", help="the headline kernel and the config-4 model forward")
+    ap.add_argument("--train-only", action="store_true",
+                    help="the headline kernel and the config-4 training forward + backward")
     ap.add_argument("--bwd-only", action="store_true", help="the headline kernel and the config-2 backward")
     ap.add_argument("--route-only", action="store_true", help="the headline kernel and config 3 / 5 routing")
     ap.add_argument("--probe", action="store_true",
                     help="counter runs: a 256 MiB device copy (calibration) then config-2 launches only")
     a = ap.parse_args()
-    if a.c2_only or a.probe or a.c4_only or a.bwd_only or a.route_only:
+    if a.c2_only or a.probe or a.c4_only or a.bwd_only or a.route_only or a.train_only:
         a.no_gather = a.no_cpu = True
     if a.gpus != 1:
         print(f"bench.py measures one GPU only; --gpus {a.gpus} is not supported in this build "
@@ -890,6 +926,18 @@ def main() -> int:
         log(f"c4 forward: {m4['ms']:.2f} ms, {m4['tokens'] / m4['ms'] * 1e3:.3e} tokens/s")
         for k, v in sorted(m4["phases_ms"].items(), key=lambda kv: -kv[1]):
             log(f"  c4 phase {k}: {v:.3f} ms")
+
+    if not a.no_gather or a.train_only:
+        log("config 4 training forward + backward")
+        t4 = bench_c4_train(torch, dev, a.steps, a.warmup)
+        secondary["c4_model_train_step"] = {
+            "what": "config 4 LM forward + cross-entropy + backward (no optimizer step), same model and ids; "
+                    "native scan backward, routing, and the retrieval's queries gradient without the gathered "
+                    "states",
+            "ms": round(t4["ms"], 3), "tokens/s": round(t4["tokens"] / t4["ms"] * 1e3),
+            "generic_path_calls": t4["generic_path_calls"], "peak_memory_gib": round(t4["peak_gib"], 1)}
+        log(f"c4 train step: {t4['ms']:.2f} ms, {t4['tokens'] / t4['ms'] * 1e3:.3e} tokens/s, generic path calls "
+            f"{t4['generic_path_calls']}, peak {t4['peak_gib']:.1f} GiB")
 
     if not a.no_gather:
         pub = bench_published(torch, dev)

@@ -205,8 +205,9 @@ int grm_hip_gather_apply(const void* memories, const int64_t* indices, const voi
  * reference's native gather has no backward).  Pairs with an index outside
  * [0, segments) get zero rows and, when bad_index_count is not NULL, are counted.
  * workspace: grm_hip_gather_apply_workspace(batch, segments, n_query * routes) bytes.
- * Limits: key_dim <= 128, segments <= 16384, hidden_size x (key_dim rounded up to
- * 16/32/64/128, + 16) x 4 bytes within 160 KB (the float32 state in LDS).
+ * Limits: key_dim <= 128, segments <= 16384, (hidden_size rounded up to 16) x
+ * (key_dim rounded up to 16/32/64/128, + 4) x 4 bytes within 160 KB (the float32
+ * state in LDS).
  */
 int grm_hip_gather_apply_bwd_queries(const void* memories, const int64_t* indices, const float* grad_out,
                                      float* grad_pairs, void* workspace, int64_t workspace_bytes, int64_t batch,

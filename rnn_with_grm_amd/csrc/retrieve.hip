@@ -54,7 +54,7 @@ struct RetrieveArgs {
   int dk;
   int v_tiles;
   int32_t* partial;  // [batch, bk_chunks, segments]: per-chunk counts, then bases (multi-workgroup bucketing)
-  int bk_chunks;     // pair chunks of BK_ITEMS per sequence
+  int bk_chunks;     // pair groups of about BK_ITEMS per sequence (strided blocks of BK_THREADS pairs)
   // Work tiles of the apply kernels: at most tile_pairs consecutive pairs of
   // one segment each, so a segment that many queries selected is spread over
   // several workgroups.  tiles [batch, tb_max] of (segment, first pair, end, 0);
@@ -110,15 +110,55 @@ __device__ void bucket_offsets(int* hist, int64_t S, int32_t* offsets) {
   __syncthreads();
 }
 
-// A row whose index is outside [0, segments): zeros, and one count.
-// Called by every lane of a wave together (bad: this lane's pair i is
-// invalid): the wave writes each invalid pair's row with consecutive lanes on
-// consecutive elements, one row after another.
+// Lane index of the r-th set bit of mask (r < popcount(mask)).
+__device__ __forceinline__ int nth_set_bit(uint64_t mask, int r) {
+  int pos = 0;
+#pragma unroll
+  for (int w = 32; w >= 1; w >>= 1) {
+    const int c = __popcll(mask & ((1ull << w) - 1u));
+    if (r >= c) {
+      r -= c;
+      mask >>= w;
+      pos += w;
+    }
+  }
+  return pos;
+}
+
+// A row whose index is outside [0, segments): zeros, and one count.  Called
+// by every lane of a wave together (bad: this lane's pair i is invalid).  With
+// 16-byte rows the wave writes several whole rows per store instruction,
+// coalesced (the first segments' short windows can leave most of a pair chunk
+// empty); otherwise one row after another, consecutive lanes on consecutive
+// elements.
 template <class EM>
 __device__ __forceinline__ void zero_rows_wave(const RetrieveArgs& a, int64_t b, int64_t i, bool bad) {
+  using raw = typename ET<EM>::raw;
   uint64_t mask = __ballot(bad);
   const int lane = threadIdx.x & 63;
   if (mask != 0u && lane == 0 && a.bad != nullptr) atomicAdd(a.bad, static_cast<int>(__popcll(mask)));
+  if (mask == 0u) return;
+  const int64_t row_bytes = static_cast<int64_t>(a.out_row) * sizeof(raw);
+  if (row_bytes % 16 == 0 && reinterpret_cast<uintptr_t>(a.out) % 16 == 0) {
+    // Whole rows in 16-byte pieces: lpr lanes per row, 64 / lpr rows per store
+    // instruction, the rows taken in ballot order (i < n_index <= INT32_MAX).
+    const int pieces = static_cast<int>(row_bytes / 16);
+    int lpr = 1;
+    while (lpr < pieces && lpr < 64) lpr <<= 1;
+    const int m = __popcll(mask);
+    const int i32 = static_cast<int>(i);
+    for (int r0 = 0; r0 < m; r0 += 64 / lpr) {
+      const int r = r0 + lane / lpr;
+      const int row = __shfl(i32, nth_set_bit(mask, r < m ? r : 0), 64);
+      if (r < m) {
+        uint4* ob = reinterpret_cast<uint4*>(static_cast<raw*>(a.out) + (b * a.n_index + row) * a.out_row);
+        for (int p = lane % lpr; p < pieces; p += lpr) ob[p] = uint4{0u, 0u, 0u, 0u};
+        if (a.scales != nullptr)
+          for (int t = lane % lpr; t < a.v_tiles; t += lpr) a.scales[(b * a.n_index + row) * a.v_tiles + t] = 0.f;
+      }
+    }
+    return;
+  }
   while (mask != 0u) {
     const int l = __ffsll(static_cast<unsigned long long>(mask)) - 1;
     mask &= mask - 1u;
@@ -158,24 +198,28 @@ __global__ __launch_bounds__(BK_THREADS) void bucket_kernel(const RetrieveArgs a
 }
 
 // The same sort over many workgroups per sequence (three launches): counts per
-// chunk of BK_ITEMS pairs, per-(chunk, segment) bases, then the scatter.  The
-// order of pairs inside a segment does not change any result.
+// pair group, per-(group, segment) bases, then the scatter.  Group c holds the
+// blocks of BK_THREADS pairs c, c + bk_chunks, c + 2 bk_chunks, ... (about
+// BK_ITEMS pairs): strided rather than contiguous, so that the empty slots of
+// the first segments' short windows, which can fill most of the first 16384
+// pairs, are zeroed by every group instead of one or two.  The order of pairs
+// inside a segment does not change any result.
 template <class EM>
 __global__ __launch_bounds__(BK_THREADS) void bucket_count_kernel(const RetrieveArgs a) {
   extern __shared__ int hist[];  // [segments]
   const int tid = threadIdx.x;
   const int64_t b = blockIdx.y, chunk = blockIdx.x;
   const int64_t S = a.segments, n = a.n_index;
-  const int64_t i0 = chunk * BK_ITEMS, i1 = min(i0 + BK_ITEMS, n);
+  const int64_t n_blocks = (n + BK_THREADS - 1) / BK_THREADS;
   const int64_t* ib = a.idx + b * n;
   for (int64_t s = tid; s < S; s += BK_THREADS) hist[s] = 0;
   __syncthreads();
-  for (int64_t j0 = i0; j0 < i1; j0 += BK_THREADS) {  // uniform trip count: whole waves zero rows
-    const int64_t i = j0 + tid;
-    const int64_t s = i < i1 ? ib[i] : 0;
+  for (int64_t blk = chunk; blk < n_blocks; blk += a.bk_chunks) {  // uniform trip count: whole waves zero rows
+    const int64_t i = blk * BK_THREADS + tid;
+    const int64_t s = i < n ? ib[i] : 0;
     const bool valid = s >= 0 && s < S;
-    if (i < i1 && valid) atomicAdd(&hist[s], 1);
-    zero_rows_wave<EM>(a, b, i, i < i1 && !valid);
+    if (i < n && valid) atomicAdd(&hist[s], 1);
+    zero_rows_wave<EM>(a, b, i, i < n && !valid);
   }
   __syncthreads();
   int32_t* pc = a.partial + (b * a.bk_chunks + chunk) * S;
@@ -210,13 +254,15 @@ __global__ __launch_bounds__(BK_THREADS) void bucket_scatter_kernel(const Retrie
   const int tid = threadIdx.x;
   const int64_t b = blockIdx.y, chunk = blockIdx.x;
   const int64_t S = a.segments, n = a.n_index;
-  const int64_t i0 = chunk * BK_ITEMS, i1 = min(i0 + BK_ITEMS, n);
+  const int64_t n_blocks = (n + BK_THREADS - 1) / BK_THREADS;
   const int64_t* ib = a.idx + b * n;
   const int32_t* pc = a.partial + (b * a.bk_chunks + chunk) * S;
   for (int64_t s = tid; s < S; s += BK_THREADS) cur[s] = pc[s];
   __syncthreads();
   int32_t* lb = a.list + b * n;
-  for (int64_t i = i0 + tid; i < i1; i += BK_THREADS) {
+  for (int64_t blk = chunk; blk < n_blocks; blk += a.bk_chunks) {  // the count kernel's pair group
+    const int64_t i = blk * BK_THREADS + tid;
+    if (i >= n) continue;
     const int64_t s = ib[i];
     if (s >= 0 && s < S) lb[atomicAdd(&cur[s], 1)] = static_cast<int32_t>(i);
   }
@@ -1017,17 +1063,29 @@ int apply_scaled_q(const RetrieveArgs& a, int q_dtype, hipStream_t s) {
 // The queries' gradient of gather_apply: for every pair (q, r) with a valid
 // index, dqp[b, q, r, :] = M[b, idx[b, q, r]]^T g[b, q, r, :] (float32 grad_out
 // rows of d_v, float32 result rows of d_k); the caller sums over r.  One
-// workgroup per (sequence, work tile) stages its segment's state in LDS as
-// float32 (row stride d_k + 16 floats, so the 64 lanes of one read - 16
-// consecutive keys of 4 consecutive rows - hit 64 distinct banks) and applies
-// its transpose with float32 MFMA (16x16x4): wave w takes 16 pairs at a time,
-// A = M^T (keys x 4 rows), B = the pairs' grad_out rows.  Each output row is
-// written by one wave: deterministic, no atomics.
+// workgroup of 8 waves per (sequence, work tile) stages its segment's state in
+// LDS as float32, rows of d_v padded to a multiple of 16 with zeros, row stride
+// DKP + 4 floats, and applies its transpose with float32 MFMA (16x16x4).  Wave
+// w takes 16 pairs at a time: in MFMA j of value block v0, lane (kq, n) gives
+// A = M[v0 + 4 kq + j][16 kb + n] and B = g[pair n][v0 + 4 kq + j], so each
+// lane's gradient values of a block are one float4 (loaded a 128-value chunk
+// ahead of the MFMAs), and the four rows one A read touches (4 apart) start
+// 16 banks apart.  Each output row is written by one wave: deterministic, no
+// atomics.
+constexpr int AT_THREADS = 512;
+constexpr int AT_CHUNK = 8;  // value blocks of 16 per prefetched chunk
+
+template <int DKP>
+__host__ __device__ constexpr int at_row_stride() { return DKP + 4; }
+
+__host__ __device__ inline int at_rows(int dv) { return (dv + 15) / 16 * 16; }
+
 template <class EL, int DKP>
-__global__ __launch_bounds__(AP_THREADS) void apply_t_kernel(const RetrieveArgs a, const float* grad, float* dqp) {
+__global__ __launch_bounds__(AT_THREADS) void apply_t_kernel(const RetrieveArgs a, const float* grad, float* dqp,
+                                                             int vec_state, int vec_grad) {
   using rawl = typename ET<EL>::raw;
-  extern __shared__ float Ms[];  // [dv][DKP + 16]
-  constexpr int MSK = DKP + 16;
+  extern __shared__ float Ms[];  // [at_rows(dv)][DKP + 4]
+  constexpr int MSK = at_row_stride<DKP>();
   constexpr int KB = DKP / 16;
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -1038,36 +1096,79 @@ __global__ __launch_bounds__(AP_THREADS) void apply_t_kernel(const RetrieveArgs 
   const int4 te = a.tiles[b * a.tb_max + tile];
   const int64_t s = te.x;
   const int p_begin = te.y, p_end = te.z;
-  const int dk = a.dk, dv = a.dv;
+  const int dk = a.dk, dv = a.dv, dv16 = at_rows(dv);
   const rawl* msrc = static_cast<const rawl*>(a.mem) + (b * a.segments + s) * dv * dk;
-  for (int e = tid; e < dv * DKP; e += AP_THREADS) {
-    const int v = e / DKP, k = e % DKP;
-    Ms[v * MSK + k] = k < dk ? ET<EL>::to_f(msrc[v * dk + k]) : 0.f;
+  if (vec_state) {
+    // dk == DKP and 16-byte aligned rows: 16 bytes of the state per thread and step
+    constexpr int PER = 16 / sizeof(rawl);
+    const int nvec = dv * DKP / PER;
+    for (int e = tid; e < nvec; e += AT_THREADS) {
+      const int idx = e * PER;
+      const int v = idx / DKP, k = idx % DKP;
+      rawl t[PER];
+      *reinterpret_cast<uint4*>(t) = *reinterpret_cast<const uint4*>(msrc + idx);
+#pragma unroll
+      for (int i = 0; i < PER; i += 4)
+        *reinterpret_cast<f32x4*>(Ms + v * MSK + k + i) =
+            f32x4{ET<EL>::to_f(t[i]), ET<EL>::to_f(t[i + 1]), ET<EL>::to_f(t[i + 2]), ET<EL>::to_f(t[i + 3])};
+    }
+    for (int e = dv * DKP + tid; e < dv16 * DKP; e += AT_THREADS) Ms[(e / DKP) * MSK + e % DKP] = 0.f;
+  } else {
+    for (int e = tid; e < dv16 * DKP; e += AT_THREADS) {
+      const int v = e / DKP, k = e % DKP;
+      Ms[v * MSK + k] = (v < dv && k < dk) ? ET<EL>::to_f(msrc[v * dk + k]) : 0.f;
+    }
   }
   __syncthreads();
   const int32_t* lb = a.list + b * a.n_index;
   const int n = lane & 15, kq = lane >> 4;
-  for (int p0 = p_begin + 16 * w; p0 < p_end; p0 += 64) {
-    const int pid = p0 + n < p_end ? lb[p0 + n] : -1;
+  const int n_chunks = (dv16 / 16 + AT_CHUNK - 1) / AT_CHUNK;
+  int p0 = p_begin + 16 * w;
+  int pid = p0 < p_end && p0 + n < p_end ? lb[p0 + n] : -1;
+  for (; p0 < p_end; p0 += 16 * (AT_THREADS / 64)) {
+    const int pn = p0 + 16 * (AT_THREADS / 64);
+    const int pid_next = pn + n < p_end ? lb[pn + n] : -1;
     const float* grow = grad + (b * a.n_index + (pid >= 0 ? pid : 0)) * static_cast<int64_t>(dv);
+    auto load_chunk = [&](f32x4* g, int c) {
+#pragma unroll
+      for (int u = 0; u < AT_CHUNK; ++u) {
+        const int vq = 16 * (AT_CHUNK * c + u) + 4 * kq;
+        f32x4 x{0.f, 0.f, 0.f, 0.f};
+        if (pid >= 0) {
+          if (vec_grad) {
+            if (vq < dv) x = *reinterpret_cast<const f32x4*>(grow + vq);
+          } else {
+#pragma unroll
+            for (int r = 0; r < 4; ++r)
+              if (vq + r < dv) x[r] = grow[vq + r];
+          }
+        }
+        g[u] = x;
+      }
+    };
     f32x4 acc[KB];
 #pragma unroll
     for (int kb = 0; kb < KB; ++kb) acc[kb] = f32x4{0.f, 0.f, 0.f, 0.f};
-    for (int v0 = 0; v0 < dv; v0 += 16) {
-      float bg[4];
+    f32x4 cur[AT_CHUNK], nxt[AT_CHUNK];
+    load_chunk(cur, 0);
+    for (int c = 0; c < n_chunks; ++c) {
+      if (c + 1 < n_chunks) load_chunk(nxt, c + 1);
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const int v = v0 + 4 * j + kq;
-        bg[j] = (pid >= 0 && v < dv) ? grow[v] : 0.f;
-      }
+      for (int u = 0; u < AT_CHUNK; ++u) {
+        const int v0 = 16 * (AT_CHUNK * c + u);
+        if (v0 < dv16) {
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const int v = v0 + 4 * j + kq;
+          for (int j = 0; j < 4; ++j) {
+            const float* mrow = Ms + (v0 + 4 * kq + j) * MSK + n;
 #pragma unroll
-        for (int kb = 0; kb < KB; ++kb) {
-          const float am = v < dv ? Ms[v * MSK + 16 * kb + n] : 0.f;
-          acc[kb] = __builtin_amdgcn_mfma_f32_16x16x4f32(am, bg[j], acc[kb], 0, 0, 0);
+            for (int kb = 0; kb < KB; ++kb)
+              acc[kb] = __builtin_amdgcn_mfma_f32_16x16x4f32(mrow[16 * kb], cur[u][j], acc[kb], 0, 0, 0);
+          }
         }
+      }
+      if (c + 1 < n_chunks) {
+#pragma unroll
+        for (int u = 0; u < AT_CHUNK; ++u) cur[u] = nxt[u];
       }
     }
     // lane (kq, n) holds keys 16 kb + 4 kq + r of pair n (the pair its pid names)
@@ -1076,7 +1177,7 @@ __global__ __launch_bounds__(AP_THREADS) void apply_t_kernel(const RetrieveArgs 
 #pragma unroll
       for (int kb = 0; kb < KB; ++kb) {
         const int k = 16 * kb + 4 * kq;
-        if (k + 4 <= dk) {
+        if (k + 4 <= dk && (dk & 3) == 0) {
           *reinterpret_cast<f32x4*>(orow + k) = acc[kb];
         } else {
 #pragma unroll
@@ -1085,12 +1186,18 @@ __global__ __launch_bounds__(AP_THREADS) void apply_t_kernel(const RetrieveArgs 
         }
       }
     }
+    pid = pid_next;
   }
+}
+
+inline size_t apply_t_lds(int dv, int dkp) {
+  return static_cast<size_t>(at_rows(dv)) * (dkp + 4) * sizeof(float);
 }
 
 template <class EL, int DKP>
 int launch_apply_t(const RetrieveArgs& a, const float* grad, float* dqp, hipStream_t s) {
-  const size_t lds = static_cast<size_t>(a.dv) * (DKP + 16) * sizeof(float);
+  using rawl = typename ET<EL>::raw;
+  const size_t lds = apply_t_lds(a.dv, DKP);
   static bool attr_set = false;
   if (!attr_set) {
     hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&apply_t_kernel<EL, DKP>),
@@ -1101,8 +1208,11 @@ int launch_apply_t(const RetrieveArgs& a, const float* grad, float* dqp, hipStre
     }
     attr_set = true;
   }
+  const int vec_state = a.dk == DKP && (DKP * sizeof(rawl)) % 16 == 0 &&
+                        reinterpret_cast<uintptr_t>(a.mem) % 16 == 0;
+  const int vec_grad = a.dv % 4 == 0 && reinterpret_cast<uintptr_t>(grad) % 16 == 0;
   const dim3 grid(static_cast<unsigned>(a.tb_max), static_cast<unsigned>(a.batch));
-  hipLaunchKernelGGL((apply_t_kernel<EL, DKP>), grid, dim3(AP_THREADS), lds, s, a, grad, dqp);
+  hipLaunchKernelGGL((apply_t_kernel<EL, DKP>), grid, dim3(AT_THREADS), lds, s, a, grad, dqp, vec_state, vec_grad);
   return check_launch("gather_apply_bwd");
 }
 
@@ -1429,7 +1539,8 @@ extern "C" int grm_hip_gather_apply_bwd_queries(const void* memories, const int6
     return GRM_HIP_EUNSUPPORTED;
   }
   const int64_t dkp = key_dim <= 16 ? 16 : key_dim <= 32 ? 32 : key_dim <= 64 ? 64 : 128;
-  if (key_dim > 128 || segments > kMaxSegments || hidden_size * (dkp + 16) * 4 > 160 * 1024) {
+  if (key_dim > 128 || segments > kMaxSegments || hidden_size > (1 << 20) ||
+      apply_t_lds(static_cast<int>(hidden_size), static_cast<int>(dkp)) > 160 * 1024) {
     set_error("gather_apply_bwd: needs key_dim <= 128, segments <= %lld and the float32 state in LDS",
               (long long)kMaxSegments);
     return GRM_HIP_EUNSUPPORTED;

@@ -563,11 +563,15 @@ class SegmentRecurrentMemoryModel(nn.Module):
         filled = idx >= 0
         idx0 = idx.clamp(min=0)
         if grad:
-            # Differentiable gates: the selected scores again, as torch ops.
-            # Indexing k_r directly keeps the backward at [B, S, D] (a gather from an
-            # expanded [B, T, S, D] view would scatter into a dense tensor of that size).
-            rows = torch.arange(B, device=idx0.device).view(B, 1, 1)
-            scores = (q_r.unsqueeze(2) * k_r[rows, idx0]).sum(-1) * gu.scale
+            # Differentiable gates: the selected scores again, as torch ops.  All scores
+            # as one product (paper_grm.py:573), then the selected ones gathered: the
+            # backward is a scatter into [B, T, S] and two GEMMs.  (Indexing k_r by the
+            # [B, T, k] indices instead makes the backward an index_put with many
+            # repeated indices, tens of ms per layer at 4 x 8192 tokens.)  float32
+            # operands, with the keys' transpose materialised, keep the batched
+            # products and their backward off 16-bit transposed views.
+            scores_all = torch.matmul(q_r.float(), k_r.float().transpose(1, 2).contiguous())
+            scores = scores_all.gather(-1, idx0) * gu.scale
             scores = scores.masked_fill(~filled, float("-inf"))
             gates = torch.softmax(scores.float() / gu.temperature, dim=-1).masked_fill(~filled, 0.0)
         gates = gu.dropout(gates)

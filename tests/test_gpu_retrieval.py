@@ -635,7 +635,8 @@ def test_retrieve_fuse_op_and_model_path(dev):
 # ---------------------------------------------------------------- gather_apply backward (queries)
 @pytest.mark.parametrize("mem_dtype", [torch.float32, torch.float16, torch.bfloat16])
 @pytest.mark.parametrize("B,Q,S,R,H,K", [(2, 100, 37, 5, 128, 128), (3, 64, 8, 8, 512, 64), (1, 129, 300, 16, 200, 32),
-                                         (2, 50, 5, 3, 8, 64), (1, 70, 3, 8, 40, 20)])
+                                         (2, 50, 5, 3, 8, 64), (1, 70, 3, 8, 40, 20), (1, 33, 6, 4, 30, 64),
+                                         (1, 1000, 4, 4, 64, 64)])
 def test_gather_apply_bwd_queries(dev, mem_dtype, B, Q, S, R, H, K):
     """The transposed apply (per pair M[idx]^T g, float32) summed over routes against the oracle's
     apply-query backward on the gathered states, at 1e-5 of the gradient's scale; invalid
@@ -681,3 +682,46 @@ def test_gather_apply_native_queries_gradient(dev):
     ref.square().sum().backward()
     torch.testing.assert_close(out.detach().cpu(), ref.detach(), rtol=1e-5, atol=1e-5)
     torch.testing.assert_close(q.grad.float().cpu(), q2.grad, rtol=1e-2, atol=1e-2)  # q.grad is bf16
+
+
+@pytest.mark.parametrize("Q", [700, 8200])
+def test_empty_slot_blocks(dev, Q):
+    """The short windows of the first segments leave whole blocks of empty slots (-1), which
+    a wave zeroes one row per lane.  gather_apply (float32 rows), retrieve_fuse (row-scaled
+    float16 rows and their scales) and the queries' gradient, through the one-workgroup sort
+    (5600 pairs) and the chunked sort (65600 pairs), against the oracle; empty slots counted."""
+    B, S, R, H, K = 2, 37, 8, 128, 16
+    g = torch.Generator().manual_seed(Q)
+    mem = (torch.randn(B, S, H, K, generator=g) * 0.3).to(torch.float16)
+    idx = torch.randint(0, S, (B, Q, R), generator=g)
+    idx[:, : Q // 3, 2:] = -1           # 48 of every 64 consecutive pairs empty
+    idx[1, Q // 2:Q // 2 + 40, :] = -1  # whole queries empty
+    n_bad = int((idx < 0).sum())
+    q = norm(torch.randn(B, Q, K, generator=g)).to(torch.bfloat16)
+    gates = torch.softmax(torch.randn(B, Q, R, generator=g), dim=-1)
+    h = torch.randn(B, Q, H, generator=g)
+    w, b = 1 + 0.1 * torch.randn(H, generator=g), 0.1 * torch.randn(H, generator=g)
+    grad = torch.randn(B, Q, R, H, generator=g)
+    print(f"empty slot blocks Q={Q} bad={n_bad}", flush=True)
+    ok = (idx >= 0).numpy()
+    gathered, _ = orc.gather(mem.double().numpy(), np.where(ok, idx.numpy(), 0))
+    gathered = gathered * ok[..., None, None]
+    D = lambda t: t.to(dev)  # noqa: E731
+    for name in ("gather_apply", "retrieve_fuse", "bwd_queries"):
+        bad = torch.zeros(1, dtype=torch.int32, device=dev)
+        if name == "gather_apply":
+            out = capi.gather_apply(D(mem), D(idx), D(q), bad_count=bad, dtype=torch.float32)
+            ref = orc.apply_query(gathered, q.double().numpy())
+            np.testing.assert_allclose(out.cpu().double().numpy(), ref, rtol=1e-5, atol=1e-6)
+        elif name == "retrieve_fuse":
+            out = capi.retrieve_fuse(D(mem), D(idx), D(q), D(gates), D(h), D(w), D(b), bad_count=bad)
+            ref = _retrieve_fuse_ref(mem, idx, q, gates, h, w, b)
+            np.testing.assert_allclose(out.cpu().double().numpy(), ref, rtol=2e-3, atol=2e-3)
+        else:
+            out = capi.gather_apply_bwd_queries(D(mem), D(idx), D(grad), bad_count=bad)
+            assert not out[:, : Q // 3, 2:].any()
+            _, ref = orc.apply_query_bwd(grad.double().numpy(), gathered, q.double().numpy())
+            np.testing.assert_allclose(out.sum(2).double().cpu().numpy(), ref, rtol=1e-5,
+                                       atol=1e-5 * max(1.0, float(np.abs(ref).max())))
+        torch.cuda.synchronize()
+        assert int(bad.item()) == n_bad, name
