@@ -157,7 +157,7 @@ def bench_n1(torch, dev, steps, warmup):
 
 def bench_c2_bwd(torch, dev, steps, warmup):
     """chunk_update_backward at config 2 through the C ABI: the forward recompute of the
-    chunk states, the chunk-parallel MFMA backward and the tile sums, timed with events
+    chunk states, the adjoint pass and the per-chunk MFMA gradients, timed with events
     around `steps` back-to-back calls."""
     from rnn_with_grm_amd import capi
 
@@ -828,11 +828,11 @@ def main() -> int:
                                           "TFLOP/s": round(r["flops"] / r["us"] / 1e6, 2)})
             log(f"{label}: {r['us']:.1f} us")
     if not a.no_gather or a.bwd_only:
-        log("config 2 backward (chunk_update_backward: recompute + MFMA backward + tile sums)")
+        log("config 2 backward (chunk_update_backward: recompute, adjoint pass, per-chunk MFMA gradients)")
         bw = bench_c2_bwd(torch, dev, max(3, a.steps // 2), 2)
         secondary["c2_backward"] = {
             "what": "chunk_update_backward at config 2 (bf16 q/k/v, fp32 state): forward recompute of the 32 "
-                    "chunk states, chunk-parallel MFMA backward, tile sums; events around back-to-back calls",
+                    "chunk states, adjoint pass, per-chunk MFMA gradients; events around back-to-back calls",
             "ms": round(bw["ms"], 4), "tokens/s": round(bw["tokens"] / bw["ms"] * 1e3)}
         log(f"c2 backward: {bw['ms']:.3f} ms per call")
     if not a.no_gather:

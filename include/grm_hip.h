@@ -116,9 +116,10 @@ int grm_hip_chunk_update_fwd_noalloc(const void* keys, const void* values, const
  *   forward as the op's aux); otherwise it is a workspace that the backward fills by
  *   running the forward again.
  * dkq_partial: float32 workspace [2, batch, ceil(value_dim / 16), seq_len, key_dim]
- *   (caller-provided; per value-tile partial sums of grad_keys and grad_queries: 16-column
- *   tiles in the scalar kernel, 32-column tiles [2, batch, value_dim / 32, seq_len, key_dim]
- *   at the front of the same buffer in the MFMA kernel for 16-bit inputs).
+ *   (caller-provided).  The scalar kernel keeps per 16-column value tile partial sums of
+ *   grad_keys and grad_queries there; the MFMA kernels for 16-bit inputs keep the adjoint
+ *   dL/dM at every 64-token chunk end, [batch, ceil(seq_len / 64), value_dim, key_dim], at
+ *   its front (they run when that fits, from about ten tokens on).
  */
 int grm_hip_chunk_update_bwd(const void* grad_hidden, const void* grad_memory_out, const void* keys,
                              const void* values, const void* queries, const void* memory,

@@ -242,28 +242,6 @@ __global__ __launch_bounds__(256) void tile_sum_kernel(const float* part, void* 
   }
 }
 
-// The same sum for two partial arrays at once, 16 bytes of each tile per
-// thread: quad i of [batch, T * dk / 4] (plane = T * dk / 4 quads per
-// sequence); thread indices from `quads` on take the second array.
-template <class E>
-__global__ __launch_bounds__(256) void tile_sum4_kernel(const float* part0, const float* part1, void* out0,
-                                                        void* out1, int tiles, int64_t plane, int64_t quads) {
-  for (int64_t j = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x; j < 2 * quads;
-       j += static_cast<int64_t>(gridDim.x) * 256) {
-    const bool second = j >= quads;
-    const int64_t i = second ? j - quads : j;
-    const int64_t b = i / plane;
-    using f32x4 = float __attribute__((ext_vector_type(4)));
-    const f32x4* p = reinterpret_cast<const f32x4*>(second ? part1 : part0) + b * tiles * plane + (i - b * plane);
-    f32x4 acc = __builtin_nontemporal_load(p);
-    for (int t = 1; t < tiles; ++t) acc += __builtin_nontemporal_load(p + t * plane);
-    static_assert(sizeof(typename ET<E>::raw) == 2, "16-bit outputs");
-    const uint32_t lo = static_cast<uint32_t>(ET<E>::from_f(acc[0])) | static_cast<uint32_t>(ET<E>::from_f(acc[1])) << 16;
-    const uint32_t hi = static_cast<uint32_t>(ET<E>::from_f(acc[2])) | static_cast<uint32_t>(ET<E>::from_f(acc[3])) << 16;
-    reinterpret_cast<uint2*>(second ? out1 : out0)[i] = make_uint2(lo, hi);
-  }
-}
-
 template <class E>
 int launch_bwd(const BwdArgs& a, void* grad_keys, void* grad_queries, hipStream_t s) {
   const dim3 grid(static_cast<unsigned>(a.batch * a.tiles));
@@ -291,28 +269,30 @@ int launch_bwd(const BwdArgs& a, void* grad_keys, void* grad_queries, hipStream_
 
 // ---------------------------------------------------------------------------
 // Chunk-parallel MFMA backward for 16-bit inputs (key_dim <= 128, value_dim a
-// multiple of 32, 16-byte rows).  The per-token recurrence above, summed over a
-// 64-token chunk: from the chunk's starting state M (the forward's chunk
-// states) and the adjoint G at its end (dL/dM after its last token), with
-// D[i][j] = decay^{i-j} (j <= i), P = c (Q K^T) o D and dS = c (dH V^T) o D,
+// multiple of 32, 16-byte rows), two kernels.  Per 64-token chunk, from the
+// chunk's starting state M (the forward's chunk states) and the adjoint G at its
+// end (dL/dM after its last token), with D[i][j] = decay^{i-j} (j <= i),
+// P = c (Q K^T) o D and dS = c (dH V^T) o D:
 //   dQ = decay^{i+1} dH M + dS K
 //   dK = dS^T Q + c decay^{L-1-j} V G
 //   dV = P^T dH + c decay^{L-1-j} K G^T
 //   G  <- decay^L G + dH^T diag(decay^{i+1}) Q      (the adjoint at the chunk's start)
-// One workgroup of 4 waves per (sequence, 32-column value tile) walks the
-// chunks from the last.  The tile's G lives in fp32 MFMA accumulators.  The
-// fp32 operands of the products (G, the chunk's starting state M and the
-// decay-weighted dH of the adjoint update) enter the MFMAs as hi + lo pairs of
-// 16-bit values (hi = x rounded, lo = x - hi rounded), two MFMAs per product,
-// so each carries ~16 (bf16) or ~22 (f16) significant bits instead of 8 / 11:
-// rounding them to one 16-bit value costs bf16 inputs ~1e-3 absolute error on
-// grad_memory over a few hundred tokens.  dQ and dK sum over every
-// value column, so each tile writes a partial and tile_sum_kernel adds the
-// tiles in order: deterministic, no atomics.  Wave w owns query/key block w
-// (tokens [16w, +16)) of every product and G rows [16 (w & 1), +16) x key
-// tiles [KT/2 (w >> 1), +KT/2).
-constexpr int MB_DV = 32;
+// Only the last line carries from chunk to chunk.  bwd_adjoint_kernel walks it
+// from the last chunk (one workgroup per sequence and 64 value rows, G in fp32
+// MFMA accumulators) and stores G at every chunk end.  bwd_grad_kernel then
+// takes one (sequence, chunk) per workgroup and all of its value columns, in
+// 32-column tiles: dQ and dK are summed over the whole value dimension in
+// registers and written once, dV tile by tile, so there are no partial sums to
+// add afterwards and the chunks run in parallel.  The fp32 operands of the
+// products (G, M and the decay-weighted dH of the adjoint update) enter the
+// MFMAs as hi + lo pairs of 16-bit values (hi = x rounded, lo = x - hi
+// rounded), two MFMAs per product, so each carries ~16 (bf16) or ~22 (f16)
+// significant bits instead of 8 / 11: rounding them to one 16-bit value costs
+// bf16 inputs ~1e-3 absolute error on grad_memory over a few hundred tokens.
+// Wave w owns query/key block w (tokens [16w, +16)) of every per-chunk product.
+constexpr int MB_DV = 32;  // value columns per tile of bwd_grad_kernel
 constexpr int MB_NT = 256;
+constexpr int AJ_V = 64;   // value rows per bwd_adjoint_kernel workgroup (16 per wave)
 
 struct BwdMArgs {
   const void* dh;
@@ -322,15 +302,15 @@ struct BwdMArgs {
   const void* queries;
   const void* memory;
   const float* states;  // [B, n_chunks, dv, dk] state after each chunk
+  float* gbuf;          // [B, n_chunks, dv, dk] adjoint at each chunk's end
+  void* dq_out;
+  void* dk_out;
   void* dv_out;
   void* dm_out;
-  float* part_k;  // [B, tiles, T, dk]
-  float* part_q;  // [B, tiles, T, dk]
   int64_t batch;
   int64_t T;
   int dk;
   int dv;
-  int tiles;
   int n_chunks;
   int mem_f32;
   int xcd_remap;
@@ -339,7 +319,19 @@ struct BwdMArgs {
 };
 
 template <int DKP>
-struct BmShape {
+struct AjShape {
+  static constexpr int KS = DKP + 8;   // Q rows (4 banks mod 64)
+  static constexpr int HS = AJ_V + 8;  // dH rows of the tile
+  static constexpr int KT = DKP / 16;
+  static constexpr int KU = DKP / 8;
+  static constexpr int K_UNITS = BCT * KU / MB_NT;
+  static constexpr int H_UNITS = BCT * (AJ_V / 8) / MB_NT;
+  static constexpr size_t lds_bytes = static_cast<size_t>(BCT * KS + BCT * HS) * 2 + (BCT + 1) * 4;
+  static_assert(K_UNITS * MB_NT == BCT * KU && H_UNITS * MB_NT == BCT * (AJ_V / 8), "tiles split evenly");
+};
+
+template <int DKP>
+struct GrShape {
   static constexpr int KS = DKP + 8;    // K, Q and 16-bit M, G rows (4 banks mod 64)
   static constexpr int VS = MB_DV + 8;  // V, dH rows
   static constexpr int PS = BCT + 8;    // P, dS rows
@@ -349,7 +341,7 @@ struct BmShape {
   static constexpr int K_UNITS = BCT * KU / MB_NT;
   static constexpr int M_UNITS = MB_DV * KU / MB_NT;
   static constexpr size_t lds_bytes =
-      static_cast<size_t>(2 * BCT * KS + 2 * BCT * VS + 6 * MB_DV * KS + 2 * BCT * PS) * 2 + (BCT + 1) * 4;
+      static_cast<size_t>(2 * BCT * KS + 2 * BCT * VS + 4 * MB_DV * KS + 2 * BCT * PS) * 2 + (BCT + 1) * 4;
   static_assert(K_UNITS * MB_NT == BCT * KU && M_UNITS * MB_NT == MB_DV * KU, "tiles split evenly");
 };
 
@@ -382,14 +374,177 @@ __device__ __forceinline__ void store4_split(typename ET<E>::raw* hi, typename E
   store4_raw<E>(lo, r);
 }
 
+// The adjoint recurrence.  Lane (g, n) of wave w holds gacc[t][r] =
+// G[v][k], v = v0 + 16 w + n, k = 16 t + 4 g + r.  Chunk staging: the loads of
+// chunk ch - 1 are in flight while chunk ch is processed.
 template <class E, int DKP>
-__global__ __launch_bounds__(MB_NT, 1) void chunk_bwd_mfma_kernel(const BwdMArgs a) {
-  using S = BmShape<DKP>;
+__global__ __launch_bounds__(MB_NT) void bwd_adjoint_kernel(const BwdMArgs a) {
+  using S = AjShape<DKP>;
   using raw = typename ET<E>::raw;
   typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
   typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+  constexpr int KS = S::KS, HS = S::HS, KT = S::KT, KU = S::KU;
+  constexpr int ES = 2;
+
+  extern __shared__ __align__(16) unsigned char smem[];
+  raw* Qs = reinterpret_cast<raw*>(smem);  // [BCT][KS]
+  raw* Hs = Qs + BCT * KS;                  // [BCT][HS] grad_hidden, the tile's value columns
+  float* pw = reinterpret_cast<float*>(Hs + BCT * HS);
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int g = lane >> 4;
+  const int n = lane & 15;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int vtiles = (a.dv + AJ_V - 1) / AJ_V;
+  int wg = blockIdx.x;
+  if (a.xcd_remap) {  // the value tiles of one sequence (same queries) on one XCD
+    const int per = gridDim.x >> 3;
+    wg = (wg & 7) * per + (wg >> 3);
+  }
+  const int tile = wg % vtiles;
+  const int64_t b = wg / vtiles;
+  const int v0 = tile * AJ_V;
+  const int dk = a.dk, dv = a.dv;
+  const int64_t T = a.T;
+  const int last_len = static_cast<int>(T - static_cast<int64_t>(a.n_chunks - 1) * BCT);
+  const raw* queries = static_cast<const raw*>(a.queries) + b * T * dk;
+  const raw* dh = static_cast<const raw*>(a.dh) + b * T * dv;
+  if (tid <= BCT) pw[tid] = a.pw[tid];
+  const int vrow = v0 + 16 * w + n;
+  const int64_t mem_b = a.mem_f32 ? 4 : ES;
+  auto g_off = [&](int t) -> int {
+    const int k = 16 * t + 4 * g;
+    return (vrow < dv && k < dk) ? vrow * dk + k : -1;
+  };
+  f32x4 gacc[KT];
+  {
+    const __amdgpu_buffer_rsrc_t rg = make_rsrc(static_cast<const unsigned char*>(a.dmo) + b * dv * dk * mem_b,
+                                                static_cast<uint32_t>(dv * dk * mem_b));
+#pragma unroll
+    for (int t = 0; t < KT; ++t) {
+      const int off = g_off(t);
+      if (a.mem_f32) {
+        const u32x4 u = __builtin_amdgcn_raw_buffer_load_b128(rg, off < 0 ? kBufOOB : off * 4, 0, 0);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) gacc[t][i] = __uint_as_float(u[i]);
+      } else {
+        const u32x2 u = __builtin_amdgcn_raw_buffer_load_b64(rg, off < 0 ? kBufOOB : off * ES, 0, 0);
+        gacc[t][0] = ET<E>::to_f(static_cast<raw>(u[0] & 0xffffu));
+        gacc[t][1] = ET<E>::to_f(static_cast<raw>(u[0] >> 16));
+        gacc[t][2] = ET<E>::to_f(static_cast<raw>(u[1] & 0xffffu));
+        gacc[t][3] = ET<E>::to_f(static_cast<raw>(u[1] >> 16));
+      }
+    }
+  }
+  __syncthreads();  // pw
+  // decay^{i+1} of the token slots i = 32p + 16 (s / 4) + 4g + s % 4
+  float gw[2][8];
+#pragma unroll
+  for (int p = 0; p < 2; ++p)
+#pragma unroll
+    for (int s = 0; s < 8; ++s) gw[p][s] = pw[32 * p + 16 * (s >> 2) + 4 * g + (s & 3) + 1];
+
+  struct Stage {
+    U8<E> q[S::K_UNITS];
+    U8<E> h[S::H_UNITS];
+  };
+  auto load_chunk = [&](int ch, Stage& sg) {
+    const int64_t t0 = static_cast<int64_t>(ch) * BCT;
+    const int L = ch == a.n_chunks - 1 ? last_len : BCT;
+    const __amdgpu_buffer_rsrc_t rq = make_rsrc(queries + t0 * dk, static_cast<uint32_t>(L * dk * ES));
+    const __amdgpu_buffer_rsrc_t rh = make_rsrc(dh + t0 * dv, static_cast<uint32_t>(L * dv * ES));
+#pragma unroll
+    for (int u = 0; u < S::K_UNITS; ++u) {
+      const int l = tid + MB_NT * u;
+      const int row = l / KU, col = 8 * (l % KU);
+      sg.q[u] = buf_load8<E>(rq, col < dk ? (row * dk + col) * ES : kBufOOB);
+    }
+#pragma unroll
+    for (int u = 0; u < S::H_UNITS; ++u) {
+      const int l = tid + MB_NT * u;
+      const int row = l / (AJ_V / 8), col = 8 * (l % (AJ_V / 8));
+      sg.h[u] = buf_load8<E>(rh, v0 + col < dv ? (row * dv + v0 + col) * ES : kBufOOB);
+    }
+  };
+  auto store_chunk = [&](const Stage& sg) {
+#pragma unroll
+    for (int u = 0; u < S::K_UNITS; ++u) {
+      const int l = tid + MB_NT * u;
+      *reinterpret_cast<U8<E>*>(Qs + (l / KU) * KS + 8 * (l % KU)) = sg.q[u];
+    }
+#pragma unroll
+    for (int u = 0; u < S::H_UNITS; ++u) {
+      const int l = tid + MB_NT * u;
+      *reinterpret_cast<U8<E>*>(Hs + (l / (AJ_V / 8)) * HS + 8 * (l % (AJ_V / 8))) = sg.h[u];
+    }
+  };
+
+  Stage stage;
+  load_chunk(a.n_chunks - 1, stage);
+  for (int ch = a.n_chunks - 1; ch >= 0; --ch) {
+    const int L = ch == a.n_chunks - 1 ? last_len : BCT;
+    store_chunk(stage);
+    if (ch > 0) load_chunk(ch - 1, stage);
+    __syncthreads();  // chunk in LDS
+    {
+      // the adjoint at this chunk's end, for bwd_grad_kernel
+      const __amdgpu_buffer_rsrc_t rs =
+          make_rsrc(a.gbuf + (b * a.n_chunks + ch) * dv * dk, static_cast<uint32_t>(dv * dk * 4));
+#pragma unroll
+      for (int t = 0; t < KT; ++t) {
+        const int off = g_off(t);
+        buf_store4<F32>(rs, off < 0 ? kBufOOB : off * 4, gacc[t]);
+      }
+    }
+    Frag8<E> hw[2], hwl[2];
+#pragma unroll
+    for (int p = 0; p < 2; ++p) {
+      const raw* hb = Hs + (32 * p + 4 * g + (n >> 2)) * HS + 16 * w + 4 * (n & 3);
+      const Frag8<E> h = bw_frag_tr<E>(hb, hb + 16 * HS);
+#pragma unroll
+      for (int s = 0; s < 8; ++s) {
+        const float x = ET<E>::to_f(h.e[s]) * gw[p][s];
+        hw[p].e[s] = ET<E>::from_f(x);
+        hwl[p].e[s] = ET<E>::from_f(x - ET<E>::to_f(hw[p].e[s]));
+      }
+    }
+    const float decay_L = pw[L];
+#pragma unroll
+    for (int t = 0; t < KT; ++t) {
+      f32x4 acc = gacc[t] * decay_L;
+#pragma unroll
+      for (int p = 0; p < 2; ++p) {
+        const raw* qb = Qs + (32 * p + 4 * g + (n >> 2)) * KS + 16 * t + 4 * (n & 3);
+        const Frag8<E> qT = bw_frag_tr<E>(qb, qb + 16 * KS);
+        acc = mfma8(qT, hw[p], acc);
+        acc = mfma8(qT, hwl[p], acc);
+      }
+      gacc[t] = acc;
+    }
+    __syncthreads();  // every read of this chunk's tiles done
+  }
+  // grad_memory: the adjoint at the sequence's start.
+  const __amdgpu_buffer_rsrc_t ro = make_rsrc(static_cast<unsigned char*>(a.dm_out) + b * dv * dk * mem_b,
+                                              static_cast<uint32_t>(dv * dk * mem_b));
+#pragma unroll
+  for (int t = 0; t < KT; ++t) {
+    const int off = g_off(t);
+    if (a.mem_f32) {
+      buf_store4<F32>(ro, off < 0 ? kBufOOB : off * 4, gacc[t]);
+    } else {
+      buf_store4<E>(ro, off < 0 ? kBufOOB : off * ES, gacc[t]);
+    }
+  }
+}
+
+// The gradients of one chunk from its starting state and the adjoint at its end.
+template <class E, int DKP>
+__global__ __launch_bounds__(MB_NT) void bwd_grad_kernel(const BwdMArgs a) {
+  using S = GrShape<DKP>;
+  using raw = typename ET<E>::raw;
+  typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
   constexpr int KS = S::KS, VS = S::VS, PS = S::PS, KT = S::KT, NKK = S::NKK, KU = S::KU;
-  constexpr int GT = KT / 2;  // G key tiles per wave
   constexpr int ES = 2;
 
   extern __shared__ __align__(16) unsigned char smem[];
@@ -399,9 +554,9 @@ __global__ __launch_bounds__(MB_NT, 1) void chunk_bwd_mfma_kernel(const BwdMArgs
   raw* Hs = Vs + BCT * VS;                  // [BCT][VS] grad_hidden tile columns
   raw* Ms = Hs + BCT * VS;                  // [MB_DV][KS] the chunk's starting state, hi
   raw* Ml = Ms + MB_DV * KS;                // [MB_DV][KS] ... lo
-  raw* Gs = Ml + MB_DV * KS;                // 2 x [MB_DV][KS] adjoint at the chunk's end, hi
-  raw* Gl = Gs + 2 * MB_DV * KS;            // 2 x [MB_DV][KS] ... lo
-  raw* Ps = Gl + 2 * MB_DV * KS;            // [BCT][PS] P
+  raw* Gs = Ml + MB_DV * KS;                // [MB_DV][KS] adjoint at the chunk's end, hi
+  raw* Gl = Gs + MB_DV * KS;                // [MB_DV][KS] ... lo
+  raw* Ps = Gl + MB_DV * KS;                // [BCT][PS] P
   raw* Ds = Ps + BCT * PS;                  // [BCT][PS] dS
   float* pw = reinterpret_cast<float*>(Ds + BCT * PS);
 
@@ -410,67 +565,110 @@ __global__ __launch_bounds__(MB_NT, 1) void chunk_bwd_mfma_kernel(const BwdMArgs
   const int g = lane >> 4;
   const int n = lane & 15;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
-
-  int wg = blockIdx.x;
-  if (a.xcd_remap) {
-    const int per = gridDim.x >> 3;
-    wg = (wg & 7) * per + (wg >> 3);
-  }
-  const int tile = wg % a.tiles;
-  const int64_t b = wg / a.tiles;
-  const int v0 = tile * MB_DV;
+  const int ch = static_cast<int>(blockIdx.x % static_cast<unsigned>(a.n_chunks));
+  const int64_t b = blockIdx.x / static_cast<unsigned>(a.n_chunks);
   const int dk = a.dk, dv = a.dv;
   const int64_t T = a.T;
-  // 32-bit chunk lengths (a 64-bit min would be a VALU compare in the loop)
-  const int last_len = static_cast<int>(T - static_cast<int64_t>(a.n_chunks - 1) * BCT);
+  const int64_t t0 = static_cast<int64_t>(ch) * BCT;
+  const int L = ch == a.n_chunks - 1 ? static_cast<int>(T - t0) : BCT;
   const float c = a.c;
   const bool f32m = a.mem_f32 != 0;
-  const raw* keys = static_cast<const raw*>(a.keys) + b * T * dk;
-  const raw* queries = static_cast<const raw*>(a.queries) + b * T * dk;
-  const raw* values = static_cast<const raw*>(a.values) + b * T * dv;
-  const raw* dh = static_cast<const raw*>(a.dh) + b * T * dv;
+  const raw* keys = static_cast<const raw*>(a.keys) + (b * T + t0) * dk;
+  const raw* queries = static_cast<const raw*>(a.queries) + (b * T + t0) * dk;
+  const raw* values = static_cast<const raw*>(a.values) + (b * T + t0) * dv;
+  const raw* dh = static_cast<const raw*>(a.dh) + (b * T + t0) * dv;
   if (tid <= BCT) pw[tid] = a.pw[tid];
-
-  // ---- the adjoint: gacc[t], lane (g, n), register r = G[v][k] with
-  //      v = v0 + 16 gvb + n and k = 16 (gk0 + t) + 4g + r.
-  const int gvb = w & 1, gk0 = GT * (w >> 1);
-  f32x4 gacc[GT];
-  auto g_off = [&](int t) -> int {
-    const int k = 16 * (gk0 + t) + 4 * g;
-    return k < dk ? (v0 + 16 * gvb + n) * dk + k : kBufOOB;
-  };
-  const int64_t mem_b = f32m ? 4 : ES;
   {
-    const __amdgpu_buffer_rsrc_t rg = make_rsrc(static_cast<const unsigned char*>(a.dmo) + b * dv * dk * mem_b,
-                                                static_cast<uint32_t>(dv * dk * mem_b));
+    const __amdgpu_buffer_rsrc_t rk = make_rsrc(keys, static_cast<uint32_t>(L * dk * ES));
+    const __amdgpu_buffer_rsrc_t rq = make_rsrc(queries, static_cast<uint32_t>(L * dk * ES));
+    U8<E> kx[S::K_UNITS], qx[S::K_UNITS];
 #pragma unroll
-    for (int t = 0; t < GT; ++t) {
-      const int off = g_off(t);
-      if (f32m) {
-        const u32x4 u = __builtin_amdgcn_raw_buffer_load_b128(rg, off == kBufOOB ? kBufOOB : off * 4, 0, 0);
+    for (int u = 0; u < S::K_UNITS; ++u) {
+      const int l = tid + MB_NT * u;
+      const int row = l / KU, col = 8 * (l % KU);
+      const int off = col < dk ? (row * dk + col) * ES : kBufOOB;
+      kx[u] = buf_load8<E>(rk, off);
+      qx[u] = buf_load8<E>(rq, off);
+    }
 #pragma unroll
-        for (int i = 0; i < 4; ++i) gacc[t][i] = __uint_as_float(u[i]);
-      } else {
-        const u32x2 u = __builtin_amdgcn_raw_buffer_load_b64(rg, off == kBufOOB ? kBufOOB : off * ES, 0, 0);
-        gacc[t][0] = ET<E>::to_f(static_cast<raw>(u[0] & 0xffffu));
-        gacc[t][1] = ET<E>::to_f(static_cast<raw>(u[0] >> 16));
-        gacc[t][2] = ET<E>::to_f(static_cast<raw>(u[1] & 0xffffu));
-        gacc[t][3] = ET<E>::to_f(static_cast<raw>(u[1] >> 16));
-      }
+    for (int u = 0; u < S::K_UNITS; ++u) {
+      const int l = tid + MB_NT * u;
+      const int row = l / KU, col = 8 * (l % KU);
+      *reinterpret_cast<U8<E>*>(Ks + row * KS + col) = kx[u];
+      *reinterpret_cast<U8<E>*>(Qs + row * KS + col) = qx[u];
     }
   }
-  auto publish_g = [&](int slot) {
-    const int base = slot * MB_DV * KS + (16 * gvb + n) * KS + 4 * g;
-#pragma unroll
-    for (int t = 0; t < GT; ++t) store4_split<E>(Gs + base + 16 * (gk0 + t), Gl + base + 16 * (gk0 + t), gacc[t]);
+
+  // Value tile staging: V / dH unit of thread t is row t / 4, columns 8 (t % 4)
+  // of the tile; state / adjoint unit u is row (t + 256 u) / KU of the tile, 8
+  // key columns (fp32, or 16-bit in m[u][0] for a 16-bit initial memory).
+  struct Stage {
+    U8<E> v, h;
+    u32x4 m[S::M_UNITS][2];
+    u32x4 gg[S::M_UNITS][2];
   };
-  publish_g(0);
-  int gslot = 0;
-  __syncthreads();  // pw
+  const unsigned char* msrc = ch == 0 ? static_cast<const unsigned char*>(a.memory) + b * dv * dk * (f32m ? 4 : ES)
+                                      : reinterpret_cast<const unsigned char*>(
+                                            a.states + (b * a.n_chunks + ch - 1) * dv * dk);
+  const bool m32 = ch != 0 || f32m;
+  const __amdgpu_buffer_rsrc_t rm = make_rsrc(msrc, static_cast<uint32_t>(dv * dk * (m32 ? 4 : ES)));
+  const __amdgpu_buffer_rsrc_t rg =
+      make_rsrc(a.gbuf + (b * a.n_chunks + ch) * dv * dk, static_cast<uint32_t>(dv * dk * 4));
+  const __amdgpu_buffer_rsrc_t rv = make_rsrc(values, static_cast<uint32_t>(L * dv * ES));
+  const __amdgpu_buffer_rsrc_t rh = make_rsrc(dh, static_cast<uint32_t>(L * dv * ES));
+  auto load_vtile = [&](int vt, Stage& sg) {
+    const int v0 = vt * MB_DV;
+    const int off = ((tid >> 2) * dv + v0 + 8 * (tid & 3)) * ES;
+    sg.v = buf_load8<E>(rv, off);
+    sg.h = buf_load8<E>(rh, off);
+#pragma unroll
+    for (int u = 0; u < S::M_UNITS; ++u) {
+      const int l = tid + MB_NT * u;
+      const int row = l / KU, col = 8 * (l % KU);
+      const int el = col < dk ? (v0 + row) * dk + col : -1;
+      if (m32) {
+        sg.m[u][0] = __builtin_amdgcn_raw_buffer_load_b128(rm, el < 0 ? kBufOOB : el * 4, 0, 0);
+        sg.m[u][1] = __builtin_amdgcn_raw_buffer_load_b128(rm, el < 0 ? kBufOOB : el * 4 + 16, 0, 0);
+      } else {
+        sg.m[u][0] = __builtin_amdgcn_raw_buffer_load_b128(rm, el < 0 ? kBufOOB : el * ES, 0, 0);
+      }
+      sg.gg[u][0] = __builtin_amdgcn_raw_buffer_load_b128(rg, el < 0 ? kBufOOB : el * 4, 0, 0);
+      sg.gg[u][1] = __builtin_amdgcn_raw_buffer_load_b128(rg, el < 0 ? kBufOOB : el * 4 + 16, 0, 0);
+    }
+  };
+  auto split8 = [&](raw* hi, raw* lo, const u32x4* x) {
+    f32x4 x0, x1;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      x0[i] = __uint_as_float(x[0][i]);
+      x1[i] = __uint_as_float(x[1][i]);
+    }
+    store4_split<E>(hi, lo, x0);
+    store4_split<E>(hi + 4, lo + 4, x1);
+  };
+  auto store_vtile = [&](const Stage& sg) {
+    *reinterpret_cast<U8<E>*>(Vs + (tid >> 2) * VS + 8 * (tid & 3)) = sg.v;
+    *reinterpret_cast<U8<E>*>(Hs + (tid >> 2) * VS + 8 * (tid & 3)) = sg.h;
+#pragma unroll
+    for (int u = 0; u < S::M_UNITS; ++u) {
+      const int l = tid + MB_NT * u;
+      const int o = (l / KU) * KS + 8 * (l % KU);
+      if (m32) {
+        split8(Ms + o, Ml + o, sg.m[u]);
+      } else {
+        *reinterpret_cast<U8<E>*>(Ms + o) = __builtin_bit_cast(U8<E>, sg.m[u][0]);
+        *reinterpret_cast<uint4*>(Ml + o) = make_uint4(0u, 0u, 0u, 0u);
+      }
+      split8(Gs + o, Gl + o, sg.gg[u]);
+    }
+  };
+
+  Stage stage;
+  load_vtile(0, stage);
+  __syncthreads();  // K, Q, pw
 
   // Causal coefficients c decay^{i-j} of this wave's P / dS rows i = 16w + n
-  // against keys j = 16 jb + 4g + r; decay^{i+1} of its dQ rows; decay^{i+1} of
-  // the token slots i = 32p + 16 (s / 4) + 4g + s % 4 of the adjoint update.
+  // against keys j = 16 jb + 4g + r; decay^{i+1} of its dQ rows.
   float coef[4][4];
 #pragma unroll
   for (int jb = 0; jb < 4; ++jb)
@@ -479,200 +677,90 @@ __global__ __launch_bounds__(MB_NT, 1) void chunk_bwd_mfma_kernel(const BwdMArgs
       const int i = 16 * w + n, j = 16 * jb + 4 * g + r;
       coef[jb][r] = (j <= i) ? c * pw[max(i - j, 0)] : 0.f;
     }
-  const float sq = pw[16 * w + n + 1];
-  float gw[2][8];
-#pragma unroll
-  for (int p = 0; p < 2; ++p)
-#pragma unroll
-    for (int s = 0; s < 8; ++s) gw[p][s] = pw[32 * p + 16 * (s >> 2) + 4 * g + (s & 3) + 1];
+  const int jrow = 16 * w + n;  // this lane's key / query row
+  const float sq = pw[jrow + 1];
+  const float wl = (jrow < L) ? c * pw[max(L - 1 - jrow, 0)] : 0.f;
 
-  // ---- chunk staging: loads of chunk ch - 1 are in flight while chunk ch is
-  // processed.  K/Q unit u of thread t is row (t + 256 u) / KU, 16-byte column
-  // (t + 256 u) % KU; its V / dH unit is row t / 4, columns 8 (t % 4) of the
-  // tile; its state unit u is row (t + 256 u) / KU of the tile, 8 key columns.
-  struct Stage {
-    U8<E> k[S::K_UNITS];
-    U8<E> q[S::K_UNITS];
-    U8<E> v, h;
-    u32x4 m[S::M_UNITS][2];  // 8 fp32 values, or 8 16-bit values in m[u][0]
-  };
-  auto load_chunk = [&](int ch, Stage& sg) {
-    const int64_t t0 = static_cast<int64_t>(ch) * BCT;
-    const int L = ch == a.n_chunks - 1 ? last_len : BCT;
-    const __amdgpu_buffer_rsrc_t rk = make_rsrc(keys + t0 * dk, static_cast<uint32_t>(L * dk * ES));
-    const __amdgpu_buffer_rsrc_t rq = make_rsrc(queries + t0 * dk, static_cast<uint32_t>(L * dk * ES));
-    const __amdgpu_buffer_rsrc_t rv = make_rsrc(values + t0 * dv, static_cast<uint32_t>(L * dv * ES));
-    const __amdgpu_buffer_rsrc_t rh = make_rsrc(dh + t0 * dv, static_cast<uint32_t>(L * dv * ES));
+  // ---- P rows of query block w (blocks right of the diagonal are zeros)
+  {
+    Frag8<E> qf[NKK];
 #pragma unroll
-    for (int u = 0; u < S::K_UNITS; ++u) {
-      const int l = tid + MB_NT * u;
-      const int row = l / KU, col = 8 * (l % KU);
-      const int off = col < dk ? (row * dk + col) * ES : kBufOOB;
-      sg.k[u] = buf_load8<E>(rk, off);
-      sg.q[u] = buf_load8<E>(rq, off);
-    }
-    const int off = ((tid >> 2) * dv + v0 + 8 * (tid & 3)) * ES;
-    sg.v = buf_load8<E>(rv, off);
-    sg.h = buf_load8<E>(rh, off);
-    const bool from_m0 = ch == 0;
-    const unsigned char* msrc = from_m0 ? static_cast<const unsigned char*>(a.memory) + b * dv * dk * mem_b
-                                        : reinterpret_cast<const unsigned char*>(
-                                              a.states + (b * a.n_chunks + ch - 1) * dv * dk);
-    const bool src32 = !from_m0 || f32m;
-    const __amdgpu_buffer_rsrc_t rm = make_rsrc(msrc, static_cast<uint32_t>(dv * dk * (src32 ? 4 : ES)));
+    for (int kk = 0; kk < NKK; ++kk)
+      qf[kk] = *reinterpret_cast<const Frag8<E>*>(Qs + jrow * KS + 32 * kk + 8 * g);
 #pragma unroll
-    for (int u = 0; u < S::M_UNITS; ++u) {
-      const int l = tid + MB_NT * u;
-      const int row = l / KU, col = 8 * (l % KU);
-      const int el = col < dk ? (v0 + row) * dk + col : -1;
-      if (src32) {
-        sg.m[u][0] = __builtin_amdgcn_raw_buffer_load_b128(rm, el < 0 ? kBufOOB : el * 4, 0, 0);
-        sg.m[u][1] = __builtin_amdgcn_raw_buffer_load_b128(rm, el < 0 ? kBufOOB : el * 4 + 16, 0, 0);
-      } else {
-        sg.m[u][0] = __builtin_amdgcn_raw_buffer_load_b128(rm, el < 0 ? kBufOOB : el * ES, 0, 0);
-      }
-    }
-  };
-  auto store_chunk = [&](int ch, const Stage& sg) {
-    const bool src32 = ch != 0 || f32m;
+    for (int jb = 0; jb < 4; ++jb) {
+      f32x4 sacc = f32x4{0.f, 0.f, 0.f, 0.f};
+      if (jb <= w) {
 #pragma unroll
-    for (int u = 0; u < S::K_UNITS; ++u) {
-      const int l = tid + MB_NT * u;
-      const int row = l / KU, col = 8 * (l % KU);
-      *reinterpret_cast<U8<E>*>(Ks + row * KS + col) = sg.k[u];
-      *reinterpret_cast<U8<E>*>(Qs + row * KS + col) = sg.q[u];
-    }
-    *reinterpret_cast<U8<E>*>(Vs + (tid >> 2) * VS + 8 * (tid & 3)) = sg.v;
-    *reinterpret_cast<U8<E>*>(Hs + (tid >> 2) * VS + 8 * (tid & 3)) = sg.h;
-#pragma unroll
-    for (int u = 0; u < S::M_UNITS; ++u) {
-      const int l = tid + MB_NT * u;
-      const int row = l / KU, col = 8 * (l % KU);
-      if (src32) {
-        f32x4 x0, x1;
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          x0[i] = __uint_as_float(sg.m[u][0][i]);
-          x1[i] = __uint_as_float(sg.m[u][1][i]);
+        for (int kk = 0; kk < NKK; ++kk) {
+          const Frag8<E> kf = *reinterpret_cast<const Frag8<E>*>(Ks + (16 * jb + n) * KS + 32 * kk + 8 * g);
+          sacc = mfma8(kf, qf[kk], sacc);
         }
-        store4_split<E>(Ms + row * KS + col, Ml + row * KS + col, x0);
-        store4_split<E>(Ms + row * KS + col + 4, Ml + row * KS + col + 4, x1);
-      } else {
-        *reinterpret_cast<U8<E>*>(Ms + row * KS + col) = __builtin_bit_cast(U8<E>, sg.m[u][0]);
-        *reinterpret_cast<uint4*>(Ml + row * KS + col) = make_uint4(0u, 0u, 0u, 0u);
       }
+      const f32x4 cf = f32x4{coef[jb][0], coef[jb][1], coef[jb][2], coef[jb][3]};
+      store4_raw<E>(Ps + jrow * PS + 16 * jb + 4 * g, sacc * cf);
     }
-  };
+  }
+  Frag8<E> kr[NKK];
+#pragma unroll
+  for (int kk = 0; kk < NKK; ++kk) kr[kk] = *reinterpret_cast<const Frag8<E>*>(Ks + jrow * KS + 32 * kk + 8 * g);
 
-  Stage stage;
-  load_chunk(a.n_chunks - 1, stage);
-  for (int ch = a.n_chunks - 1; ch >= 0; --ch) {
-    const int64_t t0 = static_cast<int64_t>(ch) * BCT;
-    const int L = ch == a.n_chunks - 1 ? last_len : BCT;
-    store_chunk(ch, stage);
-    if (ch > 0) load_chunk(ch - 1, stage);
-    __syncthreads();  // chunk in LDS
-
-    // ---- P and dS rows of query block w (blocks right of the diagonal are zeros)
-    {
-      Frag8<E> qf[NKK];
+  f32x4 dsacc[4], dq[KT], dkk[KT];
 #pragma unroll
-      for (int kk = 0; kk < NKK; ++kk)
-        qf[kk] = *reinterpret_cast<const Frag8<E>*>(Qs + (16 * w + n) * KS + 32 * kk + 8 * g);
-      const Frag8<E> hf = *reinterpret_cast<const Frag8<E>*>(Hs + (16 * w + n) * VS + 8 * g);
+  for (int jb = 0; jb < 4; ++jb) dsacc[jb] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int jb = 0; jb < 4; ++jb) {
-        f32x4 sacc = f32x4{0.f, 0.f, 0.f, 0.f}, aacc = f32x4{0.f, 0.f, 0.f, 0.f};
-        if (jb <= w) {
-#pragma unroll
-          for (int kk = 0; kk < NKK; ++kk) {
-            const Frag8<E> kf = *reinterpret_cast<const Frag8<E>*>(Ks + (16 * jb + n) * KS + 32 * kk + 8 * g);
-            sacc = mfma8(kf, qf[kk], sacc);
-          }
-          const Frag8<E> vfj = *reinterpret_cast<const Frag8<E>*>(Vs + (16 * jb + n) * VS + 8 * g);
-          aacc = mfma8(vfj, hf, aacc);
-        }
-        const f32x4 cf = f32x4{coef[jb][0], coef[jb][1], coef[jb][2], coef[jb][3]};
-        store4_raw<E>(Ps + (16 * w + n) * PS + 16 * jb + 4 * g, sacc * cf);
-        store4_raw<E>(Ds + (16 * w + n) * PS + 16 * jb + 4 * g, aacc * cf);
-      }
-    }
-    __syncthreads();  // P and dS complete
-
-    const raw* Gb = Gs + gslot * MB_DV * KS;
-    const raw* Glb = Gl + gslot * MB_DV * KS;
-    const int jrow = 16 * w + n;  // this lane's key / query row
-    const float wl = (jrow < L) ? c * pw[max(L - 1 - jrow, 0)] : 0.f;
-    // ---- dQ rows of block w: D[kcol][i] = decay^{i+1} sum_v M[v][kcol] dH[i][v] + sum_j K[j][kcol] dS[i][j]
-    {
-      const __amdgpu_buffer_rsrc_t rpq = make_rsrc(a.part_q + ((b * a.tiles + tile) * T + t0) * dk,
-                                                   static_cast<uint32_t>(L * dk * 4));
-      const Frag8<E> hq = lds_frag_4x2<E>(Hs + jrow * VS + 4 * g, Hs + jrow * VS + 4 * g + 16);
-      Frag8<E> dsf[2];
-#pragma unroll
-      for (int p = 0; p < 2; ++p)
-        dsf[p] = lds_frag_4x2<E>(Ds + jrow * PS + 32 * p + 4 * g, Ds + jrow * PS + 32 * p + 4 * g + 16);
-#pragma unroll
-      for (int kt = 0; kt < KT; ++kt) {
-        const int mo = (4 * g + (n >> 2)) * KS + 16 * kt + 4 * (n & 3);
-        f32x4 acc = mfma8(bw_frag_tr<E>(Ms + mo, Ms + mo + 16 * KS), hq, f32x4{0.f, 0.f, 0.f, 0.f});
-        acc = mfma8(bw_frag_tr<E>(Ml + mo, Ml + mo + 16 * KS), hq, acc) * sq;
-#pragma unroll
-        for (int p = 0; p < 2; ++p) {
-          if (32 * p > 16 * w + 15) continue;
-          const raw* kb = Ks + (32 * p + 4 * g + (n >> 2)) * KS + 16 * kt + 4 * (n & 3);
-          acc = mfma8(bw_frag_tr<E>(kb, kb + 16 * KS), dsf[p], acc);
-        }
-        const int kc = 16 * kt + 4 * g;
-        const u32x4 q = u32x4{__float_as_uint(acc[0]), __float_as_uint(acc[1]), __float_as_uint(acc[2]),
-                              __float_as_uint(acc[3])};
-        __builtin_amdgcn_raw_buffer_store_b128(q, rpq, kc < dk ? (jrow * dk + kc) * 4 : kBufOOB, 0, 0);
-      }
-    }
-    // ---- dK rows of block w: D[kcol][j] = c decay^{L-1-j} sum_v G[v][kcol] V[j][v] + sum_i Q[i][kcol] dS[i][j]
-    //      dV rows of block w: D[v][j]    = c decay^{L-1-j} sum_k G[v][k] K[j][k] + sum_i dH[i][v] P[i][j]
-    {
-      // Columns j of dS and P: lane n holds rows i = 32p + 4g + e (+16), column 16w + n.
-      Frag8<E> dsT[2], pT[2];
+  for (int kt = 0; kt < KT; ++kt) dq[kt] = dkk[kt] = f32x4{0.f, 0.f, 0.f, 0.f};
+  Frag8<E> pT[2];
+  const __amdgpu_buffer_rsrc_t rdv = make_rsrc(static_cast<raw*>(a.dv_out) + (b * T + t0) * dv,
+                                               static_cast<uint32_t>(L * dv * ES));
+  const int n_vt = dv / MB_DV;
+  for (int vt = 0; vt < n_vt; ++vt) {
+    store_vtile(stage);
+    if (vt + 1 < n_vt) load_vtile(vt + 1, stage);
+    __syncthreads();  // value tile in LDS (and, the first time, P)
+    if (vt == 0) {
+      // Columns j = 16w + n of P: lane n holds rows i = 32p + 4g + e (+16).
 #pragma unroll
       for (int p = 0; p < 2; ++p) {
         const int off = (32 * p + 4 * g + (n >> 2)) * PS + 16 * w + 4 * (n & 3);
-        dsT[p] = bw_frag_tr<E>(Ds + off, Ds + off + 16 * PS);
         pT[p] = bw_frag_tr<E>(Ps + off, Ps + off + 16 * PS);
       }
-      const __amdgpu_buffer_rsrc_t rpk = make_rsrc(a.part_k + ((b * a.tiles + tile) * T + t0) * dk,
-                                                   static_cast<uint32_t>(L * dk * 4));
+    }
+    // dS rows of block w, this tile's share of the sum over value columns
+    {
+      const Frag8<E> hf = *reinterpret_cast<const Frag8<E>*>(Hs + jrow * VS + 8 * g);
+#pragma unroll
+      for (int jb = 0; jb < 4; ++jb) {
+        if (jb <= w) {
+          const Frag8<E> vfj = *reinterpret_cast<const Frag8<E>*>(Vs + (16 * jb + n) * VS + 8 * g);
+          dsacc[jb] = mfma8(vfj, hf, dsacc[jb]);
+        }
+      }
+    }
+    // dQ (sum_v dH[i][v] M[v][k]) and dK (sum_v G[v][k] V[j][v]) over this tile
+    {
+      const Frag8<E> hq = lds_frag_4x2<E>(Hs + jrow * VS + 4 * g, Hs + jrow * VS + 4 * g + 16);
       const Frag8<E> vj = lds_frag_4x2<E>(Vs + jrow * VS + 4 * g, Vs + jrow * VS + 4 * g + 16);
 #pragma unroll
       for (int kt = 0; kt < KT; ++kt) {
-        const int go = (4 * g + (n >> 2)) * KS + 16 * kt + 4 * (n & 3);
-        f32x4 acc = mfma8(bw_frag_tr<E>(Gb + go, Gb + go + 16 * KS), vj, f32x4{0.f, 0.f, 0.f, 0.f});
-        acc = mfma8(bw_frag_tr<E>(Glb + go, Glb + go + 16 * KS), vj, acc) * wl;
-#pragma unroll
-        for (int p = 0; p < 2; ++p) {
-          if (32 * p + 31 < 16 * w) continue;
-          const raw* qb = Qs + (32 * p + 4 * g + (n >> 2)) * KS + 16 * kt + 4 * (n & 3);
-          acc = mfma8(bw_frag_tr<E>(qb, qb + 16 * KS), dsT[p], acc);
-        }
-        const int kc = 16 * kt + 4 * g;
-        const u32x4 q = u32x4{__float_as_uint(acc[0]), __float_as_uint(acc[1]), __float_as_uint(acc[2]),
-                              __float_as_uint(acc[3])};
-        __builtin_amdgcn_raw_buffer_store_b128(q, rpk, kc < dk ? (jrow * dk + kc) * 4 : kBufOOB, 0, 0);
+        const int mo = (4 * g + (n >> 2)) * KS + 16 * kt + 4 * (n & 3);
+        dq[kt] = mfma8(bw_frag_tr<E>(Ms + mo, Ms + mo + 16 * KS), hq, dq[kt]);
+        dq[kt] = mfma8(bw_frag_tr<E>(Ml + mo, Ml + mo + 16 * KS), hq, dq[kt]);
+        dkk[kt] = mfma8(bw_frag_tr<E>(Gs + mo, Gs + mo + 16 * KS), vj, dkk[kt]);
+        dkk[kt] = mfma8(bw_frag_tr<E>(Gl + mo, Gl + mo + 16 * KS), vj, dkk[kt]);
       }
-      const __amdgpu_buffer_rsrc_t rdv = make_rsrc(static_cast<raw*>(a.dv_out) + (b * T + t0) * dv,
-                                                   static_cast<uint32_t>(L * dv * ES));
-      Frag8<E> kr[NKK];
-#pragma unroll
-      for (int kk = 0; kk < NKK; ++kk)
-        kr[kk] = *reinterpret_cast<const Frag8<E>*>(Ks + jrow * KS + 32 * kk + 8 * g);
+    }
+    // dV rows of block w for this tile: c decay^{L-1-j} sum_k G[v][k] K[j][k] + sum_i dH[i][v] P[i][j]
+    {
+      const int v0 = vt * MB_DV;
 #pragma unroll
       for (int vb = 0; vb < 2; ++vb) {
         f32x4 acc = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int kk = 0; kk < NKK; ++kk) {
           const int go = (16 * vb + n) * KS + 32 * kk + 8 * g;
-          acc = mfma8(*reinterpret_cast<const Frag8<E>*>(Gb + go), kr[kk], acc);
-          acc = mfma8(*reinterpret_cast<const Frag8<E>*>(Glb + go), kr[kk], acc);
+          acc = mfma8(*reinterpret_cast<const Frag8<E>*>(Gs + go), kr[kk], acc);
+          acc = mfma8(*reinterpret_cast<const Frag8<E>*>(Gl + go), kr[kk], acc);
         }
         acc *= wl;
 #pragma unroll
@@ -684,79 +772,91 @@ __global__ __launch_bounds__(MB_NT, 1) void chunk_bwd_mfma_kernel(const BwdMArgs
         buf_store4<E>(rdv, (jrow * dv + v0 + 16 * vb + 4 * g) * ES, acc);
       }
     }
-    // ---- the adjoint at the chunk's start: G = decay^L G + sum_i decay^{i+1} dH[i][v] Q[i][k]
-    {
-      Frag8<E> hw[2], hwl[2];
-#pragma unroll
-      for (int p = 0; p < 2; ++p) {
-        const raw* hb = Hs + (32 * p + 4 * g + (n >> 2)) * VS + 16 * gvb + 4 * (n & 3);
-        const Frag8<E> h = bw_frag_tr<E>(hb, hb + 16 * VS);
-#pragma unroll
-        for (int s = 0; s < 8; ++s) {
-          const float x = ET<E>::to_f(h.e[s]) * gw[p][s];
-          hw[p].e[s] = ET<E>::from_f(x);
-          hwl[p].e[s] = ET<E>::from_f(x - ET<E>::to_f(hw[p].e[s]));
-        }
-      }
-      const float decay_L = pw[L];
-#pragma unroll
-      for (int t = 0; t < GT; ++t) {
-        f32x4 acc = gacc[t] * decay_L;
-#pragma unroll
-        for (int p = 0; p < 2; ++p) {
-          const raw* qb = Qs + (32 * p + 4 * g + (n >> 2)) * KS + 16 * (gk0 + t) + 4 * (n & 3);
-          const Frag8<E> qT = bw_frag_tr<E>(qb, qb + 16 * KS);
-          acc = mfma8(qT, hw[p], acc);
-          acc = mfma8(qT, hwl[p], acc);
-        }
-        gacc[t] = acc;
-      }
-      gslot ^= 1;
-      publish_g(gslot);
-    }
-    __syncthreads();  // every read of this chunk's tiles done; the new hi/lo G visible
+    __syncthreads();  // every read of this tile done
   }
 
-  // grad_memory: the adjoint at the sequence's start.
-  const __amdgpu_buffer_rsrc_t ro = make_rsrc(static_cast<unsigned char*>(a.dm_out) + b * dv * dk * mem_b,
-                                              static_cast<uint32_t>(dv * dk * mem_b));
+  // ---- dS complete: c (dH V^T) o D, rounded to the MFMA type like P
 #pragma unroll
-  for (int t = 0; t < GT; ++t) {
-    const int off = g_off(t);
-    if (f32m) {
-      buf_store4<F32>(ro, off == kBufOOB ? kBufOOB : off * 4, gacc[t]);
-    } else {
-      buf_store4<E>(ro, off == kBufOOB ? kBufOOB : off * ES, gacc[t]);
+  for (int jb = 0; jb < 4; ++jb) {
+    const f32x4 cf = f32x4{coef[jb][0], coef[jb][1], coef[jb][2], coef[jb][3]};
+    store4_raw<E>(Ds + jrow * PS + 16 * jb + 4 * g, dsacc[jb] * cf);
+  }
+  __syncthreads();
+  // ---- dQ rows of block w: decay^{i+1} sum_v dH M + sum_j dS[i][j] K[j][k]
+  {
+    const __amdgpu_buffer_rsrc_t rqo = make_rsrc(static_cast<raw*>(a.dq_out) + (b * T + t0) * dk,
+                                                 static_cast<uint32_t>(L * dk * ES));
+    Frag8<E> dsf[2];
+#pragma unroll
+    for (int p = 0; p < 2; ++p)
+      dsf[p] = lds_frag_4x2<E>(Ds + jrow * PS + 32 * p + 4 * g, Ds + jrow * PS + 32 * p + 4 * g + 16);
+#pragma unroll
+    for (int kt = 0; kt < KT; ++kt) {
+      f32x4 acc = dq[kt] * sq;
+#pragma unroll
+      for (int p = 0; p < 2; ++p) {
+        if (32 * p > 16 * w + 15) continue;
+        const raw* kb = Ks + (32 * p + 4 * g + (n >> 2)) * KS + 16 * kt + 4 * (n & 3);
+        acc = mfma8(bw_frag_tr<E>(kb, kb + 16 * KS), dsf[p], acc);
+      }
+      const int kc = 16 * kt + 4 * g;
+      buf_store4<E>(rqo, kc < dk ? (jrow * dk + kc) * ES : kBufOOB, acc);
+    }
+  }
+  // ---- dK rows of block w: c decay^{L-1-j} sum_v G V + sum_i Q[i][k] dS[i][j]
+  {
+    const __amdgpu_buffer_rsrc_t rko = make_rsrc(static_cast<raw*>(a.dk_out) + (b * T + t0) * dk,
+                                                 static_cast<uint32_t>(L * dk * ES));
+    Frag8<E> dsT[2];
+#pragma unroll
+    for (int p = 0; p < 2; ++p) {
+      const int off = (32 * p + 4 * g + (n >> 2)) * PS + 16 * w + 4 * (n & 3);
+      dsT[p] = bw_frag_tr<E>(Ds + off, Ds + off + 16 * PS);
+    }
+#pragma unroll
+    for (int kt = 0; kt < KT; ++kt) {
+      f32x4 acc = dkk[kt] * wl;
+#pragma unroll
+      for (int p = 0; p < 2; ++p) {
+        if (32 * p + 31 < 16 * w) continue;
+        const raw* qb = Qs + (32 * p + 4 * g + (n >> 2)) * KS + 16 * kt + 4 * (n & 3);
+        acc = mfma8(bw_frag_tr<E>(qb, qb + 16 * KS), dsT[p], acc);
+      }
+      const int kc = 16 * kt + 4 * g;
+      buf_store4<E>(rko, kc < dk ? (jrow * dk + kc) * ES : kBufOOB, acc);
     }
   }
 }
 
-template <class E, int DKP>
-int launch_bwd_mfma(BwdMArgs a, void* grad_keys, void* grad_queries, hipStream_t s) {
-  using S = BmShape<DKP>;
-  static bool attr_set = false;
-  if (!attr_set) {
-    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&chunk_bwd_mfma_kernel<E, DKP>),
-                                       hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(S::lds_bytes));
-    if (e != hipSuccess) {
-      set_error("chunk_update_bwd: hipFuncSetAttribute failed: %s", hipGetErrorString(e));
-      return static_cast<int>(e);
-    }
-    attr_set = true;
+template <class K>
+int allow_lds(K* fn, size_t bytes, bool& done) {
+  if (done || bytes <= 64 * 1024) return GRM_HIP_OK;
+  hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(fn), hipFuncAttributeMaxDynamicSharedMemorySize,
+                                     static_cast<int>(bytes));
+  if (e != hipSuccess) {
+    set_error("chunk_update_bwd: hipFuncSetAttribute failed: %s", hipGetErrorString(e));
+    return static_cast<int>(e);
   }
-  const int64_t grid = a.batch * a.tiles;
-  a.xcd_remap = (grid % 8 == 0) ? 1 : 0;
-  hipLaunchKernelGGL((chunk_bwd_mfma_kernel<E, DKP>), dim3(static_cast<unsigned>(grid)), dim3(MB_NT), S::lds_bytes,
-                     s, a);
-  int rc = check_launch("chunk_update_bwd");
+  done = true;
+  return GRM_HIP_OK;
+}
+
+template <class E, int DKP>
+int launch_bwd_mfma(BwdMArgs a, hipStream_t s) {
+  static bool attr_a = false, attr_g = false;
+  int rc = allow_lds(&bwd_adjoint_kernel<E, DKP>, AjShape<DKP>::lds_bytes, attr_a);
+  if (rc == GRM_HIP_OK) rc = allow_lds(&bwd_grad_kernel<E, DKP>, GrShape<DKP>::lds_bytes, attr_g);
   if (rc != GRM_HIP_OK) return rc;
-  // Both gradients in one launch: 4 columns per thread (key_dim % 8 == 0 here).
-  const int64_t quads = a.batch * a.T * a.dk / 4;
-  const int64_t want = (2 * quads + 255) / 256;
-  const unsigned g = static_cast<unsigned>(want < 256 * 128 ? want : 256 * 128);
-  hipLaunchKernelGGL(tile_sum4_kernel<E>, dim3(g < 1 ? 1 : g), dim3(256), 0, s, a.part_k, a.part_q, grad_keys,
-                     grad_queries, a.tiles, a.T * a.dk / 4, quads);
-  return check_launch("chunk_update_bwd(grad_keys, grad_queries)");
+  const int64_t grid_a = a.batch * ((a.dv + AJ_V - 1) / AJ_V);
+  a.xcd_remap = (grid_a % 8 == 0) ? 1 : 0;
+  hipLaunchKernelGGL((bwd_adjoint_kernel<E, DKP>), dim3(static_cast<unsigned>(grid_a)), dim3(MB_NT),
+                     AjShape<DKP>::lds_bytes, s, a);
+  rc = check_launch("chunk_update_bwd(adjoint)");
+  if (rc != GRM_HIP_OK) return rc;
+  const int64_t grid_g = a.batch * a.n_chunks;
+  hipLaunchKernelGGL((bwd_grad_kernel<E, DKP>), dim3(static_cast<unsigned>(grid_g)), dim3(MB_NT),
+                     GrShape<DKP>::lds_bytes, s, a);
+  return check_launch("chunk_update_bwd(gradients)");
 }
 
 }  // namespace
@@ -831,8 +931,14 @@ extern "C" int grm_hip_chunk_update_bwd(const void* grad_hidden, const void* gra
   }
 
   const char* env = getenv("GRM_HIP_BWD_MFMA");
+  // The MFMA kernels keep the adjoint at every chunk end, [batch, n_chunks,
+  // value_dim, key_dim] float32, in dkq_partial: used where that fits the
+  // buffer's documented size (from about ten tokens on; shorter sequences take
+  // the scalar kernel).
+  const bool gbuf_fits = n_chunks * value_dim <= 2 * ((value_dim + RB - 1) / RB) * seq_len;
   const bool mfma = (env == nullptr || env[0] != '0') && (in_dtype == GRM_HIP_BF16 || in_dtype == GRM_HIP_F16) &&
-                    key_dim <= 128 && key_dim % 8 == 0 && value_dim % MB_DV == 0 &&
+                    key_dim <= 128 && key_dim % 8 == 0 && value_dim % MB_DV == 0 && gbuf_fits &&
+                    batch * n_chunks <= INT32_MAX &&
                     aligned16(grad_hidden) && aligned16(keys) && aligned16(values) && aligned16(queries) &&
                     aligned16(grad_values) && aligned16(dkq_partial) && aligned16(memory) &&
                     aligned16(grad_memory_out) && aligned16(grad_memory) && aligned16(chunk_states);
@@ -846,11 +952,11 @@ extern "C" int grm_hip_chunk_update_bwd(const void* grad_hidden, const void* gra
     m.queries = queries;
     m.memory = memory;
     m.states = chunk_states;
+    m.gbuf = dkq_partial;
+    m.dq_out = grad_queries;
+    m.dk_out = grad_keys;
     m.dv_out = grad_values;
     m.dm_out = grad_memory;
-    m.tiles = static_cast<int>(value_dim / MB_DV);
-    m.part_k = dkq_partial;
-    m.part_q = dkq_partial + batch * m.tiles * seq_len * key_dim;
     m.batch = batch;
     m.T = seq_len;
     m.dk = static_cast<int>(key_dim);
@@ -860,11 +966,9 @@ extern "C" int grm_hip_chunk_update_bwd(const void* grad_hidden, const void* gra
     m.c = static_cast<float>((1.0 - memory_decay) / std::sqrt(static_cast<double>(key_dim)));
     for (int i = 0; i <= BCT; ++i) m.pw[i] = static_cast<float>(std::pow(memory_decay, i));
     if (in_dtype == GRM_HIP_F16) {
-      return key_dim <= 64 ? launch_bwd_mfma<F16, 64>(m, grad_keys, grad_queries, s)
-                           : launch_bwd_mfma<F16, 128>(m, grad_keys, grad_queries, s);
+      return key_dim <= 64 ? launch_bwd_mfma<F16, 64>(m, s) : launch_bwd_mfma<F16, 128>(m, s);
     }
-    return key_dim <= 64 ? launch_bwd_mfma<BF16, 64>(m, grad_keys, grad_queries, s)
-                         : launch_bwd_mfma<BF16, 128>(m, grad_keys, grad_queries, s);
+    return key_dim <= 64 ? launch_bwd_mfma<BF16, 64>(m, s) : launch_bwd_mfma<BF16, 128>(m, s);
   }
 
   BwdArgs a;

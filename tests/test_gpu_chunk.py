@@ -335,12 +335,15 @@ def close_elementwise(name, got, ref, rtol=2e-2, atol=2e-3):
 @pytest.mark.parametrize("dtype,mem_dtype", [(torch.bfloat16, torch.float32), (torch.float16, torch.float32),
                                              (torch.bfloat16, torch.bfloat16), (torch.float16, torch.float16)])
 @pytest.mark.parametrize("B,T,K,H", [(2, 300, 128, 128), (3, 129, 64, 64), (1, 640, 96, 96), (2, 64, 128, 32),
-                                     (1, 7, 128, 32), (2, 200, 32, 64)])
+                                     (1, 7, 128, 32), (1, 12, 128, 32), (2, 200, 32, 64), (1, 200, 64, 512)])
 def test_mfma_backward(dev, monkeypatch, dtype, mem_dtype, B, T, K, H):
-    """The chunk-parallel MFMA backward (16-bit inputs, value_dim a multiple of 32) against the
-    double-precision oracle and against the scalar per-token kernel (GRM_HIP_BWD_MFMA=0),
-    element by element at rtol 2e-2 / atol 2e-3: ragged last chunks, key widths below the
-    padded 64/128, one to four value tiles, one chunk."""
+    """The chunk-parallel MFMA backward (16-bit inputs, value_dim a multiple of 32: the adjoint
+    pass, then the per-chunk gradients over every value tile) against the double-precision
+    oracle and against the scalar per-token kernel (GRM_HIP_BWD_MFMA=0), element by element at
+    rtol 2e-2 / atol 2e-3: ragged last chunks, key widths below the padded 64/128, one to
+    sixteen value tiles, a half-filled 64-row adjoint tile (96 values), one chunk (12 tokens),
+    and 7 tokens, where the adjoint buffer would not fit the workspace and the scalar kernel
+    runs."""
     k, v, q, m = make_case(B, T, K, H, dtype, mem_dtype, seed=B * 13 + T)
     g = torch.Generator().manual_seed(7)
     dh = torch.randn(B, T, H, generator=g).to(dtype)
