@@ -656,19 +656,14 @@ __global__ __launch_bounds__(AP_THREADS) void apply_mfma16_kernel(const Retrieve
     }
   };
   load_q(pid_l);
-  // Pair ids run two steps ahead of the products and gates one step, so that
-  // neither the next step's query loads nor the output stage waits on them.
-  int pid_n = lane < p_end - p_begin - AP_N ? lb[p_begin + AP_N + lane] : -1;
-  float gate_l = 0.f;
-  if constexpr (SCALED) gate_l = pid_l >= 0 ? a.gates[b * a.n_index + pid_l] : 0.f;
   for (int p0 = p_begin; p0 < p_end; p0 += AP_N) {
     const int np = min(AP_N, p_end - p0);
     const int pid_cur = pid_l;
-    const float gate_cur = gate_l;
     const bool more = p0 + AP_N < p_end;
-    const int pid_next = pid_n;
-    pid_n = lane < p_end - p0 - 2 * AP_N ? lb[p0 + 2 * AP_N + lane] : -1;
-    if constexpr (SCALED) gate_l = pid_next >= 0 ? a.gates[b * a.n_index + pid_next] : 0.f;
+    const int pid_next = (more && lane < p_end - p0 - AP_N) ? lb[p0 + AP_N + lane] : -1;
+    // The gate of this lane's pair, loaded while the tile's products run.
+    float gate_cur = 0.f;
+    if constexpr (SCALED) gate_cur = pid_cur >= 0 ? a.gates[b * a.n_index + pid_cur] : 0.f;
     if (!split) {
       split = true;
 #pragma unroll
@@ -1032,10 +1027,7 @@ int launch_apply_scaled(const RetrieveArgs& a, hipStream_t s) {
   using Plan = MfmaPlan<EL, F32, EQ>;
   if constexpr (Plan::ok) {
     using EF = typename Plan::EF;
-    // float32 states: hi + lo bf16 parts (16 of the 24 mantissa bits, relative
-    // error <= 2^-17 per product) instead of the exact three, since the rows are
-    // kept as float16 (relative rounding 2^-11) anyway.
-    constexpr int NPART = std::is_same<EL, F32>::value && Plan::parts == 3 ? 2 : Plan::parts;
+    constexpr int NPART = Plan::parts;
     if (a.dk <= 32) return launch_apply_mfma16<EL, F32, EQ, 32, EF, NPART, true>(a, s);
     if (a.dk <= 64) return launch_apply_mfma16<EL, F32, EQ, 64, EF, NPART, true>(a, s);
     return launch_apply_mfma16<EL, F32, EQ, 128, EF, NPART, true>(a, s);
