@@ -62,11 +62,11 @@ struct VsShape {
   using raw = typename ET<E>::raw;
   static constexpr int DVT = kVsplitDv;  // value columns per workgroup
   // Row strides (elements): K, Q, V and the output tile unpadded and
-  // swizzled (kq_at, v_at, o_at); the 16-bit state 4 banks mod 64, so the
-  // 16-byte reads of 16 rows are conflict-free; P 34 banks, the 8-byte reads
-  // of 16 rows on 32 distinct banks.
+  // swizzled (kq_at, v_at, o_at); the 16-bit state unpadded with 8-byte
+  // pieces swizzled (m_at) at key_dim 128, 4 banks mod 64 otherwise; P 34
+  // banks, the 8-byte reads of 16 rows on 32 distinct banks.
   static constexpr int KS = DKP;
-  static constexpr int MS = DKP + 8;
+  static constexpr int MS = DKP == 128 ? DKP : DKP + 8;
   static constexpr int VS = DVT;
   static constexpr int PS = CT + 4;
   static constexpr int OS = DVT;
@@ -87,21 +87,38 @@ struct VsShape {
 
 // Element offsets in the swizzled tiles; col is a multiple of 4 (an 8- or
 // 16-byte piece inside one 16-byte granule).  K/Q rows of DKP elements:
-// granule (col / 8) ^ s(row), s(row) = 2 (row & 7) | bit 3 of row for 16
-// granules per row, 2 ((row >> 1) & 3) | bit 3 of row for 8; rows 16 apart
-// share s, so the two halves of a transposed fragment are 16 rows apart.
-// V rows (32 elements): granule ^ 2 * bit 2 of row.  Output rows (32
-// elements): granule ^ ((row >> 2) & 3).
+// granule (col / 8) ^ s(row), s(row) = row & 15 for 16 granules per row (the
+// 16-byte reads of 16 rows x 4 granules conflict-free; the transposed 8-byte
+// reads of the state update pay 2-way, 32 of them against 72 16-byte reads a
+// step), 2 ((row >> 1) & 3) | bit 3 of row for 8; rows 16 apart share s, so
+// the two halves of a transposed fragment are 16 rows apart.
+// V rows (32 elements): granule ^ 2 * bit 2 of row.
+// LDS on gfx950, as measured with SQ_LDS_BANK_CONFLICT: 8-byte writes go in
+// four passes of 16 consecutive lanes over 32 banks of 4 bytes, 8-byte reads
+// in two passes of 32 consecutive lanes over 64 banks; a pass costs one cycle
+// per distinct dword in its busiest bank.  The 16-bit state copy (key_dim 128:
+// 32 pieces of 8 bytes per row) and the output tile (8 pieces per 64-byte
+// row) are written as 8-byte columns of 16 rows and read as 8-byte pieces, so
+// their pieces are swizzled by row for both: m_at spreads 16 rows of one
+// column over 16 bank pairs and keeps a read pass's two lane groups (pieces
+// 2 apart) apart by bit 4; o_at spreads the 8 rows of one parity over 8
+// pieces and flips bit 0 between rows r and r + 4, which a read pass pairs.
+__device__ __forceinline__ int m_at(int row, int col) {
+  const int f = (row & 15) ^ ((row & 2) << 3);
+  return row * 128 + ((((col >> 2) ^ f)) << 2) + (col & 3);
+}
+__device__ __forceinline__ int o_at(int row, int col) {
+  const int f = ((row >> 1) & 7) ^ ((row >> 2) & 1);
+  return row * kVsplitDv + ((((col >> 2) ^ f)) << 2) + (col & 3);
+}
+
 template <int DKP>
 __device__ __forceinline__ int kq_at(int row, int col) {
-  const int s = DKP == 128 ? (((row & 7) << 1) | ((row >> 3) & 1)) : ((((row >> 1) & 3) << 1) | ((row >> 3) & 1));
+  const int s = DKP == 128 ? (row & 15) : ((((row >> 1) & 3) << 1) | ((row >> 3) & 1));
   return row * DKP + ((((col >> 3) ^ s)) << 3) + (col & 7);
 }
 __device__ __forceinline__ int v_at(int row, int col) {
   return row * kVsplitDv + (((col >> 3) ^ (((row >> 2) & 1) << 1)) << 3) + (col & 7);
-}
-__device__ __forceinline__ int o_at(int row, int col) {
-  return row * kVsplitDv + (((col >> 3) ^ ((row >> 2) & 3)) << 3) + (col & 7);
 }
 
 // Stores of results nothing in this kernel reads again (hidden rows,
@@ -240,8 +257,10 @@ __global__ __launch_bounds__(kVsThreads, 1) void scan_vsplit_kernel(const ChunkF
     const __amdgpu_buffer_rsrc_t rh = make_rsrc(hidden + (hidden != nullptr ? t0 * dv : 0),
                                                 static_cast<uint32_t>(hidden != nullptr ? L * dv * ES : 0));
     const int row = tid / VU, col = 8 * (tid % VU);
-    const u32x4 val = *reinterpret_cast<const u32x4*>(Obuf + (c & 1) * CT * OS + o_at(row, col));
-    store_stream(rh, (row * dv + v0 + col) * ES, val);
+    const raw* Ob = Obuf + (c & 1) * CT * OS;
+    const u32x2 lo = *reinterpret_cast<const u32x2*>(Ob + o_at(row, col));
+    const u32x2 hi = *reinterpret_cast<const u32x2*>(Ob + o_at(row, col + 4));
+    store_stream(rh, (row * dv + v0 + col) * ES, u32x4{lo[0], lo[1], hi[0], hi[1]});
   };
   // P wave p: S rows i = 16 p + n against key blocks jb <= p (lane holds
   // S[i][16 jb + 4g + r]); the blocks right of the diagonal are written as
@@ -299,7 +318,10 @@ __global__ __launch_bounds__(kVsThreads, 1) void scan_vsplit_kernel(const ChunkF
 #pragma unroll
     for (int vb = 0; vb < 2; ++vb)
 #pragma unroll
-      for (int kt = 0; kt < KT; ++kt) store4_raw<E>(Mb + (16 * vb + n) * MS + KH * uk + 16 * kt + 4 * g, st[vb][kt]);
+      for (int kt = 0; kt < KT; ++kt) {
+        const int row = 16 * vb + n, col = KH * uk + 16 * kt + 4 * g;
+        store4_raw<E>(Mb + (DKP == 128 ? m_at(row, col) : row * MS + col), st[vb][kt]);
+      }
   };
   // O waves: decay^{i+1} for the query rows i = 32 oq + 16 ib + n of this lane's output tiles.
   float s_start[2];
@@ -341,8 +363,14 @@ __global__ __launch_bounds__(kVsThreads, 1) void scan_vsplit_kernel(const ChunkF
 #pragma unroll
     for (int kk = 0; kk < NKK; ++kk) {
 #pragma unroll
-      for (int vb = 0; vb < 2; ++vb)
-        mf[vb][kk] = *reinterpret_cast<const Frag8<E>*>(Mb + (16 * vb + n) * MS + 32 * kk + 8 * g);
+      for (int vb = 0; vb < 2; ++vb) {
+        const int row = 16 * vb + n, col = 32 * kk + 8 * g;
+        if constexpr (DKP == 128) {
+          mf[vb][kk] = lds_frag_4x2<E>(Mb + m_at(row, col), Mb + m_at(row, col + 4));
+        } else {
+          mf[vb][kk] = *reinterpret_cast<const Frag8<E>*>(Mb + row * MS + col);
+        }
+      }
 #pragma unroll
       for (int ib = 0; ib < 2; ++ib)
         qf[ib][kk] = *reinterpret_cast<const Frag8<E>*>(Qb + kq_at<DKP>(32 * oq + 16 * ib + n, 32 * kk + 8 * g));
