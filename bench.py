@@ -746,6 +746,15 @@ def bench_c4_train(torch, dev, steps, warmup):
             "peak_gib": torch.cuda.max_memory_allocated(dev) / 2 ** 30}
 
 
+def settle(torch) -> None:
+    """Between legs: drain the GPU, hand cached blocks back and idle for two seconds, so
+    that each leg starts from the same clock and allocator state (the legs before config
+    4 write 64 GiB and more, after which the box's clocks step down for a while)."""
+    torch.cuda.synchronize()
+    torch.cuda.empty_cache()
+    time.sleep(2.0)
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -836,6 +845,7 @@ def main() -> int:
             "ms": round(bw["ms"], 4), "tokens/s": round(bw["tokens"] / bw["ms"] * 1e3)}
         log(f"c2 backward: {bw['ms']:.3f} ms per call")
     if not a.no_gather:
+        settle(torch)
         log("config 3 routing + materialised gather (64 GiB output)")
         c3 = bench_c3(torch, dev, a.steps, a.warmup)
         r, gth = c3["route"], c3["gather"]
@@ -867,6 +877,7 @@ def main() -> int:
             f"{ga['ms']:.3f}, fuse {c3['fuse']['ms']:.3f})")
 
     if not a.no_gather:
+        settle(torch)
         log("config 5: whole-sequence update (16 x 65536 tokens, 512 snapshots) + k=16 retrieval per token")
         c5 = bench_c5(torch, dev, a.steps, a.warmup)
         u, rt5, ga5 = c5["update"], c5["retrieval"], c5["gather_apply"]
@@ -914,6 +925,7 @@ def main() -> int:
             f"{c4['device_archive_ms']:.3f} ms")
 
     if not a.no_gather or a.c4_only:
+        settle(torch)
         log("config 4 end-to-end forward (4 layers, 4 x 8192 tokens)")
         m4 = bench_c4_model(torch, dev, a.steps, a.warmup)
         secondary["c4_model_forward"] = {
@@ -928,6 +940,7 @@ def main() -> int:
             log(f"  c4 phase {k}: {v:.3f} ms")
 
     if not a.no_gather or a.train_only:
+        settle(torch)
         log("config 4 training forward + backward")
         t4 = bench_c4_train(torch, dev, a.steps, a.warmup)
         secondary["c4_model_train_step"] = {

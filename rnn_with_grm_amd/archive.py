@@ -34,7 +34,7 @@ from __future__ import annotations
 
 from collections import deque
 from dataclasses import dataclass
-from typing import Deque, Dict, Optional
+from typing import Deque, Dict, List, Optional
 
 import torch
 import torch.nn as nn
@@ -116,6 +116,12 @@ class DeviceSegmentArchive(nn.Module):
         self.register_buffer("total_pushed", torch.tensor(0, dtype=torch.long))
         self.register_buffer("total_recomputed", torch.tensor(0, dtype=torch.long))
         self.register_buffer("total_retrieved", torch.tensor(0, dtype=torch.long))
+        # Host mirror of (total_retrieved, total_recomputed) for get_recompute_rate, so
+        # that a forward's report reads no device value (a forward then has no host
+        # synchronisation and can be captured in a graph).  None: read the buffers
+        # once (after a state-dict load or a change made outside this class).
+        self._host_counts: Optional[List[int]] = [0, 0]
+        self.register_load_state_dict_post_hook(lambda module, keys: setattr(module, "_host_counts", None))
 
     # ------------------------------------------------------------- bookkeeping
     def _group(self, batch_size: int) -> _Ring:
@@ -128,6 +134,12 @@ class DeviceSegmentArchive(nn.Module):
         self.total_pushed.zero_()
         self.total_recomputed.zero_()
         self.total_retrieved.zero_()
+        self._host_counts = [0, 0]
+
+    def _count_retrieved(self, n: int) -> None:
+        self.total_retrieved.add_(n)
+        if self._host_counts is not None:
+            self._host_counts[0] += n
 
     def _apply(self, fn):
         super()._apply(fn)
@@ -241,7 +253,7 @@ class DeviceSegmentArchive(nn.Module):
         slots = self.slots(topk_indices, batch_size)
         selected = cuda_ops.cuda_batched_memory_gather(ring.memories, slots, enabled=True,
                                                        debug_fallback=cuda_cpp_debug_fallback)
-        self.total_retrieved.add_(int(topk_indices.numel()))
+        self._count_retrieved(int(topk_indices.numel()))
         return selected.to(device=device, dtype=torch.float32)
 
     def retrieve_from_indices(self, query_inputs: Tensor, topk_indices: Tensor, gates: Tensor, memory_cell,
@@ -255,14 +267,16 @@ class DeviceSegmentArchive(nn.Module):
             return self._empty_retrieval(topk_indices, device, (self.hidden_size,))
         q_t = F.normalize(memory_cell.query_proj(query_inputs), p=2, dim=-1, eps=1e-6).to(torch.float32)
         slots = self.slots(topk_indices, batch_size)
-        self.total_retrieved.add_(int(topk_indices.numel()))
+        self._count_retrieved(int(topk_indices.numel()))
         return cuda_ops.cuda_gather_apply(ring.memories, slots, q_t, torch.float32,
                                           debug_fallback=cuda_cpp_debug_fallback).to(device)
 
     # ------------------------------------------------------------- reporting
     def get_recompute_rate(self) -> float:
-        total = int(self.total_retrieved.item())
-        return 0.0 if total == 0 else float(self.total_recomputed.item()) / total
+        if self._host_counts is None:
+            self._host_counts = [int(self.total_retrieved.item()), int(self.total_recomputed.item())]
+        total, recomputed = self._host_counts
+        return 0.0 if total == 0 else float(recomputed) / total
 
     def get_memory_info(self) -> Dict[str, float]:
         """Same keys as paper_grm.py:322-349; bytes count the kept entries."""

@@ -705,7 +705,7 @@ class SegmentRecurrentMemoryModel(nn.Module):
         # Routes handed out, as the reference counts them per segment (paper_grm.py:230).
         routes = sum(B * (min(T, (s + 1) * seg) - s * seg) * min(self.retrieval_top_k, min(base + s, cap))
                      for s in range(n_seg))
-        bank.total_retrieved.add_(routes)
+        bank._count_retrieved(routes)
 
         last_hidden = h_enhanced[:, -1]
         if return_all_outputs:
