@@ -195,3 +195,26 @@ def test_invalid_positions_read_zero_on_device():
     got = arch.retrieve_memories(torch.tensor([[0, -1], [2, 3]], device=dev), None, None, dev, 0.97).cpu()
     assert torch.count_nonzero(got[0, 1]) == 0 and torch.count_nonzero(got[1, 1]) == 0
     assert torch.equal(got[0, 0], mems[0, 2]) and torch.equal(got[1, 0], mems[1, 4])
+
+
+def test_recompute_rate_counters_mirrored_on_host():
+    """get_recompute_rate reads a host mirror of the counters (no device read in a forward);
+    it agrees with the buffers after retrievals, re-reads them after a state-dict load or
+    direct writes detected by the load hook, and resets with clear()."""
+    B, H, K, D, cap = 2, 8, 4, 6, 3
+    arch = DeviceSegmentArchive(H, K, D, cap, torch.float16)
+    for i in range(3):
+        arch.push(torch.full((B, H, K), float(i)), torch.zeros(B, D), SegmentCheckpoint(torch.zeros(1), torch.zeros(1)))
+    idx = torch.tensor([[0, 2], [1, 1]])
+    arch.retrieve_memories(idx, None, None, torch.device("cpu"), 0.97)
+    arch.retrieve_memories(idx, None, None, torch.device("cpu"), 0.97)
+    assert int(arch.total_retrieved) == 8 and arch._host_counts == [8, 0]
+    assert arch.get_recompute_rate() == 0.0
+    other = DeviceSegmentArchive(H, K, D, cap, torch.float16)
+    sd = arch.state_dict()
+    sd["total_recomputed"] = torch.tensor(2)
+    other.load_state_dict(sd)
+    assert other._host_counts is None
+    assert other.get_recompute_rate() == 0.25 and other._host_counts == [8, 2]
+    other.clear()
+    assert other._host_counts == [0, 0] and other.get_recompute_rate() == 0.0 and int(other.total_retrieved) == 0

@@ -431,3 +431,39 @@ def test_training_gradients_bf16_mfma_backward(dev, monkeypatch):
     assert worst_kernel < 1e-2, worst_kernel
     assert worst_cell < 4e-2, worst_cell
     assert worst_f32 < 1.5e-1, worst_f32
+
+
+@pytest.mark.gpu
+def test_model_forward_graph_capture(dev):
+    """A whole-sequence forward reads no device value on the host (the archive's counters are
+    mirrored there), so a bf16 model forward captures in a HIP graph.  Replays, with eager
+    forwards and synchronisations between them, reproduce the eager output bit for bit; the
+    archive's report after a replay matches eager's."""
+    torch.manual_seed(21)
+    model = sm.HierarchicalSegmentMemoryModel(
+        input_size=64, hidden_size=64, output_size=64, num_layers=2, segment_length=32, memory_capacity_segments=6,
+        retrieval_top_k=4, memory_key_dim=32, dropout=0.0, recomputation_ratio=0.0)
+    model = model.to(device=dev, dtype=torch.bfloat16).eval()
+    x = torch.randn(2, 352, 64, generator=torch.Generator().manual_seed(22)).to(dev, torch.bfloat16)
+    with torch.no_grad():
+        ref, _, _, aux_ref = model(x, reset_memory=True)
+        ref = ref.clone()
+        side = torch.cuda.Stream()
+        side.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(side):
+            for _ in range(2):
+                model(x, reset_memory=True)
+        torch.cuda.current_stream().wait_stream(side)
+        torch.cuda.synchronize()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            out, _, _, aux = model(x, reset_memory=True)
+        for _ in range(3):
+            graph.replay()
+            torch.cuda.synchronize()
+            assert torch.equal(out, ref)
+            eager, _, _, _ = model(x, reset_memory=True)
+            torch.cuda.synchronize()
+            assert torch.equal(eager, ref)
+    assert aux["memory_info"]["recompute_rate"] == aux_ref["memory_info"]["recompute_rate"] == 0.0
+    assert aux["num_segments"] == aux_ref["num_segments"]
