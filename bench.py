@@ -152,7 +152,24 @@ def bench_n1(torch, dev, steps, warmup):
         raise RuntimeError("north-star shape: last snapshot differs from the final state")
     flops, bytes_ = c2_counts(BH=BH, T=T, dk=D, dv=D)
     del k, v, q, m, hidden, snaps, ws
-    return {"us": ev0.elapsed_time(ev1) * 1e3 / steps, "tokens": BH * T, "flops": flops, "bytes": bytes_}
+    # The box's rate for a stream as large and as write-heavy: a device copy moving the same
+    # number of bytes (half read, half written; the scan reads 37% and writes 63%).
+    n = bytes_ // 8
+    src = torch.empty(n, dtype=torch.float32, device=dev).fill_(1.0)
+    dst = torch.empty_like(src)
+    for _ in range(2):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    ev0c, ev1c = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    ev0c.record(stream)
+    for _ in range(steps):
+        dst.copy_(src)
+    ev1c.record(stream)
+    torch.cuda.synchronize()
+    copy_us = ev0c.elapsed_time(ev1c) * 1e3 / steps
+    del src, dst
+    return {"us": ev0.elapsed_time(ev1) * 1e3 / steps, "tokens": BH * T, "flops": flops, "bytes": bytes_,
+            "copy_us": copy_us, "copy_bytes": 8 * n}
 
 
 def bench_c2_bwd(torch, dev, steps, warmup):
@@ -828,8 +845,13 @@ def main() -> int:
             "roofline": {"bound": "hbm", "achieved": round(n1_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                          "frac": round(n1_gbs / HBM_PEAK_GBS, 4), "algorithmic_bytes_per_launch": n1["bytes"]},
             "mfma": {"TFLOP/s": round(n1_tf, 2), "peak": BF16_PEAK_TFLOPS, "frac": round(n1_tf / BF16_PEAK_TFLOPS, 5),
-                     "flops_per_launch": n1["flops"]}}
-        log(f"n1: {n1['us']:.1f} us/launch, {n1_gbs:.0f} GB/s, {n1_tf:.1f} TFLOP/s")
+                     "flops_per_launch": n1["flops"]},
+            "copy_ceiling": {"what": "a device copy of the same byte count (read + write) on the same box",
+                             "us": round(n1["copy_us"], 1),
+                             "GB/s": round(n1["copy_bytes"] / n1["copy_us"] / 1e3, 1),
+                             "scan_time_vs_copy": round(n1["copy_us"] / n1["us"], 4)}}
+        log(f"n1: {n1['us']:.1f} us/launch, {n1_gbs:.0f} GB/s, {n1_tf:.1f} TFLOP/s; a copy of the same bytes "
+            f"{n1['copy_us']:.1f} us ({n1['copy_bytes'] / n1['copy_us'] / 1e3:.0f} GB/s)")
     if a.route_only:
         log("routing only: config 3 and config 5")
         for label, r in bench_routes(torch, dev, a.steps, a.warmup).items():
