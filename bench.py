@@ -732,8 +732,9 @@ def cpu_baseline(torch):
 def bench_c4_train(torch, dev, steps, warmup):
     """Config 4 training forward + backward (no optimizer step): the same LM and token ids,
     cross-entropy over next-token targets, loss.backward() through the scan's MFMA backward,
-    the routing, the retrieval's queries gradient (transposed apply, no gathered states) and
-    the torch fusion.  Returns the mean step and the generic-path calls the steps made."""
+    the routing, and the retrieval with its LayerNorm residual as one autograd function (the
+    transposed apply per query and route, no gathered states, no per-route rows kept).
+    Returns the mean step and the generic-path calls the steps made."""
     from rnn_with_grm_amd import cuda_ops
 
     B, T, V = 4, 8192, 32000
@@ -967,8 +968,8 @@ def main() -> int:
         t4 = bench_c4_train(torch, dev, a.steps, a.warmup)
         secondary["c4_model_train_step"] = {
             "what": "config 4 LM forward + cross-entropy + backward (no optimizer step), same model and ids; "
-                    "native scan backward, routing, and the retrieval's queries gradient without the gathered "
-                    "states",
+                    "native scan backward, routing, and retrieval + LayerNorm residual as one autograd function "
+                    "whose backward never forms the gathered states or the per-route rows",
             "ms": round(t4["ms"], 3), "tokens/s": round(t4["tokens"] / t4["ms"] * 1e3),
             "generic_path_calls": t4["generic_path_calls"], "peak_memory_gib": round(t4["peak_gib"], 1)}
         log(f"c4 train step: {t4['ms']:.2f} ms, {t4['tokens'] / t4['ms'] * 1e3:.3e} tokens/s, generic path calls "

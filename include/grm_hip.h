@@ -216,6 +216,22 @@ int grm_hip_gather_apply_bwd_queries(const void* memories, const int64_t* indice
                                      int64_t key_dim, int mem_dtype, int32_t* bad_index_count, void* stream);
 
 /*
+ * grm_hip_gather_apply_bwd_queries with one gradient row per query, shared by
+ * its routes (float32 grad_tokens [batch, n_query, hidden_size]):
+ *   grad_pairs[b, q, r, :] = memories[b, indices[b, q, r]]^T grad_tokens[b, q, :]
+ * For x = h + sum_r gates_r M[idx_r] q and g = dL/dx this is u_r, from which the
+ * queries' gradient is sum_r gates_r u_r and the gates' u_r . q, with no
+ * [batch, n_query, routes, hidden_size] tensor.  The reference differentiates the
+ * same composition through its gathered states (paper_grm.py:229,301-313,
+ * aggregator.py:67-145 under autograd).  Workspace, index handling and limits as
+ * grm_hip_gather_apply_bwd_queries.  ABI 105.
+ */
+int grm_hip_gather_apply_bwd_tokens(const void* memories, const int64_t* indices, const float* grad_tokens,
+                                    float* grad_pairs, void* workspace, int64_t workspace_bytes, int64_t batch,
+                                    int64_t segments, int64_t n_query, int64_t routes, int64_t hidden_size,
+                                    int64_t key_dim, int mem_dtype, int32_t* bad_index_count, void* stream);
+
+/*
  * Fused retrieval: gather + query application + gate-weighted sum + residual +
  * LayerNorm, without the per-(query, route) rows of gather_apply in float32:
  *   out[b, q, :] = LN(h_online[b, q, :] + sum_r gates[b, q, r] * M[b, idx[b, q, r]] q[b, q])

@@ -43,6 +43,7 @@ SIGNATURES = {
     "grm_hip_gather_apply": (_C, [_P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _C, _C, _C, _P, _P]),
     "grm_hip_retrieve_fuse_workspace": (_I, [_I, _I, _I, _I]),
     "grm_hip_gather_apply_bwd_queries": (_C, [_P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _C, _P, _P]),
+    "grm_hip_gather_apply_bwd_tokens": (_C, [_P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _C, _P, _P]),
     "grm_hip_project_split": (_C, [_P, _P, _P, _P, _P, _I, _I, _I, _I, _C, ctypes.c_float, _P]),
     "grm_hip_residual_layer_norm": (_C, [_P, _P, _P, _P, _P, _I, _I, _C, _C, ctypes.c_float, _P]),
     "grm_hip_retrieve_fuse": (_C, [_P, _P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _C, _C, _C,
@@ -240,6 +241,20 @@ def gather_apply_bwd_queries(memories, indices, grad_out, bad_count=None):
                                                  B, S, Q, R, H, K, dtype_code(memories.dtype), _ptr(bad_count),
                                                  _stream(memories))
     _check(rc, "grm_hip_gather_apply_bwd_queries")
+    return gp
+
+
+def gather_apply_bwd_tokens(memories, indices, grad_tokens, bad_count=None):
+    """Per-pair rows M[idx]^T g[q] for one float32 gradient row per query: [B, Q, R, K] float32."""
+    B, S, H, K = memories.shape
+    Q, R = indices.shape[1], indices.shape[2]
+    gp = torch.empty((B, Q, R, K), dtype=torch.float32, device=memories.device)
+    wsb = int(load().grm_hip_gather_apply_workspace(B, S, Q * R))
+    ws = torch.empty(max(wsb, 16), dtype=torch.uint8, device=memories.device)
+    rc = load().grm_hip_gather_apply_bwd_tokens(_ptr(memories), _ptr(indices), _ptr(grad_tokens), _ptr(gp), _ptr(ws),
+                                                wsb, B, S, Q, R, H, K, dtype_code(memories.dtype), _ptr(bad_count),
+                                                _stream(memories))
+    _check(rc, "grm_hip_gather_apply_bwd_tokens")
     return gp
 
 

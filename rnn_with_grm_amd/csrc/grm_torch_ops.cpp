@@ -2,15 +2,18 @@
 //
 // The five schemas are the reference's, character for character
 // (reference grm/csrc/bindings.cpp:5-11), so grm.core.cuda_ops and every model
-// above it bind to this library unchanged.  Eight more ops live in the same
+// above it bind to this library unchanged.  Twelve more ops live in the same
 // namespace: segment_scan_forward (whole-sequence update with per-segment
 // state snapshots), topk_route (score -> top-k -> softmax), segment_route (the
 // same routing for every segment of a sequence against the archive as it
 // grows), fuse_residual, gather_apply (gather + query application without
 // materialising the states), retrieve_fuse (gather_apply, the gate-weighted
-// sum and fuse_residual in one call), and the layer glue project_split (the
+// sum and fuse_residual in one call), the layer glue project_split (the
 // projection's split with L2-normalised keys and queries) and
-// residual_layer_norm (the block's LayerNorm(out + x)).
+// residual_layer_norm (the block's LayerNorm(out + x)), and three gradients
+// without gathered states: apply_query_backward_queries,
+// gather_apply_backward_queries (one gradient row per pair) and
+// gather_apply_backward_tokens (one row per query, shared by its routes).
 //
 // CUDA-key kernels (HIP devices dispatch on the CUDA key in PyTorch-ROCm)
 // check the inputs, allocate outputs with ATen on the input's device and call
@@ -416,6 +419,24 @@ Tensor gather_apply_backward_queries_generic(const Tensor& memories, const Tenso
   Tensor g = grad_out.to(at::kFloat);
   Tensor dq = indices.dim() == 3 ? at::einsum("bqrhk,bqrh->bqk", {sel, g}) : at::einsum("brhk,brh->bk", {sel, g});
   return dq.to(queries.scalar_type());
+}
+
+// gather_apply_backward_tokens: per (query, route) pair, M[idx]^T g[q] for one
+// float32 gradient row g per query shared by its routes ([B, Q, R, K] float32).
+// With g = dL/d(h + sum_r gates_r r_r) it gives both the queries' gradient
+// (sum_r gates_r rows) and the gates' (rows . q) without the [B, Q, R, H] rows.
+void check_bwd_tokens(const Tensor& memories, const Tensor& indices, const Tensor& grad_tokens) {
+  TORCH_CHECK(memories.dim() == 4 && indices.dim() == 3 && grad_tokens.dim() == 3,
+              "gather_apply_backward_tokens: memories [B, S, H, K], indices [B, Q, R], grad_tokens [B, Q, H]");
+  TORCH_CHECK(indices.size(0) == memories.size(0) && grad_tokens.size(0) == memories.size(0) &&
+                  grad_tokens.size(1) == indices.size(1) && grad_tokens.size(2) == memories.size(2),
+              "gather_apply_backward_tokens: shape mismatch");
+}
+
+Tensor gather_apply_backward_tokens_generic(const Tensor& memories, const Tensor& indices, const Tensor& grad_tokens) {
+  check_bwd_tokens(memories, indices, grad_tokens);
+  Tensor sel = batched_memory_gather_generic(memories, indices).to(at::kFloat);  // [B, Q, R, H, K]
+  return at::einsum("bqrhk,bqh->bqrk", {sel, grad_tokens.to(at::kFloat)}).contiguous();
 }
 
 // project_split: LinearMemoryCell.project's split of the concatenated
@@ -888,7 +909,7 @@ Tensor gather_apply_backward_queries_hip(const Tensor& memories, const Tensor& i
   const int64_t B = memories.size(0), S = memories.size(1), H = memories.size(2), K = memories.size(3);
   const int64_t kp = K <= 16 ? 16 : K <= 32 ? 32 : K <= 64 ? 64 : 128;
   if (!same_cuda_device({&memories, &indices, &grad_out, &queries}) || dtype_code(memories.scalar_type()) < 0 ||
-      K > 128 || S > 16384 || H * (kp + 16) * 4 > 160 * 1024) {
+      K > 128 || S > 16384 || (H + 15) / 16 * 16 * (kp + 4) * 4 > 160 * 1024) {
     if (memories.is_cuda()) g_generic_calls.fetch_add(1);
     return gather_apply_backward_queries_generic(memories, indices, grad_out, queries);
   }
@@ -916,6 +937,38 @@ Tensor gather_apply_backward_queries_hip(const Tensor& memories, const Tensor& i
   Tensor dq = gp.sum(2);  // fixed-order reduction over the routes
   if (idx.dim() == 2) dq = dq.squeeze(1);
   return dq.to(queries.scalar_type());
+}
+
+Tensor gather_apply_backward_tokens_hip(const Tensor& memories, const Tensor& indices, const Tensor& grad_tokens) {
+  check_bwd_tokens(memories, indices, grad_tokens);
+  const int64_t B = memories.size(0), S = memories.size(1), H = memories.size(2), K = memories.size(3);
+  const int64_t kp = K <= 16 ? 16 : K <= 32 ? 32 : K <= 64 ? 64 : 128;
+  if (!same_cuda_device({&memories, &indices, &grad_tokens}) || dtype_code(memories.scalar_type()) < 0 ||
+      K > 128 || S > 16384 || (H + 15) / 16 * 16 * (kp + 4) * 4 > 160 * 1024) {
+    if (memories.is_cuda()) g_generic_calls.fetch_add(1);
+    return gather_apply_backward_tokens_generic(memories, indices, grad_tokens);
+  }
+  c10::OptionalDeviceGuard guard(memories.device());
+  Tensor mm = memories.contiguous();
+  Tensor idx = indices.to(at::kLong).contiguous();
+  Tensor g = grad_tokens.to(at::kFloat).contiguous();
+  const int64_t Q = idx.size(1), R = idx.size(2);
+  Tensor gp = at::empty({B, Q, R, K}, mm.options().dtype(at::kFloat));
+  const int64_t wsb = grm_hip_gather_apply_workspace(B, S, Q * R);
+  Tensor ws = at::empty({std::max<int64_t>(wsb, 16)}, mm.options().dtype(at::kByte));
+  Tensor bad;
+  const bool check = check_indices_requested();
+  if (check) bad = at::zeros({1}, mm.options().dtype(at::kInt));
+  check_rc(grm_hip_gather_apply_bwd_tokens(mm.data_ptr(), idx.data_ptr<int64_t>(), g.data_ptr<float>(),
+                                           gp.data_ptr<float>(), ws.data_ptr(), wsb, B, S, Q, R, H, K,
+                                           dtype_code(mm.scalar_type()), check ? bad.data_ptr<int32_t>() : nullptr,
+                                           current_stream(mm)),
+           "gather_apply_backward_tokens");
+  if (check) {
+    const int64_t nbad = bad.item<int32_t>();
+    TORCH_CHECK_INDEX(nbad == 0, "gather_apply: ", nbad, " index values outside [0, ", S, ")");
+  }
+  return gp;
 }
 
 std::tuple<Tensor, Tensor, Tensor, Tensor> project_split_hip(const Tensor& proj, int64_t key_dim, int64_t value_dim,
@@ -1005,6 +1058,7 @@ TORCH_LIBRARY(grm_cuda, m) {
   m.def("retrieve_fuse(Tensor memories, Tensor indices, Tensor queries, Tensor gates, Tensor h_online, Tensor? weight, Tensor? bias, float eps) -> Tensor");
   m.def("project_split(Tensor proj, int key_dim, int value_dim, int extra_dim, float eps) -> (Tensor keys, Tensor values, Tensor queries, Tensor extra)");
   m.def("gather_apply_backward_queries(Tensor memories, Tensor indices, Tensor grad_out, Tensor queries) -> Tensor");
+  m.def("gather_apply_backward_tokens(Tensor memories, Tensor indices, Tensor grad_tokens) -> Tensor");
   m.def("residual_layer_norm(Tensor x, Tensor residual, Tensor? weight, Tensor? bias, float eps) -> Tensor");
 }
 
@@ -1023,6 +1077,7 @@ TORCH_LIBRARY_IMPL(grm_cuda, CPU, m) {
   m.impl("retrieve_fuse", grm::retrieve_fuse_generic);
   m.impl("project_split", grm::project_split_generic);
   m.impl("gather_apply_backward_queries", grm::gather_apply_backward_queries_generic);
+  m.impl("gather_apply_backward_tokens", grm::gather_apply_backward_tokens_generic);
   m.impl("residual_layer_norm", grm::residual_layer_norm_generic);
 }
 
@@ -1041,6 +1096,7 @@ TORCH_LIBRARY_IMPL(grm_cuda, CUDA, m) {
   m.impl("retrieve_fuse", grm::retrieve_fuse_hip);
   m.impl("project_split", grm::project_split_hip);
   m.impl("gather_apply_backward_queries", grm::gather_apply_backward_queries_hip);
+  m.impl("gather_apply_backward_tokens", grm::gather_apply_backward_tokens_hip);
   m.impl("residual_layer_norm", grm::residual_layer_norm_hip);
 }
 

@@ -1082,7 +1082,7 @@ __host__ __device__ inline int at_rows(int dv) { return (dv + 15) / 16 * 16; }
 
 template <class EL, int DKP>
 __global__ __launch_bounds__(AT_THREADS) void apply_t_kernel(const RetrieveArgs a, const float* grad, float* dqp,
-                                                             int vec_state, int vec_grad) {
+                                                             int vec_state, int vec_grad, int token_rows) {
   using rawl = typename ET<EL>::raw;
   extern __shared__ float Ms[];  // [at_rows(dv)][DKP + 4]
   constexpr int MSK = at_row_stride<DKP>();
@@ -1128,7 +1128,10 @@ __global__ __launch_bounds__(AT_THREADS) void apply_t_kernel(const RetrieveArgs 
   for (; p0 < p_end; p0 += 16 * (AT_THREADS / 64)) {
     const int pn = p0 + 16 * (AT_THREADS / 64);
     const int pid_next = pn + n < p_end ? lb[pn + n] : -1;
-    const float* grow = grad + (b * a.n_index + (pid >= 0 ? pid : 0)) * static_cast<int64_t>(dv);
+    // grad rows per pair, or (token_rows) one row per query shared by its routes
+    const int64_t grow_i = token_rows ? b * a.n_query + (pid >= 0 ? pid : 0) / a.routes
+                                      : b * a.n_index + (pid >= 0 ? pid : 0);
+    const float* grow = grad + grow_i * static_cast<int64_t>(dv);
     auto load_chunk = [&](f32x4* g, int c) {
 #pragma unroll
       for (int u = 0; u < AT_CHUNK; ++u) {
@@ -1195,7 +1198,7 @@ inline size_t apply_t_lds(int dv, int dkp) {
 }
 
 template <class EL, int DKP>
-int launch_apply_t(const RetrieveArgs& a, const float* grad, float* dqp, hipStream_t s) {
+int launch_apply_t(const RetrieveArgs& a, const float* grad, float* dqp, int token_rows, hipStream_t s) {
   using rawl = typename ET<EL>::raw;
   const size_t lds = apply_t_lds(a.dv, DKP);
   static bool attr_set = false;
@@ -1212,16 +1215,17 @@ int launch_apply_t(const RetrieveArgs& a, const float* grad, float* dqp, hipStre
                         reinterpret_cast<uintptr_t>(a.mem) % 16 == 0;
   const int vec_grad = a.dv % 4 == 0 && reinterpret_cast<uintptr_t>(grad) % 16 == 0;
   const dim3 grid(static_cast<unsigned>(a.tb_max), static_cast<unsigned>(a.batch));
-  hipLaunchKernelGGL((apply_t_kernel<EL, DKP>), grid, dim3(AT_THREADS), lds, s, a, grad, dqp, vec_state, vec_grad);
+  hipLaunchKernelGGL((apply_t_kernel<EL, DKP>), grid, dim3(AT_THREADS), lds, s, a, grad, dqp, vec_state, vec_grad,
+                     token_rows);
   return check_launch("gather_apply_bwd");
 }
 
 template <class EL>
-int dispatch_apply_t(const RetrieveArgs& a, const float* grad, float* dqp, hipStream_t s) {
-  if (a.dk <= 16) return launch_apply_t<EL, 16>(a, grad, dqp, s);
-  if (a.dk <= 32) return launch_apply_t<EL, 32>(a, grad, dqp, s);
-  if (a.dk <= 64) return launch_apply_t<EL, 64>(a, grad, dqp, s);
-  return launch_apply_t<EL, 128>(a, grad, dqp, s);
+int dispatch_apply_t(const RetrieveArgs& a, const float* grad, float* dqp, int token_rows, hipStream_t s) {
+  if (a.dk <= 16) return launch_apply_t<EL, 16>(a, grad, dqp, token_rows, s);
+  if (a.dk <= 32) return launch_apply_t<EL, 32>(a, grad, dqp, token_rows, s);
+  if (a.dk <= 64) return launch_apply_t<EL, 64>(a, grad, dqp, token_rows, s);
+  return launch_apply_t<EL, 128>(a, grad, dqp, token_rows, s);
 }
 
 int allow_segment_lds(const void* fn) {
@@ -1525,11 +1529,11 @@ extern "C" int grm_hip_retrieve_fuse(const void* memories, const int64_t* indice
   }
 }
 
-extern "C" int grm_hip_gather_apply_bwd_queries(const void* memories, const int64_t* indices, const float* grad_out,
-                                                float* grad_pairs, void* workspace, int64_t workspace_bytes,
-                                                int64_t batch, int64_t segments, int64_t n_query, int64_t routes,
-                                                int64_t hidden_size, int64_t key_dim, int mem_dtype,
-                                                int32_t* bad_index_count, void* stream) {
+namespace {
+int gather_apply_bwd_impl(const void* memories, const int64_t* indices, const float* grad_out, float* grad_pairs,
+                          void* workspace, int64_t workspace_bytes, int64_t batch, int64_t segments, int64_t n_query,
+                          int64_t routes, int64_t hidden_size, int64_t key_dim, int mem_dtype,
+                          int32_t* bad_index_count, int token_rows, void* stream) {
   if (batch < 0 || segments < 0 || n_query < 0 || routes < 0 || hidden_size < 0 || key_dim < 1) {
     set_error("gather_apply_bwd: negative size or key_dim < 1");
     return GRM_HIP_EINVAL;
@@ -1574,8 +1578,27 @@ extern "C" int grm_hip_gather_apply_bwd_queries(const void* memories, const int6
     return GRM_HIP_EUNSUPPORTED;
   }
   switch (mem_dtype) {
-    case GRM_HIP_F32: return dispatch_apply_t<F32>(a, grad_out, grad_pairs, s);
-    case GRM_HIP_F16: return dispatch_apply_t<F16>(a, grad_out, grad_pairs, s);
-    default: return dispatch_apply_t<BF16>(a, grad_out, grad_pairs, s);
+    case GRM_HIP_F32: return dispatch_apply_t<F32>(a, grad_out, grad_pairs, token_rows, s);
+    case GRM_HIP_F16: return dispatch_apply_t<F16>(a, grad_out, grad_pairs, token_rows, s);
+    default: return dispatch_apply_t<BF16>(a, grad_out, grad_pairs, token_rows, s);
   }
+}
+}  // namespace
+
+extern "C" int grm_hip_gather_apply_bwd_queries(const void* memories, const int64_t* indices, const float* grad_out,
+                                                float* grad_pairs, void* workspace, int64_t workspace_bytes,
+                                                int64_t batch, int64_t segments, int64_t n_query, int64_t routes,
+                                                int64_t hidden_size, int64_t key_dim, int mem_dtype,
+                                                int32_t* bad_index_count, void* stream) {
+  return gather_apply_bwd_impl(memories, indices, grad_out, grad_pairs, workspace, workspace_bytes, batch, segments,
+                               n_query, routes, hidden_size, key_dim, mem_dtype, bad_index_count, 0, stream);
+}
+
+extern "C" int grm_hip_gather_apply_bwd_tokens(const void* memories, const int64_t* indices, const float* grad_tokens,
+                                               float* grad_pairs, void* workspace, int64_t workspace_bytes,
+                                               int64_t batch, int64_t segments, int64_t n_query, int64_t routes,
+                                               int64_t hidden_size, int64_t key_dim, int mem_dtype,
+                                               int32_t* bad_index_count, void* stream) {
+  return gather_apply_bwd_impl(memories, indices, grad_tokens, grad_pairs, workspace, workspace_bytes, batch, segments,
+                               n_query, routes, hidden_size, key_dim, mem_dtype, bad_index_count, 1, stream);
 }

@@ -39,7 +39,7 @@ SCHEMA_OPS = (
 )
 EXTRA_OPS = ("segment_scan_forward", "topk_route", "fuse_residual", "gather_apply", "segment_route",
              "retrieve_fuse", "project_split", "residual_layer_norm", "gather_apply_backward_queries",
-             "apply_query_backward_queries")
+             "gather_apply_backward_tokens", "apply_query_backward_queries")
 
 # Environment variables of the reference (cuda_ops.py:26-32): one per op and a global one.
 GLOBAL_POLICY_ENV = "GRM_CUDA_KERNEL_POLICY"
@@ -356,6 +356,75 @@ class _GatherApplyFn(torch.autograd.Function):
         return None, None, grad_q, None
 
 
+class _RetrieveFuseFn(torch.autograd.Function):
+    """Training form of the fused retrieval, LN(h + sum_r g_r M[idx_r] q) with float32
+    arithmetic (the retriever's gather + apply, paper_grm.py:227-229,301-313, then the
+    aggregator's residual fusion, aggregator.py:67-145).  Forward: the float32 rows, then
+    fuse_residual without LayerNorm weights (x = h + sum_r g_r rows_r in one pass over the
+    rows), then LayerNorm; only x ([B, Q, H] float32) and LayerNorm's mean and 1/std are kept,
+    not the [B, Q, R, H] rows.  Backward: LayerNorm's gradient dx, then per pair
+    u_r = M[idx_r]^T dx (gather_apply_backward_tokens, one dx row per query shared by its
+    routes), dq = sum_r g_r u_r (fuse_residual again, on zero rows) and dg_r = u_r . q.  The
+    memories get no gradient (a detached archive)."""
+
+    @staticmethod
+    def _weighted_sum(base: Tensor, rows: Tensor, gates: Tensor) -> Tensor:
+        """base + sum_r gates_r rows_r for float32 [N, H] base, [N, R, H] rows, [N, R] gates."""
+        if rows.size(-1) <= 2048:
+            return torch.ops.grm_cuda.fuse_residual(base, rows, gates, None, None, 1e-5)
+        return base + (rows * gates.unsqueeze(-1)).sum(1)
+
+    @staticmethod
+    def forward(ctx, memories: Tensor, indices: Tensor, queries: Tensor, gates: Tensor, h_online: Tensor,
+                weight: Optional[Tensor], bias: Optional[Tensor], eps: float):
+        B, Q, H = h_online.shape
+        R = indices.size(-1)
+        gf = gates.float().reshape(B * Q, R).contiguous()
+        rows = torch.ops.grm_cuda.gather_apply(memories, indices, queries, torch.float32)  # [B, Q, R, H]
+        x = _RetrieveFuseFn._weighted_sum(h_online.float().reshape(B * Q, H), rows.reshape(B * Q, R, H), gf)
+        del rows
+        x = x.reshape(B, Q, H)
+        mean = rstd = None
+        if weight is None:
+            out = x
+        else:
+            out, mean, rstd = torch.native_layer_norm(x, (H,), weight.float(),
+                                                      None if bias is None else bias.float(), eps)
+        ctx.save_for_backward(memories, indices, queries, gf, x, mean, rstd, weight, bias)
+        ctx.h_dtype = h_online.dtype
+        ctx.gates_dtype = gates.dtype
+        return out.to(h_online.dtype)
+
+    @staticmethod
+    def backward(ctx, grad_out: Tensor):
+        memories, indices, queries, gf, x, mean, rstd, weight, bias = ctx.saved_tensors
+        B, Q, H = x.shape
+        R, K = gf.size(1), queries.size(-1)
+        dw = db = None
+        if weight is None:
+            dx = grad_out.float()
+        else:
+            mask = [True, ctx.needs_input_grad[5], bias is not None and ctx.needs_input_grad[6]]
+            dx, dwf, dbf = torch.ops.aten.native_layer_norm_backward(
+                grad_out.float().contiguous(), x, (H,), mean, rstd, weight.float(),
+                None if bias is None else bias.float(), mask)
+            dw = None if dwf is None else dwf.to(weight.dtype)
+            db = None if dbf is None else dbf.to(bias.dtype)
+        dq = dg = dh = None
+        if ctx.needs_input_grad[2] or ctx.needs_input_grad[3]:
+            u = torch.ops.grm_cuda.gather_apply_backward_tokens(memories, indices, dx.contiguous())  # [B, Q, R, K]
+            u = u.reshape(B * Q, R, K)
+            if ctx.needs_input_grad[2]:
+                dq = _RetrieveFuseFn._weighted_sum(u.new_zeros(B * Q, K), u, gf)
+                dq = dq.reshape(queries.shape).to(queries.dtype)
+            if ctx.needs_input_grad[3]:
+                dg = (u * queries.float().reshape(B * Q, 1, K)).sum(-1)
+                dg = dg.reshape(B, Q, R).to(ctx.gates_dtype)
+        if ctx.needs_input_grad[4]:
+            dh = dx.to(ctx.h_dtype)
+        return None, None, dq, dg, dh, dw, db, None
+
+
 # ---------------------------------------------------------------------------
 # Entry points (the reference's cuda_ops.py:347-402, then this library's own).
 
@@ -493,13 +562,19 @@ def cuda_retrieve_fuse(memories_per_batch: Tensor, topk_indices: Tensor, queries
     """LayerNorm(h + sum_r gates_r (M[idx_r] q)) for [B, Q] rows: the retriever's float32 gather +
     apply (paper_grm.py:227-229,301-313) followed by the aggregator's residual fusion
     (aggregator.py:67-145, paper_grm.py:604-611), without the [B, Q, R, H] retrieved rows.
-    Inference only (no backward): under autograd the composition runs."""
+    Without gradients the op keeps the per-route rows as row-scaled float16 in its workspace;
+    under autograd (queries, gates, h or the LayerNorm parameters; a detached archive) the
+    native _RetrieveFuseFn runs with float32 rows and keeps only [B, Q, H] for its backward.
+    Memories that need a gradient take the torch composition."""
     needs_grad = torch.is_grad_enabled() and any(
         t is not None and t.requires_grad for t in (memories_per_batch, queries, gates, h_online, weight, bias))
-    if not needs_grad and _run_native("retrieve_fuse", h_online.device, enabled=enabled,
-                                      debug_fallback=debug_fallback):
+    native = _run_native("retrieve_fuse", h_online.device, enabled=enabled, debug_fallback=debug_fallback)
+    if native and not needs_grad:
         return torch.ops.grm_cuda.retrieve_fuse(memories_per_batch, topk_indices, queries, gates, h_online, weight,
                                                 bias, float(eps))
+    if native and not memories_per_batch.requires_grad and topk_indices.dim() == 3:
+        return _RetrieveFuseFn.apply(memories_per_batch, topk_indices, queries, gates, h_online, weight, bias,
+                                     float(eps))
     B, Q, H = h_online.shape
     R = topk_indices.size(-1)
     retrieved = cuda_gather_apply(memories_per_batch, topk_indices, queries, torch.float32, enabled=enabled,

@@ -579,16 +579,24 @@ class SegmentRecurrentMemoryModel(nn.Module):
         # values exact in float32, which lets the kernel use exact 16-bit MFMA.
         q_in = q if q.dtype in (torch.bfloat16, torch.float16) else q.to(torch.float32)
         soup = self.retrieval_fusion_mode == "memory_soup"
-        if not grad and (soup or self.aggregator.fused_kernel_applies()):
+        if soup or self.aggregator.fused_kernel_applies():
             norm = self.memory_soup_norm if soup else self.aggregator.layer_norm
-            weight = norm.weight.float() if isinstance(norm, nn.LayerNorm) else None
-            bias = norm.bias.float() if isinstance(norm, nn.LayerNorm) else None
+            weight = norm.weight if isinstance(norm, nn.LayerNorm) else None
+            bias = norm.bias if isinstance(norm, nn.LayerNorm) else None
             eps = norm.eps if isinstance(norm, nn.LayerNorm) else 1e-5
-            if q.dtype in (torch.bfloat16, torch.float16):
+            if grad:
+                # Training: float32 retrieval rows, residual and LayerNorm in one autograd
+                # function whose backward takes M^T dx per query and route on the GPU; only
+                # the [B, T, H] pre-norm sum is kept for it, not the [B, T, k, H] rows.
+                fused = cuda_ops.cuda_retrieve_fuse(states, idx0, q_in, gates, h_online, weight, bias, eps,
+                                                    debug_fallback=self.cuda_cpp_debug_fallback)
+            elif q.dtype in (torch.bfloat16, torch.float16):
                 # A 16-bit model: retrieval, gate-weighted sum, residual and LayerNorm in one
                 # op; the [B, T, k, H] retrieved rows are kept as row-scaled float16 (relative
                 # rounding 2^-11 of each row's largest value), never as float32.
-                fused = cuda_ops.cuda_retrieve_fuse(states, idx0, q_in, gates.float(), h_online, weight, bias, eps,
+                fused = cuda_ops.cuda_retrieve_fuse(states, idx0, q_in, gates.float(), h_online,
+                                                    None if weight is None else weight.float(),
+                                                    None if bias is None else bias.float(), eps,
                                                     debug_fallback=self.cuda_cpp_debug_fallback)
             else:
                 H = h_online.size(-1)
@@ -596,7 +604,8 @@ class SegmentRecurrentMemoryModel(nn.Module):
                                                        debug_fallback=self.cuda_cpp_debug_fallback)
                 fused = cuda_ops.cuda_fuse_residual(h_online.float().reshape(B * T, H),
                                                     retrieved.reshape(B * T, -1, H), gates.reshape(B * T, -1),
-                                                    weight, bias, eps,
+                                                    None if weight is None else weight.float(),
+                                                    None if bias is None else bias.float(), eps,
                                                     debug_fallback=self.cuda_cpp_debug_fallback).view(B, T, H)
             fused = (self.dropout if soup else self.aggregator.dropout)(fused)
         else:

@@ -260,3 +260,67 @@ def test_glue_ops_cpu_match_torch():
         w, b = torch.randn(16, generator=g).to(dtype), torch.randn(16, generator=g).to(dtype)
         y = torch.ops.grm_cuda.residual_layer_norm(x, r, w, b, 1e-5)
         assert torch.equal(y, F.layer_norm(x + r, (16,), w, b, 1e-5))
+
+
+def _pair_bwd_ref(mem, idx, grad_tokens):
+    """Per (query, route) pair M[idx]^T g[q] from the oracle: each pair is its own rank-4
+    apply-query backward with one route, so the sum over routes cannot hide a wrong route."""
+    B, Q, R = idx.shape
+    H, K = mem.shape[2], mem.shape[3]
+    ok = (idx >= 0).numpy()
+    gathered, _ = orc.gather(mem.double().numpy(), np.where(ok, idx.numpy(), 0))
+    gathered = (gathered * ok[..., None, None]).reshape(B * Q * R, 1, H, K)
+    g = np.repeat(grad_tokens.double().numpy()[:, :, None, :], R, axis=2).reshape(B * Q * R, 1, H)
+    _, gq = orc.apply_query_bwd(g, gathered, np.zeros((B * Q * R, K)))
+    return gq.reshape(B, Q, R, K)
+
+
+def test_cpu_gather_apply_backward_tokens():
+    """The generic (CPU-key) token gradient per pair against the oracle (the generic gather, like
+    the reference's fallback, rejects out-of-range indices; the kernel's zero rows for them are
+    checked on the GPU)."""
+    if not cuda_ops.load_grm_cuda_extension():
+        pytest.skip("extension not built")
+    g = torch.Generator().manual_seed(11)
+    mem = torch.randn(2, 5, 12, 9, generator=g).to(torch.bfloat16)
+    idx = torch.randint(0, 5, (2, 7, 3), generator=g)
+    gx = torch.randn(2, 7, 12, generator=g)
+    out = torch.ops.grm_cuda.gather_apply_backward_tokens(mem, idx, gx)
+    assert out.dtype == torch.float32 and out.shape == (2, 7, 3, 9)
+    np.testing.assert_allclose(out.numpy(), _pair_bwd_ref(mem, idx, gx), rtol=1e-5, atol=1e-5)
+    with pytest.raises(RuntimeError, match="shape mismatch"):
+        torch.ops.grm_cuda.gather_apply_backward_tokens(mem, idx, gx[..., :5])
+
+
+@pytest.mark.parametrize("ln", [True, False])
+def test_cpu_retrieve_fuse_training_function(monkeypatch, ln):
+    """The training form of the fused retrieval (policy "native" on CPU tensors runs it through
+    the CPU-key ops): output and the gradients of queries, gates, h and the LayerNorm
+    parameters equal autograd through the float64 composition gather -> apply -> weighted sum ->
+    residual -> LayerNorm."""
+    monkeypatch.setenv(cuda_ops.GLOBAL_POLICY_ENV, "native")
+    if not cuda_ops.load_grm_cuda_extension():
+        pytest.skip("extension not built")
+    g = torch.Generator().manual_seed(12)
+    B, S, Q, R, H, K = 2, 6, 9, 3, 16, 8
+    mem = torch.randn(B, S, H, K, generator=g) * 0.3
+    idx = torch.randint(0, S, (B, Q, R), generator=g)
+    q = torch.nn.functional.normalize(torch.randn(B, Q, K, generator=g), dim=-1).requires_grad_(True)
+    gates = torch.softmax(torch.randn(B, Q, R, generator=g), -1).requires_grad_(True)
+    h = torch.randn(B, Q, H, generator=g).requires_grad_(True)
+    w = (1 + 0.1 * torch.randn(H, generator=g)).requires_grad_(ln)
+    b = (0.1 * torch.randn(H, generator=g)).requires_grad_(ln)
+    lw, lb = (w, b) if ln else (None, None)
+    gout = torch.randn(B, Q, H, generator=g)
+    out = cuda_ops.cuda_retrieve_fuse(mem, idx, q, gates, h, lw, lb, 1e-5)
+    assert out.grad_fn is not None and "RetrieveFuse" in type(out.grad_fn).__name__
+    wrt = [q, gates, h] + ([w, b] if ln else [])
+    grads = torch.autograd.grad(out, wrt, gout)
+    d = [t.detach().double().requires_grad_(True) for t in wrt]
+    sel = mem.double()[torch.arange(B)[:, None, None], idx]
+    x = d[2] + torch.einsum("bqr,bqrh->bqh", d[1], torch.einsum("bqrhk,bqk->bqrh", sel, d[0]))
+    ref = torch.nn.functional.layer_norm(x, (H,), d[3], d[4], 1e-5) if ln else x
+    rgrads = torch.autograd.grad(ref, d, gout.double())
+    torch.testing.assert_close(out.double(), ref.detach(), rtol=1e-5, atol=1e-5)
+    for got, want in zip(grads, rgrads):
+        torch.testing.assert_close(got.double(), want, rtol=1e-4, atol=1e-5)

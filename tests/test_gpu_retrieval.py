@@ -725,3 +725,83 @@ def test_empty_slot_blocks(dev, Q):
                                        atol=1e-5 * max(1.0, float(np.abs(ref).max())))
         torch.cuda.synchronize()
         assert int(bad.item()) == n_bad, name
+
+
+# ---------------------------------------------------------------- gather_apply backward (tokens)
+def _pair_bwd_ref(mem, idx, grad_tokens):
+    """Per (query, route) pair M[idx]^T g[q] from the oracle, each pair a one-route rank-4
+    apply-query backward; invalid indices give zero rows."""
+    B, Q, R = idx.shape
+    H, K = mem.shape[2], mem.shape[3]
+    ok = (idx >= 0).numpy()
+    gathered, _ = orc.gather(mem.double().numpy(), np.where(ok, idx.numpy(), 0))
+    gathered = (gathered * ok[..., None, None]).reshape(B * Q * R, 1, H, K)
+    g = np.repeat(grad_tokens.double().numpy()[:, :, None, :], R, axis=2).reshape(B * Q * R, 1, H)
+    _, gq = orc.apply_query_bwd(g, gathered, np.zeros((B * Q * R, K)))
+    return gq.reshape(B, Q, R, K)
+
+
+@pytest.mark.parametrize("mem_dtype", [torch.float32, torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("B,Q,S,R,H,K", [(2, 100, 37, 5, 128, 128), (3, 64, 8, 8, 512, 64), (1, 129, 300, 16, 200, 32),
+                                         (1, 70, 3, 8, 40, 20), (1, 1000, 4, 4, 64, 64)])
+def test_gather_apply_bwd_tokens(dev, mem_dtype, B, Q, S, R, H, K):
+    """One float32 gradient row per query shared by its routes: every pair's M[idx]^T g[q]
+    against the oracle at 1e-5 of the gradient's scale, invalid indices zero and counted, and
+    bit-identical to the per-pair entry point given that row repeated for each route."""
+    g = torch.Generator().manual_seed(B * Q + S + H + K)
+    mem = (torch.randn(B, S, H, K, generator=g) * 0.3).to(mem_dtype)
+    idx = torch.randint(0, S, (B, Q, R), generator=g)
+    idx[0, 2, 1] = -1
+    gx = torch.randn(B, Q, H, generator=g)
+    bad = torch.zeros(1, dtype=torch.int32, device=dev)
+    print(f"gather_apply_bwd_tokens B={B} Q={Q} S={S} R={R} H={H} K={K} {mem_dtype}", flush=True)
+    md, idd, gd = mem.to(dev), idx.to(dev), gx.to(dev)
+    gp = capi.gather_apply_bwd_tokens(md, idd, gd, bad_count=bad)
+    pairs = capi.gather_apply_bwd_queries(md, idd, gd.unsqueeze(2).expand(B, Q, R, H).contiguous())
+    torch.cuda.synchronize()
+    assert int(bad.item()) == 1
+    assert not gp[0, 2, 1].any()
+    ref = _pair_bwd_ref(mem, idx, gx)
+    np.testing.assert_allclose(gp.double().cpu().numpy(), ref, rtol=1e-5,
+                               atol=1e-5 * max(1.0, float(np.abs(ref).max())))
+    assert torch.equal(gp, pairs)
+
+
+@pytest.mark.parametrize("h_dtype,ln", [(torch.bfloat16, True), (torch.float32, True), (torch.float32, False)])
+def test_retrieve_fuse_training_gradients(dev, h_dtype, ln):
+    """The training form of cuda_retrieve_fuse (float32 rows, residual, LayerNorm, and a backward
+    through the token-gradient kernel): no generic-path call, and the output and the gradients of
+    queries, gates, h and the LayerNorm parameters against autograd through the float64
+    composition on the CPU.  16-bit q and h enter both sides with the same values; the 16-bit
+    results carry one rounding of their own dtype."""
+    g = torch.Generator().manual_seed(31)
+    B, S, Q, R, H, K = 2, 11, 300, 8, 128, 64
+    mem = (torch.randn(B, S, H, K, generator=g) * 0.2).to(torch.float16)
+    idx = torch.randint(0, S, (B, Q, R), generator=g)
+    q0 = norm(torch.randn(B, Q, K, generator=g)).to(h_dtype)
+    g0 = torch.softmax(torch.randn(B, Q, R, generator=g), -1)
+    h0 = torch.randn(B, Q, H, generator=g).to(h_dtype)
+    w0, b0 = 1 + 0.1 * torch.randn(H, generator=g), 0.1 * torch.randn(H, generator=g)
+    gout = torch.randn(B, Q, H, generator=g).to(h_dtype)
+    print(f"retrieve_fuse training gradients {h_dtype} ln={ln}", flush=True)
+    leaves = [t.to(dev).requires_grad_(True) for t in (q0, g0, h0, w0, b0)]
+    q, gates, h, w, b = leaves
+    ext = cuda_ops.extension_module()
+    generic = ext.generic_path_calls()
+    out = cuda_ops.cuda_retrieve_fuse(mem.to(dev), idx.to(dev), q, gates, h, w if ln else None, b if ln else None)
+    assert "RetrieveFuse" in type(out.grad_fn).__name__
+    wrt = leaves if ln else leaves[:3]
+    grads = torch.autograd.grad(out, wrt, gout.to(dev))
+    torch.cuda.synchronize()
+    assert ext.generic_path_calls() == generic
+    d = [t.detach().double().requires_grad_(True) for t in (q0, g0, h0, w0, b0)]
+    sel = mem.double()[torch.arange(B)[:, None, None], idx]
+    x = d[2] + torch.einsum("bqr,bqrh->bqh", d[1], torch.einsum("bqrhk,bqk->bqrh", sel, d[0]))
+    ref = torch.nn.functional.layer_norm(x, (H,), d[3], d[4], 1e-5) if ln else x
+    rgrads = torch.autograd.grad(ref, d if ln else d[:3], gout.double())
+    tol = 1e-4 if h_dtype == torch.float32 else 1e-2
+    torch.testing.assert_close(out.detach().double().cpu(), ref.detach(), rtol=tol, atol=tol)
+    for name, got, want in zip("q gates h w b".split(), grads, rgrads):
+        assert got.dtype == (torch.float32 if name in ("gates", "w", "b") else h_dtype), name
+        scale = max(1.0, float(want.abs().max()))
+        torch.testing.assert_close(got.double().cpu(), want, rtol=tol, atol=tol * scale, msg=name)
