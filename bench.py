@@ -54,21 +54,22 @@ def make_c2(dev, torch, BH=64, T=2048, D=128, seed=0):
 
 
 def timed_launches(torch, fn, steps: int, warmup: int, stream):
-    """Run fn warmup times, then time `steps` launches with events on `stream`."""
+    """Run fn warmup times, then `steps` times back to back between two events on `stream`.
+    Returns the host wall time and [mean seconds per call].  One event pair around all calls:
+    an event pair around each call of a short kernel also times the idle gap before the host
+    submits it, which is not the kernel's."""
     for _ in range(warmup):
         fn()
     torch.cuda.synchronize()
-    starts = [torch.cuda.Event(enable_timing=True) for _ in range(steps)]
-    ends = [torch.cuda.Event(enable_timing=True) for _ in range(steps)]
+    ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     t0 = time.perf_counter()
-    for i in range(steps):
-        starts[i].record(stream)
+    ev0.record(stream)
+    for _ in range(steps):
         fn()
-        ends[i].record(stream)
+    ev1.record(stream)
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
-    per = [s.elapsed_time(e) * 1e-3 for s, e in zip(starts, ends)]
-    return wall, per
+    return wall, [ev0.elapsed_time(ev1) * 1e-3 / steps]
 
 
 def bench_c2(torch, dev, steps, warmup):

@@ -21,7 +21,9 @@
 #include <stdint.h>
 #include <string.h>
 
+#include <cfloat>
 #include <cmath>
+#include <cstdlib>
 #include <type_traits>
 
 #include "grm_hip.h"
@@ -299,6 +301,74 @@ constexpr int WR_THREADS = WR_ROWS * WR_LANES;
 constexpr int WR_MAXK = 128;                  // keys per workgroup (score buffer)
 constexpr int WR_DT = 64;                     // dims per staged slice
 
+__device__ __forceinline__ void window_write_gates(const RouteArgs& a, const float (*out_s)[32],
+                                                   const int (*out_i)[32], int rl, int lane, bool row_nat,
+                                                   bool active, int64_t b, int64_t row);
+
+// The end of route_window_kernel, with every window key's exact score in sc:
+// each lane places its keys (index order in a short window, rank otherwise: a
+// key's rank is the number of window keys that beat it), then lane 0 of each
+// row writes indices, scores and gates.  Every thread of the workgroup calls it
+// (one barrier inside).
+__device__ __forceinline__ void window_select_write(const RouteArgs& a, const float (*sc)[WR_MAXK + 1],
+                                                    float (*out_s)[32], int (*out_i)[32], int rl, int lane, int nk,
+                                                    int64_t blk_lo, int64_t lo, int64_t hi, bool row_nat,
+                                                    bool active, int64_t b, int64_t row) {
+  const int k = a.k;
+  // Place this lane's keys: index order in a short window, rank otherwise.
+  if (active) {
+    for (int kl = lane; kl < nk; kl += WR_LANES) {
+      const int64_t key = blk_lo + kl;
+      if (key < lo || key >= hi) continue;
+      const float v = sc[rl][kl];
+      int slot;
+      if (row_nat) {
+        slot = static_cast<int>(key - lo);
+      } else {
+        if (!(v > -INFINITY)) continue;  // NaN or -inf: never selected
+        int rank = 0;
+        const int wl = static_cast<int>(lo - blk_lo), wh = static_cast<int>(hi - blk_lo);
+        for (int i = wl; i < wh && rank < k; ++i) {
+          const float u = sc[rl][i];
+          rank += (u > v || (u == v && i < kl)) ? 1 : 0;
+        }
+        if (rank >= k) continue;
+        slot = rank;
+      }
+      out_s[rl][slot] = v;
+      out_i[rl][slot] = static_cast<int>(key);
+    }
+  }
+  __syncthreads();
+  window_write_gates(a, out_s, out_i, rl, lane, row_nat, active, b, row);
+}
+
+// Lane 0 of each row: indices, scores and gates over the filled slots (a
+// prefix), in slot order as route_kernel sums them.
+__device__ __forceinline__ void window_write_gates(const RouteArgs& a, const float (*out_s)[32],
+                                                   const int (*out_i)[32], int rl, int lane, bool row_nat,
+                                                   bool active, int64_t b, int64_t row) {
+  const int k = a.k;
+  if (!active || lane != 0) return;
+  const int64_t obase = (b * a.n_query + row) * k;
+  int n = 0;
+  for (int m = 0; m < k; ++m) n += out_i[rl][m] >= 0 ? 1 : 0;
+  float mx = -INFINITY;
+  if (row_nat) {
+    for (int m = 0; m < n; ++m) mx = fmaxf(mx, out_s[rl][m] * a.inv_temp);
+  } else if (n > 0) {
+    mx = out_s[rl][0] * a.inv_temp;
+  }
+  float sum = 0.f;
+  for (int m = 0; m < n; ++m) sum += expf(out_s[rl][m] * a.inv_temp - mx);
+  for (int m = 0; m < k; ++m) {
+    const bool f = m < n;
+    a.idx[obase + m] = f ? out_i[rl][m] : -1;
+    a.scores[obase + m] = f ? out_s[rl][m] : -INFINITY;
+    a.gates[obase + m] = f ? expf(out_s[rl][m] * a.inv_temp - mx) / sum : 0.f;
+  }
+}
+
 // KPT keys per lane per key chunk: 8 when every workgroup's range is at most
 // 64 keys, else 16.
 template <class E, int KPT>
@@ -404,22 +474,310 @@ __global__ __launch_bounds__(WR_THREADS) void route_window_kernel(const RouteArg
   }
   __syncthreads();  // every score of the row in sc
 
-  // Place this lane's keys: index order in a short window, rank otherwise.
+  window_select_write(a, sc, out_s, out_i, rl, lane, nk, blk_lo, lo, hi, row_nat, active, b, row);
+}
+
+// Segment routing with short windows, 16-bit inputs: route_window_kernel's
+// result, bit for bit, with an MFMA pass that narrows the exact chains to a few
+// candidates per row (reference grm/core/paper_grm.py:566-589, 702-728).
+//
+//  1. 16x16x32 MFMAs give A, the approximate dot product of every (row, key)
+//     of the workgroup.  A and the exact chain add the same exact 16-bit
+//     products in fp32, so |A - chain| <= e = 4 max(dim, 64) 2^-23 |q| max|key|
+//     (norms from the staged slices, scaled up by 1.001).
+//  2. A window key is a candidate of its row when fewer than k window keys have
+//     A > A_key + W, with W twice 2e plus the ties the final multiplication by
+//     `scale` can create and the flushed-denormal terms (as in route_select.hip).
+//     A key outside that set is beaten by k keys after the exact chain and the
+//     scaling, so every key of the exact top k is a candidate.  Rows whose
+//     window holds at most k keys, or whose bound is not finite, take every
+//     window key.
+//  3. A row's candidates are dealt to its 8 lanes, WS_RMAX a lane per pass; each
+//     lane runs the exact chains of its candidates over the restaged slices
+//     (the same fp32 FMA chain over d in increasing order, times scale).
+//  4. Slots by rank among the row's candidates, then the gates as in
+//     route_window_kernel.
+constexpr int WS_RMAX = 4;  // candidate chains per lane and pass
+
+template <class E, int KPT>
+__global__ __launch_bounds__(WR_THREADS) void route_wsel_kernel(const RouteArgs a) {
+  using raw = typename ET<E>::raw;
+  static_assert(sizeof(raw) == 2, "16-bit inputs");
+  constexpr int V = 8;                    // elements per 16-byte granule
+  constexpr int RS = WR_DT + V;           // staged row stride, elements
+  constexpr int KC = WR_LANES * KPT;      // key rows staged (>= the workgroup's range)
+  constexpr int NKT = KC / 16;            // 16-key MFMA tiles
+  constexpr int TPW = NKT / 2;            // key tiles per wave (4 waves: 2 row tiles x 2)
+  constexpr int UNITS = (KC + WR_ROWS) * (WR_DT / V);
+  constexpr int UPT = (UNITS + WR_THREADS - 1) / WR_THREADS;
+  __shared__ __align__(16) raw ktile[KC * RS];
+  __shared__ __align__(16) raw qtile[WR_ROWS * RS];
+  // Approximations by key, then exact scores by candidate; rows 16-byte
+  // aligned, 4 banks apart.
+  __shared__ __align__(16) float sc[WR_ROWS][WR_MAXK + 4];
+  __shared__ float out_s[WR_ROWS][32];
+  __shared__ int out_i[WR_ROWS][32];
+  __shared__ uint8_t clist[WR_ROWS][WR_MAXK];
+  __shared__ float kred[WR_THREADS / 64];
+  __shared__ int passes_s;
+
+  const int tid = threadIdx.x;
+  const int lane = tid % WR_LANES;
+  const int rl = tid / WR_LANES;
+  const int lane64 = tid & 63;
+  const int g = lane64 >> 4, n = lane64 & 15;
+  const int w = tid >> 6;
+  const int64_t b = blockIdx.y;
+  const int64_t S = a.n_keys;
+  const int D = a.dim;
+  const int k = a.k;
+  const int64_t r0 = static_cast<int64_t>(blockIdx.x) * WR_ROWS;
+  const int64_t rlast = min(a.n_query, r0 + WR_ROWS) - 1;
+  const int64_t row = r0 + rl;
+  const bool active = row < a.n_query;
+  auto win_hi = [&](int64_t r) { return min(S, a.base + r / a.seg_len); };
+  auto win_lo = [&](int64_t h) { return h > a.cap ? h - a.cap : int64_t{0}; };
+  const int64_t blk_hi = win_hi(rlast);
+  const int64_t blk_lo = win_lo(win_hi(r0));
+  const int nk = static_cast<int>(blk_hi - blk_lo);  // <= KC, checked on the host
+  const int64_t hi = win_hi(active ? row : r0);
+  const int64_t lo = win_lo(hi);
+  const bool row_nat = hi - lo <= k;
+
+  const raw* qb = static_cast<const raw*>(a.q) + (b * a.n_query + r0) * D;
+  const raw* kb = static_cast<const raw*>(a.keys) + (b * S + blk_lo) * D;
+
+  for (int m = tid; m < WR_ROWS * 32; m += WR_THREADS) {
+    out_s[m / 32][m % 32] = -INFINITY;
+    out_i[m / 32][m % 32] = -1;
+  }
+  if (tid == 0) passes_s = 0;
+
+  // One sweep over d: each slice of WR_DT dims (key rows past nk, query rows
+  // past n_query and dims past D zero) staged, then body(d0, dims in slice).
+  // The next slice's loads are issued before the current one is used.
+  auto load_slice = [&](uint4 (&st)[UPT], int d0) {
+#pragma unroll
+    for (int i = 0; i < UPT; ++i) {
+      const int u = tid + WR_THREADS * i;
+      const int r = u / (WR_DT / V);
+      const int c = (u % (WR_DT / V)) * V;
+      st[i] = make_uint4(0, 0, 0, 0);
+      if (u < UNITS && d0 + c < D) {
+        if (r < KC) {
+          if (r < nk) st[i] = *reinterpret_cast<const uint4*>(kb + r * static_cast<int64_t>(D) + d0 + c);
+        } else if (r0 + (r - KC) < a.n_query) {
+          st[i] = *reinterpret_cast<const uint4*>(qb + (r - KC) * static_cast<int64_t>(D) + d0 + c);
+        }
+      }
+    }
+  };
+  auto sweep = [&](auto&& body) {
+    uint4 st[UPT];
+    load_slice(st, 0);
+    for (int d0 = 0; d0 < D; d0 += WR_DT) {
+      __syncthreads();  // previous slice consumed
+#pragma unroll
+      for (int i = 0; i < UPT; ++i) {
+        const int u = tid + WR_THREADS * i;
+        const int r = u / (WR_DT / V);
+        const int c = (u % (WR_DT / V)) * V;
+        if (u < UNITS) *reinterpret_cast<uint4*>((r < KC ? ktile + r * RS : qtile + (r - KC) * RS) + c) = st[i];
+      }
+      __syncthreads();
+      if (d0 + WR_DT < D) load_slice(st, d0 + WR_DT);
+      body(d0, min(WR_DT, D - d0));
+    }
+  };
+
+  // ---- 1. approximations and norms.  Wave w: row tile w & 1, key tiles
+  // (w >> 1) + 2 i; acc[i][r] is key 16 kt + 4 g + r of row 16 (w & 1) + n.
+  const int rt = w & 1;
+  f32x4 acc[TPW];
+#pragma unroll
+  for (int i = 0; i < TPW; ++i) acc[i] = f32x4{0.f, 0.f, 0.f, 0.f};
+  float qn2 = 0.f;           // partial squared norm of row rl (granule `lane` of each slice)
+  float kn2[KC / WR_ROWS];   // partial squared norms of keys rl + 32 j
+#pragma unroll
+  for (int j = 0; j < KC / WR_ROWS; ++j) kn2[j] = 0.f;
+  sweep([&](int, int) {
+#pragma unroll
+    for (int c = 0; c < WR_DT / 32; ++c) {
+      const Frag8<E> bq = __builtin_bit_cast(Frag8<E>, *reinterpret_cast<const uint4*>(qtile + (16 * rt + n) * RS + 32 * c + 8 * g));
+#pragma unroll
+      for (int i = 0; i < TPW; ++i) {
+        const int kt = (w >> 1) + 2 * i;
+        if (16 * kt < nk) {  // wave-uniform
+          const Frag8<E> ak = __builtin_bit_cast(Frag8<E>, *reinterpret_cast<const uint4*>(ktile + (16 * kt + n) * RS + 32 * c + 8 * g));
+          acc[i] = mfma8(ak, bq, acc[i]);
+        }
+      }
+    }
+    const U8<E> qv = __builtin_bit_cast(U8<E>, *reinterpret_cast<const uint4*>(qtile + rl * RS + V * lane));
+#pragma unroll
+    for (int e = 0; e < V; ++e) {
+      const float x = ET<E>::to_f(qv.e[e]);
+      qn2 = fmaf(x, x, qn2);
+    }
+#pragma unroll
+    for (int j = 0; j < KC / WR_ROWS; ++j) {
+      const U8<E> kv = __builtin_bit_cast(U8<E>, *reinterpret_cast<const uint4*>(ktile + (rl + WR_ROWS * j) * RS + V * lane));
+#pragma unroll
+      for (int e = 0; e < V; ++e) {
+        const float x = ET<E>::to_f(kv.e[e]);
+        kn2[j] = fmaf(x, x, kn2[j]);
+      }
+    }
+  });
+#pragma unroll
+  for (int i = 0; i < TPW; ++i) {
+    const int kt = (w >> 1) + 2 * i;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int key = 16 * kt + 4 * g + r;
+      if (key < nk) sc[16 * rt + n][key] = acc[i][r];
+    }
+  }
+  // Row norms over the row's 8 lanes; the largest key norm over the workgroup
+  // (NaN when any is not finite: every row then takes the exact path).
+#pragma unroll
+  for (int off = 1; off < WR_LANES; off <<= 1) qn2 += __shfl_xor(qn2, off, 64);
+  float kmx = 0.f;
+#pragma unroll
+  for (int j = 0; j < KC / WR_ROWS; ++j) {
+    float t = kn2[j];
+#pragma unroll
+    for (int off = 1; off < WR_LANES; off <<= 1) t += __shfl_xor(t, off, 64);
+    kmx = (t <= INFINITY && kmx <= INFINITY) ? fmaxf(kmx, t) : NAN;
+  }
+#pragma unroll
+  for (int off = 8; off < 64; off <<= 1) {
+    const float o = __shfl_xor(kmx, off, 64);
+    kmx = (o <= INFINITY && kmx <= INFINITY) ? fmaxf(kmx, o) : NAN;
+  }
+  if (lane64 == 0) kred[w] = kmx;
+  __syncthreads();  // sc holds every approximation, kred every wave's maximum
+  float kmax2 = kred[0];
+#pragma unroll
+  for (int i = 1; i < WR_THREADS / 64; ++i)
+    kmax2 = (kred[i] <= INFINITY && kmax2 <= INFINITY) ? fmaxf(kmax2, kred[i]) : NAN;
+
+  // ---- 2. candidates.  Bit j of cmask: key lane + 8 j of the workgroup's range.
+  const float qn = sqrtf(qn2) * 1.001f;
+  const float km = sqrtf(kmax2) * 1.001f;
+  const float e_mfma = 4.f * static_cast<float>(max(D, 64)) * 0x1p-23f * qn * km;
+  const float mag = qn * km + 4.f * e_mfma;  // >= |A| and |chain| of every key
+  const float wl = 2.f * (2.f * e_mfma + 0x1p-21f * (mag + 2.f * e_mfma) + 0x1p-148f / a.scale +
+                          4.f * static_cast<float>(D) * 0x1p-126f * (qn + km));
+  const bool sound = qn * km < 1e30f && wl <= 1e30f;  // false for NaN and inf
+  const bool take_all = row_nat || !sound;
+  const int wlo = static_cast<int>(lo - blk_lo), whi = static_cast<int>(hi - blk_lo);
+  uint32_t cmask = 0u;
   if (active) {
-    for (int kl = lane; kl < nk; kl += WR_LANES) {
+    // Each lane counts, for all its keys at once, the window keys whose A
+    // exceeds theirs by more than W (16-byte reads of the row, no early exit).
+    float t[KPT];
+    int cnt[KPT];
+#pragma unroll
+    for (int j = 0; j < KPT; ++j) {
+      const int kl = lane + WR_LANES * j;
+      t[j] = (kl >= wlo && kl < whi) ? sc[rl][kl] + wl : INFINITY;
+      cnt[j] = 0;
+    }
+    if (!take_all) {
+      for (int i = wlo & ~3; i < whi; i += 4) {
+        const float4 u4 = *reinterpret_cast<const float4*>(&sc[rl][i]);
+        const float uu[4] = {u4.x, u4.y, u4.z, u4.w};
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const float u = (i + e >= wlo && i + e < whi) ? uu[e] : -INFINITY;
+#pragma unroll
+          for (int j = 0; j < KPT; ++j) cnt[j] += u > t[j] ? 1 : 0;
+        }
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < KPT; ++j) {
+      const int kl = lane + WR_LANES * j;
+      const bool cand = kl >= wlo && kl < whi && (take_all || cnt[j] < k);
+      cmask |= cand ? (1u << j) : 0u;
+    }
+  }
+  // The row's candidates in lane order: an exclusive prefix over its 8 lanes.
+  const int mine = __builtin_popcount(cmask);
+  int incl = mine;
+#pragma unroll
+  for (int off = 1; off < WR_LANES; off <<= 1) {
+    const int o = __shfl_up(incl, off, WR_LANES);
+    incl += lane >= off ? o : 0;
+  }
+  const int total = __shfl(incl, WR_LANES - 1, WR_LANES);
+  __syncthreads();  // every approximation read
+  {
+    int pos = incl - mine;
+#pragma unroll
+    for (int j = 0; j < KPT; ++j)
+      if (cmask & (1u << j)) clist[rl][pos++] = static_cast<uint8_t>(lane + WR_LANES * j);
+  }
+  const int row_passes = (total + WR_LANES * WS_RMAX - 1) / (WR_LANES * WS_RMAX);
+  if (lane == 0 && row_passes > 0) atomicMax(&passes_s, row_passes);
+  __syncthreads();
+  const int passes = passes_s;
+
+  // ---- 3. exact chains of the candidates: candidate c of the row goes to lane
+  // c % 8, pass c / (8 WS_RMAX).
+  for (int pass = 0; pass < passes; ++pass) {
+    const int c0 = pass * WR_LANES * WS_RMAX + lane;
+    int ck[WS_RMAX];
+    float ex[WS_RMAX];
+    int nr = 0;
+#pragma unroll
+    for (int r = 0; r < WS_RMAX; ++r) {
+      const int c = c0 + WR_LANES * r;
+      ck[r] = c < total ? clist[rl][c] : 0;
+      nr += c < total ? 1 : 0;
+      ex[r] = 0.f;
+    }
+    sweep([&](int, int dl) {
+      for (int dd = 0; dd < dl; dd += V) {
+        const U8<E> qv = __builtin_bit_cast(U8<E>, *reinterpret_cast<const uint4*>(qtile + rl * RS + dd));
+        float x[V];
+#pragma unroll
+        for (int e = 0; e < V; ++e) x[e] = ET<E>::to_f(qv.e[e]);
+#pragma unroll
+        for (int r = 0; r < WS_RMAX; ++r) {
+          if (r < nr) {
+            const U8<E> kv = __builtin_bit_cast(U8<E>, *reinterpret_cast<const uint4*>(ktile + ck[r] * RS + dd));
+#pragma unroll
+            for (int e = 0; e < V; ++e) ex[r] = fmaf(x[e], ET<E>::to_f(kv.e[e]), ex[r]);
+          }
+        }
+      }
+    });
+#pragma unroll
+    for (int r = 0; r < WS_RMAX; ++r)
+      if (r < nr) sc[rl][c0 + WR_LANES * r] = ex[r] * a.scale;
+  }
+  __syncthreads();  // every candidate's exact score in sc, in candidate order
+
+  // ---- 4. slots: index order in a short window, else the rank among the row's
+  // candidates (a key that is not a candidate is beaten by k keys, so it beats
+  // no key of the top k and changes none of their ranks).
+  if (active) {
+    for (int c = lane; c < total; c += WR_LANES) {
+      const int kl = clist[rl][c];
       const int64_t key = blk_lo + kl;
-      if (key < lo || key >= hi) continue;
-      const float v = sc[rl][kl];
+      const float v = sc[rl][c];
       int slot;
       if (row_nat) {
         slot = static_cast<int>(key - lo);
       } else {
         if (!(v > -INFINITY)) continue;  // NaN or -inf: never selected
         int rank = 0;
-        const int wl = static_cast<int>(lo - blk_lo), wh = static_cast<int>(hi - blk_lo);
-        for (int i = wl; i < wh && rank < k; ++i) {
+        for (int i = 0; i < total && rank < k; ++i) {
           const float u = sc[rl][i];
-          rank += (u > v || (u == v && i < kl)) ? 1 : 0;
+          const int ki = clist[rl][i];
+          rank += (u > v || (u == v && ki < kl)) ? 1 : 0;
         }
         if (rank >= k) continue;
         slot = rank;
@@ -429,30 +787,26 @@ __global__ __launch_bounds__(WR_THREADS) void route_window_kernel(const RouteArg
     }
   }
   __syncthreads();
-  if (!active || lane != 0) return;
-  // Gates over the filled slots (a prefix), in slot order as route_kernel sums them.
-  const int64_t obase = (b * a.n_query + row) * k;
-  int n = 0;
-  for (int m = 0; m < k; ++m) n += out_i[rl][m] >= 0 ? 1 : 0;
-  float mx = -INFINITY;
-  if (row_nat) {
-    for (int m = 0; m < n; ++m) mx = fmaxf(mx, out_s[rl][m] * a.inv_temp);
-  } else if (n > 0) {
-    mx = out_s[rl][0] * a.inv_temp;
-  }
-  float sum = 0.f;
-  for (int m = 0; m < n; ++m) sum += expf(out_s[rl][m] * a.inv_temp - mx);
-  for (int m = 0; m < k; ++m) {
-    const bool f = m < n;
-    a.idx[obase + m] = f ? out_i[rl][m] : -1;
-    a.scores[obase + m] = f ? out_s[rl][m] : -INFINITY;
-    a.gates[obase + m] = f ? expf(out_s[rl][m] * a.inv_temp - mx) / sum : 0.f;
-  }
+  window_write_gates(a, out_s, out_i, rl, lane, row_nat, active, b, row);
 }
 
 template <class E>
 int launch_route_window(const RouteArgs& a, int64_t batch, int64_t span, hipStream_t s) {
   const dim3 grid(static_cast<unsigned>((a.n_query + WR_ROWS - 1) / WR_ROWS), static_cast<unsigned>(batch));
+  if constexpr (!std::is_same_v<E, F32>) {
+    // The MFMA-narrowed kernel needs a positive finite scale (the candidate
+    // bound assumes scores keep the chains' order); GRM_HIP_ROUTE_WSEL=0 keeps
+    // every window on the all-exact kernel.
+    const char* env = getenv("GRM_HIP_ROUTE_WSEL");
+    if ((env == nullptr || env[0] != '0') && a.scale > 0.f && a.scale <= FLT_MAX) {
+      if (span <= WR_LANES * 8) {
+        hipLaunchKernelGGL((route_wsel_kernel<E, 8>), grid, dim3(WR_THREADS), 0, s, a);
+      } else {
+        hipLaunchKernelGGL((route_wsel_kernel<E, 16>), grid, dim3(WR_THREADS), 0, s, a);
+      }
+      return check_launch("segment_route");
+    }
+  }
   if (span <= WR_LANES * 8) {
     hipLaunchKernelGGL((route_window_kernel<E, 8>), grid, dim3(WR_THREADS), 0, s, a);
   } else {

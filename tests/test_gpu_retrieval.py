@@ -805,3 +805,85 @@ def test_retrieve_fuse_training_gradients(dev, h_dtype, ln):
         assert got.dtype == (torch.float32 if name in ("gates", "w", "b") else h_dtype), name
         scale = max(1.0, float(want.abs().max()))
         torch.testing.assert_close(got.double().cpu(), want, rtol=tol, atol=tol * scale, msg=name)
+
+
+# ---------------------------------------------------------------- segment routing, MFMA-narrowed windows
+def _route_both(dev, monkeypatch, q, keys, k, seg, base, cap, scale):
+    """segment_route through the MFMA-narrowed window kernel and through the all-exact one
+    (GRM_HIP_ROUTE_WSEL=0), on the device."""
+    qd, kd = q.to(dev), keys.to(dev)
+    out = capi.segment_route(qd, kd, k, seg, base, cap, scale)
+    monkeypatch.setenv("GRM_HIP_ROUTE_WSEL", "0")
+    ref = capi.segment_route(qd, kd, k, seg, base, cap, scale)
+    monkeypatch.delenv("GRM_HIP_ROUTE_WSEL")
+    torch.cuda.synchronize()
+    return out, ref
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("B,T,seg,base,cap,S,D,k", [
+    (2, 2048, 64, 0, 64, 32, 512, 8),      # config 4's routing: hidden 512, 64-token segments, top-8 of 64
+    (1, 1500, 64, 40, 64, 63, 512, 8),     # a filled archive: every window 64 keys
+    (2, 700, 50, 3, 100, 17, 256, 16),     # segments straddle 32-row workgroups; up to 101 keys a workgroup
+    (1, 900, 24, 0, 120, 37, 136, 32),     # k = 32, windows of 120 keys
+    (1, 333, 7, 60, 16, 107, 512, 8),      # short segments: several windows per workgroup
+    (1, 400, 64, 0, 64, 7, 1024, 4),       # d = 1024, windows below and above k
+])
+def test_segment_route_window_select(dev, monkeypatch, dtype, B, T, seg, base, cap, S, D, k):
+    """Segment routing with 16-bit inputs whose windows fit one workgroup: the MFMA-narrowed
+    window kernel, bit-exact against the oracle's per-window routing and equal to the all-exact
+    window kernel (indices, scores and gates)."""
+    g = torch.Generator().manual_seed(T + S + D)
+    q = torch.randn(B, T, D, generator=g).to(dtype)
+    keys = (torch.randn(B, S, D, generator=g) * 0.5).to(dtype)
+    scale = 1.0 / D ** 0.5
+    print(f"window select {dtype} B={B} T={T} seg={seg} base={base} cap={cap} S={S} D={D} k={k}", flush=True)
+    (gates, idx, sc), (g0, i0, s0) = _route_both(dev, monkeypatch, q, keys, k, seg, base, cap, scale)
+    og, oi, osc = orc.segment_route(q.float().numpy(), keys.float().numpy(), k, seg, base, cap, scale)
+    assert np.array_equal(idx.cpu().numpy(), oi)
+    assert np.array_equal(sc.cpu().numpy(), osc)
+    np.testing.assert_allclose(gates.cpu().numpy(), og, rtol=1e-5, atol=1e-6)
+    assert torch.equal(idx, i0) and torch.equal(sc, s0) and torch.equal(gates, g0)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_segment_route_window_select_ties(dev, monkeypatch, dtype):
+    """Windows full of exact and near ties: duplicated keys (equal scores: the lower index wins),
+    keys one 16-bit step apart, and rows whose every window key is a candidate (all keys equal),
+    which takes several passes of exact chains per row; against the oracle and the all-exact
+    kernel."""
+    g = torch.Generator().manual_seed(77)
+    B, T, seg, cap, S, D, k = 2, 640, 32, 128, 100, 384, 32  # base 81: windows of 81 .. 100 keys
+    base_keys = torch.randn(B, 6, D, generator=g)
+    keys = base_keys[:, torch.randint(0, 6, (S,), generator=g)].clone()  # many exact duplicates
+    keys[:, ::3, 5] += 2.0 ** -6                                          # near duplicates
+    keys[1] = base_keys[1, 0]                                             # batch 1: all keys equal
+    keys = keys.to(dtype)
+    q = (base_keys[:, torch.randint(0, 6, (T,), generator=g)] + 0.01 * torch.randn(B, T, D, generator=g)).to(dtype)
+    scale = 0.05
+    print(f"window select ties {dtype}", flush=True)
+    (gates, idx, sc), (g0, i0, s0) = _route_both(dev, monkeypatch, q, keys, k, seg, 81, cap, scale)
+    og, oi, osc = orc.segment_route(q.float().numpy(), keys.float().numpy(), k, seg, 81, cap, scale)
+    assert np.array_equal(idx.cpu().numpy(), oi)
+    assert np.array_equal(sc.cpu().numpy(), osc)
+    assert torch.equal(idx, i0) and torch.equal(sc, s0) and torch.equal(gates, g0)
+
+
+def test_segment_route_window_select_nonfinite(dev, monkeypatch):
+    """A NaN query row and an infinite key take the exact path (the candidate bound is not
+    finite): the same indices, scores and gates as the all-exact window kernel, NaN for NaN."""
+    g = torch.Generator().manual_seed(78)
+    q = torch.randn(1, 256, 512, generator=g)
+    keys = torch.randn(1, 12, 512, generator=g)
+    q[0, 70, 3] = float("nan")
+    q = q.to(torch.bfloat16)
+    for bad_key in (False, True):
+        kk = keys.clone()
+        if bad_key:
+            kk[0, 2, 9] = float("inf")
+        print(f"window select non-finite bad_key={bad_key}", flush=True)
+        (gates, idx, sc), (g0, i0, s0) = _route_both(dev, monkeypatch, q, kk.to(torch.bfloat16), 4, 32, 0, 64,
+                                                     0.04)
+        assert torch.equal(idx, i0)
+        assert torch.equal(torch.nan_to_num(sc, nan=7.0), torch.nan_to_num(s0, nan=7.0))
+        assert torch.equal(torch.nan_to_num(gates, nan=7.0), torch.nan_to_num(g0, nan=7.0))
