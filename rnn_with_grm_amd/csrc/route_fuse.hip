@@ -485,19 +485,70 @@ __global__ __launch_bounds__(WR_THREADS) void route_window_kernel(const RouteArg
 //     of the workgroup.  A and the exact chain add the same exact 16-bit
 //     products in fp32, so |A - chain| <= e = 4 max(dim, 64) 2^-23 |q| max|key|
 //     (norms from the staged slices, scaled up by 1.001).
-//  2. A window key is a candidate of its row when fewer than k window keys have
-//     A > A_key + W, with W twice 2e plus the ties the final multiplication by
-//     `scale` can create and the flushed-denormal terms (as in route_select.hip).
-//     A key outside that set is beaten by k keys after the exact chain and the
-//     scaling, so every key of the exact top k is a candidate.  Rows whose
+//  2. A window key is a candidate of its row when A_key >= L - W, L the k-th
+//     largest A of the window and W twice 2e plus the ties the final
+//     multiplication by `scale` can create and the flushed-denormal terms (as in
+//     route_select.hip).  A key below that is beaten by k keys after the exact
+//     chain and the scaling, so every key of the exact top k is a candidate.
+//     For k <= KPT, L comes from a bitonic sort of each lane's KPT values and
+//     three merges across the row's 8 lanes; otherwise each key counts the
+//     window keys with A > A_key + W (the same test: fewer than k).  Rows whose
 //     window holds at most k keys, or whose bound is not finite, take every
 //     window key.
-//  3. A row's candidates are dealt to its 8 lanes, WS_RMAX a lane per pass; each
-//     lane runs the exact chains of its candidates over the restaged slices
-//     (the same fp32 FMA chain over d in increasing order, times scale).
-//  4. Slots by rank among the row's candidates, then the gates as in
-//     route_window_kernel.
-constexpr int WS_RMAX = 4;  // candidate chains per lane and pass
+//  3. The workgroup's candidates, row after row, are dealt to all 256 lanes
+//     (candidate c to thread c mod 256), so a wave runs a second round only for
+//     the candidates past the first 256; each lane runs the exact chain (the
+//     same fp32 FMA chain over d in increasing order, times scale) over the
+//     restaged slices.
+//  4. Slots by rank among the row's candidates (a key that is not a candidate
+//     is beaten by k keys, so it beats no key of the top k and changes none of
+//     their ranks), then the gates as in route_window_kernel.
+constexpr int WS_ROUNDS = 2;  // candidate rounds per pass (256 candidates a round)
+
+__device__ __forceinline__ float ws_max(float a, float b) { return __builtin_amdgcn_fmed3f(a, b, FLT_MAX); }
+__device__ __forceinline__ float ws_min(float a, float b) { return __builtin_amdgcn_fmed3f(a, b, -FLT_MAX); }
+
+// x sorted descending in place (bitonic network; NaN-free input, -inf may come
+// out as -FLT_MAX).
+template <int N>
+__device__ __forceinline__ void ws_sort_desc(float (&x)[N]) {
+#pragma unroll
+  for (int size = 2; size <= N; size <<= 1)
+#pragma unroll
+    for (int stride = size / 2; stride > 0; stride >>= 1)
+#pragma unroll
+      for (int i = 0; i < N; ++i) {
+        const int j = i ^ stride;
+        if (j > i) {
+          const float hi = ws_max(x[i], x[j]), lo = ws_min(x[i], x[j]);
+          const bool desc = (i & size) == 0 || size == N;
+          x[i] = desc ? hi : lo;
+          x[j] = desc ? lo : hi;
+        }
+      }
+}
+
+// Descending x := the N largest of x and the partner lane's x (lane ^ off),
+// descending: max(x_i, y_{N-1-i}) is bitonic and holds them; half-cleaners sort.
+template <int N>
+__device__ __forceinline__ void ws_merge_desc(float (&x)[N], int off) {
+  float y[N];
+#pragma unroll
+  for (int i = 0; i < N; ++i) y[i] = __shfl_xor(x[i], off, 64);
+#pragma unroll
+  for (int i = 0; i < N; ++i) x[i] = ws_max(x[i], y[N - 1 - i]);
+#pragma unroll
+  for (int stride = N / 2; stride > 0; stride >>= 1)
+#pragma unroll
+    for (int i = 0; i < N; ++i) {
+      const int j = i ^ stride;
+      if (j > i) {
+        const float hi = ws_max(x[i], x[j]), lo = ws_min(x[i], x[j]);
+        x[i] = hi;
+        x[j] = lo;
+      }
+    }
+}
 
 template <class E, int KPT>
 __global__ __launch_bounds__(WR_THREADS) void route_wsel_kernel(const RouteArgs a) {
@@ -510,16 +561,16 @@ __global__ __launch_bounds__(WR_THREADS) void route_wsel_kernel(const RouteArgs 
   constexpr int TPW = NKT / 2;            // key tiles per wave (4 waves: 2 row tiles x 2)
   constexpr int UNITS = (KC + WR_ROWS) * (WR_DT / V);
   constexpr int UPT = (UNITS + WR_THREADS - 1) / WR_THREADS;
+  // The key slices; after the last sweep, the rows' output slots.
   __shared__ __align__(16) raw ktile[KC * RS];
+  static_assert(sizeof(ktile) >= WR_ROWS * 32 * (sizeof(float) + sizeof(int)), "slots fit the key tile");
   __shared__ __align__(16) raw qtile[WR_ROWS * RS];
   // Approximations by key, then exact scores by candidate; rows 16-byte
   // aligned, 4 banks apart.
   __shared__ __align__(16) float sc[WR_ROWS][WR_MAXK + 4];
-  __shared__ float out_s[WR_ROWS][32];
-  __shared__ int out_i[WR_ROWS][32];
   __shared__ uint8_t clist[WR_ROWS][WR_MAXK];
+  __shared__ int rowoff[WR_ROWS + 1];  // first workgroup candidate of each row
   __shared__ float kred[WR_THREADS / 64];
-  __shared__ int passes_s;
 
   const int tid = threadIdx.x;
   const int lane = tid % WR_LANES;
@@ -546,12 +597,6 @@ __global__ __launch_bounds__(WR_THREADS) void route_wsel_kernel(const RouteArgs 
 
   const raw* qb = static_cast<const raw*>(a.q) + (b * a.n_query + r0) * D;
   const raw* kb = static_cast<const raw*>(a.keys) + (b * S + blk_lo) * D;
-
-  for (int m = tid; m < WR_ROWS * 32; m += WR_THREADS) {
-    out_s[m / 32][m % 32] = -INFINITY;
-    out_i[m / 32][m % 32] = -1;
-  }
-  if (tid == 0) passes_s = 0;
 
   // One sweep over d: each slice of WR_DT dims (key rows past nk, query rows
   // past n_query and dims past D zero) staged, then body(d0, dims in slice).
@@ -673,34 +718,60 @@ __global__ __launch_bounds__(WR_THREADS) void route_wsel_kernel(const RouteArgs 
   const bool take_all = row_nat || !sound;
   const int wlo = static_cast<int>(lo - blk_lo), whi = static_cast<int>(hi - blk_lo);
   uint32_t cmask = 0u;
-  if (active) {
-    // Each lane counts, for all its keys at once, the window keys whose A
-    // exceeds theirs by more than W (16-byte reads of the row, no early exit).
-    float t[KPT];
-    int cnt[KPT];
+  {
+    float x[KPT];
 #pragma unroll
     for (int j = 0; j < KPT; ++j) {
       const int kl = lane + WR_LANES * j;
-      t[j] = (kl >= wlo && kl < whi) ? sc[rl][kl] + wl : INFINITY;
-      cnt[j] = 0;
+      x[j] = (kl >= wlo && kl < whi) ? sc[rl][kl] : -INFINITY;
     }
-    if (!take_all) {
-      for (int i = wlo & ~3; i < whi; i += 4) {
-        const float4 u4 = *reinterpret_cast<const float4*>(&sc[rl][i]);
-        const float uu[4] = {u4.x, u4.y, u4.z, u4.w};
+    if (k <= KPT) {
+      // L: the row's KPT largest in every lane of the row (the merges run in
+      // every lane; the inputs of rows that take every key do not matter).
+      float y[KPT];
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const float u = (i + e >= wlo && i + e < whi) ? uu[e] : -INFINITY;
+      for (int j = 0; j < KPT; ++j) y[j] = sound ? x[j] : -INFINITY;  // NaN-free
+      ws_sort_desc(y);
 #pragma unroll
-          for (int j = 0; j < KPT; ++j) cnt[j] += u > t[j] ? 1 : 0;
+      for (int off = 1; off < WR_LANES; off <<= 1) ws_merge_desc(y, off);
+      float lk = y[0];
+#pragma unroll
+      for (int i = 1; i < KPT; ++i) lk = (i == k - 1) ? y[i] : lk;
+      const float thr = lk - wl;
+#pragma unroll
+      for (int j = 0; j < KPT; ++j) {
+        const int kl = lane + WR_LANES * j;
+        const bool cand = active && kl >= wlo && kl < whi && (take_all || x[j] >= thr);
+        cmask |= cand ? (1u << j) : 0u;
+      }
+    } else if (active) {
+      // Each lane counts, for all its keys at once, the window keys whose A
+      // exceeds theirs by more than W (16-byte reads of the row).
+      float t[KPT];
+      int cnt[KPT];
+#pragma unroll
+      for (int j = 0; j < KPT; ++j) {
+        t[j] = x[j] > -INFINITY ? x[j] + wl : INFINITY;
+        cnt[j] = 0;
+      }
+      if (!take_all) {
+        for (int i = wlo & ~3; i < whi; i += 4) {
+          const float4 u4 = *reinterpret_cast<const float4*>(&sc[rl][i]);
+          const float uu[4] = {u4.x, u4.y, u4.z, u4.w};
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const float u = (i + e >= wlo && i + e < whi) ? uu[e] : -INFINITY;
+#pragma unroll
+            for (int j = 0; j < KPT; ++j) cnt[j] += u > t[j] ? 1 : 0;
+          }
         }
       }
-    }
 #pragma unroll
-    for (int j = 0; j < KPT; ++j) {
-      const int kl = lane + WR_LANES * j;
-      const bool cand = kl >= wlo && kl < whi && (take_all || cnt[j] < k);
-      cmask |= cand ? (1u << j) : 0u;
+      for (int j = 0; j < KPT; ++j) {
+        const int kl = lane + WR_LANES * j;
+        const bool cand = kl >= wlo && kl < whi && (take_all || cnt[j] < k);
+        cmask |= cand ? (1u << j) : 0u;
+      }
     }
   }
   // The row's candidates in lane order: an exclusive prefix over its 8 lanes.
@@ -712,57 +783,73 @@ __global__ __launch_bounds__(WR_THREADS) void route_wsel_kernel(const RouteArgs 
     incl += lane >= off ? o : 0;
   }
   const int total = __shfl(incl, WR_LANES - 1, WR_LANES);
-  __syncthreads();  // every approximation read
   {
     int pos = incl - mine;
 #pragma unroll
     for (int j = 0; j < KPT; ++j)
       if (cmask & (1u << j)) clist[rl][pos++] = static_cast<uint8_t>(lane + WR_LANES * j);
   }
-  const int row_passes = (total + WR_LANES * WS_RMAX - 1) / (WR_LANES * WS_RMAX);
-  if (lane == 0 && row_passes > 0) atomicMax(&passes_s, row_passes);
-  __syncthreads();
-  const int passes = passes_s;
-
-  // ---- 3. exact chains of the candidates: candidate c of the row goes to lane
-  // c % 8, pass c / (8 WS_RMAX).
-  for (int pass = 0; pass < passes; ++pass) {
-    const int c0 = pass * WR_LANES * WS_RMAX + lane;
-    int ck[WS_RMAX];
-    float ex[WS_RMAX];
-    int nr = 0;
+  if (lane == 0) rowoff[rl + 1] = total;
+  __syncthreads();  // every approximation read; the lists and row totals written
+  if (tid < 64) {
+    // rowoff := exclusive prefix of the row totals (32 rows, one wave)
+    int v = tid < WR_ROWS ? rowoff[tid + 1] : 0;
 #pragma unroll
-    for (int r = 0; r < WS_RMAX; ++r) {
-      const int c = c0 + WR_LANES * r;
-      ck[r] = c < total ? clist[rl][c] : 0;
-      nr += c < total ? 1 : 0;
+    for (int off = 1; off < WR_ROWS; off <<= 1) {
+      const int o = __shfl_up(v, off, 64);
+      v += tid >= off ? o : 0;
+    }
+    if (tid < WR_ROWS) rowoff[tid + 1] = v;
+    if (tid == 0) rowoff[0] = 0;
+  }
+  __syncthreads();
+  const int ctot = rowoff[WR_ROWS];
+
+  // ---- 3. exact chains: workgroup candidate c (rows in order) on thread c mod
+  // 256, pass c / (256 WS_ROUNDS).
+  for (int pass0 = 0; pass0 < ctot; pass0 += WR_THREADS * WS_ROUNDS) {
+    int crow[WS_ROUNDS], ckey[WS_ROUNDS], cpos[WS_ROUNDS];
+    float ex[WS_ROUNDS];
+#pragma unroll
+    for (int r = 0; r < WS_ROUNDS; ++r) {
+      const int c = pass0 + WR_THREADS * r + tid;
+      int rr = 0;  // the row whose candidates hold c: rowoff[rr] <= c < rowoff[rr + 1]
+#pragma unroll
+      for (int step = WR_ROWS / 2; step > 0; step >>= 1) rr += (c >= rowoff[rr + step]) ? step : 0;
+      crow[r] = rr;
+      cpos[r] = c - rowoff[rr];
+      ckey[r] = c < ctot ? clist[rr][cpos[r]] : 0;
       ex[r] = 0.f;
     }
     sweep([&](int, int dl) {
-      for (int dd = 0; dd < dl; dd += V) {
-        const U8<E> qv = __builtin_bit_cast(U8<E>, *reinterpret_cast<const uint4*>(qtile + rl * RS + dd));
-        float x[V];
 #pragma unroll
-        for (int e = 0; e < V; ++e) x[e] = ET<E>::to_f(qv.e[e]);
+      for (int r = 0; r < WS_ROUNDS; ++r) {
+        if (pass0 + WR_THREADS * r + 64 * w < ctot) {  // wave-uniform: a candidate in this wave
+          const raw* qr = qtile + crow[r] * RS;
+          const raw* kr = ktile + ckey[r] * RS;
+          for (int dd = 0; dd < dl; dd += V) {
+            const U8<E> qv = __builtin_bit_cast(U8<E>, *reinterpret_cast<const uint4*>(qr + dd));
+            const U8<E> kv = __builtin_bit_cast(U8<E>, *reinterpret_cast<const uint4*>(kr + dd));
 #pragma unroll
-        for (int r = 0; r < WS_RMAX; ++r) {
-          if (r < nr) {
-            const U8<E> kv = __builtin_bit_cast(U8<E>, *reinterpret_cast<const uint4*>(ktile + ck[r] * RS + dd));
-#pragma unroll
-            for (int e = 0; e < V; ++e) ex[r] = fmaf(x[e], ET<E>::to_f(kv.e[e]), ex[r]);
+            for (int e = 0; e < V; ++e) ex[r] = fmaf(ET<E>::to_f(qv.e[e]), ET<E>::to_f(kv.e[e]), ex[r]);
           }
         }
       }
     });
 #pragma unroll
-    for (int r = 0; r < WS_RMAX; ++r)
-      if (r < nr) sc[rl][c0 + WR_LANES * r] = ex[r] * a.scale;
+    for (int r = 0; r < WS_ROUNDS; ++r)
+      if (pass0 + WR_THREADS * r + tid < ctot) sc[crow[r]][cpos[r]] = ex[r] * a.scale;
   }
-  __syncthreads();  // every candidate's exact score in sc, in candidate order
+  __syncthreads();  // every candidate's exact score in sc, in candidate order; ktile free
 
-  // ---- 4. slots: index order in a short window, else the rank among the row's
-  // candidates (a key that is not a candidate is beaten by k keys, so it beats
-  // no key of the top k and changes none of their ranks).
+  // ---- 4. slots in the key tile's memory.
+  float (*out_s)[32] = reinterpret_cast<float (*)[32]>(ktile);
+  int (*out_i)[32] = reinterpret_cast<int (*)[32]>(reinterpret_cast<unsigned char*>(ktile) + WR_ROWS * 32 * sizeof(float));
+  for (int m = tid; m < WR_ROWS * 32; m += WR_THREADS) {
+    out_s[m / 32][m % 32] = -INFINITY;
+    out_i[m / 32][m % 32] = -1;
+  }
+  __syncthreads();
   if (active) {
     for (int c = lane; c < total; c += WR_LANES) {
       const int kl = clist[rl][c];
