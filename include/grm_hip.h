@@ -294,6 +294,18 @@ int grm_hip_residual_layer_norm(const void* x, const void* residual, const void*
                                 float eps, void* stream);
 
 /*
+ * Archive form of float32 states: out[i] = storage(model(states[i])), each
+ * value rounded (to nearest even) to model_dtype and then to storage_dtype,
+ * which is what push() stores for a state the model computed
+ *   (reference grm/core/paper_grm.py:139-140: the model's state, then
+ *   .to(memory_storage_dtype)); the reference runs it as two torch casts.
+ * n elements, any dtype pair; a float32 model dtype is the identity step.
+ * Limits: 16-byte aligned buffers.  ABI 106.
+ */
+int grm_hip_archive_cast(const float* states, void* out, int64_t n, int model_dtype, int storage_dtype,
+                         void* stream);
+
+/*
  * Segment routing: dot-product score, top-k and softmax gates.
  *   score[b, q, s] = scale * sum_d queries[b, q, d] * keys[b, s, d]
  * Each score is one float32 fused multiply-add chain over d = 0 .. dim-1 in

@@ -90,9 +90,12 @@ class _Ring:
             memories, summaries = memories[:, n - self.capacity:], summaries[:, n - self.capacity:]
             self.head = (self.head + n - self.capacity) % self.capacity
             n = self.capacity
-        slots = (torch.arange(n, device=memories.device) + self.head) % self.capacity
-        self.memories.index_copy_(1, slots, memories.to(self.memories.dtype))
-        self.summaries.index_copy_(1, slots, summaries.to(self.summaries.dtype))
+        # The slots head .. head + n - 1 (mod capacity) are at most two runs: two slice copies.
+        first = min(n, self.capacity - self.head)
+        for dst, src in ((self.memories, memories), (self.summaries, summaries)):
+            dst[:, self.head:self.head + first].copy_(src[:, :first])
+            if first < n:
+                dst[:, :n - first].copy_(src[:, first:])
         self.head = (self.head + n) % self.capacity
         self.count = min(self.capacity, self.count + n)
 

@@ -46,6 +46,7 @@ SIGNATURES = {
     "grm_hip_gather_apply_bwd_tokens": (_C, [_P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _C, _P, _P]),
     "grm_hip_project_split": (_C, [_P, _P, _P, _P, _P, _I, _I, _I, _I, _C, ctypes.c_float, _P]),
     "grm_hip_residual_layer_norm": (_C, [_P, _P, _P, _P, _P, _I, _I, _C, _C, ctypes.c_float, _P]),
+    "grm_hip_archive_cast": (_C, [_P, _P, _I, _C, _C, _P]),
     "grm_hip_retrieve_fuse": (_C, [_P, _P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _C, _C, _C,
                                    ctypes.c_float, _P, _P]),
     "grm_hip_topk_route": (_C, [_P, _P, _P, _P, _P, _I, _I, _I, _I, _C, _I, ctypes.c_float, ctypes.c_float, _P]),
@@ -298,6 +299,15 @@ def residual_layer_norm(x, residual, weight=None, bias=None, eps: float = 1e-5, 
                                             int(x.numel() // H) if H else 0, H, dtype_code(x.dtype), pd, float(eps),
                                             _stream(x))
     _check(rc, "grm_hip_residual_layer_norm")
+    return out
+
+
+def archive_cast(states, model_dtype, storage_dtype, out=None):
+    """float32 states rounded to model_dtype, then to storage_dtype (the archive's stored form)."""
+    out = torch.empty(states.shape, dtype=storage_dtype, device=states.device) if out is None else out
+    rc = load().grm_hip_archive_cast(_ptr(states), _ptr(out), int(states.numel()), dtype_code(model_dtype),
+                                     dtype_code(storage_dtype), _stream(states))
+    _check(rc, "grm_hip_archive_cast")
     return out
 
 

@@ -9,8 +9,9 @@
 // grows), fuse_residual, gather_apply (gather + query application without
 // materialising the states), retrieve_fuse (gather_apply, the gate-weighted
 // sum and fuse_residual in one call), the layer glue project_split (the
-// projection's split with L2-normalised keys and queries) and
-// residual_layer_norm (the block's LayerNorm(out + x)), and three gradients
+// projection's split with L2-normalised keys and queries),
+// residual_layer_norm (the block's LayerNorm(out + x)) and archive_cast (the
+// archive's stored form of float32 states), and three gradients
 // without gathered states: apply_query_backward_queries,
 // gather_apply_backward_queries (one gradient row per pair) and
 // gather_apply_backward_tokens (one row per query, shared by its routes).
@@ -460,6 +461,13 @@ Tensor residual_layer_norm_generic(const Tensor& x, const Tensor& residual, cons
   TORCH_CHECK(x.sizes() == residual.sizes() && x.dim() >= 1, "residual_layer_norm: x and residual must match");
   return at::layer_norm(x + residual, {x.size(-1)}, weight.has_value() ? *weight : Tensor(),
                         bias.has_value() ? *bias : Tensor(), eps);
+}
+
+// archive_cast: float32 states rounded to the model dtype, then to the storage
+// dtype, as push() stores them (paper_grm.py:139-140).
+Tensor archive_cast_generic(const Tensor& states, at::ScalarType model_dtype, at::ScalarType storage_dtype) {
+  TORCH_CHECK(states.scalar_type() == at::kFloat, "archive_cast: states must be float32");
+  return states.to(model_dtype).to(storage_dtype);
 }
 
 // ---------------------------------------------------------------------------
@@ -1041,6 +1049,21 @@ std::tuple<Tensor, Tensor, Tensor, Tensor> chunk_update_backward_cpu(
 }
 
 }  // namespace
+Tensor archive_cast_hip(const Tensor& states, at::ScalarType model_dtype, at::ScalarType storage_dtype) {
+  TORCH_CHECK(states.scalar_type() == at::kFloat, "archive_cast: states must be float32");
+  const int md = dtype_code(model_dtype), sd = dtype_code(storage_dtype);
+  Tensor x = states.contiguous();
+  if (md < 0 || sd < 0 || !states.is_cuda() || !aligned16(x)) {
+    if (states.is_cuda()) g_generic_calls.fetch_add(1);
+    return archive_cast_generic(states, model_dtype, storage_dtype);
+  }
+  c10::OptionalDeviceGuard guard(states.device());
+  Tensor out = at::empty(x.sizes(), x.options().dtype(storage_dtype));
+  check_rc(grm_hip_archive_cast(x.data_ptr<float>(), out.data_ptr(), x.numel(), md, sd, current_stream(x)),
+           "archive_cast");
+  return out;
+}
+
 }  // namespace grm
 
 TORCH_LIBRARY(grm_cuda, m) {
@@ -1060,6 +1083,7 @@ TORCH_LIBRARY(grm_cuda, m) {
   m.def("gather_apply_backward_queries(Tensor memories, Tensor indices, Tensor grad_out, Tensor queries) -> Tensor");
   m.def("gather_apply_backward_tokens(Tensor memories, Tensor indices, Tensor grad_tokens) -> Tensor");
   m.def("residual_layer_norm(Tensor x, Tensor residual, Tensor? weight, Tensor? bias, float eps) -> Tensor");
+  m.def("archive_cast(Tensor states, ScalarType model_dtype, ScalarType storage_dtype) -> Tensor");
 }
 
 TORCH_LIBRARY_IMPL(grm_cuda, CPU, m) {
@@ -1079,6 +1103,7 @@ TORCH_LIBRARY_IMPL(grm_cuda, CPU, m) {
   m.impl("gather_apply_backward_queries", grm::gather_apply_backward_queries_generic);
   m.impl("gather_apply_backward_tokens", grm::gather_apply_backward_tokens_generic);
   m.impl("residual_layer_norm", grm::residual_layer_norm_generic);
+  m.impl("archive_cast", grm::archive_cast_generic);
 }
 
 TORCH_LIBRARY_IMPL(grm_cuda, CUDA, m) {
@@ -1098,6 +1123,7 @@ TORCH_LIBRARY_IMPL(grm_cuda, CUDA, m) {
   m.impl("gather_apply_backward_queries", grm::gather_apply_backward_queries_hip);
   m.impl("gather_apply_backward_tokens", grm::gather_apply_backward_tokens_hip);
   m.impl("residual_layer_norm", grm::residual_layer_norm_hip);
+  m.impl("archive_cast", grm::archive_cast_hip);
 }
 
 PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {

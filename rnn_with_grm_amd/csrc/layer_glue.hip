@@ -9,6 +9,9 @@
 //                        contiguous keys and queries L2-normalised, values and extra.
 //   residual_layer_norm  LayerNorm(x + residual), SegmentRecurrentMemoryLayer's
 //                        block output (grm/core/multilayer_grm.py:92-97).
+//   archive_cast         float32 states rounded to the model dtype and then to the
+//                        archive's storage dtype (push(), grm/core/paper_grm.py:
+//                        139-140), one pass instead of two casts.
 //
 // Both follow the rounding of the torch ops they replace for 16-bit rows: the
 // norm and its eps clamp are rounded to the row dtype before the division
@@ -17,6 +20,8 @@
 // One wavefront per row, 16-byte accesses.
 #include <stdint.h>
 #include <string.h>
+
+#include <algorithm>
 
 #include "grm_hip.h"
 #include "grm_hip_common.h"
@@ -199,6 +204,36 @@ __global__ __launch_bounds__(GL_THREADS) void residual_layer_norm_kernel(const R
 
 bool aligned16(const void* p) { return reinterpret_cast<uintptr_t>(p) % 16 == 0; }
 
+// archive_cast: float32 states in the form the archive stores them, rounded
+// to the model dtype and then to the storage dtype, as push() stores a state
+// the model computed (reference grm/core/paper_grm.py:139-140: the state in
+// the model's dtype, then memory_storage_dtype).  One read, one write.
+template <class M, class St>
+__global__ __launch_bounds__(GL_THREADS) void archive_cast_kernel(const float* __restrict__ src,
+                                                                  typename ET<St>::raw* __restrict__ dst,
+                                                                  int64_t n) {
+  using raw = typename ET<St>::raw;
+  auto cvt = [](float f) -> raw { return ET<St>::from_f(ET<M>::to_f(ET<M>::from_f(f))); };
+  const int64_t n8 = n / 8;
+  const int64_t stride = static_cast<int64_t>(gridDim.x) * GL_THREADS;
+  const int64_t t0 = static_cast<int64_t>(blockIdx.x) * GL_THREADS + threadIdx.x;
+  for (int64_t i = t0; i < n8; i += stride) {
+    const float4 a = reinterpret_cast<const float4*>(src)[2 * i];
+    const float4 b = reinterpret_cast<const float4*>(src)[2 * i + 1];
+    const float f[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+    if constexpr (sizeof(raw) == 2) {
+      raw r[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) r[e] = cvt(f[e]);
+      reinterpret_cast<uint4*>(dst)[i] = __builtin_bit_cast(uint4, r);
+    } else {
+      reinterpret_cast<float4*>(dst)[2 * i] = make_float4(cvt(f[0]), cvt(f[1]), cvt(f[2]), cvt(f[3]));
+      reinterpret_cast<float4*>(dst)[2 * i + 1] = make_float4(cvt(f[4]), cvt(f[5]), cvt(f[6]), cvt(f[7]));
+    }
+  }
+  for (int64_t i = 8 * n8 + t0; i < n; i += stride) dst[i] = cvt(src[i]);
+}
+
 }  // namespace
 }  // namespace grmhip
 
@@ -312,4 +347,52 @@ extern "C" int grm_hip_residual_layer_norm(const void* x, const void* residual, 
     default: go(BF16{}); break;
   }
   return check_launch("residual_layer_norm");
+}
+
+extern "C" int grm_hip_archive_cast(const float* states, void* out, int64_t n, int model_dtype, int storage_dtype,
+                                    void* stream) {
+  if (n < 0) {
+    set_error("archive_cast: negative size");
+    return GRM_HIP_EINVAL;
+  }
+  if (model_dtype < GRM_HIP_F32 || model_dtype > GRM_HIP_BF16 || storage_dtype < GRM_HIP_F32 ||
+      storage_dtype > GRM_HIP_BF16) {
+    set_error("archive_cast: unsupported dtypes %d / %d", model_dtype, storage_dtype);
+    return GRM_HIP_EUNSUPPORTED;
+  }
+  if (n == 0) return GRM_HIP_OK;
+  if (states == nullptr || out == nullptr) {
+    set_error("archive_cast: null pointer");
+    return GRM_HIP_EINVAL;
+  }
+  if (!aligned16(states) || !aligned16(out)) {
+    set_error("archive_cast: buffers must be 16-byte aligned");
+    return GRM_HIP_EUNSUPPORTED;
+  }
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const int64_t groups = (n + 7) / 8;
+  const dim3 grid(static_cast<unsigned>(std::min<int64_t>((groups + GL_THREADS - 1) / GL_THREADS, 4096)));
+  auto go = [&](auto mt) {
+    using M = decltype(mt);
+    switch (storage_dtype) {
+      case GRM_HIP_F32:
+        hipLaunchKernelGGL((archive_cast_kernel<M, F32>), grid, dim3(GL_THREADS), 0, s, states,
+                           static_cast<float*>(out), n);
+        break;
+      case GRM_HIP_F16:
+        hipLaunchKernelGGL((archive_cast_kernel<M, F16>), grid, dim3(GL_THREADS), 0, s, states,
+                           static_cast<uint16_t*>(out), n);
+        break;
+      default:
+        hipLaunchKernelGGL((archive_cast_kernel<M, BF16>), grid, dim3(GL_THREADS), 0, s, states,
+                           static_cast<uint16_t*>(out), n);
+        break;
+    }
+  };
+  switch (model_dtype) {
+    case GRM_HIP_F32: go(F32{}); break;
+    case GRM_HIP_F16: go(F16{}); break;
+    default: go(BF16{}); break;
+  }
+  return check_launch("archive_cast");
 }

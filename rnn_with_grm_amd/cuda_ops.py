@@ -39,7 +39,7 @@ SCHEMA_OPS = (
 )
 EXTRA_OPS = ("segment_scan_forward", "topk_route", "fuse_residual", "gather_apply", "segment_route",
              "retrieve_fuse", "project_split", "residual_layer_norm", "gather_apply_backward_queries",
-             "gather_apply_backward_tokens", "apply_query_backward_queries")
+             "gather_apply_backward_tokens", "apply_query_backward_queries", "archive_cast")
 
 # Environment variables of the reference (cuda_ops.py:26-32): one per op and a global one.
 GLOBAL_POLICY_ENV = "GRM_CUDA_KERNEL_POLICY"
@@ -584,6 +584,16 @@ def cuda_retrieve_fuse(memories_per_batch: Tensor, topk_indices: Tensor, queries
                                None if bias is None else bias.float(), eps, enabled=enabled,
                                debug_fallback=debug_fallback)
     return fused.reshape(B, Q, H).to(h_online.dtype)
+
+
+def cuda_archive_cast(states: Tensor, model_dtype: torch.dtype, storage_dtype: torch.dtype, *,
+                      enabled: bool = True, debug_fallback: bool = False) -> Tensor:
+    """float32 states as the archive stores them: rounded to the model dtype, then to the
+    storage dtype (push() storing the model's state, paper_grm.py:139-140), in one pass."""
+    if states.dtype == torch.float32 and _run_native("archive_cast", states.device, enabled=enabled,
+                                                     debug_fallback=debug_fallback):
+        return torch.ops.grm_cuda.archive_cast(states, model_dtype, storage_dtype)
+    return states.to(model_dtype).to(storage_dtype)
 
 
 def cuda_project_split(proj: Tensor, key_dim: int, value_dim: int, extra_dim: int = 0, eps: float = 1e-6, *,

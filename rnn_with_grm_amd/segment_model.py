@@ -674,7 +674,8 @@ class SegmentRecurrentMemoryModel(nn.Module):
         # passes no gradient back into the scan or the summaries' inputs.
         bank = self.memory_bank
         storage = bank.memory_storage_dtype
-        new_states = snaps.detach().to(dtype).to(storage)  # what push() stores, converted once
+        new_states = cuda_ops.cuda_archive_cast(snaps.detach(), dtype, storage,
+                                                debug_fallback=self.cuda_cpp_debug_fallback)  # what push() stores
         new_summaries = _segment_means(x.detach(), seg).to(storage)
         ring = bank._groups.get(B)
         base = 0 if ring is None else len(ring)

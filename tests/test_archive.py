@@ -218,3 +218,25 @@ def test_recompute_rate_counters_mirrored_on_host():
     assert other.get_recompute_rate() == 0.25 and other._host_counts == [8, 2]
     other.clear()
     assert other._host_counts == [0, 0] and other.get_recompute_rate() == 0.0 and int(other.total_retrieved) == 0
+
+
+def test_push_segments_wraps_like_repeated_push():
+    """Whole-sequence pushes of ragged sizes whose slots wrap around the ring (two runs of
+    slots), and pushes longer than the capacity, keep the same ring as one push per segment."""
+    B, H, K, D, cap = 2, 4, 3, 5, 5
+    g = torch.Generator().manual_seed(9)
+    sizes = [3, 3, 1, 4, 7, 2, 5, 6]
+    total = sum(sizes)
+    mems, sums = torch.randn(B, total, H, K, generator=g), torch.randn(B, total, D, generator=g)
+    a = DeviceSegmentArchive(H, K, D, cap, torch.float16)
+    b = DeviceSegmentArchive(H, K, D, cap, torch.float16)
+    i0 = 0
+    for n in sizes:
+        a.push_segments(mems[:, i0:i0 + n], sums[:, i0:i0 + n])
+        for i in range(i0, i0 + n):
+            b.push(mems[:, i], sums[:, i], SegmentCheckpoint(torch.zeros(1), torch.zeros(1)))
+        i0 += n
+        sa, sb = a.get_extra_state()["groups"][B], b.get_extra_state()["groups"][B]
+        assert len(sa["memories"]) == len(sb["memories"]) == min(cap, i0)
+        assert all(torch.equal(x, y) for x, y in zip(sa["memories"], sb["memories"]))
+        assert all(torch.equal(x, y) for x, y in zip(sa["summaries"], sb["summaries"]))

@@ -324,3 +324,18 @@ def test_cpu_retrieve_fuse_training_function(monkeypatch, ln):
     torch.testing.assert_close(out.double(), ref.detach(), rtol=1e-5, atol=1e-5)
     for got, want in zip(grads, rgrads):
         torch.testing.assert_close(got.double(), want, rtol=1e-4, atol=1e-5)
+
+
+def test_cpu_archive_cast():
+    """archive_cast (CPU key and the cuda_ops wrapper) is the two torch casts, model dtype first."""
+    if not cuda_ops.load_grm_cuda_extension():
+        pytest.skip("extension not built")
+    g = torch.Generator().manual_seed(13)
+    x = torch.randn(3, 5, 7, generator=g) * 1e3
+    for md in (torch.float32, torch.bfloat16, torch.float16):
+        for sd in (torch.float32, torch.bfloat16, torch.float16):
+            want = x.to(md).to(sd)
+            assert torch.equal(torch.ops.grm_cuda.archive_cast(x, md, sd), want)
+            assert torch.equal(cuda_ops.cuda_archive_cast(x, md, sd), want)
+    with pytest.raises(RuntimeError, match="float32"):
+        torch.ops.grm_cuda.archive_cast(x.half(), torch.bfloat16, torch.float16)

@@ -91,3 +91,31 @@ def test_glue_ops_through_cuda_ops(dev):
     y2.sum().backward()
     assert xr.grad is not None and ln.weight.grad is not None
     torch.testing.assert_close(y, y2.detach(), rtol=1e-5, atol=1e-5)
+
+
+@pytest.mark.parametrize("n", [8 * 4096 + 5, 1, 7, 64 * 512 * 64 * 3])
+def test_archive_cast(dev, n):
+    """archive_cast (grm_hip_archive_cast) against torch's two casts, bit for bit, for every
+    (model dtype, storage dtype) pair: values that round differently through bfloat16 than
+    straight to float16, float16 overflow and underflow, zeros of both signs, infinities and
+    NaN; sizes with a ragged tail."""
+    g = torch.Generator().manual_seed(n % 1000)
+    x = torch.randn(n, generator=g) * torch.exp2(torch.randint(-30, 30, (n,), generator=g).float())
+    special = torch.tensor([0.0, -0.0, float("inf"), -float("inf"), float("nan"), 65520.0, 1e-8, -3e-41,
+                            1.0 + 2.0 ** -8 + 2.0 ** -12, 1.0 + 2.0 ** -9 + 2.0 ** -11])
+    x[: min(n, special.numel())] = special[: min(n, special.numel())]
+    print(f"archive_cast n={n}", flush=True)
+    xd = x.to(dev)
+    for md in (torch.float32, torch.bfloat16, torch.float16):
+        for sd in (torch.float32, torch.bfloat16, torch.float16):
+            want = x.to(md).to(sd)
+            got = capi.archive_cast(xd, md, sd)
+            op = torch.ops.grm_cuda.archive_cast(xd, md, sd)
+            torch.cuda.synchronize()
+            it = torch.int32 if sd == torch.float32 else torch.int16
+            wnan = want.float().isnan()
+            for out in (got.cpu(), op.cpu()):
+                # the bits of every value, and NaN where NaN (payloads may differ)
+                assert out.dtype == sd
+                assert torch.equal(out.float().isnan(), wnan), (md, sd)
+                assert torch.equal(out.view(it)[~wnan], want.view(it)[~wnan]), (md, sd)
