@@ -119,7 +119,9 @@ int grm_hip_chunk_update_fwd_noalloc(const void* keys, const void* values, const
  *   (caller-provided).  The scalar kernel keeps per 16-column value tile partial sums of
  *   grad_keys and grad_queries there; the MFMA kernels for 16-bit inputs keep the adjoint
  *   dL/dM at every 64-token chunk end, [batch, ceil(seq_len / 64), value_dim, key_dim], at
- *   its front (they run when that fits, from about ten tokens on).
+ *   its front (they run when that fits, from about ten tokens on), followed, when the walk
+ *   over the chunks runs in parts, by each part's adjoint at its start
+ *   [batch, parts, value_dim, key_dim].
  */
 int grm_hip_chunk_update_bwd(const void* grad_hidden, const void* grad_memory_out, const void* keys,
                              const void* values, const void* queries, const void* memory,

@@ -278,8 +278,15 @@ int launch_bwd(const BwdArgs& a, void* grad_keys, void* grad_queries, hipStream_
 //   dV = P^T dH + c decay^{L-1-j} K G^T
 //   G  <- decay^L G + dH^T diag(decay^{i+1}) Q      (the adjoint at the chunk's start)
 // Only the last line carries from chunk to chunk.  bwd_adjoint_kernel walks it
-// from the last chunk (one workgroup per sequence and 64 value rows, G in fp32
-// MFMA accumulators) and stores G at every chunk end.  bwd_grad_kernel then
+// backwards over one part of the chunks (one workgroup per sequence, 64 value
+// rows and part, G in fp32 MFMA accumulators) and stores G at every chunk end.
+// The recurrence is linear: a part walked from a zero adjoint gives local
+// values, and the true adjoint at the end of chunk ch of part p is
+// local(ch) + decay^(tokens from the end of ch to the end of p) B_p, B_p the
+// true adjoint at the part's end, B_p = start(p + 1) + decay^(tokens of p + 1)
+// B_(p+1), the last part starting from dL/dM_out.  bwd_adjoint_join_kernel
+// forms the B_p and bwd_adjoint_fix_kernel adds those terms (parts walked in
+// parallel: sequences x value tiles alone are 32 workgroups at config 4).  bwd_grad_kernel then
 // takes one (sequence, chunk) per workgroup and all of its value columns, in
 // 32-column tiles: dQ and dK are summed over the whole value dimension in
 // registers and written once, dV tile by tile, so there are no partial sums to
@@ -303,6 +310,7 @@ struct BwdMArgs {
   const void* memory;
   const float* states;  // [B, n_chunks, dv, dk] state after each chunk
   float* gbuf;          // [B, n_chunks, dv, dk] adjoint at each chunk's end
+  float* lstart;        // [B, n_parts, dv, dk] each part's local adjoint at its start (n_parts > 1)
   void* dq_out;
   void* dk_out;
   void* dv_out;
@@ -312,6 +320,8 @@ struct BwdMArgs {
   int dk;
   int dv;
   int n_chunks;
+  int n_parts;          // parts of the adjoint walk
+  int cpp;              // chunks per part (the last part may hold fewer)
   int mem_f32;
   int xcd_remap;
   float c;
@@ -406,7 +416,10 @@ __global__ __launch_bounds__(MB_NT) void bwd_adjoint_kernel(const BwdMArgs a) {
     wg = (wg & 7) * per + (wg >> 3);
   }
   const int tile = wg % vtiles;
-  const int64_t b = wg / vtiles;
+  const int part = (wg / vtiles) % a.n_parts;
+  const int64_t b = wg / vtiles / a.n_parts;
+  const int c0 = part * a.cpp, c1 = min(a.n_chunks, c0 + a.cpp);  // chunks [c0, c1)
+  const bool last_part = part == a.n_parts - 1;
   const int v0 = tile * AJ_V;
   const int dk = a.dk, dv = a.dv;
   const int64_t T = a.T;
@@ -422,8 +435,11 @@ __global__ __launch_bounds__(MB_NT) void bwd_adjoint_kernel(const BwdMArgs a) {
   };
   f32x4 gacc[KT];
   {
+    // The last part's walk starts from dL/dM_out, earlier parts' from zero: a
+    // zero-sized buffer for them, whose loads return zeros (no branch here; the
+    // branch cost the walk its load scheduling, 72 -> 89 us at config 2).
     const __amdgpu_buffer_rsrc_t rg = make_rsrc(static_cast<const unsigned char*>(a.dmo) + b * dv * dk * mem_b,
-                                                static_cast<uint32_t>(dv * dk * mem_b));
+                                                last_part ? static_cast<uint32_t>(dv * dk * mem_b) : 0u);
 #pragma unroll
     for (int t = 0; t < KT; ++t) {
       const int off = g_off(t);
@@ -486,11 +502,11 @@ __global__ __launch_bounds__(MB_NT) void bwd_adjoint_kernel(const BwdMArgs a) {
   // (Loading two chunks ahead, in two register stages, measured slower: 84
   // against 71 us at config 2.)
   Stage stage;
-  load_chunk(a.n_chunks - 1, stage);
-  for (int ch = a.n_chunks - 1; ch >= 0; --ch) {
+  load_chunk(c1 - 1, stage);
+  for (int ch = c1 - 1; ch >= c0; --ch) {
     const int L = ch == a.n_chunks - 1 ? last_len : BCT;
     store_chunk(stage);
-    if (ch > 0) load_chunk(ch - 1, stage);
+    if (ch > c0) load_chunk(ch - 1, stage);
     __syncthreads();  // chunk in LDS
     {
       // the adjoint at this chunk's end, for bwd_grad_kernel
@@ -529,6 +545,17 @@ __global__ __launch_bounds__(MB_NT) void bwd_adjoint_kernel(const BwdMArgs a) {
     }
     __syncthreads();  // every read of this chunk's tiles done
   }
+  if (a.n_parts > 1) {
+    // the part's local adjoint at its start, for bwd_adjoint_fix_kernel
+    const __amdgpu_buffer_rsrc_t rl =
+        make_rsrc(a.lstart + (b * a.n_parts + part) * dv * dk, static_cast<uint32_t>(dv * dk * 4));
+#pragma unroll
+    for (int t = 0; t < KT; ++t) {
+      const int off = g_off(t);
+      buf_store4<F32>(rl, off < 0 ? kBufOOB : off * 4, gacc[t]);
+    }
+    return;
+  }
   // grad_memory: the adjoint at the sequence's start.
   const __amdgpu_buffer_rsrc_t ro = make_rsrc(static_cast<unsigned char*>(a.dm_out) + b * dv * dk * mem_b,
                                               static_cast<uint32_t>(dv * dk * mem_b));
@@ -541,6 +568,98 @@ __global__ __launch_bounds__(MB_NT) void bwd_adjoint_kernel(const BwdMArgs a) {
       buf_store4<E>(ro, off < 0 ? kBufOOB : off * ES, gacc[t]);
     }
   }
+}
+
+// The walked parts joined (n_parts > 1), two launches.  Thread t of a
+// workgroup owns float4 columns of one 64-row value tile; no LDS.
+struct AjTile {
+  static constexpr int UMAX = AJ_V * 128 / 4 / MB_NT;  // float4 units per thread at key_dim 128
+  int off[UMAX];
+  __device__ AjTile(int v0, int dv, int dk) {
+    const int qpr = dk / 4;  // dk is a multiple of 8
+#pragma unroll
+    for (int i = 0; i < UMAX; ++i) {
+      const int u = threadIdx.x + MB_NT * i;
+      const int v = v0 + u / qpr;
+      off[i] = (u < AJ_V * qpr && v < dv) ? v * dk + 4 * (u % qpr) : -1;
+    }
+  }
+  __device__ float4 ld(const float* base, int i) const {
+    return off[i] < 0 ? make_float4(0.f, 0.f, 0.f, 0.f) : *reinterpret_cast<const float4*>(base + off[i]);
+  }
+};
+
+__device__ __forceinline__ float4 axpy4(float4 x, float f, float4 y) {  // x + f y
+  return make_float4(x.x + f * y.x, x.y + f * y.y, x.z + f * y.z, x.w + f * y.w);
+}
+
+// Join: workgroup (sequence, value tile) turns the local starts into the parts'
+// boundary adjoints in place, slot p + 1 := B_p = start(p + 1) + decay^(64 cpp)
+// B_(p+1) for p = n_parts - 3 .. 0 (slot n_parts - 1 already is B_(n_parts-2):
+// the last part started from dL/dM_out), then writes grad_memory = start(0) +
+// decay^(64 cpp) B_0.  Every part but the last holds cpp full chunks.
+__global__ __launch_bounds__(MB_NT) void bwd_adjoint_join_kernel(const BwdMArgs a, int mem_dtype) {
+  const int vtiles = (a.dv + AJ_V - 1) / AJ_V;
+  const int tile = blockIdx.x % vtiles;
+  const int64_t b = blockIdx.x / vtiles;
+  const int dk = a.dk, dv = a.dv;
+  const AjTile tl(tile * AJ_V, dv, dk);
+  float f = 1.f;
+  for (int c = 0; c < a.cpp; ++c) f *= a.pw[BCT];
+  float* ls = a.lstart + b * a.n_parts * dv * dk;
+  float4 bt[AjTile::UMAX];
+#pragma unroll
+  for (int i = 0; i < AjTile::UMAX; ++i) bt[i] = tl.ld(ls + (a.n_parts - 1) * dv * dk, i);
+  for (int q = a.n_parts - 2; q >= 1; --q) {
+#pragma unroll
+    for (int i = 0; i < AjTile::UMAX; ++i) {
+      bt[i] = axpy4(tl.ld(ls + q * dv * dk, i), f, bt[i]);
+      if (tl.off[i] >= 0) *reinterpret_cast<float4*>(ls + q * dv * dk + tl.off[i]) = bt[i];
+    }
+  }
+  unsigned char* dm = static_cast<unsigned char*>(a.dm_out) + b * dv * dk * (a.mem_f32 ? 4 : 2);
+#pragma unroll
+  for (int i = 0; i < AjTile::UMAX; ++i) {
+    if (tl.off[i] < 0) continue;
+    const float4 y = axpy4(tl.ld(ls, i), f, bt[i]);
+    if (a.mem_f32) {
+      *reinterpret_cast<float4*>(reinterpret_cast<float*>(dm) + tl.off[i]) = y;
+    } else {
+      uint16_t* o = reinterpret_cast<uint16_t*>(dm) + tl.off[i];
+      if (mem_dtype == GRM_HIP_F16) {
+        o[0] = ET<F16>::from_f(y.x); o[1] = ET<F16>::from_f(y.y); o[2] = ET<F16>::from_f(y.z); o[3] = ET<F16>::from_f(y.w);
+      } else {
+        o[0] = ET<BF16>::from_f(y.x); o[1] = ET<BF16>::from_f(y.y); o[2] = ET<BF16>::from_f(y.z); o[3] = ET<BF16>::from_f(y.w);
+      }
+    }
+  }
+}
+
+// Fix-up: workgroup (sequence, value tile, chunk ch of parts 0 .. n_parts - 2)
+// adds decay^(64 (c1 - 1 - ch)) B_p to the adjoint stored at the end of ch
+// (part p = ch / cpp ends at chunk c1 - 1 = (p + 1) cpp - 1; B_p in slot p + 1).
+__global__ __launch_bounds__(MB_NT) void bwd_adjoint_fix_kernel(const BwdMArgs a) {
+  const int vtiles = (a.dv + AJ_V - 1) / AJ_V;
+  const int nfix = (a.n_parts - 1) * a.cpp;
+  const int tile = blockIdx.x % vtiles;
+  const int ch = (blockIdx.x / vtiles) % nfix;
+  const int64_t b = blockIdx.x / vtiles / nfix;
+  const int dk = a.dk, dv = a.dv;
+  const int part = ch / a.cpp;
+  const AjTile tl(tile * AJ_V, dv, dk);
+  float f = 1.f;
+  for (int c = ch; c < (part + 1) * a.cpp - 1; ++c) f *= a.pw[BCT];
+  const float* bp = a.lstart + (b * a.n_parts + part + 1) * dv * dk;
+  float* gb = a.gbuf + (b * a.n_chunks + ch) * dv * dk;
+  float4 x[AjTile::UMAX], y[AjTile::UMAX];
+#pragma unroll
+  for (int i = 0; i < AjTile::UMAX; ++i) {
+    x[i] = tl.ld(gb, i);
+    y[i] = tl.ld(bp, i);
+  }
+#pragma unroll
+  for (int i = 0; i < AjTile::UMAX; ++i)
+    if (tl.off[i] >= 0) *reinterpret_cast<float4*>(gb + tl.off[i]) = axpy4(x[i], f, y[i]);
 }
 
 // The gradients of one chunk from its starting state and the adjoint at its end.
@@ -842,17 +961,28 @@ int allow_lds(K* fn, size_t bytes, bool& done) {
 }
 
 template <class E, int DKP>
-int launch_bwd_mfma(BwdMArgs a, hipStream_t s) {
+int launch_bwd_mfma(BwdMArgs a, int mem_dtype, hipStream_t s) {
   static bool attr_a = false, attr_g = false;
   int rc = allow_lds(&bwd_adjoint_kernel<E, DKP>, AjShape<DKP>::lds_bytes, attr_a);
   if (rc == GRM_HIP_OK) rc = allow_lds(&bwd_grad_kernel<E, DKP>, GrShape<DKP>::lds_bytes, attr_g);
   if (rc != GRM_HIP_OK) return rc;
-  const int64_t grid_a = a.batch * ((a.dv + AJ_V - 1) / AJ_V);
+  const int64_t grid_a = a.batch * ((a.dv + AJ_V - 1) / AJ_V) * a.n_parts;
   a.xcd_remap = (grid_a % 8 == 0) ? 1 : 0;
   hipLaunchKernelGGL((bwd_adjoint_kernel<E, DKP>), dim3(static_cast<unsigned>(grid_a)), dim3(MB_NT),
                      AjShape<DKP>::lds_bytes, s, a);
   rc = check_launch("chunk_update_bwd(adjoint)");
   if (rc != GRM_HIP_OK) return rc;
+  if (a.n_parts > 1) {
+    const int64_t vt = (a.dv + AJ_V - 1) / AJ_V;
+    hipLaunchKernelGGL(bwd_adjoint_join_kernel, dim3(static_cast<unsigned>(a.batch * vt)), dim3(MB_NT), 0, s, a,
+                       mem_dtype);
+    rc = check_launch("chunk_update_bwd(adjoint join)");
+    if (rc != GRM_HIP_OK) return rc;
+    const int64_t grid_f = a.batch * vt * (a.n_parts - 1) * a.cpp;
+    hipLaunchKernelGGL(bwd_adjoint_fix_kernel, dim3(static_cast<unsigned>(grid_f)), dim3(MB_NT), 0, s, a);
+    rc = check_launch("chunk_update_bwd(adjoint fix-up)");
+    if (rc != GRM_HIP_OK) return rc;
+  }
   const int64_t grid_g = a.batch * a.n_chunks;
   hipLaunchKernelGGL((bwd_grad_kernel<E, DKP>), dim3(static_cast<unsigned>(grid_g)), dim3(MB_NT),
                      GrShape<DKP>::lds_bytes, s, a);
@@ -953,6 +1083,24 @@ extern "C" int grm_hip_chunk_update_bwd(const void* grad_hidden, const void* gra
     m.memory = memory;
     m.states = chunk_states;
     m.gbuf = dkq_partial;
+    // Parts of the adjoint walk when sequences x value tiles are fewer than 128
+    // workgroups: enough for the chip (about 256), at least 4 chunks a part,
+    // their local starts after the chunk-end adjoints in dkq_partial (within its
+    // documented size).  (At config 2, 128 workgroups, two parts plus the join
+    // took longer than one walk.)
+    {
+      const int64_t vt = (value_dim + AJ_V - 1) / AJ_V;
+      int64_t parts = batch * vt >= 128 ? 1 : std::min<int64_t>((256 + batch * vt - 1) / (batch * vt), n_chunks / 4);
+      parts = std::max<int64_t>(parts, 1);
+      const int64_t cpp = (n_chunks + parts - 1) / parts;
+      parts = (n_chunks + cpp - 1) / cpp;
+      const bool fits = (n_chunks + parts) * value_dim <= 2 * ((value_dim + RB - 1) / RB) * seq_len &&
+                        batch * vt * n_chunks <= INT32_MAX;
+      const char* penv = getenv("GRM_HIP_BWD_PARTS");
+      m.n_parts = (fits && (penv == nullptr || penv[0] != '0')) ? static_cast<int>(parts) : 1;
+      m.cpp = m.n_parts > 1 ? static_cast<int>(cpp) : static_cast<int>(n_chunks);
+      m.lstart = dkq_partial + batch * n_chunks * value_dim * key_dim;
+    }
     m.dq_out = grad_queries;
     m.dk_out = grad_keys;
     m.dv_out = grad_values;
@@ -966,9 +1114,9 @@ extern "C" int grm_hip_chunk_update_bwd(const void* grad_hidden, const void* gra
     m.c = static_cast<float>((1.0 - memory_decay) / std::sqrt(static_cast<double>(key_dim)));
     for (int i = 0; i <= BCT; ++i) m.pw[i] = static_cast<float>(std::pow(memory_decay, i));
     if (in_dtype == GRM_HIP_F16) {
-      return key_dim <= 64 ? launch_bwd_mfma<F16, 64>(m, s) : launch_bwd_mfma<F16, 128>(m, s);
+      return key_dim <= 64 ? launch_bwd_mfma<F16, 64>(m, mem_dtype, s) : launch_bwd_mfma<F16, 128>(m, mem_dtype, s);
     }
-    return key_dim <= 64 ? launch_bwd_mfma<BF16, 64>(m, s) : launch_bwd_mfma<BF16, 128>(m, s);
+    return key_dim <= 64 ? launch_bwd_mfma<BF16, 64>(m, mem_dtype, s) : launch_bwd_mfma<BF16, 128>(m, mem_dtype, s);
   }
 
   BwdArgs a;

@@ -359,10 +359,12 @@ class _GatherApplyFn(torch.autograd.Function):
 class _RetrieveFuseFn(torch.autograd.Function):
     """Training form of the fused retrieval, LN(h + sum_r g_r M[idx_r] q) with float32
     arithmetic (the retriever's gather + apply, paper_grm.py:227-229,301-313, then the
-    aggregator's residual fusion, aggregator.py:67-145).  Forward: the float32 rows, then
-    fuse_residual without LayerNorm weights (x = h + sum_r g_r rows_r in one pass over the
-    rows), then LayerNorm; only x ([B, Q, H] float32) and LayerNorm's mean and 1/std are kept,
-    not the [B, Q, R, H] rows.  Backward: LayerNorm's gradient dx, then per pair
+    aggregator's residual fusion, aggregator.py:67-145).  Forward: x = h + sum_r g_r rows_r
+    in float32, then LayerNorm; only x ([B, Q, H] float32) and LayerNorm's mean and 1/std are
+    kept, not the [B, Q, R, H] rows.  A 16-bit model (16-bit h and queries) takes x from
+    retrieve_fuse without LayerNorm weights, whose rows are row-scaled float16 (rounding 2^-11
+    of each row's largest value, as at inference); a float32 model takes the float32 rows of
+    gather_apply and fuse_residual's weighted sum.  Backward: LayerNorm's gradient dx, then per pair
     u_r = M[idx_r]^T dx (gather_apply_backward_tokens, one dx row per query shared by its
     routes), dq = sum_r g_r u_r (fuse_residual again, on zero rows) and dg_r = u_r . q.  The
     memories get no gradient (a detached archive)."""
@@ -380,10 +382,15 @@ class _RetrieveFuseFn(torch.autograd.Function):
         B, Q, H = h_online.shape
         R = indices.size(-1)
         gf = gates.float().reshape(B * Q, R).contiguous()
-        rows = torch.ops.grm_cuda.gather_apply(memories, indices, queries, torch.float32)  # [B, Q, R, H]
-        x = _RetrieveFuseFn._weighted_sum(h_online.float().reshape(B * Q, H), rows.reshape(B * Q, R, H), gf)
-        del rows
-        x = x.reshape(B, Q, H)
+        q16 = queries.dtype == torch.bfloat16 or (queries.dtype == torch.float16 and memories.dtype == torch.float16)
+        if q16 and h_online.dtype in (torch.bfloat16, torch.float16):
+            x = torch.ops.grm_cuda.retrieve_fuse(memories, indices, queries, gf.view(B, Q, R), h_online.float(),
+                                                 None, None, eps)
+        else:
+            rows = torch.ops.grm_cuda.gather_apply(memories, indices, queries, torch.float32)  # [B, Q, R, H]
+            x = _RetrieveFuseFn._weighted_sum(h_online.float().reshape(B * Q, H), rows.reshape(B * Q, R, H), gf)
+            del rows
+            x = x.reshape(B, Q, H)
         mean = rstd = None
         if weight is None:
             out = x

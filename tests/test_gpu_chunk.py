@@ -335,15 +335,16 @@ def close_elementwise(name, got, ref, rtol=2e-2, atol=2e-3):
 @pytest.mark.parametrize("dtype,mem_dtype", [(torch.bfloat16, torch.float32), (torch.float16, torch.float32),
                                              (torch.bfloat16, torch.bfloat16), (torch.float16, torch.float16)])
 @pytest.mark.parametrize("B,T,K,H", [(2, 300, 128, 128), (3, 129, 64, 64), (1, 640, 96, 96), (2, 64, 128, 32),
-                                     (1, 7, 128, 32), (1, 12, 128, 32), (2, 200, 32, 64), (1, 200, 64, 512)])
+                                     (1, 7, 128, 32), (1, 12, 128, 32), (2, 200, 32, 64), (1, 200, 64, 512),
+                                     (1, 2000, 64, 512), (2, 1000, 64, 96)])
 def test_mfma_backward(dev, monkeypatch, dtype, mem_dtype, B, T, K, H):
     """The chunk-parallel MFMA backward (16-bit inputs, value_dim a multiple of 32: the adjoint
     pass, then the per-chunk gradients over every value tile) against the double-precision
     oracle and against the scalar per-token kernel (GRM_HIP_BWD_MFMA=0), element by element at
     rtol 2e-2 / atol 2e-3: ragged last chunks, key widths below the padded 64/128, one to
     sixteen value tiles, a half-filled 64-row adjoint tile (96 values), one chunk (12 tokens),
-    and 7 tokens, where the adjoint buffer would not fit the workspace and the scalar kernel
-    runs."""
+    7 tokens, where the adjoint buffer would not fit the workspace and the scalar kernel runs,
+    and adjoint walks split into 2, 4 and 8 parts (640, 1000 and 2000 tokens)."""
     k, v, q, m = make_case(B, T, K, H, dtype, mem_dtype, seed=B * 13 + T)
     g = torch.Generator().manual_seed(7)
     dh = torch.randn(B, T, H, generator=g).to(dtype)
@@ -360,6 +361,34 @@ def test_mfma_backward(dev, monkeypatch, dtype, mem_dtype, B, T, K, H):
         assert torch.isfinite(x.float()).all(), name
         close_elementwise(name, x, r)
         close_elementwise(name + " vs scalar kernel", x, y.float().cpu().double().numpy())
+
+
+@pytest.mark.parametrize("B,T,K,H,mem_dtype", [(1, 2000, 64, 512, torch.float32), (2, 1000, 64, 96, torch.bfloat16),
+                                               (4, 8192, 64, 512, torch.float32)])
+def test_mfma_backward_parts(dev, monkeypatch, B, T, K, H, mem_dtype):
+    """The adjoint walk split into parts (run in parallel, then joined) against the unsplit
+    walk (GRM_HIP_BWD_PARTS=0): only the rounding order of the fp32 adjoint differs, so a
+    float32 grad_memory agrees to 1e-5 of its largest magnitude and every 16-bit gradient to
+    one rounding step of its own (2^-7 of the element, plus 1e-6 of the largest magnitude).
+    (4, 8192, 64, 512) is config 4's layer shape, eight parts of 16 chunks."""
+    k, v, q, m = make_case(B, T, K, H, torch.bfloat16, mem_dtype, seed=T + H)
+    g = torch.Generator().manual_seed(8)
+    dh = torch.randn(B, T, H, generator=g).to(torch.bfloat16)
+    dm = torch.randn(B, H, K, generator=g).to(mem_dtype)
+    args = [t.to(dev) for t in (dh, dm, k, v, q, m)]
+    print(f"mfma backward parts B={B} T={T} K={K} H={H} state {mem_dtype}", flush=True)
+    got = capi.chunk_update_bwd(*args, 0.97)
+    monkeypatch.setenv("GRM_HIP_BWD_PARTS", "0")
+    one = capi.chunk_update_bwd(*args, 0.97)
+    torch.cuda.synchronize()
+    for name, x, y in zip(("grad_keys", "grad_values", "grad_queries", "grad_memory"), got, one):
+        sixteen = x.dtype != torch.float32
+        x, y = x.float().cpu(), y.float().cpu()
+        scale = max(float(y.abs().max()), 1e-30)
+        if sixteen:
+            assert bool(((x - y).abs() <= 2.0 ** -7 * y.abs() + 1e-6 * scale).all()), name
+        else:
+            assert float((x - y).abs().max()) <= 1e-5 * scale, name
 
 
 def test_autograd_through_cuda_ops(dev):
