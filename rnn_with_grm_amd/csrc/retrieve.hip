@@ -1193,6 +1193,191 @@ __global__ __launch_bounds__(AT_THREADS) void apply_t_kernel(const RetrieveArgs 
   }
 }
 
+// The same per-pair product M[idx]^T g for float16 archives on 16-bit MFMA.
+// The state sits in LDS transposed ([DKP][value index], float16, rows padded by
+// 8 values so the 16 rows of one fragment read start 4 banks apart).  Each
+// 32-value chunk of a pair's float32 gradient row is scaled by the power of two
+// that puts its largest magnitude in [2^14, 2^15) and split into float16 parts
+// hi = round(g s) and lo = round(g s - hi); two 16x16x32 MFMAs (products of
+// float16 values are exact in fp32) and one multiply by 1/s per chunk.  Error
+// per chunk about 2^-22 of its largest magnitude times sum_v |M[v][k]|, the size
+// of the fp32 accumulation's own rounding.  Chunks of 4 are loaded one group
+// ahead, as apply_t_kernel does.
+__host__ __device__ inline int at16_stride(int dv) { return (dv + 31) / 32 * 32 + 8; }
+
+template <int DKP>
+__global__ __launch_bounds__(AT_THREADS) void apply_t16_kernel(const RetrieveArgs a, const float* grad, float* dqp,
+                                                               int vec_state, int vec_grad, int token_rows) {
+  extern __shared__ uint16_t MsT[];  // [DKP][at16_stride(dv)]
+  constexpr int KB = DKP / 16;
+  constexpr int GC = 4;  // 32-value chunks per prefetched group
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int64_t tile = blockIdx.x;
+  const int64_t b = blockIdx.y;
+  if (tile >= a.n_tiles[b]) return;
+  const int4 te = a.tiles[b * a.tb_max + tile];
+  const int64_t s = te.x;
+  const int p_begin = te.y, p_end = te.z;
+  const int dk = a.dk, dv = a.dv;
+  const int VS = at16_stride(dv);
+  const int dv32 = VS - 8;
+  const uint16_t* msrc = static_cast<const uint16_t*>(a.mem) + (b * a.segments + s) * dv * dk;
+  if (vec_state) {
+    // 16 bytes (8 key values of one value row) per thread and step, written transposed
+    const int nvec = dv * dk / 8;
+    for (int e = tid; e < nvec; e += AT_THREADS) {
+      const int idx = 8 * e;
+      const int v = idx / dk, k = idx % dk;
+      const uint4 t = *reinterpret_cast<const uint4*>(msrc + idx);
+      const uint32_t wds[4] = {t.x, t.y, t.z, t.w};
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        MsT[(k + 2 * j) * VS + v] = static_cast<uint16_t>(wds[j] & 0xffffu);
+        MsT[(k + 2 * j + 1) * VS + v] = static_cast<uint16_t>(wds[j] >> 16);
+      }
+    }
+  } else {
+    for (int e = tid; e < dv * dk; e += AT_THREADS) MsT[(e % dk) * VS + e / dk] = msrc[e];
+  }
+  if (dk < DKP || dv < dv32) {
+    for (int e = tid; e < DKP * dv32; e += AT_THREADS) {
+      const int k = e / dv32, v = e % dv32;
+      if (k >= dk || v >= dv) MsT[k * VS + v] = 0;
+    }
+  }
+  __syncthreads();
+  const int32_t* lb = a.list + b * a.n_index;
+  const int n = lane & 15, kq = lane >> 4;
+  const int nch = dv32 / 32;
+  const int ngr = (nch + GC - 1) / GC;
+  int p0 = p_begin + 16 * w;
+  int pid = p0 < p_end && p0 + n < p_end ? lb[p0 + n] : -1;
+  for (; p0 < p_end; p0 += 16 * (AT_THREADS / 64)) {
+    const int pn = p0 + 16 * (AT_THREADS / 64);
+    const int pid_next = pn + n < p_end ? lb[pn + n] : -1;
+    // grad rows per pair, or (token_rows) one row per query shared by its routes
+    const int64_t grow_i = token_rows ? b * a.n_query + (pid >= 0 ? pid : 0) / a.routes
+                                      : b * a.n_index + (pid >= 0 ? pid : 0);
+    const float* grow = grad + grow_i * static_cast<int64_t>(dv);
+    // values 32 c + 8 kq .. + 7 of this lane's pair, chunks of group gi
+    auto load_group = [&](float (&x)[GC][8], int gi) {
+#pragma unroll
+      for (int u = 0; u < GC; ++u) {
+        const int v = 32 * (GC * gi + u) + 8 * kq;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) x[u][j] = 0.f;
+        if (pid >= 0) {
+          if (vec_grad) {
+            if (v < dv) {
+              const f32x4 lo4 = *reinterpret_cast<const f32x4*>(grow + v);
+#pragma unroll
+              for (int j = 0; j < 4; ++j) x[u][j] = lo4[j];
+            }
+            if (v + 4 < dv) {
+              const f32x4 hi4 = *reinterpret_cast<const f32x4*>(grow + v + 4);
+#pragma unroll
+              for (int j = 0; j < 4; ++j) x[u][4 + j] = hi4[j];
+            }
+          } else {
+#pragma unroll
+            for (int j = 0; j < 8; ++j)
+              if (v + j < dv) x[u][j] = grow[v + j];
+          }
+        }
+      }
+    };
+    f32x4 acc[KB];
+#pragma unroll
+    for (int kb = 0; kb < KB; ++kb) acc[kb] = f32x4{0.f, 0.f, 0.f, 0.f};
+    float cur[GC][8], nxt[GC][8];
+    load_group(cur, 0);
+    for (int gi = 0; gi < ngr; ++gi) {
+      if (gi + 1 < ngr) load_group(nxt, gi + 1);
+#pragma unroll
+      for (int u = 0; u < GC; ++u) {
+        const int c = GC * gi + u;
+        if (c < nch) {
+          // the chunk's scale: its largest magnitude over the pair's 4 lanes
+          float m = 0.f;
+#pragma unroll
+          for (int j = 0; j < 8; ++j) m = fmaxf(m, fabsf(cur[u][j]));
+          m = fmaxf(m, __shfl_xor(m, 16, 64));
+          m = fmaxf(m, __shfl_xor(m, 32, 64));
+          const int ex = static_cast<int>((__float_as_uint(m) >> 23) & 0xffu);
+          // s = 2^(14 - floor(log2 m)) as a biased exponent in [1, 253]; 1 for 0 or inf
+          const int es = (m > 0.f && ex < 255) ? min(max(268 - ex, 1), 253) : 127;
+          const float sc = __uint_as_float(static_cast<uint32_t>(es) << 23);
+          const float inv = __uint_as_float(static_cast<uint32_t>(254 - es) << 23);
+          Frag8<F16> hi, lo;
+#pragma unroll
+          for (int j = 0; j < 8; ++j) {
+            const float x = cur[u][j] * sc;
+            hi.e[j] = ET<F16>::from_f(x);
+            lo.e[j] = ET<F16>::from_f(x - ET<F16>::to_f(hi.e[j]));
+          }
+          const int vA = 32 * c + 8 * kq;
+#pragma unroll
+          for (int kb = 0; kb < KB; ++kb) {
+            const Frag8<F16> am =
+                __builtin_bit_cast(Frag8<F16>, *reinterpret_cast<const uint4*>(MsT + (16 * kb + n) * VS + vA));
+            f32x4 t = mfma8(am, hi, f32x4{0.f, 0.f, 0.f, 0.f});
+            t = mfma8(am, lo, t);
+#pragma unroll
+            for (int r = 0; r < 4; ++r) acc[kb][r] = fmaf(t[r], inv, acc[kb][r]);
+          }
+        }
+      }
+      if (gi + 1 < ngr) {
+#pragma unroll
+        for (int u = 0; u < GC; ++u)
+#pragma unroll
+          for (int j = 0; j < 8; ++j) cur[u][j] = nxt[u][j];
+      }
+    }
+    // lane (kq, n) holds keys 16 kb + 4 kq + r of pair n (the pair its pid names)
+    if (pid >= 0) {
+      float* orow = dqp + (b * a.n_index + pid) * static_cast<int64_t>(dk);
+#pragma unroll
+      for (int kb = 0; kb < KB; ++kb) {
+        const int k = 16 * kb + 4 * kq;
+        if (k + 4 <= dk && (dk & 3) == 0) {
+          *reinterpret_cast<f32x4*>(orow + k) = acc[kb];
+        } else {
+#pragma unroll
+          for (int r = 0; r < 4; ++r)
+            if (k + r < dk) orow[k + r] = acc[kb][r];
+        }
+      }
+    }
+    pid = pid_next;
+  }
+}
+
+inline size_t apply_t16_lds(int dv, int dkp) { return static_cast<size_t>(dkp) * at16_stride(dv) * sizeof(uint16_t); }
+
+template <int DKP>
+int launch_apply_t16(const RetrieveArgs& a, const float* grad, float* dqp, int token_rows, hipStream_t s) {
+  const size_t lds = apply_t16_lds(a.dv, DKP);
+  static bool attr_set = false;
+  if (!attr_set) {
+    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&apply_t16_kernel<DKP>),
+                                       hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
+    if (e != hipSuccess) {
+      set_error("gather_apply_bwd: hipFuncSetAttribute failed: %s", hipGetErrorString(e));
+      return static_cast<int>(e);
+    }
+    attr_set = true;
+  }
+  const int vec_state = a.dk % 8 == 0 && reinterpret_cast<uintptr_t>(a.mem) % 16 == 0;
+  const int vec_grad = a.dv % 4 == 0 && reinterpret_cast<uintptr_t>(grad) % 16 == 0;
+  const dim3 grid(static_cast<unsigned>(a.tb_max), static_cast<unsigned>(a.batch));
+  hipLaunchKernelGGL((apply_t16_kernel<DKP>), grid, dim3(AT_THREADS), lds, s, a, grad, dqp, vec_state, vec_grad,
+                     token_rows);
+  return check_launch("gather_apply_bwd");
+}
+
 inline size_t apply_t_lds(int dv, int dkp) {
   return static_cast<size_t>(at_rows(dv)) * (dkp + 4) * sizeof(float);
 }
@@ -1222,6 +1407,16 @@ int launch_apply_t(const RetrieveArgs& a, const float* grad, float* dqp, int tok
 
 template <class EL>
 int dispatch_apply_t(const RetrieveArgs& a, const float* grad, float* dqp, int token_rows, hipStream_t s) {
+  if constexpr (std::is_same_v<EL, F16>) {
+    // float16 archives: the 16-bit MFMA form (GRM_HIP_APPLY_T16=0 keeps the fp32 one)
+    const char* env = getenv("GRM_HIP_APPLY_T16");
+    if (env == nullptr || env[0] != '0') {
+      if (a.dk <= 16) return launch_apply_t16<16>(a, grad, dqp, token_rows, s);
+      if (a.dk <= 32) return launch_apply_t16<32>(a, grad, dqp, token_rows, s);
+      if (a.dk <= 64) return launch_apply_t16<64>(a, grad, dqp, token_rows, s);
+      return launch_apply_t16<128>(a, grad, dqp, token_rows, s);
+    }
+  }
   if (a.dk <= 16) return launch_apply_t<EL, 16>(a, grad, dqp, token_rows, s);
   if (a.dk <= 32) return launch_apply_t<EL, 32>(a, grad, dqp, token_rows, s);
   if (a.dk <= 64) return launch_apply_t<EL, 64>(a, grad, dqp, token_rows, s);

@@ -887,3 +887,38 @@ def test_segment_route_window_select_nonfinite(dev, monkeypatch):
         assert torch.equal(idx, i0)
         assert torch.equal(torch.nan_to_num(sc, nan=7.0), torch.nan_to_num(s0, nan=7.0))
         assert torch.equal(torch.nan_to_num(gates, nan=7.0), torch.nan_to_num(g0, nan=7.0))
+
+
+@pytest.mark.parametrize("B,Q,S,R,H,K", [(4, 2048, 128, 8, 512, 64), (2, 300, 9, 5, 200, 40), (1, 129, 30, 16, 72, 128),
+                                         (2, 64, 3, 4, 36, 8)])
+def test_transposed_apply_f16_split(dev, monkeypatch, B, Q, S, R, H, K):
+    """Float16 archives: the 16-bit MFMA transposed apply (each 32-value chunk of a gradient row
+    scaled by a power of two and split into two float16 parts) against the fp32 MFMA kernel
+    (GRM_HIP_APPLY_T16=0) at 1e-5 of the gradient's scale, per pair and in the token form, with
+    gradient rows spanning 30 binary orders of magnitude, an all-zero row and ragged hidden and
+    key widths; and against the oracle."""
+    g = torch.Generator().manual_seed(B + Q + H)
+    mem = (torch.randn(B, S, H, K, generator=g) * 0.3).to(torch.float16)
+    idx = torch.randint(0, S, (B, Q, R), generator=g)
+    idx[0, 1, 0] = -1
+    gx = torch.randn(B, Q, H, generator=g) * torch.exp2(torch.randint(-15, 15, (B, Q, 1), generator=g).float())
+    gx[0, 3] = 0.0
+    gp = torch.randn(B, Q, R, H, generator=g)
+    print(f"f16 split transposed apply B={B} Q={Q} S={S} R={R} H={H} K={K}", flush=True)
+    md, idd = mem.to(dev), idx.to(dev)
+    tok = capi.gather_apply_bwd_tokens(md, idd, gx.to(dev))
+    pair = capi.gather_apply_bwd_queries(md, idd, gp.to(dev))
+    monkeypatch.setenv("GRM_HIP_APPLY_T16", "0")
+    tok32 = capi.gather_apply_bwd_tokens(md, idd, gx.to(dev))
+    pair32 = capi.gather_apply_bwd_queries(md, idd, gp.to(dev))
+    monkeypatch.delenv("GRM_HIP_APPLY_T16")
+    torch.cuda.synchronize()
+    assert not tok[0, 1, 0].any() and not pair[0, 1, 0].any()
+    for got, ref32 in ((tok, tok32), (pair, pair32)):
+        got, ref32 = got.cpu().double(), ref32.cpu().double()
+        # per query row: the error is relative to that row's scale
+        scale = ref32.abs().amax(dim=(2, 3), keepdim=True).clamp(min=1e-30)
+        assert float(((got - ref32).abs() / scale).max()) <= 1e-5
+    ref = _pair_bwd_ref(mem, idx, gx)
+    scale = np.abs(ref).max(axis=(2, 3), keepdims=True).clip(1e-30)
+    assert float((np.abs(tok.cpu().double().numpy() - ref) / scale).max()) <= 1e-5
