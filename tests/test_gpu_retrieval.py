@@ -922,3 +922,35 @@ def test_transposed_apply_f16_split(dev, monkeypatch, B, Q, S, R, H, K):
     ref = _pair_bwd_ref(mem, idx, gx)
     scale = np.abs(ref).max(axis=(2, 3), keepdims=True).clip(1e-30)
     assert float((np.abs(tok.cpu().double().numpy() - ref) / scale).max()) <= 1e-5
+
+
+def test_bucket_order_does_not_reach_outputs(dev):
+    """The segment sort places pairs in their buckets with LDS atomics, so the order inside a
+    bucket varies from run to run; every output is a function of one pair (or, in
+    retrieve_fuse, of one query's routes in route order), so repeated calls are bit-identical:
+    gather_apply, retrieve_fuse and both transposed applies, with thousands of pairs per segment
+    (7200 pairs: the one-workgroup sort; 72000: the chunked sort)."""
+    g = torch.Generator().manual_seed(99)
+    for B, Q, S, R in ((2, 900, 5, 8), (1, 9000, 7, 8)):
+        H, K = 128, 64
+        mem = (torch.randn(B, S, H, K, generator=g) * 0.3).to(torch.float16).to(dev)
+        idx = torch.randint(0, S, (B, Q, R), generator=g).to(dev)
+        q = norm(torch.randn(B, Q, K, generator=g)).to(torch.bfloat16).to(dev)
+        gates = torch.softmax(torch.randn(B, Q, R, generator=g), -1).to(dev)
+        h = torch.randn(B, Q, H, generator=g).to(dev)
+        gx = torch.randn(B, Q, H, generator=g).to(dev)
+        gp = torch.randn(B, Q, R, H, generator=g).to(dev)
+        print(f"bucket order B={B} Q={Q} S={S} R={R}", flush=True)
+
+        def run():
+            return (capi.gather_apply(mem, idx, q, dtype=torch.float32),
+                    capi.retrieve_fuse(mem, idx, q, gates, h),
+                    capi.gather_apply_bwd_tokens(mem, idx, gx),
+                    capi.gather_apply_bwd_queries(mem, idx, gp))
+
+        first = [t.clone() for t in run()]
+        for _ in range(3):
+            again = run()
+            torch.cuda.synchronize()
+            for a, b in zip(first, again):
+                assert torch.equal(a, b)
