@@ -155,7 +155,15 @@ def bench_n1(torch, dev, steps, warmup):
     del k, v, q, m, hidden, snaps, ws
     # The box's rate for a stream as large and as write-heavy: a device copy moving the same
     # number of bytes (half read, half written; the scan reads 37% and writes 63%).
-    n = bytes_ // 8
+    copy_us, copy_bytes = copy_rate(torch, dev, bytes_, steps, stream)
+    return {"us": ev0.elapsed_time(ev1) * 1e3 / steps, "tokens": BH * T, "flops": flops, "bytes": bytes_,
+            "copy_us": copy_us, "copy_bytes": copy_bytes}
+
+
+def copy_rate(torch, dev, nbytes, steps, stream):
+    """Microseconds per device copy of nbytes in total (nbytes / 2 read, nbytes / 2 written),
+    events around `steps` back-to-back copies: the practical ceiling of a stream of that size."""
+    n = nbytes // 8
     src = torch.empty(n, dtype=torch.float32, device=dev).fill_(1.0)
     dst = torch.empty_like(src)
     for _ in range(2):
@@ -167,10 +175,9 @@ def bench_n1(torch, dev, steps, warmup):
         dst.copy_(src)
     ev1c.record(stream)
     torch.cuda.synchronize()
-    copy_us = ev0c.elapsed_time(ev1c) * 1e3 / steps
+    us = ev0c.elapsed_time(ev1c) * 1e3 / steps
     del src, dst
-    return {"us": ev0.elapsed_time(ev1) * 1e3 / steps, "tokens": BH * T, "flops": flops, "bytes": bytes_,
-            "copy_us": copy_us, "copy_bytes": 8 * n}
+    return us, 8 * n
 
 
 def bench_c2_bwd(torch, dev, steps, warmup):
@@ -825,6 +832,9 @@ def main() -> int:
     achieved_gbs = bytes_ / t_kernel / 1e9
     tflops = flops / t_kernel / 1e12
     log(f"c2: {t_kernel * 1e6:.1f} us/launch (events around {a.steps} launches), {t_step * 1e6:.1f} us/step (wall)")
+    c2_copy_us, c2_copy_bytes = copy_rate(torch, dev, bytes_, a.steps, torch.cuda.current_stream(dev))
+    log(f"c2: a device copy of the same {c2_copy_bytes} bytes: {c2_copy_us:.1f} us "
+        f"({c2_copy_bytes / c2_copy_us / 1e3:.0f} GB/s)")
 
     traffic = None
     tfile = REPO / "profiles" / "scan_vsplit_c2_traffic.json"
@@ -1010,6 +1020,12 @@ def main() -> int:
                      "kernel": "scan_vsplit_kernel<BF16,128,4>: the one launch of a grm_hip_chunk_update_fwd call",
                      "algorithmic_bytes_per_launch": bytes_,
                      "kernel_us": round(t_kernel * 1e6, 2),
+                     "copy_ceiling": {"what": "a device copy of the same byte count (half read, half written) "
+                                              "right after the timed launches, events around the same number of "
+                                              "copies",
+                                      "us": round(c2_copy_us, 2),
+                                      "GB/s": round(c2_copy_bytes / c2_copy_us / 1e3, 1),
+                                      "kernel_time_vs_copy": round(c2_copy_us / (t_kernel * 1e6), 4)},
                      "mfma": {"TFLOP/s": round(tflops, 2), "peak": BF16_PEAK_TFLOPS,
                               "frac": round(tflops / BF16_PEAK_TFLOPS, 5), "flops_per_launch": flops}},
         "cpu_baseline": cpu,
