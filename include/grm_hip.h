@@ -296,6 +296,24 @@ int grm_hip_residual_layer_norm(const void* x, const void* residual, const void*
                                 float eps, void* stream);
 
 /*
+ * LinearMemoryCell.project in one kernel: proj = x weight^T + bias over the
+ * concatenated [key | value | query | extra] projection weights, rounded to
+ * the input dtype (F.linear's output), then split as grm_hip_project_split
+ * does: keys and queries L2-normalised (norm and eps clamp rounded to the
+ * dtype), every part written contiguous.  x [rows, in_dim], weight
+ * [2 key_dim + value_dim + extra_dim, in_dim], bias [that] or NULL, all in
+ * dtype (f16 or bf16).
+ *   (reference grm/core/paper_grm.py:491-493: key_proj / value_proj /
+ *   query_proj and F.normalize; 570-574: the gating query projection; torch
+ *   ops in the reference.)
+ * Limits: key_dim 64, value_dim and extra_dim multiples of 64, in_dim a
+ * multiple of 64, x and weight under 2 GiB, 16-byte aligned buffers.  ABI 107.
+ */
+int grm_hip_project_gemm(const void* x, const void* weight, const void* bias, void* keys, void* values,
+                         void* queries, void* extra, int64_t rows, int64_t in_dim, int64_t key_dim,
+                         int64_t value_dim, int64_t extra_dim, int dtype, float eps, void* stream);
+
+/*
  * Archive form of float32 states: out[i] = storage(model(states[i])), each
  * value rounded (to nearest even) to model_dtype and then to storage_dtype,
  * which is what push() stores for a state the model computed

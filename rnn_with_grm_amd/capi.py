@@ -47,6 +47,7 @@ SIGNATURES = {
     "grm_hip_project_split": (_C, [_P, _P, _P, _P, _P, _I, _I, _I, _I, _C, ctypes.c_float, _P]),
     "grm_hip_residual_layer_norm": (_C, [_P, _P, _P, _P, _P, _I, _I, _C, _C, ctypes.c_float, _P]),
     "grm_hip_archive_cast": (_C, [_P, _P, _I, _C, _C, _P]),
+    "grm_hip_project_gemm": (_C, [_P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _C, ctypes.c_float, _P]),
     "grm_hip_retrieve_fuse": (_C, [_P, _P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _C, _C, _C,
                                    ctypes.c_float, _P, _P]),
     "grm_hip_topk_route": (_C, [_P, _P, _P, _P, _P, _I, _I, _I, _I, _C, _I, ctypes.c_float, ctypes.c_float, _P]),
@@ -300,6 +301,19 @@ def residual_layer_norm(x, residual, weight=None, bias=None, eps: float = 1e-5, 
                                             _stream(x))
     _check(rc, "grm_hip_residual_layer_norm")
     return out
+
+
+def project_gemm(x, weight, bias, key_dim: int, value_dim: int, extra_dim: int = 0, eps: float = 1e-6):
+    """(keys, values, queries, extra) of x weight^T + bias, keys and queries L2-normalised."""
+    K = x.shape[-1]
+    rows = x.numel() // K
+    mk = lambda d: torch.empty(x.shape[:-1] + (d,), dtype=x.dtype, device=x.device)  # noqa: E731
+    k, v, q, e = mk(key_dim), mk(value_dim), mk(key_dim), mk(extra_dim)
+    rc = load().grm_hip_project_gemm(_ptr(x), _ptr(weight), _ptr(bias), _ptr(k), _ptr(v), _ptr(q),
+                                     _ptr(e) if extra_dim else None, rows, K, key_dim, value_dim, extra_dim,
+                                     dtype_code(x.dtype), float(eps), _stream(x))
+    _check(rc, "grm_hip_project_gemm")
+    return k, v, q, e
 
 
 def archive_cast(states, model_dtype, storage_dtype, out=None):

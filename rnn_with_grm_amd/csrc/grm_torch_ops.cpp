@@ -10,7 +10,8 @@
 // materialising the states), retrieve_fuse (gather_apply, the gate-weighted
 // sum and fuse_residual in one call), the layer glue project_split (the
 // projection's split with L2-normalised keys and queries),
-// residual_layer_norm (the block's LayerNorm(out + x)) and archive_cast (the
+// residual_layer_norm (the block's LayerNorm(out + x)), project_gemm (the
+// projection GEMM with project_split as its epilogue) and archive_cast (the
 // archive's stored form of float32 states), and three gradients
 // without gathered states: apply_query_backward_queries,
 // gather_apply_backward_queries (one gradient row per pair) and
@@ -453,6 +454,18 @@ std::tuple<Tensor, Tensor, Tensor, Tensor> project_split_generic(const Tensor& p
   auto parts = proj.split_with_sizes({key_dim, value_dim, key_dim, extra_dim}, -1);
   auto normalise = [&](const Tensor& t) { return (t / t.norm(2, {-1}, true).clamp_min(eps)).contiguous(); };
   return {normalise(parts[0]), parts[1].contiguous(), normalise(parts[2]), parts[3].contiguous()};
+}
+
+// project_gemm: the projection GEMM and its split in one op, F.linear(x, weight,
+// bias) then project_split (paper_grm.py:491-493, 570-574).
+std::tuple<Tensor, Tensor, Tensor, Tensor> project_gemm_generic(const Tensor& x, const Tensor& weight,
+                                                                const c10::optional<Tensor>& bias, int64_t key_dim,
+                                                                int64_t value_dim, int64_t extra_dim, double eps) {
+  TORCH_CHECK(x.dim() >= 1 && weight.dim() == 2 && weight.size(1) == x.size(-1) &&
+                  weight.size(0) == 2 * key_dim + value_dim + extra_dim,
+              "project_gemm: weight must be [2 key_dim + value_dim + extra_dim, in_dim]");
+  const Tensor proj = at::linear(x, weight, bias.has_value() ? *bias : Tensor());
+  return project_split_generic(proj, key_dim, value_dim, extra_dim, eps);
 }
 
 // residual_layer_norm: layer_norm(x + residual) (multilayer_grm.py:92-97).
@@ -1006,6 +1019,45 @@ std::tuple<Tensor, Tensor, Tensor, Tensor> project_split_hip(const Tensor& proj,
   return {k, v, q, e};
 }
 
+std::tuple<Tensor, Tensor, Tensor, Tensor> project_gemm_hip(const Tensor& x, const Tensor& weight,
+                                                            const c10::optional<Tensor>& bias, int64_t key_dim,
+                                                            int64_t value_dim, int64_t extra_dim, double eps) {
+  TORCH_CHECK(x.dim() >= 1 && weight.dim() == 2 && weight.size(1) == x.size(-1) &&
+                  weight.size(0) == 2 * key_dim + value_dim + extra_dim,
+              "project_gemm: weight must be [2 key_dim + value_dim + extra_dim, in_dim]");
+  const bool has_b = bias.has_value() && bias->defined();
+  const int dt = dtype_code(x.scalar_type());
+  const int64_t K = x.size(-1);
+  const int64_t rows = K > 0 ? x.numel() / K : 0;
+  bool ok = x.is_cuda() && weight.is_cuda() && (dt == 1 || dt == 2) && weight.scalar_type() == x.scalar_type() &&
+            key_dim == 64 && value_dim % 64 == 0 && extra_dim % 64 == 0 && K % 64 == 0 && K > 0 &&
+            rows * K * 2 <= INT32_MAX && weight.numel() * 2 <= INT32_MAX;
+  if (has_b) ok = ok && bias->is_cuda() && bias->scalar_type() == x.scalar_type() && bias->numel() == weight.size(0);
+  if (!ok) {
+    // Shapes the fused kernel does not take: the library GEMM, then the split's own kernel
+    // (which counts a generic call only where it falls back itself).
+    return project_split_hip(at::linear(x, weight, has_b ? *bias : Tensor()), key_dim, value_dim, extra_dim, eps);
+  }
+  c10::OptionalDeviceGuard guard(x.device());
+  Tensor xc = x.contiguous(), wc = weight.contiguous();
+  Tensor bc = has_b ? bias->contiguous() : Tensor();
+  if (!aligned16(xc)) xc = xc.clone();
+  if (!aligned16(wc)) wc = wc.clone();
+  auto lead = xc.sizes().vec();
+  lead.pop_back();
+  auto mk = [&](int64_t d) {
+    auto shape = lead;
+    shape.push_back(d);
+    return at::empty(shape, xc.options());
+  };
+  Tensor k = mk(key_dim), v = mk(value_dim), q = mk(key_dim), e = mk(extra_dim);
+  check_rc(grm_hip_project_gemm(xc.data_ptr(), wc.data_ptr(), has_b ? bc.data_ptr() : nullptr, k.data_ptr(),
+                                v.data_ptr(), q.data_ptr(), extra_dim > 0 ? e.data_ptr() : nullptr, rows, K, key_dim,
+                                value_dim, extra_dim, dt, static_cast<float>(eps), current_stream(xc)),
+           "project_gemm");
+  return {k, v, q, e};
+}
+
 Tensor residual_layer_norm_hip(const Tensor& x, const Tensor& residual, const c10::optional<Tensor>& weight,
                                const c10::optional<Tensor>& bias, double eps) {
   TORCH_CHECK(x.sizes() == residual.sizes() && x.dim() >= 1, "residual_layer_norm: x and residual must match");
@@ -1084,6 +1136,8 @@ TORCH_LIBRARY(grm_cuda, m) {
   m.def("gather_apply_backward_tokens(Tensor memories, Tensor indices, Tensor grad_tokens) -> Tensor");
   m.def("residual_layer_norm(Tensor x, Tensor residual, Tensor? weight, Tensor? bias, float eps) -> Tensor");
   m.def("archive_cast(Tensor states, ScalarType model_dtype, ScalarType storage_dtype) -> Tensor");
+  m.def("project_gemm(Tensor x, Tensor weight, Tensor? bias, int key_dim, int value_dim, int extra_dim, float eps) "
+        "-> (Tensor, Tensor, Tensor, Tensor)");
 }
 
 TORCH_LIBRARY_IMPL(grm_cuda, CPU, m) {
@@ -1104,6 +1158,7 @@ TORCH_LIBRARY_IMPL(grm_cuda, CPU, m) {
   m.impl("gather_apply_backward_tokens", grm::gather_apply_backward_tokens_generic);
   m.impl("residual_layer_norm", grm::residual_layer_norm_generic);
   m.impl("archive_cast", grm::archive_cast_generic);
+  m.impl("project_gemm", grm::project_gemm_generic);
 }
 
 TORCH_LIBRARY_IMPL(grm_cuda, CUDA, m) {
@@ -1124,6 +1179,7 @@ TORCH_LIBRARY_IMPL(grm_cuda, CUDA, m) {
   m.impl("gather_apply_backward_tokens", grm::gather_apply_backward_tokens_hip);
   m.impl("residual_layer_norm", grm::residual_layer_norm_hip);
   m.impl("archive_cast", grm::archive_cast_hip);
+  m.impl("project_gemm", grm::project_gemm_hip);
 }
 
 PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {

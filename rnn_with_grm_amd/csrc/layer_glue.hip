@@ -204,6 +204,184 @@ __global__ __launch_bounds__(GL_THREADS) void residual_layer_norm_kernel(const R
 
 bool aligned16(const void* p) { return reinterpret_cast<uintptr_t>(p) % 16 == 0; }
 
+// project_gemm: LinearMemoryCell.project's GEMM (the concatenated k | v | q | extra
+// projection, reference grm/core/paper_grm.py:491-493, 570-574) with project_split
+// as its epilogue.  Y = X W^T + bias on 16x16x32 MFMA, 128 x 256 output tiles,
+// K in steps of 64 staged in LDS (rows padded to 72 values: the 16 rows of a
+// fragment read start in distinct bank groups), the next step's tiles loaded
+// into registers while the current one is multiplied.  Eight waves: wave w
+// owns rows [m0 + 64 (w >> 2), + 64) and columns [n0 + 64 (w & 3), + 64); at
+// key_dim 64 a key or query block is one wave's columns, so its row norms need
+// no other wave.  Epilogue: Y + bias rounded to the
+// model dtype (F.linear's output), keys and queries L2-normalised with
+// project_split's roundings, every part written contiguous through an LDS
+// transpose (16-byte row stores).
+constexpr int PG_BM = 128, PG_BN = 256, PG_BK = 64, PG_THREADS = 512;
+constexpr int PG_S = PG_BK + 8;  // LDS row stride, elements
+
+struct GemmArgs {
+  const void* x;
+  const void* w;
+  const void* bias;
+  void* keys;
+  void* values;
+  void* queries;
+  void* extra;
+  int64_t rows;
+  int K;
+  int dk, dv, de;  // dk == 64; dv, de multiples of 64
+  float eps;
+};
+
+template <class E>
+__global__ __launch_bounds__(PG_THREADS) void project_gemm_kernel(const GemmArgs a) {
+  using raw = typename ET<E>::raw;
+  static_assert(sizeof(raw) == 2, "16-bit inputs");
+  // One buffer for both tiles, so that the epilogue's staging (4 waves x 8 KB from
+  // its start) stays inside it whatever the compiler's placement of arrays.
+  __shared__ __align__(16) raw smem[(PG_BM + PG_BN) * PG_S];
+  raw* const As = smem;
+  raw* const Ws = smem + PG_BM * PG_S;
+  const int tid = threadIdx.x, lane = tid & 63, g = lane >> 4, n = lane & 15;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int N = 2 * a.dk + a.dv + a.de;
+  const int K = a.K;
+  const int64_t m0 = static_cast<int64_t>(blockIdx.x) * PG_BM;
+  const int n0 = static_cast<int>(blockIdx.y) * PG_BN;
+  const int wr = w >> 2;              // row half
+  const int c0 = n0 + 64 * (w & 3);  // this wave's first column
+  const bool wave_on = c0 < N;
+  const __amdgpu_buffer_rsrc_t rx =
+      make_rsrc(static_cast<const raw*>(a.x) + m0 * K, static_cast<uint32_t>(min<int64_t>(a.rows - m0, PG_BM) * K * 2));
+  const __amdgpu_buffer_rsrc_t rw =
+      make_rsrc(static_cast<const raw*>(a.w) + static_cast<int64_t>(n0) * K,
+                static_cast<uint32_t>(static_cast<int64_t>(min(N - n0, PG_BN)) * K * 2));
+  constexpr int UA = PG_BM * (PG_BK / 8) / PG_THREADS;  // 16-byte units per thread
+  constexpr int UW = PG_BN * (PG_BK / 8) / PG_THREADS;
+  u32x4 ra[UA], rwv[UW];
+  auto gload = [&](int k0) {
+#pragma unroll
+    for (int i = 0; i < UA; ++i) {
+      const int u = tid + PG_THREADS * i;
+      ra[i] = __builtin_amdgcn_raw_buffer_load_b128(rx, ((u >> 3) * K + k0 + 8 * (u & 7)) * 2, 0, 0);
+    }
+#pragma unroll
+    for (int i = 0; i < UW; ++i) {
+      const int u = tid + PG_THREADS * i;
+      rwv[i] = __builtin_amdgcn_raw_buffer_load_b128(rw, ((u >> 3) * K + k0 + 8 * (u & 7)) * 2, 0, 0);
+    }
+  };
+  f32x4 acc[4][4];
+#pragma unroll
+  for (int ti = 0; ti < 4; ++ti)
+#pragma unroll
+    for (int tj = 0; tj < 4; ++tj) acc[ti][tj] = f32x4{0.f, 0.f, 0.f, 0.f};
+  gload(0);
+  for (int k0 = 0; k0 < K; k0 += PG_BK) {
+    __syncthreads();  // the previous step's fragments read
+#pragma unroll
+    for (int i = 0; i < UA; ++i) {
+      const int u = tid + PG_THREADS * i;
+      *reinterpret_cast<u32x4*>(As + (u >> 3) * PG_S + 8 * (u & 7)) = ra[i];
+    }
+#pragma unroll
+    for (int i = 0; i < UW; ++i) {
+      const int u = tid + PG_THREADS * i;
+      *reinterpret_cast<u32x4*>(Ws + (u >> 3) * PG_S + 8 * (u & 7)) = rwv[i];
+    }
+    __syncthreads();
+    if (k0 + PG_BK < K) gload(k0 + PG_BK);
+    if (wave_on) {
+#pragma unroll
+      for (int sk = 0; sk < PG_BK / 32; ++sk) {
+        Frag8<E> bf[4];
+#pragma unroll
+        for (int tj = 0; tj < 4; ++tj)
+          bf[tj] = __builtin_bit_cast(
+              Frag8<E>, *reinterpret_cast<const u32x4*>(Ws + (64 * (w & 3) + 16 * tj + n) * PG_S + 32 * sk + 8 * g));
+#pragma unroll
+        for (int ti = 0; ti < 4; ++ti) {
+          const Frag8<E> af = __builtin_bit_cast(
+              Frag8<E>, *reinterpret_cast<const u32x4*>(As + (64 * wr + 16 * ti + n) * PG_S + 32 * sk + 8 * g));
+#pragma unroll
+          for (int tj = 0; tj < 4; ++tj) acc[ti][tj] = mfma8(af, bf[tj], acc[ti][tj]);
+        }
+      }
+    }
+  }
+  __syncthreads();  // every wave done with As / Ws: they become the waves' staging
+  if (!wave_on) return;
+  // acc[ti][tj][r]: row m0 + 64 wr + 16 ti + 4 g + r, column c0 + 16 tj + n.  Y + bias in the
+  // model dtype, as F.linear returns it.
+  float bcol[4];
+#pragma unroll
+  for (int tj = 0; tj < 4; ++tj)
+    bcol[tj] = a.bias != nullptr ? ET<E>::to_f(static_cast<const raw*>(a.bias)[c0 + 16 * tj + n]) : 0.f;
+#pragma unroll
+  for (int ti = 0; ti < 4; ++ti)
+#pragma unroll
+    for (int tj = 0; tj < 4; ++tj)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) acc[ti][tj][r] = round_to<E>(acc[ti][tj][r] + bcol[tj]);
+  const int dk = a.dk, dv = a.dv, de = a.de;
+  void* out;
+  int col, ld;
+  bool norm = false;
+  if (c0 < dk) {
+    out = a.keys; col = c0; ld = dk; norm = true;
+  } else if (c0 < dk + dv) {
+    out = a.values; col = c0 - dk; ld = dv;
+  } else if (c0 < 2 * dk + dv) {
+    out = a.queries; col = c0 - dk - dv; ld = dk; norm = true;
+  } else {
+    out = a.extra; col = c0 - 2 * dk - dv; ld = de;
+  }
+  if (norm) {
+    // x / clamp_min(||x||, eps), the norm and the clamp rounded to the row dtype
+#pragma unroll
+    for (int ti = 0; ti < 4; ++ti)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        float ss = 0.f;
+#pragma unroll
+        for (int tj = 0; tj < 4; ++tj) ss = fmaf(acc[ti][tj][r], acc[ti][tj][r], ss);
+#pragma unroll
+        for (int off = 1; off < 16; off <<= 1) ss += __shfl_xor(ss, off, 64);
+        const float den = round_to<E>(fmaxf(round_to<E>(sqrtf(ss)), a.eps));
+#pragma unroll
+        for (int tj = 0; tj < 4; ++tj) acc[ti][tj][r] = acc[ti][tj][r] / den;
+      }
+  }
+  // Two halves of 32 rows through this wave's 4 KB of LDS, then 16-byte row stores.
+  raw* st = smem + w * 32 * 64;
+  static_assert(sizeof(smem) >= 8 * 32 * 64 * sizeof(raw), "staging fits");
+  raw* ob = static_cast<raw*>(out);
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+#pragma unroll
+    for (int t = 0; t < 2; ++t)
+#pragma unroll
+      for (int tj = 0; tj < 4; ++tj)
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+          st[(16 * t + 4 * g + r) * 64 + 16 * tj + n] = ET<E>::from_f(acc[2 * h + t][tj][r]);
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int u = lane + 64 * i;
+      const int rr = u >> 3, cu = 8 * (u & 7);
+      const int64_t row = m0 + 64 * wr + 32 * h + rr;
+      if (row < a.rows)
+        *reinterpret_cast<u32x4*>(ob + row * ld + col + cu) = *reinterpret_cast<const u32x4*>(st + rr * 64 + cu);
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  }
+}
+
 // archive_cast: float32 states in the form the archive stores them, rounded
 // to the model dtype and then to the storage dtype, as push() stores a state
 // the model computed (reference grm/core/paper_grm.py:139-140: the state in
@@ -395,4 +573,59 @@ extern "C" int grm_hip_archive_cast(const float* states, void* out, int64_t n, i
     default: go(BF16{}); break;
   }
   return check_launch("archive_cast");
+}
+
+extern "C" int grm_hip_project_gemm(const void* x, const void* weight, const void* bias, void* keys, void* values,
+                                    void* queries, void* extra, int64_t rows, int64_t in_dim, int64_t key_dim,
+                                    int64_t value_dim, int64_t extra_dim, int dtype, float eps, void* stream) {
+  if (rows < 0 || in_dim < 0 || key_dim < 0 || value_dim < 0 || extra_dim < 0) {
+    set_error("project_gemm: negative size");
+    return GRM_HIP_EINVAL;
+  }
+  if (dtype != GRM_HIP_F16 && dtype != GRM_HIP_BF16) {
+    set_error("project_gemm: 16-bit inputs only (dtype %d)", dtype);
+    return GRM_HIP_EUNSUPPORTED;
+  }
+  const int64_t N = 2 * key_dim + value_dim + extra_dim;
+  if (key_dim != 64 || value_dim % 64 || extra_dim % 64 || in_dim % PG_BK || in_dim == 0 ||
+      rows * in_dim * 2 > INT32_MAX || static_cast<int64_t>(PG_BN) * in_dim * 2 > INT32_MAX ||
+      N * in_dim * 2 > INT32_MAX || (rows + PG_BM - 1) / PG_BM > INT32_MAX) {
+    set_error("project_gemm: needs key_dim 64, value_dim and extra_dim multiples of 64, in_dim a multiple of %d, "
+              "and operands under 2 GiB",
+              PG_BK);
+    return GRM_HIP_EUNSUPPORTED;
+  }
+  if (rows == 0) return GRM_HIP_OK;
+  if (x == nullptr || weight == nullptr || keys == nullptr || values == nullptr || queries == nullptr ||
+      (extra_dim > 0 && extra == nullptr)) {
+    set_error("project_gemm: null pointer");
+    return GRM_HIP_EINVAL;
+  }
+  if (!aligned16(x) || !aligned16(weight) || !aligned16(keys) || !aligned16(values) || !aligned16(queries) ||
+      (extra_dim > 0 && !aligned16(extra))) {
+    set_error("project_gemm: buffers must be 16-byte aligned");
+    return GRM_HIP_EUNSUPPORTED;
+  }
+  GemmArgs a;
+  a.x = x;
+  a.w = weight;
+  a.bias = bias;
+  a.keys = keys;
+  a.values = values;
+  a.queries = queries;
+  a.extra = extra;
+  a.rows = rows;
+  a.K = static_cast<int>(in_dim);
+  a.dk = static_cast<int>(key_dim);
+  a.dv = static_cast<int>(value_dim);
+  a.de = static_cast<int>(extra_dim);
+  a.eps = eps;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const dim3 grid(static_cast<unsigned>((rows + PG_BM - 1) / PG_BM), static_cast<unsigned>((N + PG_BN - 1) / PG_BN));
+  if (dtype == GRM_HIP_F16) {
+    hipLaunchKernelGGL(project_gemm_kernel<F16>, grid, dim3(PG_THREADS), 0, s, a);
+  } else {
+    hipLaunchKernelGGL(project_gemm_kernel<BF16>, grid, dim3(PG_THREADS), 0, s, a);
+  }
+  return check_launch("project_gemm");
 }

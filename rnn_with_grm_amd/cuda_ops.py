@@ -39,7 +39,7 @@ SCHEMA_OPS = (
 )
 EXTRA_OPS = ("segment_scan_forward", "topk_route", "fuse_residual", "gather_apply", "segment_route",
              "retrieve_fuse", "project_split", "residual_layer_norm", "gather_apply_backward_queries",
-             "gather_apply_backward_tokens", "apply_query_backward_queries", "archive_cast")
+             "gather_apply_backward_tokens", "apply_query_backward_queries", "archive_cast", "project_gemm")
 
 # Environment variables of the reference (cuda_ops.py:26-32): one per op and a global one.
 GLOBAL_POLICY_ENV = "GRM_CUDA_KERNEL_POLICY"
@@ -617,6 +617,22 @@ def cuda_project_split(proj: Tensor, key_dim: int, value_dim: int, extra_dim: in
     k = torch.nn.functional.normalize(parts[0], p=2, dim=-1, eps=eps)
     q = torch.nn.functional.normalize(parts[2], p=2, dim=-1, eps=eps)
     return (k, parts[1], q) + ((parts[3],) if extra_dim else ())
+
+
+def cuda_project_gemm(x: Tensor, weight: Tensor, bias: Optional[Tensor], key_dim: int, value_dim: int,
+                      extra_dim: int = 0, eps: float = 1e-6, *, enabled: bool = True,
+                      debug_fallback: bool = False) -> Tuple[Tensor, ...]:
+    """cuda_project_split(F.linear(x, weight, bias), ...) as one op: the projection GEMM with the
+    split and the keys' and queries' L2 normalisation as its epilogue (paper_grm.py:491-493,
+    570-574).  Inference only: under autograd F.linear and cuda_project_split run."""
+    needs_grad = torch.is_grad_enabled() and any(
+        t is not None and t.requires_grad for t in (x, weight, bias))
+    if not needs_grad and _run_native("project_gemm", x.device, enabled=enabled, debug_fallback=debug_fallback):
+        k, v, q, e = torch.ops.grm_cuda.project_gemm(x, weight, bias, int(key_dim), int(value_dim), int(extra_dim),
+                                                     float(eps))
+        return (k, v, q) + ((e,) if extra_dim else ())
+    return cuda_project_split(torch.nn.functional.linear(x, weight, bias), key_dim, value_dim, extra_dim, eps,
+                              enabled=enabled, debug_fallback=debug_fallback)
 
 
 def cuda_residual_layer_norm(x: Tensor, residual: Tensor, weight: Optional[Tensor] = None,

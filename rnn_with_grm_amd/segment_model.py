@@ -165,9 +165,8 @@ class LinearMemoryCell(nn.Module):
         joins the same GEMM and its output is returned last."""
         mods = [self.key_proj, self.value_proj, self.query_proj] + ([extra] if extra is not None else [])
         weight, bias = self._concat_params(mods)
-        proj = F.linear(x, weight, bias)
         extra_dim = extra.out_features if extra is not None else 0
-        return cuda_ops.cuda_project_split(proj, self.memory_key_dim, self.hidden_size, extra_dim, _NORM_EPS)
+        return cuda_ops.cuda_project_gemm(x, weight, bias, self.memory_key_dim, self.hidden_size, extra_dim, _NORM_EPS)
 
     def _concat_params(self, mods: List[nn.Linear]) -> Tuple[Tensor, Optional[Tensor]]:
         """The projections' weights and biases concatenated for one GEMM; without autograd

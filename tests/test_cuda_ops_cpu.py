@@ -339,3 +339,21 @@ def test_cpu_archive_cast():
             assert torch.equal(cuda_ops.cuda_archive_cast(x, md, sd), want)
     with pytest.raises(RuntimeError, match="float32"):
         torch.ops.grm_cuda.archive_cast(x.half(), torch.bfloat16, torch.float16)
+
+
+def test_cpu_project_gemm_is_linear_then_split():
+    """project_gemm's CPU kernel and the cuda_ops wrapper are F.linear followed by project_split."""
+    import torch.nn.functional as F
+
+    if not cuda_ops.load_grm_cuda_extension():
+        pytest.skip("extension not built")
+    g = torch.Generator().manual_seed(14)
+    x = torch.randn(3, 5, 16, generator=g)
+    w, b = torch.randn(2 * 8 + 24 + 8, 16, generator=g), torch.randn(2 * 8 + 24 + 8, generator=g)
+    got = torch.ops.grm_cuda.project_gemm(x, w, b, 8, 24, 8, 1e-6)
+    want = torch.ops.grm_cuda.project_split(F.linear(x, w, b), 8, 24, 8, 1e-6)
+    assert all(torch.equal(a, c) for a, c in zip(got, want))
+    wrapped = cuda_ops.cuda_project_gemm(x, w, b, 8, 24, 8, 1e-6)
+    assert len(wrapped) == 4 and all(torch.equal(a, c) for a, c in zip(wrapped, want))
+    with pytest.raises(RuntimeError, match="weight must be"):
+        torch.ops.grm_cuda.project_gemm(x, w[:-1], None, 8, 24, 8, 1e-6)

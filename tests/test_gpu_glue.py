@@ -119,3 +119,56 @@ def test_archive_cast(dev, n):
                 assert out.dtype == sd
                 assert torch.equal(out.float().isnan(), wnan), (md, sd)
                 assert torch.equal(out.view(it)[~wnan], want.view(it)[~wnan]), (md, sd)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("rows,K,dv,de,with_bias", [(32768, 512, 512, 512, False), (1000, 64, 64, 0, True),
+                                                    (37, 128, 128, 64, True), (300, 192, 256, 128, False)])
+def test_project_gemm(dev, dtype, rows, K, dv, de, with_bias):
+    """project_gemm (the projection GEMM with project_split as its epilogue) against F.linear then
+    F.normalize in the same dtype.  The GEMM sums in another order than the library, so an
+    element may round to the neighbouring 16-bit value: values and extra within 2^-7 of each
+    element plus 2^-14 of the tensor's largest magnitude (cancellation near zero), keys and
+    queries within 2^-6 plus 2^-12; and at most 3% of the elements differ at all."""
+    g = torch.Generator().manual_seed(rows + K)
+    dk = 64
+    N = 2 * dk + dv + de
+    x = torch.randn(rows, K, generator=g).to(dtype)
+    w = (torch.randn(N, K, generator=g) / K ** 0.5).to(dtype)
+    b = (0.1 * torch.randn(N, generator=g)).to(dtype) if with_bias else None
+    print(f"project_gemm rows={rows} K={K} dv={dv} de={de} bias={with_bias} {dtype}", flush=True)
+    xd, wd, bd = x.to(dev), w.to(dev), (b.to(dev) if b is not None else None)
+    ext = cuda_ops.extension_module()
+    generic = ext.generic_path_calls()
+    got = capi.project_gemm(xd, wd, bd, dk, dv, de)
+    op = torch.ops.grm_cuda.project_gemm(xd, wd, bd, dk, dv, de, 1e-6)
+    torch.cuda.synchronize()
+    assert ext.generic_path_calls() == generic
+    proj = F.linear(xd, wd, bd)
+    parts = proj.split([dk, dv, dk, de], dim=-1)
+    ref = (F.normalize(parts[0], p=2, dim=-1, eps=1e-6), parts[1], F.normalize(parts[2], p=2, dim=-1, eps=1e-6),
+           parts[3])
+    for name, a_, o_, r_, rel, ab in zip(("keys", "values", "queries", "extra"), got, op, ref,
+                                         (2.0 ** -6, 2.0 ** -7, 2.0 ** -6, 2.0 ** -7),
+                                         (2.0 ** -12, 2.0 ** -14, 2.0 ** -12, 2.0 ** -14)):
+        assert torch.equal(a_, o_), name
+        if r_.numel() == 0:
+            continue
+        a64, r64 = a_.double().cpu(), r_.double().cpu()
+        scale = float(r64.abs().max())
+        assert bool(((a64 - r64).abs() <= rel * r64.abs() + ab * scale).all()), name
+        assert float((a64 != r64).double().mean()) <= 0.03, name
+
+
+def test_project_gemm_shapes_outside_the_kernel(dev):
+    """Shapes the fused kernel does not take (key_dim 32) run the library GEMM and the split's own
+    kernel (no generic call), with the same results as F.linear then project_split."""
+    g = torch.Generator().manual_seed(5)
+    x = torch.randn(50, 64, generator=g).to(torch.bfloat16).to(dev)
+    w = torch.randn(2 * 32 + 96, 64, generator=g).to(torch.bfloat16).to(dev)
+    ext = cuda_ops.extension_module()
+    generic = ext.generic_path_calls()
+    k, v, q, e = torch.ops.grm_cuda.project_gemm(x, w, None, 32, 96, 0, 1e-6)
+    assert ext.generic_path_calls() == generic
+    k2, v2, q2, e2 = torch.ops.grm_cuda.project_split(F.linear(x, w), 32, 96, 0, 1e-6)
+    assert torch.equal(k, k2) and torch.equal(v, v2) and torch.equal(q, q2)
