@@ -752,6 +752,7 @@ def bench_c4_train(torch, dev, steps, warmup):
     ids = torch.randint(0, V, (B, T), generator=g).to(dev)
     targets = torch.roll(ids, -1, dims=1)
     stream = torch.cuda.current_stream(dev)
+    torch.cuda.reset_peak_memory_stats(dev)  # this leg's own peak, not the earlier legs'
 
     def step():
         for p in params:
