@@ -210,6 +210,22 @@ def bench_c2_bwd(torch, dev, steps, warmup):
     return {"ms": ev0.elapsed_time(ev1) / steps, "tokens": BH * T}
 
 
+def near_ties(torch, lib, capi, q, keys, BH, Q, S, D, K, scale, sp):
+    """Rows whose k-th and (k+1)-th routing scores differ by less than 1e-6: one extra
+    top-(k+1) call of the same routing kernel, outside every timed region."""
+    P = lambda t: ctypes.c_void_p(t.data_ptr())  # noqa: E731
+    dev = q.device
+    idx = torch.empty((BH, Q, K + 1), dtype=torch.int64, device=dev)
+    sc = torch.empty((BH, Q, K + 1), dtype=torch.float32, device=dev)
+    gt = torch.empty((BH, Q, K + 1), dtype=torch.float32, device=dev)
+    if lib.grm_hip_topk_route(P(q), P(keys), P(idx), P(sc), P(gt), BH, Q, S, D, capi.BF16, K + 1, scale, 1.0,
+                              sp) != 0:
+        raise RuntimeError(capi.last_error())
+    gap = sc[..., K - 1] - sc[..., K]
+    return {"rows": BH * Q, "gap_below_1e-6": int((gap < 1e-6).sum()), "gap_zero": int((gap == 0).sum()),
+            "min_gap": float(gap.min())}
+
+
 def bench_c3(torch, dev, steps, warmup):
     """Routing over the archive summaries; the fused retrieval (gather_apply + fusion); the
     materialised gather."""
@@ -235,6 +251,7 @@ def bench_c3(torch, dev, steps, warmup):
             raise RuntimeError(capi.last_error())
 
     r_wall, r_per = timed_launches(torch, route, max(3, steps), warmup, stream)
+    ties = near_ties(torch, lib, capi, q, keys, BH, Q, S, D, K, scale, sp)
     out = torch.empty((BH, Q, K, D, D), dtype=torch.float32, device=dev)
 
     def gather():
@@ -309,7 +326,7 @@ def bench_c3(torch, dev, steps, warmup):
     route_bytes = q.numel() * 2 + keys.numel() * 2 + idx.numel() * 8 + 2 * sc.numel() * 4
     gather_bytes = BH * Q * K * D * D * 4 + BH * S * D * D * 4 + idx.numel() * 8
     return {
-        "route": {"ms": statistics.mean(r_per) * 1e3, "bytes": route_bytes,
+        "route": {"ms": statistics.mean(r_per) * 1e3, "bytes": route_bytes, "near_ties": ties,
                   "flops": 2 * BH * Q * S * D},
         "gather_apply": {"ms": statistics.mean(ga_per) * 1e3,
                          "bytes": BH * S * D * D * 4 + BH * Q * K * D * 4 + q.numel() * 2 + idx.numel() * 8,
@@ -497,6 +514,7 @@ def bench_c5(torch, dev, steps, warmup):
 
     n = max(3, min(steps, 10))
     r_wall, r_per = timed_launches(torch, route, n, min(warmup, 2), stream)
+    ties = near_ties(torch, lib, capi, q, summaries, BH, T, S, D, K, 1.0 / D ** 0.5, sp)
     ga_wall, ga_per = timed_launches(torch, gather_apply, n, min(warmup, 2), stream)
     fu_wall, fu_per = timed_launches(torch, fuse, n, min(warmup, 2), stream)
     rf_wall, rf_per = timed_launches(torch, retrieve_fuse, n, min(warmup, 2), stream)
@@ -516,7 +534,7 @@ def bench_c5(torch, dev, steps, warmup):
     upd_bytes = tokens * (2 * D + D) * 2 + tokens * D * 2 + BH * D * D * 4 + BH * S * D * D * 4
     out = {
         "update": {"us": statistics.mean(u_per) * 1e6, "bytes": upd_bytes, "tokens": tokens},
-        "route": {"ms": statistics.mean(r_per) * 1e3, "flops": 2 * tokens * S * D},
+        "route": {"ms": statistics.mean(r_per) * 1e3, "flops": 2 * tokens * S * D, "near_ties": ties},
         "gather_apply": {"ms": statistics.mean(ga_per) * 1e3,
                          "bytes": BH * S * D * D * 4 + tokens * K * D * 4 + q.numel() * 2 + idx.numel() * 8,
                          "flops": 2 * tokens * K * D * D},
@@ -885,7 +903,7 @@ def main() -> int:
         c3 = bench_c3(torch, dev, a.steps, a.warmup)
         r, gth = c3["route"], c3["gather"]
         secondary["c3_topk_route"] = {"ms": round(r["ms"], 4), "GB/s": round(r["bytes"] / r["ms"] / 1e6, 1),
-                                      "TFLOP/s": round(r["flops"] / r["ms"] / 1e9, 2)}
+                                      "TFLOP/s": round(r["flops"] / r["ms"] / 1e9, 2), "near_ties": r["near_ties"]}
         gbs = gth["bytes"] / gth["ms"] / 1e6
         secondary["c3_gather"] = {"ms": round(gth["ms"], 3), "GB/s": round(gbs, 1),
                                   "hbm_frac": round(gbs / HBM_PEAK_GBS, 4),
@@ -928,7 +946,8 @@ def main() -> int:
                     "reference's chunk path); the two-kernel composition (gather_apply float32 rows, then "
                     "fuse_residual) beside it",
             "ms": round(rt5["ms"], 3), "tokens/s": round(rt5["tokens"] / rt5["ms"] * 1e3),
-            "route_ms": round(c5["route"]["ms"], 3), "retrieve_fuse_ms": round(rf5["ms"], 3),
+            "route_ms": round(c5["route"]["ms"], 3), "route_near_ties": c5["route"]["near_ties"],
+            "retrieve_fuse_ms": round(rf5["ms"], 3),
             "retrieve_fuse_roofline": {"bound": "hbm", "achieved": round(rf_gbs, 1), "peak": HBM_PEAK_GBS,
                                        "unit": "GB/s", "frac": round(rf_gbs / HBM_PEAK_GBS, 4),
                                        "algorithmic_bytes": rf5["bytes"],
