@@ -544,6 +544,19 @@ class SegmentRecurrentMemoryModel(nn.Module):
             snaps.append(s2)
         return torch.cat(outs, 1), self._init_memory(B, memory.device, memory.dtype), torch.cat(snaps, 1)
 
+    def _float32_norm_params(self, weight: Optional[Tensor],
+                             bias: Optional[Tensor]) -> Tuple[Optional[Tensor], Optional[Tensor]]:
+        """float32 copies of 16-bit LayerNorm parameters for the fused kernel, made again
+        only when a parameter changed (its storage or its in-place version), so that a
+        forward does not convert them on every call."""
+        key = tuple((t.data_ptr(), t._version, t.dtype) if t is not None else None for t in (weight, bias))
+        cached = getattr(self, "_norm_f32", None)
+        if cached is None or cached[0] != key:
+            cached = (key, None if weight is None else weight.detach().float(),
+                      None if bias is None else bias.detach().float())
+            self._norm_f32 = cached
+        return cached[1], cached[2]
+
     def _retrieve(self, x: Tensor, q: Tensor, q_r: Tensor, h_online: Tensor, states: Tensor, summaries: Tensor,
                   base: int) -> Tensor:
         """Routing, retrieval and fusion for every token at once
@@ -559,9 +572,9 @@ class SegmentRecurrentMemoryModel(nn.Module):
         gates, idx, _ = cuda_ops.cuda_segment_route(q_r, k_r, top_k, seg, base, cap, gu.scale, gu.temperature,
                                                     debug_fallback=self.cuda_cpp_debug_fallback)
         _mark("segment routing (score, top-k, softmax)", x)
-        filled = idx >= 0
         idx0 = idx.clamp(min=0)
         if grad:
+            filled = idx >= 0
             # Differentiable gates: the selected scores again, as torch ops.  All scores
             # as one product (paper_grm.py:573), then the selected ones gathered: the
             # backward is a scatter into [B, T, S] and two GEMMs.  (Indexing k_r by the
@@ -593,9 +606,8 @@ class SegmentRecurrentMemoryModel(nn.Module):
                 # A 16-bit model: retrieval, gate-weighted sum, residual and LayerNorm in one
                 # op; the [B, T, k, H] retrieved rows are kept as row-scaled float16 (relative
                 # rounding 2^-11 of each row's largest value), never as float32.
-                fused = cuda_ops.cuda_retrieve_fuse(states, idx0, q_in, gates.float(), h_online,
-                                                    None if weight is None else weight.float(),
-                                                    None if bias is None else bias.float(), eps,
+                w32, b32 = self._float32_norm_params(weight, bias)
+                fused = cuda_ops.cuda_retrieve_fuse(states, idx0, q_in, gates.float(), h_online, w32, b32, eps,
                                                     debug_fallback=self.cuda_cpp_debug_fallback)
             else:
                 H = h_online.size(-1)
