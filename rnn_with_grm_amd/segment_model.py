@@ -552,8 +552,11 @@ class SegmentRecurrentMemoryModel(nn.Module):
         key = tuple((t.data_ptr(), t._version, t.dtype) if t is not None else None for t in (weight, bias))
         cached = getattr(self, "_norm_f32", None)
         if cached is None or cached[0] != key:
+            # the sources are held too, so that no other tensor can take their addresses
+            # while the copies are in use
+            src = tuple(None if t is None else t.detach() for t in (weight, bias))
             cached = (key, None if weight is None else weight.detach().float(),
-                      None if bias is None else bias.detach().float())
+                      None if bias is None else bias.detach().float(), src)
             self._norm_f32 = cached
         return cached[1], cached[2]
 

@@ -467,3 +467,32 @@ def test_model_forward_graph_capture(dev):
             assert torch.equal(eager, ref)
     assert aux["memory_info"]["recompute_rate"] == aux_ref["memory_info"]["recompute_rate"] == 0.0
     assert aux["num_segments"] == aux_ref["num_segments"]
+
+
+def test_cached_norm_parameters_follow_updates():
+    """The fused retrieval's float32 copies of 16-bit LayerNorm parameters are reused
+    between forwards; an in-place update of a parameter (an optimizer step, a state-dict
+    load) or a new parameter tensor must reach the next forward."""
+    import copy
+
+    torch.manual_seed(5)
+    model = sm.SegmentRecurrentMemoryModel(16, 24, 8, segment_length=4, memory_capacity_segments=8,
+                                           retrieval_top_k=2, memory_key_dim=8, dropout=0.0,
+                                           recomputation_ratio=0.0).to(torch.bfloat16).eval()
+    x = torch.randn(2, 24, 16, generator=torch.Generator().manual_seed(6)).to(torch.bfloat16)
+    norm = model.aggregator.layer_norm
+    with torch.no_grad():
+        model(x, reset_memory=True)
+        assert getattr(model, "_norm_f32", None) is not None, "the fused 16-bit retrieval path did not run"
+        norm.weight.mul_(2.0)
+        norm.bias.add_(0.5)
+        got = model(x, reset_memory=True)[0]
+        fresh = copy.deepcopy(model)
+        fresh._norm_f32 = None
+        ref = fresh(x, reset_memory=True)[0]
+        assert torch.equal(got, ref)
+        norm.weight = torch.nn.Parameter(torch.full_like(norm.weight, 0.25))
+        got = model(x, reset_memory=True)[0]
+        fresh.aggregator.layer_norm.weight = torch.nn.Parameter(torch.full_like(norm.weight, 0.25))
+        fresh._norm_f32 = None
+        assert torch.equal(got, fresh(x, reset_memory=True)[0])
