@@ -20,6 +20,13 @@ def make_chunk_case(T, B=2, H=16, K=8, dtype=torch.float32, seed=0):
     return k, v, q, m
 
 
+@pytest.fixture(autouse=True, scope="module")
+def _extension_loaded():
+    """The tests below call torch.ops.grm_cuda directly, so the extension is
+    loaded before the first of them, whatever order they run in."""
+    assert cuda_ops.load_grm_cuda_extension(), cuda_ops.get_grm_cuda_runtime_status()["load_error"]
+
+
 def np64(t):
     return t.detach().double().numpy()
 
