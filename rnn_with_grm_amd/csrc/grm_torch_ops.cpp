@@ -793,8 +793,17 @@ std::tuple<Tensor, Tensor, Tensor> topk_route_hip(const Tensor& queries, const T
   TORCH_CHECK(top_k >= 1, "topk_route: top_k must be >= 1");
   TORCH_CHECK(temperature > 0, "topk_route: temperature must be > 0");
   const int64_t k = std::min(top_k, keys.size(1));
-  TORCH_CHECK(k == keys.size(1) || k <= 128, "topk_route: top_k beyond 128 (and below n_keys) is not routed "
-              "on the GPU");
+  if (k > 128 && k < keys.size(1)) {
+    // Beyond the select kernels' k: every key's exact score in index order (the
+    // k == n_keys branch), then a stable descending sort on the device, which
+    // orders equal scores by index as the kernels do.  Gates as softmax in float64.
+    auto all = topk_route_hip(queries, keys, keys.size(1), scale, temperature);
+    auto sorted = at::sort(std::get<2>(all), /*stable=*/true, /*dim=*/-1, /*descending=*/true);
+    Tensor sc = std::get<0>(sorted).narrow(-1, 0, k).contiguous();
+    Tensor idx = std::get<1>(all).gather(-1, std::get<1>(sorted).narrow(-1, 0, k)).contiguous();
+    Tensor gt = at::softmax(sc.to(at::kDouble) / temperature, -1).to(at::kFloat);
+    return {gt, idx, sc};
+  }
   c10::OptionalDeviceGuard guard(queries.device());
   auto [q, kk] = route_operands("topk_route", queries, keys);
   const int64_t B = q.size(0), Q = q.size(1), S = kk.size(1), D = q.size(2);

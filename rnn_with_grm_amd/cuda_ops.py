@@ -507,8 +507,9 @@ def cuda_segment_route(queries: Tensor, keys: Tensor, top_k: int, segment_len: i
     Returns (gates, indices, scores), each [B, Q, top_k]; indices are absolute key
     positions, and a window of n <= top_k keys fills slots n.. with index -1,
     score -inf and gate 0."""
-    if _run_native("topk_route", queries.device, enabled=enabled, debug_fallback=debug_fallback,
-                   auto_on_cpu=True):
+    native = _run_native("topk_route", queries.device, enabled=enabled, debug_fallback=debug_fallback,
+                         auto_on_cpu=True)
+    if native and top_k <= 128:
         return torch.ops.grm_cuda.segment_route(queries, keys, int(top_k), int(segment_len), int(base),
                                                 int(capacity), float(scale), float(temperature))
     B, Q, _ = queries.shape
@@ -520,7 +521,8 @@ def cuda_segment_route(queries: Tensor, keys: Tensor, top_k: int, segment_len: i
         lo = max(0, hi - capacity)
         if hi > lo:
             rows = slice(t0, t0 + segment_len)
-            g, i, sc = cuda_topk_route(queries[:, rows], keys[:, lo:hi], top_k, scale, temperature, enabled=False)
+            # top_k beyond the one-launch kernel's 128: each window through topk_route's own op
+            g, i, sc = cuda_topk_route(queries[:, rows], keys[:, lo:hi], top_k, scale, temperature, enabled=native)
             n = g.size(-1)
             gates[:, rows, :n], idx[:, rows, :n], scores[:, rows, :n] = g.float(), i + lo, sc.float()
     return gates, idx, scores

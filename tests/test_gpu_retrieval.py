@@ -355,6 +355,32 @@ def test_segment_route_bit_exact(dev, dtype, B, T, seg, base, cap, S, D, k):
     assert torch.equal(i2, idx) and torch.equal(s2, sc) and torch.equal(g2, gates)
 
 
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_topk_route_beyond_128(dev, dtype):
+    """top_k = 150 of 300 keys (beyond the select kernels' 128, with duplicate keys for
+    ties): every key's exact score, then a stable sort on the device; indices and scores
+    bit-exact against the oracle, no host round trip; and the per-window segment routing
+    built on it matches the oracle's."""
+    g = torch.Generator().manual_seed(15)
+    base = norm(torch.randn(2, 150, 64, generator=g))
+    keys = torch.cat([base, base], dim=1).to(dtype)  # every score appears twice
+    q = norm(torch.randn(2, 70, 64, generator=g)).to(dtype)
+    print(f"topk_route k=150 of 300 {dtype}", flush=True)
+    generic = cuda_ops.extension_module().generic_path_calls()
+    gates, idx, sc = torch.ops.grm_cuda.topk_route(q.to(dev), keys.to(dev), 150, 0.125, 1.0)
+    assert cuda_ops.extension_module().generic_path_calls() == generic
+    og, oi, osc = orc.topk_route(q.float().numpy(), keys.float().numpy(), 150, 0.125)
+    assert np.array_equal(idx.cpu().numpy(), oi)
+    assert np.array_equal(sc.cpu().numpy(), osc)
+    np.testing.assert_allclose(gates.cpu().numpy(), og, rtol=1e-5, atol=1e-6)
+    print(f"segment routing k=150 {dtype}", flush=True)
+    gates, idx, sc = cuda_ops.cuda_segment_route(q.to(dev), keys.to(dev), 150, 2, 100, 180, 0.125)
+    og, oi, osc = orc.segment_route(q.float().numpy(), keys.float().numpy(), 150, 2, 100, 180, 0.125)
+    assert np.array_equal(idx.cpu().numpy(), oi)
+    assert np.array_equal(sc.cpu().numpy(), osc)
+    np.testing.assert_allclose(gates.cpu().numpy(), og, rtol=1e-5, atol=1e-6)
+
+
 def test_topk_route_ties(dev):
     """Duplicate keys give equal scores; the lower index must win every tie."""
     g = torch.Generator().manual_seed(6)

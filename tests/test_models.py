@@ -384,6 +384,45 @@ def test_model_top_k_beyond_32_gpu(dev):
     torch.testing.assert_close(c.cpu(), cr, rtol=1e-4, atol=3e-5)
 
 
+def _topk_beyond_128_model():
+    torch.manual_seed(5)
+    return sm.SegmentRecurrentMemoryModel(16, 24, 8, segment_length=2, memory_capacity_segments=200,
+                                          retrieval_top_k=150, memory_key_dim=8, dropout=0.0,
+                                          recomputation_ratio=0.0)
+
+
+def test_model_top_k_beyond_128_cpu():
+    """retrieval_top_k = 150 over up to 200 archived segments: beyond the one-launch
+    segment routing kernel's k, each window is routed by topk_route's op; matches the
+    PyTorch fallbacks."""
+    model = _topk_beyond_128_model().eval()
+    x = torch.randn(2, 500, 16, generator=torch.Generator().manual_seed(6))
+    with torch.no_grad():
+        out, _, c, _ = model(x, reset_memory=True)
+        model.cuda_cpp_debug_fallback = True
+        ref, _, cr, _ = model(x, reset_memory=True)
+    torch.testing.assert_close(out, ref, rtol=1e-4, atol=1e-5)
+    torch.testing.assert_close(c, cr, rtol=1e-4, atol=1e-5)
+
+
+@pytest.mark.gpu
+def test_model_top_k_beyond_128_gpu(dev):
+    """The same on the GPU: routing with 150 of up to 200 segments per row stays on the device."""
+    from rnn_with_grm_amd import cuda_ops
+
+    model = _topk_beyond_128_model().eval()
+    x = torch.randn(2, 500, 16, generator=torch.Generator().manual_seed(6))
+    print(f"model top_k=150 on {dev}", flush=True)
+    with torch.no_grad():
+        ref, _, cr, _ = model(x, reset_memory=True)
+        gpu = model.to(dev)
+        generic = cuda_ops.extension_module().generic_path_calls()
+        out, _, c, _ = gpu(x.to(dev), reset_memory=True)
+        assert cuda_ops.extension_module().generic_path_calls() == generic
+    torch.testing.assert_close(out.cpu(), ref, rtol=1e-4, atol=3e-5)
+    torch.testing.assert_close(c.cpu(), cr, rtol=1e-4, atol=3e-5)
+
+
 def _bf16_training_grads(dev, dtype):
     """Parameter gradients of one training call of a 2-layer model whose hidden size (64)
     is a multiple of 32 and key size (32) a multiple of 8: in bf16 the scan's backward is
