@@ -72,34 +72,34 @@ def timed_launches(torch, fn, steps: int, warmup: int, stream):
     return wall, [ev0.elapsed_time(ev1) * 1e-3 / steps]
 
 
-def bench_c2(torch, dev, steps, warmup):
+def bench_scan(torch, dev, steps, warmup, BH=64, T=2048, D=128, seed=0, C=64):
+    """One grm_hip_chunk_update_fwd launch per step over BH sequences x T tokens (bf16 q/k/v,
+    fp32 state, chunk 64, the T/64 per-chunk snapshots written), inputs resident and outputs
+    preallocated.  One timed loop of `steps` back-to-back launches after `warmup` untimed ones,
+    read by two clocks: the host clock between two synchronisations (wall time per step) and two
+    HIP events on the kernel's stream around the same launches (average launch duration, with no
+    per-launch event overhead, which is what a kernel trace of these launches reports).  Both
+    come from the same launches because the box's clocks drift under sustained load."""
     from rnn_with_grm_amd import capi
 
     lib = capi.load()
-    k, v, q, m = [t.to(dev) for t in make_c2(dev, torch)]
-    BH, T, D = k.shape
+    k, v, q, m = [t.to(dev) for t in make_c2(dev, torch, BH=BH, T=T, D=D, seed=seed)]
     hidden = torch.empty((BH, T, D), dtype=torch.bfloat16, device=dev)
     mem_out = torch.empty((BH, D, D), dtype=torch.float32, device=dev)
-    snaps = torch.empty((BH, T // 64, D, D), dtype=torch.float32, device=dev)
-    wsb = capi.fwd_workspace_bytes(BH, T, D, D, 64)
+    snaps = torch.empty((BH, T // C, D, D), dtype=torch.float32, device=dev)
+    wsb = capi.fwd_workspace_bytes(BH, T, D, D, C)
     ws = torch.empty(max(wsb // 4, 1), dtype=torch.float32, device=dev)
     stream = torch.cuda.current_stream(dev)
     sp = ctypes.c_void_p(stream.cuda_stream)
     P = lambda t: ctypes.c_void_p(t.data_ptr())  # noqa: E731
     args = (P(k), P(v), P(q), P(m), P(hidden), P(mem_out), P(snaps), P(ws), wsb, BH, T, D, D, capi.BF16, capi.F32,
-            0.97, 64, sp)
+            0.97, C, sp)
 
     def step():
         rc = lib.grm_hip_chunk_update_fwd(*args)
         if rc != 0:
             raise RuntimeError(capi.last_error())
 
-    # One timed loop of K back-to-back steps, read by two clocks: the host clock between
-    # two synchronisations (value) and two HIP events on the kernel's stream around the
-    # same launches (roofline: average launch duration, with no per-launch event overhead,
-    # which is what a kernel trace of these launches reports).  Both come from the same
-    # launches because the box's clocks drift under sustained load (a second loop of the
-    # same kernel right after the first has run up to 20% slower).
     for _ in range(warmup):
         step()
     torch.cuda.synchronize()
@@ -111,53 +111,31 @@ def bench_c2(torch, dev, steps, warmup):
     ev1.record(stream)
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
-    per = [ev0.elapsed_time(ev1) * 1e-3 / steps]
-    return wall, per, (k, v, q, m, hidden, snaps)
-
-
-def bench_n1(torch, dev, steps, warmup):
-    """The north-star shape: B*H = 64 sequences (B=8, H=8) x T = 8192 tokens, d_k = d_v = 128,
-    chunk 64, bf16 q/k/v, fp32 state, the 128 per-chunk snapshots of every sequence written;
-    one grm_hip_chunk_update_fwd launch per step, events around back-to-back launches."""
-    from rnn_with_grm_amd import capi
-
-    lib = capi.load()
-    BH, T, D = 64, 8192, 128
-    k, v, q, m = [t.to(dev) for t in make_c2(dev, torch, BH=BH, T=T, D=D, seed=3)]
-    hidden = torch.empty((BH, T, D), dtype=torch.bfloat16, device=dev)
-    mem_out = torch.empty((BH, D, D), dtype=torch.float32, device=dev)
-    snaps = torch.empty((BH, T // 64, D, D), dtype=torch.float32, device=dev)
-    wsb = capi.fwd_workspace_bytes(BH, T, D, D, 64)
-    ws = torch.empty(max(wsb // 4, 1), dtype=torch.float32, device=dev)
-    stream = torch.cuda.current_stream(dev)
-    sp = ctypes.c_void_p(stream.cuda_stream)
-    P = lambda t: ctypes.c_void_p(t.data_ptr())  # noqa: E731
-    args = (P(k), P(v), P(q), P(m), P(hidden), P(mem_out), P(snaps), P(ws), wsb, BH, T, D, D, capi.BF16, capi.F32,
-            0.97, 64, sp)
-
-    def step():
-        rc = lib.grm_hip_chunk_update_fwd(*args)
-        if rc != 0:
-            raise RuntimeError(capi.last_error())
-
-    for _ in range(warmup):
-        step()
-    torch.cuda.synchronize()
-    ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    ev0.record(stream)
-    for _ in range(steps):
-        step()
-    ev1.record(stream)
-    torch.cuda.synchronize()
     if not (bool(torch.isfinite(snaps[:, -1]).all()) and torch.equal(snaps[:, -1], mem_out)):
-        raise RuntimeError("north-star shape: last snapshot differs from the final state")
-    flops, bytes_ = c2_counts(BH=BH, T=T, dk=D, dv=D)
-    del k, v, q, m, hidden, snaps, ws
-    # The box's rate for a stream as large and as write-heavy: a device copy moving the same
-    # number of bytes (half read, half written; the scan reads 37% and writes 63%).
+        raise RuntimeError(f"scan {BH}x{T}: last snapshot differs from the final state")
+    flops, bytes_ = c2_counts(BH=BH, T=T, dk=D, dv=D, C=C)
+    us = ev0.elapsed_time(ev1) * 1e3 / steps
+    del k, v, q, m, hidden, snaps, ws, mem_out
+    # The box's rate for a stream as large: a device copy moving the same number of bytes
+    # (half read, half written), right after the timed launches.
     copy_us, copy_bytes = copy_rate(torch, dev, bytes_, steps, stream)
-    return {"us": ev0.elapsed_time(ev1) * 1e3 / steps, "tokens": BH * T, "flops": flops, "bytes": bytes_,
+    return {"wall_s": wall, "us": us, "tokens": BH * T, "flops": flops, "bytes": bytes_,
             "copy_us": copy_us, "copy_bytes": copy_bytes}
+
+
+def scan_record(r, what):
+    """The roofline / MFMA / copy-ceiling record of one bench_scan result."""
+    gbs = r["bytes"] / r["us"] / 1e3
+    tf = r["flops"] / r["us"] / 1e6
+    return {"what": what, "us": round(r["us"], 1), "tokens/s": round(r["tokens"] / r["us"] * 1e6),
+            "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                         "frac": round(gbs / HBM_PEAK_GBS, 4), "algorithmic_bytes_per_launch": r["bytes"]},
+            "mfma": {"TFLOP/s": round(tf, 2), "peak": BF16_PEAK_TFLOPS, "frac": round(tf / BF16_PEAK_TFLOPS, 5),
+                     "flops_per_launch": r["flops"]},
+            "copy_ceiling": {"what": "a device copy of the same byte count (half read, half written) right after "
+                                     "the timed launches, events around the same number of copies",
+                             "us": round(r["copy_us"], 1), "GB/s": round(r["copy_bytes"] / r["copy_us"] / 1e3, 1),
+                             "kernel_time_vs_copy": round(r["copy_us"] / r["us"], 4)}}
 
 
 def copy_rate(torch, dev, nbytes, steps, stream):
@@ -702,6 +680,7 @@ def cpu_baseline(torch):
     q1 = nrm(torch.randn(8, 512, 64, generator=g), dim=-1)
     m1 = torch.zeros(8, 64, 64)
     k2, v2, q2, m2 = make_c2(None, torch)
+    kn, vn, qn, mn = make_c2(None, torch, BH=64, T=8192, seed=3)
     # config 3 slice: one of the 64 (b, h) sequences, 256 of its 2048 queries (x 512 to the full batch)
     q3 = nrm(torch.randn(1, 256, 128, generator=g), dim=-1).to(torch.bfloat16)
     keys3 = nrm(torch.randn(1, 256, 128, generator=g), dim=-1).to(torch.bfloat16)
@@ -724,6 +703,8 @@ def cpu_baseline(torch):
         return torch_port.fuse_residual(h, r[0], gates[0], ln_w, ln_b)
 
     legs = [
+        ("n1", "full north-star shape (64 x 8192 tokens, d=128, chunk 64, bf16 inputs, fp32 math, 128 snapshots "
+               "per sequence)", 64 * 8192, 1, lambda: torch_port.segment_scan(kn, vn, qn, mn, 0.97, 64)),
         ("c1", "full config 1 (fp32, 8 x 512 tokens, d=64, chunk 64)", 8 * 512, 1,
          lambda: torch_port.segment_scan(k1, v1, q1, m1, 0.97, 64)),
         ("c2", "full config 2 (64 x 2048 tokens, d=128, bf16 inputs, fp32 math)", 64 * 2048, 1,
@@ -747,11 +728,13 @@ def cpu_baseline(torch):
                          "tokens/s": round(tokens / sec)}
         out[threads] = res
     threads = host["usable"]
-    c2 = out[threads]["c2"]
-    return {"value": c2["tokens/s"], "unit": "tokens/s", "cores": threads, "kind": "port",
-            "sample": f"full config 2 (64 x 2048 tokens, d=128, fp32 math on bf16-rounded inputs), one "
-                      f"_vectorized_chunk_update per 64-token segment, median of {c2['runs']} runs on {threads} "
-                      f"threads (the host's usable CPUs: min of os.cpu_count(), affinity and cgroup quota)",
+    n1 = out[threads]["n1"]
+    return {"value": n1["tokens/s"], "unit": "tokens/s", "cores": threads, "kind": "port",
+            "sample": f"the headline workload in full: north-star shape (64 x 8192 tokens, d=128, chunk 64, fp32 math "
+                      f"on bf16-rounded inputs, the 128 snapshots per sequence kept), one _vectorized_chunk_update "
+                      f"per 64-token segment (cuda_ops.py:218-254), median of {n1['runs']} runs of "
+                      f"{n1['slice_seconds']:.2f} s on {threads} threads (the host's usable CPUs: min of "
+                      f"os.cpu_count(), affinity and cgroup quota)",
             "host": host, "one_thread": out[1], "legs": out[threads]}
 
 
@@ -791,6 +774,26 @@ def bench_c4_train(torch, dev, steps, warmup):
             "peak_gib": torch.cuda.max_memory_allocated(dev) / 2 ** 30}
 
 
+def committed_traffic(name, source):
+    """HBM bytes per launch from a committed counter summary (profiles/<name>: FETCH_SIZE and
+    WRITE_SIZE of the kernel, scaled by a copy of known size), with the sha256 of the kernel
+    source it was measured on.  A summary measured on other source is stale: None, and a note."""
+    import hashlib
+
+    f = REPO / "profiles" / name
+    if not f.exists():
+        return None, f"no counter summary {f.name}"
+    try:
+        rec = json.loads(f.read_text())
+    except ValueError:
+        return None, f"{f.name} unreadable"
+    src = REPO / "rnn_with_grm_amd" / "csrc" / source
+    sha = hashlib.sha256(src.read_bytes()).hexdigest()[:16]
+    if rec.get("source_sha256_16") != sha:
+        return None, f"{f.name} was measured on another {source} ({rec.get('source_sha256_16')} vs {sha})"
+    return rec.get("hbm_bytes_per_launch"), f"profiles/{f.name}: {rec.get('command', '')}"
+
+
 def settle(torch) -> None:
     """Between legs: drain the GPU, hand cached blocks back and idle for two seconds, so
     that each leg starts from the same clock and allocator state (the legs before config
@@ -814,7 +817,9 @@ def main() -> int:
     ap.add_argument("--bwd-only", action="store_true", help="the headline kernel and the config-2 backward")
     ap.add_argument("--route-only", action="store_true", help="the headline kernel and config 3 / 5 routing")
     ap.add_argument("--probe", action="store_true",
-                    help="counter runs: a 256 MiB device copy (calibration) then config-2 launches only")
+                    help="counter runs: a 256 MiB device copy (calibration), then launches of one scan shape only")
+    ap.add_argument("--probe-shape", choices=("n1", "c2", "c5"), default="n1",
+                    help="the scan shape of --probe: the north-star shape (the headline), config 2 or config 5")
     a = ap.parse_args()
     if a.c2_only or a.probe or a.c4_only or a.bwd_only or a.route_only or a.train_only:
         a.no_gather = a.no_cpu = True
@@ -842,47 +847,36 @@ def main() -> int:
         torch.cuda.synchronize()
         log(f"probe copy: {src.numel()} bytes read and written")
         del src, dst
-    log(f"config 2 fused chunk-update+query: warmup {a.warmup}, steps {a.steps}")
-    wall, per, _ = bench_c2(torch, dev, a.steps, a.warmup)
-    flops, bytes_ = c2_counts()
-    t_step = wall / a.steps
-    t_kernel = statistics.mean(per)
-    tokens = 64 * 2048
+        if a.probe_shape != "n1":
+            shape = {"c2": dict(BH=64, T=2048, seed=0), "c5": dict(BH=16, T=65536, seed=5, C=128)}[a.probe_shape]
+            r = bench_scan(torch, dev, a.steps, a.warmup, **shape)
+            log(f"probe {a.probe_shape}: {r['us']:.1f} us/launch, {r['bytes'] / r['us'] / 1e3:.0f} GB/s")
+            return 0
+
+    # Headline: the north-star shape (B=8 x H=8 sequences x 8192 tokens, d = 128, chunk 64).
+    log(f"north-star shape fused chunk-update+query (64 x 8192 tokens): warmup {a.warmup}, steps {a.steps}")
+    n1 = bench_scan(torch, dev, a.steps, a.warmup, BH=64, T=8192, seed=3)
+    t_step = n1["wall_s"] / a.steps
+    t_kernel = n1["us"] * 1e-6
+    tokens, flops, bytes_ = n1["tokens"], n1["flops"], n1["bytes"]
     achieved_gbs = bytes_ / t_kernel / 1e9
     tflops = flops / t_kernel / 1e12
-    log(f"c2: {t_kernel * 1e6:.1f} us/launch (events around {a.steps} launches), {t_step * 1e6:.1f} us/step (wall)")
-    c2_copy_us, c2_copy_bytes = copy_rate(torch, dev, bytes_, a.steps, torch.cuda.current_stream(dev))
-    log(f"c2: a device copy of the same {c2_copy_bytes} bytes: {c2_copy_us:.1f} us "
-        f"({c2_copy_bytes / c2_copy_us / 1e3:.0f} GB/s)")
-
-    traffic = None
-    tfile = REPO / "profiles" / "scan_vsplit_c2_traffic.json"
-    if tfile.exists():
-        try:
-            traffic = json.loads(tfile.read_text()).get("hbm_bytes_per_launch")
-        except Exception:
-            traffic = None
+    log(f"n1: {n1['us']:.1f} us/launch (events around {a.steps} launches), {t_step * 1e6:.1f} us/step (wall), "
+        f"{achieved_gbs:.0f} GB/s; a copy of the same bytes {n1['copy_us']:.1f} us "
+        f"({n1['copy_bytes'] / n1['copy_us'] / 1e3:.0f} GB/s)")
+    traffic, traffic_note = committed_traffic("scan_vsplit_n1_traffic.json", "chunk_scan_vsplit.hip")
 
     secondary = {}
-    if not a.no_gather:
-        log("north-star shape: B*H=64 x T=8192, d=128, chunk 64")
-        n1 = bench_n1(torch, dev, max(3, a.steps // 2), 2)
-        n1_gbs = n1["bytes"] / n1["us"] / 1e3
-        n1_tf = n1["flops"] / n1["us"] / 1e6
-        secondary["n1_update"] = {
-            "what": "north-star shape: fused chunk-update + query, B=8 x H=8 sequences x 8192 tokens, d_k=d_v=128, "
-                    "chunk 64, bf16 q/k/v, fp32 state, 128 snapshots per sequence; one launch per step",
-            "us": round(n1["us"], 1), "tokens/s": round(n1["tokens"] / n1["us"] * 1e6),
-            "roofline": {"bound": "hbm", "achieved": round(n1_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                         "frac": round(n1_gbs / HBM_PEAK_GBS, 4), "algorithmic_bytes_per_launch": n1["bytes"]},
-            "mfma": {"TFLOP/s": round(n1_tf, 2), "peak": BF16_PEAK_TFLOPS, "frac": round(n1_tf / BF16_PEAK_TFLOPS, 5),
-                     "flops_per_launch": n1["flops"]},
-            "copy_ceiling": {"what": "a device copy of the same byte count (read + write) on the same box",
-                             "us": round(n1["copy_us"], 1),
-                             "GB/s": round(n1["copy_bytes"] / n1["copy_us"] / 1e3, 1),
-                             "scan_time_vs_copy": round(n1["copy_us"] / n1["us"], 4)}}
-        log(f"n1: {n1['us']:.1f} us/launch, {n1_gbs:.0f} GB/s, {n1_tf:.1f} TFLOP/s; a copy of the same bytes "
-            f"{n1['copy_us']:.1f} us ({n1['copy_bytes'] / n1['copy_us'] / 1e3:.0f} GB/s)")
+    if not a.probe:
+        log("config 2 fused chunk-update+query (64 x 2048 tokens)")
+        c2 = bench_scan(torch, dev, a.steps, a.warmup, BH=64, T=2048, seed=0)
+        secondary["c2_update"] = scan_record(
+            c2, "BASELINE config 2: fused chunk-update + query, 64 sequences x 2048 tokens, d_k=d_v=128, chunk 64, "
+                "bf16 q/k/v, fp32 state, 32 snapshots per sequence; one launch per step (scan_vsplit_kernel)")
+        c2_tr, c2_note = committed_traffic("scan_vsplit_c2_traffic.json", "chunk_scan_vsplit.hip")
+        secondary["c2_update"]["roofline"]["traffic"] = c2_tr
+        secondary["c2_update"]["roofline"]["traffic_note"] = c2_note
+        log(f"c2: {c2['us']:.1f} us/launch, {c2['bytes'] / c2['us'] / 1e3:.0f} GB/s")
     if a.route_only:
         log("routing only: config 3 and config 5")
         for label, r in bench_routes(torch, dev, a.steps, a.warmup).items():
@@ -1014,10 +1008,10 @@ def main() -> int:
 
     cpu = None
     if not a.no_cpu:
-        log("cpu baseline (torch-CPU port: configs 1 and 2 full, configs 3 and 5 slices)")
+        log("cpu baseline (torch-CPU port: north-star shape, configs 1 and 2 full, configs 3 and 5 slices)")
         cpu = cpu_baseline(torch)
         log(f"cpu: {cpu['value']:.3e} tokens/s on {cpu['cores']} threads ({cpu['host']}); one thread "
-            f"{cpu['one_thread']['c2']['tokens/s']:.3e}")
+            f"{cpu['one_thread']['n1']['tokens/s']:.3e}")
 
     line = {
         "metric": METRIC,
@@ -1032,20 +1026,21 @@ def main() -> int:
         "vs_baseline": None,
         "dtype": "bf16",
         "data": "synthetic (seeded N(0,1) q,k,v with q,k L2-normalised, state N(0,0.02))",
-        "config": {"workload": "BASELINE config 2: fused chunk-update + query, bf16 q/k/v, fp32 state, "
-                               "64 sequences (B*H) x 2048 tokens, d_k=d_v=128, chunk 64, 32 snapshots per sequence",
-                   "global_batch": 64, "seq_len": 2048, "parallelism": "single GPU"},
+        "config": {"workload": "north-star shape (BASELINE north_star): fused chunk-update + query, B=8 x H=8 = 64 "
+                               "sequences x 8192 tokens, d_k=d_v=128, chunk 64, bf16 q/k/v, fp32 state, 128 "
+                               "snapshots per sequence",
+                   "global_batch": 64, "seq_len": 8192, "parallelism": "single GPU"},
         "roofline": {"bound": "hbm", "achieved": round(achieved_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(achieved_gbs / HBM_PEAK_GBS, 4), "traffic": traffic,
+                     "frac": round(achieved_gbs / HBM_PEAK_GBS, 4), "traffic": traffic, "traffic_note": traffic_note,
                      "kernel": "scan_vsplit_kernel<BF16,128,4>: the one launch of a grm_hip_chunk_update_fwd call",
                      "algorithmic_bytes_per_launch": bytes_,
                      "kernel_us": round(t_kernel * 1e6, 2),
                      "copy_ceiling": {"what": "a device copy of the same byte count (half read, half written) "
                                               "right after the timed launches, events around the same number of "
                                               "copies",
-                                      "us": round(c2_copy_us, 2),
-                                      "GB/s": round(c2_copy_bytes / c2_copy_us / 1e3, 1),
-                                      "kernel_time_vs_copy": round(c2_copy_us / (t_kernel * 1e6), 4)},
+                                      "us": round(n1["copy_us"], 2),
+                                      "GB/s": round(n1["copy_bytes"] / n1["copy_us"] / 1e3, 1),
+                                      "kernel_time_vs_copy": round(n1["copy_us"] / (t_kernel * 1e6), 4)},
                      "mfma": {"TFLOP/s": round(tflops, 2), "peak": BF16_PEAK_TFLOPS,
                               "frac": round(tflops / BF16_PEAK_TFLOPS, 5), "flops_per_launch": flops}},
         "cpu_baseline": cpu,

@@ -334,3 +334,99 @@ def test_c4_model_forward_tracks_float32(dev):
     print(f"config 4 model bf16 vs fp32: relative L2 {rel:.3e}, tokens beyond 0.1: {frac_far:.4f}", flush=True)
     assert rel < 5e-2, rel
     assert frac_far < 0.02, frac_far
+
+
+# ---------------------------------------------------------------- config 1
+def c1_inputs():
+    """Config 1 exactly: fp32, B=2 x H=4 -> 8 sequences, T=512, d_k=d_v=64, q, k, v ~ N(0,1) from
+    seed 0 (drawn in that order) with q and k L2-normalised per row, zero initial state."""
+    g = torch.Generator().manual_seed(0)
+    q = nrm(torch.randn(2, 4, 512, 64, generator=g)).reshape(8, 512, 64)
+    k = nrm(torch.randn(2, 4, 512, 64, generator=g)).reshape(8, 512, 64)
+    v = torch.randn(2, 4, 512, 64, generator=g).reshape(8, 512, 64)
+    m = torch.zeros(8, 64, 64)
+    return k, v, q, m
+
+
+def test_config1_hip_path(dev):
+    """Config 1 on the HIP path, against the double-precision oracle at 1e-5 (rtol and atol), every
+    sequence and every element: the C ABI with 64-token snapshots, torch.ops.grm_cuda's
+    chunk_update_forward (the reference's op, one call over all 512 tokens), cuda_segment_scan, and
+    the reference model's granularity, cuda_chunk_update once per 64-token chunk carrying the
+    state.  The native kernels must run (launch counter), with no generic-path call."""
+    from rnn_with_grm_amd import cuda_ops
+
+    k, v, q, m = c1_inputs()
+    rh, rm, rs = orc.chunk_update_seq(k.double().numpy(), v.double().numpy(), q.double().numpy(),
+                                      m.double().numpy(), 0.97, 64)
+    kd, vd, qd, md = k.to(dev), v.to(dev), q.to(dev), m.to(dev)
+    ext = cuda_ops.extension_module()
+    launches, generic = ext.hip_launch_count(), ext.generic_path_calls()
+    print("config 1: fp32 8 x 512, d=64, chunk 64", flush=True)
+    outs = {}
+    outs["capi"] = capi.chunk_update_fwd(kd, vd, qd, md, 0.97, 64)
+    h, mo, aux = torch.ops.grm_cuda.chunk_update_forward(kd, vd, qd, md, 0.97)
+    outs["op"] = (h, mo, None)
+    outs["segment_scan"] = cuda_ops.cuda_segment_scan(kd, vd, qd, md, 0.97, 64)
+    state, hs, snaps = md, [], []
+    for t0 in range(0, 512, 64):
+        hh, state = cuda_ops.cuda_chunk_update(kd[:, t0:t0 + 64], vd[:, t0:t0 + 64], qd[:, t0:t0 + 64], state, 0.97)
+        hs.append(hh)
+        snaps.append(state)
+    outs["per_chunk"] = (torch.cat(hs, 1), state, torch.stack(snaps, 1))
+    torch.cuda.synchronize()
+    assert ext.hip_launch_count() > launches and ext.generic_path_calls() == generic
+    for name, (hid, mout, sn) in outs.items():
+        assert hid.dtype == torch.float32 and mout.dtype == torch.float32
+        np.testing.assert_allclose(hid.cpu().double().numpy(), rh, rtol=1e-5, atol=1e-5, err_msg=f"{name} hidden")
+        np.testing.assert_allclose(mout.cpu().double().numpy(), rm, rtol=1e-5, atol=1e-5, err_msg=f"{name} memory")
+        if sn is not None:
+            assert sn.shape == (8, 8, 64, 64)
+            np.testing.assert_allclose(sn.cpu().double().numpy(), rs, rtol=1e-5, atol=1e-5,
+                                       err_msg=f"{name} snapshots")
+
+
+# ---------------------------------------------------------------- config 3, fused retrieval
+def test_config3_retrieve_fuse(dev):
+    """The launch the bench times for config 3's fused retrieval, at its geometry: 64 sequences x
+    2048 bf16 queries, S=256 fp32 128x128 states, top-8 routing, h_online = M_online q, residual +
+    LayerNorm (affine).  Four whole sequences (all 2048 queries each) element by element against
+    the oracle's gather -> apply -> residual + LayerNorm in double precision at rtol 2e-2 /
+    atol 2e-3 and relative L2 1e-3; the routing of those sequences bit-exact against the
+    oracle's; every sequence against the float32 two-kernel composition."""
+    BH, Q, S, D, K = 64, 2048, 256, 128, 8
+    g = torch.Generator().manual_seed(1)
+    q = nrm(torch.randn(BH, Q, D, generator=g)).to(torch.bfloat16)
+    keys = nrm(torch.randn(BH, S, D, generator=g)).to(torch.bfloat16)
+    states = torch.randn(BH, S, D, D, generator=g) * 0.02
+    online = torch.randn(BH, D, D, generator=g) * 0.02
+    w = 1 + 0.1 * torch.randn(D, generator=g)
+    bias = 0.1 * torch.randn(D, generator=g)
+    qd, kd, sd = q.to(dev), keys.to(dev), states.to(dev)
+    h = torch.bmm(qd.float(), online.to(dev).transpose(1, 2).contiguous())       # h_online = M_online q
+    print("config 3 retrieve_fuse: 64 x 2048 queries, S=256, k=8", flush=True)
+    gates, idx, _ = capi.topk_route(qd, kd, K, 1.0 / D ** 0.5)
+    fused = capi.retrieve_fuse(sd, idx, qd, gates, h, w.to(dev), bias.to(dev))
+    rows = capi.gather_apply(sd, idx, qd, dtype=torch.float32)
+    comp = capi.fuse_residual(h.view(BH * Q, D), rows.view(BH * Q, K, D), gates.view(BH * Q, K), w.to(dev),
+                              bias.to(dev)).view(BH, Q, D)
+    torch.cuda.synchronize()
+    del rows
+    torch.testing.assert_close(fused, comp, rtol=2e-3, atol=2e-3)
+    hc, gc, ic = h.cpu().double().numpy(), gates.cpu().double().numpy(), idx.cpu().numpy()
+    for b in (0, 21, 42, 63):
+        og, oi, _ = orc.topk_route(q[b:b + 1].float().numpy(), keys[b:b + 1].float().numpy(), K, 1.0 / D ** 0.5)
+        assert np.array_equal(ic[b:b + 1], oi), f"routing of sequence {b}"
+        ref = np.empty((Q, D))
+        for q0 in range(0, Q, 256):
+            gathered, bad = orc.gather(states[b:b + 1].double().numpy(), ic[b:b + 1, q0:q0 + 256])
+            assert bad == 0
+            r = orc.apply_query(gathered, q[b:b + 1, q0:q0 + 256].double().numpy())[0]
+            ref[q0:q0 + 256] = orc.fuse_residual(hc[b, q0:q0 + 256], r, gc[b, q0:q0 + 256], w.double().numpy(),
+                                                 bias.double().numpy())
+        got = fused[b].cpu().double().numpy()
+        np.testing.assert_allclose(got, ref, rtol=2e-2, atol=2e-3, err_msg=f"retrieve_fuse sequence {b}")
+        rel = np.linalg.norm(got - ref) / np.linalg.norm(ref)
+        print(f"config 3 retrieve_fuse sequence {b}: relative L2 {rel:.3e}, max abs {np.abs(got - ref).max():.3e}",
+              flush=True)
+        assert rel < 1e-3, rel
