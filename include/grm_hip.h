@@ -87,8 +87,9 @@ int64_t grm_hip_chunk_update_fwd_workspace(int64_t batch, int64_t seq_len, int64
  * that forbid hipMalloc).  No counterpart in the reference.
  * Same arguments and results as grm_hip_chunk_update_fwd minus the workspace:
  * the time-split scratch is a fixed device array inside the library of
- * GRM_HIP_NOALLOC_SCRATCH_BYTES per GPU, held from the first call on a GPU
- * until the process ends.  Calls whose sizes need more time-split scratch than
+ * GRM_HIP_NOALLOC_SCRATCH_BYTES per GPU, resident on every GPU where the
+ * library's scan kernels are loaded (whether or not this entry point is ever
+ * called) until the process ends.  Calls whose sizes need more time-split scratch than
  * that (grm_hip_chunk_update_fwd_workspace() above the limit) are rejected with
  * GRM_HIP_EINVAL and a message.  Every call on one GPU shares that GPU's
  * scratch: calls that overlap on one GPU (different streams, or host threads

@@ -274,7 +274,16 @@ class DeviceSegmentArchive(nn.Module):
                                           debug_fallback=cuda_cpp_debug_fallback).to(device)
 
     # ------------------------------------------------------------- reporting
+    def refresh_counters(self) -> None:
+        """Read the counter buffers again at the next report.  The host mirror advances when
+        Python code runs a forward; a captured graph replayed N times advances the device
+        buffers N times and the mirror not at all, so call this after replaying a graph
+        that contains a forward."""
+        self._host_counts = None
+
     def get_recompute_rate(self) -> float:
+        """total_recomputed / total_retrieved from the host mirror (no device read), or from
+        the buffers after a state-dict load or refresh_counters()."""
         if self._host_counts is None:
             self._host_counts = [int(self.total_retrieved.item()), int(self.total_recomputed.item())]
         total, recomputed = self._host_counts

@@ -980,3 +980,29 @@ def test_bucket_order_does_not_reach_outputs(dev):
             torch.cuda.synchronize()
             for a, b in zip(first, again):
                 assert torch.equal(a, b)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16])
+def test_apply_degenerate_shapes_clear_outputs(dev, dtype):
+    """key_dim 0 (apply_query forward) and no routes (apply_query backward) clear the output with
+    the library's fill kernel, not a memset: buffers filled with 7 before the call read zero after
+    it, in every dtype, with odd element counts."""
+    import ctypes
+
+    lib = capi.load()
+    sp = ctypes.c_void_p(torch.cuda.current_stream(dev).cuda_stream)
+    P = lambda t: ctypes.c_void_p(t.data_ptr())  # noqa: E731
+    B, Q, R, H = 3, 5, 2, 7
+    dummy = torch.zeros(8, dtype=dtype, device=dev)  # inputs of zero elements, never read
+    mem, q = dummy, dummy
+    out = torch.full((B, Q, R, H), 7.0, dtype=dtype, device=dev)
+    rc = lib.grm_hip_apply_query_fwd(P(mem), P(q), P(out), B, Q, R, H, 0, capi.dtype_code(dtype), sp)
+    assert rc == 0, capi.last_error()
+    K = 9
+    q = torch.randn(B, Q, K, device=dev).to(dtype)
+    gq = torch.full((B, Q, K), 7.0, dtype=dtype, device=dev)
+    rc = lib.grm_hip_apply_query_bwd(P(dummy), P(dummy), P(q), P(dummy), P(gq), B, Q, 0, H, K, capi.dtype_code(dtype),
+                                     sp)
+    assert rc == 0, capi.last_error()
+    torch.cuda.synchronize()
+    assert int(torch.count_nonzero(out)) == 0 and int(torch.count_nonzero(gq)) == 0

@@ -506,6 +506,12 @@ def test_model_forward_graph_capture(dev):
             assert torch.equal(eager, ref)
     assert aux["memory_info"]["recompute_rate"] == aux_ref["memory_info"]["recompute_rate"] == 0.0
     assert aux["num_segments"] == aux_ref["num_segments"]
+    # replays advance the device counters only; refresh_counters() makes the next report read them
+    for layer in model.layers:
+        bank = layer.memory_bank
+        bank.refresh_counters()
+        assert bank.get_recompute_rate() == 0.0
+        assert bank._host_counts[0] == int(bank.total_retrieved.item()) > 0
 
 
 def test_cached_norm_parameters_follow_updates():
