@@ -315,6 +315,28 @@ int grm_hip_project_gemm(const void* x, const void* weight, const void* bias, vo
                          int64_t value_dim, int64_t extra_dim, int dtype, float eps, void* stream);
 
 /*
+ * The layer's output side in one kernel:
+ *   y   = x weight^T + bias, rounded to dtype (F.linear's output);
+ *   s   = y + residual, rounded to dtype (the torch add);
+ *   out = LayerNorm(s) over the out_dim columns, statistics in float32,
+ *         times ln_weight plus ln_bias (param_dtype; NULL for none).
+ *   (reference grm/core/paper_grm.py:709: output_proj, then
+ *   grm/core/multilayer_grm.py:92-97: layer_norm(outputs + x); a library GEMM
+ *   and torch ops in the reference.)
+ * x [rows, in_dim], weight [out_dim, in_dim], bias [out_dim] or NULL, residual
+ * and out [rows, out_dim], all dtype (f16 or bf16).  For the backward, pre
+ * (NULL: not written) receives s, and mean / rstd (float32 [rows], both or
+ * neither) the LayerNorm's row statistics, as aten's native_layer_norm saves
+ * them.
+ * Limits: in_dim a positive multiple of 64, out_dim a positive multiple of 64
+ * and at most 512, weight under 2 GiB, 16-byte aligned buffers.  ABI 108.
+ */
+int grm_hip_linear_residual_layer_norm(const void* x, const void* weight, const void* bias, const void* residual,
+                                       const void* ln_weight, const void* ln_bias, void* out, void* pre,
+                                       float* mean, float* rstd, int64_t rows, int64_t in_dim, int64_t out_dim,
+                                       int dtype, int param_dtype, float eps, void* stream);
+
+/*
  * Archive form of float32 states: out[i] = storage(model(states[i])), each
  * value rounded (to nearest even) to model_dtype and then to storage_dtype,
  * which is what push() stores for a state the model computed

@@ -48,6 +48,8 @@ SIGNATURES = {
     "grm_hip_residual_layer_norm": (_C, [_P, _P, _P, _P, _P, _I, _I, _C, _C, ctypes.c_float, _P]),
     "grm_hip_archive_cast": (_C, [_P, _P, _I, _C, _C, _P]),
     "grm_hip_project_gemm": (_C, [_P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _C, ctypes.c_float, _P]),
+    "grm_hip_linear_residual_layer_norm": (_C, [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _C, _C,
+                                                ctypes.c_float, _P]),
     "grm_hip_retrieve_fuse": (_C, [_P, _P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _C, _C, _C,
                                    ctypes.c_float, _P, _P]),
     "grm_hip_topk_route": (_C, [_P, _P, _P, _P, _P, _I, _I, _I, _I, _C, _I, ctypes.c_float, ctypes.c_float, _P]),
@@ -314,6 +316,25 @@ def project_gemm(x, weight, bias, key_dim: int, value_dim: int, extra_dim: int =
                                      dtype_code(x.dtype), float(eps), _stream(x))
     _check(rc, "grm_hip_project_gemm")
     return k, v, q, e
+
+
+def linear_residual_layer_norm(x, weight, bias, residual, ln_weight=None, ln_bias=None, eps: float = 1e-5,
+                               save: bool = False):
+    """LayerNorm(round(x weight^T + bias) + residual) in one kernel.  Returns out, or with save
+    (out, pre, mean, rstd): the LayerNorm input and its float32 row statistics."""
+    K, N = x.shape[-1], weight.shape[0]
+    rows = x.numel() // K if K else 0
+    out = torch.empty(x.shape[:-1] + (N,), dtype=x.dtype, device=x.device)
+    pre = torch.empty_like(out) if save else None
+    mean = torch.empty(rows, dtype=torch.float32, device=x.device) if save else None
+    rstd = torch.empty(rows, dtype=torch.float32, device=x.device) if save else None
+    pd = dtype_code(ln_weight.dtype) if ln_weight is not None else dtype_code(x.dtype)
+    rc = load().grm_hip_linear_residual_layer_norm(_ptr(x), _ptr(weight), _ptr(bias), _ptr(residual),
+                                                   _ptr(ln_weight), _ptr(ln_bias), _ptr(out), _ptr(pre), _ptr(mean),
+                                                   _ptr(rstd), rows, K, N, dtype_code(x.dtype), pd, float(eps),
+                                                   _stream(x))
+    _check(rc, "grm_hip_linear_residual_layer_norm")
+    return (out, pre, mean, rstd) if save else out
 
 
 def archive_cast(states, model_dtype, storage_dtype, out=None):

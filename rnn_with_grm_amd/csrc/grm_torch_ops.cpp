@@ -2,7 +2,7 @@
 //
 // The five schemas are the reference's, character for character
 // (reference grm/csrc/bindings.cpp:5-11), so grm.core.cuda_ops and every model
-// above it bind to this library unchanged.  Twelve more ops live in the same
+// above it bind to this library unchanged.  Fourteen more ops live in the same
 // namespace: segment_scan_forward (whole-sequence update with per-segment
 // state snapshots), topk_route (score -> top-k -> softmax), segment_route (the
 // same routing for every segment of a sequence against the archive as it
@@ -11,7 +11,9 @@
 // sum and fuse_residual in one call), the layer glue project_split (the
 // projection's split with L2-normalised keys and queries),
 // residual_layer_norm (the block's LayerNorm(out + x)), project_gemm (the
-// projection GEMM with project_split as its epilogue) and archive_cast (the
+// projection GEMM with project_split as its epilogue),
+// linear_residual_layer_norm (the output projection GEMM with the block's
+// residual add and LayerNorm as its epilogue) and archive_cast (the
 // archive's stored form of float32 states), and three gradients
 // without gathered states: apply_query_backward_queries,
 // gather_apply_backward_queries (one gradient row per pair) and
@@ -474,6 +476,24 @@ Tensor residual_layer_norm_generic(const Tensor& x, const Tensor& residual, cons
   TORCH_CHECK(x.sizes() == residual.sizes() && x.dim() >= 1, "residual_layer_norm: x and residual must match");
   return at::layer_norm(x + residual, {x.size(-1)}, weight.has_value() ? *weight : Tensor(),
                         bias.has_value() ? *bias : Tensor(), eps);
+}
+
+// linear_residual_layer_norm: the layer's output projection and its block output,
+// layer_norm(linear(x, weight, bias) + residual) (paper_grm.py:709,
+// multilayer_grm.py:92-97).  With save, also the LayerNorm input and its float32
+// row statistics (native_layer_norm's saved tensors, flattened to [rows]).
+std::tuple<Tensor, Tensor, Tensor, Tensor> linear_residual_layer_norm_generic(
+    const Tensor& x, const Tensor& weight, const c10::optional<Tensor>& bias, const Tensor& residual,
+    const c10::optional<Tensor>& ln_weight, const c10::optional<Tensor>& ln_bias, double eps, bool save) {
+  TORCH_CHECK(x.dim() >= 1 && weight.dim() == 2 && weight.size(1) == x.size(-1) && residual.dim() == x.dim() &&
+                  residual.size(-1) == weight.size(0) && residual.numel() / residual.size(-1) == x.numel() / x.size(-1),
+              "linear_residual_layer_norm: weight must be [out_dim, in_dim] and residual [..., out_dim] like x");
+  const Tensor s = at::linear(x, weight, bias.has_value() ? *bias : Tensor()) + residual;
+  const Tensor w = ln_weight.has_value() ? *ln_weight : Tensor(), b = ln_bias.has_value() ? *ln_bias : Tensor();
+  if (!save) return {at::layer_norm(s, {s.size(-1)}, w, b, eps), Tensor(), Tensor(), Tensor()};
+  auto res = at::native_layer_norm(s, {s.size(-1)}, w, b, eps);
+  return {std::get<0>(res), s, std::get<1>(res).reshape({-1}).to(at::kFloat),
+          std::get<2>(res).reshape({-1}).to(at::kFloat)};
 }
 
 // archive_cast: float32 states rounded to the model dtype, then to the storage
@@ -1098,6 +1118,53 @@ Tensor residual_layer_norm_hip(const Tensor& x, const Tensor& residual, const c1
   return out;
 }
 
+std::tuple<Tensor, Tensor, Tensor, Tensor> linear_residual_layer_norm_hip(
+    const Tensor& x, const Tensor& weight, const c10::optional<Tensor>& bias, const Tensor& residual,
+    const c10::optional<Tensor>& ln_weight, const c10::optional<Tensor>& ln_bias, double eps, bool save) {
+  TORCH_CHECK(x.dim() >= 1 && weight.dim() == 2 && weight.size(1) == x.size(-1) && residual.dim() == x.dim() &&
+                  residual.size(-1) == weight.size(0) && residual.numel() / residual.size(-1) == x.numel() / x.size(-1),
+              "linear_residual_layer_norm: weight must be [out_dim, in_dim] and residual [..., out_dim] like x");
+  const bool has_b = bias.has_value() && bias->defined();
+  const bool has_w = ln_weight.has_value() && ln_weight->defined();
+  const bool has_lb = ln_bias.has_value() && ln_bias->defined();
+  const int dt = dtype_code(x.scalar_type());
+  const int pd = has_w ? dtype_code(ln_weight->scalar_type()) : dt;
+  const int64_t K = x.size(-1), N = weight.size(0);
+  const int64_t rows = K > 0 ? x.numel() / K : 0;
+  bool ok = same_cuda_device({&x, &weight, &residual}) && (dt == 1 || dt == 2) &&
+            weight.scalar_type() == x.scalar_type() && residual.scalar_type() == x.scalar_type() && pd >= 0 &&
+            K % 64 == 0 && K > 0 && N % 64 == 0 && N > 0 && N <= 512 && weight.numel() * 2 <= INT32_MAX;
+  if (has_b) ok = ok && bias->is_cuda() && bias->scalar_type() == x.scalar_type() && bias->numel() == N;
+  if (has_w) ok = ok && ln_weight->is_cuda() && ln_weight->numel() == N;
+  if (has_lb) ok = ok && has_w && ln_bias->is_cuda() && ln_bias->numel() == N &&
+                   ln_bias->scalar_type() == ln_weight->scalar_type();
+  if (!ok) {
+    if (x.is_cuda()) g_generic_calls.fetch_add(1);
+    return linear_residual_layer_norm_generic(x, weight, bias, residual, ln_weight, ln_bias, eps, save);
+  }
+  c10::OptionalDeviceGuard guard(x.device());
+  Tensor xc = x.contiguous(), wc = weight.contiguous(), rc = residual.contiguous();
+  Tensor bc = has_b ? bias->contiguous() : Tensor();
+  Tensor lw = has_w ? ln_weight->contiguous() : Tensor(), lb = has_lb ? ln_bias->contiguous() : Tensor();
+  if (!aligned16(xc)) xc = xc.clone();
+  if (!aligned16(wc)) wc = wc.clone();
+  if (!aligned16(rc)) rc = rc.clone();
+  if (has_w && !aligned16(lw)) lw = lw.clone();
+  if (has_lb && !aligned16(lb)) lb = lb.clone();
+  Tensor out = at::empty_like(rc);
+  Tensor pre = save ? at::empty_like(rc) : Tensor();
+  Tensor mean = save ? at::empty({rows}, xc.options().dtype(at::kFloat)) : Tensor();
+  Tensor rstd = save ? at::empty({rows}, xc.options().dtype(at::kFloat)) : Tensor();
+  check_rc(grm_hip_linear_residual_layer_norm(
+               xc.data_ptr(), wc.data_ptr(), has_b ? bc.data_ptr() : nullptr, rc.data_ptr(),
+               has_w ? lw.data_ptr() : nullptr, has_lb ? lb.data_ptr() : nullptr, out.data_ptr(),
+               save ? pre.data_ptr() : nullptr, save ? mean.data_ptr<float>() : nullptr,
+               save ? rstd.data_ptr<float>() : nullptr, rows, K, N, dt, pd, static_cast<float>(eps),
+               current_stream(xc)),
+           "linear_residual_layer_norm");
+  return {out, pre, mean, rstd};
+}
+
 // CPU-key wrappers for the generic forms.
 std::tuple<Tensor, Tensor, Tensor, Tensor> chunk_update_backward_cpu(
     const Tensor& grad_hidden, const Tensor& grad_memory_out, const Tensor& keys,
@@ -1147,6 +1214,8 @@ TORCH_LIBRARY(grm_cuda, m) {
   m.def("archive_cast(Tensor states, ScalarType model_dtype, ScalarType storage_dtype) -> Tensor");
   m.def("project_gemm(Tensor x, Tensor weight, Tensor? bias, int key_dim, int value_dim, int extra_dim, float eps) "
         "-> (Tensor, Tensor, Tensor, Tensor)");
+  m.def("linear_residual_layer_norm(Tensor x, Tensor weight, Tensor? bias, Tensor residual, Tensor? ln_weight, "
+        "Tensor? ln_bias, float eps, bool save) -> (Tensor out, Tensor pre, Tensor mean, Tensor rstd)");
 }
 
 TORCH_LIBRARY_IMPL(grm_cuda, CPU, m) {
@@ -1168,6 +1237,7 @@ TORCH_LIBRARY_IMPL(grm_cuda, CPU, m) {
   m.impl("residual_layer_norm", grm::residual_layer_norm_generic);
   m.impl("archive_cast", grm::archive_cast_generic);
   m.impl("project_gemm", grm::project_gemm_generic);
+  m.impl("linear_residual_layer_norm", grm::linear_residual_layer_norm_generic);
 }
 
 TORCH_LIBRARY_IMPL(grm_cuda, CUDA, m) {
@@ -1189,6 +1259,7 @@ TORCH_LIBRARY_IMPL(grm_cuda, CUDA, m) {
   m.impl("residual_layer_norm", grm::residual_layer_norm_hip);
   m.impl("archive_cast", grm::archive_cast_hip);
   m.impl("project_gemm", grm::project_gemm_hip);
+  m.impl("linear_residual_layer_norm", grm::linear_residual_layer_norm_hip);
 }
 
 PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {

@@ -39,7 +39,8 @@ SCHEMA_OPS = (
 )
 EXTRA_OPS = ("segment_scan_forward", "topk_route", "fuse_residual", "gather_apply", "segment_route",
              "retrieve_fuse", "project_split", "residual_layer_norm", "gather_apply_backward_queries",
-             "gather_apply_backward_tokens", "apply_query_backward_queries", "archive_cast", "project_gemm")
+             "gather_apply_backward_tokens", "apply_query_backward_queries", "archive_cast", "project_gemm",
+             "linear_residual_layer_norm")
 
 # Environment variables of the reference (cuda_ops.py:26-32): one per op and a global one.
 GLOBAL_POLICY_ENV = "GRM_CUDA_KERNEL_POLICY"
@@ -621,18 +622,83 @@ def cuda_project_split(proj: Tensor, key_dim: int, value_dim: int, extra_dim: in
     return (k, parts[1], q) + ((parts[3],) if extra_dim else ())
 
 
+class _ProjectGemmFn(torch.autograd.Function):
+    """project_gemm under autograd: the fused GEMM + split + normalise forward; the backward
+    takes the normalisation's gradient in float32 (dp = (dy - y (y . dy)) / ||p||, or dy / eps
+    where the norm is clamped: F.normalize's derivative) from the key and query projections'
+    norms, recomputed with two GEMMs of key_dim columns, then the GEMM's gradients on the
+    library (dx = dP W, dW = dP^T x, db = sum dP)."""
+
+    @staticmethod
+    def forward(ctx, x, weight, bias, key_dim, value_dim, extra_dim, eps):
+        k, v, q, e = torch.ops.grm_cuda.project_gemm(x, weight, bias, key_dim, value_dim, extra_dim, eps)
+        ctx.save_for_backward(x, weight, bias)
+        ctx.dims = (key_dim, value_dim, extra_dim, eps)
+        return k, v, q, e
+
+    @staticmethod
+    def backward(ctx, dk, dv, dq, de):
+        x, weight, bias = ctx.saved_tensors
+        dkd, dvd, ded, eps = ctx.dims
+        K = x.size(-1)
+        x2 = x.reshape(-1, K)
+        rows = x2.size(0)
+        dt = x.dtype
+
+        def grad_or_zeros(g, d):
+            return torch.zeros(rows, d, dtype=dt, device=x.device) if g is None else g.reshape(rows, d)
+
+        def normalize_grad(lo, g):
+            p = torch.nn.functional.linear(x2, weight[lo:lo + dkd], None if bias is None else bias[lo:lo + dkd])
+            p = p.float()
+            norm = p.norm(dim=-1, keepdim=True)
+            den = norm.clamp_min(eps)
+            y = p / den
+            gf = g.float()
+            dp = torch.where(norm > eps, (gf - y * (y * gf).sum(-1, keepdim=True)) / den, gf / eps)
+            return dp.to(dt)
+
+        parts = [normalize_grad(0, grad_or_zeros(dk, dkd)), grad_or_zeros(dv, dvd),
+                 normalize_grad(dkd + dvd, grad_or_zeros(dq, dkd))]
+        if ded:
+            parts.append(grad_or_zeros(de, ded))
+        dP = torch.cat(parts, -1)
+        dx = dW = db = None
+        if ctx.needs_input_grad[0]:
+            dx = (dP @ weight).reshape(x.shape)
+        if ctx.needs_input_grad[1]:
+            dW = dP.t() @ x2
+        if bias is not None and ctx.needs_input_grad[2]:
+            db = dP.sum(0)
+        return dx, dW, db, None, None, None, None
+
+
+def _project_gemm_fused(x: Tensor, weight: Tensor, bias: Optional[Tensor], key_dim: int, value_dim: int,
+                        extra_dim: int) -> bool:
+    """Shapes the fused projection kernel takes (the op runs the library GEMM otherwise)."""
+    return (x.is_cuda and x.dtype in (torch.bfloat16, torch.float16) and weight.dtype == x.dtype
+            and (bias is None or bias.dtype == x.dtype) and key_dim == 64 and value_dim % 64 == 0
+            and extra_dim % 64 == 0 and x.size(-1) % 64 == 0 and x.size(-1) > 0)
+
+
 def cuda_project_gemm(x: Tensor, weight: Tensor, bias: Optional[Tensor], key_dim: int, value_dim: int,
                       extra_dim: int = 0, eps: float = 1e-6, *, enabled: bool = True,
                       debug_fallback: bool = False) -> Tuple[Tensor, ...]:
     """cuda_project_split(F.linear(x, weight, bias), ...) as one op: the projection GEMM with the
     split and the keys' and queries' L2 normalisation as its epilogue (paper_grm.py:491-493,
-    570-574).  Inference only: under autograd F.linear and cuda_project_split run."""
+    570-574).  Under autograd, 16-bit inputs take _ProjectGemmFn (the fused forward, a native
+    backward on library GEMMs); other dtypes F.linear and cuda_project_split."""
     needs_grad = torch.is_grad_enabled() and any(
         t is not None and t.requires_grad for t in (x, weight, bias))
-    if not needs_grad and _run_native("project_gemm", x.device, enabled=enabled, debug_fallback=debug_fallback):
-        k, v, q, e = torch.ops.grm_cuda.project_gemm(x, weight, bias, int(key_dim), int(value_dim), int(extra_dim),
-                                                     float(eps))
-        return (k, v, q) + ((e,) if extra_dim else ())
+    if _run_native("project_gemm", x.device, enabled=enabled, debug_fallback=debug_fallback):
+        if not needs_grad:
+            k, v, q, e = torch.ops.grm_cuda.project_gemm(x, weight, bias, int(key_dim), int(value_dim),
+                                                         int(extra_dim), float(eps))
+            return (k, v, q) + ((e,) if extra_dim else ())
+        if _project_gemm_fused(x, weight, bias, key_dim, value_dim, extra_dim):
+            k, v, q, e = _ProjectGemmFn.apply(x, weight, bias, int(key_dim), int(value_dim), int(extra_dim),
+                                              float(eps))
+            return (k, v, q) + ((e,) if extra_dim else ())
     return cuda_project_split(torch.nn.functional.linear(x, weight, bias), key_dim, value_dim, extra_dim, eps,
                               enabled=enabled, debug_fallback=debug_fallback)
 
@@ -650,6 +716,71 @@ def cuda_residual_layer_norm(x: Tensor, residual: Tensor, weight: Optional[Tenso
     return torch.nn.functional.layer_norm(x + residual, (x.size(-1),), weight, bias, eps)
 
 
+class _LinearResidualLayerNormFn(torch.autograd.Function):
+    """linear_residual_layer_norm under autograd: the fused forward also writes the LayerNorm's
+    input s = linear(x) + residual and its float32 row statistics; the backward is aten's
+    native_layer_norm_backward on them (ds and the LayerNorm parameters' gradients), then
+    ds flows to the residual unchanged and through the linear map on the library
+    (dx = ds W, dW = ds^T x, db = sum ds)."""
+
+    @staticmethod
+    def forward(ctx, x, weight, bias, residual, ln_weight, ln_bias, eps):
+        out, pre, mean, rstd = torch.ops.grm_cuda.linear_residual_layer_norm(x, weight, bias, residual, ln_weight,
+                                                                            ln_bias, eps, True)
+        ctx.save_for_backward(x, weight, pre, mean, rstd, ln_weight, ln_bias)
+        ctx.has_bias = bias is not None
+        return out
+
+    @staticmethod
+    def backward(ctx, dout):
+        x, weight, pre, mean, rstd, ln_weight, ln_bias = ctx.saved_tensors
+        N, K = weight.shape
+        rows = pre.numel() // N
+        mask = [True, ln_weight is not None and ctx.needs_input_grad[4],
+                ln_bias is not None and ctx.needs_input_grad[5]]
+        ds, dlw, dlb = torch.ops.aten.native_layer_norm_backward(
+            dout.reshape(rows, N).contiguous(), pre.reshape(rows, N), [N], mean.view(rows, 1), rstd.view(rows, 1),
+            ln_weight, ln_bias, mask)
+        x2 = x.reshape(rows, K)
+        dx = dW = db = dres = None
+        if ctx.needs_input_grad[0]:
+            dx = (ds @ weight).reshape(x.shape)
+        if ctx.needs_input_grad[1]:
+            dW = ds.t() @ x2
+        if ctx.has_bias and ctx.needs_input_grad[2]:
+            db = ds.sum(0)
+        if ctx.needs_input_grad[3]:
+            dres = ds.reshape(pre.shape)
+        return dx, dW, db, dres, dlw if mask[1] else None, dlb if mask[2] else None, None
+
+
+def _linear_res_ln_fused(x: Tensor, weight: Tensor, bias: Optional[Tensor], residual: Tensor) -> bool:
+    N, K = weight.shape
+    return (x.is_cuda and x.dtype in (torch.bfloat16, torch.float16) and weight.dtype == x.dtype
+            and residual.dtype == x.dtype and (bias is None or bias.dtype == x.dtype) and K % 64 == 0 and K > 0
+            and N % 64 == 0 and 0 < N <= 512)
+
+
+def cuda_linear_residual_layer_norm(x: Tensor, weight: Tensor, bias: Optional[Tensor], residual: Tensor,
+                                    ln_weight: Optional[Tensor] = None, ln_bias: Optional[Tensor] = None,
+                                    eps: float = 1e-5, *, enabled: bool = True,
+                                    debug_fallback: bool = False) -> Tensor:
+    """layer_norm(F.linear(x, weight, bias) + residual): the model's output projection
+    (paper_grm.py:709) and the block output (multilayer_grm.py:92-97) as one GEMM whose epilogue
+    is the residual add and the LayerNorm.  Under autograd, 16-bit inputs take
+    _LinearResidualLayerNormFn; other dtypes the torch composition."""
+    needs_grad = torch.is_grad_enabled() and any(
+        t is not None and t.requires_grad for t in (x, weight, bias, residual, ln_weight, ln_bias))
+    if _run_native("linear_residual_layer_norm", x.device, enabled=enabled, debug_fallback=debug_fallback):
+        if not needs_grad:
+            return torch.ops.grm_cuda.linear_residual_layer_norm(x, weight, bias, residual, ln_weight, ln_bias,
+                                                                 float(eps), False)[0]
+        if _linear_res_ln_fused(x, weight, bias, residual):
+            return _LinearResidualLayerNormFn.apply(x, weight, bias, residual, ln_weight, ln_bias, float(eps))
+    y = torch.nn.functional.linear(x, weight, bias)
+    return torch.nn.functional.layer_norm(y + residual, (y.size(-1),), ln_weight, ln_bias, eps)
+
+
 __all__ = [
     "GrmExtensionUnavailable",
     "cuda_apply_query",
@@ -657,6 +788,8 @@ __all__ = [
     "cuda_chunk_update",
     "cuda_fuse_residual",
     "cuda_gather_apply",
+    "cuda_linear_residual_layer_norm",
+    "cuda_project_gemm",
     "cuda_project_split",
     "cuda_residual_layer_norm",
     "cuda_retrieve_fuse",

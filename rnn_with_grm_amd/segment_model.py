@@ -646,6 +646,15 @@ class SegmentRecurrentMemoryModel(nn.Module):
     def forward(self, x_seq: Tensor, h_init: Optional[Tensor] = None, c_init: Optional[Tensor] = None,
                 return_all_outputs: bool = True, return_hidden_states: bool = False,
                 reset_memory: bool = False) -> Tuple[Tensor, Tensor, Optional[Tensor], Optional[Dict[str, Any]]]:
+        return self._forward_impl(x_seq, h_init, c_init, return_all_outputs, return_hidden_states, reset_memory)
+
+    def _forward_impl(self, x_seq: Tensor, h_init: Optional[Tensor], c_init: Optional[Tensor],
+                      return_all_outputs: bool, return_hidden_states: bool, reset_memory: bool,
+                      out_norm: Optional[Tuple[Tensor, nn.LayerNorm]] = None
+                      ) -> Tuple[Tensor, Tensor, Optional[Tensor], Optional[Dict[str, Any]]]:
+        """forward(); with out_norm = (residual, norm) and all outputs returned, the output is
+        norm(output_proj(h) + residual) instead of output_proj(h): SegmentRecurrentMemoryLayer's
+        block output (multilayer_grm.py:92-97) as the epilogue of the output projection's GEMM."""
         if x_seq.ndim == 2:
             x_seq = x_seq.unsqueeze(1 if self.batch_first else 0)
         x = x_seq if self.batch_first else x_seq.transpose(0, 1)
@@ -705,8 +714,17 @@ class SegmentRecurrentMemoryModel(nn.Module):
             h_enhanced = self._retrieve(x, q, q_r, h_online, states, summaries, base)
         else:
             h_enhanced = h_online
-        y = self.output_proj(h_enhanced)
-        _mark("output projection GEMM", x)
+        if out_norm is not None:
+            residual, norm = out_norm
+            if not self.batch_first:
+                residual = residual.transpose(0, 1)
+            y = cuda_ops.cuda_linear_residual_layer_norm(h_enhanced, self.output_proj.weight, self.output_proj.bias,
+                                                         residual, norm.weight, norm.bias, norm.eps,
+                                                         debug_fallback=self.cuda_cpp_debug_fallback)
+            _mark("output projection GEMM + layer residual + LayerNorm", x)
+        else:
+            y = self.output_proj(h_enhanced)
+            _mark("output projection GEMM", x)
 
         # Push every segment (paper_grm.py:718-724); only the last `capacity` survive.
         # Checkpoints of the kept segments: one time-major copy of their inputs
@@ -786,6 +804,11 @@ class SegmentRecurrentMemoryLayer(nn.Module):
                 reset_memory: bool = False) -> Tuple[Tensor, Tensor, Optional[Tensor], Optional[Dict]]:
         if x.ndim == 2:
             x = x.unsqueeze(1 if self.batch_first else 0)
+        if return_all_outputs and isinstance(self.layer_norm, nn.LayerNorm):
+            # the residual add and the LayerNorm run as the output projection's epilogue
+            outputs, h_final, memory_final, aux = self.grm._forward_impl(
+                x, h_init, c_init, True, return_hidden_states, reset_memory, out_norm=(x, self.layer_norm))
+            return self.dropout(outputs), h_final, memory_final, aux
         outputs, h_final, memory_final, aux = self.grm(x, h_init=h_init, c_init=c_init,
                                                        return_all_outputs=return_all_outputs,
                                                        return_hidden_states=return_hidden_states,

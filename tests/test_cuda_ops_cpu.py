@@ -364,3 +364,85 @@ def test_cpu_project_gemm_is_linear_then_split():
     assert len(wrapped) == 4 and all(torch.equal(a, c) for a, c in zip(wrapped, want))
     with pytest.raises(RuntimeError, match="weight must be"):
         torch.ops.grm_cuda.project_gemm(x, w[:-1], None, 8, 24, 8, 1e-6)
+
+
+def test_cpu_linear_residual_layer_norm_is_linear_then_layer_norm():
+    """linear_residual_layer_norm's CPU kernel is layer_norm(F.linear(x, w, b) + residual); with
+    save it also returns the LayerNorm input and native_layer_norm's row statistics."""
+    import torch.nn.functional as F
+
+    if not cuda_ops.load_grm_cuda_extension():
+        pytest.skip("extension not built")
+    g = torch.Generator().manual_seed(15)
+    x, res = torch.randn(3, 7, 24, generator=g), torch.randn(3, 7, 16, generator=g)
+    w, b = torch.randn(16, 24, generator=g), torch.randn(16, generator=g)
+    lw, lb = torch.randn(16, generator=g), torch.randn(16, generator=g)
+    s = F.linear(x, w, b) + res
+    want = F.layer_norm(s, (16,), lw, lb, 1e-5)
+    out, pre, mean, rstd = torch.ops.grm_cuda.linear_residual_layer_norm(x, w, b, res, lw, lb, 1e-5, True)
+    torch.testing.assert_close(out, want)
+    torch.testing.assert_close(pre, s)
+    _, m, r = torch.ops.aten.native_layer_norm(s, [16], lw, lb, 1e-5)
+    torch.testing.assert_close(mean, m.reshape(-1))
+    torch.testing.assert_close(rstd, r.reshape(-1))
+    assert torch.equal(torch.ops.grm_cuda.linear_residual_layer_norm(x, w, b, res, lw, lb, 1e-5, False)[0], out)
+    torch.testing.assert_close(cuda_ops.cuda_linear_residual_layer_norm(x, w, b, res, lw, lb, 1e-5), want)
+    with pytest.raises(RuntimeError, match="weight must be"):
+        torch.ops.grm_cuda.linear_residual_layer_norm(x, w[:, :-1], b, res, lw, lb, 1e-5, False)
+
+
+@pytest.mark.parametrize("affine", [True, False])
+def test_linear_residual_layer_norm_backward_matches_autograd(affine):
+    """_LinearResidualLayerNormFn's backward (aten's layer-norm backward on the saved input and
+    statistics, then the linear map's gradients) equals torch autograd of F.linear + add +
+    layer_norm, float32 on the CPU, for every input."""
+    import torch.nn.functional as F
+
+    if not cuda_ops.load_grm_cuda_extension():
+        pytest.skip("extension not built")
+    g = torch.Generator().manual_seed(16)
+    ins = [torch.randn(2, 9, 24, generator=g), torch.randn(16, 24, generator=g), torch.randn(16, generator=g),
+           torch.randn(2, 9, 16, generator=g)]
+    ln = [torch.randn(16, generator=g), torch.randn(16, generator=g)] if affine else [None, None]
+    dout = torch.randn(2, 9, 16, generator=g)
+    a = [t.clone().requires_grad_(True) for t in ins] + [None if t is None else t.clone().requires_grad_(True)
+                                                          for t in ln]
+    out = cuda_ops._LinearResidualLayerNormFn.apply(*a, 1e-5)
+    got = torch.autograd.grad(out, [t for t in a if t is not None], dout)
+    r = [t.clone().requires_grad_(True) for t in ins] + [None if t is None else t.clone().requires_grad_(True)
+                                                          for t in ln]
+    ref_out = F.layer_norm(F.linear(r[0], r[1], r[2]) + r[3], (16,), r[4], r[5], 1e-5)
+    want = torch.autograd.grad(ref_out, [t for t in r if t is not None], dout)
+    torch.testing.assert_close(out, ref_out)
+    for x, y in zip(got, want):
+        torch.testing.assert_close(x, y, rtol=1e-5, atol=1e-5)
+
+
+def test_project_gemm_backward_matches_autograd():
+    """_ProjectGemmFn's backward (F.normalize's derivative from recomputed norms, then the GEMM's
+    gradients) equals torch autograd of F.linear + split + F.normalize, float32 on the CPU, with
+    an extra part, unused outputs, and one row whose key projection is below the eps clamp."""
+    import torch.nn.functional as F
+
+    if not cuda_ops.load_grm_cuda_extension():
+        pytest.skip("extension not built")
+    g = torch.Generator().manual_seed(17)
+    dk, dv, de, K = 8, 24, 16, 20
+    x = torch.randn(3, 5, K, generator=g)
+    w = torch.randn(2 * dk + dv + de, K, generator=g)
+    b = torch.randn(2 * dk + dv + de, generator=g)
+    w[:dk] *= 1e-9  # key projections of tiny norm ...
+    b[:dk] *= 1e-9  # ... below eps for every row: the clamped branch
+    grads = [torch.randn(3, 5, d, generator=g) for d in (dk, dv, dk, de)]
+    for used in ((0, 1, 2, 3), (1, 2)):
+        a = [t.clone().requires_grad_(True) for t in (x, w, b)]
+        outs = cuda_ops._ProjectGemmFn.apply(a[0], a[1], a[2], dk, dv, de, 1e-6)
+        got = torch.autograd.grad([outs[i] for i in used], a, [grads[i] for i in used])
+        r = [t.clone().requires_grad_(True) for t in (x, w, b)]
+        p = F.linear(r[0], r[1], r[2]).split([dk, dv, dk, de], -1)
+        ref = (F.normalize(p[0], dim=-1, eps=1e-6), p[1], F.normalize(p[2], dim=-1, eps=1e-6), p[3])
+        want = torch.autograd.grad([ref[i] for i in used], r, [grads[i] for i in used])
+        for o, rr in zip(outs, ref):
+            torch.testing.assert_close(o, rr)
+        for gg, ww in zip(got, want):
+            torch.testing.assert_close(gg, ww, rtol=1e-4, atol=1e-5)

@@ -172,3 +172,170 @@ def test_project_gemm_shapes_outside_the_kernel(dev):
     assert ext.generic_path_calls() == generic
     k2, v2, q2, e2 = torch.ops.grm_cuda.project_split(F.linear(x, w), 32, 96, 0, 1e-6)
     assert torch.equal(k, k2) and torch.equal(v, v2) and torch.equal(q, q2)
+
+
+# ---------------------------------------------------------------- output projection + residual + LayerNorm
+@pytest.mark.parametrize("dtype,pdtype", [(torch.bfloat16, torch.bfloat16), (torch.float16, torch.float16),
+                                          (torch.bfloat16, torch.float32)])
+@pytest.mark.parametrize("rows,K,N,with_bias,affine", [(32768, 512, 512, True, True), (1000, 64, 64, True, True),
+                                                       (37, 128, 192, False, True), (130, 256, 512, True, False),
+                                                       (65, 512, 448, False, False)])
+def test_linear_residual_layer_norm(dev, dtype, pdtype, rows, K, N, with_bias, affine):
+    """linear_residual_layer_norm (the output projection GEMM with the block's residual add and
+    LayerNorm as its epilogue) against torch's F.linear, add and F.layer_norm in the same dtype:
+    the LayerNorm input (pre) within one unit in the last place of torch's F.linear + residual and
+    at most 3% of its elements different (the GEMM sums in another order); the output within one
+    unit of F.layer_norm of that same input, float32 statistics within 1e-5 of
+    native_layer_norm's; the whole output at relative L2 below 1e-2 of the float32 composition;
+    save=False writes the same output.  (32768, 512, 512) is config 4's layer."""
+    g = torch.Generator().manual_seed(rows + K + N)
+    x = torch.randn(rows, K, generator=g).to(dtype).to(dev)
+    w = (torch.randn(N, K, generator=g) / K ** 0.5).to(dtype).to(dev)
+    b = (0.1 * torch.randn(N, generator=g)).to(dtype).to(dev) if with_bias else None
+    r = torch.randn(rows, N, generator=g).to(dtype).to(dev)
+    lw = (1 + 0.1 * torch.randn(N, generator=g)).to(pdtype).to(dev) if affine else None
+    lb = (0.1 * torch.randn(N, generator=g)).to(pdtype).to(dev) if affine else None
+    print(f"linear_residual_layer_norm rows={rows} K={K} N={N} bias={with_bias} affine={affine} {dtype}/{pdtype}",
+          flush=True)
+    ext = cuda_ops.extension_module()
+    generic, launches = ext.generic_path_calls(), ext.hip_launch_count()
+    out, pre, mean, rstd = capi.linear_residual_layer_norm(x, w, b, r, lw, lb, 1e-5, save=True)
+    out2 = torch.ops.grm_cuda.linear_residual_layer_norm(x, w, b, r, lw, lb, 1e-5, False)[0]
+    torch.cuda.synchronize()
+    assert ext.generic_path_calls() == generic and ext.hip_launch_count() > launches
+    assert torch.equal(out, out2)
+    e = {torch.bfloat16: 2.0 ** -7, torch.float16: 2.0 ** -10}[dtype]  # one unit in the last place at 1
+    y_ref = F.linear(x, w, b)
+    s_ref = y_ref + r
+    # y may round to the neighbouring value (another summation order): s moves by one step of y,
+    # then rounds once more
+    bound = e * (y_ref.double().abs() + s_ref.double().abs()) + 1e-6
+    assert bool(((pre.double() - s_ref.double()).abs() <= bound).all())
+    assert float((pre != s_ref).double().mean()) <= 0.03
+    # the LayerNorm of that same input: float32 statistics, one rounding of the output
+    ln32, m_ref, r_ref = torch.ops.aten.native_layer_norm(pre.float(), [N], None if lw is None else lw.float(),
+                                                          None if lb is None else lb.float(), 1e-5)
+    assert bool(((out.double() - ln32.double()).abs() <= e * ln32.double().abs() + 1e-4).all())
+    torch.testing.assert_close(mean, m_ref.reshape(-1), rtol=1e-5, atol=1e-5)
+    torch.testing.assert_close(rstd, r_ref.reshape(-1), rtol=1e-5, atol=1e-5)
+    f32 = F.layer_norm(F.linear(x.float(), w.float(), None if b is None else b.float()) + r.float(), (N,),
+                       None if lw is None else lw.float(), None if lb is None else lb.float(), 1e-5)
+    rel = float((out.float() - f32).norm() / f32.norm())
+    assert rel < 1e-2, rel
+
+
+def test_linear_residual_layer_norm_outside_the_kernel(dev):
+    """Shapes the kernel does not take (out_dim 576, float32) run the generic composition on the
+    device and count a generic call; the C ABI refuses them with a message."""
+    g = torch.Generator().manual_seed(9)
+    x = torch.randn(10, 64, generator=g).to(torch.bfloat16).to(dev)
+    w = torch.randn(576, 64, generator=g).to(torch.bfloat16).to(dev)
+    r = torch.randn(10, 576, generator=g).to(torch.bfloat16).to(dev)
+    ext = cuda_ops.extension_module()
+    generic = ext.generic_path_calls()
+    out = torch.ops.grm_cuda.linear_residual_layer_norm(x, w, None, r, None, None, 1e-5, False)[0]
+    assert ext.generic_path_calls() == generic + 1
+    torch.testing.assert_close(out, F.layer_norm(F.linear(x, w) + r, (576,)))
+    with pytest.raises(RuntimeError, match="out_dim"):
+        capi.linear_residual_layer_norm(x, w, None, r)
+
+
+def _bf16_grad_close(name, got, ref):
+    got, ref = got.double().cpu(), ref.double().cpu()
+    rel = float((got - ref).norm() / ref.norm().clamp_min(1e-30))
+    assert rel < 1e-2, (name, rel)
+    scale = float(ref.abs().max())
+    assert bool(((got - ref).abs() <= 3e-2 * ref.abs() + 1e-2 * scale).all()), name
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_linear_residual_layer_norm_training_form(dev, dtype):
+    """cuda_linear_residual_layer_norm under autograd (_LinearResidualLayerNormFn: the fused
+    forward, aten's LayerNorm backward on its saved input and statistics, the linear map's
+    gradients on the library): output and every gradient against float32 autograd of
+    F.linear + add + F.layer_norm on the same 16-bit inputs, relative L2 below 1e-2."""
+    g = torch.Generator().manual_seed(23)
+    rows, K, N = 4096, 512, 512
+    vals = [torch.randn(rows, K, generator=g), torch.randn(N, K, generator=g) / K ** 0.5,
+            0.1 * torch.randn(N, generator=g), torch.randn(rows, N, generator=g),
+            1 + 0.1 * torch.randn(N, generator=g), 0.1 * torch.randn(N, generator=g)]
+    dout = torch.randn(rows, N, generator=g).to(dtype).to(dev)
+    a = [v.to(dtype).to(dev).requires_grad_(True) for v in vals]
+    out = cuda_ops.cuda_linear_residual_layer_norm(*a, 1e-5)
+    got = torch.autograd.grad(out, a, dout)
+    f = [v.to(dtype).float().to(dev).requires_grad_(True) for v in vals]
+    ref_out = F.layer_norm(F.linear(f[0], f[1], f[2]) + f[3], (N,), f[4], f[5], 1e-5)
+    want = torch.autograd.grad(ref_out, f, dout.float())
+    _bf16_grad_close("out", out.detach(), ref_out.detach())
+    for name, x_, y_ in zip(("x", "weight", "bias", "residual", "ln_weight", "ln_bias"), got, want):
+        assert x_.dtype == dtype
+        _bf16_grad_close(name, x_, y_)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_project_gemm_training_form(dev, dtype):
+    """cuda_project_gemm under autograd (_ProjectGemmFn: the fused forward, F.normalize's
+    derivative in float32 from recomputed norms, the GEMM's gradients on the library) against
+    float32 autograd of F.linear + split + F.normalize on the same 16-bit inputs, relative L2
+    below 1e-2, with config 4's layer shape (key 64, value 512, gating query 512)."""
+    g = torch.Generator().manual_seed(29)
+    rows, K, dk, dv, de = 4096, 512, 64, 512, 512
+    N = 2 * dk + dv + de
+    vals = [torch.randn(rows, K, generator=g), torch.randn(N, K, generator=g) / K ** 0.5,
+            0.1 * torch.randn(N, generator=g)]
+    douts = [torch.randn(rows, d, generator=g).to(dtype).to(dev) for d in (dk, dv, dk, de)]
+    a = [v.to(dtype).to(dev).requires_grad_(True) for v in vals]
+    outs = cuda_ops.cuda_project_gemm(a[0], a[1], a[2], dk, dv, de, 1e-6)
+    got = torch.autograd.grad(outs, a, douts)
+    f = [v.to(dtype).float().to(dev).requires_grad_(True) for v in vals]
+    p = F.linear(f[0], f[1], f[2]).split([dk, dv, dk, de], -1)
+    ref = (F.normalize(p[0], dim=-1, eps=1e-6), p[1], F.normalize(p[2], dim=-1, eps=1e-6), p[3])
+    want = torch.autograd.grad(ref, f, [d.float() for d in douts])
+    for o, rr in zip(outs, ref):
+        _bf16_grad_close("forward", o.detach(), rr.detach())
+    for name, x_, y_ in zip(("x", "weight", "bias"), got, want):
+        assert x_.dtype == dtype
+        _bf16_grad_close(name, x_, y_)
+
+
+def test_model_training_uses_fused_glue(dev, monkeypatch):
+    """A bf16 two-layer hierarchical model's training step (forward, loss, backward) runs the
+    fused projection and output forms under autograd, and its parameter gradients agree with the
+    same step through the torch compositions of those two ops (everything else unchanged) to
+    relative L2 2e-2 per parameter."""
+    from rnn_with_grm_amd.segment_model import HierarchicalSegmentMemoryModel
+
+    torch.manual_seed(31)
+    model = HierarchicalSegmentMemoryModel(128, 128, 128, num_layers=2, segment_length=64, memory_capacity_segments=8,
+                                           retrieval_top_k=4, memory_key_dim=64, dropout=0.0,
+                                           recomputation_ratio=0.0).to(dev, torch.bfloat16)
+    x = torch.randn(2, 512, 128, generator=torch.Generator().manual_seed(32)).to(dev, torch.bfloat16)
+    tgt = torch.randn(2, 512, 128, generator=torch.Generator().manual_seed(33)).to(dev, torch.bfloat16)
+    calls = {"proj": 0, "out": 0}
+    pg, lr = cuda_ops._ProjectGemmFn.apply, cuda_ops._LinearResidualLayerNormFn.apply
+
+    def count(key, fn):
+        def wrapped(*args):
+            calls[key] += 1
+            return fn(*args)
+        return wrapped
+
+    def step():
+        model.zero_grad(set_to_none=True)
+        out, _, _, _ = model(x, reset_memory=True)
+        (out.float() - tgt.float()).square().mean().backward()
+        return {n: p.grad.detach().clone() for n, p in model.named_parameters() if p.grad is not None}
+
+    monkeypatch.setattr(cuda_ops._ProjectGemmFn, "apply", count("proj", pg))
+    monkeypatch.setattr(cuda_ops._LinearResidualLayerNormFn, "apply", count("out", lr))
+    fused = step()
+    assert calls["proj"] == 2 and calls["out"] == 2, calls
+    monkeypatch.setattr(cuda_ops, "_project_gemm_fused", lambda *a: False)
+    monkeypatch.setattr(cuda_ops, "_linear_res_ln_fused", lambda *a: False)
+    plain = step()
+    assert calls["proj"] == 2 and calls["out"] == 2, calls
+    assert fused.keys() == plain.keys() and len(fused) > 10
+    for n in fused:
+        a_, b_ = fused[n].double(), plain[n].double()
+        rel = float((a_ - b_).norm() / b_.norm().clamp_min(1e-30))
+        assert rel < 2e-2, (n, rel)
