@@ -34,6 +34,7 @@ sys.path.insert(0, str(REPO))
 
 HBM_PEAK_GBS = 8000.0       # MI355X HBM3E, GB/s
 BF16_PEAK_TFLOPS = 2500.0   # MI355X dense bf16 MFMA
+FP32_PEAK_TFLOPS = 157.3    # MI355X dense fp32 MFMA
 METRIC = "chunk-update+query tokens/s & %MFMA peak; top-k gather GB/s & %HBM, 1 GPU"
 
 
@@ -315,7 +316,10 @@ def bench_c3(torch, dev, steps, warmup):
                          "bytes": BH * S * D * D * 4 + BH * Q * K * D * 4 + q.numel() * 2 + idx.numel() * 8,
                          "flops": 2 * BH * Q * K * D * D},
         "fuse": {"ms": statistics.mean(fu_per) * 1e3},
-        "retrieve_fuse": {"ms": statistics.mean(rf_per) * 1e3},
+        "retrieve_fuse": {"ms": statistics.mean(rf_per) * 1e3,
+                          "bytes": BH * S * D * D * 4 + q.numel() * 2 + idx.numel() * 8 + gt.numel() * 4 +
+                                   2 * BH * Q * D * 4,
+                          "intermediate_bytes": 2 * (BH * Q * K * D * 2 + BH * Q * K * 4)},
         "retrieval": {"ms": statistics.mean(rt_per) * 1e3},
         "composition": {"ms": statistics.mean(cp_per) * 1e3},
         "gather": {"ms": statistics.mean(g_per) * 1e3, "bytes": gather_bytes,
@@ -779,6 +783,27 @@ def bench_c4_train(torch, dev, steps, warmup):
             "peak_gib": torch.cuda.max_memory_allocated(dev) / 2 ** 30}
 
 
+def retrieval_roofline(ms, flops, alg_bytes, rows_bytes=None):
+    """Roofline of a fused retrieval launch: max(F / P, B / BW) with F the float32-semantics FLOPs of the
+    gathered applies (2 per multiply-add of every selected 128 x 128 state with its query) against the
+    dense float32 MFMA peak, and B its algorithmic HBM bytes against 8 TB/s.  The kernel computes the
+    float32 products as three bf16 MFMA products (hi*hi + hi*lo + lo*hi), so the bf16 rate it issues is
+    reported beside it."""
+    t_f = flops / (FP32_PEAK_TFLOPS * 1e12)
+    t_b = alg_bytes / (HBM_PEAK_GBS * 1e9)
+    t = ms * 1e-3
+    rec = {"bound": "mfma_fp32" if t_f >= t_b else "hbm", "achieved": round(max(t_f, t_b) / t, 4), "peak": 1.0,
+           "unit": "fraction of roofline time", "frac": round(max(t_f, t_b) / t, 4),
+           "fp32_TFLOP/s": round(flops / t / 1e12, 1), "fp32_peak_TFLOP/s": FP32_PEAK_TFLOPS,
+           "fp32_floor_ms": round(t_f * 1e3, 4), "hbm_GB/s": round(alg_bytes / t / 1e9, 1),
+           "hbm_floor_ms": round(t_b * 1e3, 4), "algorithmic_bytes": alg_bytes, "flops": flops,
+           "bf16x3_issued_TFLOP/s": round(3 * flops / t / 1e12, 1)}
+    if rows_bytes is not None:
+        rec["traffic"] = {"float16_rows_written_and_read": rows_bytes, "over_algorithmic": round(
+            (alg_bytes + rows_bytes) / alg_bytes, 3)}
+    return rec
+
+
 def committed_traffic(name, source):
     """HBM bytes per launch from a committed counter summary (profiles/<name>: FETCH_SIZE and
     WRITE_SIZE of the kernel, scaled by a copy of known size), with the sha256 of the kernel
@@ -924,6 +949,9 @@ def main() -> int:
                     "composition (gather_apply in float32, then fuse_residual) beside it",
             "ms": round(rt["ms"], 4), "route_ms": round(r["ms"], 4),
             "retrieve_fuse_ms": round(c3["retrieve_fuse"]["ms"], 4),
+            "retrieve_fuse_roofline": retrieval_roofline(c3["retrieve_fuse"]["ms"], ga["flops"],
+                                                         c3["retrieve_fuse"]["bytes"],
+                                                         c3["retrieve_fuse"]["intermediate_bytes"]),
             "composition_ms": round(c3["composition"]["ms"], 4), "gather_apply_ms": round(ga["ms"], 4),
             "fuse_ms": round(c3["fuse"]["ms"], 4),
             "gather_apply_GB/s": round(ga["bytes"] / ga["ms"] / 1e6, 1),
@@ -943,7 +971,6 @@ def main() -> int:
                                   "GB/s": round(ugbs, 1), "hbm_frac": round(ugbs / HBM_PEAK_GBS, 4),
                                   "bytes": u["bytes"]}
         rf5 = c5["retrieve_fuse"]
-        rf_gbs = rf5["bytes"] / rf5["ms"] / 1e6
         secondary["c5_retrieval_fused"] = {
             "what": "route (top-16 of 512 snapshots per token) -> retrieve_fuse (gather + apply + gate-weighted sum "
                     "+ residual + LayerNorm), every token routed over all 512 states (no causal mask, as the "
@@ -952,10 +979,8 @@ def main() -> int:
             "ms": round(rt5["ms"], 3), "tokens/s": round(rt5["tokens"] / rt5["ms"] * 1e3),
             "route_ms": round(c5["route"]["ms"], 3), "route_near_ties": c5["route"]["near_ties"],
             "retrieve_fuse_ms": round(rf5["ms"], 3),
-            "retrieve_fuse_roofline": {"bound": "hbm", "achieved": round(rf_gbs, 1), "peak": HBM_PEAK_GBS,
-                                       "unit": "GB/s", "frac": round(rf_gbs / HBM_PEAK_GBS, 4),
-                                       "algorithmic_bytes": rf5["bytes"],
-                                       "float16_rows_written_and_read": rf5["intermediate_bytes"]},
+            "retrieve_fuse_roofline": retrieval_roofline(rf5["ms"], ga5["flops"], rf5["bytes"],
+                                                         rf5["intermediate_bytes"]),
             "composition_ms": round(c5["composition"]["ms"], 3), "gather_apply_ms": round(ga5["ms"], 3),
             "fuse_ms": round(c5["fuse"]["ms"], 3),
             "route_TFLOP/s": round(c5["route"]["flops"] / c5["route"]["ms"] / 1e9, 1),
