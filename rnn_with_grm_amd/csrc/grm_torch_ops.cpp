@@ -287,18 +287,24 @@ std::tuple<Tensor, Tensor, Tensor> topk_route_cpu(const Tensor& queries, const T
         all[s] = acc * fs;
         order[s] = s;
       }
-      if (k < S) {
+      // k < S: a NaN or -inf score is never selected (NaN sorts as -inf; slots left
+      // at -inf are empty, (-1, -inf, 0)).  k >= S: every key in index order.
+      const bool select = k < S;
+      if (select) {
+        for (int64_t s = 0; s < S; ++s) all[s] = std::isnan(all[s]) ? -INFINITY : all[s];
         std::stable_sort(order.begin(), order.end(),
                          [&](int64_t x, int64_t y) { return all[x] > all[y]; });
       }
+      auto filled = [&](int64_t m) { return !select || all[order[m]] > -INFINITY; };
       float mx = -INFINITY;
-      for (int64_t m = 0; m < k; ++m) mx = std::max(mx, all[order[m]] * inv_t);
+      for (int64_t m = 0; m < k; ++m) mx = filled(m) ? std::max(mx, all[order[m]] * inv_t) : mx;
       float sum = 0.f;
-      for (int64_t m = 0; m < k; ++m) sum += std::exp(all[order[m]] * inv_t - mx);
+      for (int64_t m = 0; m < k; ++m) sum += filled(m) ? std::exp(all[order[m]] * inv_t - mx) : 0.f;
       for (int64_t m = 0; m < k; ++m) {
-        ip[r * k + m] = order[m];
-        sp[r * k + m] = all[order[m]];
-        gp[r * k + m] = std::exp(all[order[m]] * inv_t - mx) / sum;
+        const bool f = filled(m);
+        ip[r * k + m] = f ? order[m] : -1;
+        sp[r * k + m] = f ? all[order[m]] : -INFINITY;
+        gp[r * k + m] = f ? std::exp(all[order[m]] * inv_t - mx) / sum : 0.f;
       }
     }
   });
@@ -816,12 +822,19 @@ std::tuple<Tensor, Tensor, Tensor> topk_route_hip(const Tensor& queries, const T
   if (k > 128 && k < keys.size(1)) {
     // Beyond the select kernels' k: every key's exact score in index order (the
     // k == n_keys branch), then a stable descending sort on the device, which
-    // orders equal scores by index as the kernels do.  Gates as softmax in float64.
+    // orders equal scores by index as the kernels do.  As in the kernels, a NaN or
+    // -inf score is never selected: NaN sorts as -inf, and slots left at -inf are
+    // empty (-1, -inf, 0).  Gates as softmax in float64 over the filled slots.
     auto all = topk_route_hip(queries, keys, keys.size(1), scale, temperature);
-    auto sorted = at::sort(std::get<2>(all), /*stable=*/true, /*dim=*/-1, /*descending=*/true);
+    Tensor all_sc = std::get<2>(all);
+    all_sc = at::where(at::isnan(all_sc), at::full({}, -INFINITY, all_sc.options()), all_sc);
+    auto sorted = at::sort(all_sc, /*stable=*/true, /*dim=*/-1, /*descending=*/true);
     Tensor sc = std::get<0>(sorted).narrow(-1, 0, k).contiguous();
     Tensor idx = std::get<1>(all).gather(-1, std::get<1>(sorted).narrow(-1, 0, k)).contiguous();
+    const Tensor empty = sc == -INFINITY;
+    idx.masked_fill_(empty, -1);
     Tensor gt = at::softmax(sc.to(at::kDouble) / temperature, -1).to(at::kFloat);
+    gt.masked_fill_(empty, 0.0);
     return {gt, idx, sc};
   }
   c10::OptionalDeviceGuard guard(queries.device());

@@ -245,22 +245,7 @@ __global__ __launch_bounds__(RT) void route_kernel(const RouteArgs a) {
     }
     return;
   }
-  const float mx = top_s[0] * a.inv_temp;
-  float e[KMAX];
-  float sum = 0.f;
-#pragma unroll
-  for (int m = 0; m < KMAX; ++m) {
-    e[m] = (m < k) ? expf(top_s[m] * a.inv_temp - mx) : 0.f;
-    sum += e[m];
-  }
-#pragma unroll
-  for (int m = 0; m < KMAX; ++m) {
-    if (m < k) {
-      a.idx[obase + m] = top_i[m];
-      a.scores[obase + m] = top_s[m];
-      a.gates[obase + m] = e[m] / sum;
-    }
-  }
+  write_topk_row<KMAX>(a.idx, a.scores, a.gates, obase, k, a.inv_temp, top_s, top_i);
 }
 
 template <class E>
@@ -1293,22 +1278,7 @@ __global__ __launch_bounds__(RM_THREADS, 2) void route_mfma_kernel(const RouteAr
     }
     return;
   }
-  const float mx = top_s[0] * a.inv_temp;
-  float e[KMAX];
-  float sum = 0.f;
-#pragma unroll
-  for (int m = 0; m < KMAX; ++m) {
-    e[m] = (m < k) ? expf(top_s[m] * a.inv_temp - mx) : 0.f;
-    sum += e[m];
-  }
-#pragma unroll
-  for (int m = 0; m < KMAX; ++m) {
-    if (m < k) {
-      a.idx[obase + m] = top_i[m];
-      a.scores[obase + m] = top_s[m];
-      a.gates[obase + m] = e[m] / sum;
-    }
-  }
+  write_topk_row<KMAX>(a.idx, a.scores, a.gates, obase, k, a.inv_temp, top_s, top_i);
 }
 
 // Whether route_mfma_kernel covers these arguments; ib = index bits.

@@ -534,22 +534,7 @@ __global__ __launch_bounds__(ST) void route_select_kernel(const SelParams p) {
       }
       continue;
     }
-    const float mx = top_s[0] * a.inv_temp;
-    float e[KMAX];
-    float sum = 0.f;
-#pragma unroll
-    for (int m = 0; m < KMAX; ++m) {
-      e[m] = (m < k) ? expf(top_s[m] * a.inv_temp - mx) : 0.f;
-      sum += e[m];
-    }
-#pragma unroll
-    for (int m = 0; m < KMAX; ++m) {
-      if (m < k) {
-        a.idx[obase + m] = top_i[m];
-        a.scores[obase + m] = top_s[m];
-        a.gates[obase + m] = e[m] / sum;
-      }
-    }
+    write_topk_row<KMAX>(a.idx, a.scores, a.gates, obase, k, a.inv_temp, top_s, top_i);
   }
 }
 

@@ -446,3 +446,26 @@ def test_project_gemm_backward_matches_autograd():
             torch.testing.assert_close(o, rr)
         for gg, ww in zip(got, want):
             torch.testing.assert_close(gg, ww, rtol=1e-4, atol=1e-5)
+
+
+def test_cpu_topk_route_non_finite_rule():
+    """The CPU kernel's rule for non-finite scores (the GPU paths share it): a NaN or -inf score is
+    never selected, slots left over are (-1, -inf, 0), gates the softmax of the filled slots;
+    with k >= n_keys every key comes back in index order, as in the reference's branch."""
+    if not cuda_ops.load_grm_cuda_extension():
+        pytest.skip("extension not built")
+    g = torch.Generator().manual_seed(18)
+    q = torch.nn.functional.normalize(torch.randn(1, 4, 16, generator=g), dim=-1)
+    keys = torch.nn.functional.normalize(torch.randn(1, 6, 16, generator=g), dim=-1)
+    q[0, 1] = float("nan")
+    keys[0, 2, 3] = float("nan")
+    gates, idx, sc = torch.ops.grm_cuda.topk_route(q, keys, 3, 0.25, 1.0)
+    assert (idx[0, 1] == -1).all() and torch.isinf(sc[0, 1]).all() and (gates[0, 1] == 0).all()
+    assert not (idx == 2).any()
+    full = (q[0, 0] @ keys[0].T * 0.25)
+    full[2] = -float("inf")
+    top = torch.sort(full, descending=True, stable=True)
+    assert torch.equal(idx[0, 0], top.indices[:3])
+    torch.testing.assert_close(gates[0, 0], torch.softmax(top.values[:3], -1), rtol=1e-5, atol=1e-6)
+    gates_all, idx_all, _ = torch.ops.grm_cuda.topk_route(q, keys, 6, 0.25, 1.0)
+    assert torch.equal(idx_all[0, 0], torch.arange(6))

@@ -374,11 +374,13 @@ def test_topk_route_beyond_128(dev, dtype):
     assert np.array_equal(sc.cpu().numpy(), osc)
     np.testing.assert_allclose(gates.cpu().numpy(), og, rtol=1e-5, atol=1e-6)
     print(f"segment routing k=150 {dtype}", flush=True)
-    gates, idx, sc = cuda_ops.cuda_segment_route(q.to(dev), keys.to(dev), 150, 2, 100, 180, 0.125)
-    og, oi, osc = orc.segment_route(q.float().numpy(), keys.float().numpy(), 150, 2, 100, 180, 0.125)
-    assert np.array_equal(idx.cpu().numpy(), oi)
-    assert np.array_equal(sc.cpu().numpy(), osc)
-    np.testing.assert_allclose(gates.cpu().numpy(), og, rtol=1e-5, atol=1e-6)
+    # windows of 100-134 keys (at most k: index order), then of 160-194 keys (beyond k: the sort)
+    for seg_base, cap in ((100, 180), (160, 250)):
+        gates, idx, sc = cuda_ops.cuda_segment_route(q.to(dev), keys.to(dev), 150, 2, seg_base, cap, 0.125)
+        og, oi, osc = orc.segment_route(q.float().numpy(), keys.float().numpy(), 150, 2, seg_base, cap, 0.125)
+        assert np.array_equal(idx.cpu().numpy(), oi), (seg_base, cap)
+        assert np.array_equal(sc.cpu().numpy(), osc), (seg_base, cap)
+        np.testing.assert_allclose(gates.cpu().numpy(), og, rtol=1e-5, atol=1e-6)
 
 
 def test_topk_route_ties(dev):
@@ -1006,3 +1008,52 @@ def test_apply_degenerate_shapes_clear_outputs(dev, dtype):
     assert rc == 0, capi.last_error()
     torch.cuda.synchronize()
     assert int(torch.count_nonzero(out)) == 0 and int(torch.count_nonzero(gq)) == 0
+
+
+def _nonfinite_expect(q, keys, k, scale):
+    """topk_route's rule for non-finite scores, from the oracle's canonical scores in index order:
+    a NaN or -inf score is never selected, the rest by (score descending, index ascending); slots
+    left over are (-1, -inf, 0); gates are the softmax of the filled slots."""
+    S = keys.shape[1]
+    _, _, all_sc = orc.topk_route(q, keys, S, scale)          # k == S: every score, index order
+    B, Q = all_sc.shape[:2]
+    idx = np.full((B, Q, k), -1, dtype=np.int64)
+    sc = np.full((B, Q, k), -np.inf, dtype=np.float32)
+    gt = np.zeros((B, Q, k))
+    for b in range(B):
+        for r in range(Q):
+            s = all_sc[b, r]
+            ok = np.flatnonzero(s > -np.inf)                   # False for NaN
+            order = ok[np.argsort(-s[ok], kind="stable")][:k]
+            idx[b, r, :len(order)] = order
+            sc[b, r, :len(order)] = s[order]
+            if len(order):
+                e = np.exp(s[order].astype(np.float64) - s[order].max())
+                gt[b, r, :len(order)] = e / e.sum()
+    return gt, idx, sc
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("S,k", [(40, 3), (40, 8), (300, 150)])
+def test_topk_route_non_finite(dev, dtype, S, k):
+    """One rule for non-finite scores on every routing path (the select kernels at k <= 32 and
+    k <= 128, the sort beyond 128): a NaN or -inf score is never selected, empty slots are
+    (-1, -inf, 0), gates the softmax of the filled slots.  A query row of NaN (no slot filled),
+    a key with a NaN (never selected by any row of its batch entry), and a key scoring -inf for
+    every row."""
+    g = torch.Generator().manual_seed(S + k)
+    q = torch.randn(2, 30, 64, generator=g)
+    q[..., 0] = q[..., 0].abs() + 0.1   # positive first component: key 9 below scores -inf
+    q = norm(q)
+    keys = norm(torch.randn(2, S, 64, generator=g))
+    q[0, 3] = float("nan")
+    keys[1, 5, 7] = float("nan")
+    keys[0, 9, 0] = float("-inf")
+    q, keys = q.to(dtype), keys.to(dtype)
+    print(f"topk_route non-finite S={S} k={k} {dtype}", flush=True)
+    gates, idx, sc = torch.ops.grm_cuda.topk_route(q.to(dev), keys.to(dev), k, 0.125, 1.0)
+    og, oi, osc = _nonfinite_expect(q.float().numpy(), keys.float().numpy(), k, 0.125)
+    assert np.array_equal(idx.cpu().numpy(), oi)
+    assert np.array_equal(sc.cpu().numpy(), osc)
+    np.testing.assert_allclose(gates.cpu().numpy(), og, rtol=1e-5, atol=1e-6)
+    assert bool((idx[0, 3] == -1).all()) and not bool((idx[1] == 5).any()) and not bool((idx[0] == 9).any())
