@@ -390,6 +390,44 @@ int grm_hip_segment_route(const void* queries, const void* keys, int64_t* topk_i
                           int64_t base, int64_t capacity, float scale, float temperature, void* stream);
 
 /*
+ * Segment-window retrieval: retrieve_fuse for the indices of grm_hip_segment_route,
+ * summing each query's routes without one row per (query, route):
+ *   out[b, t, :] = LN(h_online[b, t, :] + sum_r gates[b, t, r] * M[b, idx[b, t, r]] q[b, t])
+ * Query t sees the entries [lo(t), hi(t)), hi(t) = base + t / segment_len,
+ * lo(t) = max(0, hi(t) - capacity), as in grm_hip_segment_route.  A negative
+ * index is an empty slot.  An index outside the query's window, or repeating an
+ * earlier route of the same query, contributes nothing and, when
+ * bad_index_count is not NULL, increments that device int32 counter.
+ * The products are retrieve_fuse's exact 16-bit MFMA products; each query's
+ * float32 sum runs in index order over the entries, then leaves as float16
+ * scaled by a power of two per (query, 128-value tile) (relative rounding 2^-11
+ * of the tile's largest value) for the residual + LayerNorm pass, as one route
+ * of retrieve_fuse.  Deterministic, no atomics in the sums.
+ * Dtypes, layouts and LayerNorm parameters as grm_hip_retrieve_fuse (float16
+ * memories with bf16 queries use float16 MFMA with each query scaled by a power of
+ * two: its components within 2^-29 of its largest magnitude are exact, smaller
+ * ones kept to 2^-40 of it).  Workspace: grm_hip_segment_retrieve_fuse_workspace(
+ * batch, n_query, value_dim, key_dim, segment_len, base, capacity, mem_dtype) bytes
+ * (the scaled sums and a copy of the windows' entries in MMA fragment order).
+ * Replaces, for the reference's segment loop (grm/core/paper_grm.py:702-728),
+ * the retriever and the aggregator's residual fusion it runs per segment
+ *   (paper_grm.py:229,301-313,604-611; grm/core/aggregator.py:67-145).
+ * Limits: key_dim <= 128 and a multiple of 8, value_dim a multiple of 8 and
+ * <= 2048, routes <= 32, min(capacity, base + (n_query - 1) / segment_len) +
+ * 127 / segment_len + 1 <= 256, base + (n_query - 1) / segment_len <= segments;
+ * otherwise GRM_HIP_EUNSUPPORTED or GRM_HIP_EINVAL.  ABI 109.
+ */
+int64_t grm_hip_segment_retrieve_fuse_workspace(int64_t batch, int64_t n_query, int64_t value_dim, int64_t key_dim,
+                                                int64_t segment_len, int64_t base, int64_t capacity, int mem_dtype);
+int grm_hip_segment_retrieve_fuse(const void* memories, const int64_t* indices, const void* queries,
+                                  const float* gates, const void* h_online, const void* ln_weight,
+                                  const void* ln_bias, void* out, void* workspace, int64_t workspace_bytes,
+                                  int64_t batch, int64_t segments, int64_t n_query, int64_t routes,
+                                  int64_t value_dim, int64_t key_dim, int64_t segment_len, int64_t base,
+                                  int64_t capacity, int mem_dtype, int q_dtype, int h_dtype, float eps,
+                                  int32_t* bad_index_count, void* stream);
+
+/*
  * Residual fusion of the online state with gated retrieved states:
  *   x = h_online[n] + sum_r gates[n, r] * retrieved[n, r]
  *   out[n] = layer_norm(x) * weight + bias      (ln_weight == NULL: no LayerNorm)

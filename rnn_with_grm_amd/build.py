@@ -29,7 +29,8 @@ LIB_EXT = PKG_DIR / "grm_cuda_ext.so"
 
 OFFLOAD_ARCH = "gfx950"
 HIP_SOURCES = ["grm_capi.hip", "chunk_scan.hip", "chunk_scan_wide.hip", "chunk_scan_vsplit.hip", "chunk_bwd.hip",
-               "gather_apply.hip", "retrieve.hip", "route_fuse.hip", "route_select.hip", "layer_glue.hip"]
+               "gather_apply.hip", "retrieve.hip", "retrieve_window.hip", "route_fuse.hip", "route_select.hip",
+               "layer_glue.hip"]
 EXT_SOURCE = "grm_torch_ops.cpp"
 
 # Packed fp32 instructions are kept out of every kernel (the flag is for the
@@ -73,7 +74,8 @@ def _stale(target: Path, deps: List[Path]) -> bool:
 
 
 def _headers() -> List[Path]:
-    return [INCLUDE / "grm_hip.h", CSRC / "grm_hip_common.h", CSRC / "chunk_scan.h", CSRC / "route_select.h"]
+    return [INCLUDE / "grm_hip.h", CSRC / "grm_hip_common.h", CSRC / "chunk_scan.h", CSRC / "route_select.h",
+            CSRC / "retrieve.h"]
 
 
 def build_hip_library(force: bool = True, verbose: bool = False, jobs: Optional[int] = None) -> Path:

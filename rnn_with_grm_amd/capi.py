@@ -52,6 +52,9 @@ SIGNATURES = {
                                                 ctypes.c_float, _P]),
     "grm_hip_retrieve_fuse": (_C, [_P, _P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _C, _C, _C,
                                    ctypes.c_float, _P, _P]),
+    "grm_hip_segment_retrieve_fuse_workspace": (_I, [_I, _I, _I, _I, _I, _I, _I, _C]),
+    "grm_hip_segment_retrieve_fuse": (_C, [_P, _P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _I, _I,
+                                           _I, _C, _C, _C, ctypes.c_float, _P, _P]),
     "grm_hip_topk_route": (_C, [_P, _P, _P, _P, _P, _I, _I, _I, _I, _C, _I, ctypes.c_float, ctypes.c_float, _P]),
     "grm_hip_segment_route": (_C, [_P, _P, _P, _P, _P, _I, _I, _I, _I, _C, _I, _I, _I, _I, ctypes.c_float,
                                    ctypes.c_float, _P]),
@@ -277,6 +280,29 @@ def retrieve_fuse(memories, indices, queries, gates, h_online, ln_weight=None, l
                                       dtype_code(memories.dtype), dtype_code(queries.dtype),
                                       dtype_code(h_online.dtype), float(eps), _ptr(bad_count), _stream(memories))
     _check(rc, "grm_hip_retrieve_fuse")
+    return out
+
+
+def segment_retrieve_fuse(memories, indices, queries, gates, h_online, segment_len: int, base: int, capacity: int,
+                          ln_weight=None, ln_bias=None, eps=1e-5, bad_count=None, out=None):
+    """retrieve_fuse for the indices of segment routing: query t sees the entries [lo(t), hi(t)),
+    hi(t) = base + t // segment_len, lo(t) = max(0, hi(t) - capacity); negative indices are empty
+    slots, indices outside the window (or repeated within a query) contribute nothing and are
+    counted in bad_count.  Each query's routes are summed in the kernel (no per-route rows)."""
+    B, S, H, K = memories.shape
+    Q, R = indices.shape[1], indices.shape[2]
+    if out is None:
+        out = torch.empty_like(h_online)
+    wsb = int(load().grm_hip_segment_retrieve_fuse_workspace(B, Q, H, K, int(segment_len), int(base), int(capacity),
+                                                              dtype_code(memories.dtype)))
+    ws = torch.empty(max(wsb, 16), dtype=torch.uint8, device=memories.device)
+    rc = load().grm_hip_segment_retrieve_fuse(_ptr(memories), _ptr(indices), _ptr(queries), _ptr(gates),
+                                              _ptr(h_online), _ptr(ln_weight), _ptr(ln_bias), _ptr(out), _ptr(ws),
+                                              wsb, B, S, Q, R, H, K, int(segment_len), int(base), int(capacity),
+                                              dtype_code(memories.dtype), dtype_code(queries.dtype),
+                                              dtype_code(h_online.dtype), float(eps), _ptr(bad_count),
+                                              _stream(memories))
+    _check(rc, "grm_hip_segment_retrieve_fuse")
     return out
 
 

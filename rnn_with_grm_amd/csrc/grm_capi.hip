@@ -37,7 +37,7 @@ int check_launch(const char* what) {
 
 }  // namespace grmhip
 
-extern "C" int grm_hip_abi_version(void) { return 108; }
+extern "C" int grm_hip_abi_version(void) { return 109; }
 
 extern "C" const char* grm_hip_last_error(void) { return grmhip::g_last_error; }
 

@@ -2,13 +2,15 @@
 //
 // The five schemas are the reference's, character for character
 // (reference grm/csrc/bindings.cpp:5-11), so grm.core.cuda_ops and every model
-// above it bind to this library unchanged.  Fourteen more ops live in the same
+// above it bind to this library unchanged.  Fifteen more ops live in the same
 // namespace: segment_scan_forward (whole-sequence update with per-segment
 // state snapshots), topk_route (score -> top-k -> softmax), segment_route (the
 // same routing for every segment of a sequence against the archive as it
 // grows), fuse_residual, gather_apply (gather + query application without
 // materialising the states), retrieve_fuse (gather_apply, the gate-weighted
-// sum and fuse_residual in one call), the layer glue project_split (the
+// sum and fuse_residual in one call), segment_retrieve_fuse (the same for the
+// windows of segment routing, summing the routes without per-route rows), the
+// layer glue project_split (the
 // projection's split with L2-normalised keys and queries),
 // residual_layer_norm (the block's LayerNorm(out + x)), project_gemm (the
 // projection GEMM with project_split as its epilogue),
@@ -415,6 +417,67 @@ Tensor retrieve_fuse_generic(const Tensor& memories, const Tensor& indices, cons
   Tensor r = gather_apply_generic(memories, indices, queries, at::kFloat).reshape({B * Q, R, H});
   // float32 sum and LayerNorm, one rounding to h's dtype at the end
   return fuse_residual_generic(h.reshape({B * Q, H}).to(at::kFloat), r, gates.reshape({B * Q, R}), weight, bias, eps)
+      .to(h.scalar_type())
+      .reshape({B, Q, H});
+}
+
+// segment_retrieve_fuse: retrieve_fuse for the indices of segment routing
+// (paper_grm.py:702-728 -> _route_chunk, :566-589): query t sees the archive
+// entries [lo(t), hi(t)), hi(t) = base + t / segment_len, lo(t) = max(0, hi(t) -
+// capacity).  A negative index is an empty slot; an index outside the query's
+// window, or repeating an earlier route of the same query, contributes nothing
+// (and is reported when GRM_HIP_CHECK_INDICES is set).
+bool check_indices_requested();
+
+void check_segment_window(int64_t segment_len, int64_t base, int64_t capacity) {
+  TORCH_CHECK(segment_len >= 1 && base >= 0 && capacity >= 1,
+              "segment_retrieve_fuse: needs segment_len >= 1, base >= 0 and capacity >= 1");
+}
+
+// [B, Q, R] bool: the pairs that contribute.
+Tensor segment_window_valid(const Tensor& indices, int64_t segment_len, int64_t base, int64_t capacity) {
+  const int64_t Q = indices.size(1), R = indices.size(2);
+  Tensor t = at::arange(Q, indices.options().dtype(at::kLong));
+  Tensor hi = (at::floor_divide(t, segment_len) + base).view({1, Q, 1});
+  Tensor lo = at::clamp_min(hi - capacity, 0);
+  Tensor idx = indices.to(at::kLong);
+  Tensor valid = idx.ge(lo).logical_and(idx.lt(hi));
+  if (R > 1) {
+    Tensor eq = idx.unsqueeze(-1).eq(idx.unsqueeze(-2));  // [B, Q, R, R]: route r against route r2
+    Tensor earlier = at::ones({R, R}, indices.options().dtype(at::kBool)).tril(-1);
+    valid = valid.logical_and(eq.logical_and(earlier).any(-1).logical_not());
+  }
+  return valid;
+}
+
+void check_window_indices(const Tensor& indices, const Tensor& valid) {
+  if (!check_indices_requested()) return;
+  const int64_t nbad = indices.ge(0).logical_and(valid.logical_not()).sum().item<int64_t>();
+  TORCH_CHECK_INDEX(nbad == 0, "segment_retrieve_fuse: ", nbad,
+                    " index values outside their query's window or repeated");
+}
+
+Tensor segment_retrieve_fuse_generic(const Tensor& memories, const Tensor& indices, const Tensor& queries,
+                                     const Tensor& gates, const Tensor& h, const c10::optional<Tensor>& weight,
+                                     const c10::optional<Tensor>& bias, double eps, int64_t segment_len, int64_t base,
+                                     int64_t capacity) {
+  check_retrieve_fuse_inputs(memories, indices, queries, gates, h);
+  check_segment_window(segment_len, base, capacity);
+  const int64_t B = h.size(0), Q = h.size(1), H = h.size(2), R = indices.size(2), S = memories.size(1);
+  TORCH_CHECK(Q == 0 || base + (Q - 1) / segment_len <= S,
+              "segment_retrieve_fuse: windows past the archive (base + (Q - 1) / segment_len > segments)");
+  Tensor valid = segment_window_valid(indices, segment_len, base, capacity);
+  check_window_indices(indices, valid);
+  Tensor r;
+  if (S == 0 || R == 0) {
+    r = at::zeros({B * Q, R, H}, h.options().dtype(at::kFloat));
+  } else {
+    Tensor idx = indices.to(at::kLong).masked_fill(valid.logical_not(), 0);
+    r = gather_apply_generic(memories, idx, queries, at::kFloat).reshape({B * Q, R, H});
+    r = r.masked_fill(valid.logical_not().reshape({B * Q, R, 1}), 0.0);
+  }
+  Tensor g = gates.to(at::kFloat).masked_fill(valid.logical_not(), 0.0).reshape({B * Q, R});
+  return fuse_residual_generic(h.reshape({B * Q, H}).to(at::kFloat), r, g, weight, bias, eps)
       .to(h.scalar_type())
       .reshape({B, Q, H});
 }
@@ -966,6 +1029,68 @@ Tensor retrieve_fuse_hip(const Tensor& memories, const Tensor& indices, const Te
   return out;
 }
 
+Tensor segment_retrieve_fuse_hip(const Tensor& memories, const Tensor& indices, const Tensor& queries,
+                                 const Tensor& gates, const Tensor& h, const c10::optional<Tensor>& weight,
+                                 const c10::optional<Tensor>& bias, double eps, int64_t segment_len, int64_t base,
+                                 int64_t capacity) {
+  check_retrieve_fuse_inputs(memories, indices, queries, gates, h);
+  check_segment_window(segment_len, base, capacity);
+  const bool has_w = weight.has_value() && weight->defined();
+  const bool has_b = bias.has_value() && bias->defined();
+  const int64_t B = memories.size(0), S = memories.size(1), H = memories.size(2), K = memories.size(3);
+  const int64_t Q = indices.size(1), R = indices.size(2);
+  TORCH_CHECK(Q == 0 || base + (Q - 1) / segment_len <= S,
+              "segment_retrieve_fuse: windows past the archive (base + (Q - 1) / segment_len > segments)");
+  const int md = dtype_code(memories.scalar_type()), qd = dtype_code(queries.scalar_type());
+  const int hd = dtype_code(h.scalar_type());
+  const bool q16 = queries.scalar_type() == at::kBFloat16 ||
+                   (queries.scalar_type() == at::kHalf && memories.scalar_type() == at::kHalf);
+  const int64_t span = std::min(capacity, base + (Q > 0 ? (Q - 1) / segment_len : 0)) + 127 / segment_len + 1;
+  bool ok = same_cuda_device({&memories, &indices, &queries, &gates, &h}) && md >= 0 && qd >= 0 && hd >= 0 && q16 &&
+            K <= 128 && K % 8 == 0 && H % 8 == 0 && H <= 2048 && R <= 32 && span <= 256;
+  if (has_w) ok = ok && weight->is_cuda() && weight->numel() == H;
+  if (has_b) ok = ok && has_w && bias->is_cuda() && bias->numel() == H;
+  if (!ok) {
+    // retrieve_fuse over the masked pairs (an invalid pair: index 0, gate 0).
+    Tensor valid = segment_window_valid(indices, segment_len, base, capacity);
+    check_window_indices(indices, valid);
+    if (S == 0) return segment_retrieve_fuse_generic(memories, indices, queries, gates, h, weight, bias, eps,
+                                                     segment_len, base, capacity);
+    return retrieve_fuse_hip(memories, indices.to(at::kLong).masked_fill(valid.logical_not(), 0), queries,
+                             gates.to(at::kFloat).masked_fill(valid.logical_not(), 0.0), h, weight, bias, eps);
+  }
+  c10::OptionalDeviceGuard guard(memories.device());
+  Tensor mm = memories.contiguous(), idx = indices.to(at::kLong).contiguous(), q = queries.contiguous();
+  Tensor gc = gates.to(at::kFloat).contiguous(), hc = h.contiguous();
+  Tensor wc = has_w ? weight->to(at::kFloat).contiguous() : Tensor();
+  Tensor bc = has_b ? bias->to(at::kFloat).contiguous() : Tensor();
+  if (!aligned16(mm) || !aligned16(q) || !aligned16(hc) || (has_w && !aligned16(wc)) || (has_b && !aligned16(bc))) {
+    mm = mm.clone();
+    q = q.clone();
+    hc = hc.clone();
+    if (has_w) wc = wc.clone();
+    if (has_b) bc = bc.clone();
+  }
+  Tensor out = at::empty_like(hc);
+  const int64_t wsb = grm_hip_segment_retrieve_fuse_workspace(B, Q, H, K, segment_len, base, capacity, md);
+  Tensor ws = at::empty({std::max<int64_t>(wsb, 16)}, mm.options().dtype(at::kByte));
+  Tensor bad;
+  const bool check = check_indices_requested();
+  if (check) bad = at::zeros({1}, mm.options().dtype(at::kInt));
+  check_rc(grm_hip_segment_retrieve_fuse(mm.data_ptr(), idx.data_ptr<int64_t>(), q.data_ptr(), gc.data_ptr<float>(),
+                                         hc.data_ptr(), has_w ? wc.data_ptr() : nullptr,
+                                         has_b ? bc.data_ptr() : nullptr, out.data_ptr(), ws.data_ptr(), wsb, B, S, Q,
+                                         R, H, K, segment_len, base, capacity, md, qd, hd, static_cast<float>(eps),
+                                         check ? bad.data_ptr<int32_t>() : nullptr, current_stream(mm)),
+           "segment_retrieve_fuse");
+  if (check) {
+    const int64_t nbad = bad.item<int32_t>();
+    TORCH_CHECK_INDEX(nbad == 0, "segment_retrieve_fuse: ", nbad,
+                      " index values outside their query's window or repeated");
+  }
+  return out;
+}
+
 Tensor gather_apply_backward_queries_hip(const Tensor& memories, const Tensor& indices, const Tensor& grad_out,
                                          const Tensor& queries) {
   check_gather_apply_inputs(memories, indices, queries);
@@ -1229,6 +1354,8 @@ TORCH_LIBRARY(grm_cuda, m) {
         "-> (Tensor, Tensor, Tensor, Tensor)");
   m.def("linear_residual_layer_norm(Tensor x, Tensor weight, Tensor? bias, Tensor residual, Tensor? ln_weight, "
         "Tensor? ln_bias, float eps, bool save) -> (Tensor out, Tensor pre, Tensor mean, Tensor rstd)");
+  m.def("segment_retrieve_fuse(Tensor memories, Tensor indices, Tensor queries, Tensor gates, Tensor h_online, "
+        "Tensor? weight, Tensor? bias, float eps, int segment_len, int base, int capacity) -> Tensor");
 }
 
 TORCH_LIBRARY_IMPL(grm_cuda, CPU, m) {
@@ -1251,6 +1378,7 @@ TORCH_LIBRARY_IMPL(grm_cuda, CPU, m) {
   m.impl("archive_cast", grm::archive_cast_generic);
   m.impl("project_gemm", grm::project_gemm_generic);
   m.impl("linear_residual_layer_norm", grm::linear_residual_layer_norm_generic);
+  m.impl("segment_retrieve_fuse", grm::segment_retrieve_fuse_generic);
 }
 
 TORCH_LIBRARY_IMPL(grm_cuda, CUDA, m) {
@@ -1273,6 +1401,7 @@ TORCH_LIBRARY_IMPL(grm_cuda, CUDA, m) {
   m.impl("archive_cast", grm::archive_cast_hip);
   m.impl("project_gemm", grm::project_gemm_hip);
   m.impl("linear_residual_layer_norm", grm::linear_residual_layer_norm_hip);
+  m.impl("segment_retrieve_fuse", grm::segment_retrieve_fuse_hip);
 }
 
 PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {

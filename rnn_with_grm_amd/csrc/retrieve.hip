@@ -23,6 +23,7 @@
 
 #include "grm_hip.h"
 #include "grm_hip_common.h"
+#include "retrieve.h"
 
 namespace grmhip {
 namespace {
@@ -34,7 +35,7 @@ constexpr int BK_ITEMS = 16384;      // pairs per workgroup when one sequence's 
 constexpr int64_t kMultiBucketPairs = 4 * BK_ITEMS;  // from this many pairs per sequence
 constexpr int64_t kMaxSegments = 16384;
 constexpr int AP_THREADS = 256;      // apply kernel: 4 waves
-constexpr int AP_V = 128;            // value rows per workgroup
+constexpr int AP_V = kScaledTile;    // value rows per workgroup
 constexpr int AP_N = 64;             // (q, r) pairs per tile
 
 struct RetrieveArgs {
@@ -820,27 +821,6 @@ bool vec_ok(const RetrieveArgs& a) {
          a.n_query * static_cast<int64_t>(a.dk) * static_cast<int64_t>(sizeof(typename ET<EQ>::raw)) < INT32_MAX;
 }
 
-// Exact 16-bit MFMA when both operands are exact in one 16-bit MFMA input type
-// EF: the query in the arithmetic type EM must be exact in EF, and the stored
-// memories split into NPART parts of EF without loss.  Otherwise fp32 MFMA.
-template <class EL, class EM, class EQ>
-struct MfmaPlan {
-  static constexpr bool kSame = std::is_same<EL, EM>::value;
-  static constexpr bool kF32 = std::is_same<EM, F32>::value;
-  // EM 16-bit (then EL == EM): the query is cast to EM, EF = EM, one part.
-  // EM float32: queries bf16 with fp32 / bf16 / f16 memories (3 / 1 / 2 bf16
-  // parts), or f16 queries with f16 memories (one f16 part).
-  static constexpr bool kBf16Q = std::is_same<EQ, BF16>::value;
-  static constexpr bool kF16Both = std::is_same<EQ, F16>::value && std::is_same<EL, F16>::value;
-  static constexpr bool ok = !kF32 ? kSame : (kBf16Q || kF16Both);
-  using EF = typename std::conditional<!kF32, EM, typename std::conditional<kF16Both, F16, BF16>::type>::type;
-  static constexpr int parts = !kF32 ? 1
-                               : kF16Both ? 1
-                               : std::is_same<EL, F32>::value ? 3
-                               : std::is_same<EL, F16>::value ? 2
-                                                              : 1;
-};
-
 template <class EL, class EM, class EQ>
 int dispatch_dk(const RetrieveArgs& a, hipStream_t s) {
   if (vec_ok<EL, EQ>(a)) {
@@ -878,19 +858,6 @@ int dispatch_q(const RetrieveArgs& a, int q_dtype, hipStream_t s) {
 // with r in order 0 .. R-1 (the gates are already in the rows), a two-pass
 // mean / variance in fp32.  lpr lanes share a row, each covering NV groups of
 // 8 consecutive columns (16-byte float16 loads of the rows).
-struct FuseScaledArgs {
-  const void* h;
-  const uint16_t* rows;
-  const float* scales;
-  const void* w;
-  const void* bias;
-  void* out;
-  int64_t n_rows;
-  int routes;
-  int hidden;
-  int v_tiles;
-  float eps;
-};
 
 template <class E>
 __device__ __forceinline__ void load8(__amdgpu_buffer_rsrc_t r, int off, float (&f)[8]) {
@@ -1019,6 +986,18 @@ int launch_fuse_scaled(const FuseScaledArgs& a, hipStream_t s) {
   else go(std::integral_constant<int, 8>{});
   return check_launch("retrieve_fuse(fuse)");
 }
+
+}  // namespace
+
+int fuse_scaled(const FuseScaledArgs& a, int h_dtype, hipStream_t s) {
+  switch (h_dtype) {
+    case GRM_HIP_F32: return launch_fuse_scaled<F32>(a, s);
+    case GRM_HIP_F16: return launch_fuse_scaled<F16>(a, s);
+    default: return launch_fuse_scaled<BF16>(a, s);
+  }
+}
+
+namespace {
 
 // The scaled apply runs the exact 16-bit MFMA kernel with float32 arithmetic;
 // other dtype pairs and unaligned shapes are not supported by retrieve_fuse.
@@ -1717,11 +1696,7 @@ extern "C" int grm_hip_retrieve_fuse(const void* memories, const int64_t* indice
   f.hidden = static_cast<int>(value_dim);
   f.v_tiles = v_tiles;
   f.eps = eps;
-  switch (h_dtype) {
-    case GRM_HIP_F32: return launch_fuse_scaled<F32>(f, s);
-    case GRM_HIP_F16: return launch_fuse_scaled<F16>(f, s);
-    default: return launch_fuse_scaled<BF16>(f, s);
-  }
+  return fuse_scaled(f, h_dtype, s);
 }
 
 namespace {

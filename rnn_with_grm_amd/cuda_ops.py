@@ -40,7 +40,7 @@ SCHEMA_OPS = (
 EXTRA_OPS = ("segment_scan_forward", "topk_route", "fuse_residual", "gather_apply", "segment_route",
              "retrieve_fuse", "project_split", "residual_layer_norm", "gather_apply_backward_queries",
              "gather_apply_backward_tokens", "apply_query_backward_queries", "archive_cast", "project_gemm",
-             "linear_residual_layer_norm")
+             "linear_residual_layer_norm", "segment_retrieve_fuse")
 
 # Environment variables of the reference (cuda_ops.py:26-32): one per op and a global one.
 GLOBAL_POLICY_ENV = "GRM_CUDA_KERNEL_POLICY"
@@ -596,6 +596,51 @@ def cuda_retrieve_fuse(memories_per_batch: Tensor, topk_indices: Tensor, queries
     return fused.reshape(B, Q, H).to(h_online.dtype)
 
 
+def _segment_window_valid(indices: Tensor, segment_len: int, base: int, capacity: int) -> Tensor:
+    """[B, Q, R] bool: the (query, route) pairs inside the query's routing window
+    [max(0, hi - capacity), hi), hi = base + t // segment_len, and not repeating an
+    earlier route of the same query."""
+    Q, R = indices.shape[1], indices.shape[2]
+    hi = (torch.arange(Q, device=indices.device) // segment_len + base).view(1, Q, 1)
+    lo = (hi - capacity).clamp(min=0)
+    valid = (indices >= lo) & (indices < hi)
+    if R > 1:
+        earlier = torch.ones(R, R, dtype=torch.bool, device=indices.device).tril(-1)
+        valid = valid & ~((indices.unsqueeze(-1) == indices.unsqueeze(-2)) & earlier).any(-1)
+    return valid
+
+
+def cuda_segment_retrieve_fuse(memories_per_batch: Tensor, topk_indices: Tensor, queries: Tensor, gates: Tensor,
+                               h_online: Tensor, weight: Optional[Tensor], bias: Optional[Tensor], eps: float,
+                               segment_len: int, base: int, capacity: int, *, enabled: bool = True,
+                               debug_fallback: bool = False) -> Tensor:
+    """cuda_retrieve_fuse for the indices of segment routing (paper_grm.py:702-728 ->
+    _route_chunk, :566-589): query t routes over the archive entries [lo(t), hi(t)),
+    hi(t) = base + t // segment_len, lo(t) = max(0, hi(t) - capacity).  A negative index
+    is an empty slot; an index outside the window or repeated within a query contributes
+    nothing.  The native op sums each query's routes inside the kernel, one workgroup per
+    block of queries walking the block's window, so no per-route rows are written.
+    Inference only (no autograd)."""
+    if _run_native("retrieve_fuse", h_online.device, enabled=enabled, debug_fallback=debug_fallback):
+        return torch.ops.grm_cuda.segment_retrieve_fuse(memories_per_batch, topk_indices, queries, gates, h_online,
+                                                        weight, bias, float(eps), int(segment_len), int(base),
+                                                        int(capacity))
+    B, Q, H = h_online.shape
+    R = topk_indices.size(-1)
+    valid = _segment_window_valid(topk_indices, segment_len, base, capacity)
+    if memories_per_batch.size(1) == 0 or R == 0:
+        retrieved = h_online.new_zeros(B, Q, R, H, dtype=torch.float32)
+    else:
+        retrieved = cuda_gather_apply(memories_per_batch, topk_indices.masked_fill(~valid, 0), queries, torch.float32,
+                                      enabled=enabled, debug_fallback=debug_fallback)
+        retrieved = retrieved.masked_fill(~valid.unsqueeze(-1), 0.0)
+    fused = cuda_fuse_residual(h_online.reshape(B * Q, H).float(), retrieved.reshape(B * Q, R, H),
+                               gates.float().masked_fill(~valid, 0.0).reshape(B * Q, R),
+                               None if weight is None else weight.float(), None if bias is None else bias.float(),
+                               eps, enabled=enabled, debug_fallback=debug_fallback)
+    return fused.reshape(B, Q, H).to(h_online.dtype)
+
+
 def cuda_archive_cast(states: Tensor, model_dtype: torch.dtype, storage_dtype: torch.dtype, *,
                       enabled: bool = True, debug_fallback: bool = False) -> Tensor:
     """float32 states as the archive stores them: rounded to the model dtype, then to the
@@ -793,6 +838,7 @@ __all__ = [
     "cuda_project_split",
     "cuda_residual_layer_norm",
     "cuda_retrieve_fuse",
+    "cuda_segment_retrieve_fuse",
     "cuda_segment_route",
     "cuda_segment_scan",
     "cuda_topk_route",

@@ -607,11 +607,13 @@ class SegmentRecurrentMemoryModel(nn.Module):
                                                     debug_fallback=self.cuda_cpp_debug_fallback)
             elif q.dtype in (torch.bfloat16, torch.float16):
                 # A 16-bit model: retrieval, gate-weighted sum, residual and LayerNorm in one
-                # op; the [B, T, k, H] retrieved rows are kept as row-scaled float16 (relative
-                # rounding 2^-11 of each row's largest value), never as float32.
+                # op over the routing windows: each block of tokens walks its window of
+                # archive entries and sums its routes in float32, the sums kept as
+                # tile-scaled float16 (relative rounding 2^-11) for the LayerNorm pass.
                 w32, b32 = self._float32_norm_params(weight, bias)
-                fused = cuda_ops.cuda_retrieve_fuse(states, idx0, q_in, gates.float(), h_online, w32, b32, eps,
-                                                    debug_fallback=self.cuda_cpp_debug_fallback)
+                fused = cuda_ops.cuda_segment_retrieve_fuse(states, idx, q_in, gates.float(), h_online, w32, b32,
+                                                            eps, seg, base, cap,
+                                                            debug_fallback=self.cuda_cpp_debug_fallback)
             else:
                 H = h_online.size(-1)
                 retrieved = cuda_ops.cuda_gather_apply(states, idx0, q_in, torch.float32,

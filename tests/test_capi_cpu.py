@@ -37,7 +37,7 @@ def test_workspace_query():
 
 def test_abi_version_and_counters():
     lib = capi.load()
-    assert lib.grm_hip_abi_version() == 108
+    assert lib.grm_hip_abi_version() == 109
     assert capi.launch_count() >= 0
 
 

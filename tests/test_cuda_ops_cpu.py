@@ -237,6 +237,47 @@ def test_cpu_gather_apply_is_the_composition():
         torch.ops.grm_cuda.gather_apply(m16, idx, q, torch.bfloat16)
 
 
+def test_cpu_segment_retrieve_fuse_window_rule(monkeypatch):
+    """The generic segment_retrieve_fuse (CPU key): only the pairs inside the query's routing
+    window [max(0, hi - capacity), hi), hi = base + t // segment_len, that do not repeat an
+    earlier route contribute; against the oracle's gather -> apply -> residual + LayerNorm over
+    exactly those pairs, the PyTorch fallback of cuda_segment_retrieve_fuse, and the index
+    check (GRM_HIP_CHECK_INDICES) naming the bad pairs."""
+    g = torch.Generator().manual_seed(9)
+    B, Q, S, H, K, R, seg, base, cap = 2, 40, 8, 16, 8, 4, 6, 2, 3
+    mem = torch.randn(B, S, H, K, generator=g)
+    q = torch.randn(B, Q, K, generator=g)
+    h = torch.randn(B, Q, H, generator=g)
+    gates = torch.softmax(torch.randn(B, Q, R, generator=g), -1)
+    w, b = 1 + 0.1 * torch.randn(H, generator=g), 0.1 * torch.randn(H, generator=g)
+    idx = torch.randint(-1, S, (B, Q, R), generator=g)
+    idx[0, 5, 2] = idx[0, 5, 1] = base + 5 // seg - 1  # a repeat inside the window
+    out = torch.ops.grm_cuda.segment_retrieve_fuse(mem, idx, q, gates, h, w, b, 1e-5, seg, base, cap)
+    t = np.arange(Q)[None, :, None]
+    hi = base + t // seg
+    lo = np.maximum(hi - cap, 0)
+    ix = idx.numpy()
+    valid = (ix >= lo) & (ix < hi)
+    for r in range(R):
+        for r2 in range(r):
+            valid[:, :, r] &= ix[:, :, r] != ix[:, :, r2]
+    assert not valid[0, 5, 2] and valid[0, 5, 1]
+    gathered, _ = orc.gather(np64(mem), np.where(valid, ix, 0))
+    rows = orc.apply_query(gathered, np64(q)) * valid[..., None]
+    ref = orc.fuse_residual(np64(h).reshape(B * Q, H), rows.reshape(B * Q, R, H),
+                            (np64(gates) * valid).reshape(B * Q, R), np64(w), np64(b)).reshape(B, Q, H)
+    np.testing.assert_allclose(out.numpy(), ref, rtol=1e-5, atol=1e-5)
+    fb = cuda_ops.cuda_segment_retrieve_fuse(mem, idx, q, gates, h, w, b, 1e-5, seg, base, cap, debug_fallback=True)
+    np.testing.assert_allclose(fb.numpy(), ref, rtol=1e-5, atol=1e-5)
+    nbad = int(((ix >= 0) & ~valid).sum())
+    assert nbad > 0
+    monkeypatch.setenv("GRM_HIP_CHECK_INDICES", "1")
+    with pytest.raises(IndexError, match=f"{nbad} index values outside their query's window or repeated"):
+        torch.ops.grm_cuda.segment_retrieve_fuse(mem, idx, q, gates, h, w, b, 1e-5, seg, base, cap)
+    with pytest.raises(RuntimeError, match="windows past the archive"):
+        torch.ops.grm_cuda.segment_retrieve_fuse(mem, idx, q, gates, h, w, b, 1e-5, seg, base + S, cap)
+
+
 def test_shape_errors_raise_like_reference():
     k, v, q, m = make_chunk_case(4)
     with pytest.raises(RuntimeError, match="keys must have shape"):

@@ -660,6 +660,169 @@ def test_retrieve_fuse_op_and_model_path(dev):
     assert torch.equal(d, e.reshape(B, Q, H))
 
 
+# ---------------------------------------------------------------- segment-window retrieval
+def _window_indices(g, B, Q, R, S, seg, base, cap):
+    """Routing-like indices: query t takes up to R distinct entries of its window
+    [max(0, hi - cap), hi), hi = base + t // seg, the rest -1; then three bad pairs are
+    planted (an entry past the window, one before it, and a repeat of an earlier route)
+    where the window allows.  Returns the indices and the number of bad pairs."""
+    idx = torch.full((B, Q, R), -1, dtype=torch.long)
+    for bb in range(B):
+        for t in range(Q):
+            hi = base + t // seg
+            lo = max(0, hi - cap)
+            n = min(R, hi - lo)
+            if n > 0:
+                idx[bb, t, :n] = lo + torch.randperm(hi - lo, generator=g)[:n]
+    bad = 0
+    t = Q - 1
+    hi = base + t // seg
+    if hi < S and R >= 1:
+        idx[0, t, 0] = hi  # past the window
+        bad += 1
+    t = Q // 2
+    hi = base + t // seg
+    if hi - cap > 0 and R >= 2:
+        idx[-1, t, 1] = hi - cap - 1  # before the window
+        bad += 1
+    for t in range(Q):
+        if R >= 3 and int(idx[0, t, 0]) >= 0 and int(idx[0, t, 2]) >= 0 and int(idx[0, t, 0]) < base + t // seg:
+            idx[0, t, 2] = idx[0, t, 0]  # a repeat
+            bad += 1
+            break
+    return idx, bad
+
+
+def _window_valid_np(idx, seg, base, cap):
+    B, Q, R = idx.shape
+    hi = base + np.arange(Q)[None, :, None] // seg
+    lo = np.maximum(hi - cap, 0)
+    valid = (idx >= lo) & (idx < hi)
+    for r in range(R):
+        for r2 in range(r):
+            valid[:, :, r] &= idx[:, :, r] != idx[:, :, r2]
+    return valid
+
+
+@pytest.mark.parametrize("mem_dtype,q_dtype", [(torch.float16, torch.bfloat16), (torch.bfloat16, torch.bfloat16),
+                                               (torch.float32, torch.bfloat16), (torch.float16, torch.float16)])
+@pytest.mark.parametrize("h_dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("B,Q,H,K,seg,base,cap,R,ln", [(2, 300, 128, 64, 64, 0, 64, 8, True),
+                                                       (1, 1000, 512, 64, 64, 3, 64, 8, True),
+                                                       (2, 257, 200, 32, 7, 5, 20, 4, False),
+                                                       (1, 130, 40, 48, 1, 0, 100, 16, True),
+                                                       (3, 64, 264, 128, 16, 2, 9, 8, True)])
+def test_segment_retrieve_fuse(dev, mem_dtype, q_dtype, h_dtype, B, Q, H, K, seg, base, cap, R, ln):
+    """segment_retrieve_fuse (each query block walks its routing window, the routes summed in
+    the kernel) against the oracle's gather -> apply -> residual + LayerNorm over the window's
+    valid pairs, at retrieve_fuse's bars (rtol 2e-2 / atol 2e-3; the sums leave as tile-scaled
+    float16); against the float32 two-kernel composition over the same pairs; bad pairs
+    (outside the window, repeated) counted and contributing nothing, empty slots (-1) not
+    counted; run to run bit for bit.  Windows of one entry per token (segment_len 1), partial
+    value tiles, key widths 32 / 48 / 64 / 128."""
+    g = torch.Generator().manual_seed(B * 11 + Q + H + K)
+    S = base + (Q - 1) // seg + 1
+    mem = (torch.randn(B, S, H, K, generator=g) * 0.3).to(mem_dtype)
+    idx, nbad = _window_indices(g, B, Q, R, S, seg, base, cap)
+    q = norm(torch.randn(B, Q, K, generator=g)).to(q_dtype)
+    gates = torch.softmax(torch.randn(B, Q, R, generator=g), dim=-1)
+    h = torch.randn(B, Q, H, generator=g).to(h_dtype)
+    w = (1 + 0.1 * torch.randn(H, generator=g)) if ln else None
+    b = (0.1 * torch.randn(H, generator=g)) if ln else None
+    print(f"segment_retrieve_fuse B={B} Q={Q} H={H} K={K} seg={seg} base={base} cap={cap} R={R} mem {mem_dtype} "
+          f"q {q_dtype} h {h_dtype} ln={ln}", flush=True)
+    D = lambda t: None if t is None else t.to(dev)  # noqa: E731
+    bad = torch.zeros(1, dtype=torch.int32, device=dev)
+    args = (D(mem), D(idx), D(q), D(gates), D(h), seg, base, cap, D(w), D(b))
+    out = capi.segment_retrieve_fuse(*args, bad_count=bad)
+    out2 = capi.segment_retrieve_fuse(*args)
+    valid = _window_valid_np(idx.numpy(), seg, base, cap)
+    vt = torch.from_numpy(valid)
+    idx_m = torch.where(vt, idx, torch.zeros_like(idx))
+    rows = capi.gather_apply(D(mem), D(idx_m), D(q), dtype=torch.float32) * D(vt).unsqueeze(-1)
+    comp = capi.fuse_residual(D(h).float().reshape(B * Q, H), rows.reshape(B * Q, R, H),
+                              (D(gates) * D(vt)).reshape(B * Q, R), D(w), D(b)).reshape(B, Q, H).to(h_dtype)
+    torch.cuda.synchronize()
+    assert out.dtype == h_dtype and out.shape == (B, Q, H)
+    assert int(bad.item()) == nbad
+    assert torch.equal(out, out2), "segment_retrieve_fuse is not deterministic"
+    ref = _retrieve_fuse_ref(mem, torch.where(vt, idx, torch.full_like(idx, -1)), q, gates, h, w, b)
+    got = out.float().cpu().double().numpy()
+    np.testing.assert_allclose(got, ref, rtol=2e-2, atol=2e-3)
+    if h_dtype == torch.float32:
+        err = np.abs(got - ref).max() / max(np.abs(ref).max(), 1e-30)
+        assert err < 2e-3, err
+        torch.testing.assert_close(out, comp, rtol=2e-3, atol=2e-3)
+    else:
+        torch.testing.assert_close(out.float(), comp.float(), rtol=1e-2, atol=1e-2)
+
+
+def test_segment_retrieve_fuse_config4_geometry(dev):
+    """One config-4 layer's retrieval at full size (4 x 8192 tokens, 64-token segments, capacity
+    64, top-8, float16 archive 512 x 64, bf16 queries and rows, LayerNorm) with the indices and
+    gates of segment routing: the window kernel against retrieve_fuse over the same pairs (both
+    keep tile-scaled float16 intermediates) and against the float32 two-kernel composition on
+    two sequences."""
+    g = torch.Generator().manual_seed(44)
+    B, T, H, K, seg, cap, R = 4, 8192, 512, 64, 64, 64, 8
+    S = T // seg
+    mem = (torch.randn(B, S, H, K, generator=g) * 0.05).to(torch.float16).to(dev)
+    q = norm(torch.randn(B, T, K, generator=g)).to(torch.bfloat16).to(dev)
+    keys = norm(torch.randn(B, S, K, generator=g)).to(torch.bfloat16).to(dev)
+    h = torch.randn(B, T, H, generator=g).to(torch.bfloat16).to(dev)
+    w = (1 + 0.1 * torch.randn(H, generator=g)).to(dev)
+    b = (0.1 * torch.randn(H, generator=g)).to(dev)
+    print("segment_retrieve_fuse config-4 geometry", flush=True)
+    gates, idx, _ = capi.segment_route(q, keys, R, seg, 0, cap, K ** -0.5, 1.0)
+    bad = torch.zeros(1, dtype=torch.int32, device=dev)
+    out = capi.segment_retrieve_fuse(mem, idx, q, gates, h, seg, 0, cap, w, b, bad_count=bad)
+    ref = capi.retrieve_fuse(mem, idx.clamp(min=0), q, gates, h, w, b)
+    torch.cuda.synchronize()
+    assert int(bad.item()) == 0
+    torch.testing.assert_close(out.float(), ref.float(), rtol=1e-2, atol=1e-2)
+    assert (out != ref).float().mean().item() < 0.05
+    for bb in (0, 3):
+        rows = capi.gather_apply(mem[bb:bb + 1], idx[bb:bb + 1].clamp(min=0), q[bb:bb + 1], dtype=torch.float32)
+        comp = capi.fuse_residual(h[bb].float(), rows.reshape(T, R, H), gates[bb].reshape(T, R), w, b)
+        torch.testing.assert_close(out[bb].float(), comp, rtol=1e-2, atol=1e-2)
+
+
+def test_segment_retrieve_fuse_op_and_fallbacks(dev):
+    """torch.ops.grm_cuda.segment_retrieve_fuse equals capi.segment_retrieve_fuse with no generic
+    path; float32 queries take retrieve_fuse over the masked pairs (same result as the float32
+    composition over the window's pairs); cuda_segment_retrieve_fuse's PyTorch fallback agrees."""
+    from rnn_with_grm_amd import cuda_ops
+
+    g = torch.Generator().manual_seed(43)
+    B, Q, H, K, seg, base, cap, R = 2, 500, 256, 64, 32, 4, 12, 8
+    S = base + (Q - 1) // seg + 1
+    idx, _ = _window_indices(g, B, Q, R, S, seg, base, cap)
+    mem = (torch.randn(B, S, H, K, generator=g) * 0.1).to(dev)
+    idx = idx.to(dev)
+    q = norm(torch.randn(B, Q, K, generator=g)).to(torch.bfloat16).to(dev)
+    gates = torch.softmax(torch.randn(B, Q, R, generator=g), -1).to(dev)
+    h = torch.randn(B, Q, H, generator=g).to(dev)
+    w, b = torch.ones(H, device=dev), torch.zeros(H, device=dev)
+    ext = cuda_ops.extension_module()
+    generic = ext.generic_path_calls()
+    with torch.no_grad():
+        a = cuda_ops.cuda_segment_retrieve_fuse(mem, idx, q, gates, h, w, b, 1e-5, seg, base, cap)
+    c = capi.segment_retrieve_fuse(mem, idx, q, gates, h, seg, base, cap, w, b)
+    assert torch.equal(a, c) and ext.generic_path_calls() == generic
+    with torch.no_grad():
+        fb = cuda_ops.cuda_segment_retrieve_fuse(mem, idx, q, gates, h, w, b, 1e-5, seg, base, cap,
+                                                 debug_fallback=True)
+    torch.testing.assert_close(fb, a, rtol=2e-3, atol=2e-3)
+    qf = q.float()
+    with torch.no_grad():
+        d = cuda_ops.cuda_segment_retrieve_fuse(mem, idx, qf, gates, h, w, b, 1e-5, seg, base, cap)
+    valid = torch.from_numpy(_window_valid_np(idx.cpu().numpy(), seg, base, cap)).to(dev)
+    rows = capi.gather_apply(mem, torch.where(valid, idx, torch.zeros_like(idx)), qf, dtype=torch.float32)
+    e = capi.fuse_residual(h.reshape(B * Q, H), (rows * valid.unsqueeze(-1)).reshape(B * Q, R, H),
+                           (gates * valid).reshape(B * Q, R), w, b)
+    torch.testing.assert_close(d, e.reshape(B, Q, H), rtol=1e-5, atol=1e-5)
+
+
 # ---------------------------------------------------------------- gather_apply backward (queries)
 @pytest.mark.parametrize("mem_dtype", [torch.float32, torch.float16, torch.bfloat16])
 @pytest.mark.parametrize("B,Q,S,R,H,K", [(2, 100, 37, 5, 128, 128), (3, 64, 8, 8, 512, 64), (1, 129, 300, 16, 200, 32),
