@@ -414,7 +414,7 @@ int grm_hip_segment_route(const void* queries, const void* keys, int64_t* topk_i
  *   (paper_grm.py:229,301-313,604-611; grm/core/aggregator.py:67-145).
  * Limits: key_dim <= 128 and a multiple of 8, value_dim a multiple of 8 and
  * <= 2048, routes <= 32, min(capacity, base + (n_query - 1) / segment_len) +
- * 127 / segment_len + 1 <= 256, base + (n_query - 1) / segment_len <= segments;
+ * 95 / segment_len + 1 <= 256, base + (n_query - 1) / segment_len <= segments;
  * otherwise GRM_HIP_EUNSUPPORTED or GRM_HIP_EINVAL.  ABI 109.
  */
 int64_t grm_hip_segment_retrieve_fuse_workspace(int64_t batch, int64_t n_query, int64_t value_dim, int64_t key_dim,

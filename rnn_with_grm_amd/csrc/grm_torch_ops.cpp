@@ -1045,20 +1045,21 @@ Tensor segment_retrieve_fuse_hip(const Tensor& memories, const Tensor& indices, 
   const int hd = dtype_code(h.scalar_type());
   const bool q16 = queries.scalar_type() == at::kBFloat16 ||
                    (queries.scalar_type() == at::kHalf && memories.scalar_type() == at::kHalf);
-  const int64_t span = std::min(capacity, base + (Q > 0 ? (Q - 1) / segment_len : 0)) + 127 / segment_len + 1;
   bool ok = same_cuda_device({&memories, &indices, &queries, &gates, &h}) && md >= 0 && qd >= 0 && hd >= 0 && q16 &&
-            K <= 128 && K % 8 == 0 && H % 8 == 0 && H <= 2048 && R <= 32 && span <= 256;
+            K <= 128 && K % 8 == 0 && H % 8 == 0 && H <= 2048 && R <= 32;
   if (has_w) ok = ok && weight->is_cuda() && weight->numel() == H;
   if (has_b) ok = ok && has_w && bias->is_cuda() && bias->numel() == H;
-  if (!ok) {
-    // retrieve_fuse over the masked pairs (an invalid pair: index 0, gate 0).
+  // retrieve_fuse over the masked pairs (an invalid pair: index 0, gate 0): the inputs the
+  // window kernel does not cover, including windows wider than one workgroup's entries
+  auto masked = [&]() {
     Tensor valid = segment_window_valid(indices, segment_len, base, capacity);
     check_window_indices(indices, valid);
     if (S == 0) return segment_retrieve_fuse_generic(memories, indices, queries, gates, h, weight, bias, eps,
                                                      segment_len, base, capacity);
     return retrieve_fuse_hip(memories, indices.to(at::kLong).masked_fill(valid.logical_not(), 0), queries,
                              gates.to(at::kFloat).masked_fill(valid.logical_not(), 0.0), h, weight, bias, eps);
-  }
+  };
+  if (!ok) return masked();
   c10::OptionalDeviceGuard guard(memories.device());
   Tensor mm = memories.contiguous(), idx = indices.to(at::kLong).contiguous(), q = queries.contiguous();
   Tensor gc = gates.to(at::kFloat).contiguous(), hc = h.contiguous();
@@ -1077,12 +1078,14 @@ Tensor segment_retrieve_fuse_hip(const Tensor& memories, const Tensor& indices, 
   Tensor bad;
   const bool check = check_indices_requested();
   if (check) bad = at::zeros({1}, mm.options().dtype(at::kInt));
-  check_rc(grm_hip_segment_retrieve_fuse(mm.data_ptr(), idx.data_ptr<int64_t>(), q.data_ptr(), gc.data_ptr<float>(),
-                                         hc.data_ptr(), has_w ? wc.data_ptr() : nullptr,
-                                         has_b ? bc.data_ptr() : nullptr, out.data_ptr(), ws.data_ptr(), wsb, B, S, Q,
-                                         R, H, K, segment_len, base, capacity, md, qd, hd, static_cast<float>(eps),
-                                         check ? bad.data_ptr<int32_t>() : nullptr, current_stream(mm)),
-           "segment_retrieve_fuse");
+  const int rc = grm_hip_segment_retrieve_fuse(mm.data_ptr(), idx.data_ptr<int64_t>(), q.data_ptr(),
+                                               gc.data_ptr<float>(), hc.data_ptr(), has_w ? wc.data_ptr() : nullptr,
+                                               has_b ? bc.data_ptr() : nullptr, out.data_ptr(), ws.data_ptr(), wsb, B,
+                                               S, Q, R, H, K, segment_len, base, capacity, md, qd, hd,
+                                               static_cast<float>(eps), check ? bad.data_ptr<int32_t>() : nullptr,
+                                               current_stream(mm));
+  if (rc == GRM_HIP_EUNSUPPORTED) return masked();  // rejected before any launch
+  check_rc(rc, "segment_retrieve_fuse");
   if (check) {
     const int64_t nbad = bad.item<int32_t>();
     TORCH_CHECK_INDEX(nbad == 0, "segment_retrieve_fuse: ", nbad,

@@ -12,7 +12,7 @@
 // retrieve_fuse sorts (query, route) pairs by archive entry, applies each entry
 // to the queries that selected it and writes one float16 row per pair, which a
 // second pass sums per query: at config 4 that is 268 MB written and read back
-// per layer.  Here the 128 queries of a block see at most capacity + 128 /
+// per layer.  Here the 96 queries of a block see at most capacity + 95 /
 // segment_len + 1 entries, so one workgroup per (block, 128-value tile) walks
 // those entries in index order and adds each entry's products into float32
 // accumulators in LDS (one row per query).  Wave w owns value rows [16 w, 16 w +
@@ -45,13 +45,14 @@ namespace {
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
 constexpr int WR_THREADS = 512;       // 8 waves, 16 value rows each
-constexpr int WR_TOK = 128;           // queries per workgroup
+constexpr int WR_TOK = 96;            // queries per workgroup (two workgroups' LDS fit one CU)
 constexpr int WR_V = kScaledTile;     // value rows per workgroup
 constexpr int WR_AS = WR_V + 4;       // accumulator row stride (floats)
 constexpr int WR_SPAN_MAX = 256;      // archive entries one block's windows may span
 constexpr int WR_ROUTES_MAX = 32;
 constexpr int kDeadItem = 1 << 30;    // a padding work item: no pairs
 static_assert(WR_V == 16 * (WR_THREADS / 64), "one 16-row slice per wave");
+static_assert(WR_TOK % 16 == 0, "the output pass takes 16 queries per wave round");
 
 struct WinArgs {
   const void* msw;      // the window's entries in fragment order: [batch, n_ent, ent_units, 16 bytes]
@@ -152,8 +153,8 @@ __global__ __launch_bounds__(WR_THREADS) void retrieve_window_kernel(const WinAr
   // ---- every global input of the block first (queries, indices, gates), then the
   // accumulators and the histogram zeroed while they arrive; the queries into LDS
   constexpr int UPR = DKP / 8;                         // 16-byte units per query row; UPR lanes share a row
-  constexpr int QPT = WR_TOK * UPR / WR_THREADS;       // query units per thread
-  constexpr int PPT = WR_TOK * WR_ROUTES_MAX / WR_THREADS;  // pairs per thread at most
+  constexpr int QPT = (WR_TOK * UPR + WR_THREADS - 1) / WR_THREADS;  // query units per thread
+  constexpr int PPT = (WR_TOK * WR_ROUTES_MAX + WR_THREADS - 1) / WR_THREADS;  // pairs per thread at most
   const int n_pairs = nt * R;
   u32x4 qv[QPT];
   int64_t jv[PPT];
@@ -201,10 +202,12 @@ __global__ __launch_bounds__(WR_THREADS) void retrieve_window_kernel(const WinAr
         const int sh = min(max(15 - ex, -100), 100);
         const u32x4 h = u32x4{pack2<F16>(ldexpf(x[0], sh), ldexpf(x[1], sh)), pack2<F16>(ldexpf(x[2], sh), ldexpf(x[3], sh)),
                               pack2<F16>(ldexpf(x[4], sh), ldexpf(x[5], sh)), pack2<F16>(ldexpf(x[6], sh), ldexpf(x[7], sh))};
-        *reinterpret_cast<u32x4*>(qs + t * QS + 8 * u) = h;
-        if (u == 0) tscale[t] = ldexpf(1.f, -sh);
+        if (t < WR_TOK) {
+          *reinterpret_cast<u32x4*>(qs + t * QS + 8 * u) = h;
+          if (u == 0) tscale[t] = ldexpf(1.f, -sh);
+        }
       } else {
-        *reinterpret_cast<u32x4*>(qs + t * QS + 8 * u) = v;
+        if (t < WR_TOK) *reinterpret_cast<u32x4*>(qs + t * QS + 8 * u) = v;
       }
     }
   }
