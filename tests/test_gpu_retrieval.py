@@ -823,6 +823,36 @@ def test_segment_retrieve_fuse_op_and_fallbacks(dev):
     torch.testing.assert_close(d, e.reshape(B, Q, H), rtol=1e-5, atol=1e-5)
 
 
+def test_segment_retrieve_fuse_wide_window_falls_back(dev):
+    """A capacity wider than one block of queries can hold (capacity + 95 / segment_len + 1 > 256
+    entries): the C entry rejects it before any launch (GRM_HIP_EUNSUPPORTED) and the op runs
+    retrieve_fuse over the masked pairs, with the same result as the float32 composition over the
+    window's valid pairs."""
+    from rnn_with_grm_amd import cuda_ops
+
+    g = torch.Generator().manual_seed(45)
+    B, Q, H, K, seg, base, cap, R = 1, 600, 128, 64, 2, 0, 300, 8
+    S = base + (Q - 1) // seg + 1
+    idx, _ = _window_indices(g, B, Q, R, S, seg, base, cap)
+    mem = (torch.randn(B, S, H, K, generator=g) * 0.1).to(torch.float16).to(dev)
+    q = norm(torch.randn(B, Q, K, generator=g)).to(torch.bfloat16).to(dev)
+    gates = torch.softmax(torch.randn(B, Q, R, generator=g), -1).to(dev)
+    h = torch.randn(B, Q, H, generator=g).to(torch.bfloat16).to(dev)
+    w, b = torch.ones(H, device=dev), torch.zeros(H, device=dev)
+    idx = idx.to(dev)
+    with pytest.raises(RuntimeError, match="use retrieve_fuse"):
+        capi.segment_retrieve_fuse(mem, idx, q, gates, h, seg, base, cap, w, b)
+    print("segment_retrieve_fuse wide window", flush=True)
+    with torch.no_grad():
+        out = cuda_ops.cuda_segment_retrieve_fuse(mem, idx, q, gates, h, w, b, 1e-5, seg, base, cap)
+    valid = torch.from_numpy(_window_valid_np(idx.cpu().numpy(), seg, base, cap)).to(dev)
+    rows = capi.gather_apply(mem, torch.where(valid, idx, torch.zeros_like(idx)), q, dtype=torch.float32)
+    comp = capi.fuse_residual(h.float().reshape(B * Q, H), (rows * valid.unsqueeze(-1)).reshape(B * Q, R, H),
+                              (gates * valid).reshape(B * Q, R), w, b).reshape(B, Q, H).to(torch.bfloat16)
+    torch.cuda.synchronize()
+    torch.testing.assert_close(out.float(), comp.float(), rtol=1e-2, atol=1e-2)
+
+
 # ---------------------------------------------------------------- gather_apply backward (queries)
 @pytest.mark.parametrize("mem_dtype", [torch.float32, torch.float16, torch.bfloat16])
 @pytest.mark.parametrize("B,Q,S,R,H,K", [(2, 100, 37, 5, 128, 128), (3, 64, 8, 8, 512, 64), (1, 129, 300, 16, 200, 32),
