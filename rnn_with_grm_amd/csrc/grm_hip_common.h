@@ -178,9 +178,48 @@ __device__ __forceinline__ void store4_raw(typename ET<E>::raw* p, f32x4 v) {
 // column masks become offset selects instead of branches.
 constexpr int kBufOOB = 0x7ffffff0;  // an offset past every resource used here
 
+// 64-bit integer min / max for device code.  HIP's min<int64_t> / max<int64_t>
+// (an explicit template argument) compile to double arithmetic on the vector
+// unit, and a buffer resource built from such a result is treated as
+// divergent: every load through it gets a readfirstlane loop.
+__host__ __device__ __forceinline__ int64_t min_i64(int64_t a, int64_t b) { return a < b ? a : b; }
+__host__ __device__ __forceinline__ int64_t max_i64(int64_t a, int64_t b) { return a > b ? a : b; }
+
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t bytes) {
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), static_cast<short>(0),
                                            static_cast<int>(bytes), 0x00020000);
+}
+
+// Rows dealt `per` lanes each (per a power of two, at most 64) to a workgroup
+// whose first row is `block_first`: this lane's row, its wavefront's first row
+// (wave-uniform) and how many of the wavefront's rows lie below n_rows.  A
+// buffer resource built per lane from tid / per is divergent as far as the
+// compiler can tell, and every load through it gets a readfirstlane loop; one
+// built at the wavefront's first row and spanning its rows (wave_rows_rsrc) is
+// uniform, and each lane adds local * row_bytes to its offsets.  Rows past
+// n_rows fall outside it: they read zeros and their stores drop.
+struct WaveRows {
+  int64_t row;    // this lane's row
+  int64_t first;  // the wavefront's first row
+  int local;      // row - first
+  int count;      // rows of the wavefront below n_rows, 0 .. 64 / per
+};
+
+__device__ __forceinline__ WaveRows wave_rows(int64_t block_first, int per, int64_t n_rows) {
+  WaveRows w;
+  const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x) >> 6);
+  const int rows_per_wave = 64 / per;
+  w.local = static_cast<int>(threadIdx.x & 63) / per;
+  w.first = block_first + static_cast<int64_t>(wave) * rows_per_wave;
+  w.row = w.first + w.local;
+  const int64_t left = n_rows - w.first;
+  w.count = static_cast<int>(left < 0 ? 0 : (left < rows_per_wave ? left : rows_per_wave));
+  return w;
+}
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t wave_rows_rsrc(const void* base, const WaveRows& w,
+                                                                 uint32_t row_bytes) {
+  return make_rsrc(static_cast<const char*>(base) + w.first * row_bytes, static_cast<uint32_t>(w.count) * row_bytes);
 }
 
 // Eight consecutive elements starting at byte offset `off` (OOB -> zeros).

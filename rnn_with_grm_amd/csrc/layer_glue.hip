@@ -140,7 +140,10 @@ __device__ __forceinline__ void split_segment(const SplitArgs& a, int64_t row, i
 template <class E>
 __global__ __launch_bounds__(GL_THREADS) void project_split_kernel(const SplitArgs a) {
   const int lane = threadIdx.x & 63;
-  const int64_t row = static_cast<int64_t>(blockIdx.x) * (GL_THREADS / 64) + (threadIdx.x >> 6);
+  // (readfirstlane: the row is wave-uniform, and the compiler then knows it, so the row's
+  // buffer resources stay scalar)
+  const int64_t row = static_cast<int64_t>(blockIdx.x) * (GL_THREADS / 64) +
+                      __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x) >> 6);
   if (row >= a.rows) return;  // wave-uniform
   split_segment<E, true>(a, row, lane, 0, a.dk, a.keys);
   split_segment<E, false>(a, row, lane, a.dk, a.dv, a.values);
@@ -167,7 +170,10 @@ __global__ __launch_bounds__(GL_THREADS) void residual_layer_norm_kernel(const R
   using rawp = typename ET<P>::raw;
   constexpr int ES = sizeof(raw), PS = sizeof(rawp);
   const int lane = threadIdx.x & 63;
-  const int64_t row = static_cast<int64_t>(blockIdx.x) * (GL_THREADS / 64) + (threadIdx.x >> 6);
+  // (readfirstlane: the row is wave-uniform, and the compiler then knows it, so the row's
+  // buffer resources stay scalar)
+  const int64_t row = static_cast<int64_t>(blockIdx.x) * (GL_THREADS / 64) +
+                      __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x) >> 6);
   if (row >= a.rows) return;  // wave-uniform
   const int H = a.hidden, units = H / 8;
   const __amdgpu_buffer_rsrc_t rx = make_rsrc(static_cast<const raw*>(a.x) + row * H, H * ES);
@@ -363,7 +369,7 @@ __global__ __launch_bounds__(PG_THREADS) void project_gemm_kernel(const GemmArgs
   const int c0 = n0 + 64 * (w & 3);  // this wave's first column
   const bool wave_on = c0 < N;
   const __amdgpu_buffer_rsrc_t rx =
-      make_rsrc(static_cast<const raw*>(a.x) + m0 * K, static_cast<uint32_t>(min<int64_t>(a.rows - m0, PG_BM) * K * 2));
+      make_rsrc(static_cast<const raw*>(a.x) + m0 * K, static_cast<uint32_t>(min_i64(a.rows - m0, PG_BM) * K * 2));
   const __amdgpu_buffer_rsrc_t rw =
       make_rsrc(static_cast<const raw*>(a.w) + static_cast<int64_t>(n0) * K,
                 static_cast<uint32_t>(static_cast<int64_t>(min(N - n0, PG_BN)) * K * 2));
@@ -503,7 +509,7 @@ __global__ __launch_bounds__(OL_THREADS) void out_ln_kernel(const OutLnArgs a) {
   const int64_t m0 = static_cast<int64_t>(blockIdx.x) * OL_BM;
   const int c0 = 64 * w;
   const bool wave_on = c0 < N;
-  const int tile_rows = static_cast<int>(min<int64_t>(a.rows - m0, OL_BM));
+  const int tile_rows = static_cast<int>(min_i64(a.rows - m0, OL_BM));
   const __amdgpu_buffer_rsrc_t rx = make_rsrc(static_cast<const raw*>(a.h) + m0 * K,
                                               static_cast<uint32_t>(tile_rows * K * 2));
   const __amdgpu_buffer_rsrc_t rw = make_rsrc(a.w, static_cast<uint32_t>(static_cast<int64_t>(N) * K * 2));

@@ -895,13 +895,13 @@ __global__ __launch_bounds__(256) void fuse_scaled_kernel(const FuseScaledArgs a
   using raw = typename ET<E>::raw;
   const int tid = threadIdx.x;
   const int sub = tid & (lpr - 1);
-  const int64_t row = static_cast<int64_t>(blockIdx.x) * (256 / lpr) + tid / lpr;
-  const bool live = row < a.n_rows;
+  const WaveRows wr = wave_rows(static_cast<int64_t>(blockIdx.x) * (256 / lpr), lpr, a.n_rows);
+  const bool live = wr.row < a.n_rows;
   const int H = a.hidden;
-  const int64_t rr = live ? row : 0;
-  const __amdgpu_buffer_rsrc_t rh = make_rsrc(static_cast<const raw*>(a.h) + rr * H, H * sizeof(raw));
-  const __amdgpu_buffer_rsrc_t rrow =
-      make_rsrc(a.rows + rr * a.routes * H, static_cast<uint32_t>(a.routes * H * 2));
+  const int64_t rr = live ? wr.row : 0;
+  const int hb = H * static_cast<int>(sizeof(raw)), rowb = a.routes * H * 2;  // row bytes of h / out, of rows
+  const __amdgpu_buffer_rsrc_t rh = wave_rows_rsrc(a.h, wr, hb);
+  const __amdgpu_buffer_rsrc_t rrow = wave_rows_rsrc(a.rows, wr, rowb);
   const float* sc = a.scales + rr * a.routes * a.v_tiles;
   float x[NV][8];
 #pragma unroll
@@ -909,7 +909,7 @@ __global__ __launch_bounds__(256) void fuse_scaled_kernel(const FuseScaledArgs a
     const int c = (sub + lpr * v) * 8;
     const bool in = live && c < H;
     float hv[8];
-    load8<E>(rh, in ? c * static_cast<int>(sizeof(raw)) : kBufOOB, hv);
+    load8<E>(rh, in ? wr.local * hb + c * static_cast<int>(sizeof(raw)) : kBufOOB, hv);
     float r[8];
 #pragma unroll
     for (int e = 0; e < 8; ++e) r[e] = 0.f;
@@ -918,17 +918,17 @@ __global__ __launch_bounds__(256) void fuse_scaled_kernel(const FuseScaledArgs a
     for (int j = 0; j < a.routes; ++j) {
       const float sj = in ? sc[j * a.v_tiles + tile] : 0.f;
       float rv[8];
-      load8<F16>(rrow, in ? (j * H + c) * 2 : kBufOOB, rv);
+      load8<F16>(rrow, in ? wr.local * rowb + (j * H + c) * 2 : kBufOOB, rv);
 #pragma unroll
       for (int e = 0; e < 8; ++e) r[e] = fmaf(sj, rv[e], r[e]);
     }
 #pragma unroll
     for (int e = 0; e < 8; ++e) x[v][e] = c < H ? hv[e] + r[e] : 0.f;
   }
-  const __amdgpu_buffer_rsrc_t ro = make_rsrc(static_cast<raw*>(a.out) + rr * H, H * sizeof(raw));
+  const __amdgpu_buffer_rsrc_t ro = wave_rows_rsrc(a.out, wr, hb);
   auto out_off = [&](int v) {
     const int c = (sub + lpr * v) * 8;
-    return (live && c < H) ? c * static_cast<int>(sizeof(raw)) : kBufOOB;
+    return (live && c < H) ? wr.local * hb + c * static_cast<int>(sizeof(raw)) : kBufOOB;
   };
   if (a.w == nullptr) {
 #pragma unroll

@@ -144,9 +144,9 @@ __global__ __launch_bounds__(WR_THREADS) void retrieve_window_kernel(const WinAr
   const int64_t b = logical / per_b;
   const int vt = (logical % per_b) / a.n_blocks, blk = logical % a.n_blocks;
   const int64_t t0 = static_cast<int64_t>(blk) * WR_TOK;
-  const int nt = static_cast<int>(min<int64_t>(WR_TOK, a.n_query - t0));
+  const int nt = static_cast<int>(min_i64(WR_TOK, a.n_query - t0));
   const int64_t hi_b = a.base + (t0 + nt - 1) / a.seg_len;
-  const int64_t lo_b = max<int64_t>(0, a.base + t0 / a.seg_len - a.capacity);
+  const int64_t lo_b = max_i64(0, a.base + t0 / a.seg_len - a.capacity);
   const int span = static_cast<int>(hi_b - lo_b);  // <= WR_SPAN_MAX (host check)
   const int dk = a.dk, dv = a.dv;
 
@@ -223,7 +223,7 @@ __global__ __launch_bounds__(WR_THREADS) void retrieve_window_kernel(const WinAr
     const int e = tid + WR_THREADS * i;
     if (e < n_pairs) {
       const int64_t t = t0 + e / R, j = jv[i];
-      const int64_t hi = a.base + t / a.seg_len, lo = max<int64_t>(0, hi - a.capacity);
+      const int64_t hi = a.base + t / a.seg_len, lo = max_i64(0, hi - a.capacity);
       relv[e] = j < 0 ? -1 : (j >= lo && j < hi) ? static_cast<int>(j - lo_b) : -2;
     }
   }

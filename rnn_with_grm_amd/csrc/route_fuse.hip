@@ -1414,19 +1414,19 @@ __global__ __launch_bounds__(256) void fuse_vec_kernel(const FuseArgs a, const i
   typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
   const int tid = threadIdx.x;
   const int sub = tid & (lpr - 1);
-  const int64_t row = static_cast<int64_t>(blockIdx.x) * (256 / lpr) + tid / lpr;
-  const bool live = row < a.rows;
+  const WaveRows wr = wave_rows(static_cast<int64_t>(blockIdx.x) * (256 / lpr), lpr, a.rows);
+  const bool live = wr.row < a.rows;
   const int H = a.hidden;
-  const int64_t rr = live ? row : 0;
-  const __amdgpu_buffer_rsrc_t rh = make_rsrc(static_cast<const raw*>(a.h) + rr * H, H * sizeof(raw));
-  const __amdgpu_buffer_rsrc_t rret =
-      make_rsrc(static_cast<const raw*>(a.ret) + rr * a.routes * H, static_cast<uint32_t>(a.routes * H * sizeof(raw)));
+  const int64_t rr = live ? wr.row : 0;
+  const int hb = H * static_cast<int>(sizeof(raw)), retb = a.routes * hb;  // row bytes of h / out and of ret
+  const __amdgpu_buffer_rsrc_t rh = wave_rows_rsrc(a.h, wr, hb);
+  const __amdgpu_buffer_rsrc_t rret = wave_rows_rsrc(a.ret, wr, retb);
   const float* g = a.gates + rr * a.routes;
   float x[NV][VE];
 #pragma unroll
   for (int v = 0; v < NV; ++v) {
     const int c = (sub + lpr * v) * VE;
-    const int off = (live && c < H) ? c * static_cast<int>(sizeof(raw)) : kBufOOB;
+    const int off = (live && c < H) ? wr.local * hb + c * static_cast<int>(sizeof(raw)) : kBufOOB;
     float hv[VE];
     load_group<E>(rh, off, hv);
     float r[VE];
@@ -1435,7 +1435,7 @@ __global__ __launch_bounds__(256) void fuse_vec_kernel(const FuseArgs a, const i
 #pragma unroll 8
     for (int j = 0; j < a.routes; ++j) {
       const float gj = g[j];
-      const int o2 = (live && c < H) ? (j * H + c) * static_cast<int>(sizeof(raw)) : kBufOOB;
+      const int o2 = (live && c < H) ? wr.local * retb + (j * H + c) * static_cast<int>(sizeof(raw)) : kBufOOB;
       float rv[VE];
       load_group<E>(rret, o2, rv);
 #pragma unroll
@@ -1444,11 +1444,10 @@ __global__ __launch_bounds__(256) void fuse_vec_kernel(const FuseArgs a, const i
 #pragma unroll
     for (int e = 0; e < VE; ++e) x[v][e] = (c < H) ? hv[e] + r[e] : 0.f;
   }
-  raw* out = static_cast<raw*>(a.out) + rr * H;
-  const __amdgpu_buffer_rsrc_t ro = make_rsrc(out, H * sizeof(raw));
+  const __amdgpu_buffer_rsrc_t ro = wave_rows_rsrc(a.out, wr, hb);
   auto store = [&](int v, const float (&y)[VE]) {
     const int c = (sub + lpr * v) * VE;
-    const int off = (live && c < H) ? c * static_cast<int>(sizeof(raw)) : kBufOOB;
+    const int off = (live && c < H) ? wr.local * hb + c * static_cast<int>(sizeof(raw)) : kBufOOB;
     if constexpr (VE == 8) {
       uint4 pk;
       pk.x = ET<E>::from_f(y[0]) | (static_cast<uint32_t>(ET<E>::from_f(y[1])) << 16);
