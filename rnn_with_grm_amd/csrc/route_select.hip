@@ -415,26 +415,35 @@ __global__ __launch_bounds__(ST) void route_select_kernel(const SelParams p) {
 #pragma unroll
     for (int qt = 0; qt < 4; ++qt) thr_q[qt] = __shfl(thr, 16 * qt + n, 64);
 
-    // ---- pass 2: candidates A >= L - W into the rows' lists.  The four lanes of a
-    // row (lanes n, n + 16, n + 32, n + 48) count their hits; a prefix over them
-    // gives each its slots, so the lists are filled without atomics.
+    // ---- pass 2: candidates A >= L - W into the rows' lists.  Each lane marks its
+    // hits in one 64-bit mask per row tile over up to kFlush steps; the marks are
+    // then appended together.  The four lanes of a row (lanes n, n + 16, n + 32,
+    // n + 48) count their hits; a prefix over them gives each its slots, so the
+    // lists are filled without atomics, and one loop takes every lane's hits of
+    // the group (its trip count is the largest number of hits one lane holds, not
+    // a sum over the steps of each step's largest).
     asm volatile("" ::: "memory");  // reload the B operands rather than keep them
     load_bq();
     int filled[4] = {0, 0, 0, 0};  // list length of row 16 qt + n, the same in its four lanes
-    auto append = [&](int s0, const f32x4 (&acc)[4][2]) {
-      // bit 4 kt + r of byte qt: key s0 + 16 kt + 4 g + r of row 16 qt + n
-      uint32_t hits = 0u;
+    constexpr int kFlush = 8;      // steps per group: 8 bits each
+    // bit 8 i + 4 kt + r of hq[qt]: key s0g + SKT i + 16 kt + 4 g + r of row 16 qt + n
+    uint64_t hq[4] = {0u, 0u, 0u, 0u};
+    auto mark = [&](int i, const f32x4 (&acc)[4][2]) {
 #pragma unroll
-      for (int qt = 0; qt < 4; ++qt)
+      for (int qt = 0; qt < 4; ++qt) {
+        uint32_t b = 0u;
 #pragma unroll
         for (int kt = 0; kt < 2; ++kt)
 #pragma unroll
-          for (int r = 0; r < 4; ++r)
-            hits |= (acc[qt][kt][r] >= thr_q[qt] ? 1u : 0u) << (8 * qt + 4 * kt + r);
+          for (int r = 0; r < 4; ++r) b |= (acc[qt][kt][r] >= thr_q[qt] ? 1u : 0u) << (4 * kt + r);
+        hq[qt] |= static_cast<uint64_t>(b) << (8 * i);
+      }
+    };
+    auto flush = [&](int s0g) {
       int base[4];
 #pragma unroll
       for (int qt = 0; qt < 4; ++qt) {
-        const int mine = __builtin_popcount((hits >> (8 * qt)) & 0xffu);
+        const int mine = __builtin_popcountll(hq[qt]);
         // Exclusive prefix over g and the total, with lane swaps (no LDS): the
         // 16-lane swap pairs g = 0 with 1 and 2 with 3, the 32-lane swap the halves.
         const auto p16 = __builtin_amdgcn_permlane16_swap(mine, mine, false, false);
@@ -445,31 +454,43 @@ __global__ __launch_bounds__(ST) void route_select_kernel(const SelParams p) {
         base[qt] = filled[qt] + ((g & 1) ? even : 0) + (g >= 2 ? low : 0);
         filled[qt] += low + high;
       }
-      while (hits != 0u) {
-        const int j = __builtin_ctz(hits);
-        hits &= hits - 1u;
-        const int qt = j >> 3;
+      while ((hq[0] | hq[1] | hq[2] | hq[3]) != 0u) {
+        // the lowest hit of the first non-empty mask
+        const int qt = hq[0] != 0u ? 0 : hq[1] != 0u ? 1 : hq[2] != 0u ? 2 : 3;
+        const uint64_t m = qt == 0 ? hq[0] : qt == 1 ? hq[1] : qt == 2 ? hq[2] : hq[3];
+        const int j = __builtin_ctzll(m);
+        const uint64_t rest = m & (m - 1u);
         const int row = 16 * qt + n;
-        const int key = s0 + 16 * ((j >> 2) & 1) + 4 * g + (j & 3);
+        const int key = s0g + SKT * (j >> 3) + 16 * ((j >> 2) & 1) + 4 * g + (j & 3);
         const int pos = qt == 0 ? base[0] : qt == 1 ? base[1] : qt == 2 ? base[2] : base[3];
         if (pos < cap) lst[row * cap + pos] = static_cast<uint16_t>(key);
 #pragma unroll
-        for (int t = 0; t < 4; ++t) base[t] += (t == qt) ? 1 : 0;
+        for (int t = 0; t < 4; ++t) {
+          base[t] += (t == qt) ? 1 : 0;
+          hq[t] = (t == qt) ? rest : hq[t];
+        }
       }
     };
-    for (int s0 = in_a; s0 < in_b; s0 += SKT) {
-      f32x4 acc[4][2];
-      scores(s0, acc);
-      append(s0, acc);
-    }
-    for (int s0 = wave_lo; s0 < wave_hi; s0 += SKT) {
-      if (s0 == in_a) s0 = max(in_b, in_a);  // the boundary steps only
-      if (s0 >= wave_hi) break;
-      f32x4 acc[4][2];
-      scores(s0, acc);
-      mask(s0, acc);
-      append(s0, acc);
-    }
+    // Steps in groups of kFlush over a contiguous range of key steps; `masked`
+    // for the steps at the window boundaries.
+    auto pass2 = [&](int lo, int hi, bool masked) {
+      int i = 0, s0g = lo;
+      for (int s0 = lo; s0 < hi; s0 += SKT) {
+        f32x4 acc[4][2];
+        scores(s0, acc);
+        if (masked) mask(s0, acc);
+        mark(i, acc);
+        if (++i == kFlush) {
+          flush(s0g);
+          i = 0;
+          s0g = s0 + SKT;
+        }
+      }
+      if (i != 0) flush(s0g);
+    };
+    pass2(in_a, in_b, false);
+    pass2(wave_lo, min(in_a, wave_hi), true);      // the boundary steps below the interior
+    pass2(max(in_b, in_a), wave_hi, true);         // and above it
     // the row owner (lane 16 g + n owns row 16 g + n) takes its row's length
     const int c = g == 0 ? filled[0] : g == 1 ? filled[1] : g == 2 ? filled[2] : filled[3];
     wave_sync_lds();
