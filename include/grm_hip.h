@@ -92,9 +92,14 @@ int64_t grm_hip_chunk_update_fwd_workspace(int64_t batch, int64_t seq_len, int64
  * called) until the process ends.  Calls whose sizes need more time-split scratch than
  * that (grm_hip_chunk_update_fwd_workspace() above the limit) are rejected with
  * GRM_HIP_EINVAL and a message.  Every call on one GPU shares that GPU's
- * scratch: calls that overlap on one GPU (different streams, or host threads
- * without ordering) race and must not be issued.  The scratch needs no clearing
- * between calls.
+ * scratch, so calls take it in turn: a call on a different stream than the
+ * previous call on that GPU first makes its stream wait for the previous
+ * call's kernels (an event the library records after each call; the event
+ * and the scratch's address are set up at the first call on a device and
+ * kept), and calls from several host threads hold a lock while they launch.
+ * Under stream capture nothing is recorded or waited for: replays of a
+ * captured call must not overlap other calls on the same GPU.  The scratch
+ * needs no clearing between calls.
  */
 #define GRM_HIP_NOALLOC_SCRATCH_BYTES (32ll << 20)
 int64_t grm_hip_chunk_update_fwd_noalloc_limit(void);

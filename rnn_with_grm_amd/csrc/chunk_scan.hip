@@ -821,10 +821,16 @@ static __device__ __align__(256) unsigned char scratch[kNoAllocScratchBytes];
 
 std::mutex g_scratch_mu;
 void* g_scratch_ptr[kMaxDevices] = {};
+// Per device: an event recorded on the stream of the last call (after its
+// launches) and that stream, so that a call on another stream first waits for
+// it.  Created with the address lookup, once per device, and kept.
+hipEvent_t g_scratch_done[kMaxDevices] = {};
+hipStream_t g_scratch_stream[kMaxDevices] = {};
+bool g_scratch_recorded[kMaxDevices] = {};
 
-// The current device's copy of `scratch`, looked up once per device (with that
-// device current) and kept.
-int scratch_for_current_device(void** out) {
+// The current device's index and copy of `scratch`, looked up once per device
+// (with that device current) and kept.  Called with g_scratch_mu held.
+int scratch_for_current_device(int* dev_out, void** out) {
   int dev = -1;
   hipError_t e = hipGetDevice(&dev);
   if (e != hipSuccess) {
@@ -835,7 +841,6 @@ int scratch_for_current_device(void** out) {
     set_error("chunk_update_fwd_noalloc: device %d beyond the %d this library tracks", dev, kMaxDevices);
     return GRM_HIP_EUNSUPPORTED;
   }
-  std::lock_guard<std::mutex> lock(g_scratch_mu);
   if (g_scratch_ptr[dev] == nullptr) {
     void* p = nullptr;
     e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
@@ -844,8 +849,17 @@ int scratch_for_current_device(void** out) {
                 hipGetErrorString(e));
       return e != hipSuccess ? static_cast<int>(e) : GRM_HIP_EINVAL;
     }
+    hipEvent_t ev = nullptr;
+    e = hipEventCreateWithFlags(&ev, hipEventDisableTiming);
+    if (e != hipSuccess) {
+      set_error("chunk_update_fwd_noalloc: hipEventCreateWithFlags failed on device %d: %s", dev,
+                hipGetErrorString(e));
+      return static_cast<int>(e);
+    }
+    g_scratch_done[dev] = ev;
     g_scratch_ptr[dev] = p;
   }
+  *dev_out = dev;
   *out = g_scratch_ptr[dev];
   return GRM_HIP_OK;
 }
@@ -867,12 +881,47 @@ extern "C" int grm_hip_chunk_update_fwd_noalloc(const void* keys, const void* va
               (long long)need, (long long)kNoAllocScratchBytes);
     return GRM_HIP_EINVAL;
   }
-  void* ws = nullptr;
-  if (need > 0) {
-    int rc = scratch_for_current_device(&ws);
-    if (rc != GRM_HIP_OK) return rc;
+  if (need == 0) {  // no time split: the scratch is not used
+    return grm_hip_chunk_update_fwd(keys, values, queries, memory, hidden, memory_out, snapshots, nullptr, 0, batch,
+                                    seq_len, key_dim, value_dim, in_dtype, mem_dtype, memory_decay, snapshot_len,
+                                    stream);
   }
-  return grm_hip_chunk_update_fwd(keys, values, queries, memory, hidden, memory_out, snapshots, ws,
-                                  need > 0 ? kNoAllocScratchBytes : 0, batch, seq_len, key_dim, value_dim,
-                                  in_dtype, mem_dtype, memory_decay, snapshot_len, stream);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+  hipError_t e = hipStreamIsCapturing(s, &cap);
+  if (e != hipSuccess) {
+    set_error("chunk_update_fwd_noalloc: hipStreamIsCapturing failed: %s", hipGetErrorString(e));
+    return static_cast<int>(e);
+  }
+  const bool capturing = cap != hipStreamCaptureStatusNone;
+  // Held over the wait, the launches and the record: calls from several host
+  // threads take the scratch one after another.
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  int dev = -1;
+  void* ws = nullptr;
+  int rc = scratch_for_current_device(&dev, &ws);
+  if (rc != GRM_HIP_OK) return rc;
+  // A call on another stream than the last one waits for the last one's kernels, so
+  // calls on different streams take the scratch in turn instead of racing on it.
+  // Under stream capture the library orders nothing: the caller orders replays.
+  if (!capturing && g_scratch_recorded[dev] && g_scratch_stream[dev] != s) {
+    e = hipStreamWaitEvent(s, g_scratch_done[dev], 0);
+    if (e != hipSuccess) {
+      set_error("chunk_update_fwd_noalloc: hipStreamWaitEvent failed: %s", hipGetErrorString(e));
+      return static_cast<int>(e);
+    }
+  }
+  rc = grm_hip_chunk_update_fwd(keys, values, queries, memory, hidden, memory_out, snapshots, ws,
+                                kNoAllocScratchBytes, batch, seq_len, key_dim, value_dim, in_dtype, mem_dtype,
+                                memory_decay, snapshot_len, stream);
+  if (rc == GRM_HIP_OK && !capturing) {
+    e = hipEventRecord(g_scratch_done[dev], s);
+    if (e != hipSuccess) {
+      set_error("chunk_update_fwd_noalloc: hipEventRecord failed: %s", hipGetErrorString(e));
+      return static_cast<int>(e);
+    }
+    g_scratch_stream[dev] = s;
+    g_scratch_recorded[dev] = true;
+  }
+  return rc;
 }
