@@ -143,16 +143,12 @@ __device__ __forceinline__ int key_off(int r, int u) {
   return (r * NG + (u ^ (r & (NG - 1)))) * 8;
 }
 
-// Exact scores of two keys: each the fp32 FMA chain over d in increasing order,
-// times scale.  qv holds the row's query as packed bf16.  FULL (dim == DKP):
+// Exact score of one key: the fp32 FMA chain over d in increasing order, times
+// scale.  qf holds the row's query converted to fp32 once.  FULL (dim == DKP):
 // one straight-line body, so the key loads of every granule are in flight
 // together; otherwise granules past dim are skipped (they are zero, but an
-// extra fma(0, 0, -0) would turn a -0 chain into +0).
-// Exact score of one key: the fp32 FMA chain over d in increasing order, times
-// scale.  qf holds the row's query converted to fp32 once.  Granules past dim
-// are skipped (they are zero, but an extra fma(0, 0, -0) would turn a -0 chain
-// into +0).  One chain per call: the chain's FMAs issue back to back, and the
-// key conversions fill the gaps.
+// extra fma(0, 0, -0) would turn a -0 chain into +0).  One chain per call: the
+// chain's FMAs issue back to back, and the key conversions fill the gaps.
 template <int DKP, bool FULL>
 __device__ __forceinline__ float exact_one(const float (&qf)[DKP], const uint16_t* klds, int key, int dim,
                                            float scale) {
