@@ -39,16 +39,18 @@ struct ChunkFwdArgs {
   float part_decay;   // decay^(part_chunks * chunk)
   float* part_states; // [batch, n_parts - 1, dv, dk]: end-state contribution of each part
   int part_starts; // part_states[q] holds M_{q+1} (combined) rather than D_q (wide kernel)
-  int snap_full_lines; // value-split kernel: snapshot stores in whole 128-byte lines (full_line_pair)
+  int snap_full_lines; // value-split kernel, key_dim <= 64: snapshot stores in whole 128-byte lines (full_line_pair)
   float c;         // (1 - decay) / sqrt(d_k)
   float pw[PW_N];  // decay^n rounded from double
 };
 
-// Snapshot bytes per call from which the value-split kernel stores snapshots
-// in whole 128-byte lines: below it the writes stay in the 256 MB memory-side
-// cache and the lane permutation only costs issue slots (config 2, value
-// split: 48.8 -> 62.9 us); above it half-line writes cost HBM efficiency
-// (64 x 8192 tokens: 290 -> 265 us).
+// Snapshot bytes per call from which the value-split kernel with key_dim <= 64
+// stores snapshots in whole 128-byte lines: below it the writes stay in the
+// 256 MB memory-side cache and the lane permutation only costs issue slots
+// (config 2, value split: 48.8 -> 62.9 us); above it half-line writes cost HBM
+// efficiency (64 x 8192 tokens: 290 -> 265 us, measured with key_dim 128 before
+// that kernel stored its snapshots from an fp32 copy in LDS, always in whole
+// lines).
 constexpr int64_t kFullLineSnapBytes = 320ll << 20;
 
 typedef float f32x4_t __attribute__((ext_vector_type(4)));

@@ -36,6 +36,19 @@
 // 16-byte granules are XOR-swizzled by row, so that both the 16-byte reads of
 // 16 rows and the transposed 8-byte reads of 8 rows x 32 bytes (one half-wave)
 // land on distinct banks.
+//
+// Key width 128 (SO) moves the stores off the update waves' chain.  Issuing a
+// snapshot's stores stalled those waves, the step's critical path, for about
+// a third of the step once the snapshots go to HBM (64 sequences x 8192
+// tokens), while the other six waves waited at the barrier.  There the state
+// copy is fp32 (the output waves round their operand from it), the output
+// waves store the hidden rows straight from their accumulators (two lane
+// swaps give each lane 8 consecutive values; no output tile, no flush), and
+// each snapshot is stored from the fp32 copy in whole lines: rows 16 vb +
+// [0, 8) by the output waves in the next step, rows 16 vb + [8, 16) by the
+// update waves right after writing the copy.  Splitting it so measured faster
+// than either role storing all of it (or the update waves storing from their
+// accumulators through a lane permutation), with the same bytes written.
 #include <stdint.h>
 #include <string.h>
 
@@ -78,9 +91,16 @@ struct VsShape {
   static constexpr int K_UNITS = CT * KU / kVsPThreads;
   static constexpr int BUF = CT * (2 * KS + VS);  // K, Q, V of one chunk
   static constexpr int MB = DVT * MS;             // one 16-bit state copy
+  // SO (key_dim 128): the state copy between the update and output waves is fp32, the
+  // output waves store the snapshots from it and the hidden rows from their accumulators
+  // (no output tile in LDS).
+  static constexpr bool SO = DKP == 128;
+  static constexpr int MFB = DVT * 128;  // floats in one fp32 state copy
   static constexpr size_t lds_elems =
-      static_cast<size_t>(kVsStages * BUF + 2 * CT * PS + 2 * CT * OS + 2 * MB);
-  static constexpr size_t lds_bytes = lds_elems * sizeof(raw) + PW_N * sizeof(float);
+      SO ? static_cast<size_t>(kVsStages * BUF + 2 * CT * PS)
+         : static_cast<size_t>(kVsStages * BUF + 2 * CT * PS + 2 * CT * OS + 2 * MB);
+  static constexpr size_t lds_bytes =
+      lds_elems * sizeof(raw) + (SO ? 2 * MFB * sizeof(float) : 0) + PW_N * sizeof(float);
   static_assert(K_UNITS * kVsPThreads == CT * KU && CT * VU == kVsPThreads, "tiles split evenly");
   static_assert(lds_bytes <= kMaxLds, "tile set must fit one CU's LDS");
 };
@@ -111,6 +131,12 @@ __device__ __forceinline__ int o_at(int row, int col) {
   const int f = ((row >> 1) & 7) ^ ((row >> 2) & 1);
   return row * kVsplitDv + ((((col >> 2) ^ f)) << 2) + (col & 3);
 }
+
+// fp32 state copy (SO): rows of 128 floats, 16-byte granule G (keys 4G .. 4G + 3)
+// at G ^ (row & 15): the update waves' writes (16 rows x one granule per 16
+// lanes), the output waves' operand reads (the same) and the snapshot reads (32
+// consecutive granules of one row per 32 lanes) fall on distinct bank groups.
+__device__ __forceinline__ int mf_at(int row, int G) { return row * 128 + 4 * (G ^ (row & 15)); }
 
 template <int DKP>
 __device__ __forceinline__ int kq_at(int row, int col) {
@@ -171,7 +197,8 @@ __global__ __launch_bounds__(kVsThreads, 1) void scan_vsplit_kernel(const ChunkF
   raw* Pbuf = stages + kVsStages * BUF;            // 2 x [CT][PS]  P = S * coef, row = query
   raw* Obuf = Pbuf + 2 * CT * PS;                  // 2 x [CT][OS]  output tile, row = query
   raw* Mbuf = Obuf + 2 * CT * OS;                  // 2 x [DVT][MS] state before a chunk, 16-bit
-  float* pw = reinterpret_cast<float*>(Mbuf + 2 * MB);  // [PW_N]
+  float* Mf = reinterpret_cast<float*>(Pbuf + 2 * CT * PS);  // SO: 2 x [DVT][128] fp32 state
+  float* pw = S::SO ? Mf + 2 * S::MFB : reinterpret_cast<float*>(Mbuf + 2 * MB);  // [PW_N]
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -314,6 +341,15 @@ __global__ __launch_bounds__(kVsThreads, 1) void scan_vsplit_kernel(const ChunkF
   };
   const int64_t mem_b = f32m ? 4 : ES;
   auto publish_state = [&](int slot) {
+    if constexpr (S::SO) {
+      float* M = Mf + slot * S::MFB;
+#pragma unroll
+      for (int vb = 0; vb < 2; ++vb)
+#pragma unroll
+        for (int kt = 0; kt < KT; ++kt)
+          *reinterpret_cast<f32x4*>(M + mf_at(16 * vb + n, 16 * uk + 4 * kt + g)) = st[vb][kt];
+      return;
+    }
     raw* Mb = Mbuf + slot * MB;
 #pragma unroll
     for (int vb = 0; vb < 2; ++vb)
@@ -350,6 +386,26 @@ __global__ __launch_bounds__(kVsThreads, 1) void scan_vsplit_kernel(const ChunkF
         vf[vb][p] = vs_frag_tr<E>(base, base + 16 * S::VS);
       }
   };
+  // SO: output wave oq stores state rows [16 oq, + 8) of a snapshot from the fp32
+  // copy in slot `slot`, two whole 512-byte rows per store; update wave uk stores
+  // rows 16 vb + [8, 16) of its key half [64 uk, + 64), four 256-byte row halves
+  // per store, right after writing them to the copy.
+  auto o_snap = [&](int si, int slot, int oq) {
+    const float* M = Mf + slot * S::MFB;
+    const __amdgpu_buffer_rsrc_t rs =
+        make_rsrc(a.snapshots + (b * a.n_snap + si) * dv * dk, static_cast<uint32_t>(dv * dk * 4));
+    const int G = lane & 31, h = lane >> 5;
+    // one lane offset; the row offsets 2j apart go in the scalar offset
+    const int voff = 4 * G < dk ? ((v0 + 16 * oq + h) * dk + 4 * G) * 4 : kBufOOB;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const f32x4 v = *reinterpret_cast<const f32x4*>(M + mf_at(16 * oq + 2 * j + h, G));
+      u32x4 q;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) q[i] = __float_as_uint(v[i]);
+      __builtin_amdgcn_raw_buffer_store_b128(q, rs, voff, 8 * dk * j, kStreamStore);
+    }
+  };
   // Every LDS operand of a step is read first, so the reads overlap one another
   // instead of each waiting for the product before it.
   auto o_chunk = [&](int c, auto oq_c) {
@@ -365,7 +421,13 @@ __global__ __launch_bounds__(kVsThreads, 1) void scan_vsplit_kernel(const ChunkF
 #pragma unroll
       for (int vb = 0; vb < 2; ++vb) {
         const int row = 16 * vb + n, col = 32 * kk + 8 * g;
-        if constexpr (DKP == 128) {
+        if constexpr (S::SO) {
+          const float* M = Mf + (c & 1) * S::MFB;
+          const f32x4 lo = *reinterpret_cast<const f32x4*>(M + mf_at(row, 8 * kk + 2 * g));
+          const f32x4 hi = *reinterpret_cast<const f32x4*>(M + mf_at(row, 8 * kk + 2 * g + 1));
+          mf[vb][kk] = __builtin_bit_cast(Frag8<E>, u32x4{pack2<E>(lo[0], lo[1]), pack2<E>(lo[2], lo[3]),
+                                                          pack2<E>(hi[0], hi[1]), pack2<E>(hi[2], hi[3])});
+        } else if constexpr (DKP == 128) {
           mf[vb][kk] = lds_frag_4x2<E>(Mb + m_at(row, col), Mb + m_at(row, col + 4));
         } else {
           mf[vb][kk] = *reinterpret_cast<const Frag8<E>*>(Mb + row * MS + col);
@@ -393,11 +455,18 @@ __global__ __launch_bounds__(kVsThreads, 1) void scan_vsplit_kernel(const ChunkF
         }
       }
     }
-    // O^T = decay^{i+1} M Q^T + V^T P^T: A = state rows v (16-bit copy) then
+    // O^T = decay^{i+1} M Q^T + V^T P^T: A = state rows v (16-bit, from the copy) then
     // V^T rows v; B = Q rows i then P rows i.
+    __amdgpu_buffer_rsrc_t rh;
+    if constexpr (S::SO) {
+      const int64_t t0 = static_cast<int64_t>(c) * chunk;
+      rh = make_rsrc(hidden + (hidden != nullptr ? t0 * dv : 0),
+                     static_cast<uint32_t>(hidden != nullptr ? chunk_len(c) * dv * ES : 0));
+    }
 #pragma unroll
     for (int ib = 0; ib < 2; ++ib) {
       const int iblk = 2 * oq + ib;
+      f32x4 ov[2];
 #pragma unroll
       for (int vb = 0; vb < 2; ++vb) {
         f32x4 o = f32x4{0.f, 0.f, 0.f, 0.f};
@@ -409,8 +478,26 @@ __global__ __launch_bounds__(kVsThreads, 1) void scan_vsplit_kernel(const ChunkF
           if (2 * p > iblk) continue;
           o = mfma8(vf[vb][p], pf[ib][p], o);
         }
-        store4_raw<E>(Ob + o_at(16 * iblk + n, 16 * vb + 4 * g), o);
+        if constexpr (S::SO) {
+          ov[vb] = o;
+        } else {
+          store4_raw<E>(Ob + o_at(16 * iblk + n, 16 * vb + 4 * g), o);
+        }
       }
+      if constexpr (S::SO) {
+        // Lane (g, n) holds values 4g .. 4g + 3 of both 16-value halves of token
+        // 16 iblk + n; two swaps give it values 8g .. 8g + 7, one 16-byte store.
+        const auto s0 = __builtin_amdgcn_permlane32_swap(pack2<E>(ov[0][0], ov[0][1]), pack2<E>(ov[1][0], ov[1][1]),
+                                                         false, false);
+        const auto s1 = __builtin_amdgcn_permlane32_swap(pack2<E>(ov[0][2], ov[0][3]), pack2<E>(ov[1][2], ov[1][3]),
+                                                         false, false);
+        const auto t0 = __builtin_amdgcn_permlane16_swap(s0[0], s0[1], false, false);
+        const auto t1 = __builtin_amdgcn_permlane16_swap(s1[0], s1[1], false, false);
+        store_stream(rh, ((16 * iblk + n) * dv + v0 + 8 * g) * ES, u32x4{t0[0], t1[0], t0[1], t1[1]});
+      }
+    }
+    if constexpr (S::SO) {
+      if (a.snap_every > 0 && c > 0 && c % a.snap_every == 0) o_snap(c / a.snap_every - 1, c & 1, oq);
     }
   };
   int snap_phase = a.snap_every > 0 ? 1 % a.snap_every : 1;  // == 0: a snapshot follows the current chunk
@@ -448,7 +535,7 @@ __global__ __launch_bounds__(kVsThreads, 1) void scan_vsplit_kernel(const ChunkF
       }
     // The snapshot's stores go out before the 16-bit copy for the output waves
     // (measured about 1% faster at 64 x 8192 tokens, same results).
-    if (a.snap_every > 0 && (snap_phase == 0 || c + 1 == n_chunks)) {
+    if (!S::SO && a.snap_every > 0 && (snap_phase == 0 || c + 1 == n_chunks)) {
       const int si = c / a.snap_every;
       const __amdgpu_buffer_rsrc_t rs =
           make_rsrc(a.snapshots + (b * a.n_snap + si) * dv * dk, static_cast<uint32_t>(dv * dk * 4));
@@ -479,6 +566,27 @@ __global__ __launch_bounds__(kVsThreads, 1) void scan_vsplit_kernel(const ChunkF
       }
     }
     publish_state((c + 1) & 1);
+    if constexpr (S::SO) {
+      // Rows 16 vb + [8, 16) of this wave's key half, read back from the copy it has
+      // just written (its own writes: no barrier needed), four rows x 256 bytes per
+      // store; the row offsets 4 and 16 apart go in the scalar offset.
+      if (a.snap_every > 0 && (snap_phase == 0 || c + 1 == n_chunks)) {
+        const float* M = Mf + ((c + 1) & 1) * S::MFB;
+        const __amdgpu_buffer_rsrc_t rs = make_rsrc(a.snapshots + (b * a.n_snap + c / a.snap_every) * dv * dk,
+                                                    static_cast<uint32_t>(dv * dk * 4));
+        const int G = 16 * uk + (lane & 15), q = lane >> 4;
+        const int voff = 4 * G < dk ? ((v0 + 8 + q) * dk + 4 * G) * 4 : kBufOOB;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const int dr = 16 * (j >> 1) + 4 * (j & 1);
+          const f32x4 v = *reinterpret_cast<const f32x4*>(M + mf_at(8 + dr + q, G));
+          u32x4 qv;
+#pragma unroll
+          for (int i = 0; i < 4; ++i) qv[i] = __float_as_uint(v[i]);
+          __builtin_amdgcn_raw_buffer_store_b128(qv, rs, voff, 4 * dk * dr, kStreamStore);
+        }
+      }
+    }
     if (a.snap_every > 0) snap_phase = (snap_phase + 1 == a.snap_every) ? 0 : snap_phase + 1;
   };
 
@@ -515,12 +623,12 @@ __global__ __launch_bounds__(kVsThreads, 1) void scan_vsplit_kernel(const ChunkF
         __syncthreads();
         load_chunk(c + i + PF, sg[i]);
         store_chunk(c + i + 2, sg[(i + 2) % PF]);
-        flush_out(c + i - 1);
+        if constexpr (!S::SO) flush_out(c + i - 1);
         if (c + i + 1 < n_chunks) s_chunk(c + i + 1, mw_c);
       }
     }
     __syncthreads();
-    flush_out(n_chunks - 1);
+    if constexpr (!S::SO) flush_out(n_chunks - 1);
   };
   if (p_wave) {
     if (mw == 0) {
@@ -579,6 +687,9 @@ __global__ __launch_bounds__(kVsThreads, 1) void scan_vsplit_kernel(const ChunkF
     }
   }
   __syncthreads();
+  if constexpr (S::SO) {
+    if (o_wave && a.snap_every > 0) o_snap((n_chunks - 1) / a.snap_every, n_chunks & 1, mw & 1);
+  }
   if (o_wave || a.memory_out == nullptr) return;
   const __amdgpu_buffer_rsrc_t ro = make_rsrc(static_cast<unsigned char*>(a.memory_out) + b * dv * dk * mem_b,
                                               static_cast<uint32_t>(dv * dk * mem_b));

@@ -216,7 +216,9 @@ def test_full_line_snapshots(dev, monkeypatch, B, T, K, H, seg):
     """The value-split scan's full-line snapshot stores (a lane permutation that gives each
     store whole 128-byte lines, chosen from 320 MB of snapshots, forced here with
     GRM_HIP_SNAP_FULL_LINES=1) write the same bytes as the per-tile stores (=0): key widths
-    below the padded 64/128 (partial last lines), ragged chunks, fp32 and bf16 states."""
+    below the padded 64 (partial last lines), ragged chunks, fp32 and bf16 states.  At key
+    widths 65-128 the kernel stores snapshots from its fp32 state copy whatever the flag,
+    so both calls take that path and are checked against the oracle."""
     for mem_dtype in (torch.float32, torch.bfloat16):
         k, v, q, m = make_case(B, T, K, H, torch.bfloat16, mem_dtype, seed=B * 31 + T + K)
         kd, vd, qd, md = k.to(dev), v.to(dev), q.to(dev), m.to(dev)
