@@ -840,11 +840,11 @@ def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
-    # 80 warm-up launches of the headline scan (about 20 ms): the board's power controller lowers the
+    # 120 warm-up launches of the headline scan (about 30 ms): the board's power controller lowers the
     # clocks for the first tens of back-to-back launches of this kernel and then restores them, so the
-    # timed launches start once the rate has settled (measured: 249 us, a dip to 280-320 us over
-    # launches 10-40, then 248-250 us from launch 60 on, steady over 250 launches).
-    ap.add_argument("--warmup", type=int, default=80)
+    # timed launches start once the rate has settled (measured: 233-250 us, a dip to 270-287 us over
+    # launches 10-25, 240 us around launch 100, then 238 us from launch 120 on, steady over 600 launches).
+    ap.add_argument("--warmup", type=int, default=120)
     ap.add_argument("--no-gather", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--c2-only", action="store_true", help="only the headline kernel (quick sweeps)")
