@@ -229,6 +229,9 @@ __global__ __launch_bounds__(kVsThreads, 1) void scan_vsplit_kernel(const ChunkF
   const raw* queries = static_cast<const raw*>(a.queries) + b * T * dk;
   const raw* values = static_cast<const raw*>(a.values) + b * T * dv;
   raw* hidden = a.hidden != nullptr ? static_cast<raw*>(a.hidden) + b * T * dv : nullptr;
+  // Without hidden rows (the backward's recompute of the chunk states) nothing reads
+  // Q, S or the output tiles: the queries are not loaded and S and O^T are skipped.
+  const bool want_out = a.hidden != nullptr;
 
   // Chunk lengths in 32-bit scalar arithmetic: a 64-bit min here is a VALU
   // compare whose temporary VGPR pair the register allocator may take from a
@@ -251,7 +254,7 @@ __global__ __launch_bounds__(kVsThreads, 1) void scan_vsplit_kernel(const ChunkF
     const int64_t t0 = static_cast<int64_t>(c) * chunk;
     const int L = chunk_len(c);
     const __amdgpu_buffer_rsrc_t rk = make_rsrc(keys + t0 * dk, static_cast<uint32_t>(L * dk * ES));
-    const __amdgpu_buffer_rsrc_t rq = make_rsrc(queries + t0 * dk, static_cast<uint32_t>(L * dk * ES));
+    const __amdgpu_buffer_rsrc_t rq = make_rsrc(queries + t0 * dk, static_cast<uint32_t>(want_out ? L * dk * ES : 0));
     const __amdgpu_buffer_rsrc_t rv = make_rsrc(values + t0 * dv, static_cast<uint32_t>(L * dv * ES));
 #pragma unroll
     for (int u = 0; u < K_UNITS; ++u) {
@@ -613,7 +616,7 @@ __global__ __launch_bounds__(kVsThreads, 1) void scan_vsplit_kernel(const ChunkF
         coef[jb][r] = (j <= i_loc) ? a.c * pw[max(i_loc - j, 0)] : 0.f;
       }
     }
-    s_chunk(0, mw_c);
+    if (want_out) s_chunk(0, mw_c);
     // Step c: load chunk c + PF into the slot chunk c held, stage chunk c + 2,
     // flush chunk c - 1's output, S of chunk c + 1.
     for (int c = 0; c < n_chunks; c += PF) {
@@ -624,7 +627,7 @@ __global__ __launch_bounds__(kVsThreads, 1) void scan_vsplit_kernel(const ChunkF
         load_chunk(c + i + PF, sg[i]);
         store_chunk(c + i + 2, sg[(i + 2) % PF]);
         if constexpr (!S::SO) flush_out(c + i - 1);
-        if (c + i + 1 < n_chunks) s_chunk(c + i + 1, mw_c);
+        if (want_out && c + i + 1 < n_chunks) s_chunk(c + i + 1, mw_c);
       }
     }
     __syncthreads();
@@ -678,12 +681,16 @@ __global__ __launch_bounds__(kVsThreads, 1) void scan_vsplit_kernel(const ChunkF
   // Step c: scan chunk c.
   for (int c = 0; c < n_chunks; ++c) {
     __syncthreads();
-    if (mw == 0) {
-      o_chunk(c, std::integral_constant<int, 0>{});
-    } else if (mw == 1) {
-      o_chunk(c, std::integral_constant<int, 1>{});
-    } else {
+    if (mw >= 2) {
       u_chunk(c);
+    } else if (want_out) {
+      if (mw == 0) {
+        o_chunk(c, std::integral_constant<int, 0>{});
+      } else {
+        o_chunk(c, std::integral_constant<int, 1>{});
+      }
+    } else if constexpr (S::SO) {
+      if (a.snap_every > 0 && c > 0 && c % a.snap_every == 0) o_snap(c / a.snap_every - 1, c & 1, mw & 1);
     }
   }
   __syncthreads();
