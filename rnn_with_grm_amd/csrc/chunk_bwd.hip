@@ -279,7 +279,10 @@ int launch_bwd(const BwdArgs& a, void* grad_keys, void* grad_queries, hipStream_
 //   G  <- decay^L G + dH^T diag(decay^{i+1}) Q      (the adjoint at the chunk's start)
 // Only the last line carries from chunk to chunk.  bwd_adjoint_kernel walks it
 // backwards over one part of the chunks (one workgroup per sequence, 64 value
-// rows and part, G in fp32 MFMA accumulators) and stores G at every chunk end.
+// rows and part, G in fp32 MFMA accumulators; eight waves, each 16 value rows
+// and half of the key columns, so each chunk's MFMA chain per wave is half as
+// long as with four: config 2's backward 238 -> 232 us) and stores G at every
+// chunk end.
 // The recurrence is linear: a part walked from a zero adjoint gives local
 // values, and the true adjoint at the end of chunk ch of part p is
 // local(ch) + decay^(tokens from the end of ch to the end of p) B_p, B_p the
@@ -299,7 +302,8 @@ int launch_bwd(const BwdArgs& a, void* grad_keys, void* grad_queries, hipStream_
 // Wave w owns query/key block w (tokens [16w, +16)) of every per-chunk product.
 constexpr int MB_DV = 32;  // value columns per tile of bwd_grad_kernel
 constexpr int MB_NT = 256;
-constexpr int AJ_V = 64;   // value rows per bwd_adjoint_kernel workgroup (16 per wave)
+constexpr int AJ_V = 64;   // value rows per bwd_adjoint_kernel workgroup
+constexpr int AJ_NT = 512; // bwd_adjoint_kernel: 8 waves, wave w owns value rows 16 (w & 3) .. + 16 and key half w >> 2
 
 struct BwdMArgs {
   const void* dh;
@@ -334,10 +338,11 @@ struct AjShape {
   static constexpr int HS = AJ_V + 8;  // dH rows of the tile
   static constexpr int KT = DKP / 16;
   static constexpr int KU = DKP / 8;
-  static constexpr int K_UNITS = BCT * KU / MB_NT;
-  static constexpr int H_UNITS = BCT * (AJ_V / 8) / MB_NT;
+  static constexpr int KTW = KT / 2;   // key tiles of one wave
+  static constexpr int K_UNITS = BCT * KU / AJ_NT;
+  static constexpr int H_UNITS = BCT * (AJ_V / 8) / AJ_NT;
   static constexpr size_t lds_bytes = static_cast<size_t>(BCT * KS + BCT * HS) * 2 + (BCT + 1) * 4;
-  static_assert(K_UNITS * MB_NT == BCT * KU && H_UNITS * MB_NT == BCT * (AJ_V / 8), "tiles split evenly");
+  static_assert(K_UNITS * AJ_NT == BCT * KU && H_UNITS * AJ_NT == BCT * (AJ_V / 8), "tiles split evenly");
 };
 
 template <int DKP>
@@ -391,12 +396,12 @@ __device__ __forceinline__ void store4_split(typename ET<E>::raw* hi, typename E
 // G[v][k], v = v0 + 16 w + n, k = 16 t + 4 g + r.  Chunk staging: the loads of
 // chunk ch - 1 are in flight while chunk ch is processed.
 template <class E, int DKP>
-__global__ __launch_bounds__(MB_NT) void bwd_adjoint_kernel(const BwdMArgs a) {
+__global__ __launch_bounds__(AJ_NT) void bwd_adjoint_kernel(const BwdMArgs a) {
   using S = AjShape<DKP>;
   using raw = typename ET<E>::raw;
   typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
   typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
-  constexpr int KS = S::KS, HS = S::HS, KT = S::KT, KU = S::KU;
+  constexpr int KS = S::KS, HS = S::HS, KT = S::KTW, KU = S::KU;
   constexpr int ES = 2;
 
   extern __shared__ __align__(16) unsigned char smem[];
@@ -427,10 +432,11 @@ __global__ __launch_bounds__(MB_NT) void bwd_adjoint_kernel(const BwdMArgs a) {
   const raw* queries = static_cast<const raw*>(a.queries) + b * T * dk;
   const raw* dh = static_cast<const raw*>(a.dh) + b * T * dv;
   if (tid <= BCT) pw[tid] = a.pw[tid];
-  const int vrow = v0 + 16 * w + n;
+  const int wr = w & 3, kt0 = KT * (w >> 2);  // value block, first key tile of this wave
+  const int vrow = v0 + 16 * wr + n;
   const int64_t mem_b = a.mem_f32 ? 4 : ES;
   auto g_off = [&](int t) -> int {
-    const int k = 16 * t + 4 * g;
+    const int k = 16 * (kt0 + t) + 4 * g;
     return (vrow < dv && k < dk) ? vrow * dk + k : -1;
   };
   f32x4 gacc[KT];
@@ -475,13 +481,13 @@ __global__ __launch_bounds__(MB_NT) void bwd_adjoint_kernel(const BwdMArgs a) {
     const __amdgpu_buffer_rsrc_t rh = make_rsrc(dh + t0 * dv, static_cast<uint32_t>(L * dv * ES));
 #pragma unroll
     for (int u = 0; u < S::K_UNITS; ++u) {
-      const int l = tid + MB_NT * u;
+      const int l = tid + AJ_NT * u;
       const int row = l / KU, col = 8 * (l % KU);
       sg.q[u] = buf_load8<E>(rq, col < dk ? (row * dk + col) * ES : kBufOOB);
     }
 #pragma unroll
     for (int u = 0; u < S::H_UNITS; ++u) {
-      const int l = tid + MB_NT * u;
+      const int l = tid + AJ_NT * u;
       const int row = l / (AJ_V / 8), col = 8 * (l % (AJ_V / 8));
       sg.h[u] = buf_load8<E>(rh, v0 + col < dv ? (row * dv + v0 + col) * ES : kBufOOB);
     }
@@ -489,12 +495,12 @@ __global__ __launch_bounds__(MB_NT) void bwd_adjoint_kernel(const BwdMArgs a) {
   auto store_chunk = [&](const Stage& sg) {
 #pragma unroll
     for (int u = 0; u < S::K_UNITS; ++u) {
-      const int l = tid + MB_NT * u;
+      const int l = tid + AJ_NT * u;
       *reinterpret_cast<U8<E>*>(Qs + (l / KU) * KS + 8 * (l % KU)) = sg.q[u];
     }
 #pragma unroll
     for (int u = 0; u < S::H_UNITS; ++u) {
-      const int l = tid + MB_NT * u;
+      const int l = tid + AJ_NT * u;
       *reinterpret_cast<U8<E>*>(Hs + (l / (AJ_V / 8)) * HS + 8 * (l % (AJ_V / 8))) = sg.h[u];
     }
   };
@@ -521,7 +527,7 @@ __global__ __launch_bounds__(MB_NT) void bwd_adjoint_kernel(const BwdMArgs a) {
     Frag8<E> hw[2], hwl[2];
 #pragma unroll
     for (int p = 0; p < 2; ++p) {
-      const raw* hb = Hs + (32 * p + 4 * g + (n >> 2)) * HS + 16 * w + 4 * (n & 3);
+      const raw* hb = Hs + (32 * p + 4 * g + (n >> 2)) * HS + 16 * wr + 4 * (n & 3);
       const Frag8<E> h = bw_frag_tr<E>(hb, hb + 16 * HS);
 #pragma unroll
       for (int s = 0; s < 8; ++s) {
@@ -536,7 +542,7 @@ __global__ __launch_bounds__(MB_NT) void bwd_adjoint_kernel(const BwdMArgs a) {
       f32x4 acc = gacc[t] * decay_L;
 #pragma unroll
       for (int p = 0; p < 2; ++p) {
-        const raw* qb = Qs + (32 * p + 4 * g + (n >> 2)) * KS + 16 * t + 4 * (n & 3);
+        const raw* qb = Qs + (32 * p + 4 * g + (n >> 2)) * KS + 16 * (kt0 + t) + 4 * (n & 3);
         const Frag8<E> qT = bw_frag_tr<E>(qb, qb + 16 * KS);
         acc = mfma8(qT, hw[p], acc);
         acc = mfma8(qT, hwl[p], acc);
@@ -968,7 +974,7 @@ int launch_bwd_mfma(BwdMArgs a, int mem_dtype, hipStream_t s) {
   if (rc != GRM_HIP_OK) return rc;
   const int64_t grid_a = a.batch * ((a.dv + AJ_V - 1) / AJ_V) * a.n_parts;
   a.xcd_remap = (grid_a % 8 == 0) ? 1 : 0;
-  hipLaunchKernelGGL((bwd_adjoint_kernel<E, DKP>), dim3(static_cast<unsigned>(grid_a)), dim3(MB_NT),
+  hipLaunchKernelGGL((bwd_adjoint_kernel<E, DKP>), dim3(static_cast<unsigned>(grid_a)), dim3(AJ_NT),
                      AjShape<DKP>::lds_bytes, s, a);
   rc = check_launch("chunk_update_bwd(adjoint)");
   if (rc != GRM_HIP_OK) return rc;
